@@ -1,0 +1,214 @@
+// Host side of a run. See runner.h.
+#include "runner.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+
+namespace msx {
+
+std::vector<std::vector<float>> initialize(const Program& p, uint64_t seed, Stream stream) {
+  std::vector<std::vector<float>> out;
+  for (auto& d : p.params) {
+    int64_t n = d.ty.count();
+    if (n > (int64_t(1) << 32)) throw IrError("`" + d.path + "` has more elements than a draw addresses");
+    switch (d.init) {
+      case Init::XavierUniform:
+        if (d.ty.rank() != 2) throw IrError("`" + d.path + "`: xavier_uniform needs rank 2 [In, Out]");
+        out.push_back(xavier_uniform(seed, stream, d.path, d.ty.shape[0], d.ty.shape[1]));
+        break;
+      case Init::Zeros: out.emplace_back(size_t(n), 0.0f); break;
+      case Init::Ones: out.emplace_back(size_t(n), 1.0f); break;
+    }
+  }
+  return out;
+}
+
+Feed::Feed(const Compiled& c) : cfg_(c.config) {
+  const Program& fwd = c.forward;
+  if (cfg_.feed == FeedKind::Teacher) {
+    const Node* x = fwd.input(cfg_.x);
+    const Node* y = fwd.input(cfg_.y);
+    if (!x || !y) throw IrError("teacher data needs the input and the target");
+    x_count_ = x->ty.count();
+    y_count_ = y->ty.count();
+    x_ = standard_normal(cfg_.seed, Stream::Data, cfg_.x, x_count_);
+    target_.assign(size_t(y_count_), 0.0f);
+  } else if (cfg_.feed == FeedKind::Classifier) {
+    int64_t n = cfg_.batch * cfg_.features;
+    uint64_t xid = canonical_id(cfg_.x), lid = canonical_id(cfg_.labels);
+    x_.resize(size_t(n));
+    for (int64_t i = 0; i < n; ++i)
+      x_[size_t(i)] = float(uniform_word(philox_block(cfg_.seed, Stream::Data, xid, uint32_t(i)).w[0]));
+    labels_.resize(size_t(cfg_.batch));
+    for (int64_t i = 0; i < cfg_.batch; ++i) {
+      uint64_t w = philox_block(cfg_.seed, Stream::Data, lid, uint32_t(i)).w[0];
+      labels_[size_t(i)] = int32_t((w * uint64_t(cfg_.classes)) >> 32);
+    }
+  } else {
+    // Zipf(s) over ranks 1..M, rank r -> token first_token + r - 1; the CDF summed ascending in f64.
+    int64_t M = cfg_.vocab - cfg_.first_token;
+    zipf_cdf_.resize(size_t(M));
+    double acc = 0;
+    for (int64_t r = 1; r <= M; ++r) {
+      acc += std::pow(double(r), -cfg_.zipf_s);
+      zipf_cdf_[size_t(r - 1)] = acc;
+    }
+    for (auto& v : zipf_cdf_) v /= acc;
+    zipf_cdf_.back() = 1.0;
+  }
+}
+
+int32_t Feed::zipf(uint64_t step, uint32_t row, uint64_t draw) const {
+  (void)step;
+  double u = uniform_word(philox_block(cfg_.seed, Stream::Data, draw, row).w[0]);
+  auto it = std::lower_bound(zipf_cdf_.begin(), zipf_cdf_.end(), u);
+  int64_t r = int64_t(it - zipf_cdf_.begin());
+  if (r >= int64_t(zipf_cdf_.size())) r = int64_t(zipf_cdf_.size()) - 1;
+  return int32_t(cfg_.first_token + r);
+}
+
+Batch Feed::batch(uint64_t step) const {
+  Batch b;
+  switch (cfg_.feed) {
+    case FeedKind::Teacher:
+      b.f32[cfg_.x] = x_;
+      b.f32[cfg_.y] = target_;
+      break;
+    case FeedKind::Classifier:
+      b.f32[cfg_.x] = x_;
+      b.i32[cfg_.labels] = labels_;
+      b.f32[cfg_.weights].assign(size_t(cfg_.batch), 1.0f);
+      break;
+    case FeedKind::NextToken:
+    case FeedKind::MaskedLm: {
+      int64_t B = cfg_.batch, S = cfg_.seq, N = B * S;
+      uint64_t draw = dropout_id(cfg_.ids, step);  // per-step draw id of the token stream
+      std::vector<int32_t> tokens(static_cast<size_t>(N));
+      for (int64_t r = 0; r < N; ++r) tokens[size_t(r)] = zipf(step, uint32_t(r), draw);
+      std::vector<int32_t> ids(static_cast<size_t>(N)), positions(static_cast<size_t>(N)), labels(static_cast<size_t>(N));
+      std::vector<float> weights(static_cast<size_t>(N)), mask(static_cast<size_t>(N), 1.0f);
+      for (int64_t r = 0; r < N; ++r) positions[size_t(r)] = int32_t(r % S);
+      if (cfg_.feed == FeedKind::NextToken) {
+        for (int64_t r = 0; r < N; ++r) {
+          ids[size_t(r)] = tokens[size_t(r)];
+          bool last = (r % S) == S - 1;
+          labels[size_t(r)] = last ? 0 : tokens[size_t(r + 1)];
+          weights[size_t(r)] = last ? 0.0f : 1.0f;
+        }
+      } else {
+        // dataset/mlm.rs:766-785 with MaskingPolicy::BERT (mlm.rs:67-72), [MASK] = 4, five specials.
+        const double selection = 0.15, mask_fraction = 0.8, random_fraction = 0.1;
+        const uint64_t specials = 5, random_tokens = uint64_t(cfg_.vocab) - specials;
+        for (int64_t r = 0; r < N; ++r) {
+          int32_t label = tokens[size_t(r)];
+          Philox4 w = philox_block(cfg_.seed, Stream::Masking, step, uint32_t(r));
+          bool selected = label >= int32_t(specials) && uniform_word(w.w[0]) < selection;
+          int32_t id;
+          if (!selected) id = label;
+          else if (uniform_word(w.w[1]) < mask_fraction) id = 4;
+          else if (uniform_word(w.w[1]) < mask_fraction + random_fraction)
+            id = int32_t(specials + ((uint64_t(w.w[2]) * random_tokens) >> 32));
+          else id = label;
+          ids[size_t(r)] = id;
+          labels[size_t(r)] = label;
+          weights[size_t(r)] = selected ? 1.0f : 0.0f;
+        }
+      }
+      b.i32[cfg_.ids] = ids;
+      b.i32[cfg_.positions] = positions;
+      b.f32[cfg_.key_mask] = mask;
+      b.i32[cfg_.labels] = labels;
+      b.f32[cfg_.weights] = weights;
+      break;
+    }
+  }
+  return b;
+}
+
+void masked_gather(const std::vector<int32_t>& labels, const std::vector<float>& weights, uint64_t capacity,
+                   uint64_t step, std::vector<int32_t>& rows, std::vector<int32_t>& out_labels,
+                   std::vector<float>& out_weights) {
+  size_t selected = 0;
+  for (float w : weights) selected += w != 0.0f;
+  if (selected > capacity)
+    throw IrError("E-DATA-012: the batch of step " + std::to_string(step) + " has " + std::to_string(selected) +
+                  " rows of non-zero weight, more than the " + std::to_string(capacity) +
+                  " rows the masked-row gather holds");
+  rows.clear();
+  out_labels.clear();
+  out_weights.clear();
+  for (size_t r = 0; r < weights.size(); ++r)
+    if (weights[r] != 0.0f) {
+      rows.push_back(int32_t(r));
+      out_labels.push_back(r < labels.size() ? labels[r] : 0);
+      out_weights.push_back(weights[r]);
+    }
+  rows.resize(capacity, 0);
+  out_labels.resize(capacity, 0);
+  out_weights.resize(capacity, 0.0f);
+}
+
+StepInputs step_inputs(const Compiled& c, const Feed& feed, uint64_t step, uint64_t end) {
+  StepInputs in;
+  in.batch = feed.batch(step);
+  const Program& p = c.step.program;
+  if (const Node* rows = p.input(kMaskedRowsInput)) {
+    const auto& cfg = c.config;
+    std::vector<int32_t> r, l;
+    std::vector<float> w;
+    masked_gather(in.batch.i32.at(cfg.labels), in.batch.f32.at(cfg.weights), uint64_t(rows->ty.count()), step, r, l, w);
+    in.batch.i32[kMaskedRowsInput] = std::move(r);
+    in.batch.i32[std::string(kMaskedLabelsPrefix) + cfg.labels] = std::move(l);
+    in.batch.f32[std::string(kMaskedWeightsPrefix) + cfg.weights] = std::move(w);
+  }
+  for (auto& site : dropout_sites(p)) {
+    int32_t t[2];
+    dropout_token(site, step, t);
+    in.batch.i32[site] = {t[0], t[1]};
+  }
+  if (c.step.rule == Rule::AdamW) {
+    StepScalars s = adamw_scalars(c.step.adamw, c.step.lr, step + 1, end);
+    in.batch.f32[kLrTInput] = {s.lr_t};
+    in.batch.f32[kC1Input] = {s.c1};
+    in.batch.f32[kC2Input] = {s.c2};
+  }
+  return in;
+}
+
+RunResult run(const Compiled& c, Engine& engine, uint64_t steps) {
+  RunResult out;
+  const uint64_t end = steps;
+  if (c.step.rule == Rule::AdamW && steps > 0 && c.step.adamw.warmup_steps >= end)
+    throw IrError("the warmup of " + std::to_string(c.step.adamw.warmup_steps) +
+                  " steps is not shorter than the run of " + std::to_string(end) + " steps");
+  out.initial = initialize(c.forward, c.config.seed, Stream::Init);
+  Feed feed(c);
+  if (feed.needs_teacher()) {
+    auto teacher = initialize(c.forward, c.config.seed, Stream::Teacher);
+    feed.set_target(engine.predict(teacher, feed.batch(0)));
+  }
+  engine.set_params(out.initial);
+  auto t0 = std::chrono::steady_clock::now();
+  for (uint64_t step = 0; step < end; ++step) engine.train_step(step_inputs(c, feed, step, end));
+  out.losses = engine.losses();
+  auto t1 = std::chrono::steady_clock::now();
+  out.train_seconds = std::chrono::duration<double>(t1 - t0).count();
+  Batch last = feed.batch(end);
+  if (const Node* rows = c.step.program.input(kMaskedRowsInput)) {
+    std::vector<int32_t> r, l;
+    std::vector<float> w;
+    masked_gather(last.i32.at(c.config.labels), last.f32.at(c.config.weights), uint64_t(rows->ty.count()), end, r, l, w);
+  }
+  out.losses.push_back(engine.final_loss(last));
+  out.params = engine.params();
+  for (size_t k = 0; k < out.losses.size(); ++k)
+    if (!std::isfinite(out.losses[k])) {
+      out.nonfinite_step = int64_t(k);
+      out.losses.resize(k + 1);
+      break;
+    }
+  return out;
+}
+
+}  // namespace msx

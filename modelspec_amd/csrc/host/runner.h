@@ -1,0 +1,91 @@
+// The host side of a training run: parameter initialization, the synthetic batches of each
+// config, the per-step host inputs (dropout tokens, AdamW scalars, the masked-row gather) and the
+// step loop, over an Engine that executes the compiled step.
+//
+// Restates crates/modelspec-runtime/src/train/runner.rs:365-470 (loop semantics: the loss of
+// step k is the loss before update k; the final loss is the dropout-free forward program on the
+// final parameters), train/init.rs:335-352 (initialize), train/data.rs:189-211 (teacher data),
+// train/masked.rs:58-118 (host gather) and dataset/mlm.rs:717-788 (BERT masking rule).
+#pragma once
+#include <map>
+#include <string>
+#include <vector>
+
+#include "models.h"
+#include "rng.h"
+
+namespace msx {
+
+struct Batch {
+  std::map<std::string, std::vector<float>> f32;
+  std::map<std::string, std::vector<int32_t>> i32;
+};
+
+// Initial parameter values by ParamId: xavier draws on `stream`, zeros, ones (init.rs:335-352).
+std::vector<std::vector<float>> initialize(const Program& p, uint64_t seed, Stream stream);
+
+// The synthetic batch source of a compiled config.
+class Feed {
+ public:
+  explicit Feed(const Compiled& c);
+  // The batch of step `step` (Teacher and Classifier data are the same every step).
+  Batch batch(uint64_t step) const;
+  // Teacher data: the input tensor and the (zero) target before set_target.
+  void set_target(std::vector<float> y) { target_ = std::move(y); }
+  bool needs_teacher() const { return cfg_.feed == FeedKind::Teacher; }
+
+ private:
+  TrainConfig cfg_;
+  std::vector<double> zipf_cdf_;
+  std::vector<float> x_, target_;
+  std::vector<int32_t> labels_;
+  int64_t x_count_ = 0, y_count_ = 0;
+  int32_t zipf(uint64_t step, uint32_t row, uint64_t draw) const;
+};
+
+// The masked-row gather of one batch (train/masked.rs:97-118): rows of non-zero weight
+// ascending, then padding rows 0 / label 0 / weight +0.0 up to `capacity`; more selected rows than
+// the capacity is refused with an IrError naming E-DATA-012.
+void masked_gather(const std::vector<int32_t>& labels, const std::vector<float>& weights, uint64_t capacity,
+                   uint64_t step, std::vector<int32_t>& rows, std::vector<int32_t>& out_labels,
+                   std::vector<float>& out_weights);
+
+// Everything one training step reads besides parameters and moments.
+struct StepInputs {
+  Batch batch;  // declared data, gathered rows, dropout tokens, AdamW scalars, by input name
+};
+
+// Builds the inputs of training step `step` of a run ending at `end` (runner.rs:410-440).
+StepInputs step_inputs(const Compiled& c, const Feed& feed, uint64_t step, uint64_t end);
+
+// What executes the compiled step: the HIP device runtime, or the CPU oracle in tests.
+class Engine {
+ public:
+  virtual ~Engine() = default;
+  // Parameter values by ParamId; AdamW moments restart at zero.
+  virtual void set_params(const std::vector<std::vector<float>>& values) = 0;
+  virtual std::vector<std::vector<float>> params() = 0;
+  // Moments by ParamId (empty for SGD): first then second.
+  virtual std::vector<std::vector<float>> moments(char which) = 0;
+  // The forward program's prediction under `values` on `batch` (synthetic teacher targets).
+  virtual std::vector<float> predict(const std::vector<std::vector<float>>& values, const Batch& batch) = 0;
+  // One training step: loss of the current parameters, then their update. The loss may be
+  // collected later by losses().
+  virtual void train_step(const StepInputs& in) = 0;
+  // The forward program's loss on the current parameters, after every queued step.
+  virtual float final_loss(const Batch& batch) = 0;
+  // The losses of the train steps run since set_params, in order.
+  virtual std::vector<float> losses() = 0;
+};
+
+struct RunResult {
+  std::vector<std::vector<float>> initial;
+  std::vector<float> losses;  // steps + 1
+  std::vector<std::vector<float>> params;
+  double train_seconds = 0;   // wall clock of the step loop (runner.rs loop; train.rs:17-31 --clock)
+  int64_t nonfinite_step = -1;
+};
+
+RunResult run(const Compiled& c, Engine& engine, uint64_t steps);
+
+}  // namespace msx

@@ -1,0 +1,182 @@
+// TEST INFRASTRUCTURE — the CPU oracle's engine and its C API (liboracle.so). Loaded only by
+// tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the checker.
+//
+// The engine runs a compiled training step the way crates/modelspec-runtime/src/train/optimizer.rs
+// (PreparedStep::evaluate_with_ids, Evaluated::apply, lines 137-151 and 443-520) does: evaluate the
+// step program on the inputs, parameters and moments, then take each update and next moment as the
+// new state.
+#include <chrono>
+#include <cstring>
+#include <memory>
+
+#include "../modelspec_amd/csrc/host/runner.h"
+#include "interp.h"
+
+namespace {
+thread_local std::string g_error;
+
+class OracleEngine : public msx::Engine {
+ public:
+  explicit OracleEngine(const msx::Compiled& c) : c_(c) {}
+
+  void set_params(const std::vector<std::vector<float>>& values) override {
+    params_ = values;
+    m_.clear();
+    v_.clear();
+    for (auto& [param, mo] : c_.step.moments) {
+      m_[param].assign(values[param].size(), 0.0f);
+      v_[param].assign(values[param].size(), 0.0f);
+    }
+    losses_.clear();
+  }
+  std::vector<std::vector<float>> params() override { return params_; }
+  std::vector<std::vector<float>> moments(char which) override {
+    std::vector<std::vector<float>> out(params_.size());
+    for (auto& [param, v] : which == 'm' ? m_ : v_) out[param] = v;
+    return out;
+  }
+  std::vector<float> predict(const std::vector<std::vector<float>>& values, const msx::Batch& b) override {
+    oracle::Interpreter it(c_.forward, true, c_.config.seed);
+    it.run(b.f32, b.i32, values);
+    return it.value(c_.prediction);
+  }
+  void train_step(const msx::StepInputs& in) override {
+    const msx::TrainingStep& s = c_.step;
+    auto f32 = in.batch.f32;
+    for (auto& [param, mo] : s.moments) {
+      const std::string& path = s.program.params[param].path;
+      f32[msx::moment_input('m', path)] = m_[param];
+      f32[msx::moment_input('v', path)] = v_[param];
+    }
+    oracle::Interpreter it(s.program, true, c_.config.seed);
+    it.run(f32, in.batch.i32, params_);
+    losses_.push_back(it.value(s.loss)[0]);
+    for (auto& [param, u] : s.updates) params_[param] = it.value(u);
+    for (auto& [param, mo] : s.moments) {
+      m_[param] = it.value(mo.m_next);
+      v_[param] = it.value(mo.v_next);
+    }
+  }
+  float final_loss(const msx::Batch& b) override {
+    oracle::Interpreter it(c_.forward, true, c_.config.seed);
+    it.run(b.f32, b.i32, params_);
+    return it.value(c_.forward.outputs[0])[0];
+  }
+  std::vector<float> losses() override { return losses_; }
+
+ private:
+  const msx::Compiled& c_;
+  std::vector<std::vector<float>> params_;
+  std::map<uint32_t, std::vector<float>> m_, v_;
+  std::vector<float> losses_;
+};
+
+struct Prog {
+  msx::Program program;
+  std::unique_ptr<oracle::Interpreter> interp;
+  bool has_seed;
+  uint64_t seed;
+};
+}  // namespace
+
+extern "C" {
+
+const char* orc_last_error() { return g_error.c_str(); }
+
+// Trains `config` for `steps` steps (negative: the config's own) and writes steps + 1 losses and
+// the final parameters, concatenated in ParamId order. Returns 0, or -1 with orc_last_error().
+int orc_train(const char* config, int64_t steps, int64_t masked_rows, float* losses, uint64_t losses_len,
+              float* params_out, uint64_t params_len, double* train_seconds) {
+  try {
+    msx::Compiled c = msx::compile_config(config, masked_rows, steps);
+    OracleEngine e(c);
+    msx::RunResult r = msx::run(c, e, c.config.steps);
+    if (r.nonfinite_step >= 0) { g_error = "E-TRAIN-001: non-finite loss at step " + std::to_string(r.nonfinite_step); return -1; }
+    if (losses_len < r.losses.size()) { g_error = "losses buffer too small"; return -1; }
+    std::memcpy(losses, r.losses.data(), r.losses.size() * sizeof(float));
+    uint64_t off = 0;
+    for (auto& p : r.params) {
+      if (off + p.size() > params_len) { g_error = "params buffer too small"; return -1; }
+      std::memcpy(params_out + off, p.data(), p.size() * sizeof(float));
+      off += p.size();
+    }
+    if (train_seconds) *train_seconds = r.train_seconds;
+    return 0;
+  } catch (const std::exception& ex) {
+    g_error = ex.what();
+    return -1;
+  }
+}
+
+// Times `steps` training steps of `config` on this thread; writes seconds per step.
+int orc_time_steps(const char* config, int64_t steps, int64_t masked_rows, double* seconds_per_step) {
+  try {
+    msx::Compiled c = msx::compile_config(config, masked_rows, -1);
+    OracleEngine e(c);
+    msx::Feed feed(c);
+    if (feed.needs_teacher()) feed.set_target(e.predict(msx::initialize(c.forward, c.config.seed, msx::Stream::Teacher), feed.batch(0)));
+    e.set_params(msx::initialize(c.forward, c.config.seed, msx::Stream::Init));
+    std::vector<msx::StepInputs> ins;
+    for (int64_t s = 0; s < steps; ++s) ins.push_back(msx::step_inputs(c, feed, uint64_t(s), c.config.steps));
+    auto t0 = std::chrono::steady_clock::now();
+    for (auto& in : ins) e.train_step(in);
+    auto t1 = std::chrono::steady_clock::now();
+    *seconds_per_step = std::chrono::duration<double>(t1 - t0).count() / double(steps);
+    return 0;
+  } catch (const std::exception& ex) {
+    g_error = ex.what();
+    return -1;
+  }
+}
+
+void* orc_prog_new(const char* program_text, int has_seed, uint64_t seed) {
+  try {
+    auto* p = new Prog;
+    p->program = msx::parse_program(program_text);
+    p->has_seed = has_seed != 0;
+    p->seed = seed;
+    return p;
+  } catch (const std::exception& ex) {
+    g_error = ex.what();
+    return nullptr;
+  }
+}
+
+void orc_prog_free(void* h) { delete static_cast<Prog*>(h); }
+
+// dtypes: 0 = f32, 1 = i32. Params by ParamId.
+int orc_prog_run(void* h, int n_in, const char** names, const int* dtypes, const void** data, const uint64_t* counts,
+                 int n_params, const float** params, const uint64_t* pcounts) {
+  try {
+    auto* p = static_cast<Prog*>(h);
+    std::map<std::string, std::vector<float>> f32;
+    std::map<std::string, std::vector<int32_t>> i32;
+    for (int k = 0; k < n_in; ++k) {
+      if (dtypes[k] == 0) f32[names[k]].assign(static_cast<const float*>(data[k]), static_cast<const float*>(data[k]) + counts[k]);
+      else i32[names[k]].assign(static_cast<const int32_t*>(data[k]), static_cast<const int32_t*>(data[k]) + counts[k]);
+    }
+    std::vector<std::vector<float>> ps;
+    for (int k = 0; k < n_params; ++k) ps.emplace_back(params[k], params[k] + pcounts[k]);
+    p->interp = std::make_unique<oracle::Interpreter>(p->program, p->has_seed, p->seed);
+    p->interp->run(f32, i32, ps);
+    return 0;
+  } catch (const std::exception& ex) {
+    g_error = ex.what();
+    return -1;
+  }
+}
+
+int orc_prog_output(void* h, int k, float* out, uint64_t count) {
+  try {
+    auto* p = static_cast<Prog*>(h);
+    const auto& v = p->interp->value(p->program.outputs.at(size_t(k)));
+    if (v.size() != count) { g_error = "output size mismatch"; return -1; }
+    std::memcpy(out, v.data(), count * sizeof(float));
+    return 0;
+  } catch (const std::exception& ex) {
+    g_error = ex.what();
+    return -1;
+  }
+}
+
+}  // extern "C"
