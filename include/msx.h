@@ -1,0 +1,106 @@
+/* modelspec-hip: the C ABI of the MI355X training-step backend (libmsx.so).
+ *
+ * The reference host (crates/modelspec-cli/src/train.rs:1045-1200, Backend at :577-584) calls
+ * its Vulkan runner through Rust functions; this header is the surface an `extern "C"` FFI crate
+ * binds in their place for `train --backend hip`. Conventions: every function returns 0 or a
+ * negative status (MSX_E_*), with msx_last_error() holding the message of the calling thread's
+ * last failure; no exception crosses the ABI; every host pointer is caller-owned and read only
+ * during the call; one context per thread.
+ */
+#ifndef MSX_H
+#define MSX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSX_OK 0
+#define MSX_E_INVALID -1     /* malformed IR, a shape or name the step does not declare */
+#define MSX_E_DATA -2        /* E-DATA-011 / E-DATA-012: ids, labels, weights, masks, gather capacity */
+#define MSX_E_DEVICE -3      /* E-TARGET-002/003: no HIP runtime or no such device */
+#define MSX_E_NONFINITE -4   /* E-TRAIN-001: a loss stopped being finite */
+#define MSX_E_UNSUPPORTED -5 /* a step op or shape this backend has no kernel for */
+
+typedef struct msx_ctx msx_ctx;
+
+/* A named host tensor: dtype 0 = f32, 1 = i32; `count` elements at `data`. */
+typedef struct {
+  const char* name;
+  int32_t dtype;
+  const void* data;
+  uint64_t count;
+} msx_tensor;
+
+typedef struct {
+  uint64_t steps;
+  uint64_t graph_launches;
+  uint64_t kernels_per_step;
+  uint64_t bytes_uploaded;
+  uint64_t device_bytes;
+} msx_run_stats;
+
+/* The message of this thread's last failure ("" after a success). */
+const char* msx_last_error(void);
+
+/* Number of visible HIP devices (0 when the runtime finds none). */
+int msx_device_count(void);
+
+/* Compiles a built-in config (linear_regression, mlp_classifier, transformer_block, bert_tiny,
+ * bert_cpu, bert_micro, block_micro, mlp_micro) to the printed training step and forward program
+ * (ir/print.rs text). masked_rows / steps < 0 take the config's own. Free both with msx_free.
+ * Replaces compile::compile_training_with, crates/modelspec-core/src/compile.rs:85-118. */
+int msx_compile_config(const char* config, int64_t masked_rows, int64_t steps, char** step_ir, char** forward_ir);
+void msx_free(void* p);
+
+/* Opens device `device`. Replaces vulkan::on_device (crates/modelspec-runtime/src/vulkan/mod.rs:216-552). */
+int msx_open(int device, msx_ctx** out);
+void msx_close(msx_ctx* ctx);
+
+/* Loads a training step (the text of `modelspec ir --stage training` with its optimizer) and the
+ * dropout-free forward program, plans them, and allocates every device buffer of the run.
+ * `prediction_output` is the index in the forward program's outputs of the model prediction.
+ * Replaces stepwise::train_stepwise_on_device's set-up (vulkan/stepwise.rs:289-400). */
+int msx_load(msx_ctx* ctx, const char* step_ir, const char* forward_ir, uint64_t seed, uint32_t prediction_output);
+
+/* Uploads every parameter (ParamId order, `n` arrays of counts[i] floats) and zeroes the AdamW
+ * moments and the loss log. Replaces the parameter upload of vulkan/stepwise.rs:343-400. */
+int msx_set_params(msx_ctx* ctx, const float* const* values, const uint64_t* counts, uint32_t n);
+int msx_read_param(msx_ctx* ctx, uint32_t param, float* out, uint64_t count);
+/* which = 'm' or 'v'. */
+int msx_read_moment(msx_ctx* ctx, uint32_t param, int32_t which, float* out, uint64_t count);
+
+/* Runs `n` training steps. Step i reads the n_inputs[i] tensors at inputs[i]: the batch, the
+ * masked-row gather, one i32[2] token per dropout site and, under AdamW, optimizer.lr_t / c1 / c2
+ * (the inputs the reference host feeds per step, vulkan/stepwise.rs:1454-1551). The losses of the
+ * n steps are written to losses_out (may be null). */
+int msx_run_steps(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, const uint32_t* n_inputs, float* losses_out);
+
+/* The forward program on the current parameters: its loss, and the prediction if requested. */
+int msx_forward(msx_ctx* ctx, const msx_tensor* inputs, uint32_t n_inputs, float* loss_out, float* prediction_out,
+                uint64_t prediction_count);
+
+int msx_stats(msx_ctx* ctx, msx_run_stats* out);
+
+/* A whole run of a built-in config on the context's device: initial parameters from the seed,
+ * synthetic batches, `steps` steps (negative: the config's own), the final loss. Writes steps + 1
+ * losses and the final parameters concatenated in ParamId order. Replaces the device branch of
+ * crates/modelspec-cli/src/train.rs:1045-1200 with runner::run_checked's loop semantics. */
+int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t masked_rows, float* losses,
+                     uint64_t losses_len, float* params, uint64_t params_len, double* train_seconds);
+
+/* One program (print.rs text of a Tensor IR program) on the device, for per-op tests: inputs by
+ * name, parameters by ParamId; output k read back with msx_prog_output. */
+typedef struct msx_prog msx_prog;
+int msx_prog_new(msx_ctx* ctx, const char* program_text, uint64_t seed, msx_prog** out);
+int msx_prog_run(msx_prog* prog, const msx_tensor* inputs, uint32_t n_inputs, const float* const* params,
+                 const uint64_t* param_counts, uint32_t n_params);
+int msx_prog_output(msx_prog* prog, uint32_t k, float* out, uint64_t count);
+void msx_prog_free(msx_prog* prog);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,234 @@
+"""ctypes bindings of libmsx.so (include/msx.h).
+
+Loading fails loudly when the library is missing: there is no CPU fallback in this package.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmsx.so")
+
+CONFIGS = ("linear_regression", "mnist_mlp", "mlp_classifier", "transformer_block", "bert_tiny",
+           "bert_cpu", "bert_micro", "block_micro", "mlp_micro")
+
+STATUS = {0: "ok", -1: "invalid", -2: "data", -3: "device", -4: "nonfinite", -5: "unsupported"}
+
+
+class MsxError(RuntimeError):
+    def __init__(self, code, message):
+        super().__init__(f"{STATUS.get(code, code)}: {message}")
+        self.code = code
+
+
+class Tensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_int32), ("data", ctypes.c_void_p),
+                ("count", ctypes.c_uint64)]
+
+
+class RunStats(ctypes.Structure):
+    _fields_ = [("steps", ctypes.c_uint64), ("graph_launches", ctypes.c_uint64),
+                ("kernels_per_step", ctypes.c_uint64), ("bytes_uploaded", ctypes.c_uint64),
+                ("device_bytes", ctypes.c_uint64)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MsxError(-3, f"{LIB_PATH} is not built: run `python -m modelspec_amd.build` (hipcc, gfx950)")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, c64, u64, u32, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int32
+        L.msx_last_error.restype = ctypes.c_char_p
+        L.msx_compile_config.argtypes = [ctypes.c_char_p, c64, c64, ctypes.POINTER(vp), ctypes.POINTER(vp)]
+        L.msx_free.argtypes = [vp]
+        L.msx_open.argtypes = [ctypes.c_int, ctypes.POINTER(vp)]
+        L.msx_close.argtypes = [vp]
+        L.msx_load.argtypes = [vp, ctypes.c_char_p, ctypes.c_char_p, u64, u32]
+        L.msx_set_params.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(u64), u32]
+        L.msx_read_param.argtypes = [vp, u32, vp, u64]
+        L.msx_read_moment.argtypes = [vp, u32, i32, vp, u64]
+        L.msx_run_steps.argtypes = [vp, u32, ctypes.POINTER(ctypes.POINTER(Tensor)), ctypes.POINTER(u32), vp]
+        L.msx_forward.argtypes = [vp, ctypes.POINTER(Tensor), u32, vp, vp, u64]
+        L.msx_stats.argtypes = [vp, ctypes.POINTER(RunStats)]
+        L.msx_train_config.argtypes = [vp, ctypes.c_char_p, c64, c64, vp, u64, vp, u64, ctypes.POINTER(ctypes.c_double)]
+        L.msx_prog_new.argtypes = [vp, ctypes.c_char_p, u64, ctypes.POINTER(vp)]
+        L.msx_prog_run.argtypes = [vp, ctypes.POINTER(Tensor), u32, ctypes.POINTER(vp), ctypes.POINTER(u64), u32]
+        L.msx_prog_output.argtypes = [vp, u32, vp, u64]
+        L.msx_prog_free.argtypes = [vp]
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc != 0:
+        raise MsxError(rc, lib().msx_last_error().decode())
+
+
+def device_count():
+    return lib().msx_device_count()
+
+
+def compile_config(name, masked_rows=-1, steps=-1):
+    """The printed training step and forward program of a built-in config."""
+    s, f = ctypes.c_void_p(), ctypes.c_void_p()
+    _check(lib().msx_compile_config(name.encode(), masked_rows, steps, ctypes.byref(s), ctypes.byref(f)))
+    try:
+        return ctypes.string_at(s).decode(), ctypes.string_at(f).decode()
+    finally:
+        lib().msx_free(s)
+        lib().msx_free(f)
+
+
+def _tensors(named):
+    """(ctypes array, keepalive) of msx_tensor from {name: ndarray}."""
+    keep, arr = [], (Tensor * max(1, len(named)))()
+    for i, (name, a) in enumerate(named.items()):
+        a = np.ascontiguousarray(a)
+        if a.dtype == np.float32:
+            dt = 0
+        elif a.dtype == np.int32:
+            dt = 1
+        else:
+            raise TypeError(f"input {name}: dtype {a.dtype} is neither float32 nor int32")
+        nb = name.encode()
+        keep += [a, nb]
+        arr[i] = Tensor(nb, dt, a.ctypes.data, a.size)
+    return arr, keep
+
+
+class Program:
+    """One Tensor IR program on the device (per-op parity tests)."""
+
+    def __init__(self, ctx, text, seed=0):
+        self._h = ctypes.c_void_p()
+        _check(lib().msx_prog_new(ctx._h, text.encode(), seed, ctypes.byref(self._h)))
+
+    def run(self, inputs, params=()):
+        arr, keep = _tensors(inputs)
+        ps = [np.ascontiguousarray(p, np.float32) for p in params]
+        pv = (ctypes.c_void_p * max(1, len(ps)))(*[p.ctypes.data for p in ps])
+        pc = (ctypes.c_uint64 * max(1, len(ps)))(*[p.size for p in ps])
+        _check(lib().msx_prog_run(self._h, arr, len(inputs), pv, pc, len(ps)))
+
+    def output(self, k, count):
+        out = np.empty(count, np.float32)
+        _check(lib().msx_prog_output(self._h, k, out.ctypes.data, count))
+        return out
+
+    def close(self):
+        if self._h:
+            lib().msx_prog_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+
+class Context:
+    """A device context: msx_open / msx_close."""
+
+    def __init__(self, device=0):
+        self._h = ctypes.c_void_p()
+        _check(lib().msx_open(device, ctypes.byref(self._h)))
+
+    def close(self):
+        if self._h:
+            lib().msx_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def load(self, step_ir, forward_ir, seed, prediction_output=1):
+        _check(lib().msx_load(self._h, step_ir.encode(), forward_ir.encode(), seed, prediction_output))
+
+    def set_params(self, values):
+        vs = [np.ascontiguousarray(v, np.float32) for v in values]
+        pv = (ctypes.c_void_p * len(vs))(*[v.ctypes.data for v in vs])
+        pc = (ctypes.c_uint64 * len(vs))(*[v.size for v in vs])
+        _check(lib().msx_set_params(self._h, pv, pc, len(vs)))
+
+    def read_param(self, k, count):
+        out = np.empty(count, np.float32)
+        _check(lib().msx_read_param(self._h, k, out.ctypes.data, count))
+        return out
+
+    def read_moment(self, k, which, count):
+        out = np.empty(count, np.float32)
+        _check(lib().msx_read_moment(self._h, k, ord(which), out.ctypes.data, count))
+        return out
+
+    def run_steps(self, per_step):
+        """per_step: list of {name: ndarray}; returns the losses."""
+        n = len(per_step)
+        arrs, keep = [], []
+        for named in per_step:
+            a, k = _tensors(named)
+            arrs.append(a)
+            keep += k
+        ptrs = (ctypes.POINTER(Tensor) * n)(*[ctypes.cast(a, ctypes.POINTER(Tensor)) for a in arrs])
+        counts = (ctypes.c_uint32 * n)(*[len(d) for d in per_step])
+        losses = np.empty(n, np.float32)
+        _check(lib().msx_run_steps(self._h, n, ptrs, counts, losses.ctypes.data))
+        return losses
+
+    def forward(self, inputs, prediction_count=0):
+        arr, keep = _tensors(inputs)
+        loss = ctypes.c_float()
+        pred = np.empty(prediction_count, np.float32) if prediction_count else None
+        _check(lib().msx_forward(self._h, arr, len(inputs), ctypes.addressof(loss),
+                                 pred.ctypes.data if pred is not None else None, prediction_count))
+        return loss.value, pred
+
+    def stats(self):
+        s = RunStats()
+        _check(lib().msx_stats(self._h, ctypes.byref(s)))
+        return {f: getattr(s, f) for f, _ in RunStats._fields_}
+
+    def train_config(self, name, steps=-1, masked_rows=-1, n_params=None):
+        """A whole synthetic run of a built-in config: (losses[steps+1], flat params, seconds)."""
+        step_ir, _ = compile_config(name, masked_rows, steps)
+        if n_params is None:
+            n_params = param_count(step_ir)
+        n_steps = steps if steps >= 0 else config_steps(name)
+        losses = np.zeros(n_steps + 1, np.float32)
+        params = np.zeros(n_params, np.float32)
+        secs = ctypes.c_double()
+        _check(lib().msx_train_config(self._h, name.encode(), steps, masked_rows, losses.ctypes.data, losses.size,
+                                      params.ctypes.data, params.size, ctypes.byref(secs)))
+        return losses, params, secs.value
+
+    def program(self, text, seed=0):
+        return Program(self, text, seed)
+
+
+def param_shapes(step_ir):
+    """[(path, shape)] of the `param` lines of a printed step, in ParamId order."""
+    out = []
+    for line in step_ir.splitlines():
+        if line.startswith("param @"):
+            path = line[len("param @"):line.index(":")]
+            dims = line[line.index("[") + 1:line.index("]")]
+            shape = tuple(int(d) for d in dims.split(",")) if dims.strip() else ()
+            out.append((path, shape))
+    return out
+
+
+def param_count(step_ir):
+    return int(sum(int(np.prod(s)) for _, s in param_shapes(step_ir)))
+
+
+_STEPS = {"linear_regression": 500, "mnist_mlp": 1800, "mlp_classifier": 1000, "mlp_micro": 20,
+          "transformer_block": 500, "block_micro": 20, "bert_tiny": 1000, "bert_cpu": 800, "bert_micro": 20}
+
+
+def config_steps(name):
+    return _STEPS[name]

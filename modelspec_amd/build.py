@@ -1,0 +1,65 @@
+"""Builds libmsx.so (host runtime + gfx950 kernels, one hipcc invocation) in-tree.
+
+The shared library is the product: the C ABI of include/msx.h over the HIP runtime. Every
+source is compiled with -ffp-contract=off (no fusion the source does not write) and the packed
+FP32 instructions disabled; kernels target gfx950 only.
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libmsx.so")
+SOURCES = [
+    "capi.cpp",
+    "host/ir.cpp",
+    "host/passes.cpp",
+    "host/rng.cpp",
+    "host/models.cpp",
+    "host/runner.cpp",
+    "hip/runtime.cpp",
+    "hip/kernels.hip",
+]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = [
+    "-std=c++17", "-O3", "-fPIC", "-shared", "--offload-arch=gfx950",
+    "-ffp-contract=off", "-fno-fast-math",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-parameter", "-Wno-unused-result",
+]
+
+
+def build(verbose=False):
+    objs = []
+    build_dir = os.path.join(HERE, "_build")
+    os.makedirs(build_dir, exist_ok=True)
+    procs = []
+    for src in SOURCES:
+        path = os.path.join(CSRC, src)
+        obj = os.path.join(build_dir, src.replace("/", "_") + ".o")
+        lang = ["-x", "hip"] if src.endswith((".hip", "runtime.cpp", "capi.cpp")) else []
+        cmd = [HIPCC] + [f for f in FLAGS if f != "-shared"] + ["-c"] + lang + [path, "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
+        objs.append(obj)
+    failed = []
+    for src, p in procs:
+        out, _ = p.communicate()
+        text = out.decode(errors="replace")
+        if p.returncode != 0:
+            failed.append((src, text))
+        elif verbose and text.strip():
+            print(text)
+    if failed:
+        for src, text in failed:
+            sys.stderr.write(f"--- {src}\n{text}\n")
+        raise RuntimeError("hipcc failed for " + ", ".join(s for s, _ in failed))
+    cmd = [HIPCC] + FLAGS + objs + ["-o", LIB]
+    subprocess.run(cmd, check=True)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

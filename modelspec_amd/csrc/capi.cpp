@@ -1,0 +1,277 @@
+// The C ABI of libmsx.so (include/msx.h): status codes, no exception across the boundary.
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+
+#include "../../include/msx.h"
+#include "hip/runtime.h"
+#include "host/models.h"
+#include "host/runner.h"
+
+namespace {
+thread_local std::string g_error;
+
+int fail(int code, const std::string& what) {
+  g_error = what;
+  return code;
+}
+
+// Runs `f`, mapping the exceptions of the host and device layers to status codes.
+template <class F>
+int guarded(F&& f) {
+  try {
+    g_error.clear();
+    return f();
+  } catch (const msx::HipError& e) {
+    return fail(MSX_E_DEVICE, e.what());
+  } catch (const msx::IrError& e) {
+    std::string w = e.what();
+    if (w.find("E-DATA-") != std::string::npos || w.find("key mask") != std::string::npos ||
+        w.find("loss weight") != std::string::npos)
+      return fail(MSX_E_DATA, w);
+    if (w.find("no HIP kernel") != std::string::npos || w.find("not the AdamW/SGD template") != std::string::npos)
+      return fail(MSX_E_UNSUPPORTED, w);
+    return fail(MSX_E_INVALID, w);
+  } catch (const std::exception& e) {
+    std::string w = e.what();
+    if (w.find("kernel launch refused") != std::string::npos) return fail(MSX_E_UNSUPPORTED, w);
+    return fail(MSX_E_INVALID, w);
+  }
+}
+
+char* dup(const std::string& s) {
+  char* p = static_cast<char*>(std::malloc(s.size() + 1));
+  std::memcpy(p, s.c_str(), s.size() + 1);
+  return p;
+}
+
+msx::Batch batch_of(const msx_tensor* t, uint32_t n) {
+  msx::Batch b;
+  for (uint32_t i = 0; i < n; ++i) {
+    if (!t[i].name) throw msx::IrError("an input has no name");
+    if (t[i].dtype == 0) {
+      auto* f = static_cast<const float*>(t[i].data);
+      b.f32[t[i].name].assign(f, f + t[i].count);
+    } else if (t[i].dtype == 1) {
+      auto* v = static_cast<const int32_t*>(t[i].data);
+      b.i32[t[i].name].assign(v, v + t[i].count);
+    } else {
+      throw msx::IrError(std::string("input `") + t[i].name + "` has an unknown dtype");
+    }
+  }
+  return b;
+}
+}  // namespace
+
+struct msx_ctx {
+  int device = 0;
+  std::unique_ptr<msx::Session> session;
+  msx::TrainingStep step;
+  msx::Program forward;
+};
+
+struct msx_prog {
+  std::unique_ptr<msx::Session> session;
+  msx::Program program;
+};
+
+extern "C" {
+
+const char* msx_last_error(void) { return g_error.c_str(); }
+
+int msx_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+int msx_compile_config(const char* config, int64_t masked_rows, int64_t steps, char** step_ir, char** forward_ir) {
+  return guarded([&] {
+    msx::Compiled c = msx::compile_config(config, masked_rows, steps);
+    if (step_ir) *step_ir = dup(msx::print_step(c.step));
+    if (forward_ir) *forward_ir = dup(msx::print_program(c.forward));
+    return MSX_OK;
+  });
+}
+
+void msx_free(void* p) { std::free(p); }
+
+int msx_open(int device, msx_ctx** out) {
+  return guarded([&] {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(MSX_E_DEVICE, "E-TARGET-002: no HIP device is visible");
+    if (device < 0 || device >= n) return fail(MSX_E_DEVICE, "E-TARGET-003: no HIP device " + std::to_string(device));
+    msx::hip_check(hipSetDevice(device), "hipSetDevice");
+    auto* c = new msx_ctx;
+    c->device = device;
+    *out = c;
+    return MSX_OK;
+  });
+}
+
+void msx_close(msx_ctx* ctx) {
+  try {
+    delete ctx;
+  } catch (...) {
+  }
+}
+
+int msx_load(msx_ctx* ctx, const char* step_ir, const char* forward_ir, uint64_t seed, uint32_t prediction_output) {
+  return guarded([&] {
+    ctx->session.reset();
+    ctx->step = msx::parse_step(step_ir);
+    if (!ctx->step.has_optimizer) return fail(MSX_E_INVALID, "the step IR has no optimizer");
+    ctx->forward = msx::parse_program(forward_ir);
+    if (prediction_output >= ctx->forward.outputs.size()) return fail(MSX_E_INVALID, "no such forward output");
+    ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, seed,
+                                                  ctx->forward.outputs[prediction_output]);
+    return MSX_OK;
+  });
+}
+
+int msx_set_params(msx_ctx* ctx, const float* const* values, const uint64_t* counts, uint32_t n) {
+  return guarded([&] {
+    if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
+    std::vector<std::vector<float>> v;
+    for (uint32_t i = 0; i < n; ++i) v.emplace_back(values[i], values[i] + counts[i]);
+    ctx->session->set_params(v);
+    return MSX_OK;
+  });
+}
+
+int msx_read_param(msx_ctx* ctx, uint32_t param, float* out, uint64_t count) {
+  return guarded([&] {
+    if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
+    auto all = ctx->session->params();
+    if (param >= all.size() || all[param].size() != count) return fail(MSX_E_INVALID, "no such parameter or wrong count");
+    std::memcpy(out, all[param].data(), count * 4);
+    return MSX_OK;
+  });
+}
+
+int msx_read_moment(msx_ctx* ctx, uint32_t param, int32_t which, float* out, uint64_t count) {
+  return guarded([&] {
+    if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
+    auto all = ctx->session->moments(char(which));
+    if (param >= all.size() || all[param].size() != count) return fail(MSX_E_INVALID, "no such moment or wrong count");
+    std::memcpy(out, all[param].data(), count * 4);
+    return MSX_OK;
+  });
+}
+
+int msx_run_steps(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, const uint32_t* n_inputs, float* losses_out) {
+  return guarded([&] {
+    if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
+    size_t before = ctx->session->losses().size();
+    for (uint32_t i = 0; i < n; ++i) {
+      msx::StepInputs in;
+      in.batch = batch_of(inputs[i], n_inputs[i]);
+      ctx->session->train_step(in);
+    }
+    auto all = ctx->session->losses();
+    if (losses_out)
+      for (uint32_t i = 0; i < n; ++i) losses_out[i] = all.at(before + i);
+    for (uint32_t i = 0; i < n; ++i)
+      if (!std::isfinite(all.at(before + i)))
+        return fail(MSX_E_NONFINITE, "E-TRAIN-001: the loss of step " + std::to_string(before + i) + " is not finite");
+    return MSX_OK;
+  });
+}
+
+int msx_forward(msx_ctx* ctx, const msx_tensor* inputs, uint32_t n_inputs, float* loss_out, float* prediction_out,
+                uint64_t prediction_count) {
+  return guarded([&] {
+    if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
+    msx::Batch b = batch_of(inputs, n_inputs);
+    float loss = ctx->session->final_loss(b);
+    if (loss_out) *loss_out = loss;
+    if (prediction_out) {
+      uint32_t pred = 0;
+      for (auto o : ctx->forward.outputs)
+        if (o != ctx->forward.outputs[0]) pred = o;
+      if (ctx->forward.node(pred).ty.count() != int64_t(prediction_count)) return fail(MSX_E_INVALID, "prediction count");
+      msx::hip_check(hipMemcpy(prediction_out, ctx->session->forward_value(pred), prediction_count * 4, hipMemcpyDeviceToHost),
+                     "hipMemcpy (prediction)");
+    }
+    return MSX_OK;
+  });
+}
+
+int msx_stats(msx_ctx* ctx, msx_run_stats* out) {
+  return guarded([&] {
+    if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
+    const auto& s = ctx->session->stats();
+    out->steps = s.steps;
+    out->graph_launches = s.graph_launches;
+    out->kernels_per_step = s.kernels_per_step;
+    out->bytes_uploaded = s.bytes_uploaded;
+    out->device_bytes = s.device_bytes;
+    return MSX_OK;
+  });
+}
+
+int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t masked_rows, float* losses,
+                     uint64_t losses_len, float* params, uint64_t params_len, double* train_seconds) {
+  return guarded([&] {
+    msx::Compiled c = msx::compile_config(config, masked_rows, steps);
+    ctx->session.reset();
+    ctx->step = c.step;
+    ctx->forward = c.forward;
+    ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction);
+    msx::RunResult r = msx::run(c, *ctx->session, c.config.steps);
+    if (losses_len < r.losses.size()) return fail(MSX_E_INVALID, "losses buffer too small");
+    std::memcpy(losses, r.losses.data(), r.losses.size() * 4);
+    uint64_t off = 0;
+    for (auto& p : r.params) {
+      if (off + p.size() > params_len) return fail(MSX_E_INVALID, "params buffer too small");
+      std::memcpy(params + off, p.data(), p.size() * 4);
+      off += p.size();
+    }
+    if (train_seconds) *train_seconds = r.train_seconds;
+    if (r.nonfinite_step >= 0)
+      return fail(MSX_E_NONFINITE, "E-TRAIN-001: the loss of step " + std::to_string(r.nonfinite_step) + " is not finite");
+    return MSX_OK;
+  });
+}
+
+int msx_prog_new(msx_ctx* ctx, const char* program_text, uint64_t seed, msx_prog** out) {
+  return guarded([&] {
+    auto pr = std::make_unique<msx_prog>();
+    pr->program = msx::parse_program(program_text);
+    msx::TrainingStep none;
+    none.program = pr->program;
+    none.loss = pr->program.outputs.at(0);
+    pr->session = std::make_unique<msx::Session>(ctx->device, none, pr->program, seed, pr->program.outputs.at(0));
+    *out = pr.release();
+    return MSX_OK;
+  });
+}
+
+int msx_prog_run(msx_prog* prog, const msx_tensor* inputs, uint32_t n_inputs, const float* const* params,
+                 const uint64_t* param_counts, uint32_t n_params) {
+  return guarded([&] {
+    std::vector<std::vector<float>> v;
+    for (uint32_t i = 0; i < n_params; ++i) v.emplace_back(params[i], params[i] + param_counts[i]);
+    prog->session->load_params(v);
+    prog->session->run_forward(batch_of(inputs, n_inputs));
+    return MSX_OK;
+  });
+}
+
+int msx_prog_output(msx_prog* prog, uint32_t k, float* out, uint64_t count) {
+  return guarded([&] {
+    uint32_t v = prog->program.outputs.at(k);
+    if (prog->program.node(v).ty.count() != int64_t(count)) return fail(MSX_E_INVALID, "output count");
+    msx::hip_check(hipMemcpy(out, prog->session->forward_value(v), count * 4, hipMemcpyDeviceToHost), "hipMemcpy (output)");
+    return MSX_OK;
+  });
+}
+
+void msx_prog_free(msx_prog* prog) {
+  try {
+    delete prog;
+  } catch (...) {
+  }
+}
+
+}  // extern "C"

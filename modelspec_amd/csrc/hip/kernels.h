@@ -1,0 +1,90 @@
+// Launchers of the CDNA4 (gfx950) kernels of the training step. Every launcher checks the shape
+// assumptions of its kernel on the host before launching and enqueues on `s`.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace msx::hk {
+
+// Sets the launch attributes some kernels need (large dynamic LDS). Call once per process and
+// device before launching, never during stream capture.
+void prepare();
+
+enum EwOp : int { EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_RELU, EW_RELU_GRAD, EW_GELU, EW_GELU_GRAD, EW_SQRT, EW_COPY };
+
+// o[i] = op(a[a_scalar ? 0 : i], b[b_scalar ? 0 : i]) for i < n (binary ops), op(a[i]) for unary.
+void elementwise(hipStream_t s, int op, const float* a, const float* b, float* o, int64_t n, bool a_scalar, bool b_scalar);
+void fill_from(hipStream_t s, const float* scalar, float* o, int64_t n);  // BroadcastScalar
+void fill_zero(hipStream_t s, void* o, int64_t bytes);                     // kernel, not a memset
+void copy(hipStream_t s, const float* a, float* o, int64_t n);
+
+// C[M,N] = op(A) op(B) (+ bias[N]); A is [M,K] row-major with leading dimension lda, or [K,M]
+// (read transposed) when ta; B is [K,N], or [N,K] when tb. When `pre` is non-null the kernel writes
+// the biased value there too and `out` gets GELU of it (act = 1) or ReLU (act = 2).
+// `workspace` (split_k * M * N floats) takes split-K partials, summed in slice order.
+struct GemmArgs {
+  const float* a; const float* b; float* c; const float* bias;
+  int64_t m, n, k, lda, ldb, ldc;
+  bool ta, tb;
+  float* workspace; int64_t workspace_floats;
+};
+int gemm_split_for(int64_t m, int64_t n, int64_t k);  // the split-K factor the launcher uses
+void gemm(hipStream_t s, const GemmArgs& g);
+
+void transpose(hipStream_t s, const float* a, float* o, int64_t rows, int64_t cols);  // a [rows,cols] -> o [cols,rows]
+
+void add_rows(hipStream_t s, const float* x, const float* bias, float* o, int64_t rows, int64_t h);
+// out[c] = sum over rows of x[r, c] (optionally times xhat from stats); partial = [chunks, h].
+void column_sum(hipStream_t s, const float* x, float* out, int64_t rows, int64_t h, float* partial, int64_t partial_floats);
+void ln_grad_gamma(hipStream_t s, const float* x, const float* g, const float* stats, float* out, int64_t rows,
+                   int64_t h, float* partial, int64_t partial_floats);
+int64_t column_chunks(int64_t rows, int64_t h);
+
+// LayerNorm family, eps 1e-12. stats = [rows, 2] (mean, rstd).
+void ln_stats(hipStream_t s, const float* x, float* stats, int64_t rows, int64_t h);
+void layer_norm(hipStream_t s, const float* x, const float* gamma, const float* beta, float* y, float* stats,
+                int64_t rows, int64_t h);
+void ln_grad_x(hipStream_t s, const float* x, const float* gamma, const float* g, const float* stats, float* dx,
+               int64_t rows, int64_t h);
+
+void embedding(hipStream_t s, const float* table, const int32_t* ids, float* o, int64_t n, int64_t rows, int64_t h);
+// Deterministic sorted-segment scatter: out = 0; out[ids[k]] += g[k] in ascending k.
+// keys: n 64-bit scratch words.
+void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* out, int64_t n, int64_t rows,
+                    int64_t h, uint64_t* keys);
+
+void dropout(hipStream_t s, const float* x, float* o, int64_t n, const int32_t* token, uint64_t seed,
+             uint64_t threshold, float scale);
+
+// Attention over a key mask [B, S]; q [B*L, H], k/v [B*S, H].
+bool attention_fits(int64_t s, int64_t d);
+void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v, const float* mask, float* o,
+                   int64_t B, int64_t L, int64_t S, int64_t H, int64_t heads);
+// Any of dq/dk/dv may be null.
+void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v, const float* mask, const float* g,
+                   float* dq, float* dk, float* dv, int64_t B, int64_t L, int64_t S, int64_t H, int64_t heads);
+
+// Cross-entropy: stats = [rows, 2] (max, total); den = [1] f32 weight sum rounded from f64.
+void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, int64_t v);
+void ce_loss(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats,
+             float* loss, float* den, int64_t rows, int64_t v);
+void ce_grad(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats,
+             const float* den, const float* g, float* o, int64_t rows, int64_t v);
+
+void softmax(hipStream_t s, const float* x, float* o, int64_t rows, int64_t k);
+void softmax_grad(hipStream_t s, const float* y, const float* g, float* o, int64_t rows, int64_t k);
+
+// Whole-tensor sums in f64 (ReduceSum, ReduceMean, Mse), one deterministic block.
+void reduce_sum(hipStream_t s, const float* a, float* o, int64_t n, bool mean);
+void mse(hipStream_t s, const float* a, const float* b, float* o, int64_t n);
+
+// The AdamW update of ir/training.rs:941-980 over one flat arena, in place.
+struct AdamWConsts { float beta1, rest1, beta2, rest2, eps, decay; };
+void adamw(hipStream_t s, float* p, const float* g, float* m, float* v, int64_t n, AdamWConsts k, const float* lr_t,
+           const float* c1, const float* c2);
+void sgd(hipStream_t s, float* p, const float* g, int64_t n, const float* lr);
+
+void record_loss(hipStream_t s, const float* loss, float* losses, uint32_t* counter, uint32_t capacity);
+
+}  // namespace msx::hk

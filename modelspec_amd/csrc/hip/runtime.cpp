@@ -1,0 +1,784 @@
+// The HIP device runtime. See runtime.h.
+#include "runtime.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <array>
+#include <set>
+
+namespace msx {
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw HipError(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+DeviceArena::~DeviceArena() {
+  if (base_) (void)hipFree(base_);
+}
+
+void* DeviceArena::reserve(size_t bytes) {
+  size_t at = size_;
+  size_ += (std::max<size_t>(bytes, 4) + 255) / 256 * 256;
+  return reinterpret_cast<void*>(at + 1);  // a token: offset + 1, never null
+}
+
+void DeviceArena::commit() {
+  if (base_) throw HipError("arena committed twice");
+  if (size_ == 0) size_ = 256;
+  hip_check(hipMalloc(&base_, size_), "hipMalloc (plan arena)");
+  hip_check(hipMemset(base_, 0, size_), "hipMemset (plan arena)");
+}
+
+void* DeviceArena::at(void* token) const {
+  if (!base_) throw HipError("arena used before commit");
+  return base_ + (reinterpret_cast<size_t>(token) - 1);
+}
+
+namespace {
+bool is_moment_input(const std::string& name) { return name.rfind("optimizer.m@", 0) == 0 || name.rfind("optimizer.v@", 0) == 0; }
+
+// A MatMul operand with its Transpose chain folded: the source value and whether it is read
+// transposed.
+struct Resolved { uint32_t src; bool flip; };
+Resolved resolve(const Program& p, uint32_t v) {
+  bool flip = false;
+  while (p.node(v).op == Op::Transpose) {
+    flip = !flip;
+    v = p.node(v).operands[0];
+  }
+  return {v, flip};
+}
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------
+Executor::Executor(Session& s, const Program& p, bool is_step) : s_(s), p_(p), is_step_(is_step) {
+  build();
+  for (int i = 0; i < kRing; ++i) {
+    hip_check(hipHostMalloc(&pinned_[i], std::max<size_t>(input_bytes_, 256), hipHostMallocDefault), "hipHostMalloc");
+    hip_check(hipEventCreateWithFlags(&slot_done_[i], hipEventDisableTiming), "hipEventCreate");
+  }
+}
+
+Executor::~Executor() {
+  for (int i = 0; i < kRing; ++i) {
+    if (slot_done_[i]) (void)hipEventDestroy(slot_done_[i]);
+    if (pinned_[i]) (void)hipHostFree(pinned_[i]);
+  }
+}
+
+void* Executor::ptr(uint32_t id) const {
+  auto f = fixed_.find(id);
+  if (f != fixed_.end()) return f->second;
+  auto t = token_.find(id);
+  if (t != token_.end()) return arena_.at(t->second);
+  throw IrError("value %" + std::to_string(id) + " has no device storage");
+}
+
+const void* Executor::value(uint32_t id) const { return ptr(id); }
+
+void Executor::build() {
+  const Program& p = p_;
+  const size_t n = p.nodes.size();
+  const TrainingStep& st = s_.step_;
+
+  // --- which nodes run ----------------------------------------------------------------------
+  std::set<uint32_t> optimizer;  // nodes the fused optimizer launch computes
+  std::vector<uint32_t> roots(p.outputs.begin(), p.outputs.end());
+  if (is_step_) {
+    std::set<uint32_t> state_outputs;
+    for (auto& [param, u] : st.updates) state_outputs.insert(u);
+    for (auto& [param, m] : st.moments) { state_outputs.insert(m.m_next); state_outputs.insert(m.v_next); }
+    // Match the optimizer's per-parameter template (ir/training.rs:737-980) node by node.
+    auto nd = [&](uint32_t v) -> const Node& { return p.node(v); };
+    auto expect = [&](uint32_t v, Op op, size_t arity) -> const Node& {
+      const Node& x = nd(v);
+      if (x.op != op || x.operands.size() != arity)
+        throw IrError(std::string("the optimizer subgraph is not the AdamW/SGD template at %") + std::to_string(v));
+      optimizer.insert(v);
+      return x;
+    };
+    auto scalar_is = [&](uint32_t v, float want) {
+      const Node& x = nd(v);
+      if (x.op != Op::Scalar || std::memcmp(&x.scalar, &want, 4) != 0)
+        throw IrError("an optimizer constant differs from the step's hyperparameters");
+      optimizer.insert(v);
+    };
+    if (st.rule == Rule::AdamW) {
+      float k[6];
+      st.adamw.constants(k);
+      for (auto& [param, u] : st.updates) {
+        uint32_t g = st.gradients.at(param);
+        const Moments& mo = st.moments.at(param);
+        uint32_t pr = 0;
+        for (auto& x : p.nodes)
+          if (x.op == Op::ParamRead && x.param == param) { pr = x.id; break; }
+        const Node& sub = expect(u, Op::Sub, 2);
+        if (sub.operands[0] != pr) throw IrError("AdamW update does not read the parameter");
+        const Node& scaled = expect(sub.operands[1], Op::Mul, 2);
+        if (scaled.operands[0] != *st.lr_t) throw IrError("AdamW step is not scaled by lr_t");
+        const Node& stp = expect(scaled.operands[1], Op::Add, 2);
+        const Node& dir = expect(stp.operands[0], Op::Div, 2);
+        const Node& shrink = expect(stp.operands[1], Op::Mul, 2);
+        scalar_is(shrink.operands[0], k[5]);
+        if (shrink.operands[1] != pr) throw IrError("AdamW decay does not read the parameter");
+        const Node& mhat = expect(dir.operands[0], Op::Mul, 2);
+        const Node& den = expect(dir.operands[1], Op::Add, 2);
+        scalar_is(den.operands[1], k[4]);
+        const Node& root = expect(den.operands[0], Op::Sqrt, 1);
+        const Node& vhat = expect(root.operands[0], Op::Mul, 2);
+        if (mhat.operands[0] != mo.m_next || mhat.operands[1] != *st.c1) throw IrError("AdamW m_hat");
+        if (vhat.operands[0] != mo.v_next || vhat.operands[1] != *st.c2) throw IrError("AdamW v_hat");
+        const Node& mn = expect(mo.m_next, Op::Add, 2);
+        const Node& dm = expect(mn.operands[0], Op::Mul, 2);
+        const Node& nm = expect(mn.operands[1], Op::Mul, 2);
+        scalar_is(dm.operands[0], k[0]);
+        scalar_is(nm.operands[0], k[1]);
+        if (dm.operands[1] != mo.m || nm.operands[1] != g) throw IrError("AdamW first moment");
+        const Node& vn = expect(mo.v_next, Op::Add, 2);
+        const Node& dv = expect(vn.operands[0], Op::Mul, 2);
+        const Node& nv = expect(vn.operands[1], Op::Mul, 2);
+        scalar_is(dv.operands[0], k[2]);
+        if (dv.operands[1] != mo.v || nv.operands[1] != g) throw IrError("AdamW second moment");
+        const Node& sg = expect(nv.operands[0], Op::Mul, 2);
+        scalar_is(sg.operands[0], k[3]);
+        if (sg.operands[1] != g) throw IrError("AdamW scaled gradient");
+      }
+    } else {
+      for (auto& [param, u] : st.updates) {
+        const Node& sub = expect(u, Op::Sub, 2);
+        const Node& scaled = expect(sub.operands[1], Op::Mul, 2);
+        scalar_is(scaled.operands[0], st.lr);
+        if (scaled.operands[1] != st.gradients.at(param)) throw IrError("SGD update does not read the gradient");
+      }
+    }
+  }
+  std::vector<bool> need(n, false);
+  for (auto o : roots) need[p.pos.at(o)] = true;
+  for (size_t k = n; k-- > 0;)
+    if (need[k])
+      for (auto o : p.nodes[k].operands) need[p.pos.at(o)] = true;
+
+  std::vector<std::vector<size_t>> consumers(n);
+  for (size_t k = 0; k < n; ++k)
+    if (need[k])
+      for (auto o : p.nodes[k].operands) consumers[p.pos.at(o)].push_back(k);
+  std::set<uint32_t> outputs(p.outputs.begin(), p.outputs.end());
+
+  // --- fusions ------------------------------------------------------------------------------
+  std::set<uint32_t> folded;     // Transposes read in place by every consumer (all MatMuls)
+  std::set<uint32_t> mm_fused;   // MatMuls whose one consumer AddRows takes them as a biased GEMM
+  for (size_t k = 0; k < n; ++k) {
+    if (!need[k]) continue;
+    const Node& x = p.nodes[k];
+    if (x.op == Op::Transpose && !outputs.count(x.id) && !consumers[k].empty()) {
+      bool all_mm = true;
+      for (auto c : consumers[k]) all_mm = all_mm && p.nodes[c].op == Op::MatMul;
+      if (all_mm) folded.insert(x.id);
+    }
+    if (x.op == Op::MatMul && !outputs.count(x.id) && consumers[k].size() == 1) {
+      const Node& c = p.nodes[consumers[k][0]];
+      if (c.op == Op::AddRows && c.operands[0] == x.id && c.operands[1] != x.id) mm_fused.insert(x.id);
+    }
+  }
+  // Attention gradients over the same operands run as one launch.
+  std::map<std::vector<uint32_t>, std::array<int64_t, 3>> attn_groups;
+  for (size_t k = 0; k < n; ++k) {
+    if (!need[k]) continue;
+    const Node& x = p.nodes[k];
+    int slot = x.op == Op::AttentionGradQ ? 0 : x.op == Op::AttentionGradK ? 1 : x.op == Op::AttentionGradV ? 2 : -1;
+    if (slot < 0) continue;
+    auto key = x.operands;
+    key.push_back(uint32_t(x.heads));
+    auto it = attn_groups.find(key);
+    if (it == attn_groups.end()) it = attn_groups.emplace(key, std::array<int64_t, 3>{-1, -1, -1}).first;
+    it->second[size_t(slot)] = int64_t(x.id);
+  }
+
+  // --- storage ------------------------------------------------------------------------------
+  std::map<uint32_t, float> constants;
+  for (size_t k = 0; k < n; ++k) {
+    if (!need[k]) continue;
+    const Node& x = p.nodes[k];
+    if (optimizer.count(x.id) && x.op != Op::Scalar) continue;
+    switch (x.op) {
+      case Op::Input:
+        if (is_moment_input(x.name)) {
+          // optimizer.<m|v>@<path>: the moment arena slice of that parameter.
+          std::string path = x.name.substr(12);
+          uint32_t param = UINT32_MAX;
+          for (size_t q = 0; q < p.params.size(); ++q)
+            if (p.params[q].path == path) param = uint32_t(q);
+          if (param == UINT32_MAX) throw IrError("moment input of an unknown parameter: " + x.name);
+          fixed_[x.id] = (x.name[10] == 'm' ? s_.m_ : s_.v_) + s_.offset_[param];
+        } else {
+          InputSlot slot{x.name, x.ty.dtype, x.ty.count(), input_bytes_, x.id};
+          input_bytes_ += (size_t(std::max<int64_t>(x.ty.count(), 1)) * 4 + 255) / 256 * 256;
+          inputs_.push_back(slot);
+        }
+        break;
+      case Op::ParamRead: fixed_[x.id] = s_.param_ + s_.offset_[x.param]; break;
+      case Op::Scalar:
+        token_[x.id] = arena_.reserve(4);
+        constants[x.id] = x.scalar;
+        break;
+      default:
+        if (folded.count(x.id) || mm_fused.count(x.id)) break;
+        token_[x.id] = arena_.reserve(size_t(x.ty.count()) * 4);
+        break;
+    }
+  }
+  // Gradients the optimizer reads live in the gradient arena at their parameter's offset.
+  std::vector<std::pair<uint32_t, uint32_t>> grad_copies;  // (value, param)
+  if (is_step_) {
+    std::set<uint32_t> claimed;
+    for (auto& [param, g] : st.gradients) {
+      const Node& x = p.node(g);
+      bool own = token_.count(g) && !claimed.count(g) && x.op != Op::Scalar;
+      if (own) {
+        token_.erase(g);
+        fixed_[g] = s_.grad_ + s_.offset_[param];
+        claimed.insert(g);
+      } else {
+        grad_copies.push_back({g, param});
+      }
+    }
+  }
+  input_token_ = arena_.reserve(std::max<size_t>(input_bytes_, 256));
+
+  // Workspaces, reserved per launch now; resolved after commit.
+  struct Pending { std::function<Launch()> make; };
+  std::vector<Pending> pending;
+  std::map<uint32_t, void*> ln_stats_tok;             // LN input value -> stats [rows, 2]
+  std::map<uint32_t, void*> ce_stats_tok;             // logits value -> stats [rows, 2]
+  std::map<std::pair<uint32_t, uint32_t>, void*> ce_den_tok;  // (logits, weights) -> den
+  auto R = [&](size_t bytes) { return arena_.reserve(bytes); };
+  auto A = [this](void* tok) { return arena_.at(tok); };
+  auto P = [this](uint32_t id) { return ptr(id); };
+  auto F = [this](uint32_t id) { return static_cast<float*>(ptr(id)); };
+  auto I = [this](uint32_t id) { return static_cast<int32_t*>(ptr(id)); };
+  auto shape = [&](uint32_t v) -> const std::vector<int64_t>& { return p.node(v).ty.shape; };
+  const uint64_t seed = s_.seed_;
+
+  for (size_t k = 0; k < n; ++k) {
+    if (!need[k]) continue;
+    const Node& x = p.nodes[k];
+    if (optimizer.count(x.id)) continue;
+    const uint32_t id = x.id;
+    const auto& o = x.operands;
+    const int64_t count = x.ty.count();
+    std::string what = std::string(op_name(x.op)) + " %" + std::to_string(id);
+    auto push = [&](std::function<void(hipStream_t)> f) { pending.push_back({[what, f] { return Launch{what, f}; }}); };
+    switch (x.op) {
+      case Op::Input: case Op::ParamRead: case Op::Scalar: break;
+      case Op::Add: case Op::Sub: case Op::Mul: case Op::Div: {
+        int op = x.op == Op::Add ? hk::EW_ADD : x.op == Op::Sub ? hk::EW_SUB : x.op == Op::Mul ? hk::EW_MUL : hk::EW_DIV;
+        bool as = p.node(o[0]).ty.rank() == 0 && count > 1, bs = p.node(o[1]).ty.rank() == 0 && count > 1;
+        uint32_t a = o[0], b = o[1];
+        push([=](hipStream_t s) { hk::elementwise(s, op, F(a), F(b), F(id), count, as, bs); });
+        break;
+      }
+      case Op::Relu: case Op::Gelu: case Op::Sqrt: case Op::StopGradient: {
+        int op = x.op == Op::Relu ? hk::EW_RELU : x.op == Op::Gelu ? hk::EW_GELU : x.op == Op::Sqrt ? hk::EW_SQRT : hk::EW_COPY;
+        uint32_t a = o[0];
+        push([=](hipStream_t s) { hk::elementwise(s, op, F(a), nullptr, F(id), count, false, false); });
+        break;
+      }
+      case Op::ReluGrad: case Op::GeluGrad: {
+        int op = x.op == Op::ReluGrad ? hk::EW_RELU_GRAD : hk::EW_GELU_GRAD;
+        uint32_t a = o[0], g = o[1];
+        push([=](hipStream_t s) { hk::elementwise(s, op, F(a), F(g), F(id), count, false, false); });
+        break;
+      }
+      case Op::MatMul: case Op::AddRows: {
+        uint32_t mm = x.op == Op::MatMul ? id : o[0];
+        if (x.op == Op::MatMul && mm_fused.count(id)) break;
+        bool fused = x.op == Op::AddRows && mm_fused.count(o[0]);
+        if (x.op == Op::AddRows && !fused) {
+          uint32_t a = o[0], b = o[1];
+          int64_t rows = x.ty.shape[0], h = x.ty.shape[1];
+          push([=](hipStream_t s) { hk::add_rows(s, F(a), F(b), F(id), rows, h); });
+          break;
+        }
+        const Node& m = p.node(mm);
+        Resolved ra = resolve(p, m.operands[0]), rb = resolve(p, m.operands[1]);
+        int64_t M = m.ty.shape[0], N = m.ty.shape[1], K = shape(m.operands[0])[1];
+        hk::GemmArgs g{};
+        g.m = M; g.n = N; g.k = K; g.ldc = N;
+        g.ta = ra.flip; g.lda = ra.flip ? M : K;
+        g.tb = rb.flip; g.ldb = rb.flip ? K : N;
+        int split = hk::gemm_split_for(M, N, K);
+        void* ws = split > 1 ? R(size_t(split) * size_t(M * N) * 4) : nullptr;
+        g.workspace_floats = split > 1 ? int64_t(split) * M * N : 0;
+        uint32_t asrc = ra.src, bsrc = rb.src;
+        int64_t bias_id = fused ? int64_t(o[1]) : -1;
+        push([=](hipStream_t s) {
+          hk::GemmArgs a = g;
+          a.a = F(asrc);
+          a.b = F(bsrc);
+          a.c = F(id);
+          a.bias = bias_id >= 0 ? F(uint32_t(bias_id)) : nullptr;
+          a.workspace = ws ? static_cast<float*>(A(ws)) : nullptr;
+          hk::gemm(s, a);
+        });
+        break;
+      }
+      case Op::Transpose: {
+        if (folded.count(id)) break;
+        Resolved r = resolve(p, o[0]);
+        uint32_t src = r.src;
+        if (r.flip) {  // the transpose of a transpose: a copy of the source
+          push([=](hipStream_t s) { hk::copy(s, F(src), F(id), count); });
+        } else {
+          int64_t rows = shape(src)[0], cols = shape(src)[1];
+          push([=](hipStream_t s) { hk::transpose(s, F(src), F(id), rows, cols); });
+        }
+        break;
+      }
+      case Op::ReduceSum: case Op::ReduceMean: {
+        uint32_t a = o[0];
+        int64_t na = p.node(a).ty.count();
+        bool mean = x.op == Op::ReduceMean;
+        push([=](hipStream_t s) { hk::reduce_sum(s, F(a), F(id), na, mean); });
+        break;
+      }
+      case Op::Mse: {
+        uint32_t a = o[0], b = o[1];
+        int64_t na = p.node(a).ty.count();
+        push([=](hipStream_t s) { hk::mse(s, F(a), F(b), F(id), na); });
+        break;
+      }
+      case Op::BroadcastScalar: {
+        uint32_t a = o[0];
+        push([=](hipStream_t s) { hk::fill_from(s, F(a), F(id), count); });
+        break;
+      }
+      case Op::Embedding: {
+        uint32_t t = o[0], ids = o[1];
+        int64_t rows = shape(t)[0], h = shape(t)[1], nn = shape(ids)[0];
+        if (p.node(ids).op == Op::Input) id_bounds_[p.node(ids).name] = rows;
+        push([=](hipStream_t s) { hk::embedding(s, F(t), I(ids), F(id), nn, rows, h); });
+        break;
+      }
+      case Op::EmbeddingGrad: {
+        uint32_t ids = o[0], g = o[1];
+        int64_t nn = shape(ids)[0], h = shape(g)[1], rows = x.rows;
+        if (p.node(ids).op == Op::Input) {
+          auto it = id_bounds_.find(p.node(ids).name);
+          id_bounds_[p.node(ids).name] = it == id_bounds_.end() ? rows : std::min(it->second, rows);
+        }
+        void* keys = R(size_t(std::max<int64_t>(nn, 1)) * 8);
+        push([=](hipStream_t s) { hk::embedding_grad(s, I(ids), F(g), F(id), nn, rows, h, static_cast<uint64_t*>(A(keys))); });
+        break;
+      }
+      case Op::SumRows: {
+        uint32_t a = o[0];
+        int64_t rows = shape(a)[0], h = shape(a)[1];
+        int64_t pf = hk::column_chunks(rows, h) * h;
+        void* part = R(size_t(pf) * 4);
+        push([=](hipStream_t s) { hk::column_sum(s, F(a), F(id), rows, h, static_cast<float*>(A(part)), pf); });
+        break;
+      }
+      case Op::LayerNorm: case Op::LayerNormGradX: case Op::LayerNormGradGamma: {
+        uint32_t xv = o[0];
+        int64_t rows = shape(xv)[0], h = shape(xv)[1];
+        bool have = ln_stats_tok.count(xv) != 0;
+        if (!have) ln_stats_tok[xv] = R(size_t(rows) * 8);
+        void* stats = ln_stats_tok[xv];
+        if (x.op == Op::LayerNorm) {
+          uint32_t gm = o[1], bt = o[2];
+          bool write_stats = !have;
+          push([=](hipStream_t s) {
+            hk::layer_norm(s, F(xv), F(gm), F(bt), F(id), write_stats ? static_cast<float*>(A(stats)) : nullptr, rows, h);
+          });
+          break;
+        }
+        if (!have) push([=](hipStream_t s) { hk::ln_stats(s, F(xv), static_cast<float*>(A(stats)), rows, h); });
+        if (x.op == Op::LayerNormGradX) {
+          uint32_t gm = o[1], g = o[2];
+          push([=](hipStream_t s) { hk::ln_grad_x(s, F(xv), F(gm), F(g), static_cast<float*>(A(stats)), F(id), rows, h); });
+        } else {
+          uint32_t g = o[1];
+          int64_t pf = hk::column_chunks(rows, h) * h;
+          void* part = R(size_t(pf) * 4);
+          push([=](hipStream_t s) {
+            hk::ln_grad_gamma(s, F(xv), F(g), static_cast<float*>(A(stats)), F(id), rows, h, static_cast<float*>(A(part)), pf);
+          });
+        }
+        break;
+      }
+      case Op::Softmax: {
+        uint32_t a = o[0];
+        int64_t rows = x.ty.shape[0], kk = x.ty.shape[1];
+        push([=](hipStream_t s) { hk::softmax(s, F(a), F(id), rows, kk); });
+        break;
+      }
+      case Op::SoftmaxGrad: {
+        uint32_t y = o[0], g = o[1];
+        int64_t rows = x.ty.shape[0], kk = x.ty.shape[1];
+        push([=](hipStream_t s) { hk::softmax_grad(s, F(y), F(g), F(id), rows, kk); });
+        break;
+      }
+      case Op::Attention: case Op::AttentionGradQ: case Op::AttentionGradK: case Op::AttentionGradV: {
+        if (p.node(o[3]).ty.dtype != DType::F32) throw IrError("attention over key spans has no HIP kernel yet");
+        uint32_t q = o[0], kv = o[1], v = o[2], mask = o[3];
+        int64_t B = shape(mask)[0], S = shape(mask)[1], L = shape(q)[0] / B, H = shape(q)[1], heads = x.heads;
+        if (!hk::attention_fits(S, H / heads)) throw IrError("attention shape has no HIP kernel (head width or sequence too large)");
+        if (p.node(mask).op == Op::Input) key_masks_.push_back(p.node(mask).name);
+        if (x.op == Op::Attention) {
+          push([=](hipStream_t s) { hk::attention_fwd(s, F(q), F(kv), F(v), F(mask), F(id), B, L, S, H, heads); });
+          break;
+        }
+        auto key = o;
+        key.push_back(uint32_t(x.heads));
+        auto& grp = attn_groups.at(key);
+        int64_t first = -1;
+        for (auto g : grp)
+          if (g >= 0 && (first < 0 || p.pos.at(uint32_t(g)) < p.pos.at(uint32_t(first)))) first = g;
+        if (first != int64_t(id)) break;  // the group's first member launches for all three
+        uint32_t g = o[4];
+        std::array<int64_t, 3> members = grp;
+        push([=](hipStream_t s) {
+          auto out = [&](int64_t v2) { return v2 >= 0 ? F(uint32_t(v2)) : nullptr; };
+          hk::attention_bwd(s, F(q), F(kv), F(v), F(mask), F(g), out(members[0]), out(members[1]), out(members[2]), B, L, S,
+                            H, heads);
+        });
+        break;
+      }
+      case Op::CrossEntropy: case Op::CrossEntropyGrad: {
+        uint32_t lg = o[0], lab = o[1], w = o[2];
+        int64_t rows = shape(lg)[0], v = shape(lg)[1];
+        if (p.node(lab).op == Op::Input) id_bounds_["#labels:" + p.node(lab).name] = v;
+        if (p.node(w).op == Op::Input) id_bounds_["#weights:" + p.node(w).name] = 0;
+        bool have = ce_stats_tok.count(lg) != 0;
+        if (!have) {
+          ce_stats_tok[lg] = R(size_t(rows) * 8);
+          void* st2 = ce_stats_tok[lg];
+          push([=](hipStream_t s) { hk::ce_stats(s, F(lg), static_cast<float*>(A(st2)), rows, v); });
+        }
+        void* stats = ce_stats_tok[lg];
+        auto dkey = std::make_pair(lg, w);
+        bool have_den = ce_den_tok.count(dkey) != 0;
+        if (!have_den) ce_den_tok[dkey] = R(4);
+        void* den = ce_den_tok[dkey];
+        if (x.op == Op::CrossEntropy) {
+          push([=](hipStream_t s) {
+            hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(stats)), F(id), static_cast<float*>(A(den)), rows, v);
+          });
+        } else {
+          if (!have_den) {
+            void* scratch = R(4);
+            push([=](hipStream_t s) {
+              hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(stats)), static_cast<float*>(A(scratch)),
+                          static_cast<float*>(A(den)), rows, v);
+            });
+          }
+          uint32_t g = o[3];
+          push([=](hipStream_t s) {
+            hk::ce_grad(s, F(lg), I(lab), F(w), static_cast<float*>(A(stats)), static_cast<float*>(A(den)), F(g), F(id), rows, v);
+          });
+        }
+        break;
+      }
+      case Op::Dropout: case Op::DropoutGrad: {
+        uint32_t tok = o[size_t(token_operand(x.op))], a = o[x.op == Op::Dropout ? 0 : 1];
+        uint64_t threshold = dropout_threshold(x.scalar);
+        float scale = 1.0f / (1.0f - x.scalar);
+        push([=](hipStream_t s) { hk::dropout(s, F(a), F(id), count, I(tok), seed, threshold, scale); });
+        break;
+      }
+      case Op::Count_: break;
+    }
+  }
+  // The optimizer: gradients not computed in place are copied into the arena, then one launch
+  // updates every trained parameter and its moments.
+  if (is_step_) {
+    for (auto [g, param] : grad_copies) {
+      int64_t cnt = p.node(g).ty.count();
+      float* dst = s_.grad_ + s_.offset_[param];
+      pending.push_back({[=] { return Launch{"GradientCopy", [=](hipStream_t s) { hk::copy(s, F(g), dst, cnt); }}; }});
+    }
+    int64_t nt = s_.trained_;
+    if (st.rule == Rule::AdamW && !st.updates.empty()) {
+      float k[6];
+      st.adamw.constants(k);
+      hk::AdamWConsts c{k[0], k[1], k[2], k[3], k[4], k[5]};
+      uint32_t lr = *st.lr_t, c1 = *st.c1, c2 = *st.c2;
+      pending.push_back({[=] {
+        return Launch{"AdamW", [=](hipStream_t s) { hk::adamw(s, s_.param_, s_.grad_, s_.m_, s_.v_, nt, c, F(lr), F(c1), F(c2)); }};
+      }});
+    } else if (st.rule == Rule::Sgd && !st.updates.empty()) {
+      uint32_t rate = p.node(st.updates.begin()->second).operands[1];
+      uint32_t lr_scalar = p.node(rate).operands[0];
+      pending.push_back({[=] { return Launch{"SGD", [=](hipStream_t s) { hk::sgd(s, s_.param_, s_.grad_, nt, F(lr_scalar)); }}; }});
+    }
+    loss_value = st.loss;
+    uint32_t loss = st.loss;
+    pending.push_back({[=] {
+      return Launch{"RecordLoss", [=](hipStream_t s) { hk::record_loss(s, F(loss), s_.losses_dev_, s_.counter_, s_.loss_capacity_); }};
+    }});
+  } else {
+    loss_value = p.outputs.at(0);
+  }
+
+  arena_.commit();
+  for (auto& [vid, val] : constants) hip_check(hipMemcpy(ptr(vid), &val, 4, hipMemcpyHostToDevice), "hipMemcpy (constants)");
+  for (auto& slot : inputs_) fixed_[slot.id] = static_cast<char*>(arena_.at(input_token_)) + slot.offset;
+  for (auto& pd : pending) launches_.push_back(pd.make());
+}
+
+void Executor::stage(const Batch& batch) {
+  // The checks the reference makes before a step reads an id (interpreter.rs:700-715,
+  // 1146-1262): ids inside their table, labels inside the classes, weights finite and not
+  // negative, key masks of 0 and 1 with a 1 in every sequence.
+  for (auto& [key, rows] : id_bounds_) {
+    if (key.rfind("#weights:", 0) == 0) {
+      auto it = batch.f32.find(key.substr(9));
+      if (it == batch.f32.end()) continue;
+      for (size_t r = 0; r < it->second.size(); ++r) {
+        float w = it->second[r];
+        if (!(w * 0.0f == 0.0f) || w < 0.0f) throw IrError("loss weight " + std::to_string(r) + " is negative or not finite");
+      }
+      continue;
+    }
+    bool label = key.rfind("#labels:", 0) == 0;
+    std::string name = label ? key.substr(8) : key;
+    auto it = batch.i32.find(name);
+    if (it == batch.i32.end()) continue;
+    for (size_t r = 0; r < it->second.size(); ++r) {
+      int32_t v = it->second[r];
+      if (v < 0 || v >= rows)
+        throw IrError("E-DATA-011: `" + name + "` holds " + std::to_string(v) + " at " + std::to_string(r) + ", outside [0, " +
+                      std::to_string(rows) + ")");
+    }
+  }
+  for (auto& name : key_masks_) {
+    auto it = batch.f32.find(name);
+    if (it == batch.f32.end()) continue;
+    const Node* in = p_.input(name);
+    int64_t S = in->ty.shape[1];
+    for (size_t b = 0; b * size_t(S) < it->second.size(); ++b) {
+      bool any = false;
+      for (int64_t j = 0; j < S; ++j) {
+        float m = it->second[b * size_t(S) + size_t(j)];
+        if (m != 0.0f && m != 1.0f) throw IrError("key mask `" + name + "` holds a value other than 0 and 1");
+        any = any || m == 1.0f;
+      }
+      if (!any) throw IrError("key mask `" + name + "`: sequence " + std::to_string(b) + " has no unmasked key");
+    }
+  }
+  int slot = next_slot_;
+  next_slot_ = (next_slot_ + 1) % kRing;
+  hip_check(hipEventSynchronize(slot_done_[slot]), "hipEventSynchronize (staging slot)");
+  char* host = static_cast<char*>(pinned_[slot]);
+  for (auto& in : inputs_) {
+    const void* src = nullptr;
+    size_t have = 0;
+    if (in.dtype == DType::F32) {
+      auto it = batch.f32.find(in.name);
+      if (it != batch.f32.end()) { src = it->second.data(); have = it->second.size(); }
+    } else {
+      auto it = batch.i32.find(in.name);
+      if (it != batch.i32.end()) { src = it->second.data(); have = it->second.size(); }
+    }
+    if (!src && in.count > 0) throw IrError("missing input `" + in.name + "`");
+    if (int64_t(have) != in.count) throw IrError("input `" + in.name + "` has " + std::to_string(have) + " elements, not " + std::to_string(in.count));
+    std::memcpy(host + in.offset, src, size_t(in.count) * 4);
+  }
+  if (input_bytes_) {
+    hip_check(hipMemcpyAsync(arena_.at(input_token_), host, input_bytes_, hipMemcpyHostToDevice, s_.stream_), "hipMemcpyAsync (inputs)");
+    s_.stats_.bytes_uploaded += input_bytes_;
+  }
+  hip_check(hipEventRecord(slot_done_[slot], s_.stream_), "hipEventRecord");
+}
+
+void Executor::run(hipStream_t s) {
+  for (auto& l : launches_) {
+    l.run(s);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw HipError(l.what + ": " + hipGetErrorString(e));
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+Session::Session(int device, const TrainingStep& step, const Program& forward, uint64_t seed, uint32_t prediction)
+    : device_(device), step_(step), forward_(forward), seed_(seed), prediction_(prediction) {
+  step_.program.reindex();
+  forward_.reindex();
+  hip_check(hipSetDevice(device), "hipSetDevice");
+  hk::prepare();
+  hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+  const auto& params = step_.program.params;
+  offset_.assign(params.size(), 0);
+  int64_t at = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    for (size_t q = 0; q < params.size(); ++q) {
+      bool trained = step_.updates.count(uint32_t(q)) != 0;
+      if (trained != (pass == 0)) continue;
+      offset_[q] = at;
+      at += (params[q].ty.count() + 63) / 64 * 64;
+    }
+    if (pass == 0) trained_ = at;
+  }
+  total_ = std::max<int64_t>(at, 64);
+  size_t floats = size_t(total_) * 4 + loss_capacity_ + 64;
+  hip_check(hipMalloc(&state_mem_, floats * 4), "hipMalloc (parameter state)");
+  hip_check(hipMemset(state_mem_, 0, floats * 4), "hipMemset (parameter state)");
+  float* base = static_cast<float*>(state_mem_);
+  param_ = base;
+  grad_ = base + total_;
+  m_ = base + 2 * total_;
+  v_ = base + 3 * total_;
+  losses_dev_ = base + 4 * total_;
+  counter_ = reinterpret_cast<uint32_t*>(base + 4 * total_ + loss_capacity_);
+  if (step_.has_optimizer) step_exec_ = std::make_unique<Executor>(*this, step_.program, true);
+  fwd_exec_ = std::make_unique<Executor>(*this, forward_, false);
+  stats_.device_bytes = floats * 4;
+}
+
+Session::~Session() {
+  if (stream_) (void)hipStreamSynchronize(stream_);
+  if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+  if (graph_) (void)hipGraphDestroy(graph_);
+  step_exec_.reset();
+  fwd_exec_.reset();
+  if (state_mem_) (void)hipFree(state_mem_);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+size_t Session::launches_per_step() const { return step_exec_ ? step_exec_->launches().size() : 0; }
+
+const void* Session::forward_value(uint32_t id) const { return fwd_exec_->value(id); }
+
+void Session::run_forward(const Batch& batch) {
+  fwd_exec_->stage(batch);
+  fwd_exec_->run(stream_);
+  sync();
+}
+
+void Session::sync() { hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize"); }
+
+void Session::upload_params(const std::vector<std::vector<float>>& values) {
+  const auto& params = step_.program.params;
+  if (values.size() != params.size()) throw IrError("set_params: wrong number of parameters");
+  sync();
+  for (size_t q = 0; q < params.size(); ++q) {
+    if (int64_t(values[q].size()) != params[q].ty.count()) throw IrError("set_params: `" + params[q].path + "` has the wrong size");
+    hip_check(hipMemcpy(param_ + offset_[q], values[q].data(), values[q].size() * 4, hipMemcpyHostToDevice), "hipMemcpy (params)");
+  }
+}
+
+void Session::set_params(const std::vector<std::vector<float>>& values) {
+  upload_params(values);
+  hk::fill_zero(stream_, grad_, total_ * 4);
+  hk::fill_zero(stream_, m_, total_ * 4);
+  hk::fill_zero(stream_, v_, total_ * 4);
+  hk::fill_zero(stream_, counter_, 64 * 4);
+  sync();
+  steps_since_reset_ = 0;
+}
+
+std::vector<std::vector<float>> Session::params() {
+  sync();
+  std::vector<std::vector<float>> out;
+  for (size_t q = 0; q < step_.program.params.size(); ++q) {
+    std::vector<float> v(size_t(step_.program.params[q].ty.count()));
+    hip_check(hipMemcpy(v.data(), param_ + offset_[q], v.size() * 4, hipMemcpyDeviceToHost), "hipMemcpy (read params)");
+    out.push_back(std::move(v));
+  }
+  return out;
+}
+
+std::vector<std::vector<float>> Session::moments(char which) {
+  sync();
+  std::vector<std::vector<float>> out(step_.program.params.size());
+  for (auto& [q, mo] : step_.moments) {
+    std::vector<float> v(size_t(step_.program.params[q].ty.count()));
+    float* src = (which == 'm' ? m_ : v_) + offset_[q];
+    hip_check(hipMemcpy(v.data(), src, v.size() * 4, hipMemcpyDeviceToHost), "hipMemcpy (read moments)");
+    out[q] = std::move(v);
+  }
+  return out;
+}
+
+std::vector<float> Session::predict(const std::vector<std::vector<float>>& values, const Batch& batch) {
+  upload_params(values);
+  fwd_exec_->stage(batch);
+  fwd_exec_->run(stream_);
+  sync();
+  std::vector<float> out(size_t(forward_.node(prediction_).ty.count()));
+  hip_check(hipMemcpy(out.data(), fwd_exec_->value(prediction_), out.size() * 4, hipMemcpyDeviceToHost), "hipMemcpy (prediction)");
+  return out;
+}
+
+void Session::train_step(const StepInputs& in) {
+  step_exec_->stage(in.batch);
+  if (use_graph_) {
+    if (!graph_exec_) {
+      hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+      try {
+        step_exec_->run(stream_);
+      } catch (...) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(stream_, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      hip_check(hipStreamEndCapture(stream_, &graph_), "hipStreamEndCapture");
+      hip_check(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0), "hipGraphInstantiate");
+      size_t nodes = 0;
+      hip_check(hipGraphGetNodes(graph_, nullptr, &nodes), "hipGraphGetNodes");
+      stats_.kernels_per_step = nodes;
+    }
+    hip_check(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
+    stats_.graph_launches += 1;
+  } else {
+    step_exec_->run(stream_);
+  }
+  stats_.steps += 1;
+  steps_since_reset_ += 1;
+}
+
+std::vector<std::pair<std::string, float>> Session::profile_step(const StepInputs& in) {
+  step_exec_->stage(in.batch);
+  const auto& ls = step_exec_->launches();
+  std::vector<hipEvent_t> ev(ls.size() + 1);
+  for (auto& e : ev) hip_check(hipEventCreate(&e), "hipEventCreate");
+  hip_check(hipEventRecord(ev[0], stream_), "hipEventRecord");
+  for (size_t i = 0; i < ls.size(); ++i) {
+    ls[i].run(stream_);
+    hip_check(hipEventRecord(ev[i + 1], stream_), "hipEventRecord");
+  }
+  sync();
+  std::vector<std::pair<std::string, float>> out;
+  for (size_t i = 0; i < ls.size(); ++i) {
+    float ms = 0;
+    hip_check(hipEventElapsedTime(&ms, ev[i], ev[i + 1]), "hipEventElapsedTime");
+    out.push_back({ls[i].what, ms});
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  stats_.steps += 1;
+  steps_since_reset_ += 1;
+  return out;
+}
+
+float Session::final_loss(const Batch& batch) {
+  fwd_exec_->stage(batch);
+  fwd_exec_->run(stream_);
+  sync();
+  float loss = 0;
+  hip_check(hipMemcpy(&loss, fwd_exec_->value(fwd_exec_->loss_value), 4, hipMemcpyDeviceToHost), "hipMemcpy (loss)");
+  return loss;
+}
+
+std::vector<float> Session::losses() {
+  sync();
+  uint32_t count = 0;
+  hip_check(hipMemcpy(&count, counter_, 4, hipMemcpyDeviceToHost), "hipMemcpy (loss counter)");
+  count = std::min(count, loss_capacity_);
+  std::vector<float> out(count);
+  if (count) hip_check(hipMemcpy(out.data(), losses_dev_, count * 4, hipMemcpyDeviceToHost), "hipMemcpy (losses)");
+  return out;
+}
+
+}  // namespace msx

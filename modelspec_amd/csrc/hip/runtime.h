@@ -1,0 +1,146 @@
+// The HIP device runtime: executes a compiled training step (and its forward program) on one
+// MI355X. It replaces the reference's Vulkan stepwise runner
+// (crates/modelspec-runtime/src/vulkan/stepwise.rs:289-400, 975-1551): parameters and AdamW
+// moments stay resident in HBM for the whole run, each step's host inputs are packed into one
+// pinned staging slot and copied in one transfer, and the step's kernels are captured once into a
+// hipGraph and relaunched every step.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <functional>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../host/runner.h"
+#include "kernels.h"
+
+namespace msx {
+
+struct HipError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+void hip_check(hipError_t e, const char* what);
+
+// One device allocation carved by a bump allocator; everything a plan needs is reserved when the
+// plan is built, so a captured step never allocates.
+class DeviceArena {
+ public:
+  ~DeviceArena();
+  void* reserve(size_t bytes);  // 256-byte aligned, zero-initialized at commit()
+  void commit();                // one hipMalloc of everything reserved
+  void* at(void* token) const;  // device address of a reservation
+  size_t bytes() const { return size_; }
+
+ private:
+  size_t size_ = 0;
+  char* base_ = nullptr;
+};
+
+struct Launch {
+  std::string what;  // op name and value, for profiles and errors
+  std::function<void(hipStream_t)> run;
+};
+
+struct RunStats {
+  uint64_t steps = 0, graph_launches = 0, kernels_per_step = 0, bytes_uploaded = 0, device_bytes = 0;
+};
+
+class Executor;
+
+// A loaded training run on one device.
+class Session : public Engine {
+ public:
+  Session(int device, const TrainingStep& step, const Program& forward, uint64_t seed, uint32_t prediction);
+  ~Session() override;
+
+  void set_params(const std::vector<std::vector<float>>& values) override;
+  std::vector<std::vector<float>> params() override;
+  std::vector<std::vector<float>> moments(char which) override;
+  std::vector<float> predict(const std::vector<std::vector<float>>& values, const Batch& batch) override;
+  void train_step(const StepInputs& in) override;
+  float final_loss(const Batch& batch) override;
+  std::vector<float> losses() override;
+
+  // Runs the step plan eagerly (no graph) with one event pair around every launch; returns the
+  // launches and their milliseconds for the current inputs (the step's update is applied).
+  std::vector<std::pair<std::string, float>> profile_step(const StepInputs& in);
+  void use_graph(bool on) { use_graph_ = on; }
+  void sync();
+  hipStream_t stream() const { return stream_; }
+  const RunStats& stats() const { return stats_; }
+  size_t launches_per_step() const;
+  // The forward program alone, on the current parameters (per-op tests, evaluation).
+  void run_forward(const Batch& batch);
+  const void* forward_value(uint32_t id) const;
+  void load_params(const std::vector<std::vector<float>>& values) { upload_params(values); }
+
+ private:
+  friend class Executor;
+  int device_;
+  hipStream_t stream_ = nullptr;
+  TrainingStep step_;
+  Program forward_;
+  uint64_t seed_;
+  uint32_t prediction_;
+  bool use_graph_ = true;
+
+  // Parameter, gradient and moment arenas share offsets: element i of each is the same element
+  // of the same parameter. Parameters with a gradient come first, so the optimizer runs over one
+  // prefix [0, trained_) of the arenas.
+  std::vector<int64_t> offset_;  // per ParamId, in floats
+  int64_t total_ = 0, trained_ = 0;
+  float *param_ = nullptr, *grad_ = nullptr, *m_ = nullptr, *v_ = nullptr;
+  float* losses_dev_ = nullptr;
+  uint32_t* counter_ = nullptr;
+  uint32_t loss_capacity_ = 1u << 20;
+  void* state_mem_ = nullptr;
+
+  std::unique_ptr<Executor> step_exec_, fwd_exec_;
+  hipGraph_t graph_ = nullptr;
+  hipGraphExec_t graph_exec_ = nullptr;
+  RunStats stats_;
+  uint64_t steps_since_reset_ = 0;
+
+  void upload_params(const std::vector<std::vector<float>>& values);
+};
+
+// Executes one Program: value storage, staged inputs, the fused launch list.
+class Executor {
+ public:
+  Executor(Session& s, const Program& p, bool is_step);
+  ~Executor();
+  // Packs `batch` (and checks ids, labels and key masks) into the next pinned slot and enqueues
+  // its copy to the device input block.
+  void stage(const Batch& batch);
+  void run(hipStream_t s);  // every launch, in order
+  const std::vector<Launch>& launches() const { return launches_; }
+  const void* value(uint32_t id) const;
+  uint32_t loss_value = 0;
+
+ private:
+  Session& s_;
+  const Program& p_;
+  bool is_step_;
+  DeviceArena arena_;
+  std::map<uint32_t, void*> token_;   // arena reservation per value
+  std::map<uint32_t, void*> fixed_;   // values living in the session's arenas
+  std::vector<Launch> launches_;
+  struct InputSlot { std::string name; DType dtype; int64_t count; size_t offset; uint32_t id; };
+  std::vector<InputSlot> inputs_;
+  size_t input_bytes_ = 0;
+  void* input_token_ = nullptr;
+  static constexpr int kRing = 4;
+  void* pinned_[kRing] = {};
+  hipEvent_t slot_done_[kRing] = {};
+  int next_slot_ = 0;
+  // id checks before upload: input name -> rows it indexes (Embedding / EmbeddingGrad / labels)
+  std::map<std::string, int64_t> id_bounds_;
+  std::vector<std::string> key_masks_;
+  void build();
+  void* ptr(uint32_t id) const;
+};
+
+}  // namespace msx

@@ -92,6 +92,25 @@ Compiled linear_regression() {
   return finish(c, L.b.finish(), loss, pred, Rule::Sgd, 0.1f, {});
 }
 
+// examples/mnist_mlp.mspec: 784 -> 64 relu -> 10, no bias, mse, SGD 0.1, teacher data.
+Compiled mnist_mlp() {
+  Lowering L;
+  L.model = "MnistMlp";
+  L.param("w1", Type::f32({784, 64}), Init::XavierUniform);
+  L.param("w2", Type::f32({64, 10}), Init::XavierUniform);
+  L.declare({{"x", Type::f32({100, 784})}, {"y", Type::f32({100, 10})}});
+  uint32_t pred = L.matmul(L.op(Op::Relu, {L.matmul(L.d("x"), L.p("w1"))}), L.p("w2"));
+  uint32_t loss = L.op(Op::Mse, {pred, L.d("y")});
+  TrainConfig c;
+  c.name = "mnist_mlp";
+  c.steps = 1800;
+  c.seed = 42;
+  c.feed = FeedKind::Teacher;
+  c.x = "x";
+  c.y = "y";
+  return finish(c, L.b.finish(), loss, pred, Rule::Sgd, 0.1f, {});
+}
+
 // The MLP classifier of the configs: 784-256-10 with biases, ReLU, softmax cross_entropy.
 Compiled mlp_classifier(int64_t batch, uint64_t steps) {
   Lowering L;
@@ -261,7 +280,7 @@ Compiled bert(const std::string& name, int64_t V, int64_t H, int64_t heads, int6
 }  // namespace
 
 std::vector<std::string> config_names() {
-  return {"linear_regression", "mlp_classifier", "transformer_block", "bert_tiny", "bert_cpu", "bert_micro",
+  return {"linear_regression", "mnist_mlp", "mlp_classifier", "transformer_block", "bert_tiny", "bert_cpu", "bert_micro",
           "block_micro", "mlp_micro"};
 }
 
@@ -269,6 +288,7 @@ Compiled compile_config(const std::string& name, int64_t masked_rows, int64_t st
   auto steps = [&](uint64_t d) { return steps_override >= 0 ? uint64_t(steps_override) : d; };
   Compiled c;
   if (name == "linear_regression") c = linear_regression();
+  else if (name == "mnist_mlp") c = mnist_mlp();
   else if (name == "mlp_classifier") c = mlp_classifier(64, 1000);
   else if (name == "mlp_micro") c = mlp_classifier(8, 20);
   else if (name == "transformer_block") c = transformer_block(4096, 128, 2, 512, 32, 128, 500, name);
