@@ -91,6 +91,14 @@ int msx_stats(msx_ctx* ctx, msx_run_stats* out);
 int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t masked_rows, float* losses,
                      uint64_t losses_len, float* params, uint64_t params_len, double* train_seconds);
 
+/* Times `steps` graph-launched training steps of a built-in config after `warmup` (HIP events on
+ * the run's stream; host inputs made before the timed region), then profiles one more step
+ * eagerly with an event pair per launch into `profile` ("launch\tms" lines; free with msx_free).
+ * Replaces `train --clock --profile` (crates/modelspec-cli/src/train.rs:17-31,
+ * vulkan/profile.rs:1-14). */
+int msx_bench_config(msx_ctx* ctx, const char* config, int64_t masked_rows, uint32_t warmup, uint32_t steps,
+                     double* ms_per_step, float* last_loss, char** profile);
+
 /* One program (print.rs text of a Tensor IR program) on the device, for per-op tests: inputs by
  * name, parameters by ParamId; output k read back with msx_prog_output. */
 typedef struct msx_prog msx_prog;

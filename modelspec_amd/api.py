@@ -232,3 +232,22 @@ _STEPS = {"linear_regression": 500, "mnist_mlp": 1800, "mlp_classifier": 1000, "
 
 def config_steps(name):
     return _STEPS[name]
+
+
+def bench_config(ctx, name, warmup, steps, masked_rows=-1, profile=True):
+    """(ms per step, last loss, [(launch, ms)] of one eagerly profiled step)."""
+    L = lib()
+    L.msx_bench_config.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint32,
+                                   ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_float),
+                                   ctypes.POINTER(ctypes.c_void_p)]
+    ms, loss, rep = ctypes.c_double(), ctypes.c_float(), ctypes.c_void_p()
+    _check(L.msx_bench_config(ctx._h, name.encode(), masked_rows, warmup, steps, ctypes.byref(ms), ctypes.byref(loss),
+                              ctypes.byref(rep) if profile else None))
+    rows = []
+    if profile and rep.value:
+        text = ctypes.string_at(rep).decode()
+        L.msx_free(rep)
+        for line in text.splitlines():
+            what, t = line.rsplit("\t", 1)
+            rows.append((what, float(t)))
+    return ms.value, loss.value, rows

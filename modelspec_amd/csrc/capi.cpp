@@ -45,6 +45,12 @@ char* dup(const std::string& s) {
   return p;
 }
 
+// The smallest run length whose AdamW warmup stays shorter than the run.
+uint64_t c_steps_floor(const char* config) {
+  msx::Compiled c = msx::compile_config(config, -1, -1);
+  return c.step.rule == msx::Rule::AdamW ? c.step.adamw.warmup_steps + 1 : 1;
+}
+
 msx::Batch batch_of(const msx_tensor* t, uint32_t n) {
   msx::Batch b;
   for (uint32_t i = 0; i < n; ++i) {
@@ -230,6 +236,50 @@ int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t ma
     if (train_seconds) *train_seconds = r.train_seconds;
     if (r.nonfinite_step >= 0)
       return fail(MSX_E_NONFINITE, "E-TRAIN-001: the loss of step " + std::to_string(r.nonfinite_step) + " is not finite");
+    return MSX_OK;
+  });
+}
+
+int msx_bench_config(msx_ctx* ctx, const char* config, int64_t masked_rows, uint32_t warmup, uint32_t steps,
+                     double* ms_per_step, float* last_loss, char** profile) {
+  return guarded([&] {
+    uint64_t total = uint64_t(warmup) + steps + 1;
+    msx::Compiled c = msx::compile_config(config, masked_rows, int64_t(std::max<uint64_t>(total, c_steps_floor(config))));
+    ctx->session.reset();
+    ctx->step = c.step;
+    ctx->forward = c.forward;
+    ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction);
+    msx::Session& s = *ctx->session;
+    msx::Feed feed(c);
+    if (feed.needs_teacher())
+      feed.set_target(s.predict(msx::initialize(c.forward, c.config.seed, msx::Stream::Teacher), feed.batch(0)));
+    s.set_params(msx::initialize(c.forward, c.config.seed, msx::Stream::Init));
+    const uint64_t end = c.config.steps;
+    // Host inputs of every step are made before the timed region: it times the device's steps.
+    std::vector<msx::StepInputs> ins;
+    for (uint64_t k = 0; k < total; ++k) ins.push_back(msx::step_inputs(c, feed, k, end));
+    for (uint32_t k = 0; k < warmup; ++k) s.train_step(ins[k]);
+    s.sync();
+    hipEvent_t e0, e1;
+    msx::hip_check(hipEventCreate(&e0), "hipEventCreate");
+    msx::hip_check(hipEventCreate(&e1), "hipEventCreate");
+    msx::hip_check(hipEventRecord(e0, s.stream()), "hipEventRecord");
+    for (uint32_t k = 0; k < steps; ++k) s.train_step(ins[warmup + k]);
+    msx::hip_check(hipEventRecord(e1, s.stream()), "hipEventRecord");
+    s.sync();
+    float ms = 0;
+    msx::hip_check(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (ms_per_step) *ms_per_step = steps ? double(ms) / steps : 0.0;
+    auto losses = s.losses();
+    if (last_loss) *last_loss = losses.empty() ? 0.0f : losses.back();
+    if (profile) {
+      auto rows = s.profile_step(ins[warmup + steps]);
+      std::string text;
+      for (auto& [what, t] : rows) text += what + "\t" + std::to_string(t) + "\n";
+      *profile = dup(text);
+    }
     return MSX_OK;
   });
 }

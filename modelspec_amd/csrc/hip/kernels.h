@@ -57,13 +57,19 @@ void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* ou
 void dropout(hipStream_t s, const float* x, float* o, int64_t n, const int32_t* token, uint64_t seed,
              uint64_t threshold, float scale);
 
-// Attention over a key mask [B, S]; q [B*L, H], k/v [B*S, H].
+// Attention over a key mask [B, S]; q [B*L, H], k/v [B*S, H] (attention.hip).
 bool attention_fits(int64_t s, int64_t d);
+bool attention_mfma(int64_t L, int64_t S, int64_t d);  // the MFMA path runs (else the scalar one)
+// stats: [B*heads*L, 2] softmax maximum and sum per query (written when non-null; required by the
+// MFMA backward).
 void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v, const float* mask, float* o,
-                   int64_t B, int64_t L, int64_t S, int64_t H, int64_t heads);
-// Any of dq/dk/dv may be null.
-void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v, const float* mask, const float* g,
-                   float* dq, float* dk, float* dv, int64_t B, int64_t L, int64_t S, int64_t H, int64_t heads);
+                   float* stats, int64_t B, int64_t L, int64_t S, int64_t H, int64_t heads);
+// Any of dk/dv may be null; the MFMA path needs dq, o (the forward's output), stats and dsum
+// ([B*heads*L] scratch).
+void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v, const float* mask, const float* o,
+                   const float* stats, const float* g, float* dq, float* dk, float* dv, float* dsum, int64_t B,
+                   int64_t L, int64_t S, int64_t H, int64_t heads);
+void prepare_attention();
 
 // Cross-entropy: stats = [rows, 2] (max, total); den = [1] f32 weight sum rounded from f64.
 void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, int64_t v);

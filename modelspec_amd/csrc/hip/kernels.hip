@@ -485,220 +485,6 @@ void dropout(hipStream_t s, const float* x, float* o, int64_t n, const int32_t* 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Attention: one block per (sequence, head) [and query block]. K and V of the head staged in LDS;
-// a thread owns a query row (forward, dQ) or a key row (dK, dV). Scores are fused dot products
-// over the head's columns; the softmax takes the maximum over unmasked keys first.
-template <int D>
-__global__ __launch_bounds__(64) void k_attn_fwd(const float* __restrict__ q, const float* __restrict__ k,
-                                                 const float* __restrict__ v, const float* __restrict__ mask,
-                                                 float* __restrict__ o, int L, int S, int H, int heads, float scale) {
-  extern __shared__ float sm[];
-  float* Ks = sm;
-  float* Vs = sm + S * D;
-  float* Ms = sm + 2 * S * D;
-  const int b = blockIdx.x / heads, head = blockIdx.x % heads;
-  for (int e = threadIdx.x; e < S * D; e += blockDim.x) {
-    int j = e / D, c = e % D;
-    Ks[e] = k[(int64_t(b) * S + j) * H + head * D + c];
-    Vs[e] = v[(int64_t(b) * S + j) * H + head * D + c];
-  }
-  for (int j = threadIdx.x; j < S; j += blockDim.x) Ms[j] = mask[int64_t(b) * S + j];
-  __syncthreads();
-  const int i = blockIdx.y * blockDim.x + threadIdx.x;
-  if (i >= L) return;
-  const int64_t row = int64_t(b) * L + i;
-  float qr[D], acc[D];
-#pragma unroll
-  for (int c = 0; c < D; ++c) { qr[c] = q[row * H + head * D + c]; acc[c] = 0.0f; }
-  float mx = 0.0f;
-  bool first = true;
-  for (int j = 0; j < S; ++j) {
-    if (Ms[j] == 0.0f) continue;
-    const float* kj = Ks + j * D;
-    float sc = qr[0] * kj[0];
-#pragma unroll
-    for (int c = 1; c < D; ++c) sc = __builtin_fmaf(qr[c], kj[c], sc);
-    sc = sc * scale;
-    if (first || sc > mx) mx = sc;
-    first = false;
-  }
-  float total = 0.0f;
-  for (int j = 0; j < S; ++j) {
-    if (Ms[j] == 0.0f) continue;
-    const float* kj = Ks + j * D;
-    float sc = qr[0] * kj[0];
-#pragma unroll
-    for (int c = 1; c < D; ++c) sc = __builtin_fmaf(qr[c], kj[c], sc);
-    float e = expf(sc * scale - mx);
-    total += e;
-    const float* vj = Vs + j * D;
-#pragma unroll
-    for (int c = 0; c < D; ++c) acc[c] = __builtin_fmaf(e, vj[c], acc[c]);
-  }
-#pragma unroll
-  for (int c = 0; c < D; ++c) o[row * H + head * D + c] = acc[c] / total;
-}
-
-template <int D>
-__global__ __launch_bounds__(256) void k_attn_bwd(const float* __restrict__ q, const float* __restrict__ k,
-                                                  const float* __restrict__ v, const float* __restrict__ mask,
-                                                  const float* __restrict__ g, float* __restrict__ dq,
-                                                  float* __restrict__ dk, float* __restrict__ dv, int L, int S, int H,
-                                                  int heads, float scale) {
-  extern __shared__ float sm[];
-  float* Qs = sm;
-  float* Gs = Qs + L * D;
-  float* Ks = Gs + L * D;
-  float* Vs = Ks + S * D;
-  float* Ms = Vs + S * D;
-  float* st_m = Ms + S;
-  float* st_l = st_m + L;
-  float* st_d = st_l + L;
-  const int b = blockIdx.x / heads, head = blockIdx.x % heads;
-  for (int e = threadIdx.x; e < L * D; e += blockDim.x) {
-    int i = e / D, c = e % D;
-    Qs[e] = q[(int64_t(b) * L + i) * H + head * D + c];
-    Gs[e] = g[(int64_t(b) * L + i) * H + head * D + c];
-  }
-  for (int e = threadIdx.x; e < S * D; e += blockDim.x) {
-    int j = e / D, c = e % D;
-    Ks[e] = k[(int64_t(b) * S + j) * H + head * D + c];
-    Vs[e] = v[(int64_t(b) * S + j) * H + head * D + c];
-  }
-  for (int j = threadIdx.x; j < S; j += blockDim.x) Ms[j] = mask[int64_t(b) * S + j];
-  __syncthreads();
-  auto dot = [](const float* x, const float* y) {
-    float s = x[0] * y[0];
-#pragma unroll
-    for (int c = 1; c < D; ++c) s = __builtin_fmaf(x[c], y[c], s);
-    return s;
-  };
-  // Phase 1, per query row: softmax statistics, d = sum_j P dP, and dQ.
-  for (int i = threadIdx.x; i < L; i += blockDim.x) {
-    const float* qi = Qs + i * D;
-    const float* gi = Gs + i * D;
-    float mx = 0.0f;
-    bool first = true;
-    for (int j = 0; j < S; ++j) {
-      if (Ms[j] == 0.0f) continue;
-      float sc = dot(qi, Ks + j * D) * scale;
-      if (first || sc > mx) mx = sc;
-      first = false;
-    }
-    float total = 0.0f;
-    for (int j = 0; j < S; ++j) {
-      if (Ms[j] == 0.0f) continue;
-      total += expf(dot(qi, Ks + j * D) * scale - mx);
-    }
-    float dd = 0.0f;
-    for (int j = 0; j < S; ++j) {
-      if (Ms[j] == 0.0f) continue;
-      float p = expf(dot(qi, Ks + j * D) * scale - mx) / total;
-      dd = __builtin_fmaf(p, dot(gi, Vs + j * D), dd);
-    }
-    st_m[i] = mx;
-    st_l[i] = total;
-    st_d[i] = dd;
-    if (dq) {
-      float acc[D];
-#pragma unroll
-      for (int c = 0; c < D; ++c) acc[c] = 0.0f;
-      for (int j = 0; j < S; ++j) {
-        if (Ms[j] == 0.0f) continue;
-        float p = expf(dot(qi, Ks + j * D) * scale - mx) / total;
-        float ds = p * (dot(gi, Vs + j * D) - dd);
-        const float* kj = Ks + j * D;
-#pragma unroll
-        for (int c = 0; c < D; ++c) acc[c] = __builtin_fmaf(ds, kj[c], acc[c]);
-      }
-#pragma unroll
-      for (int c = 0; c < D; ++c) dq[(int64_t(b) * L + i) * H + head * D + c] = acc[c] * scale;
-    }
-  }
-  __syncthreads();
-  // Phase 2, per key row: dV = sum_i P g_i, dK = scale * sum_i dS q_i; a masked key stays +0.
-  for (int j = threadIdx.x; j < S; j += blockDim.x) {
-    const int64_t out = (int64_t(b) * S + j) * H + head * D;
-    const bool live = Ms[j] != 0.0f;
-    if (dv) {
-      float acc[D];
-#pragma unroll
-      for (int c = 0; c < D; ++c) acc[c] = 0.0f;
-      if (live)
-        for (int i = 0; i < L; ++i) {
-          float p = expf(dot(Qs + i * D, Ks + j * D) * scale - st_m[i]) / st_l[i];
-          const float* gi = Gs + i * D;
-#pragma unroll
-          for (int c = 0; c < D; ++c) acc[c] = __builtin_fmaf(p, gi[c], acc[c]);
-        }
-#pragma unroll
-      for (int c = 0; c < D; ++c) dv[out + c] = acc[c];
-    }
-    if (dk) {
-      float acc[D];
-#pragma unroll
-      for (int c = 0; c < D; ++c) acc[c] = 0.0f;
-      if (live)
-        for (int i = 0; i < L; ++i) {
-          const float* qi = Qs + i * D;
-          float p = expf(dot(qi, Ks + j * D) * scale - st_m[i]) / st_l[i];
-          float ds = p * (dot(Gs + i * D, Vs + j * D) - st_d[i]);
-#pragma unroll
-          for (int c = 0; c < D; ++c) acc[c] = __builtin_fmaf(ds, qi[c], acc[c]);
-        }
-#pragma unroll
-      for (int c = 0; c < D; ++c) dk[out + c] = live ? acc[c] * scale : 0.0f;
-    }
-  }
-}
-
-namespace {
-size_t fwd_lds(int64_t S, int64_t d) { return size_t((2 * S * d + S) * 4); }
-size_t bwd_lds(int64_t L, int64_t S, int64_t d) { return size_t((2 * L * d + 2 * S * d + S + 3 * L) * 4); }
-const size_t kLdsMax = 160 * 1024;
-}  // namespace
-
-bool attention_fits(int64_t s, int64_t d) {
-  return (d == 16 || d == 32 || d == 64 || d == 128) && bwd_lds(s, s, d) <= kLdsMax && s <= 65535;
-}
-
-void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v, const float* mask, float* o,
-                   int64_t B, int64_t L, int64_t S, int64_t H, int64_t heads) {
-  int64_t d = H / heads;
-  if (!attention_fits(S, d) || L > S) bad("attention shape outside the kernel's LDS budget");
-  float scale = 1.0f / sqrtf(float(d));
-  dim3 grid(unsigned(B * heads), unsigned((L + 63) / 64));
-  size_t lds = fwd_lds(S, d);
-  auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, grid, dim3(64), lds, s, q, k, v, mask, o, int(L), int(S), int(H), int(heads), scale);
-  };
-  switch (d) {
-    case 16: go(k_attn_fwd<16>); break;
-    case 32: go(k_attn_fwd<32>); break;
-    case 64: go(k_attn_fwd<64>); break;
-    default: go(k_attn_fwd<128>); break;
-  }
-}
-
-void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v, const float* mask, const float* g,
-                   float* dq, float* dk, float* dv, int64_t B, int64_t L, int64_t S, int64_t H, int64_t heads) {
-  int64_t d = H / heads;
-  if (!attention_fits(S, d) || L > S) bad("attention shape outside the kernel's LDS budget");
-  float scale = 1.0f / sqrtf(float(d));
-  size_t lds = bwd_lds(L, S, d);
-  int threads = int(std::min<int64_t>(256, std::max<int64_t>(64, (S + 63) / 64 * 64)));
-  auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(unsigned(B * heads)), dim3(threads), lds, s, q, k, v, mask, g, dq, dk, dv, int(L),
-                       int(S), int(H), int(heads), scale);
-  };
-  switch (d) {
-    case 16: go(k_attn_bwd<16>); break;
-    case 32: go(k_attn_bwd<32>); break;
-    case 64: go(k_attn_bwd<64>); break;
-    default: go(k_attn_bwd<128>); break;
-  }
-}
-
 // ---------------------------------------------------------------------------------------------
 // Cross-entropy. Row statistics once per logits tensor; the loss sums in f64 in one block.
 __global__ void k_ce_stats(const float* __restrict__ x, float* __restrict__ stats, int64_t v) {
@@ -891,16 +677,10 @@ __global__ void k_record_loss(const float* __restrict__ loss, float* __restrict_
 }
 void prepare() {
   // Kernels whose dynamic LDS may exceed the 64 KiB default; set once, outside any capture.
-  const void* kernels[] = {
-      reinterpret_cast<const void*>(k_attn_fwd<16>),  reinterpret_cast<const void*>(k_attn_fwd<32>),
-      reinterpret_cast<const void*>(k_attn_fwd<64>),  reinterpret_cast<const void*>(k_attn_fwd<128>),
-      reinterpret_cast<const void*>(k_attn_bwd<16>),  reinterpret_cast<const void*>(k_attn_bwd<32>),
-      reinterpret_cast<const void*>(k_attn_bwd<64>),  reinterpret_cast<const void*>(k_attn_bwd<128>),
-      reinterpret_cast<const void*>(k_sort_ids)};
-  for (const void* k : kernels) {
-    hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, int(kLdsMax));
-    if (e != hipSuccess) throw std::runtime_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
-  }
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_sort_ids),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (e != hipSuccess) throw std::runtime_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+  prepare_attention();
 }
 
 void record_loss(hipStream_t s, const float* loss, float* losses, uint32_t* counter, uint32_t capacity) {

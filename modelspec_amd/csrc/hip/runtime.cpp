@@ -252,6 +252,7 @@ void Executor::build() {
   std::map<uint32_t, void*> ln_stats_tok;             // LN input value -> stats [rows, 2]
   std::map<uint32_t, void*> ce_stats_tok;             // logits value -> stats [rows, 2]
   std::map<std::pair<uint32_t, uint32_t>, void*> ce_den_tok;  // (logits, weights) -> den
+  std::map<std::vector<uint32_t>, std::pair<uint32_t, void*>> attn_fwd;  // operands -> (output, stats)
   auto R = [&](size_t bytes) { return arena_.reserve(bytes); };
   auto A = [this](void* tok) { return arena_.at(tok); };
   auto P = [this](uint32_t id) { return ptr(id); };
@@ -267,7 +268,12 @@ void Executor::build() {
     const uint32_t id = x.id;
     const auto& o = x.operands;
     const int64_t count = x.ty.count();
-    std::string what = std::string(op_name(x.op)) + " %" + std::to_string(id);
+    std::string what = std::string(op_name(x.op)) + " %" + std::to_string(id) + " " + type_string(x.ty);
+    if (x.op == Op::MatMul || (x.op == Op::AddRows && mm_fused.count(o[0]))) {
+      const Node& m = p.node(x.op == Op::MatMul ? id : o[0]);
+      what += " k=" + std::to_string(shape(m.operands[0])[1]);
+      if (x.op == Op::AddRows) what = "MatMul+AddRows" + what.substr(7);
+    }
     auto push = [&](std::function<void(hipStream_t)> f) { pending.push_back({[what, f] { return Launch{what, f}; }}); };
     switch (x.op) {
       case Op::Input: case Op::ParamRead: case Op::Scalar: break;
@@ -425,8 +431,14 @@ void Executor::build() {
         int64_t B = shape(mask)[0], S = shape(mask)[1], L = shape(q)[0] / B, H = shape(q)[1], heads = x.heads;
         if (!hk::attention_fits(S, H / heads)) throw IrError("attention shape has no HIP kernel (head width or sequence too large)");
         if (p.node(mask).op == Op::Input) key_masks_.push_back(p.node(mask).name);
+        auto fkey = std::vector<uint32_t>{q, kv, v, mask, uint32_t(heads)};
+        bool mfma = hk::attention_mfma(L, S, H / heads);
         if (x.op == Op::Attention) {
-          push([=](hipStream_t s) { hk::attention_fwd(s, F(q), F(kv), F(v), F(mask), F(id), B, L, S, H, heads); });
+          void* st2 = mfma ? R(size_t(B * heads * L) * 8) : nullptr;
+          attn_fwd[fkey] = {id, st2};
+          push([=](hipStream_t s) {
+            hk::attention_fwd(s, F(q), F(kv), F(v), F(mask), F(id), st2 ? static_cast<float*>(A(st2)) : nullptr, B, L, S, H, heads);
+          });
           break;
         }
         auto key = o;
@@ -438,10 +450,32 @@ void Executor::build() {
         if (first != int64_t(id)) break;  // the group's first member launches for all three
         uint32_t g = o[4];
         std::array<int64_t, 3> members = grp;
+        // The backward reads the forward's output and softmax statistics: those of the step's own
+        // Attention over the same operands, else a forward run into scratch first.
+        int64_t fwd_out = -1;
+        void *stats_tok = nullptr, *scratch_o = nullptr, *dsum = nullptr, *dq_scratch = nullptr;
+        if (mfma) {
+          auto f = attn_fwd.find(fkey);
+          if (f != attn_fwd.end()) {
+            fwd_out = int64_t(f->second.first);
+            stats_tok = f->second.second;
+          } else {
+            scratch_o = R(size_t(shape(q)[0] * H) * 4);
+            stats_tok = R(size_t(B * heads * L) * 8);
+            push([=](hipStream_t s) {
+              hk::attention_fwd(s, F(q), F(kv), F(v), F(mask), static_cast<float*>(A(scratch_o)),
+                                static_cast<float*>(A(stats_tok)), B, L, S, H, heads);
+            });
+          }
+          dsum = R(size_t(B * heads * L) * 4);
+          if (members[0] < 0) dq_scratch = R(size_t(shape(q)[0] * H) * 4);
+        }
         push([=](hipStream_t s) {
           auto out = [&](int64_t v2) { return v2 >= 0 ? F(uint32_t(v2)) : nullptr; };
-          hk::attention_bwd(s, F(q), F(kv), F(v), F(mask), F(g), out(members[0]), out(members[1]), out(members[2]), B, L, S,
-                            H, heads);
+          float* dq = members[0] >= 0 ? F(uint32_t(members[0])) : (dq_scratch ? static_cast<float*>(A(dq_scratch)) : nullptr);
+          const float* fo = fwd_out >= 0 ? F(uint32_t(fwd_out)) : (scratch_o ? static_cast<float*>(A(scratch_o)) : nullptr);
+          hk::attention_bwd(s, F(q), F(kv), F(v), F(mask), fo, stats_tok ? static_cast<float*>(A(stats_tok)) : nullptr, F(g), dq,
+                            out(members[1]), out(members[2]), dsum ? static_cast<float*>(A(dsum)) : nullptr, B, L, S, H, heads);
         });
         break;
       }
