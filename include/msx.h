@@ -55,6 +55,11 @@ int msx_device_count(void);
 int msx_compile_config(const char* config, int64_t masked_rows, int64_t steps, char** step_ir, char** forward_ir);
 void msx_free(void* p);
 
+/* Parses a printed training step and prints it back (msx_free the result): the validation
+ * msx_load applies before planning, without a device. Replaces artifact::read's checks of the
+ * plan it consumes (crates/modelspec-core/src/artifact.rs:426). */
+int msx_check_ir(const char* step_ir, char** normalized);
+
 /* Opens device `device`. Replaces vulkan::on_device (crates/modelspec-runtime/src/vulkan/mod.rs:216-552). */
 int msx_open(int device, msx_ctx** out);
 void msx_close(msx_ctx* ctx);
@@ -92,12 +97,13 @@ int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t ma
                      uint64_t losses_len, float* params, uint64_t params_len, double* train_seconds);
 
 /* Times `steps` graph-launched training steps of a built-in config after `warmup` (HIP events on
- * the run's stream; host inputs made before the timed region), then profiles one more step
- * eagerly with an event pair per launch into `profile` ("launch\tms" lines; free with msx_free).
- * Replaces `train --clock --profile` (crates/modelspec-cli/src/train.rs:17-31,
- * vulkan/profile.rs:1-14). */
+ * the run's stream after every step into step_ms[steps], may be null; host inputs made before the
+ * timed region), then runs `profile_reps` more steps eagerly with an event pair around every
+ * launch into `profile` ("launch\tms\tflop\tbytes" lines, ms the mean over the reps, flop and
+ * bytes the reference's algorithmic count; free with msx_free). Replaces `train --clock
+ * --profile` (crates/modelspec-cli/src/train.rs:17-31, vulkan/profile.rs:1-14). */
 int msx_bench_config(msx_ctx* ctx, const char* config, int64_t masked_rows, uint32_t warmup, uint32_t steps,
-                     double* ms_per_step, float* last_loss, char** profile);
+                     double* ms_per_step, double* step_ms, float* last_loss, uint32_t profile_reps, char** profile);
 
 /* One program (print.rs text of a Tensor IR program) on the device, for per-op tests: inputs by
  * name, parameters by ParamId; output k read back with msx_prog_output. */

@@ -234,20 +234,34 @@ def config_steps(name):
     return _STEPS[name]
 
 
-def bench_config(ctx, name, warmup, steps, masked_rows=-1, profile=True):
-    """(ms per step, last loss, [(launch, ms)] of one eagerly profiled step)."""
+def bench_config(ctx, name, warmup, steps, masked_rows=-1, profile_reps=1):
+    """(mean ms per step, [ms of each timed step], last loss, [(launch, ms, flop, bytes)])."""
     L = lib()
     L.msx_bench_config.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint32,
-                                   ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_float),
-                                   ctypes.POINTER(ctypes.c_void_p)]
+                                   ctypes.POINTER(ctypes.c_double), ctypes.c_void_p, ctypes.POINTER(ctypes.c_float),
+                                   ctypes.c_uint32, ctypes.POINTER(ctypes.c_void_p)]
     ms, loss, rep = ctypes.c_double(), ctypes.c_float(), ctypes.c_void_p()
-    _check(L.msx_bench_config(ctx._h, name.encode(), masked_rows, warmup, steps, ctypes.byref(ms), ctypes.byref(loss),
-                              ctypes.byref(rep) if profile else None))
+    per_step = np.zeros(max(1, steps), np.float64)
+    _check(L.msx_bench_config(ctx._h, name.encode(), masked_rows, warmup, steps, ctypes.byref(ms),
+                              per_step.ctypes.data, ctypes.byref(loss), profile_reps,
+                              ctypes.byref(rep) if profile_reps else None))
     rows = []
-    if profile and rep.value:
+    if profile_reps and rep.value:
         text = ctypes.string_at(rep).decode()
         L.msx_free(rep)
         for line in text.splitlines():
-            what, t = line.rsplit("\t", 1)
-            rows.append((what, float(t)))
-    return ms.value, loss.value, rows
+            what, t, flop, nbytes = line.rsplit("\t", 3)
+            rows.append((what, float(t), float(flop), float(nbytes)))
+    return ms.value, per_step[:steps].tolist(), loss.value, rows
+
+
+def check_ir(step_ir):
+    """Parse + print of a training step through the library (no device needed)."""
+    out = ctypes.c_void_p()
+    L = lib()
+    L.msx_check_ir.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]
+    _check(L.msx_check_ir(step_ir.encode(), ctypes.byref(out)))
+    try:
+        return ctypes.string_at(out).decode()
+    finally:
+        L.msx_free(out)

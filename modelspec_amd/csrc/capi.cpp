@@ -102,6 +102,14 @@ int msx_compile_config(const char* config, int64_t masked_rows, int64_t steps, c
 
 void msx_free(void* p) { std::free(p); }
 
+int msx_check_ir(const char* step_ir, char** normalized) {
+  return guarded([&] {
+    msx::TrainingStep t = msx::parse_step(step_ir);
+    if (normalized) *normalized = dup(msx::print_step(t));
+    return MSX_OK;
+  });
+}
+
 int msx_open(int device, msx_ctx** out) {
   return guarded([&] {
     int n = 0;
@@ -241,9 +249,9 @@ int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t ma
 }
 
 int msx_bench_config(msx_ctx* ctx, const char* config, int64_t masked_rows, uint32_t warmup, uint32_t steps,
-                     double* ms_per_step, float* last_loss, char** profile) {
+                     double* ms_per_step, double* step_ms, float* last_loss, uint32_t profile_reps, char** profile) {
   return guarded([&] {
-    uint64_t total = uint64_t(warmup) + steps + 1;
+    uint64_t total = uint64_t(warmup) + steps + std::max<uint32_t>(1, profile_reps);
     msx::Compiled c = msx::compile_config(config, masked_rows, int64_t(std::max<uint64_t>(total, c_steps_floor(config))));
     ctx->session.reset();
     ctx->step = c.step;
@@ -260,24 +268,38 @@ int msx_bench_config(msx_ctx* ctx, const char* config, int64_t masked_rows, uint
     for (uint64_t k = 0; k < total; ++k) ins.push_back(msx::step_inputs(c, feed, k, end));
     for (uint32_t k = 0; k < warmup; ++k) s.train_step(ins[k]);
     s.sync();
-    hipEvent_t e0, e1;
-    msx::hip_check(hipEventCreate(&e0), "hipEventCreate");
-    msx::hip_check(hipEventCreate(&e1), "hipEventCreate");
-    msx::hip_check(hipEventRecord(e0, s.stream()), "hipEventRecord");
-    for (uint32_t k = 0; k < steps; ++k) s.train_step(ins[warmup + k]);
-    msx::hip_check(hipEventRecord(e1, s.stream()), "hipEventRecord");
+    // One event after every step: the step times, whose median the benchmark reports.
+    std::vector<hipEvent_t> ev(size_t(steps) + 1);
+    for (auto& e : ev) msx::hip_check(hipEventCreate(&e), "hipEventCreate");
+    msx::hip_check(hipEventRecord(ev[0], s.stream()), "hipEventRecord");
+    for (uint32_t k = 0; k < steps; ++k) {
+      s.train_step(ins[warmup + k]);
+      msx::hip_check(hipEventRecord(ev[k + 1], s.stream()), "hipEventRecord");
+    }
     s.sync();
-    float ms = 0;
-    msx::hip_check(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-    if (ms_per_step) *ms_per_step = steps ? double(ms) / steps : 0.0;
+    double total_ms = 0;
+    for (uint32_t k = 0; k < steps; ++k) {
+      float ms = 0;
+      msx::hip_check(hipEventElapsedTime(&ms, ev[k], ev[k + 1]), "hipEventElapsedTime");
+      if (step_ms) step_ms[k] = double(ms);
+      total_ms += ms;
+    }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    if (ms_per_step) *ms_per_step = steps ? total_ms / steps : 0.0;
     auto losses = s.losses();
     if (last_loss) *last_loss = losses.empty() ? 0.0f : losses.back();
     if (profile) {
-      auto rows = s.profile_step(ins[warmup + steps]);
+      // Eager steps with an event pair around every launch; each launch's mean over the reps.
+      std::vector<msx::Session::Timed> acc;
+      uint32_t reps = std::max<uint32_t>(1, profile_reps);
+      for (uint32_t r = 0; r < reps; ++r) {
+        auto rows = s.profile_step(ins[warmup + steps + r]);
+        if (acc.empty()) acc = rows;
+        else for (size_t i = 0; i < rows.size(); ++i) acc[i].ms += rows[i].ms;
+      }
       std::string text;
-      for (auto& [what, t] : rows) text += what + "\t" + std::to_string(t) + "\n";
+      for (auto& t : acc)
+        text += t.what + "\t" + std::to_string(t.ms / reps) + "\t" + std::to_string(t.flop) + "\t" + std::to_string(t.bytes) + "\n";
       *profile = dup(text);
     }
     return MSX_OK;

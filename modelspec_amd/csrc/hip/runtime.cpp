@@ -247,7 +247,7 @@ void Executor::build() {
   input_token_ = arena_.reserve(std::max<size_t>(input_bytes_, 256));
 
   // Workspaces, reserved per launch now; resolved after commit.
-  struct Pending { std::function<Launch()> make; };
+  struct Pending { std::function<Launch()> make; double flop = 0, bytes = 0; };
   std::vector<Pending> pending;
   std::map<uint32_t, void*> ln_stats_tok;             // LN input value -> stats [rows, 2]
   std::map<uint32_t, void*> ce_stats_tok;             // logits value -> stats [rows, 2]
@@ -275,6 +275,31 @@ void Executor::build() {
       if (x.op == Op::AddRows) what = "MatMul+AddRows" + what.substr(7);
     }
     auto push = [&](std::function<void(hipStream_t)> f) { pending.push_back({[what, f] { return Launch{what, f}; }}); };
+    const size_t first_pending = pending.size();
+    // Algorithmic cost of the node (kernel.rs:1221, 1565): flops of contractions, bytes of the
+    // values every other op reads and writes.
+    double flop = 0, bytes = 0;
+    auto elems = [&](uint32_t v) { return double(p.node(v).ty.count()); };
+    switch (x.op) {
+      case Op::MatMul: case Op::AddRows: {
+        if (x.op == Op::AddRows && !mm_fused.count(o[0])) { bytes = 4 * (2 * elems(id) + elems(o[1])); break; }
+        const Node& m = p.node(x.op == Op::MatMul ? id : o[0]);
+        double M = double(m.ty.shape[0]), N = double(m.ty.shape[1]), K = double(shape(m.operands[0])[1]);
+        flop = 2 * M * N * K;
+        bytes = 4 * (M * K + K * N + M * N + (x.op == Op::AddRows ? N : 0));
+        break;
+      }
+      case Op::Attention: case Op::AttentionGradQ: case Op::AttentionGradK: case Op::AttentionGradV: {
+        int64_t B = shape(o[3])[0], S = shape(o[3])[1], L = shape(o[0])[0] / B, H = shape(o[0])[1];
+        flop = (x.op == Op::Attention ? 4.0 : 8.0) * double(B) * double(L) * double(S) * double(H);
+        break;
+      }
+      case Op::Input: case Op::ParamRead: case Op::Scalar: break;
+      default:
+        for (auto v : o) bytes += 4 * elems(v);
+        bytes += 4 * double(count);
+        break;
+    }
     switch (x.op) {
       case Op::Input: case Op::ParamRead: case Op::Scalar: break;
       case Op::Add: case Op::Sub: case Op::Mul: case Op::Div: {
@@ -523,6 +548,10 @@ void Executor::build() {
       }
       case Op::Count_: break;
     }
+    if (pending.size() > first_pending) {
+      pending.back().flop = flop;
+      pending.back().bytes = bytes;
+    }
   }
   // The optimizer: gradients not computed in place are copied into the arena, then one launch
   // updates every trained parameter and its moments.
@@ -541,6 +570,7 @@ void Executor::build() {
       pending.push_back({[=] {
         return Launch{"AdamW", [=](hipStream_t s) { hk::adamw(s, s_.param_, s_.grad_, s_.m_, s_.v_, nt, c, F(lr), F(c1), F(c2)); }};
       }});
+      pending.back().bytes = 7.0 * 4.0 * double(nt);
     } else if (st.rule == Rule::Sgd && !st.updates.empty()) {
       uint32_t rate = p.node(st.updates.begin()->second).operands[1];
       uint32_t lr_scalar = p.node(rate).operands[0];
@@ -558,7 +588,11 @@ void Executor::build() {
   arena_.commit();
   for (auto& [vid, val] : constants) hip_check(hipMemcpy(ptr(vid), &val, 4, hipMemcpyHostToDevice), "hipMemcpy (constants)");
   for (auto& slot : inputs_) fixed_[slot.id] = static_cast<char*>(arena_.at(input_token_)) + slot.offset;
-  for (auto& pd : pending) launches_.push_back(pd.make());
+  for (auto& pd : pending) {
+    launches_.push_back(pd.make());
+    launches_.back().flop = pd.flop;
+    launches_.back().bytes = pd.bytes;
+  }
 }
 
 void Executor::stage(const Batch& batch) {
@@ -773,7 +807,7 @@ void Session::train_step(const StepInputs& in) {
   steps_since_reset_ += 1;
 }
 
-std::vector<std::pair<std::string, float>> Session::profile_step(const StepInputs& in) {
+std::vector<Session::Timed> Session::profile_step(const StepInputs& in) {
   step_exec_->stage(in.batch);
   const auto& ls = step_exec_->launches();
   std::vector<hipEvent_t> ev(ls.size() + 1);
@@ -784,11 +818,11 @@ std::vector<std::pair<std::string, float>> Session::profile_step(const StepInput
     hip_check(hipEventRecord(ev[i + 1], stream_), "hipEventRecord");
   }
   sync();
-  std::vector<std::pair<std::string, float>> out;
+  std::vector<Timed> out;
   for (size_t i = 0; i < ls.size(); ++i) {
     float ms = 0;
     hip_check(hipEventElapsedTime(&ms, ev[i], ev[i + 1]), "hipEventElapsedTime");
-    out.push_back({ls[i].what, ms});
+    out.push_back({ls[i].what, ms, ls[i].flop, ls[i].bytes});
   }
   for (auto& e : ev) (void)hipEventDestroy(e);
   stats_.steps += 1;

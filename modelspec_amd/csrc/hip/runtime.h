@@ -42,6 +42,10 @@ class DeviceArena {
 struct Launch {
   std::string what;  // op name and value, for profiles and errors
   std::function<void(hipStream_t)> run;
+  // Algorithmic work of the node this launch completes, by the reference's counting rule
+  // (crates/modelspec-core/src/ir/kernel.rs:1221, 1565): 2mnk for a matmul, 4 / 8 B heads L S d
+  // for attention forward / backward, bytes of the values read and written otherwise.
+  double flop = 0, bytes = 0;
 };
 
 struct RunStats {
@@ -66,7 +70,8 @@ class Session : public Engine {
 
   // Runs the step plan eagerly (no graph) with one event pair around every launch; returns the
   // launches and their milliseconds for the current inputs (the step's update is applied).
-  std::vector<std::pair<std::string, float>> profile_step(const StepInputs& in);
+  struct Timed { std::string what; float ms; double flop, bytes; };
+  std::vector<Timed> profile_step(const StepInputs& in);
   void use_graph(bool on) { use_graph_ = on; }
   void sync();
   hipStream_t stream() const { return stream_; }

@@ -195,7 +195,7 @@ Compiled transformer_block(int64_t V, int64_t H, int64_t heads, int64_t F, int64
   a.weight_decay = 0.01f;
   a.beta1 = 0.9f;
   a.beta2 = 0.999f;
-  a.eps = 1e-8f;
+  a.eps = 1e-6f;  // the reference examples' eps (examples/bert_tiny.mspec); the config names none
   a.warmup_steps = 0;
   return finish(c, L.b.finish(), loss, logits, Rule::AdamW, 1e-3f, a);
 }

@@ -83,6 +83,82 @@ extern "C" {
 
 const char* orc_last_error() { return g_error.c_str(); }
 
+// The host draws the oracle interprets with, for known-answer tests.
+void orc_philox(const uint32_t counter[4], const uint32_t key[2], uint32_t out[4]) {
+  msx::Philox4 r = msx::philox4x32_10(counter, key);
+  for (int i = 0; i < 4; ++i) out[i] = r.w[i];
+}
+void orc_blake3(const void* data, uint64_t len, uint8_t out[32]) { msx::blake3(data, size_t(len), out); }
+uint64_t orc_canonical_id(const char* path) { return msx::canonical_id(path); }
+uint64_t orc_dropout_id(const char* site, uint64_t step) { return msx::dropout_id(site, step); }
+uint64_t orc_dropout_threshold(float p) { return msx::dropout_threshold(p); }
+int orc_dropout_keeps(uint64_t seed, uint64_t id, uint32_t index, float p) { return msx::dropout_keeps(seed, id, index, p); }
+void orc_adamw_scalars(float lr, uint64_t t, uint64_t steps, uint64_t warmup, float beta1, float beta2, float out[3]) {
+  msx::AdamWConfig a;
+  a.beta1 = beta1;
+  a.beta2 = beta2;
+  a.warmup_steps = warmup;
+  msx::StepScalars s = msx::adamw_scalars(a, lr, t, steps);
+  out[0] = s.lr_t;
+  out[1] = s.c1;
+  out[2] = s.c2;
+}
+
+// The inputs of training step `step` of a built-in config, one name per line with its dtype, for
+// tests that feed the same step to both backends: names joined by '\n' into `names` (malloc'd),
+// data concatenated into a malloc'd buffer of 4-byte words.
+int orc_step_inputs(const char* config, int64_t steps, int64_t masked_rows, uint64_t step, char** names,
+                    void** data, uint64_t* words) {
+  try {
+    msx::Compiled c = msx::compile_config(config, masked_rows, steps);
+    msx::Feed feed(c);
+    if (feed.needs_teacher()) {
+      OracleEngine e(c);
+      feed.set_target(e.predict(msx::initialize(c.forward, c.config.seed, msx::Stream::Teacher), feed.batch(0)));
+    }
+    msx::StepInputs in = msx::step_inputs(c, feed, step, c.config.steps);
+    std::string text;
+    std::vector<uint32_t> buf;
+    for (auto& [name, v] : in.batch.f32) {
+      text += name + "\tf32\t" + std::to_string(v.size()) + "\n";
+      const uint32_t* w = reinterpret_cast<const uint32_t*>(v.data());
+      buf.insert(buf.end(), w, w + v.size());
+    }
+    for (auto& [name, v] : in.batch.i32) {
+      text += name + "\ti32\t" + std::to_string(v.size()) + "\n";
+      const uint32_t* w = reinterpret_cast<const uint32_t*>(v.data());
+      buf.insert(buf.end(), w, w + v.size());
+    }
+    *names = static_cast<char*>(std::malloc(text.size() + 1));
+    std::memcpy(*names, text.c_str(), text.size() + 1);
+    *data = std::malloc(std::max<size_t>(buf.size(), 1) * 4);
+    std::memcpy(*data, buf.data(), buf.size() * 4);
+    *words = buf.size();
+    return 0;
+  } catch (const std::exception& ex) {
+    g_error = ex.what();
+    return -1;
+  }
+}
+void orc_free(void* p) { std::free(p); }
+
+// The initial parameters of a built-in config (ParamId order, concatenated).
+int orc_init_params(const char* config, float* out, uint64_t len) {
+  try {
+    msx::Compiled c = msx::compile_config(config, -1, -1);
+    uint64_t off = 0;
+    for (auto& p : msx::initialize(c.forward, c.config.seed, msx::Stream::Init)) {
+      if (off + p.size() > len) { g_error = "buffer too small"; return -1; }
+      std::memcpy(out + off, p.data(), p.size() * 4);
+      off += p.size();
+    }
+    return 0;
+  } catch (const std::exception& ex) {
+    g_error = ex.what();
+    return -1;
+  }
+}
+
 // Trains `config` for `steps` steps (negative: the config's own) and writes steps + 1 losses and
 // the final parameters, concatenated in ParamId order. Returns 0, or -1 with orc_last_error().
 int orc_train(const char* config, int64_t steps, int64_t masked_rows, float* losses, uint64_t losses_len,

@@ -1,0 +1,162 @@
+"""TEST INFRASTRUCTURE: ctypes bindings of oracle/liboracle.so, the CPU oracle (a C++
+restatement of the reference interpreter). Used only as the checker of the HIP backend."""
+import ctypes
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "oracle", "liboracle.so")
+
+vp, u64, i64, u32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int64, ctypes.c_uint32
+
+
+class Oracle:
+    def __init__(self):
+        if not os.path.exists(LIB):
+            import subprocess
+            subprocess.run(["make", "-C", os.path.join(ROOT, "oracle")], check=True)
+        L = ctypes.CDLL(LIB)
+        L.orc_last_error.restype = ctypes.c_char_p
+        L.orc_train.argtypes = [ctypes.c_char_p, i64, i64, vp, u64, vp, u64, ctypes.POINTER(ctypes.c_double)]
+        L.orc_time_steps.argtypes = [ctypes.c_char_p, i64, i64, ctypes.POINTER(ctypes.c_double)]
+        L.orc_prog_new.argtypes = [ctypes.c_char_p, ctypes.c_int, u64]
+        L.orc_prog_new.restype = vp
+        L.orc_prog_free.argtypes = [vp]
+        L.orc_prog_run.argtypes = [vp, ctypes.c_int, vp, vp, vp, vp, ctypes.c_int, vp, vp]
+        L.orc_prog_output.argtypes = [vp, ctypes.c_int, vp, u64]
+        L.orc_philox.argtypes = [vp, vp, vp]
+        L.orc_blake3.argtypes = [ctypes.c_char_p, u64, vp]
+        L.orc_canonical_id.argtypes = [ctypes.c_char_p]
+        L.orc_canonical_id.restype = u64
+        L.orc_dropout_id.argtypes = [ctypes.c_char_p, u64]
+        L.orc_dropout_id.restype = u64
+        L.orc_dropout_threshold.argtypes = [ctypes.c_float]
+        L.orc_dropout_threshold.restype = u64
+        L.orc_dropout_keeps.argtypes = [u64, u64, u32, ctypes.c_float]
+        L.orc_adamw_scalars.argtypes = [ctypes.c_float, u64, u64, u64, ctypes.c_float, ctypes.c_float, vp]
+        L.orc_step_inputs.argtypes = [ctypes.c_char_p, i64, i64, u64, ctypes.POINTER(vp), ctypes.POINTER(vp),
+                                      ctypes.POINTER(u64)]
+        L.orc_free.argtypes = [vp]
+        L.orc_init_params.argtypes = [ctypes.c_char_p, vp, u64]
+        self.L = L
+
+    def err(self):
+        return self.L.orc_last_error().decode()
+
+    def train(self, config, steps=-1, masked_rows=-1, n_params=None, n_steps=None):
+        from modelspec_amd import api
+        step_ir, _ = api.compile_config(config, masked_rows, steps)
+        n_params = n_params or api.param_count(step_ir)
+        n_steps = n_steps if n_steps is not None else (steps if steps >= 0 else api.config_steps(config))
+        losses = np.zeros(n_steps + 1, np.float32)
+        params = np.zeros(n_params, np.float32)
+        secs = ctypes.c_double()
+        rc = self.L.orc_train(config.encode(), steps, masked_rows, losses.ctypes.data, losses.size, params.ctypes.data,
+                              params.size, ctypes.byref(secs))
+        if rc != 0:
+            raise RuntimeError(self.err())
+        return losses, params, secs.value
+
+    def seconds_per_step(self, config, steps, masked_rows=-1):
+        s = ctypes.c_double()
+        if self.L.orc_time_steps(config.encode(), steps, masked_rows, ctypes.byref(s)) != 0:
+            raise RuntimeError(self.err())
+        return s.value
+
+    def philox(self, counter, key):
+        c = np.array(counter, np.uint32)
+        k = np.array(key, np.uint32)
+        o = np.zeros(4, np.uint32)
+        self.L.orc_philox(c.ctypes.data, k.ctypes.data, o.ctypes.data)
+        return [int(x) for x in o]
+
+    def blake3(self, data):
+        out = (ctypes.c_uint8 * 32)()
+        self.L.orc_blake3(data, len(data), out)
+        return bytes(out)
+
+    def canonical_id(self, path):
+        return self.L.orc_canonical_id(path.encode())
+
+    def dropout_id(self, site, step):
+        return self.L.orc_dropout_id(site.encode(), step)
+
+    def dropout_threshold(self, p):
+        return self.L.orc_dropout_threshold(p)
+
+    def dropout_keeps(self, seed, id_, index, p):
+        return bool(self.L.orc_dropout_keeps(seed, id_, index, p))
+
+    def adamw_scalars(self, lr, t, steps, warmup, beta1=0.9, beta2=0.999):
+        o = np.zeros(3, np.float32)
+        self.L.orc_adamw_scalars(lr, t, steps, warmup, beta1, beta2, o.ctypes.data)
+        return o
+
+    def step_inputs(self, config, step, steps=-1, masked_rows=-1):
+        names, data, words = vp(), vp(), u64()
+        if self.L.orc_step_inputs(config.encode(), steps, masked_rows, step, ctypes.byref(names), ctypes.byref(data),
+                                  ctypes.byref(words)) != 0:
+            raise RuntimeError(self.err())
+        text = ctypes.string_at(names).decode()
+        raw = np.frombuffer(ctypes.string_at(data, words.value * 4), np.uint32).copy()
+        self.L.orc_free(names)
+        self.L.orc_free(data)
+        out, off = {}, 0
+        for line in text.splitlines():
+            name, dt, n = line.split("\t")
+            n = int(n)
+            chunk = raw[off:off + n]
+            off += n
+            out[name] = chunk.view(np.float32) if dt == "f32" else chunk.view(np.int32)
+        return out
+
+    def init_params(self, config, n):
+        out = np.zeros(n, np.float32)
+        if self.L.orc_init_params(config.encode(), out.ctypes.data, n) != 0:
+            raise RuntimeError(self.err())
+        return out
+
+    def run_program(self, text, inputs, params=(), seed=0, outputs=(0,)):
+        """Evaluates a printed program; returns the requested outputs as float32 arrays."""
+        h = self.L.orc_prog_new(text.encode(), 1, seed)
+        if not h:
+            raise RuntimeError(self.err())
+        try:
+            names = [n.encode() for n in inputs]
+            arrs = [np.ascontiguousarray(a) for a in inputs.values()]
+            n = len(arrs)
+            c_names = (ctypes.c_char_p * max(1, n))(*names)
+            c_dt = (ctypes.c_int * max(1, n))(*[0 if a.dtype == np.float32 else 1 for a in arrs])
+            c_data = (ctypes.c_void_p * max(1, n))(*[a.ctypes.data for a in arrs])
+            c_cnt = (ctypes.c_uint64 * max(1, n))(*[a.size for a in arrs])
+            ps = [np.ascontiguousarray(p, np.float32) for p in params]
+            c_p = (ctypes.c_void_p * max(1, len(ps)))(*[p.ctypes.data for p in ps])
+            c_pc = (ctypes.c_uint64 * max(1, len(ps)))(*[p.size for p in ps])
+            if self.L.orc_prog_run(h, n, c_names, c_dt, c_data, c_cnt, len(ps), c_p, c_pc) != 0:
+                raise RuntimeError(self.err())
+            res = []
+            for k in outputs:
+                cnt = output_count(text, k)
+                o = np.zeros(cnt, np.float32)
+                if self.L.orc_prog_output(h, k, o.ctypes.data, cnt) != 0:
+                    raise RuntimeError(self.err())
+                res.append(o)
+            return res
+        finally:
+            self.L.orc_prog_free(h)
+
+
+def output_count(text, k):
+    """Element count of output k of a printed program."""
+    outs = [int(line.split("%")[1].split()[0]) for line in text.splitlines() if line.startswith("output %")]
+    want = outs[k]
+    for line in text.splitlines():
+        s = line
+        for tag in ("forward ", "loss ", "gradient ", "optimizer "):
+            if s.startswith(tag):
+                s = s[len(tag):]
+        if s.startswith(f"%{want}:"):
+            dims = s[s.index("[") + 1:s.index("]")]
+            return int(np.prod([int(d) for d in dims.split(",")])) if dims.strip() else 1
+    raise KeyError(want)

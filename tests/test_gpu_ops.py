@@ -1,0 +1,196 @@
+"""Each HIP kernel against the CPU oracle on the same inputs, through the C ABI (msx_prog_*).
+
+Tolerance per kernel (common/mod.rs:17-40): |g - c| <= 1e-5 + 1e-4 * r, r = |c| elementwise and
+the sum of |terms| for contractions and sums. Integer and indexing work (gathers, the sorted-segment
+scatter, dropout masks) must match bit for bit."""
+import numpy as np
+import pytest
+
+from ops_lib import Draw, Prog, fast_values, within
+
+pytestmark = pytest.mark.gpu
+
+
+def both(ctx, oracle, p, inputs, outputs, seed=0, params=()):
+    text = p.text()
+    want = oracle.run_program(text, inputs, params, seed=seed, outputs=outputs)
+    prog = ctx.program(text, seed)
+    try:
+        prog.run(inputs, params)
+        got = [prog.output(k, w.size) for k, w in zip(outputs, want)]
+    finally:
+        prog.close()
+    return got, want
+
+
+@pytest.mark.parametrize("m,k,n,ta,tb", [
+    (5, 7, 3, False, False), (64, 64, 64, False, False), (130, 70, 33, True, False),
+    (33, 129, 65, False, True), (128, 4096, 128, True, False), (832, 128, 1000, False, True),
+    (100, 3000, 17, True, True),
+])
+def test_matmul(ctx, oracle, m, k, n, ta, tb):
+    a = fast_values(1, m * k).reshape((k, m) if ta else (m, k))
+    b = fast_values(2, k * n).reshape((n, k) if tb else (k, n))
+    p = Prog()
+    ai = p.input("a", a.shape)
+    bi = p.input("b", b.shape)
+    lhs = p.op("Transpose", [ai], (m, k)) if ta else ai
+    rhs = p.op("Transpose", [bi], (k, n)) if tb else bi
+    p.out(p.op("MatMul", [lhs, rhs], (m, n)))
+    (g,), (w,) = both(ctx, oracle, p, {"a": a, "b": b}, (0,))
+    A = (a.T if ta else a).astype(np.float64)
+    B = (b.T if tb else b).astype(np.float64)
+    ok, worst = within(g, w, (np.abs(A) @ np.abs(B)).reshape(-1))
+    assert ok, worst
+
+
+def test_matmul_with_bias_epilogue_and_sum_rows(ctx, oracle):
+    m, k, n = 4096, 128, 128
+    x, w, bias = fast_values(3, m * k).reshape(m, k), fast_values(4, k * n, 0.1).reshape(k, n), fast_values(5, n)
+    p = Prog()
+    xi, wi, bi = p.input("x", (m, k)), p.input("w", (k, n)), p.input("b", (n,))
+    y = p.op("AddRows", [p.op("MatMul", [xi, wi], (m, n)), bi], (m, n))
+    s = p.op("SumRows", [y], (n,))
+    (gy, gs), (wy, ws) = both(ctx, oracle, p.out(y, s), {"x": x, "w": w, "b": bias}, (0, 1))
+    r = (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64) + np.abs(bias)).reshape(-1)
+    assert within(gy, wy, r)[0]
+    assert within(gs, ws, np.abs(wy.reshape(m, n)).sum(axis=0))[0]
+
+
+@pytest.mark.parametrize("rows,h", [(6, 8), (4096, 128), (832, 128), (33, 200)])
+def test_layer_norm_family(ctx, oracle, rows, h):
+    x = fast_values(6, rows * h).reshape(rows, h)
+    gamma, beta = fast_values(7, h, 0.5), fast_values(8, h, 0.5)
+    G = fast_values(9, rows * h).reshape(rows, h)
+    p = Prog()
+    xi, gi, bi, Gi = p.input("x", (rows, h)), p.input("g", (h,)), p.input("b", (h,)), p.input("G", (rows, h))
+    y = p.op("LayerNorm", [xi, gi, bi], (rows, h))
+    dx = p.op("LayerNormGradX", [xi, gi, Gi], (rows, h))
+    dg = p.op("LayerNormGradGamma", [xi, Gi], (h,))
+    got, want = both(ctx, oracle, p.out(y, dx, dg), {"x": x, "g": gamma, "b": beta, "G": G}, (0, 1, 2))
+    # r: the magnitude of each term: |xhat| |gamma| + |beta| for y; sums of |terms| for the grads.
+    xhat = np.abs((x - x.mean(1, keepdims=True)) / x.std(1, keepdims=True))
+    assert within(got[0], want[0], (xhat * np.abs(gamma) + np.abs(beta) + 1).reshape(-1))[0]
+    rx = (np.abs(G) * np.abs(gamma)).sum(1, keepdims=True) / h * (1 + xhat) / x.std(1, keepdims=True)
+    assert within(got[1], want[1], (np.abs(want[1].reshape(rows, h)) + rx).reshape(-1))[0]
+    assert within(got[2], want[2], (np.abs(G) * xhat).sum(0))[0]
+
+
+def test_gelu_relu_elementwise(ctx, oracle):
+    n = 4096 * 512
+    x, G = fast_values(10, n), fast_values(11, n)
+    p = Prog()
+    xi, Gi = p.input("x", (n,)), p.input("G", (n,))
+    outs = [p.op("Gelu", [xi], (n,)), p.op("GeluGrad", [xi, Gi], (n,)), p.op("Relu", [xi], (n,)),
+            p.op("ReluGrad", [xi, Gi], (n,)), p.op("Add", [xi, Gi], (n,)), p.op("Mul", [xi, Gi], (n,)),
+            p.op("Sub", [xi, Gi], (n,))]
+    got, want = both(ctx, oracle, p.out(*outs), {"x": x, "G": G}, tuple(range(len(outs))))
+    for k, (g, w) in enumerate(zip(got, want)):
+        if k >= 2:  # relu, add, mul, sub: one correctly rounded operation, bit for bit
+            assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), k
+        else:
+            assert within(g, w, np.abs(w) + np.abs(x) * 1e-2)[0], k
+
+
+@pytest.mark.parametrize("B,S,H,heads,masked", [
+    (2, 16, 32, 2, False), (2, 16, 32, 2, True), (32, 128, 128, 2, False), (4, 128, 128, 2, True),
+    (2, 24, 32, 2, True),  # S not a multiple of 16: the scalar path
+    (2, 64, 256, 2, False),  # head width 128
+])
+def test_attention_and_gradients(ctx, oracle, B, S, H, heads, masked):
+    n = B * S * H
+    q, k, v, G = (fast_values(s, n, 0.5).reshape(B * S, H) for s in (12, 13, 14, 15))
+    mask = np.ones((B, S), np.float32)
+    if masked:
+        rng = np.random.default_rng(1)
+        mask[rng.random((B, S)) < 0.3] = 0.0
+        mask[:, 0] = 1.0
+    p = Prog()
+    qi, ki, vi = p.input("q", (B * S, H)), p.input("k", (B * S, H)), p.input("v", (B * S, H))
+    mi, Gi = p.input("mask", (B, S)), p.input("G", (B * S, H))
+    attr = f"[heads = {heads}]"
+    outs = [p.op("Attention", [qi, ki, vi, mi], (B * S, H), attr)]
+    for op in ("AttentionGradQ", "AttentionGradK", "AttentionGradV"):
+        outs.append(p.op(op, [qi, ki, vi, mi, Gi], (B * S, H), attr))
+    got, want = both(ctx, oracle, p.out(*outs), {"q": q, "k": k, "v": v, "mask": mask, "G": G}, (0, 1, 2, 3))
+    d = H // heads
+    # r: sum over keys of |p| |v|-like terms, bounded by the largest row magnitudes.
+    scale = np.abs(v).max() + np.abs(G).max() * (np.abs(q).max() + np.abs(k).max()) * np.sqrt(d) * 2
+    for idx, (g, w) in enumerate(zip(got, want)):
+        ok, worst = within(g, w, np.abs(w) + scale)
+        assert ok, (idx, worst)
+    if masked:
+        dead = np.flatnonzero(mask.reshape(-1) == 0)
+        for g in (got[2], got[3]):
+            assert np.all(g.reshape(B * S, H)[dead] == 0)
+
+
+def test_cross_entropy_and_gradient_full_head(ctx, oracle):
+    rows, V = 832, 30522
+    x = fast_values(16, rows * V).reshape(rows, V)
+    rng = np.random.default_rng(2)
+    labels = rng.integers(0, V, rows).astype(np.int32)
+    w = (rng.random(rows) < 0.75).astype(np.float32)
+    p = Prog()
+    xi, li, wi = p.input("x", (rows, V)), p.input("labels", (rows,), "i32"), p.input("w", (rows,))
+    loss = p.op("CrossEntropy", [xi, li, wi], ())
+    g = p.op("CrossEntropyGrad", [xi, li, wi, p.scalar(1.0)], (rows, V))
+    (gl, gg), (wl, wg) = both(ctx, oracle, p.out(loss, g), {"x": x, "labels": labels, "w": w}, (0, 1))
+    assert within(gl, wl, np.abs(wl) + 10)[0]
+    assert within(gg, wg, np.abs(wg) + 1.0 / w.sum())[0]
+
+
+def test_embedding_gather_and_sorted_segment_scatter_are_bit_exact(ctx, oracle):
+    rows, h, n = 30522, 128, 4096
+    rng = np.random.default_rng(3)
+    ranks = np.arange(1, rows - 4)
+    prob = ranks ** -1.1
+    ids = (5 + rng.choice(len(ranks), n, p=prob / prob.sum())).astype(np.int32)  # Zipf: hot rows
+    table = fast_values(17, rows * h).reshape(rows, h)
+    G = fast_values(18, n * h).reshape(n, h)
+    p = Prog()
+    ti, ii, Gi = p.input("t", (rows, h)), p.input("ids", (n,), "i32"), p.input("G", (n, h))
+    e = p.op("Embedding", [ti, ii], (n, h))
+    dg = p.op("EmbeddingGrad", [ii, Gi], (rows, h), f"[{rows}]")
+    got, want = both(ctx, oracle, p.out(e, dg), {"t": table, "ids": ids, "G": G}, (0, 1))
+    for g, w in zip(got, want):
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
+
+
+def test_dropout_masks_are_bit_exact_at_full_size(ctx, oracle):
+    n = 4096 * 128
+    x = fast_values(19, n)
+    token = np.array([-0x1357, 0x2468ACE], np.int32)
+    p = Prog()
+    xi, ti = p.input("x", (n,)), p.input("tok", (2,), "i32")
+    y = p.op("Dropout", [xi, ti], (n,), "[p = 0.1, site = tok]")
+    dy = p.op("DropoutGrad", [ti, xi], (n,), "[p = 0.1, site = tok]")
+    got, want = both(ctx, oracle, p.out(y, dy), {"x": x, "tok": token}, (0, 1), seed=42)
+    for g, w in zip(got, want):
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
+    kept = np.mean(got[0] != 0)
+    assert 0.88 < kept < 0.92
+
+
+def test_whole_tensor_sums(ctx, oracle):
+    n = 1 << 16
+    a, b = fast_values(20, n), fast_values(21, n)
+    p = Prog()
+    ai, bi = p.input("a", (256, 256)), p.input("b", (256, 256))
+    outs = [p.op("ReduceSum", [ai], ()), p.op("ReduceMean", [ai], ()), p.op("Mse", [ai, bi], ())]
+    got, want = both(ctx, oracle, p.out(*outs), {"a": a, "b": b}, (0, 1, 2))
+    r = [np.abs(a).sum(), np.abs(a).mean(), ((a - b) ** 2).mean()]
+    for g, w, rr in zip(got, want, r):
+        assert within(g, w, rr, atol=1e-6, rtol=1e-6)[0]
+
+
+def test_transpose_and_broadcast(ctx, oracle):
+    x = fast_values(22, 130 * 70).reshape(130, 70)
+    p = Prog()
+    xi = p.input("x", (130, 70))
+    t = p.op("Transpose", [xi], (70, 130))
+    s = p.op("ReduceSum", [xi], ())
+    bcast = p.op("BroadcastScalar", [s], (3, 5), "[3, 5]")
+    got, want = both(ctx, oracle, p.out(t, bcast), {"x": x}, (0, 1))
+    assert np.array_equal(got[0], want[0])
+    assert within(got[1], want[1], np.abs(x).sum())[0]
