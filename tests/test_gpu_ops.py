@@ -168,7 +168,7 @@ def test_dropout_masks_are_bit_exact_at_full_size(ctx, oracle):
     got, want = both(ctx, oracle, p.out(y, dy), {"x": x, "tok": token}, (0, 1), seed=42)
     for g, w in zip(got, want):
         assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
-    kept = np.mean(got[0] != 0)
+    kept = np.mean(got[0] != 0) / np.mean(x != 0)  # x holds planted zeros
     assert 0.88 < kept < 0.92
 
 
