@@ -30,6 +30,9 @@ struct GemmArgs {
   float* workspace; int64_t workspace_floats;
 };
 int gemm_split_for(int64_t m, int64_t n, int64_t k);  // the split-K factor the launcher uses
+// Floats of workspace a gemm of this shape needs (0 without split-K): the slices' partial tiles
+// and one counter per output tile, zero before the first launch and left zero by every launch.
+int64_t gemm_workspace(int64_t m, int64_t n, int64_t k);
 void gemm(hipStream_t s, const GemmArgs& g);
 
 void transpose(hipStream_t s, const float* a, float* o, int64_t rows, int64_t cols);  // a [rows,cols] -> o [cols,rows]
@@ -40,6 +43,9 @@ void column_sum(hipStream_t s, const float* x, float* out, int64_t rows, int64_t
 void ln_grad_gamma(hipStream_t s, const float* x, const float* g, const float* stats, float* out, int64_t rows,
                    int64_t h, float* partial, int64_t partial_floats);
 int64_t column_chunks(int64_t rows, int64_t h);
+// Floats of scratch a column reduction needs: the chunk partials and one counter per column tile
+// (zero before the first launch; every launch leaves them zero).
+int64_t column_workspace(int64_t rows, int64_t h);
 
 // LayerNorm family, eps 1e-12. stats = [rows, 2] (mean, rstd).
 void ln_stats(hipStream_t s, const float* x, float* stats, int64_t rows, int64_t h);

@@ -119,97 +119,175 @@ void fill_zero(hipStream_t s, void* o, int64_t bytes) {
 
 // ---------------------------------------------------------------------------------------------
 // GEMM on the f32 MFMA: a 64x64 output tile per 256-thread block, each wave a 32x32 quarter as
-// 2x2 MFMA 16x16x4 tiles, K staged through LDS 16 at a time. Operands may be read transposed in
-// place. Split-K writes each slice's partial to the workspace; a second kernel sums the slices in
-// ascending order, so the result is deterministic.
+// 2x2 MFMA 16x16x4 tiles. K advances 32 at a time through double-buffered LDS; the next K tile's
+// global loads (float4 where the operand's layout allows) are in flight while the MFMAs of the
+// current one run. Operands may be read transposed in place. Under split-K every slice writes its
+// partial tile to the workspace and k_splitk_sum adds the slices in ascending order, with every
+// slice's load in flight at once: deterministic.
 namespace {
-constexpr int BM = 64, BN = 64, BK = 16;
+constexpr int BM = 64, BN = 64, BK = 32, LDP = 68;  // LDS row stride (floats)
+
+// Loads of one K tile of an operand into registers, branch-free: out-of-range elements read a
+// clamped in-range address and are zeroed by a select, so no load waits on another. The (r, k)
+// element is A[r * lda + k], or A[k * lda + r] when T; thread t takes the float4 groups t and
+// t + 256 of the tile along the operand's contiguous dimension. V: the groups are 16-byte aligned
+// and the contiguous extent is a multiple of 4, so a group is wholly in or out of range.
+template <bool T, bool V>
+__device__ __forceinline__ void load_tile(const float* __restrict__ A, int64_t lda, int64_t rows, int64_t kend,
+                                          int64_t r0, int64_t k0, int tid, float (&reg)[8]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = tid + h * 256;
+    int r, k;
+    if (!T) { r = e >> 3; k = (e & 7) * 4; } else { k = e >> 4; r = (e & 15) * 4; }
+    const int64_t gr = r0 + r, gk = k0 + k;
+    if (V) {
+      const bool ok = !T ? (gr < rows && gk < kend) : (gk < kend && gr < rows);
+      const int64_t cr = gr < rows ? gr : rows - 1;
+      const int64_t ck = gk < kend ? gk : kend - 4;
+      const int64_t crr = !T ? cr : (gr < rows ? gr : rows - 4);
+      const int64_t ckk = !T ? ck : (gk < kend ? gk : kend - 1);
+      const float4 f = *reinterpret_cast<const float4*>(!T ? A + crr * lda + ckk : A + ckk * lda + crr);
+      reg[4 * h] = ok ? f.x : 0.0f;
+      reg[4 * h + 1] = ok ? f.y : 0.0f;
+      reg[4 * h + 2] = ok ? f.z : 0.0f;
+      reg[4 * h + 3] = ok ? f.w : 0.0f;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t rr = !T ? gr : gr + j, kk = !T ? gk + j : gk;
+        const bool ok = rr < rows && kk < kend;
+        const int64_t cr = rr < rows ? rr : rows - 1, ck = kk < kend ? kk : kend - 1;
+        const float x = !T ? A[cr * lda + ck] : A[ck * lda + cr];
+        reg[4 * h + j] = ok ? x : 0.0f;
+      }
+    }
+  }
 }
 
-template <bool TA, bool TB>
+// Stores a K tile into LDS as S[k][r].
+template <bool T>
+__device__ __forceinline__ void store_tile(float* S, int tid, const float (&reg)[8]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = tid + h * 256;
+    if (!T) {
+      const int r = e >> 3, k = (e & 7) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) S[(k + j) * LDP + r] = reg[4 * h + j];
+    } else {
+      const int k = e >> 4, r = (e & 15) * 4;
+      *reinterpret_cast<float4*>(S + k * LDP + r) = make_float4(reg[4 * h], reg[4 * h + 1], reg[4 * h + 2], reg[4 * h + 3]);
+    }
+  }
+}
+}  // namespace
+
+template <bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                               float* __restrict__ C, const float* __restrict__ bias, int64_t M,
                                               int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                                               int64_t kchunk, float* __restrict__ ws) {
-  __shared__ float As[BK][BM + 4];
-  __shared__ float Bs[BK][BN + 4];
+  __shared__ float As[2][BK * LDP];
+  __shared__ float Bs[2][BK * LDP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t m0 = int64_t(blockIdx.y) * BM, n0 = int64_t(blockIdx.x) * BN;
   const int64_t kbeg = int64_t(blockIdx.z) * kchunk;
   const int64_t kend = K < kbeg + kchunk ? K : kbeg + kchunk;
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   v4f acc00 = {0, 0, 0, 0}, acc01 = acc00, acc10 = acc00, acc11 = acc00;
+  float ra[8], rb[8];
+  // B's (k, j) element is B[k * ldb + j], or B[j * ldb + k] when TB: the same loader with the
+  // roles of "row" and "contiguous" swapped.
+  load_tile<TA, VA>(A, lda, M, kend, m0, kbeg, tid, ra);
+  load_tile<!TB, VB>(B, ldb, N, kend, n0, kbeg, tid, rb);
+  int buf = 0;
   for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
-#pragma unroll
-    for (int e0 = 0; e0 < BM * BK; e0 += 256) {
-      int e = e0 + tid;
-      int i, kk;
-      if (!TA) { i = e / BK; kk = e % BK; } else { kk = e / BM; i = e % BM; }
-      int64_t gi = m0 + i, gk = k0 + kk;
-      float v = 0.0f;
-      if (gi < M && gk < kend) v = TA ? A[gk * lda + gi] : A[gi * lda + gk];
-      As[kk][i] = v;
-    }
-#pragma unroll
-    for (int e0 = 0; e0 < BK * BN; e0 += 256) {
-      int e = e0 + tid;
-      int j, kk;
-      if (!TB) { kk = e / BN; j = e % BN; } else { j = e / BK; kk = e % BK; }
-      int64_t gj = n0 + j, gk = k0 + kk;
-      float v = 0.0f;
-      if (gj < N && gk < kend) v = TB ? B[gj * ldb + gk] : B[gk * ldb + gj];
-      Bs[kk][j] = v;
-    }
+    store_tile<TA>(As[buf], tid, ra);
+    store_tile<!TB>(Bs[buf], tid, rb);
     __syncthreads();
+    if (k0 + BK < kend) {
+      load_tile<TA, VA>(A, lda, M, kend, m0, k0 + BK, tid, ra);
+      load_tile<!TB, VB>(B, ldb, N, kend, n0, k0 + BK, tid, rb);
+    }
+    const float* as = As[buf];
+    const float* bs = Bs[buf];
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 4) {
-      const int kr = kk + (lane >> 4), c = lane & 15;
-      float a0 = As[kr][wm + c], a1 = As[kr][wm + 16 + c];
-      float b0 = Bs[kr][wn + c], b1 = Bs[kr][wn + 16 + c];
+      const int kr = (kk + (lane >> 4)) * LDP, c = lane & 15;
+      const float a0 = as[kr + wm + c], a1 = as[kr + wm + 16 + c];
+      const float b0 = bs[kr + wn + c], b1 = bs[kr + wn + 16 + c];
       acc00 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc00, 0, 0, 0);
       acc01 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc01, 0, 0, 0);
       acc10 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc10, 0, 0, 0);
       acc11 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc11, 0, 0, 0);
     }
-    __syncthreads();
+    buf ^= 1;
   }
   const v4f* accs[4] = {&acc00, &acc01, &acc10, &acc11};
+  if (!ws) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int64_t col = n0 + wn + (t & 1) * 16 + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = m0 + wm + (t >> 1) * 16 + 4 * (lane >> 4) + r;
+        if (row < M && col < N) C[row * ldc + col] = bias ? (*accs[t])[r] + bias[col] : (*accs[t])[r];
+      }
+    }
+    return;
+  }
+  // Split-K: this slice's partial tile; k_splitk_sum adds the slices in order.
+  const int64_t tile = int64_t(blockIdx.y) * gridDim.x + blockIdx.x;
+  float* part = ws + (int64_t(blockIdx.z) * gridDim.x * gridDim.y + tile) * (BM * BN);
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const int si = t >> 1, sj = t & 1;
-    const int64_t col = n0 + wn + sj * 16 + (lane & 15);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int64_t row = m0 + wm + si * 16 + 4 * (lane >> 4) + r;
-      if (row < M && col < N) {
-        float v = (*accs[t])[r];
-        if (ws) ws[int64_t(blockIdx.z) * M * N + row * N + col] = v;
-        else C[row * ldc + col] = bias ? v + bias[col] : v;
-      }
+      const int lr = wm + (t >> 1) * 16 + 4 * (lane >> 4) + r, lc = wn + (t & 1) * 16 + (lane & 15);
+      part[lr * BN + lc] = (*accs[t])[r];
     }
   }
 }
 
-__global__ void k_splitk_reduce(const float* __restrict__ ws, float* __restrict__ C, const float* __restrict__ bias,
-                                int64_t M, int64_t N, int64_t ldc, int splits) {
-  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  int64_t mn = M * N;
-  for (; i < mn; i += int64_t(gridDim.x) * blockDim.x) {
-    float acc = ws[i];
-    for (int z = 1; z < splits; ++z) acc = acc + ws[int64_t(z) * mn + i];
-    int64_t row = i / N, col = i % N;
-    C[row * ldc + col] = bias ? acc + bias[col] : acc;
-  }
+// Sums the split-K partial tiles in ascending slice order, one output element a thread; every
+// slice's load is issued before the adds.
+template <int SPLIT>
+__global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ ws, float* __restrict__ C,
+                                                    const float* __restrict__ bias, int64_t M, int64_t N, int64_t ldc,
+                                                    int tiles_x, int64_t tiles, int splits) {
+  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;  // over tiles * BM * BN
+  const int64_t tile = e / (BM * BN);
+  if (tile >= tiles) return;
+  const int in = int(e % (BM * BN));
+  const int64_t row = int64_t(tile / tiles_x) * BM + in / BN, col = int64_t(tile % tiles_x) * BN + in % BN;
+  const int64_t stride = tiles * (BM * BN);
+  float t[SPLIT];
+#pragma unroll
+  for (int z = 0; z < SPLIT; ++z) t[z] = z < splits ? ws[z * stride + e] : 0.0f;
+  float s = t[0];
+#pragma unroll
+  for (int z = 1; z < SPLIT; ++z)
+    if (z < splits) s += t[z];
+  for (int z = SPLIT; z < splits; ++z) s += ws[z * stride + e];
+  if (row < M && col < N) C[row * ldc + col] = bias ? s + bias[col] : s;
 }
 
 int gemm_split_for(int64_t m, int64_t n, int64_t k) {
   int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  if (tiles >= 512 || k < 256) return 1;
+  if (tiles >= 256 || k < 512) return 1;
   int64_t want = (1024 + tiles - 1) / tiles;
   int64_t most = k / 128;
   int64_t split = std::max<int64_t>(1, std::min(want, most));
   int64_t chunk = ((k + split - 1) / split + BK - 1) / BK * BK;
   return int((k + chunk - 1) / chunk);
+}
+
+int64_t gemm_workspace(int64_t m, int64_t n, int64_t k) {
+  int split = gemm_split_for(m, n, k);
+  if (split <= 1) return 0;
+  int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  return tiles * split * BM * BN;  // the slices' partial tiles
 }
 
 void gemm(hipStream_t s, const GemmArgs& g) {
@@ -218,25 +296,43 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   int split = gemm_split_for(g.m, g.n, g.k);
   int64_t chunk = ((g.k + split - 1) / split + BK - 1) / BK * BK;
   split = int((g.k + chunk - 1) / chunk);
+  int64_t tiles = ((g.m + BM - 1) / BM) * ((g.n + BN - 1) / BN);
   float* ws = nullptr;
   if (split > 1) {
-    if (!g.workspace || g.workspace_floats < int64_t(split) * g.m * g.n) bad("gemm split-K workspace too small");
+    if (!g.workspace || g.workspace_floats < tiles * split * BM * BN) bad("gemm split-K workspace too small");
     ws = g.workspace;
   }
   dim3 grid(unsigned((g.n + BN - 1) / BN), unsigned((g.m + BM - 1) / BM), unsigned(split));
   if (grid.y > 65535) bad("gemm M too large");
-  auto launch = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, g.a, g.b, g.c, split > 1 ? nullptr : g.bias, g.m, g.n, g.k,
-                       g.lda, g.ldb, g.ldc, chunk, ws);
+  // float4 loads need a leading dimension and base address that keep every group 16-byte aligned.
+  // float4 loads need 16-byte aligned groups and a contiguous extent that is a multiple of 4.
+  auto aligned = [](const float* p, int64_t ld, int64_t extent) {
+    return (reinterpret_cast<uintptr_t>(p) % 16 == 0) && ld % 4 == 0 && extent % 4 == 0;
   };
-  if (!g.ta && !g.tb) launch(k_gemm<false, false>);
-  else if (g.ta && !g.tb) launch(k_gemm<true, false>);
-  else if (!g.ta && g.tb) launch(k_gemm<false, true>);
-  else launch(k_gemm<true, true>);
+  const bool va = aligned(g.a, g.lda, g.ta ? g.m : g.k), vb = aligned(g.b, g.ldb, g.tb ? g.k : g.n);
+#define MSX_GEMM(TA, TB, VA, VB)                                                                                 \
+  hipLaunchKernelGGL((k_gemm<TA, TB, VA, VB>), grid, dim3(256), 0, s, g.a, g.b, g.c, g.bias, g.m, g.n, g.k, g.lda, \
+                     g.ldb, g.ldc, chunk, ws)
+#define MSX_GEMM_V(TA, TB)                  \
+  if (va && vb) MSX_GEMM(TA, TB, true, true);        \
+  else if (va) MSX_GEMM(TA, TB, true, false);        \
+  else if (vb) MSX_GEMM(TA, TB, false, true);        \
+  else MSX_GEMM(TA, TB, false, false);
+  if (!g.ta && !g.tb) { MSX_GEMM_V(false, false) }
+  else if (g.ta && !g.tb) { MSX_GEMM_V(true, false) }
+  else if (!g.ta && g.tb) { MSX_GEMM_V(false, true) }
+  else { MSX_GEMM_V(true, true) }
+#undef MSX_GEMM_V
+#undef MSX_GEMM
   if (split > 1) {
-    int64_t mn = g.m * g.n;
-    hipLaunchKernelGGL(k_splitk_reduce, dim3(std::min<unsigned>(blocks_for(mn, 256), 8192)), dim3(256), 0, s, ws,
-                       g.c, g.bias, g.m, g.n, g.ldc, split);
+    unsigned blocks = unsigned((tiles * BM * BN + 255) / 256);
+    int tx = int((g.n + BN - 1) / BN);
+    if (split <= 8)
+      hipLaunchKernelGGL(k_splitk_sum<8>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, tx, tiles, split);
+    else if (split <= 16)
+      hipLaunchKernelGGL(k_splitk_sum<16>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, tx, tiles, split);
+    else
+      hipLaunchKernelGGL(k_splitk_sum<32>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, tx, tiles, split);
   }
 }
 
@@ -274,52 +370,79 @@ void add_rows(hipStream_t s, const float* x, const float* b, float* o, int64_t r
 }
 
 int64_t column_chunks(int64_t rows, int64_t h) {
-  int64_t colblocks = (h + 255) / 256;
-  int64_t chunks = (rows + 63) / 64;
-  int64_t cap = std::max<int64_t>(1, 2048 / colblocks);
-  return std::max<int64_t>(1, std::min(chunks, cap));
+  int64_t tiles = (h + 63) / 64;
+  int64_t chunks = (rows + 31) / 32;                  // at least 32 rows a block
+  int64_t want = std::max<int64_t>(1, 512 / tiles);   // about 512 blocks in flight
+  return std::max<int64_t>(1, std::min(chunks, want));
 }
 
-// Partial column sums over row chunks; with stats, of g * xhat (LayerNormGradGamma).
-__global__ void k_column_partial(const float* __restrict__ x, const float* __restrict__ g,
-                                 const float* __restrict__ stats, float* __restrict__ partial, int64_t rows, int64_t h,
-                                 int64_t rows_per) {
-  int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (c >= h) return;
-  int64_t r0 = int64_t(blockIdx.y) * rows_per, r1 = std::min(rows, r0 + rows_per);
+// Column sums of x (or of g * xhat with LayerNorm statistics: LayerNormGradGamma). A block sums
+// 64 columns over a chunk of rows, its four waves interleaving rows; the chunk's partial goes to
+// `partial`, and the last block of a column tile to finish (counted by an integer atomic, reset by
+// that block for the next launch) adds the chunks' partials in ascending chunk order.
+__global__ __launch_bounds__(256) void k_column_sum(const float* __restrict__ x, const float* __restrict__ g,
+                                                    const float* __restrict__ stats, float* __restrict__ partial,
+                                                    float* __restrict__ out, unsigned* __restrict__ counter,
+                                                    int64_t rows, int64_t h, int64_t rows_per, int chunks) {
+  __shared__ float red[4][64];
+  __shared__ int last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t c = int64_t(blockIdx.x) * 64 + lane;
+  const int64_t r0 = int64_t(blockIdx.y) * rows_per, r1 = std::min(rows, r0 + rows_per);
   float acc = 0.0f;
-  bool first = true;
-  for (int64_t r = r0; r < r1; ++r) {
-    float t;
+  if (c < h) {
     if (stats) {
-      float xhat = (x[r * h + c] - stats[2 * r]) * stats[2 * r + 1];
-      t = g[r * h + c] * xhat;
+#pragma unroll 4
+      for (int64_t r = r0 + wave; r < r1; r += 4) acc += g[r * h + c] * ((x[r * h + c] - stats[2 * r]) * stats[2 * r + 1]);
     } else {
-      t = x[r * h + c];
+#pragma unroll 4
+      for (int64_t r = r0 + wave; r < r1; r += 4) acc += x[r * h + c];
     }
-    acc = first ? t : acc + t;
-    first = false;
   }
-  partial[int64_t(blockIdx.y) * h + c] = acc;
-}
-__global__ void k_column_final(const float* __restrict__ partial, float* __restrict__ out, int64_t h, int64_t chunks) {
-  int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (c >= h) return;
-  float acc = partial[c];
-  for (int64_t z = 1; z < chunks; ++z) acc = acc + partial[z * h + c];
-  out[c] = acc;
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && c < h) partial[int64_t(blockIdx.y) * h + c] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) last = atomicAdd(&counter[blockIdx.x], 1u) == unsigned(chunks - 1);
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  // Released by the other blocks' fences; never read here before, so plain loads see them. Wave
+  // w adds the chunks z = w mod 4 in ascending order with up to 16 loads in flight; the four wave
+  // sums are added in wave order.
+  float s = 0.0f;
+  if (c < h) {
+    for (int z0 = wave; z0 < chunks; z0 += 64) {
+      float t[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int z = z0 + 4 * u;
+        t[u] = z < chunks ? partial[int64_t(z) * h + c] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) s += t[u];
+    }
+  }
+  __syncthreads();
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && c < h) out[c] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+  if (threadIdx.x == 0) counter[blockIdx.x] = 0u;
 }
 static void column_reduce(hipStream_t s, const float* x, const float* g, const float* stats, float* out, int64_t rows,
                           int64_t h, float* partial, int64_t partial_floats) {
   if (h <= 0) return;
   if (rows <= 0) { fill_zero(s, out, h * 4); return; }
   int64_t chunks = column_chunks(rows, h);
-  if (partial_floats < chunks * h) bad("column reduction partial buffer too small");
   int64_t per = (rows + chunks - 1) / chunks;
   chunks = (rows + per - 1) / per;
-  hipLaunchKernelGGL(k_column_partial, dim3(unsigned((h + 255) / 256), unsigned(chunks)), dim3(256), 0, s, x, g,
-                     stats, partial, rows, h, per);
-  hipLaunchKernelGGL(k_column_final, dim3(unsigned((h + 255) / 256)), dim3(256), 0, s, partial, out, h, chunks);
+  int64_t tiles = (h + 63) / 64;
+  // The partial buffer holds chunks * h floats, then one counter per column tile.
+  if (partial_floats < chunks * h + tiles) bad("column reduction partial buffer too small");
+  unsigned* counter = reinterpret_cast<unsigned*>(partial + chunks * h);
+  hipLaunchKernelGGL(k_column_sum, dim3(unsigned(tiles), unsigned(chunks)), dim3(256), 0, s, x, g, stats, partial, out,
+                     counter, rows, h, per, int(chunks));
 }
 void column_sum(hipStream_t s, const float* x, float* out, int64_t rows, int64_t h, float* partial, int64_t pf) {
   column_reduce(s, x, nullptr, nullptr, out, rows, h, partial, pf);
@@ -328,6 +451,7 @@ void ln_grad_gamma(hipStream_t s, const float* x, const float* g, const float* s
                    int64_t h, float* partial, int64_t pf) {
   column_reduce(s, x, g, stats, out, rows, h, partial, pf);
 }
+int64_t column_workspace(int64_t rows, int64_t h) { return column_chunks(rows, h) * h + (h + 63) / 64 + 64; }
 
 // ---------------------------------------------------------------------------------------------
 // LayerNorm family: one wave per row, four rows per block.
@@ -416,40 +540,121 @@ void embedding(hipStream_t s, const float* table, const int32_t* ids, float* o, 
                      o, n, rows, h);
 }
 
-// Stable order of (id, k): one block bitonic-sorts the unique keys id << 32 | k in LDS.
+// Stable order of (id, k): one block of 1024 threads bitonic-sorts the unique keys id << 32 | k.
+// Thread t holds the E = pow2 / 1024 consecutive keys [t E, t E + E) in registers: strides below
+// E compare within the thread, strides below 64 E across the wave by shuffles, wider ones through
+// LDS.
+template <int E>
 __global__ __launch_bounds__(1024) void k_sort_ids(const int32_t* __restrict__ ids, uint64_t* __restrict__ keys,
-                                                   int64_t n, int64_t pow2) {
+                                                   int64_t n) {
   extern __shared__ uint64_t sk[];
-  for (int64_t i = threadIdx.x; i < pow2; i += blockDim.x)
-    sk[i] = i < n ? (uint64_t(uint32_t(ids[i])) << 32) | uint64_t(i) : ~uint64_t(0);
-  __syncthreads();
+  const int t = threadIdx.x;
+  const int64_t pow2 = int64_t(E) * 1024;
+  uint64_t v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    int64_t i = int64_t(t) * E + e;
+    v[e] = i < n ? (uint64_t(uint32_t(ids[i])) << 32) | uint64_t(i) : ~uint64_t(0);
+  }
   for (int64_t size = 2; size <= pow2; size <<= 1) {
     for (int64_t stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int64_t i = threadIdx.x; i < pow2; i += blockDim.x) {
-        int64_t j = i ^ stride;
-        if (j > i) {
+      if (stride < E) {
+        // The register pairs of each in-thread stride, unrolled with constant indices.
+#pragma unroll
+        for (int sh = 8; sh >= 1; sh >>= 1) {
+          if (sh >= E || sh != int(stride)) continue;
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const int f = e ^ sh;
+            if (f > e) {
+              const int64_t i = int64_t(t) * E + e;
+              const bool up = (i & size) == 0;
+              const uint64_t a = v[e], b = v[f];
+              const bool swap = (a > b) == up;
+              v[e] = swap ? b : a;
+              v[f] = swap ? a : b;
+            }
+          }
+        }
+      } else if (stride < int64_t(E) * 64) {
+        const int lanes = int(stride / E);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          int64_t i = int64_t(t) * E + e;
+          uint32_t lo = __shfl_xor(uint32_t(v[e]), lanes, 64), hi = __shfl_xor(uint32_t(v[e] >> 32), lanes, 64);
+          uint64_t other = (uint64_t(hi) << 32) | lo;
           bool up = (i & size) == 0;
-          uint64_t a = sk[i], b = sk[j];
-          if ((a > b) == up) { sk[i] = b; sk[j] = a; }
+          bool lower = (i & stride) == 0;  // this element is the pair's lower index
+          bool take_min = lower == up;
+          v[e] = take_min ? (other < v[e] ? other : v[e]) : (other > v[e] ? other : v[e]);
+        }
+      } else {
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < E; ++e) sk[int64_t(t) * E + e] = v[e];
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          int64_t i = int64_t(t) * E + e;
+          uint64_t other = sk[i ^ stride];
+          bool up = (i & size) == 0;
+          bool lower = (i & stride) == 0;
+          bool take_min = lower == up;
+          v[e] = take_min ? (other < v[e] ? other : v[e]) : (other > v[e] ? other : v[e]);
         }
       }
-      __syncthreads();
     }
   }
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) keys[i] = sk[i];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    int64_t i = int64_t(t) * E + e;
+    if (i < n) keys[i] = v[e];
+  }
 }
 
-// One block per sorted position; the first position of each id sums its rows in ascending k.
-__global__ void k_segment_sum(const uint64_t* __restrict__ keys, const float* __restrict__ g, float* __restrict__ out,
-                              int64_t n, int64_t rows, int64_t h) {
-  int64_t p = blockIdx.x;
-  uint32_t id = uint32_t(keys[p] >> 32);
+// One block per sorted position; the block of an id's first position adds the id's rows in
+// ascending k, from +0, one f32 rounding per add: the reference's order (interpreter.rs:931-941),
+// bit for bit. The segment's rows are staged through LDS a chunk at a time, every load of a chunk
+// in flight together; the in-order adds then read LDS.
+__global__ __launch_bounds__(256) void k_segment_sum(const uint64_t* __restrict__ keys, const float* __restrict__ g,
+                                                     float* __restrict__ out, int64_t n, int64_t rows, int64_t h,
+                                                     int chunk) {
+  extern __shared__ float stage[];
+  __shared__ int seg_end;
+  const int tid = threadIdx.x;
+  const int64_t p = blockIdx.x;
+  const uint32_t id = uint32_t(keys[p] >> 32);
   if (p > 0 && uint32_t(keys[p - 1] >> 32) == id) return;
   if (int64_t(id) >= rows) return;
-  for (int64_t c = threadIdx.x; c < h; c += blockDim.x) {
-    float acc = 0.0f;
-    for (int64_t q = p; q < n && uint32_t(keys[q] >> 32) == id; ++q) acc = acc + g[int64_t(uint32_t(keys[q])) * h + c];
-    out[int64_t(id) * h + c] = acc;
+  if (tid == 0) seg_end = int(n);
+  __syncthreads();
+  for (int64_t base = p + 1; base < n; base += 256) {
+    const int64_t idx = base + tid;
+    if (idx < n && uint32_t(keys[idx] >> 32) != id) atomicMin(&seg_end, int(idx));
+    __syncthreads();
+    if (seg_end < base + 256) break;
+  }
+  const int64_t end = seg_end;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // columns tid, tid + 256, ... (h <= 1024)
+  for (int64_t q0 = p; q0 < end; q0 += chunk) {
+    const int64_t cnt = end - q0 < chunk ? end - q0 : chunk;
+    for (int64_t e = tid; e < cnt * h; e += 256) {
+      const int64_t r = e / h, c = e - r * h;
+      stage[e] = g[int64_t(uint32_t(keys[q0 + r])) * h + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = tid + 256 * u;
+      if (c < h)
+        for (int64_t r = 0; r < cnt; ++r) acc[u] = acc[u] + stage[r * h + c];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t c = tid + 256 * u;
+    if (c < h) out[int64_t(id) * h + c] = acc[u];
   }
 }
 
@@ -457,12 +662,21 @@ void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* ou
                     uint64_t* keys) {
   fill_zero(s, out, rows * h * 4);
   if (n <= 0) return;
-  int64_t pow2 = 1;
+  if (n > 16384) bad("embedding gradient over more than 16384 ids");
+  int64_t pow2 = 1024;
   while (pow2 < n) pow2 <<= 1;
-  if (pow2 * 8 > 160 * 1024) bad("embedding gradient over more than 16384 ids");
-  hipLaunchKernelGGL(k_sort_ids, dim3(1), dim3(1024), size_t(pow2 * 8), s, ids, keys, n, pow2);
-  hipLaunchKernelGGL(k_segment_sum, dim3(unsigned(n)), dim3(h >= 256 ? 256 : (h >= 128 ? 128 : 64)), 0, s, keys, g,
-                     out, n, rows, h);
+  size_t lds = size_t(pow2) * 8;
+  switch (pow2 / 1024) {
+    case 1: hipLaunchKernelGGL(k_sort_ids<1>, dim3(1), dim3(1024), lds, s, ids, keys, n); break;
+    case 2: hipLaunchKernelGGL(k_sort_ids<2>, dim3(1), dim3(1024), lds, s, ids, keys, n); break;
+    case 4: hipLaunchKernelGGL(k_sort_ids<4>, dim3(1), dim3(1024), lds, s, ids, keys, n); break;
+    case 8: hipLaunchKernelGGL(k_sort_ids<8>, dim3(1), dim3(1024), lds, s, ids, keys, n); break;
+    default: hipLaunchKernelGGL(k_sort_ids<16>, dim3(1), dim3(1024), lds, s, ids, keys, n); break;
+  }
+  if (h > 1024) bad("embedding gradient rows wider than 1024");
+  const int chunk = int(std::max<int64_t>(1, std::min<int64_t>(64, 16384 / h)));
+  hipLaunchKernelGGL(k_segment_sum, dim3(unsigned(n)), dim3(256), size_t(chunk) * size_t(h) * 4, s, keys, g, out, n,
+                     rows, h, chunk);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -487,23 +701,43 @@ void dropout(hipStream_t s, const float* x, float* o, int64_t n, const int32_t* 
 // ---------------------------------------------------------------------------------------------
 // ---------------------------------------------------------------------------------------------
 // Cross-entropy. Row statistics once per logits tensor; the loss sums in f64 in one block.
-__global__ void k_ce_stats(const float* __restrict__ x, float* __restrict__ stats, int64_t v) {
+// Row maximum, then the sum of exp(x - max), each pass with eight loads in flight per thread.
+__global__ __launch_bounds__(256) void k_ce_stats(const float* __restrict__ x, float* __restrict__ stats, int64_t v) {
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
   const float* row = x + r * v;
+  const int tid = threadIdx.x;
   float m = -INFINITY;
-  for (int64_t c = threadIdx.x; c < v; c += blockDim.x) m = fmaxf(m, row[c]);
+  for (int64_t c0 = 0; c0 < v; c0 += 256 * 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t c = c0 + tid + 256 * u;
+      t[u] = c < v ? row[c] : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m = fmaxf(m, t[u]);
+  }
   m = wave_max(m);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  if ((tid & 63) == 0) red[tid >> 6] = m;
   __syncthreads();
   m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   __syncthreads();
-  float t = 0.0f;
-  for (int64_t c = threadIdx.x; c < v; c += blockDim.x) t += expf(row[c] - m);
-  t = wave_sum(t);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
+  float total = 0.0f;
+  for (int64_t c0 = 0; c0 < v; c0 += 256 * 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t c = c0 + tid + 256 * u;
+      t[u] = c < v ? row[c] : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) total += expf(t[u] - m);
+  }
+  total = wave_sum(total);
+  if ((tid & 63) == 0) red[tid >> 6] = total;
   __syncthreads();
-  if (threadIdx.x == 0) { stats[2 * r] = m; stats[2 * r + 1] = (red[0] + red[1]) + (red[2] + red[3]); }
+  if (tid == 0) { stats[2 * r] = m; stats[2 * r + 1] = (red[0] + red[1]) + (red[2] + red[3]); }
 }
 void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, int64_t v) {
   if (rows <= 0) return;
@@ -677,9 +911,13 @@ __global__ void k_record_loss(const float* __restrict__ loss, float* __restrict_
 }
 void prepare() {
   // Kernels whose dynamic LDS may exceed the 64 KiB default; set once, outside any capture.
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_sort_ids),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-  if (e != hipSuccess) throw std::runtime_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+  const void* sorts[] = {reinterpret_cast<const void*>(k_sort_ids<1>), reinterpret_cast<const void*>(k_sort_ids<2>),
+                         reinterpret_cast<const void*>(k_sort_ids<4>), reinterpret_cast<const void*>(k_sort_ids<8>),
+                         reinterpret_cast<const void*>(k_sort_ids<16>)};
+  for (const void* k : sorts) {
+    hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) throw std::runtime_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+  }
   prepare_attention();
 }
 

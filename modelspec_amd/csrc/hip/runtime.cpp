@@ -338,9 +338,9 @@ void Executor::build() {
         g.m = M; g.n = N; g.k = K; g.ldc = N;
         g.ta = ra.flip; g.lda = ra.flip ? M : K;
         g.tb = rb.flip; g.ldb = rb.flip ? K : N;
-        int split = hk::gemm_split_for(M, N, K);
-        void* ws = split > 1 ? R(size_t(split) * size_t(M * N) * 4) : nullptr;
-        g.workspace_floats = split > 1 ? int64_t(split) * M * N : 0;
+        int64_t wsf = hk::gemm_workspace(M, N, K);
+        void* ws = wsf > 0 ? R(size_t(wsf) * 4) : nullptr;
+        g.workspace_floats = wsf;
         uint32_t asrc = ra.src, bsrc = rb.src;
         int64_t bias_id = fused ? int64_t(o[1]) : -1;
         push([=](hipStream_t s) {
@@ -405,7 +405,7 @@ void Executor::build() {
       case Op::SumRows: {
         uint32_t a = o[0];
         int64_t rows = shape(a)[0], h = shape(a)[1];
-        int64_t pf = hk::column_chunks(rows, h) * h;
+        int64_t pf = hk::column_workspace(rows, h);
         void* part = R(size_t(pf) * 4);
         push([=](hipStream_t s) { hk::column_sum(s, F(a), F(id), rows, h, static_cast<float*>(A(part)), pf); });
         break;
@@ -430,7 +430,7 @@ void Executor::build() {
           push([=](hipStream_t s) { hk::ln_grad_x(s, F(xv), F(gm), F(g), static_cast<float*>(A(stats)), F(id), rows, h); });
         } else {
           uint32_t g = o[1];
-          int64_t pf = hk::column_chunks(rows, h) * h;
+          int64_t pf = hk::column_workspace(rows, h);
           void* part = R(size_t(pf) * 4);
           push([=](hipStream_t s) {
             hk::ln_grad_gamma(s, F(xv), F(g), static_cast<float*>(A(stats)), F(id), rows, h, static_cast<float*>(A(part)), pf);

@@ -29,7 +29,7 @@ def key_biases(step_ir):
     for vid, (op, _, body) in nodes.items():
         if op != "ParamRead":
             continue
-        path = body.split("@")[1]
+        path = body.split("@")[1].split()[0]
         rs = readers(vid)
         fwd = [r for r in rs if r[1] == "AddRows" and r[2] == 1]
         if fwd and any(n[1] == "Attention" and n[2] == 1 for n in readers(fwd[0][0])):
