@@ -20,19 +20,21 @@ void fill_zero(hipStream_t s, void* o, int64_t bytes);                     // ke
 void copy(hipStream_t s, const float* a, float* o, int64_t n);
 
 // C[M,N] = op(A) op(B) (+ bias[N]); A is [M,K] row-major with leading dimension lda, or [K,M]
-// (read transposed) when ta; B is [K,N], or [N,K] when tb. When `pre` is non-null the kernel writes
-// the biased value there too and `out` gets GELU of it (act = 1) or ReLU (act = 2).
-// `workspace` (split_k * M * N floats) takes split-K partials, summed in slice order.
+// (read transposed) when ta; B is [K,N], or [N,K] when tb.
+// `workspace` (gemm_workspace floats) takes split-K partials, summed in slice order. When
+// `colsum` is non-null it receives the N column sums of op(B) over K as well (a bias gradient
+// beside its weight gradient).
 struct GemmArgs {
   const float* a; const float* b; float* c; const float* bias;
   int64_t m, n, k, lda, ldb, ldc;
   bool ta, tb;
   float* workspace; int64_t workspace_floats;
+  float* colsum;
 };
 int gemm_split_for(int64_t m, int64_t n, int64_t k);  // the split-K factor the launcher uses
-// Floats of workspace a gemm of this shape needs (0 without split-K): the slices' partial tiles
-// and one counter per output tile, zero before the first launch and left zero by every launch.
-int64_t gemm_workspace(int64_t m, int64_t n, int64_t k);
+// Floats of workspace a gemm of this shape needs (0 without split-K): the slices' partial tiles,
+// then the slices' column sums when asked for.
+int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum = false);
 void gemm(hipStream_t s, const GemmArgs& g);
 
 void transpose(hipStream_t s, const float* a, float* o, int64_t rows, int64_t cols);  // a [rows,cols] -> o [cols,rows]
@@ -53,12 +55,26 @@ void layer_norm(hipStream_t s, const float* x, const float* gamma, const float* 
                 int64_t rows, int64_t h);
 void ln_grad_x(hipStream_t s, const float* x, const float* gamma, const float* g, const float* stats, float* dx,
                int64_t rows, int64_t h);
+// LayerNorm backward in one pass: dx when non-null, and when `partial` is non-null the per-block
+// partial sums [ln_backward_blocks, 2 h] of g * xhat (gamma gradient) then g (beta gradient), to be
+// added by column_finalize. gamma may be null when dx is.
+int64_t ln_backward_blocks(int64_t rows, int64_t h);
+void ln_backward(hipStream_t s, const float* x, const float* gamma, const float* g, const float* stats, float* dx,
+                 float* partial, int64_t rows, int64_t h);
+
+// Sums of block partials [chunks, width] over the blocks, columns below `split` to out_lo and the
+// rest to out_hi; up to kColumnJobs reductions a launch (`first` is set by column_finalize).
+struct ColumnJob { const float* partial; float* out_lo; float* out_hi; int32_t chunks, width, split, first; };
+constexpr int kColumnJobs = 16;
+struct ColumnJobs { ColumnJob job[kColumnJobs]; int32_t count; };
+void column_finalize(hipStream_t s, const ColumnJob* jobs, int count);
 
 void embedding(hipStream_t s, const float* table, const int32_t* ids, float* o, int64_t n, int64_t rows, int64_t h);
-// Deterministic sorted-segment scatter: out = 0; out[ids[k]] += g[k] in ascending k.
-// keys: n 64-bit scratch words.
+// Deterministic sorted-segment scatter: out = 0; out[ids[k]] += g[k] in ascending k. `work` holds
+// embedding_grad_workspace(n, rows) bytes of scratch (16-byte aligned).
+int64_t embedding_grad_workspace(int64_t n, int64_t rows);
 void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* out, int64_t n, int64_t rows,
-                    int64_t h, uint64_t* keys);
+                    int64_t h, void* work, int64_t work_bytes);
 
 void dropout(hipStream_t s, const float* x, float* o, int64_t n, const int32_t* token, uint64_t seed,
              uint64_t threshold, float scale);

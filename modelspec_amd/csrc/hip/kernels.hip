@@ -187,7 +187,7 @@ template <bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                               float* __restrict__ C, const float* __restrict__ bias, int64_t M,
                                               int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-                                              int64_t kchunk, float* __restrict__ ws) {
+                                              int64_t kchunk, float* __restrict__ ws, float* __restrict__ colsum) {
   __shared__ float As[2][BK * LDP];
   __shared__ float Bs[2][BK * LDP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -197,6 +197,10 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   v4f acc00 = {0, 0, 0, 0}, acc01 = acc00, acc10 = acc00, acc11 = acc00;
   float ra[8], rb[8];
+  // Column sums of B (the bias gradient beside a weight gradient), taken from the LDS tiles by the
+  // first row of blocks: thread t adds column t mod 64 over rows 8 (t / 64) .. + 8 of each K tile.
+  const bool sums = colsum != nullptr && blockIdx.y == 0;
+  float csum = 0.0f;
   // B's (k, j) element is B[k * ldb + j], or B[j * ldb + k] when TB: the same loader with the
   // roles of "row" and "contiguous" swapped.
   load_tile<TA, VA>(A, lda, M, kend, m0, kbeg, tid, ra);
@@ -222,7 +226,22 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
       acc10 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc10, 0, 0, 0);
       acc11 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc11, 0, 0, 0);
     }
+    if (sums) {
+      const int c = tid & 63, kg = (tid >> 6) * 8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) csum += bs[(kg + j) * LDP + c];
+    }
     buf ^= 1;
+  }
+  if (sums) {
+    __syncthreads();
+    float* red = As[0];
+    red[tid] = csum;
+    __syncthreads();
+    if (tid < 64 && n0 + tid < N) {
+      const float v = ((red[tid] + red[64 + tid]) + red[128 + tid]) + red[192 + tid];
+      colsum[(ws ? int64_t(blockIdx.z) * N : 0) + n0 + tid] = v;
+    }
   }
   const v4f* accs[4] = {&acc00, &acc01, &acc10, &acc11};
   if (!ws) {
@@ -255,10 +274,25 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
 template <int SPLIT>
 __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ ws, float* __restrict__ C,
                                                     const float* __restrict__ bias, int64_t M, int64_t N, int64_t ldc,
-                                                    int tiles_x, int64_t tiles, int splits) {
-  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;  // over tiles * BM * BN
+                                                    int tiles_x, int64_t tiles, int splits, float* __restrict__ colsum) {
+  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;  // over tiles * BM * BN, then N column sums
   const int64_t tile = e / (BM * BN);
-  if (tile >= tiles) return;
+  if (tile >= tiles) {
+    // The slices' column sums follow the partial tiles in the workspace.
+    const int64_t col = e - tiles * (BM * BN);
+    if (!colsum || col >= N) return;
+    const float* cs = ws + int64_t(splits) * tiles * (BM * BN) + col;
+    float t[SPLIT];
+#pragma unroll
+    for (int z = 0; z < SPLIT; ++z) t[z] = z < splits ? cs[z * N] : 0.0f;
+    float s = t[0];
+#pragma unroll
+    for (int z = 1; z < SPLIT; ++z)
+      if (z < splits) s += t[z];
+    for (int z = SPLIT; z < splits; ++z) s += cs[z * N];
+    colsum[col] = s;
+    return;
+  }
   const int in = int(e % (BM * BN));
   const int64_t row = int64_t(tile / tiles_x) * BM + in / BN, col = int64_t(tile % tiles_x) * BN + in % BN;
   const int64_t stride = tiles * (BM * BN);
@@ -283,11 +317,11 @@ int gemm_split_for(int64_t m, int64_t n, int64_t k) {
   return int((k + chunk - 1) / chunk);
 }
 
-int64_t gemm_workspace(int64_t m, int64_t n, int64_t k) {
+int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum) {
   int split = gemm_split_for(m, n, k);
   if (split <= 1) return 0;
   int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  return tiles * split * BM * BN;  // the slices' partial tiles
+  return tiles * split * BM * BN + (colsum ? split * n : 0);  // the slices' partial tiles, column sums
 }
 
 void gemm(hipStream_t s, const GemmArgs& g) {
@@ -299,10 +333,12 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   int64_t tiles = ((g.m + BM - 1) / BM) * ((g.n + BN - 1) / BN);
   float* ws = nullptr;
   if (split > 1) {
-    if (!g.workspace || g.workspace_floats < tiles * split * BM * BN) bad("gemm split-K workspace too small");
+    if (!g.workspace || g.workspace_floats < tiles * split * BM * BN + (g.colsum ? split * g.n : 0))
+      bad("gemm split-K workspace too small");
     ws = g.workspace;
   }
   dim3 grid(unsigned((g.n + BN - 1) / BN), unsigned((g.m + BM - 1) / BM), unsigned(split));
+  float* csum = g.colsum ? (ws ? ws + int64_t(split) * tiles * BM * BN : g.colsum) : nullptr;
   if (grid.y > 65535) bad("gemm M too large");
   // float4 loads need a leading dimension and base address that keep every group 16-byte aligned.
   // float4 loads need 16-byte aligned groups and a contiguous extent that is a multiple of 4.
@@ -312,7 +348,7 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   const bool va = aligned(g.a, g.lda, g.ta ? g.m : g.k), vb = aligned(g.b, g.ldb, g.tb ? g.k : g.n);
 #define MSX_GEMM(TA, TB, VA, VB)                                                                                 \
   hipLaunchKernelGGL((k_gemm<TA, TB, VA, VB>), grid, dim3(256), 0, s, g.a, g.b, g.c, g.bias, g.m, g.n, g.k, g.lda, \
-                     g.ldb, g.ldc, chunk, ws)
+                     g.ldb, g.ldc, chunk, ws, csum)
 #define MSX_GEMM_V(TA, TB)                  \
   if (va && vb) MSX_GEMM(TA, TB, true, true);        \
   else if (va) MSX_GEMM(TA, TB, true, false);        \
@@ -325,14 +361,17 @@ void gemm(hipStream_t s, const GemmArgs& g) {
 #undef MSX_GEMM_V
 #undef MSX_GEMM
   if (split > 1) {
-    unsigned blocks = unsigned((tiles * BM * BN + 255) / 256);
+    unsigned blocks = unsigned((tiles * BM * BN + (g.colsum ? g.n : 0) + 255) / 256);
     int tx = int((g.n + BN - 1) / BN);
     if (split <= 8)
-      hipLaunchKernelGGL(k_splitk_sum<8>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, tx, tiles, split);
+      hipLaunchKernelGGL(k_splitk_sum<8>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, tx, tiles, split,
+                         g.colsum);
     else if (split <= 16)
-      hipLaunchKernelGGL(k_splitk_sum<16>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, tx, tiles, split);
+      hipLaunchKernelGGL(k_splitk_sum<16>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, tx, tiles, split,
+                         g.colsum);
     else
-      hipLaunchKernelGGL(k_splitk_sum<32>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, tx, tiles, split);
+      hipLaunchKernelGGL(k_splitk_sum<32>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, tx, tiles, split,
+                         g.colsum);
   }
 }
 
@@ -525,6 +564,136 @@ void ln_grad_x(hipStream_t s, const float* x, const float* gamma, const float* g
   hipLaunchKernelGGL(k_ln_grad_x, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, gamma, g, stats, dx, rows, h);
 }
 
+// The LayerNorm backward of one input in one pass: dx (LayerNormGradX) and, per block of rows, the
+// partial column sums of g * xhat (LayerNormGradGamma) and of g (the beta gradient, SumRows), to
+// partial[block] = [gamma sums (h), beta sums (h)]; column_finalize adds the blocks' partials. A
+// wave takes a row at a time, lane l holding columns l + 64 j.
+template <int CPL>
+__global__ __launch_bounds__(256) void k_ln_backward(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                     const float* __restrict__ g, const float* __restrict__ stats,
+                                                     float* __restrict__ dx, float* __restrict__ partial, int64_t rows,
+                                                     int64_t h, int64_t rows_per) {
+  extern __shared__ float red[];  // [4 waves][2 h]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r0 = int64_t(blockIdx.x) * rows_per, r1 = std::min<int64_t>(rows, r0 + rows_per);
+  float gm[CPL], pg[CPL], pb[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int64_t c = lane + 64 * j;
+    gm[j] = c < h && gamma ? gamma[c] : 0.0f;
+    pg[j] = 0.0f;
+    pb[j] = 0.0f;
+  }
+  const float width = float(h);
+  for (int64_t row = r0 + wave; row < r1; row += 4) {
+    const float mean = stats[2 * row], rstd = stats[2 * row + 1];
+    float xv[CPL], gv[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int64_t c = lane + 64 * j;
+      xv[j] = c < h ? x[row * h + c] : 0.0f;
+      gv[j] = c < h ? g[row * h + c] : 0.0f;
+    }
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const float xhat = (xv[j] - mean) * rstd;
+      const float gx = gv[j] * gm[j];
+      s1 += gx;
+      s2 = __builtin_fmaf(gx, xhat, s2);
+      pg[j] += gv[j] * xhat;
+      pb[j] += gv[j];
+    }
+    if (dx) {
+      const float mean_gx = wave_sum(s1) / width, mean_gx_xhat = wave_sum(s2) / width;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int64_t c = lane + 64 * j;
+        const float xhat = (xv[j] - mean) * rstd;
+        const float gx = gv[j] * gm[j];
+        if (c < h) dx[row * h + c] = rstd * ((gx - mean_gx) - xhat * mean_gx_xhat);
+      }
+    }
+  }
+  if (!partial) return;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int64_t c = lane + 64 * j;
+    if (c < h) {
+      red[wave * 2 * h + c] = pg[j];
+      red[wave * 2 * h + h + c] = pb[j];
+    }
+  }
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < 2 * h; c += 256)
+    partial[int64_t(blockIdx.x) * 2 * h + c] = ((red[c] + red[2 * h + c]) + red[4 * h + c]) + red[6 * h + c];
+}
+
+int64_t ln_backward_blocks(int64_t rows, int64_t h) {
+  (void)h;
+  return std::max<int64_t>(1, std::min<int64_t>((rows + 15) / 16, 256));
+}
+void ln_backward(hipStream_t s, const float* x, const float* gamma, const float* g, const float* stats, float* dx,
+                 float* partial, int64_t rows, int64_t h) {
+  if (rows <= 0 || h <= 0) return;
+  if (h > 1024) bad("LayerNorm backward rows wider than 1024");
+  const int64_t blocks = ln_backward_blocks(rows, h);
+  const int64_t per = (rows + blocks - 1) / blocks;
+  const size_t lds = size_t(8 * h) * 4;
+  const int cpl = int((h + 63) / 64);
+#define MSX_LNB(C) hipLaunchKernelGGL(k_ln_backward<C>, dim3(unsigned(blocks)), dim3(256), lds, s, x, gamma, g, stats, dx, \
+                                      partial, rows, h, per)
+  if (cpl <= 1) MSX_LNB(1);
+  else if (cpl <= 2) MSX_LNB(2);
+  else if (cpl <= 4) MSX_LNB(4);
+  else if (cpl <= 8) MSX_LNB(8);
+  else MSX_LNB(16);
+#undef MSX_LNB
+}
+
+// Column sums of block partials for several reductions in one launch: job j owns blocks
+// [first, first + ceil(width / 256)); a thread adds one column's partials in ascending block order,
+// 16 loads in flight, and writes it to out_lo[c] (c < split) or out_hi[c - split] (a null output
+// is skipped).
+__global__ __launch_bounds__(256) void k_column_finalize(ColumnJobs jobs) {
+  int j = 0;
+  while (j + 1 < jobs.count && int(blockIdx.x) >= jobs.job[j + 1].first) ++j;
+  const ColumnJob& J = jobs.job[j];
+  const int64_t c = int64_t(int(blockIdx.x) - J.first) * 256 + threadIdx.x;
+  if (c >= J.width) return;
+  float s = 0.0f;
+  for (int z0 = 0; z0 < J.chunks; z0 += 16) {
+    float t[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int z = z0 + u < J.chunks ? z0 + u : J.chunks - 1;
+      t[u] = J.partial[int64_t(z) * J.width + c];
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (z0 + u < J.chunks) s += t[u];
+  }
+  if (c < J.split) {
+    if (J.out_lo) J.out_lo[c] = s;
+  } else if (J.out_hi) {
+    J.out_hi[c - J.split] = s;
+  }
+}
+void column_finalize(hipStream_t s, const ColumnJob* jobs, int count) {
+  for (int base = 0; base < count; base += kColumnJobs) {
+    ColumnJobs b{};
+    int blocks = 0;
+    b.count = std::min(kColumnJobs, count - base);
+    for (int j = 0; j < b.count; ++j) {
+      b.job[j] = jobs[base + j];
+      if (b.job[j].chunks <= 0 || b.job[j].width <= 0) bad("column finalize job without partials");
+      b.job[j].first = blocks;
+      blocks += int((b.job[j].width + 255) / 256);
+    }
+    hipLaunchKernelGGL(k_column_finalize, dim3(unsigned(blocks)), dim3(256), 0, s, b);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 __global__ void k_embedding(const float* __restrict__ table, const int32_t* __restrict__ ids, float* __restrict__ o,
                             int64_t n, int64_t rows, int64_t h) {
@@ -658,11 +827,195 @@ __global__ __launch_bounds__(256) void k_segment_sum(const uint64_t* __restrict_
   }
 }
 
+// The counting plan of EmbeddingGrad for tables of at most kPlanRows rows, one block of 1024
+// threads with a per-row counter in LDS: counts per id, one exclusive scan that yields each id's
+// start in `order` and its segment index, the segment list (id, start, count) in ascending id, a
+// presence bitmap of the table's rows, and the positions k grouped by id, ascending in each group. A counter word packs the start (low 16 bits) and the
+// segment index (high 16 bits); n < 2^16 keeps them apart.
+constexpr int64_t kPlanRows = 32768;
+__global__ __launch_bounds__(1024) void k_embed_plan(const int32_t* __restrict__ ids, int64_t n, int64_t rows,
+                                                     int32_t* __restrict__ order, int32_t* __restrict__ segs,
+                                                     int32_t* __restrict__ nseg, uint32_t* __restrict__ present) {
+  extern __shared__ uint32_t cnt[];
+  __shared__ uint32_t wave_tot[16];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  for (int64_t r = t; r < rows; r += 1024) cnt[r] = 0;
+  __syncthreads();
+  for (int64_t k = t; k < n; k += 1024) {
+    const uint32_t id = uint32_t(ids[k]);
+    if (id < uint64_t(rows)) atomicAdd(&cnt[id], 1u);
+  }
+  __syncthreads();
+  // Thread t owns rows [t per, (t + 1) per); a row's packed value is count | (count > 0) << 16.
+  const int64_t per = (rows + 1023) / 1024;
+  const int64_t r0 = std::min<int64_t>(rows, t * per), r1 = std::min<int64_t>(rows, r0 + per);
+  uint32_t local = 0;
+  for (int64_t r = r0; r < r1; ++r) {
+    const uint32_t c = cnt[r];
+    local += c | (c ? 0x10000u : 0u);
+  }
+  uint32_t incl = local;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  uint32_t run = incl - local;
+  for (int w = 0; w < wave; ++w) run += wave_tot[w];
+  if (t == 1023) *nseg = int32_t((run + local) >> 16);
+  for (int64_t r = r0; r < r1; ++r) {
+    const uint32_t c = cnt[r];
+    cnt[r] = run;
+    if (c) {
+      const uint32_t sidx = run >> 16;
+      segs[3 * sidx] = int32_t(r);
+      segs[3 * sidx + 1] = int32_t(run & 0xFFFFu);
+      segs[3 * sidx + 2] = int32_t(c);
+      run += c | 0x10000u;
+    }
+  }
+  __syncthreads();
+  // Row r is present when the segment index steps between r and r + 1.
+  const uint32_t total_seg = (wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3] + wave_tot[4] + wave_tot[5] +
+                              wave_tot[6] + wave_tot[7] + wave_tot[8] + wave_tot[9] + wave_tot[10] + wave_tot[11] +
+                              wave_tot[12] + wave_tot[13] + wave_tot[14] + wave_tot[15]) >> 16;
+  for (int64_t w = t; w < (rows + 31) / 32; w += 1024) {
+    uint32_t bits = 0;
+    for (int b = 0; b < 32; ++b) {
+      const int64_t r = w * 32 + b;
+      if (r >= rows) break;
+      const uint32_t here = cnt[r] >> 16, next = r + 1 < rows ? cnt[r + 1] >> 16 : total_seg;
+      bits |= (next != here ? 1u : 0u) << b;
+    }
+    present[w] = bits;
+  }
+  __syncthreads();
+  // Stable placement, 1024 positions a round. In a wave, a lane's rank among the lanes before it
+  // with the same id comes from a scan of the wave's ids; the first such lane (the leader) then
+  // takes the id's cursor forward by the wave's count, the 16 waves one after another, so the
+  // positions of an id land in ascending k.
+  for (int64_t base = 0; base < n; base += 1024) {
+    const int64_t k = base + t;
+    const uint32_t id = k < n ? uint32_t(ids[k]) : 0xFFFFFFFFu;
+    const bool valid = id < uint64_t(rows);
+    int rank = 0, count = 0, leader = 64;
+    for (int j = 0; j < 64; ++j) {
+      const uint32_t other = __shfl(id, j, 64);
+      const bool same = other == id;
+      rank += (same && j < lane) ? 1 : 0;
+      count += same ? 1 : 0;
+      leader = (same && leader == 64) ? j : leader;
+    }
+    uint32_t cursor = 0;
+    for (int w = 0; w < 16; ++w) {
+      if (wave == w && valid && leader == lane) cursor = atomicAdd(&cnt[id], uint32_t(count));
+      __syncthreads();
+    }
+    cursor = __shfl(cursor, leader & 63, 64);
+    if (valid) order[(cursor & 0xFFFFu) + uint32_t(rank)] = int32_t(k);
+  }
+}
+
+// Block b zeroes the absent rows of its stripe of the table, then, when b is below the segment
+// count, sums segment b: the rows g[k] of its positions are added in ascending k from +0, one f32
+// rounding per add: the reference's order (interpreter.rs:931-941), bit for bit. Rows come in
+// chunks of `ch` through LDS, all of a chunk's loads in flight together.
+constexpr int kSumThreads = 256;
+__global__ __launch_bounds__(kSumThreads) void k_embed_sum(const float* __restrict__ g, const int32_t* __restrict__ order,
+                                                           const int32_t* __restrict__ segs,
+                                                           const int32_t* __restrict__ nseg,
+                                                           const uint32_t* __restrict__ present, float* __restrict__ out,
+                                                           int64_t rows, int64_t h, int64_t stripe, int ch, bool vec) {
+  extern __shared__ float lds[];
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  {
+    const int64_t z0 = b * stripe, z1 = std::min<int64_t>(rows, z0 + stripe);
+    for (int64_t r = z0; r < z1; ++r) {
+      if ((present[r >> 5] >> (r & 31)) & 1u) continue;
+      for (int64_t c = tid; c < h; c += kSumThreads) out[r * h + c] = 0.0f;
+    }
+  }
+  if (b >= *nseg) return;
+  const int32_t id = segs[3 * b], start = segs[3 * b + 1], c = segs[3 * b + 2];
+  const int32_t* ks = order + start;  // the segment's positions, ascending
+  float* stage = lds;
+  // Thread tid adds columns tid, tid + 256, tid + 512, tid + 768 (h <= 1024).
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int q0 = 0; q0 < c; q0 += ch) {
+    const int cnt = c - q0 < ch ? c - q0 : ch;
+    __syncthreads();
+    if (vec) {
+      // Up to 8 float4 a thread, every load issued before the first LDS store; the tail reads a
+      // clamped in-range element and skips the store.
+      const int h4 = int(h >> 2), tot = cnt * h4;
+      float4 tmp[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        int e = tid + u * kSumThreads;
+        e = e < tot ? e : tot - 1;
+        const int r = e / h4;
+        tmp[u] = reinterpret_cast<const float4*>(g + int64_t(ks[q0 + r]) * h)[e - r * h4];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = tid + u * kSumThreads;
+        if (e < tot) reinterpret_cast<float4*>(stage)[e] = tmp[u];
+      }
+    } else {
+      for (int64_t e = tid; e < int64_t(cnt) * h; e += kSumThreads) {
+        const int r = int(e / h);
+        stage[e] = g[int64_t(ks[q0 + r]) * h + (e - int64_t(r) * h)];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t col = tid + int64_t(kSumThreads) * u;
+      if (col < h)
+        for (int r = 0; r < cnt; ++r) acc[u] = acc[u] + stage[int64_t(r) * h + col];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t col = tid + int64_t(kSumThreads) * u;
+    if (col < h) out[int64_t(id) * h + col] = acc[u];
+  }
+}
+
+int64_t embedding_grad_workspace(int64_t n, int64_t rows) {
+  // The counting plan: order [n], segments [3 n], the segment count, the presence bitmap; the
+  // sort fallback: n 64-bit keys.
+  const int64_t plan = 4 * (4 * n + 1) + 4 * ((rows + 31) / 32) + 16;
+  return std::max<int64_t>(plan, 8 * n) + 256;
+}
+
 void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* out, int64_t n, int64_t rows, int64_t h,
-                    uint64_t* keys) {
-  fill_zero(s, out, rows * h * 4);
-  if (n <= 0) return;
+                    void* work, int64_t work_bytes) {
   if (n > 16384) bad("embedding gradient over more than 16384 ids");
+  if (h > 1024) bad("embedding gradient rows wider than 1024");
+  if (work_bytes < embedding_grad_workspace(n, rows)) bad("embedding gradient workspace too small");
+  if (n <= 0 || rows <= 0 || h <= 0) { fill_zero(s, out, rows * h * 4); return; }
+  if (rows <= kPlanRows) {
+    int32_t* order = static_cast<int32_t*>(work);
+    int32_t* segs = order + n;
+    int32_t* nseg = segs + 3 * n;
+    uint32_t* present = reinterpret_cast<uint32_t*>(nseg + 1);
+    hipLaunchKernelGGL(k_embed_plan, dim3(1), dim3(1024), size_t(rows) * 4, s, ids, n, rows, order, segs, nseg, present);
+    const int64_t blocks = std::max<int64_t>(n, 1024);
+    const int64_t stripe = (rows + blocks - 1) / blocks;
+    const bool vec = h % 4 == 0 && reinterpret_cast<uintptr_t>(g) % 16 == 0;
+    const int ch = int(vec ? std::max<int64_t>(1, 2048 / (h / 4)) : std::max<int64_t>(1, std::min<int64_t>(64, 8192 / h)));
+    hipLaunchKernelGGL(k_embed_sum, dim3(unsigned(blocks)), dim3(kSumThreads), size_t(ch) * size_t(h) * 4, s, g, order,
+                       segs, nseg, present, out, rows, h, stripe, ch, vec);
+    return;
+  }
+  // Tables beyond the LDS counters: a bitonic sort of the (id, k) keys, then one block per sorted
+  // position.
+  uint64_t* keys = static_cast<uint64_t*>(work);
+  fill_zero(s, out, rows * h * 4);
   int64_t pow2 = 1024;
   while (pow2 < n) pow2 <<= 1;
   size_t lds = size_t(pow2) * 8;
@@ -673,7 +1026,6 @@ void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* ou
     case 8: hipLaunchKernelGGL(k_sort_ids<8>, dim3(1), dim3(1024), lds, s, ids, keys, n); break;
     default: hipLaunchKernelGGL(k_sort_ids<16>, dim3(1), dim3(1024), lds, s, ids, keys, n); break;
   }
-  if (h > 1024) bad("embedding gradient rows wider than 1024");
   const int chunk = int(std::max<int64_t>(1, std::min<int64_t>(64, 16384 / h)));
   hipLaunchKernelGGL(k_segment_sum, dim3(unsigned(n)), dim3(256), size_t(chunk) * size_t(h) * 4, s, keys, g, out, n,
                      rows, h, chunk);
@@ -914,6 +1266,9 @@ void prepare() {
   const void* sorts[] = {reinterpret_cast<const void*>(k_sort_ids<1>), reinterpret_cast<const void*>(k_sort_ids<2>),
                          reinterpret_cast<const void*>(k_sort_ids<4>), reinterpret_cast<const void*>(k_sort_ids<8>),
                          reinterpret_cast<const void*>(k_sort_ids<16>)};
+  const void* plan = reinterpret_cast<const void*>(k_embed_plan);
+  hipError_t pe = hipFuncSetAttribute(plan, hipFuncAttributeMaxDynamicSharedMemorySize, int(kPlanRows * 4));
+  if (pe != hipSuccess) throw std::runtime_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(pe));
   for (const void* k : sorts) {
     hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) throw std::runtime_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));

@@ -181,6 +181,67 @@ void Executor::build() {
       if (c.op == Op::AddRows && c.operands[0] == x.id && c.operands[1] != x.id) mm_fused.insert(x.id);
     }
   }
+  // A SumRows of a MatMul's un-transposed B operand (the bias gradient beside its weight gradient)
+  // is taken by that GEMM from its LDS tiles, when no reader of the sum comes before the GEMM.
+  std::map<uint32_t, uint32_t> colsum_of;  // MatMul -> SumRows
+  std::set<uint32_t> colsum_fused;
+  for (size_t k = 0; k < n; ++k) {
+    if (!need[k] || p.nodes[k].op != Op::SumRows) continue;
+    const uint32_t a = p.nodes[k].operands[0];
+    for (auto c : consumers[p.pos.at(a)]) {
+      const Node& m = p.nodes[c];
+      if (m.op != Op::MatMul || mm_fused.count(m.id) || colsum_of.count(m.id)) continue;
+      Resolved rb = resolve(p, m.operands[1]);
+      if (rb.src != a || rb.flip) continue;
+      bool late = true;
+      for (auto r2 : consumers[k]) late = late && r2 > c;
+      if (!late) continue;
+      colsum_of[m.id] = p.nodes[k].id;
+      colsum_fused.insert(p.nodes[k].id);
+      break;
+    }
+  }
+  // The LayerNorm gradients of one (input, output gradient) pair run as one pass: dx, and block
+  // partials of the gamma and beta sums, finished by a batched column reduction, deferred to the
+  // end of the step when only the optimizer reads them. The pass runs at its first member.
+  struct LnGroup { int64_t dx = -1, gamma = -1, beta = -1, gm = -1; size_t first = SIZE_MAX; };
+  std::map<std::pair<uint32_t, uint32_t>, LnGroup> ln_groups;
+  for (size_t k = 0; k < n; ++k) {
+    if (!need[k]) continue;
+    const Node& x = p.nodes[k];
+    if (x.op == Op::LayerNormGradX) {
+      auto& gr = ln_groups[{x.operands[0], x.operands[2]}];
+      gr.dx = x.id;
+      gr.gm = x.operands[1];
+      gr.first = std::min(gr.first, k);
+    } else if (x.op == Op::LayerNormGradGamma) {
+      auto& gr = ln_groups[{x.operands[0], x.operands[1]}];
+      gr.gamma = x.id;
+      gr.first = std::min(gr.first, k);
+    }
+  }
+  std::map<uint32_t, std::pair<uint32_t, uint32_t>> ln_member;  // member -> group key
+  for (auto& [key, gr] : ln_groups) {
+    for (auto v : {gr.dx, gr.gamma})
+      if (v >= 0) ln_member[uint32_t(v)] = key;
+  }
+  for (size_t k = 0; k < n; ++k) {
+    if (!need[k] || p.nodes[k].op != Op::SumRows || colsum_fused.count(p.nodes[k].id)) continue;
+    for (auto& [key, gr] : ln_groups) {
+      if (key.second != p.nodes[k].operands[0] || gr.beta >= 0) continue;
+      gr.beta = p.nodes[k].id;
+      gr.first = std::min(gr.first, k);
+      ln_member[p.nodes[k].id] = key;
+      break;
+    }
+  }
+  auto only_optimizer_reads = [&](int64_t v) {
+    if (v < 0) return true;
+    if (outputs.count(uint32_t(v))) return false;
+    for (auto c : consumers[p.pos.at(uint32_t(v))])
+      if (!optimizer.count(p.nodes[c].id)) return false;
+    return true;
+  };
   // Attention gradients over the same operands run as one launch.
   std::map<std::vector<uint32_t>, std::array<int64_t, 3>> attn_groups;
   for (size_t k = 0; k < n; ++k) {
@@ -253,6 +314,8 @@ void Executor::build() {
   std::map<uint32_t, void*> ce_stats_tok;             // logits value -> stats [rows, 2]
   std::map<std::pair<uint32_t, uint32_t>, void*> ce_den_tok;  // (logits, weights) -> den
   std::map<std::vector<uint32_t>, std::pair<uint32_t, void*>> attn_fwd;  // operands -> (output, stats)
+  struct DeferredColumns { void* partial; int64_t gamma, beta; int32_t chunks, h; };
+  std::vector<DeferredColumns> deferred;
   auto R = [&](size_t bytes) { return arena_.reserve(bytes); };
   auto A = [this](void* tok) { return arena_.at(tok); };
   auto P = [this](uint32_t id) { return ptr(id); };
@@ -273,6 +336,7 @@ void Executor::build() {
       const Node& m = p.node(x.op == Op::MatMul ? id : o[0]);
       what += " k=" + std::to_string(shape(m.operands[0])[1]);
       if (x.op == Op::AddRows) what = "MatMul+AddRows" + what.substr(7);
+      if (x.op == Op::MatMul && colsum_of.count(id)) what += " +SumRows %" + std::to_string(colsum_of.at(id));
     }
     auto push = [&](std::function<void(hipStream_t)> f) { pending.push_back({[what, f] { return Launch{what, f}; }}); };
     const size_t first_pending = pending.size();
@@ -338,7 +402,8 @@ void Executor::build() {
         g.m = M; g.n = N; g.k = K; g.ldc = N;
         g.ta = ra.flip; g.lda = ra.flip ? M : K;
         g.tb = rb.flip; g.ldb = rb.flip ? K : N;
-        int64_t wsf = hk::gemm_workspace(M, N, K);
+        const int64_t cs_id = x.op == Op::MatMul && colsum_of.count(id) ? int64_t(colsum_of.at(id)) : -1;
+        int64_t wsf = hk::gemm_workspace(M, N, K, cs_id >= 0);
         void* ws = wsf > 0 ? R(size_t(wsf) * 4) : nullptr;
         g.workspace_floats = wsf;
         uint32_t asrc = ra.src, bsrc = rb.src;
@@ -350,6 +415,7 @@ void Executor::build() {
           a.c = F(id);
           a.bias = bias_id >= 0 ? F(uint32_t(bias_id)) : nullptr;
           a.workspace = ws ? static_cast<float*>(A(ws)) : nullptr;
+          a.colsum = cs_id >= 0 ? F(uint32_t(cs_id)) : nullptr;
           hk::gemm(s, a);
         });
         break;
@@ -398,11 +464,14 @@ void Executor::build() {
           auto it = id_bounds_.find(p.node(ids).name);
           id_bounds_[p.node(ids).name] = it == id_bounds_.end() ? rows : std::min(it->second, rows);
         }
-        void* keys = R(size_t(std::max<int64_t>(nn, 1)) * 8);
-        push([=](hipStream_t s) { hk::embedding_grad(s, I(ids), F(g), F(id), nn, rows, h, static_cast<uint64_t*>(A(keys))); });
+        const int64_t wb = hk::embedding_grad_workspace(nn, rows);
+        void* work = R(size_t(wb));
+        push([=](hipStream_t s) { hk::embedding_grad(s, I(ids), F(g), F(id), nn, rows, h, A(work), wb); });
         break;
       }
       case Op::SumRows: {
+        if (colsum_fused.count(id)) break;  // taken by its GEMM
+        if (ln_member.count(id)) goto layer_norm_backward;
         uint32_t a = o[0];
         int64_t rows = shape(a)[0], h = shape(a)[1];
         int64_t pf = hk::column_workspace(rows, h);
@@ -411,6 +480,7 @@ void Executor::build() {
         break;
       }
       case Op::LayerNorm: case Op::LayerNormGradX: case Op::LayerNormGradGamma: {
+        if (x.op != Op::LayerNorm) goto layer_norm_backward;
         uint32_t xv = o[0];
         int64_t rows = shape(xv)[0], h = shape(xv)[1];
         bool have = ln_stats_tok.count(xv) != 0;
@@ -424,17 +494,45 @@ void Executor::build() {
           });
           break;
         }
-        if (!have) push([=](hipStream_t s) { hk::ln_stats(s, F(xv), static_cast<float*>(A(stats)), rows, h); });
-        if (x.op == Op::LayerNormGradX) {
-          uint32_t gm = o[1], g = o[2];
-          push([=](hipStream_t s) { hk::ln_grad_x(s, F(xv), F(gm), F(g), static_cast<float*>(A(stats)), F(id), rows, h); });
-        } else {
-          uint32_t g = o[1];
-          int64_t pf = hk::column_workspace(rows, h);
-          void* part = R(size_t(pf) * 4);
-          push([=](hipStream_t s) {
-            hk::ln_grad_gamma(s, F(xv), F(g), static_cast<float*>(A(stats)), F(id), rows, h, static_cast<float*>(A(part)), pf);
-          });
+        goto layer_norm_backward;
+      }
+      layer_norm_backward: {
+        const auto key = ln_member.at(id);
+        const LnGroup gr = ln_groups.at(key);
+        if (gr.first != k) break;  // launched with the group's first member
+        const uint32_t xv = key.first, g = key.second;
+        const int64_t rows = shape(xv)[0], h = shape(xv)[1];
+        if (!ln_stats_tok.count(xv)) {
+          void* st2 = ln_stats_tok[xv] = R(size_t(rows) * 8);
+          push([=](hipStream_t s) { hk::ln_stats(s, F(xv), static_cast<float*>(A(st2)), rows, h); });
+        }
+        void* stats = ln_stats_tok.at(xv);
+        const bool sums = gr.gamma >= 0 || gr.beta >= 0;
+        const int64_t chunks = hk::ln_backward_blocks(rows, h);
+        void* part = sums ? R(size_t(chunks * 2 * h) * 4) : nullptr;
+        const int64_t dxv = gr.dx, gmv = gr.gm;
+        what = "LayerNormBackward";
+        for (auto [tag, v] : {std::pair<const char*, int64_t>{" dx %", gr.dx}, {" gamma %", gr.gamma}, {" beta %", gr.beta}})
+          if (v >= 0) what += tag + std::to_string(v);
+        what += " " + type_string(p.node(xv).ty);
+        push([=](hipStream_t s) {
+          hk::ln_backward(s, F(xv), gmv >= 0 ? F(uint32_t(gmv)) : nullptr, F(g), static_cast<float*>(A(stats)),
+                          dxv >= 0 ? F(uint32_t(dxv)) : nullptr, part ? static_cast<float*>(A(part)) : nullptr, rows, h);
+        });
+        bytes = 4.0 * double(rows * h * (dxv >= 0 ? 3 : 2) + (gmv >= 0 ? h : 0) + (sums ? 2 * h : 0));
+        if (sums) {
+          DeferredColumns d{part, gr.gamma, gr.beta, int32_t(chunks), int32_t(h)};
+          if (only_optimizer_reads(gr.gamma) && only_optimizer_reads(gr.beta)) {
+            deferred.push_back(d);
+          } else {
+            pending.back().bytes = bytes;
+            push([=](hipStream_t s) {
+              hk::ColumnJob j{static_cast<float*>(A(d.partial)), d.gamma >= 0 ? F(uint32_t(d.gamma)) : nullptr,
+                              d.beta >= 0 ? F(uint32_t(d.beta)) : nullptr, d.chunks, 2 * d.h, d.h, 0};
+              hk::column_finalize(s, &j, 1);
+            });
+            bytes = 4.0 * double(chunks * 2 * h + 2 * h);
+          }
         }
         break;
       }
@@ -552,6 +650,24 @@ void Executor::build() {
       pending.back().flop = flop;
       pending.back().bytes = bytes;
     }
+  }
+  // The LayerNorm gamma and beta sums only the optimizer reads, in one launch.
+  if (!deferred.empty()) {
+    std::string what = "ColumnFinalize x" + std::to_string(deferred.size());
+    double bytes = 0;
+    for (auto& d : deferred) bytes += 4.0 * double(int64_t(d.chunks) * 2 * d.h + 2 * d.h);
+    pending.push_back({[this, what, deferred, F, A] {
+                         return Launch{what, [this, deferred, F, A](hipStream_t s) {
+                                         std::vector<hk::ColumnJob> jobs;
+                                         for (auto& d : deferred)
+                                           jobs.push_back({static_cast<float*>(A(d.partial)),
+                                                           d.gamma >= 0 ? F(uint32_t(d.gamma)) : nullptr,
+                                                           d.beta >= 0 ? F(uint32_t(d.beta)) : nullptr, d.chunks,
+                                                           2 * d.h, d.h, 0});
+                                         hk::column_finalize(s, jobs.data(), int(jobs.size()));
+                                       }};
+                       },
+                       0, bytes});
   }
   // The optimizer: gradients not computed in place are copied into the arena, then one launch
   // updates every trained parameter and its moments.

@@ -57,7 +57,21 @@ def test_matmul_with_bias_epilogue_and_sum_rows(ctx, oracle):
     assert within(gs, ws, np.abs(wy.reshape(m, n)).sum(axis=0))[0]
 
 
-@pytest.mark.parametrize("rows,h", [(6, 8), (4096, 128), (832, 128), (33, 200)])
+@pytest.mark.parametrize("rows,m,n", [(7, 5, 3), (4096, 128, 128), (4096, 512, 128), (4096, 128, 512),
+                                      (832, 128, 30522), (300, 33, 70)])
+def test_weight_gradient_gemm_takes_the_bias_gradient(ctx, oracle, rows, m, n):
+    """dW = x^T dy with db = SumRows(dy) read from the same GEMM's tiles (with and without split-K)."""
+    x, dy = fast_values(31, rows * m).reshape(rows, m), fast_values(32, rows * n).reshape(rows, n)
+    p = Prog()
+    xi, di = p.input("x", (rows, m)), p.input("dy", (rows, n))
+    dw = p.op("MatMul", [p.op("Transpose", [xi], (m, rows)), di], (m, n))
+    db = p.op("SumRows", [di], (n,))
+    (gw, gb), (ww, wb) = both(ctx, oracle, p.out(dw, db), {"x": x, "dy": dy}, (0, 1))
+    assert within(gw, ww, (np.abs(x.T).astype(np.float64) @ np.abs(dy)).reshape(-1))[0]
+    assert within(gb, wb, np.abs(dy).astype(np.float64).sum(0))[0]
+
+
+@pytest.mark.parametrize("rows,h", [(6, 8), (4096, 128), (832, 128), (33, 200), (100, 768)])
 def test_layer_norm_family(ctx, oracle, rows, h):
     x = fast_values(6, rows * h).reshape(rows, h)
     gamma, beta = fast_values(7, h, 0.5), fast_values(8, h, 0.5)
@@ -67,13 +81,25 @@ def test_layer_norm_family(ctx, oracle, rows, h):
     y = p.op("LayerNorm", [xi, gi, bi], (rows, h))
     dx = p.op("LayerNormGradX", [xi, gi, Gi], (rows, h))
     dg = p.op("LayerNormGradGamma", [xi, Gi], (h,))
-    got, want = both(ctx, oracle, p.out(y, dx, dg), {"x": x, "g": gamma, "b": beta, "G": G}, (0, 1, 2))
+    db = p.op("SumRows", [Gi], (h,))
+    got, want = both(ctx, oracle, p.out(y, dx, dg, db), {"x": x, "g": gamma, "b": beta, "G": G}, (0, 1, 2, 3))
     # r: the magnitude of each term: |xhat| |gamma| + |beta| for y; sums of |terms| for the grads.
     xhat = np.abs((x - x.mean(1, keepdims=True)) / x.std(1, keepdims=True))
     assert within(got[0], want[0], (xhat * np.abs(gamma) + np.abs(beta) + 1).reshape(-1))[0]
     rx = (np.abs(G) * np.abs(gamma)).sum(1, keepdims=True) / h * (1 + xhat) / x.std(1, keepdims=True)
     assert within(got[1], want[1], (np.abs(want[1].reshape(rows, h)) + rx).reshape(-1))[0]
     assert within(got[2], want[2], (np.abs(G) * xhat).sum(0))[0]
+    assert within(got[3], want[3], np.abs(G).astype(np.float64).sum(0))[0]
+
+
+def test_layer_norm_gamma_gradient_alone(ctx, oracle):
+    rows, h = 512, 128
+    x, G = fast_values(41, rows * h).reshape(rows, h), fast_values(42, rows * h).reshape(rows, h)
+    p = Prog()
+    xi, Gi = p.input("x", (rows, h)), p.input("G", (rows, h))
+    (g,), (w,) = both(ctx, oracle, p.out(p.op("LayerNormGradGamma", [xi, Gi], (h,))), {"x": x, "G": G}, (0,))
+    xhat = np.abs((x - x.mean(1, keepdims=True)) / x.std(1, keepdims=True))
+    assert within(g, w, (np.abs(G) * xhat).sum(0))[0]
 
 
 def test_gelu_relu_elementwise(ctx, oracle):
@@ -140,12 +166,25 @@ def test_cross_entropy_and_gradient_full_head(ctx, oracle):
     assert within(gg, wg, np.abs(wg) + 1.0 / w.sum())[0]
 
 
-def test_embedding_gather_and_sorted_segment_scatter_are_bit_exact(ctx, oracle):
-    rows, h, n = 30522, 128, 4096
+def embedding_ids(kind, rows, n, rng):
+    if kind == "zipf":  # hot rows, as token ids
+        ranks = np.arange(1, rows - 4)
+        prob = ranks ** -1.1
+        return (5 + rng.choice(len(ranks), n, p=prob / prob.sum())).astype(np.int32)
+    if kind == "positions":  # every row n / rows times, as position ids
+        return np.tile(np.arange(rows, dtype=np.int32), n // rows + 1)[:n]
+    if kind == "same":  # one segment holding every position
+        return np.full(n, rows // 2, np.int32)
+    return rng.integers(0, rows, n).astype(np.int32)
+
+
+@pytest.mark.parametrize("kind,rows,h,n", [
+    ("zipf", 30522, 128, 4096), ("positions", 128, 128, 4096), ("same", 50, 64, 3000), ("uniform", 7, 130, 1),
+    ("uniform", 1000, 96, 1500), ("zipf", 40000, 128, 2048), ("uniform", 32768, 8, 16384),
+])
+def test_embedding_gather_and_sorted_segment_scatter_are_bit_exact(ctx, oracle, kind, rows, h, n):
     rng = np.random.default_rng(3)
-    ranks = np.arange(1, rows - 4)
-    prob = ranks ** -1.1
-    ids = (5 + rng.choice(len(ranks), n, p=prob / prob.sum())).astype(np.int32)  # Zipf: hot rows
+    ids = embedding_ids(kind, rows, n, rng)
     table = fast_values(17, rows * h).reshape(rows, h)
     G = fast_values(18, n * h).reshape(n, h)
     p = Prog()
