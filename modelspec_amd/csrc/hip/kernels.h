@@ -22,19 +22,24 @@ void copy(hipStream_t s, const float* a, float* o, int64_t n);
 // C[M,N] = op(A) op(B) (+ bias[N]); A is [M,K] row-major with leading dimension lda, or [K,M]
 // (read transposed) when ta; B is [K,N], or [N,K] when tb.
 // `workspace` (gemm_workspace floats) takes split-K partials, summed in slice order. When
-// `colsum` is non-null it receives the N column sums of op(B) over K as well (a bias gradient
-// beside its weight gradient).
+// `colsum` is non-null it receives the N column sums of op(B) over K as well, or with `sum_a` the
+// M row sums of op(A) (a bias gradient beside its weight gradient). With `defer` the split-K sums
+// are left to column_finalize jobs (gemm_deferred_jobs); the output must then be dense (ldc = n).
+struct ColumnJob;
 struct GemmArgs {
   const float* a; const float* b; float* c; const float* bias;
   int64_t m, n, k, lda, ldb, ldc;
   bool ta, tb;
   float* workspace; int64_t workspace_floats;
   float* colsum;
+  bool sum_a, defer;
 };
 int gemm_split_for(int64_t m, int64_t n, int64_t k);  // the split-K factor the launcher uses
-// Floats of workspace a gemm of this shape needs (0 without split-K): the slices' partial tiles,
-// then the slices' column sums when asked for.
-int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum = false);
+// Floats of workspace a gemm of this shape needs (0 without split-K): the slices' partial
+// products, then the slices' column (row) sums when asked for.
+int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum = false, bool sum_a = false);
+// The column_finalize jobs that finish a deferred split-K gemm (0, 1 or 2 written to jobs).
+int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs);
 void gemm(hipStream_t s, const GemmArgs& g);
 
 void transpose(hipStream_t s, const float* a, float* o, int64_t rows, int64_t cols);  // a [rows,cols] -> o [cols,rows]
@@ -70,11 +75,10 @@ struct ColumnJobs { ColumnJob job[kColumnJobs]; int32_t count; };
 void column_finalize(hipStream_t s, const ColumnJob* jobs, int count);
 
 void embedding(hipStream_t s, const float* table, const int32_t* ids, float* o, int64_t n, int64_t rows, int64_t h);
-// Deterministic sorted-segment scatter: out = 0; out[ids[k]] += g[k] in ascending k. `work` holds
-// embedding_grad_workspace(n, rows) bytes of scratch (16-byte aligned).
-int64_t embedding_grad_workspace(int64_t n, int64_t rows);
+// Deterministic segmented scatter: e = 0; e[ids[k]] += g[k] in ascending k (no float atomics);
+// out = e, or addend + e when addend is non-null.
 void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* out, int64_t n, int64_t rows,
-                    int64_t h, void* work, int64_t work_bytes);
+                    int64_t h, const float* addend = nullptr);
 
 void dropout(hipStream_t s, const float* x, float* o, int64_t n, const int32_t* token, uint64_t seed,
              uint64_t threshold, float scale);

@@ -187,7 +187,8 @@ template <bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                               float* __restrict__ C, const float* __restrict__ bias, int64_t M,
                                               int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-                                              int64_t kchunk, float* __restrict__ ws, float* __restrict__ colsum) {
+                                              int64_t kchunk, float* __restrict__ ws, float* __restrict__ colsum,
+                                              bool sum_a) {
   __shared__ float As[2][BK * LDP];
   __shared__ float Bs[2][BK * LDP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -197,9 +198,10 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   v4f acc00 = {0, 0, 0, 0}, acc01 = acc00, acc10 = acc00, acc11 = acc00;
   float ra[8], rb[8];
-  // Column sums of B (the bias gradient beside a weight gradient), taken from the LDS tiles by the
-  // first row of blocks: thread t adds column t mod 64 over rows 8 (t / 64) .. + 8 of each K tile.
-  const bool sums = colsum != nullptr && blockIdx.y == 0;
+  // Column sums of op(B) over K (or, with sum_a, row sums of op(A)): a bias gradient beside its
+  // weight gradient, taken from the LDS tiles by the first row (column) of blocks: thread t adds
+  // tile column t mod 64 over K rows 8 (t / 64) .. + 8 of each K tile.
+  const bool sums = colsum != nullptr && (sum_a ? blockIdx.x == 0 : blockIdx.y == 0);
   float csum = 0.0f;
   // B's (k, j) element is B[k * ldb + j], or B[j * ldb + k] when TB: the same loader with the
   // roles of "row" and "contiguous" swapped.
@@ -228,8 +230,9 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
     }
     if (sums) {
       const int c = tid & 63, kg = (tid >> 6) * 8;
+      const float* ss = sum_a ? as : bs;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) csum += bs[(kg + j) * LDP + c];
+      for (int j = 0; j < 8; ++j) csum += ss[(kg + j) * LDP + c];
     }
     buf ^= 1;
   }
@@ -238,9 +241,10 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
     float* red = As[0];
     red[tid] = csum;
     __syncthreads();
-    if (tid < 64 && n0 + tid < N) {
+    const int64_t base = sum_a ? m0 : n0, width = sum_a ? M : N;
+    if (tid < 64 && base + tid < width) {
       const float v = ((red[tid] + red[64 + tid]) + red[128 + tid]) + red[192 + tid];
-      colsum[(ws ? int64_t(blockIdx.z) * N : 0) + n0 + tid] = v;
+      colsum[(ws ? int64_t(blockIdx.z) * width : 0) + base + tid] = v;
     }
   }
   const v4f* accs[4] = {&acc00, &acc01, &acc10, &acc11};
@@ -256,91 +260,97 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
     }
     return;
   }
-  // Split-K: this slice's partial tile; k_splitk_sum adds the slices in order.
-  const int64_t tile = int64_t(blockIdx.y) * gridDim.x + blockIdx.x;
-  float* part = ws + (int64_t(blockIdx.z) * gridDim.x * gridDim.y + tile) * (BM * BN);
+  // Split-K: this slice's partial product, [M, N] row-major at slice z; the slices are added in
+  // order by k_splitk_sum or a deferred column_finalize job.
+  float* part = ws + int64_t(blockIdx.z) * M * N;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
+    const int64_t col = n0 + wn + (t & 1) * 16 + (lane & 15);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int lr = wm + (t >> 1) * 16 + 4 * (lane >> 4) + r, lc = wn + (t & 1) * 16 + (lane & 15);
-      part[lr * BN + lc] = (*accs[t])[r];
+      const int64_t row = m0 + wm + (t >> 1) * 16 + 4 * (lane >> 4) + r;
+      if (row < M && col < N) part[row * N + col] = (*accs[t])[r];
     }
   }
 }
 
-// Sums the split-K partial tiles in ascending slice order, one output element a thread; every
-// slice's load is issued before the adds.
+// Sums the split-K partial products in ascending slice order, one output element a thread, every
+// slice's load issued before the adds; the threads past M * N do the same for the slices' column
+// (row) sums.
 template <int SPLIT>
 __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ ws, float* __restrict__ C,
                                                     const float* __restrict__ bias, int64_t M, int64_t N, int64_t ldc,
-                                                    int tiles_x, int64_t tiles, int splits, float* __restrict__ colsum) {
-  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;  // over tiles * BM * BN, then N column sums
-  const int64_t tile = e / (BM * BN);
-  if (tile >= tiles) {
-    // The slices' column sums follow the partial tiles in the workspace.
-    const int64_t col = e - tiles * (BM * BN);
-    if (!colsum || col >= N) return;
-    const float* cs = ws + int64_t(splits) * tiles * (BM * BN) + col;
-    float t[SPLIT];
-#pragma unroll
-    for (int z = 0; z < SPLIT; ++z) t[z] = z < splits ? cs[z * N] : 0.0f;
-    float s = t[0];
-#pragma unroll
-    for (int z = 1; z < SPLIT; ++z)
-      if (z < splits) s += t[z];
-    for (int z = SPLIT; z < splits; ++z) s += cs[z * N];
-    colsum[col] = s;
-    return;
-  }
-  const int in = int(e % (BM * BN));
-  const int64_t row = int64_t(tile / tiles_x) * BM + in / BN, col = int64_t(tile % tiles_x) * BN + in % BN;
-  const int64_t stride = tiles * (BM * BN);
+                                                    int splits, float* __restrict__ colsum, int64_t width) {
+  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t mn = M * N;
+  const bool cs = e >= mn;
+  if (cs && (!colsum || e - mn >= width)) return;
+  const float* src = cs ? ws + int64_t(splits) * mn + (e - mn) : ws + e;
+  const int64_t stride = cs ? width : mn;
   float t[SPLIT];
 #pragma unroll
-  for (int z = 0; z < SPLIT; ++z) t[z] = z < splits ? ws[z * stride + e] : 0.0f;
+  for (int z = 0; z < SPLIT; ++z) t[z] = z < splits ? src[z * stride] : 0.0f;
   float s = t[0];
 #pragma unroll
   for (int z = 1; z < SPLIT; ++z)
     if (z < splits) s += t[z];
-  for (int z = SPLIT; z < splits; ++z) s += ws[z * stride + e];
-  if (row < M && col < N) C[row * ldc + col] = bias ? s + bias[col] : s;
+  for (int z = SPLIT; z < splits; ++z) s += src[z * stride];
+  if (cs) {
+    colsum[e - mn] = s;
+  } else {
+    const int64_t row = e / N, col = e - row * N;
+    C[row * ldc + col] = bias ? s + bias[col] : s;
+  }
 }
 
-int gemm_split_for(int64_t m, int64_t n, int64_t k) {
-  int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  if (tiles >= 256 || k < 512) return 1;
-  int64_t want = (1024 + tiles - 1) / tiles;
-  int64_t most = k / 128;
-  int64_t split = std::max<int64_t>(1, std::min(want, most));
+namespace {
+// The split-K factor and the K extent of a slice (a multiple of BK).
+struct SplitPlan { int split; int64_t chunk; };
+SplitPlan split_plan(int64_t m, int64_t n, int64_t k) {
+  const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  int64_t split = 1;
+  if (tiles < 256 && k >= 512) split = std::max<int64_t>(1, std::min((1024 + tiles - 1) / tiles, k / 128));
   int64_t chunk = ((k + split - 1) / split + BK - 1) / BK * BK;
-  return int((k + chunk - 1) / chunk);
+  return {int((k + chunk - 1) / chunk), chunk};
+}
+}  // namespace
+
+int gemm_split_for(int64_t m, int64_t n, int64_t k) { return split_plan(m, n, k).split; }
+
+int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum, bool sum_a) {
+  const int split = gemm_split_for(m, n, k);
+  if (split <= 1) return 0;
+  return int64_t(split) * m * n + (colsum ? int64_t(split) * (sum_a ? m : n) : 0);  // partials, then sums
 }
 
-int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum) {
-  int split = gemm_split_for(m, n, k);
+int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs) {
+  const int split = gemm_split_for(g.m, g.n, g.k);
   if (split <= 1) return 0;
-  int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  return tiles * split * BM * BN + (colsum ? split * n : 0);  // the slices' partial tiles, column sums
+  if (g.bias || g.ldc != g.n) bad("deferred split-K needs a dense output without bias");
+  if (g.m * g.n > INT32_MAX) bad("deferred split-K output too large");
+  jobs[0] = ColumnJob{g.workspace, g.c, nullptr, split, int32_t(g.m * g.n), int32_t(g.m * g.n), 0};
+  if (!g.colsum) return 1;
+  const int64_t width = g.sum_a ? g.m : g.n;
+  jobs[1] = ColumnJob{g.workspace + int64_t(split) * g.m * g.n, g.colsum, nullptr, split, int32_t(width), int32_t(width), 0};
+  return 2;
 }
 
 void gemm(hipStream_t s, const GemmArgs& g) {
   if (g.m <= 0 || g.n <= 0) return;
   if (g.k <= 0) bad("gemm with k = 0");
-  int split = gemm_split_for(g.m, g.n, g.k);
-  int64_t chunk = ((g.k + split - 1) / split + BK - 1) / BK * BK;
-  split = int((g.k + chunk - 1) / chunk);
-  int64_t tiles = ((g.m + BM - 1) / BM) * ((g.n + BN - 1) / BN);
+  const SplitPlan plan = split_plan(g.m, g.n, g.k);
+  const int split = plan.split;
+  const int64_t chunk = plan.chunk;
   float* ws = nullptr;
   if (split > 1) {
-    if (!g.workspace || g.workspace_floats < tiles * split * BM * BN + (g.colsum ? split * g.n : 0))
+    if (!g.workspace || g.workspace_floats < gemm_workspace(g.m, g.n, g.k, g.colsum != nullptr, g.sum_a))
       bad("gemm split-K workspace too small");
     ws = g.workspace;
   }
   dim3 grid(unsigned((g.n + BN - 1) / BN), unsigned((g.m + BM - 1) / BM), unsigned(split));
-  float* csum = g.colsum ? (ws ? ws + int64_t(split) * tiles * BM * BN : g.colsum) : nullptr;
   if (grid.y > 65535) bad("gemm M too large");
-  // float4 loads need a leading dimension and base address that keep every group 16-byte aligned.
+  const int64_t width = g.sum_a ? g.m : g.n;
+  float* csum = g.colsum ? (ws ? ws + int64_t(split) * g.m * g.n : g.colsum) : nullptr;
   // float4 loads need 16-byte aligned groups and a contiguous extent that is a multiple of 4.
   auto aligned = [](const float* p, int64_t ld, int64_t extent) {
     return (reinterpret_cast<uintptr_t>(p) % 16 == 0) && ld % 4 == 0 && extent % 4 == 0;
@@ -348,7 +358,7 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   const bool va = aligned(g.a, g.lda, g.ta ? g.m : g.k), vb = aligned(g.b, g.ldb, g.tb ? g.k : g.n);
 #define MSX_GEMM(TA, TB, VA, VB)                                                                                 \
   hipLaunchKernelGGL((k_gemm<TA, TB, VA, VB>), grid, dim3(256), 0, s, g.a, g.b, g.c, g.bias, g.m, g.n, g.k, g.lda, \
-                     g.ldb, g.ldc, chunk, ws, csum)
+                     g.ldb, g.ldc, chunk, ws, csum, g.sum_a)
 #define MSX_GEMM_V(TA, TB)                  \
   if (va && vb) MSX_GEMM(TA, TB, true, true);        \
   else if (va) MSX_GEMM(TA, TB, true, false);        \
@@ -360,18 +370,15 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   else { MSX_GEMM_V(true, true) }
 #undef MSX_GEMM_V
 #undef MSX_GEMM
-  if (split > 1) {
-    unsigned blocks = unsigned((tiles * BM * BN + (g.colsum ? g.n : 0) + 255) / 256);
-    int tx = int((g.n + BN - 1) / BN);
-    if (split <= 8)
-      hipLaunchKernelGGL(k_splitk_sum<8>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, tx, tiles, split,
-                         g.colsum);
-    else if (split <= 16)
-      hipLaunchKernelGGL(k_splitk_sum<16>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, tx, tiles, split,
-                         g.colsum);
-    else
-      hipLaunchKernelGGL(k_splitk_sum<32>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, tx, tiles, split,
-                         g.colsum);
+  if (split > 1 && !g.defer) {
+    const int64_t total = g.m * g.n + (g.colsum ? width : 0);
+    const unsigned blocks = unsigned((total + 255) / 256);
+#define MSX_SPLITK(S) hipLaunchKernelGGL(k_splitk_sum<S>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, \
+                                         split, g.colsum, width)
+    if (split <= 8) MSX_SPLITK(8);
+    else if (split <= 16) MSX_SPLITK(16);
+    else MSX_SPLITK(32);
+#undef MSX_SPLITK
   }
 }
 
@@ -709,326 +716,171 @@ void embedding(hipStream_t s, const float* table, const int32_t* ids, float* o, 
                      o, n, rows, h);
 }
 
-// Stable order of (id, k): one block of 1024 threads bitonic-sorts the unique keys id << 32 | k.
-// Thread t holds the E = pow2 / 1024 consecutive keys [t E, t E + E) in registers: strides below
-// E compare within the thread, strides below 64 E across the wave by shuffles, wider ones through
-// LDS.
-template <int E>
-__global__ __launch_bounds__(1024) void k_sort_ids(const int32_t* __restrict__ ids, uint64_t* __restrict__ keys,
-                                                   int64_t n) {
-  extern __shared__ uint64_t sk[];
-  const int t = threadIdx.x;
-  const int64_t pow2 = int64_t(E) * 1024;
-  uint64_t v[E];
+// EmbeddingGrad in one launch, deterministic, with no float atomics, optionally added to `addend`
+// (out = addend + EmbeddingGrad, elementwise). Block b first writes the rows of its stripe of the
+// table that no id names (zero, or the addend's row + 0), then, when position b is the first occurrence of
+// its id, collects that id's positions in ascending k (wave ballots over the ids, staged in LDS)
+// and adds the rows g[k] in that order from +0, one f32 rounding per add: the reference's order
+// (interpreter.rs:931-941), bit for bit. The rows come through LDS a chunk of `ch` at a time, with
+// kDepth chunks' loads in flight in registers ahead of the adds.
+constexpr int kEgThreads = 256, kDepth = 4, kEgVec = 4;  // float4 loads a thread per chunk
+
+// One chunk of rows in registers: kEgVec float4 a thread.
+struct EgChunk { float4 v[kEgVec]; };
+// Chunk q's loads: float4 e = tid + u * 256 of its cnt * h4; the tail (and a chunk past the end)
+// reads an in-range element that is never stored.
+__device__ __forceinline__ EgChunk eg_issue(const float* __restrict__ g, const int32_t* list, int64_t h, int h4, int q,
+                                            int ch, int total, int tid) {
+  const int q0 = q * ch;
+  const int cnt = q0 < total ? min(ch, total - q0) : 1;
+  const int tot = cnt * h4;
+  const int base = q0 < total ? q0 : 0;
+  EgChunk r;
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    int64_t i = int64_t(t) * E + e;
-    v[e] = i < n ? (uint64_t(uint32_t(ids[i])) << 32) | uint64_t(i) : ~uint64_t(0);
+  for (int u = 0; u < kEgVec; ++u) {
+    int e = tid + u * kEgThreads;
+    e = e < tot ? e : tot - 1;
+    const int rr = e / h4;
+    r.v[u] = reinterpret_cast<const float4*>(g + int64_t(list[base + rr]) * h)[e - rr * h4];
   }
-  for (int64_t size = 2; size <= pow2; size <<= 1) {
-    for (int64_t stride = size >> 1; stride > 0; stride >>= 1) {
-      if (stride < E) {
-        // The register pairs of each in-thread stride, unrolled with constant indices.
+  return r;
+}
+// Stores chunk q from r into LDS, refills r with chunk q + kDepth, and adds the chunk's rows in order.
+__device__ __forceinline__ void eg_step(const float* __restrict__ g, const int32_t* list, float* stage, int64_t h,
+                                        int h4, int q, int ch, int total, int chunks, int tid, EgChunk& r,
+                                        float& a0, float& a1, float& a2, float& a3) {
+  if (q >= chunks) return;  // uniform across the block
+  const int cnt = min(ch, total - q * ch), tot = cnt * h4;
+  __syncthreads();
 #pragma unroll
-        for (int sh = 8; sh >= 1; sh >>= 1) {
-          if (sh >= E || sh != int(stride)) continue;
-#pragma unroll
-          for (int e = 0; e < E; ++e) {
-            const int f = e ^ sh;
-            if (f > e) {
-              const int64_t i = int64_t(t) * E + e;
-              const bool up = (i & size) == 0;
-              const uint64_t a = v[e], b = v[f];
-              const bool swap = (a > b) == up;
-              v[e] = swap ? b : a;
-              v[f] = swap ? a : b;
-            }
-          }
-        }
-      } else if (stride < int64_t(E) * 64) {
-        const int lanes = int(stride / E);
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          int64_t i = int64_t(t) * E + e;
-          uint32_t lo = __shfl_xor(uint32_t(v[e]), lanes, 64), hi = __shfl_xor(uint32_t(v[e] >> 32), lanes, 64);
-          uint64_t other = (uint64_t(hi) << 32) | lo;
-          bool up = (i & size) == 0;
-          bool lower = (i & stride) == 0;  // this element is the pair's lower index
-          bool take_min = lower == up;
-          v[e] = take_min ? (other < v[e] ? other : v[e]) : (other > v[e] ? other : v[e]);
-        }
-      } else {
-        __syncthreads();
-#pragma unroll
-        for (int e = 0; e < E; ++e) sk[int64_t(t) * E + e] = v[e];
-        __syncthreads();
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          int64_t i = int64_t(t) * E + e;
-          uint64_t other = sk[i ^ stride];
-          bool up = (i & size) == 0;
-          bool lower = (i & stride) == 0;
-          bool take_min = lower == up;
-          v[e] = take_min ? (other < v[e] ? other : v[e]) : (other > v[e] ? other : v[e]);
-        }
-      }
-    }
+  for (int u = 0; u < kEgVec; ++u) {
+    const int e = tid + u * kEgThreads;
+    if (e < tot) reinterpret_cast<float4*>(stage)[e] = r.v[u];
   }
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    int64_t i = int64_t(t) * E + e;
-    if (i < n) keys[i] = v[e];
-  }
+  __syncthreads();
+  if (q + kDepth < chunks) r = eg_issue(g, list, h, h4, q + kDepth, ch, total, tid);
+  const int64_t c0 = tid, c1 = tid + kEgThreads, c2 = tid + 2 * kEgThreads, c3 = tid + 3 * kEgThreads;
+  if (c0 < h) for (int rr = 0; rr < cnt; ++rr) a0 = a0 + stage[int64_t(rr) * h + c0];
+  if (c1 < h) for (int rr = 0; rr < cnt; ++rr) a1 = a1 + stage[int64_t(rr) * h + c1];
+  if (c2 < h) for (int rr = 0; rr < cnt; ++rr) a2 = a2 + stage[int64_t(rr) * h + c2];
+  if (c3 < h) for (int rr = 0; rr < cnt; ++rr) a3 = a3 + stage[int64_t(rr) * h + c3];
 }
 
-// One block per sorted position; the block of an id's first position adds the id's rows in
-// ascending k, from +0, one f32 rounding per add: the reference's order (interpreter.rs:931-941),
-// bit for bit. The segment's rows are staged through LDS a chunk at a time, every load of a chunk
-// in flight together; the in-order adds then read LDS.
-__global__ __launch_bounds__(256) void k_segment_sum(const uint64_t* __restrict__ keys, const float* __restrict__ g,
-                                                     float* __restrict__ out, int64_t n, int64_t rows, int64_t h,
-                                                     int chunk) {
-  extern __shared__ float stage[];
-  __shared__ int seg_end;
-  const int tid = threadIdx.x;
-  const int64_t p = blockIdx.x;
-  const uint32_t id = uint32_t(keys[p] >> 32);
-  if (p > 0 && uint32_t(keys[p - 1] >> 32) == id) return;
-  if (int64_t(id) >= rows) return;
-  if (tid == 0) seg_end = int(n);
-  __syncthreads();
-  for (int64_t base = p + 1; base < n; base += 256) {
-    const int64_t idx = base + tid;
-    if (idx < n && uint32_t(keys[idx] >> 32) != id) atomicMin(&seg_end, int(idx));
-    __syncthreads();
-    if (seg_end < base + 256) break;
-  }
-  const int64_t end = seg_end;
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // columns tid, tid + 256, ... (h <= 1024)
-  for (int64_t q0 = p; q0 < end; q0 += chunk) {
-    const int64_t cnt = end - q0 < chunk ? end - q0 : chunk;
-    for (int64_t e = tid; e < cnt * h; e += 256) {
-      const int64_t r = e / h, c = e - r * h;
-      stage[e] = g[int64_t(uint32_t(keys[q0 + r])) * h + c];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t c = tid + 256 * u;
-      if (c < h)
-        for (int64_t r = 0; r < cnt; ++r) acc[u] = acc[u] + stage[r * h + c];
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int64_t c = tid + 256 * u;
-    if (c < h) out[int64_t(id) * h + c] = acc[u];
-  }
-}
-
-// The counting plan of EmbeddingGrad for tables of at most kPlanRows rows, one block of 1024
-// threads with a per-row counter in LDS: counts per id, one exclusive scan that yields each id's
-// start in `order` and its segment index, the segment list (id, start, count) in ascending id, a
-// presence bitmap of the table's rows, and the positions k grouped by id, ascending in each group. A counter word packs the start (low 16 bits) and the
-// segment index (high 16 bits); n < 2^16 keeps them apart.
-constexpr int64_t kPlanRows = 32768;
-__global__ __launch_bounds__(1024) void k_embed_plan(const int32_t* __restrict__ ids, int64_t n, int64_t rows,
-                                                     int32_t* __restrict__ order, int32_t* __restrict__ segs,
-                                                     int32_t* __restrict__ nseg, uint32_t* __restrict__ present) {
-  extern __shared__ uint32_t cnt[];
-  __shared__ uint32_t wave_tot[16];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  for (int64_t r = t; r < rows; r += 1024) cnt[r] = 0;
-  __syncthreads();
-  for (int64_t k = t; k < n; k += 1024) {
-    const uint32_t id = uint32_t(ids[k]);
-    if (id < uint64_t(rows)) atomicAdd(&cnt[id], 1u);
-  }
-  __syncthreads();
-  // Thread t owns rows [t per, (t + 1) per); a row's packed value is count | (count > 0) << 16.
-  const int64_t per = (rows + 1023) / 1024;
-  const int64_t r0 = std::min<int64_t>(rows, t * per), r1 = std::min<int64_t>(rows, r0 + per);
-  uint32_t local = 0;
-  for (int64_t r = r0; r < r1; ++r) {
-    const uint32_t c = cnt[r];
-    local += c | (c ? 0x10000u : 0u);
-  }
-  uint32_t incl = local;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t o = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += o;
-  }
-  if (lane == 63) wave_tot[wave] = incl;
-  __syncthreads();
-  uint32_t run = incl - local;
-  for (int w = 0; w < wave; ++w) run += wave_tot[w];
-  if (t == 1023) *nseg = int32_t((run + local) >> 16);
-  for (int64_t r = r0; r < r1; ++r) {
-    const uint32_t c = cnt[r];
-    cnt[r] = run;
-    if (c) {
-      const uint32_t sidx = run >> 16;
-      segs[3 * sidx] = int32_t(r);
-      segs[3 * sidx + 1] = int32_t(run & 0xFFFFu);
-      segs[3 * sidx + 2] = int32_t(c);
-      run += c | 0x10000u;
-    }
-  }
-  __syncthreads();
-  // Row r is present when the segment index steps between r and r + 1.
-  const uint32_t total_seg = (wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3] + wave_tot[4] + wave_tot[5] +
-                              wave_tot[6] + wave_tot[7] + wave_tot[8] + wave_tot[9] + wave_tot[10] + wave_tot[11] +
-                              wave_tot[12] + wave_tot[13] + wave_tot[14] + wave_tot[15]) >> 16;
-  for (int64_t w = t; w < (rows + 31) / 32; w += 1024) {
-    uint32_t bits = 0;
-    for (int b = 0; b < 32; ++b) {
-      const int64_t r = w * 32 + b;
-      if (r >= rows) break;
-      const uint32_t here = cnt[r] >> 16, next = r + 1 < rows ? cnt[r + 1] >> 16 : total_seg;
-      bits |= (next != here ? 1u : 0u) << b;
-    }
-    present[w] = bits;
-  }
-  __syncthreads();
-  // Stable placement, 1024 positions a round. In a wave, a lane's rank among the lanes before it
-  // with the same id comes from a scan of the wave's ids; the first such lane (the leader) then
-  // takes the id's cursor forward by the wave's count, the 16 waves one after another, so the
-  // positions of an id land in ascending k.
-  for (int64_t base = 0; base < n; base += 1024) {
-    const int64_t k = base + t;
-    const uint32_t id = k < n ? uint32_t(ids[k]) : 0xFFFFFFFFu;
-    const bool valid = id < uint64_t(rows);
-    int rank = 0, count = 0, leader = 64;
-    for (int j = 0; j < 64; ++j) {
-      const uint32_t other = __shfl(id, j, 64);
-      const bool same = other == id;
-      rank += (same && j < lane) ? 1 : 0;
-      count += same ? 1 : 0;
-      leader = (same && leader == 64) ? j : leader;
-    }
-    uint32_t cursor = 0;
-    for (int w = 0; w < 16; ++w) {
-      if (wave == w && valid && leader == lane) cursor = atomicAdd(&cnt[id], uint32_t(count));
-      __syncthreads();
-    }
-    cursor = __shfl(cursor, leader & 63, 64);
-    if (valid) order[(cursor & 0xFFFFu) + uint32_t(rank)] = int32_t(k);
-  }
-}
-
-// Block b zeroes the absent rows of its stripe of the table, then, when b is below the segment
-// count, sums segment b: the rows g[k] of its positions are added in ascending k from +0, one f32
-// rounding per add: the reference's order (interpreter.rs:931-941), bit for bit. Rows come in
-// chunks of `ch` through LDS, all of a chunk's loads in flight together.
-constexpr int kSumThreads = 256;
-__global__ __launch_bounds__(kSumThreads) void k_embed_sum(const float* __restrict__ g, const int32_t* __restrict__ order,
-                                                           const int32_t* __restrict__ segs,
-                                                           const int32_t* __restrict__ nseg,
-                                                           const uint32_t* __restrict__ present, float* __restrict__ out,
-                                                           int64_t rows, int64_t h, int64_t stripe, int ch, bool vec) {
-  extern __shared__ float lds[];
-  const int tid = threadIdx.x;
+__global__ __launch_bounds__(kEgThreads) void k_embedding_grad(const int32_t* __restrict__ ids, const float* __restrict__ g,
+                                                               const float* __restrict__ addend, float* __restrict__ out,
+                                                               int n, int64_t rows, int64_t h, int64_t stripe, int ch,
+                                                               bool vec) {
+  extern __shared__ int32_t eg_lds[];
+  int32_t* sid = eg_lds;                                      // [n] the ids
+  int32_t* list = sid + n;                                    // [n] this block's positions
+  float* stage = reinterpret_cast<float*>(list + n);          // [ch * h]
+  __shared__ uint32_t mask;
+  __shared__ int wave_cnt[kEgThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t b = blockIdx.x;
-  {
-    const int64_t z0 = b * stripe, z1 = std::min<int64_t>(rows, z0 + stripe);
-    for (int64_t r = z0; r < z1; ++r) {
-      if ((present[r >> 5] >> (r & 31)) & 1u) continue;
-      for (int64_t c = tid; c < h; c += kSumThreads) out[r * h + c] = 0.0f;
+  for (int j0 = 0; j0 < n; j0 += kEgThreads * 8) {
+    int32_t t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + tid + u * kEgThreads;
+      t[u] = ids[j < n ? j : n - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + tid + u * kEgThreads;
+      if (j < n) sid[j] = t[u];
     }
   }
-  if (b >= *nseg) return;
-  const int32_t id = segs[3 * b], start = segs[3 * b + 1], c = segs[3 * b + 2];
-  const int32_t* ks = order + start;  // the segment's positions, ascending
-  float* stage = lds;
+  if (tid == 0) mask = 0;
+  __syncthreads();
+  // The stripe (at most 32 rows): rows no id names are zero.
+  const int64_t z0 = b * stripe, z1 = std::min<int64_t>(rows, z0 + stripe);
+  if (z0 < z1) {
+    for (int j = tid; j < n; j += kEgThreads) {
+      const int64_t id = sid[j];
+      if (id >= z0 && id < z1) atomicOr(&mask, 1u << uint32_t(id - z0));
+    }
+    __syncthreads();
+    const uint32_t m = mask;
+    for (int64_t r = z0; r < z1; ++r)
+      if (!((m >> uint32_t(r - z0)) & 1u))
+        for (int64_t c = tid; c < h; c += kEgThreads) out[r * h + c] = addend ? addend[r * h + c] + 0.0f : 0.0f;
+  }
+  if (b >= n) return;
+  const int32_t id = sid[b];
+  if (id < 0 || int64_t(id) >= rows) return;
+  int dup = 0;
+  for (int j = tid; j < int(b); j += kEgThreads) dup |= sid[j] == id ? 1 : 0;
+  if (__syncthreads_or(dup)) return;
+  // The positions of `id`, ascending.
+  int total = 0;
+  for (int j0 = int(b); j0 < n; j0 += kEgThreads) {
+    const int j = j0 + tid;
+    const bool hit = j < n && sid[j] == id;
+    const uint64_t bal = __ballot(hit);
+    if (lane == 0) wave_cnt[wave] = __popcll(bal);
+    __syncthreads();
+    int off = total;
+    for (int w = 0; w < wave; ++w) off += wave_cnt[w];
+    if (hit) list[off + __popcll(bal & ((uint64_t(1) << lane) - 1))] = j;
+#pragma unroll
+    for (int w = 0; w < kEgThreads / 64; ++w) total += wave_cnt[w];
+    __syncthreads();
+  }
   // Thread tid adds columns tid, tid + 256, tid + 512, tid + 768 (h <= 1024).
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int q0 = 0; q0 < c; q0 += ch) {
-    const int cnt = c - q0 < ch ? c - q0 : ch;
-    __syncthreads();
-    if (vec) {
-      // Up to 8 float4 a thread, every load issued before the first LDS store; the tail reads a
-      // clamped in-range element and skips the store.
-      const int h4 = int(h >> 2), tot = cnt * h4;
-      float4 tmp[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        int e = tid + u * kSumThreads;
-        e = e < tot ? e : tot - 1;
-        const int r = e / h4;
-        tmp[u] = reinterpret_cast<const float4*>(g + int64_t(ks[q0 + r]) * h)[e - r * h4];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int e = tid + u * kSumThreads;
-        if (e < tot) reinterpret_cast<float4*>(stage)[e] = tmp[u];
-      }
-    } else {
-      for (int64_t e = tid; e < int64_t(cnt) * h; e += kSumThreads) {
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  if (vec) {
+    const int h4 = int(h >> 2);
+    const int chunks = (total + ch - 1) / ch;
+    EgChunk r0 = eg_issue(g, list, h, h4, 0, ch, total, tid);
+    EgChunk r1 = eg_issue(g, list, h, h4, 1, ch, total, tid);
+    EgChunk r2 = eg_issue(g, list, h, h4, 2, ch, total, tid);
+    EgChunk r3 = eg_issue(g, list, h, h4, 3, ch, total, tid);
+    for (int q = 0; q < chunks; q += kDepth) {
+      eg_step(g, list, stage, h, h4, q, ch, total, chunks, tid, r0, a0, a1, a2, a3);
+      eg_step(g, list, stage, h, h4, q + 1, ch, total, chunks, tid, r1, a0, a1, a2, a3);
+      eg_step(g, list, stage, h, h4, q + 2, ch, total, chunks, tid, r2, a0, a1, a2, a3);
+      eg_step(g, list, stage, h, h4, q + 3, ch, total, chunks, tid, r3, a0, a1, a2, a3);
+    }
+  } else {
+    for (int q0 = 0; q0 < total; q0 += ch) {
+      const int cnt = min(ch, total - q0);
+      __syncthreads();
+      for (int64_t e = tid; e < int64_t(cnt) * h; e += kEgThreads) {
         const int r = int(e / h);
-        stage[e] = g[int64_t(ks[q0 + r]) * h + (e - int64_t(r) * h)];
+        stage[e] = g[int64_t(list[q0 + r]) * h + (e - int64_t(r) * h)];
       }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t col = tid + int64_t(kSumThreads) * u;
-      if (col < h)
-        for (int r = 0; r < cnt; ++r) acc[u] = acc[u] + stage[int64_t(r) * h + col];
+      __syncthreads();
+      const int64_t c0 = tid, c1 = tid + kEgThreads, c2 = tid + 2 * kEgThreads, c3 = tid + 3 * kEgThreads;
+      if (c0 < h) for (int rr = 0; rr < cnt; ++rr) a0 = a0 + stage[int64_t(rr) * h + c0];
+      if (c1 < h) for (int rr = 0; rr < cnt; ++rr) a1 = a1 + stage[int64_t(rr) * h + c1];
+      if (c2 < h) for (int rr = 0; rr < cnt; ++rr) a2 = a2 + stage[int64_t(rr) * h + c2];
+      if (c3 < h) for (int rr = 0; rr < cnt; ++rr) a3 = a3 + stage[int64_t(rr) * h + c3];
     }
   }
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int64_t col = tid + int64_t(kSumThreads) * u;
-    if (col < h) out[int64_t(id) * h + col] = acc[u];
-  }
-}
-
-int64_t embedding_grad_workspace(int64_t n, int64_t rows) {
-  // The counting plan: order [n], segments [3 n], the segment count, the presence bitmap; the
-  // sort fallback: n 64-bit keys.
-  const int64_t plan = 4 * (4 * n + 1) + 4 * ((rows + 31) / 32) + 16;
-  return std::max<int64_t>(plan, 8 * n) + 256;
+  float* o = out + int64_t(id) * h;
+  const float* ad = addend ? addend + int64_t(id) * h : nullptr;
+  if (tid < h) o[tid] = ad ? ad[tid] + a0 : a0;
+  if (tid + kEgThreads < h) o[tid + kEgThreads] = ad ? ad[tid + kEgThreads] + a1 : a1;
+  if (tid + 2 * kEgThreads < h) o[tid + 2 * kEgThreads] = ad ? ad[tid + 2 * kEgThreads] + a2 : a2;
+  if (tid + 3 * kEgThreads < h) o[tid + 3 * kEgThreads] = ad ? ad[tid + 3 * kEgThreads] + a3 : a3;
 }
 
 void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* out, int64_t n, int64_t rows, int64_t h,
-                    void* work, int64_t work_bytes) {
+                    const float* addend) {
   if (n > 16384) bad("embedding gradient over more than 16384 ids");
   if (h > 1024) bad("embedding gradient rows wider than 1024");
-  if (work_bytes < embedding_grad_workspace(n, rows)) bad("embedding gradient workspace too small");
-  if (n <= 0 || rows <= 0 || h <= 0) { fill_zero(s, out, rows * h * 4); return; }
-  if (rows <= kPlanRows) {
-    int32_t* order = static_cast<int32_t*>(work);
-    int32_t* segs = order + n;
-    int32_t* nseg = segs + 3 * n;
-    uint32_t* present = reinterpret_cast<uint32_t*>(nseg + 1);
-    hipLaunchKernelGGL(k_embed_plan, dim3(1), dim3(1024), size_t(rows) * 4, s, ids, n, rows, order, segs, nseg, present);
-    const int64_t blocks = std::max<int64_t>(n, 1024);
-    const int64_t stripe = (rows + blocks - 1) / blocks;
-    const bool vec = h % 4 == 0 && reinterpret_cast<uintptr_t>(g) % 16 == 0;
-    const int ch = int(vec ? std::max<int64_t>(1, 2048 / (h / 4)) : std::max<int64_t>(1, std::min<int64_t>(64, 8192 / h)));
-    hipLaunchKernelGGL(k_embed_sum, dim3(unsigned(blocks)), dim3(kSumThreads), size_t(ch) * size_t(h) * 4, s, g, order,
-                       segs, nseg, present, out, rows, h, stripe, ch, vec);
-    return;
-  }
-  // Tables beyond the LDS counters: a bitonic sort of the (id, k) keys, then one block per sorted
-  // position.
-  uint64_t* keys = static_cast<uint64_t*>(work);
-  fill_zero(s, out, rows * h * 4);
-  int64_t pow2 = 1024;
-  while (pow2 < n) pow2 <<= 1;
-  size_t lds = size_t(pow2) * 8;
-  switch (pow2 / 1024) {
-    case 1: hipLaunchKernelGGL(k_sort_ids<1>, dim3(1), dim3(1024), lds, s, ids, keys, n); break;
-    case 2: hipLaunchKernelGGL(k_sort_ids<2>, dim3(1), dim3(1024), lds, s, ids, keys, n); break;
-    case 4: hipLaunchKernelGGL(k_sort_ids<4>, dim3(1), dim3(1024), lds, s, ids, keys, n); break;
-    case 8: hipLaunchKernelGGL(k_sort_ids<8>, dim3(1), dim3(1024), lds, s, ids, keys, n); break;
-    default: hipLaunchKernelGGL(k_sort_ids<16>, dim3(1), dim3(1024), lds, s, ids, keys, n); break;
-  }
-  const int chunk = int(std::max<int64_t>(1, std::min<int64_t>(64, 16384 / h)));
-  hipLaunchKernelGGL(k_segment_sum, dim3(unsigned(n)), dim3(256), size_t(chunk) * size_t(h) * 4, s, keys, g, out, n,
-                     rows, h, chunk);
+  if (rows <= 0 || h <= 0) return;
+  if (n <= 0 && !addend) { fill_zero(s, out, rows * h * 4); return; }
+  const int64_t blocks = std::max<int64_t>(n, (rows + 31) / 32);
+  if (blocks > 2147483647) bad("embedding gradient table too large");
+  const int64_t stripe = (rows + blocks - 1) / blocks;  // <= 32
+  const bool vec = h % 4 == 0 && reinterpret_cast<uintptr_t>(g) % 16 == 0;
+  // A chunk fills the float4 registers of every thread (vec) or 4096 floats.
+  const int ch = int(vec ? std::max<int64_t>(1, int64_t(kEgThreads) * kEgVec / (h / 4)) : std::max<int64_t>(1, 4096 / h));
+  const size_t lds = size_t(2 * n) * 4 + size_t(ch) * size_t(h) * 4;
+  hipLaunchKernelGGL(k_embedding_grad, dim3(unsigned(blocks)), dim3(kEgThreads), lds, s, ids, g, addend, out, int(n),
+                     rows, h, stripe, ch, vec);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1263,16 +1115,9 @@ __global__ void k_record_loss(const float* __restrict__ loss, float* __restrict_
 }
 void prepare() {
   // Kernels whose dynamic LDS may exceed the 64 KiB default; set once, outside any capture.
-  const void* sorts[] = {reinterpret_cast<const void*>(k_sort_ids<1>), reinterpret_cast<const void*>(k_sort_ids<2>),
-                         reinterpret_cast<const void*>(k_sort_ids<4>), reinterpret_cast<const void*>(k_sort_ids<8>),
-                         reinterpret_cast<const void*>(k_sort_ids<16>)};
-  const void* plan = reinterpret_cast<const void*>(k_embed_plan);
-  hipError_t pe = hipFuncSetAttribute(plan, hipFuncAttributeMaxDynamicSharedMemorySize, int(kPlanRows * 4));
-  if (pe != hipSuccess) throw std::runtime_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(pe));
-  for (const void* k : sorts) {
-    hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) throw std::runtime_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
-  }
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_embedding_grad),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+  if (e != hipSuccess) throw std::runtime_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
   prepare_attention();
 }
 

@@ -166,14 +166,16 @@ void Executor::build() {
   std::set<uint32_t> outputs(p.outputs.begin(), p.outputs.end());
 
   // --- fusions ------------------------------------------------------------------------------
-  std::set<uint32_t> folded;     // Transposes read in place by every consumer (all MatMuls)
+  // Transposes read in place by every consumer: MatMuls read through them, and a Transpose of one
+  // is computed from the source.
+  std::set<uint32_t> folded;
   std::set<uint32_t> mm_fused;   // MatMuls whose one consumer AddRows takes them as a biased GEMM
   for (size_t k = 0; k < n; ++k) {
     if (!need[k]) continue;
     const Node& x = p.nodes[k];
     if (x.op == Op::Transpose && !outputs.count(x.id) && !consumers[k].empty()) {
       bool all_mm = true;
-      for (auto c : consumers[k]) all_mm = all_mm && p.nodes[c].op == Op::MatMul;
+      for (auto c : consumers[k]) all_mm = all_mm && (p.nodes[c].op == Op::MatMul || p.nodes[c].op == Op::Transpose);
       if (all_mm) folded.insert(x.id);
     }
     if (x.op == Op::MatMul && !outputs.count(x.id) && consumers[k].size() == 1) {
@@ -181,6 +183,20 @@ void Executor::build() {
       if (c.op == Op::AddRows && c.operands[0] == x.id && c.operands[1] != x.id) mm_fused.insert(x.id);
     }
   }
+  // A MatMul read only by a Transpose that nothing reads through (no MatMul or Transpose reader)
+  // is computed transposed, as B^T A^T, straight into the Transpose's value.
+  std::map<uint32_t, uint32_t> mm_transposed;  // MatMul -> Transpose
+  for (size_t k = 0; k < n; ++k) {
+    const Node& x = p.nodes[k];
+    if (!need[k] || x.op != Op::MatMul || outputs.count(x.id) || mm_fused.count(x.id) || consumers[k].size() != 1) continue;
+    const Node& t = p.nodes[consumers[k][0]];
+    if (t.op != Op::Transpose || folded.count(t.id)) continue;
+    bool through = false;
+    for (auto c : consumers[p.pos.at(t.id)]) through = through || p.nodes[c].op == Op::MatMul || p.nodes[c].op == Op::Transpose;
+    if (!through) mm_transposed[x.id] = t.id;
+  }
+  std::set<uint32_t> transposed_out;
+  for (auto [m, t] : mm_transposed) transposed_out.insert(t);
   // A SumRows of a MatMul's un-transposed B operand (the bias gradient beside its weight gradient)
   // is taken by that GEMM from its LDS tiles, when no reader of the sum comes before the GEMM.
   std::map<uint32_t, uint32_t> colsum_of;  // MatMul -> SumRows
@@ -200,6 +216,20 @@ void Executor::build() {
       colsum_fused.insert(p.nodes[k].id);
       break;
     }
+  }
+  // Add(X, EmbeddingGrad) with the EmbeddingGrad read only there and X computed before it: the
+  // scatter writes X + its result straight into the Add's value.
+  std::map<uint32_t, std::pair<uint32_t, uint32_t>> eg_add;  // EmbeddingGrad -> (Add, X)
+  std::set<uint32_t> eg_add_nodes;
+  for (size_t k = 0; k < n; ++k) {
+    const Node& x = p.nodes[k];
+    if (!need[k] || x.op != Op::EmbeddingGrad || outputs.count(x.id) || consumers[k].size() != 1) continue;
+    const Node& a = p.nodes[consumers[k][0]];
+    if (a.op != Op::Add || a.operands[0] == a.operands[1]) continue;
+    const uint32_t other = a.operands[0] == x.id ? a.operands[1] : a.operands[0];
+    if (p.node(other).ty.shape != x.ty.shape || p.pos.at(other) > k) continue;
+    eg_add[x.id] = {a.id, other};
+    eg_add_nodes.insert(a.id);
   }
   // The LayerNorm gradients of one (input, output gradient) pair run as one pass: dx, and block
   // partials of the gamma and beta sums, finished by a batched column reduction, deferred to the
@@ -235,9 +265,9 @@ void Executor::build() {
       break;
     }
   }
+  // (Program outputs are read after the last launch, so they do not hold a reduction back.)
   auto only_optimizer_reads = [&](int64_t v) {
     if (v < 0) return true;
-    if (outputs.count(uint32_t(v))) return false;
     for (auto c : consumers[p.pos.at(uint32_t(v))])
       if (!optimizer.count(p.nodes[c].id)) return false;
     return true;
@@ -284,7 +314,7 @@ void Executor::build() {
         constants[x.id] = x.scalar;
         break;
       default:
-        if (folded.count(x.id) || mm_fused.count(x.id)) break;
+        if (folded.count(x.id) || mm_fused.count(x.id) || mm_transposed.count(x.id) || eg_add.count(x.id)) break;
         token_[x.id] = arena_.reserve(size_t(x.ty.count()) * 4);
         break;
     }
@@ -314,8 +344,10 @@ void Executor::build() {
   std::map<uint32_t, void*> ce_stats_tok;             // logits value -> stats [rows, 2]
   std::map<std::pair<uint32_t, uint32_t>, void*> ce_den_tok;  // (logits, weights) -> den
   std::map<std::vector<uint32_t>, std::pair<uint32_t, void*>> attn_fwd;  // operands -> (output, stats)
-  struct DeferredColumns { void* partial; int64_t gamma, beta; int32_t chunks, h; };
-  std::vector<DeferredColumns> deferred;
+  // Reductions left to the batched column finalize: partial sums at `offset` floats into the
+  // workspace `tok`, finished into the values lo (columns below split) and hi.
+  struct DeferredJob { void* tok; int64_t offset, lo, hi; int32_t chunks, width, split; };
+  std::vector<DeferredJob> deferred;
   auto R = [&](size_t bytes) { return arena_.reserve(bytes); };
   auto A = [this](void* tok) { return arena_.at(tok); };
   auto P = [this](uint32_t id) { return ptr(id); };
@@ -367,6 +399,7 @@ void Executor::build() {
     switch (x.op) {
       case Op::Input: case Op::ParamRead: case Op::Scalar: break;
       case Op::Add: case Op::Sub: case Op::Mul: case Op::Div: {
+        if (eg_add_nodes.count(id)) break;  // written by its EmbeddingGrad
         int op = x.op == Op::Add ? hk::EW_ADD : x.op == Op::Sub ? hk::EW_SUB : x.op == Op::Mul ? hk::EW_MUL : hk::EW_DIV;
         bool as = p.node(o[0]).ty.rank() == 0 && count > 1, bs = p.node(o[1]).ty.rank() == 0 && count > 1;
         uint32_t a = o[0], b = o[1];
@@ -389,6 +422,8 @@ void Executor::build() {
         uint32_t mm = x.op == Op::MatMul ? id : o[0];
         if (x.op == Op::MatMul && mm_fused.count(id)) break;
         bool fused = x.op == Op::AddRows && mm_fused.count(o[0]);
+        const bool swap = x.op == Op::MatMul && mm_transposed.count(id);
+        const uint32_t out_id = swap ? mm_transposed.at(id) : id;
         if (x.op == Op::AddRows && !fused) {
           uint32_t a = o[0], b = o[1];
           int64_t rows = x.ty.shape[0], h = x.ty.shape[1];
@@ -399,29 +434,49 @@ void Executor::build() {
         Resolved ra = resolve(p, m.operands[0]), rb = resolve(p, m.operands[1]);
         int64_t M = m.ty.shape[0], N = m.ty.shape[1], K = shape(m.operands[0])[1];
         hk::GemmArgs g{};
-        g.m = M; g.n = N; g.k = K; g.ldc = N;
-        g.ta = ra.flip; g.lda = ra.flip ? M : K;
-        g.tb = rb.flip; g.ldb = rb.flip ? K : N;
+        uint32_t asrc = ra.src, bsrc = rb.src;
+        if (!swap) {
+          g.m = M; g.n = N; g.k = K; g.ldc = N;
+          g.ta = ra.flip; g.lda = ra.flip ? M : K;
+          g.tb = rb.flip; g.ldb = rb.flip ? K : N;
+        } else {
+          // C^T [N, M] = op(B)^T op(A)^T: B's source becomes the left operand, A's the right.
+          g.m = N; g.n = M; g.k = K; g.ldc = M;
+          g.ta = !rb.flip; g.lda = rb.flip ? K : N;
+          g.tb = !ra.flip; g.ldb = ra.flip ? M : K;
+          std::swap(asrc, bsrc);
+        }
         const int64_t cs_id = x.op == Op::MatMul && colsum_of.count(id) ? int64_t(colsum_of.at(id)) : -1;
-        int64_t wsf = hk::gemm_workspace(M, N, K, cs_id >= 0);
+        g.sum_a = swap;  // the column sums of B are the row sums of the swapped left operand
+        int64_t wsf = hk::gemm_workspace(g.m, g.n, g.k, cs_id >= 0, g.sum_a);
         void* ws = wsf > 0 ? R(size_t(wsf) * 4) : nullptr;
         g.workspace_floats = wsf;
-        uint32_t asrc = ra.src, bsrc = rb.src;
         int64_t bias_id = fused ? int64_t(o[1]) : -1;
+        // Split-K partials only the optimizer reads are summed by the batched column finalize.
+        g.defer = wsf > 0 && bias_id < 0 && only_optimizer_reads(int64_t(out_id)) && only_optimizer_reads(cs_id);
         push([=](hipStream_t s) {
           hk::GemmArgs a = g;
           a.a = F(asrc);
           a.b = F(bsrc);
-          a.c = F(id);
+          a.c = F(out_id);
           a.bias = bias_id >= 0 ? F(uint32_t(bias_id)) : nullptr;
           a.workspace = ws ? static_cast<float*>(A(ws)) : nullptr;
           a.colsum = cs_id >= 0 ? F(uint32_t(cs_id)) : nullptr;
           hk::gemm(s, a);
         });
+        if (g.defer) {
+          const int split = hk::gemm_split_for(g.m, g.n, g.k);
+          const int32_t mn = int32_t(g.m * g.n);
+          deferred.push_back({ws, 0, int64_t(out_id), -1, split, mn, mn});
+          if (cs_id >= 0) {
+            const int32_t w = int32_t(g.sum_a ? g.m : g.n);
+            deferred.push_back({ws, int64_t(split) * g.m * g.n, cs_id, -1, split, w, w});
+          }
+        }
         break;
       }
       case Op::Transpose: {
-        if (folded.count(id)) break;
+        if (folded.count(id) || transposed_out.count(id)) break;
         Resolved r = resolve(p, o[0]);
         uint32_t src = r.src;
         if (r.flip) {  // the transpose of a transpose: a copy of the source
@@ -464,9 +519,14 @@ void Executor::build() {
           auto it = id_bounds_.find(p.node(ids).name);
           id_bounds_[p.node(ids).name] = it == id_bounds_.end() ? rows : std::min(it->second, rows);
         }
-        const int64_t wb = hk::embedding_grad_workspace(nn, rows);
-        void* work = R(size_t(wb));
-        push([=](hipStream_t s) { hk::embedding_grad(s, I(ids), F(g), F(id), nn, rows, h, A(work), wb); });
+        if (eg_add.count(id)) {
+          const auto [sum_id, addend] = eg_add.at(id);
+          what = "EmbeddingGrad+Add %" + std::to_string(id) + " %" + std::to_string(sum_id) + " " + type_string(x.ty);
+          push([=](hipStream_t s) { hk::embedding_grad(s, I(ids), F(g), F(sum_id), nn, rows, h, F(addend)); });
+          bytes += 8.0 * double(count);
+        } else {
+          push([=](hipStream_t s) { hk::embedding_grad(s, I(ids), F(g), F(id), nn, rows, h); });
+        }
         break;
       }
       case Op::SumRows: {
@@ -521,14 +581,14 @@ void Executor::build() {
         });
         bytes = 4.0 * double(rows * h * (dxv >= 0 ? 3 : 2) + (gmv >= 0 ? h : 0) + (sums ? 2 * h : 0));
         if (sums) {
-          DeferredColumns d{part, gr.gamma, gr.beta, int32_t(chunks), int32_t(h)};
+          DeferredJob d{part, 0, gr.gamma, gr.beta, int32_t(chunks), int32_t(2 * h), int32_t(h)};
           if (only_optimizer_reads(gr.gamma) && only_optimizer_reads(gr.beta)) {
             deferred.push_back(d);
           } else {
             pending.back().bytes = bytes;
             push([=](hipStream_t s) {
-              hk::ColumnJob j{static_cast<float*>(A(d.partial)), d.gamma >= 0 ? F(uint32_t(d.gamma)) : nullptr,
-                              d.beta >= 0 ? F(uint32_t(d.beta)) : nullptr, d.chunks, 2 * d.h, d.h, 0};
+              hk::ColumnJob j{static_cast<float*>(A(d.tok)), d.lo >= 0 ? F(uint32_t(d.lo)) : nullptr,
+                              d.hi >= 0 ? F(uint32_t(d.hi)) : nullptr, d.chunks, d.width, d.split, 0};
               hk::column_finalize(s, &j, 1);
             });
             bytes = 4.0 * double(chunks * 2 * h + 2 * h);
@@ -651,19 +711,20 @@ void Executor::build() {
       pending.back().bytes = bytes;
     }
   }
-  // The LayerNorm gamma and beta sums only the optimizer reads, in one launch.
+  // The reductions only the optimizer reads (LayerNorm gamma and beta sums, split-K weight
+  // gradients and their bias sums), in one launch.
   if (!deferred.empty()) {
     std::string what = "ColumnFinalize x" + std::to_string(deferred.size());
     double bytes = 0;
-    for (auto& d : deferred) bytes += 4.0 * double(int64_t(d.chunks) * 2 * d.h + 2 * d.h);
+    for (auto& d : deferred) bytes += 4.0 * double(int64_t(d.chunks) * d.width + d.width);
     pending.push_back({[this, what, deferred, F, A] {
                          return Launch{what, [this, deferred, F, A](hipStream_t s) {
                                          std::vector<hk::ColumnJob> jobs;
                                          for (auto& d : deferred)
-                                           jobs.push_back({static_cast<float*>(A(d.partial)),
-                                                           d.gamma >= 0 ? F(uint32_t(d.gamma)) : nullptr,
-                                                           d.beta >= 0 ? F(uint32_t(d.beta)) : nullptr, d.chunks,
-                                                           2 * d.h, d.h, 0});
+                                           jobs.push_back({static_cast<float*>(A(d.tok)) + d.offset,
+                                                           d.lo >= 0 ? F(uint32_t(d.lo)) : nullptr,
+                                                           d.hi >= 0 ? F(uint32_t(d.hi)) : nullptr, d.chunks,
+                                                           d.width, d.split, 0});
                                          hk::column_finalize(s, jobs.data(), int(jobs.size()));
                                        }};
                        },

@@ -71,6 +71,33 @@ def test_weight_gradient_gemm_takes_the_bias_gradient(ctx, oracle, rows, m, n):
     assert within(gb, wb, np.abs(dy).astype(np.float64).sum(0))[0]
 
 
+@pytest.mark.parametrize("v,h,r,n", [(1000, 64, 96, 256), (30522, 128, 832, 4096)])
+def test_tied_decoder_gradients(ctx, oracle, v, h, r, n):
+    """The tied-embedding decoder's graph: logits = h E^T, dX = dl E, the decoder weight gradient
+    computed transposed (with the bias sums as row sums of its left operand) and added to the
+    embedding gradient by the scatter."""
+    E, x = fast_values(51, v * h).reshape(v, h), fast_values(52, r * h).reshape(r, h)
+    dl, G = fast_values(53, r * v).reshape(r, v), fast_values(54, n * h).reshape(n, h)
+    ids = embedding_ids("zipf", v, n, np.random.default_rng(5))
+    p = Prog()
+    Ei, xi, di, ii, Gi = p.input("E", (v, h)), p.input("x", (r, h)), p.input("dl", (r, v)), p.input("ids", (n,), "i32"), p.input("G", (n, h))
+    t1 = p.op("Transpose", [Ei], (h, v))
+    logits = p.op("MatMul", [xi, t1], (r, v))
+    dx = p.op("MatMul", [di, p.op("Transpose", [t1], (v, h))], (r, h))
+    dw = p.op("MatMul", [p.op("Transpose", [xi], (h, r)), di], (h, v))
+    db = p.op("SumRows", [di], (v,))
+    eg = p.op("EmbeddingGrad", [ii, Gi], (v, h), f"[{v}]")
+    total = p.op("Add", [p.op("Transpose", [dw], (v, h)), eg], (v, h))
+    got, want = both(ctx, oracle, p.out(logits, dx, db, total), {"E": E, "x": x, "dl": dl, "ids": ids, "G": G}, (0, 1, 2, 3))
+    ax, aE, adl = (np.abs(a).astype(np.float64) for a in (x, E, dl))
+    assert within(got[0], want[0], (ax @ aE.T).reshape(-1))[0]
+    assert within(got[1], want[1], (adl @ aE).reshape(-1))[0]
+    assert within(got[2], want[2], adl.sum(0))[0]
+    seg = np.zeros((v, h))
+    np.add.at(seg, ids, np.abs(G).astype(np.float64))
+    assert within(got[3], want[3], ((ax.T @ adl).T + seg).reshape(-1))[0]
+
+
 @pytest.mark.parametrize("rows,h", [(6, 8), (4096, 128), (832, 128), (33, 200), (100, 768)])
 def test_layer_norm_family(ctx, oracle, rows, h):
     x = fast_values(6, rows * h).reshape(rows, h)
