@@ -45,21 +45,15 @@ void gemm(hipStream_t s, const GemmArgs& g);
 void transpose(hipStream_t s, const float* a, float* o, int64_t rows, int64_t cols);  // a [rows,cols] -> o [cols,rows]
 
 void add_rows(hipStream_t s, const float* x, const float* bias, float* o, int64_t rows, int64_t h);
-// out[c] = sum over rows of x[r, c] (optionally times xhat from stats); partial = [chunks, h].
-void column_sum(hipStream_t s, const float* x, float* out, int64_t rows, int64_t h, float* partial, int64_t partial_floats);
-void ln_grad_gamma(hipStream_t s, const float* x, const float* g, const float* stats, float* out, int64_t rows,
-                   int64_t h, float* partial, int64_t partial_floats);
-int64_t column_chunks(int64_t rows, int64_t h);
-// Floats of scratch a column reduction needs: the chunk partials and one counter per column tile
-// (zero before the first launch; every launch leaves them zero).
-int64_t column_workspace(int64_t rows, int64_t h);
+// Partial column sums of x [rows, h] into partial [column_partial_chunks, h], finished by
+// column_finalize (a SumRows).
+int64_t column_partial_chunks(int64_t rows, int64_t h);
+void column_partial(hipStream_t s, const float* x, float* partial, int64_t rows, int64_t h);
 
 // LayerNorm family, eps 1e-12. stats = [rows, 2] (mean, rstd).
 void ln_stats(hipStream_t s, const float* x, float* stats, int64_t rows, int64_t h);
 void layer_norm(hipStream_t s, const float* x, const float* gamma, const float* beta, float* y, float* stats,
                 int64_t rows, int64_t h);
-void ln_grad_x(hipStream_t s, const float* x, const float* gamma, const float* g, const float* stats, float* dx,
-               int64_t rows, int64_t h);
 // LayerNorm backward in one pass: dx when non-null, and when `partial` is non-null the per-block
 // partial sums [ln_backward_blocks, 2 h] of g * xhat (gamma gradient) then g (beta gradient), to be
 // added by column_finalize. gamma may be null when dx is.

@@ -415,89 +415,37 @@ void add_rows(hipStream_t s, const float* x, const float* b, float* o, int64_t r
   hipLaunchKernelGGL(k_add_rows, dim3(std::min<unsigned>(blocks_for(n, 256), 8192)), dim3(256), 0, s, x, b, o, n, h);
 }
 
-int64_t column_chunks(int64_t rows, int64_t h) {
-  int64_t tiles = (h + 63) / 64;
-  int64_t chunks = (rows + 31) / 32;                  // at least 32 rows a block
-  int64_t want = std::max<int64_t>(1, 512 / tiles);   // about 512 blocks in flight
-  return std::max<int64_t>(1, std::min(chunks, want));
-}
-
-// Column sums of x (or of g * xhat with LayerNorm statistics: LayerNormGradGamma). A block sums
-// 64 columns over a chunk of rows, its four waves interleaving rows; the chunk's partial goes to
-// `partial`, and the last block of a column tile to finish (counted by an integer atomic, reset by
-// that block for the next launch) adds the chunks' partials in ascending chunk order.
-__global__ __launch_bounds__(256) void k_column_sum(const float* __restrict__ x, const float* __restrict__ g,
-                                                    const float* __restrict__ stats, float* __restrict__ partial,
-                                                    float* __restrict__ out, unsigned* __restrict__ counter,
-                                                    int64_t rows, int64_t h, int64_t rows_per, int chunks) {
-  __shared__ float red[4][64];
-  __shared__ int last;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t c = int64_t(blockIdx.x) * 64 + lane;
-  const int64_t r0 = int64_t(blockIdx.y) * rows_per, r1 = std::min(rows, r0 + rows_per);
-  float acc = 0.0f;
-  if (c < h) {
-    if (stats) {
-#pragma unroll 4
-      for (int64_t r = r0 + wave; r < r1; r += 4) acc += g[r * h + c] * ((x[r * h + c] - stats[2 * r]) * stats[2 * r + 1]);
-    } else {
-#pragma unroll 4
-      for (int64_t r = r0 + wave; r < r1; r += 4) acc += x[r * h + c];
-    }
-  }
-  red[wave][lane] = acc;
-  __syncthreads();
-  if (wave == 0 && c < h) partial[int64_t(blockIdx.y) * h + c] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last = atomicAdd(&counter[blockIdx.x], 1u) == unsigned(chunks - 1);
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  // Released by the other blocks' fences; never read here before, so plain loads see them. Wave
-  // w adds the chunks z = w mod 4 in ascending order with up to 16 loads in flight; the four wave
-  // sums are added in wave order.
+// Partial column sums: block (x, y) adds columns 256 x + t over the rows of chunk y, eight rows in
+// flight a thread, into partial[y, c]; column_finalize adds the chunks.
+__global__ __launch_bounds__(256) void k_column_partial(const float* __restrict__ x, float* __restrict__ partial,
+                                                        int64_t rows, int64_t h, int64_t rows_per) {
+  const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t r0 = int64_t(blockIdx.y) * rows_per, r1 = std::min<int64_t>(rows, r0 + rows_per);
+  if (c >= h) return;
   float s = 0.0f;
-  if (c < h) {
-    for (int z0 = wave; z0 < chunks; z0 += 64) {
-      float t[16];
+  for (int64_t r = r0; r < r1; r += 8) {
+    float t[8];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int z = z0 + 4 * u;
-        t[u] = z < chunks ? partial[int64_t(z) * h + c] : 0.0f;
-      }
+    for (int u = 0; u < 8; ++u) t[u] = x[(r + u < r1 ? r + u : r1 - 1) * h + c];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) s += t[u];
-    }
+    for (int u = 0; u < 8; ++u)
+      if (r + u < r1) s += t[u];
   }
-  __syncthreads();
-  red[wave][lane] = s;
-  __syncthreads();
-  if (wave == 0 && c < h) out[c] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
-  if (threadIdx.x == 0) counter[blockIdx.x] = 0u;
+  partial[int64_t(blockIdx.y) * h + c] = s;
 }
-static void column_reduce(hipStream_t s, const float* x, const float* g, const float* stats, float* out, int64_t rows,
-                          int64_t h, float* partial, int64_t partial_floats) {
-  if (h <= 0) return;
-  if (rows <= 0) { fill_zero(s, out, h * 4); return; }
-  int64_t chunks = column_chunks(rows, h);
-  int64_t per = (rows + chunks - 1) / chunks;
-  chunks = (rows + per - 1) / per;
-  int64_t tiles = (h + 63) / 64;
-  // The partial buffer holds chunks * h floats, then one counter per column tile.
-  if (partial_floats < chunks * h + tiles) bad("column reduction partial buffer too small");
-  unsigned* counter = reinterpret_cast<unsigned*>(partial + chunks * h);
-  hipLaunchKernelGGL(k_column_sum, dim3(unsigned(tiles), unsigned(chunks)), dim3(256), 0, s, x, g, stats, partial, out,
-                     counter, rows, h, per, int(chunks));
+int64_t column_partial_chunks(int64_t rows, int64_t h) {
+  const int64_t tiles = (h + 255) / 256;
+  const int64_t want = std::max<int64_t>(1, 512 / tiles);  // about 512 blocks
+  return std::max<int64_t>(1, std::min<int64_t>(want, (rows + 15) / 16));
 }
-void column_sum(hipStream_t s, const float* x, float* out, int64_t rows, int64_t h, float* partial, int64_t pf) {
-  column_reduce(s, x, nullptr, nullptr, out, rows, h, partial, pf);
+void column_partial(hipStream_t s, const float* x, float* partial, int64_t rows, int64_t h) {
+  if (rows <= 0 || h <= 0) return;
+  const int64_t chunks = column_partial_chunks(rows, h);
+  const int64_t per = (rows + chunks - 1) / chunks;
+  if ((rows + per - 1) / per != chunks) bad("column partial chunking");
+  hipLaunchKernelGGL(k_column_partial, dim3(unsigned((h + 255) / 256), unsigned(chunks)), dim3(256), 0, s, x, partial,
+                     rows, h, per);
 }
-void ln_grad_gamma(hipStream_t s, const float* x, const float* g, const float* stats, float* out, int64_t rows,
-                   int64_t h, float* partial, int64_t pf) {
-  column_reduce(s, x, g, stats, out, rows, h, partial, pf);
-}
-int64_t column_workspace(int64_t rows, int64_t h) { return column_chunks(rows, h) * h + (h + 63) / 64 + 64; }
 
 // ---------------------------------------------------------------------------------------------
 // LayerNorm family: one wave per row, four rows per block.
@@ -540,35 +488,6 @@ void layer_norm(hipStream_t s, const float* x, const float* gamma, const float* 
                 int64_t rows, int64_t h) {
   if (rows <= 0) return;
   hipLaunchKernelGGL(k_layer_norm, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, gamma, beta, y, stats, rows, h);
-}
-
-__global__ void k_ln_grad_x(const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ g,
-                            const float* __restrict__ stats, float* __restrict__ dx, int64_t rows, int64_t h) {
-  int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  int lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  const float mean = stats[2 * row], rstd = stats[2 * row + 1];
-  const float* xr = x + row * h;
-  const float* gr = g + row * h;
-  float s1 = 0.0f, s2 = 0.0f;
-  for (int64_t c = lane; c < h; c += 64) {
-    float gx = gr[c] * gamma[c];
-    float xhat = (xr[c] - mean) * rstd;
-    s1 += gx;
-    s2 = __builtin_fmaf(gx, xhat, s2);
-  }
-  const float width = float(h);
-  const float mean_gx = wave_sum(s1) / width, mean_gx_xhat = wave_sum(s2) / width;
-  for (int64_t c = lane; c < h; c += 64) {
-    float gx = gr[c] * gamma[c];
-    float xhat = (xr[c] - mean) * rstd;
-    dx[row * h + c] = rstd * ((gx - mean_gx) - xhat * mean_gx_xhat);
-  }
-}
-void ln_grad_x(hipStream_t s, const float* x, const float* gamma, const float* g, const float* stats, float* dx,
-               int64_t rows, int64_t h) {
-  if (rows <= 0) return;
-  hipLaunchKernelGGL(k_ln_grad_x, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, gamma, g, stats, dx, rows, h);
 }
 
 // The LayerNorm backward of one input in one pass: dx (LayerNormGradX) and, per block of rows, the
@@ -717,13 +636,14 @@ void embedding(hipStream_t s, const float* table, const int32_t* ids, float* o, 
 }
 
 // EmbeddingGrad in one launch, deterministic, with no float atomics, optionally added to `addend`
-// (out = addend + EmbeddingGrad, elementwise). Block b first writes the rows of its stripe of the
-// table that no id names (zero, or the addend's row + 0), then, when position b is the first occurrence of
-// its id, collects that id's positions in ascending k (wave ballots over the ids, staged in LDS)
-// and adds the rows g[k] in that order from +0, one f32 rounding per add: the reference's order
+// (out = addend + EmbeddingGrad, elementwise). Blocks [0, n) take a position each: the block of an
+// id's first position collects the id's positions in ascending k (wave ballots over the ids) and
+// adds the rows g[k] in that order from +0, one f32 rounding per add: the reference's order
 // (interpreter.rs:931-941), bit for bit. The rows come through LDS a chunk of `ch` at a time, with
-// kDepth chunks' loads in flight in registers ahead of the adds.
+// kDepth chunks' loads in flight in registers ahead of the adds. Blocks from n on write the rows
+// of their stripe of the table that no id names.
 constexpr int kEgThreads = 256, kDepth = 4, kEgVec = 4;  // float4 loads a thread per chunk
+constexpr int kEgIds = 16;                                // ids a thread a round
 
 // One chunk of rows in registers: kEgVec float4 a thread.
 struct EgChunk { float4 v[kEgVec]; };
@@ -771,60 +691,102 @@ __global__ __launch_bounds__(kEgThreads) void k_embedding_grad(const int32_t* __
                                                                int n, int64_t rows, int64_t h, int64_t stripe, int ch,
                                                                bool vec) {
   extern __shared__ int32_t eg_lds[];
-  int32_t* sid = eg_lds;                                      // [n] the ids
-  int32_t* list = sid + n;                                    // [n] this block's positions
+  int32_t* list = eg_lds;                                     // [n] the positions of this block's id
   float* stage = reinterpret_cast<float*>(list + n);          // [ch * h]
   __shared__ uint32_t mask;
-  __shared__ int wave_cnt[kEgThreads / 64];
+  __shared__ int cnt[kEgIds][kEgThreads / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t b = blockIdx.x;
-  for (int j0 = 0; j0 < n; j0 += kEgThreads * 8) {
-    int32_t t[8];
+  if (int64_t(blockIdx.x) >= n) {
+    // A stripe block: the rows of its stripe (at most 32) that no id names are zero, or the
+    // addend's row + 0.
+    const int64_t z0 = (int64_t(blockIdx.x) - n) * stripe, z1 = std::min<int64_t>(rows, z0 + stripe);
+    if (tid == 0) mask = 0;
+    __syncthreads();
+    for (int base = 0; base < n; base += kEgThreads * kEgIds) {
+      int32_t t[kEgIds];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int j = j0 + tid + u * kEgThreads;
-      t[u] = ids[j < n ? j : n - 1];
-    }
+      for (int u = 0; u < kEgIds; ++u) {
+        const int j = base + tid + u * kEgThreads;
+        t[u] = ids[j < n ? j : n - 1];
+      }
+      uint32_t bits = 0;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int j = j0 + tid + u * kEgThreads;
-      if (j < n) sid[j] = t[u];
-    }
-  }
-  if (tid == 0) mask = 0;
-  __syncthreads();
-  // The stripe (at most 32 rows): rows no id names are zero.
-  const int64_t z0 = b * stripe, z1 = std::min<int64_t>(rows, z0 + stripe);
-  if (z0 < z1) {
-    for (int j = tid; j < n; j += kEgThreads) {
-      const int64_t id = sid[j];
-      if (id >= z0 && id < z1) atomicOr(&mask, 1u << uint32_t(id - z0));
+      for (int u = 0; u < kEgIds; ++u) bits |= (t[u] >= z0 && t[u] < z1) ? 1u << uint32_t(t[u] - z0) : 0u;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) bits |= __shfl_xor(bits, d, 64);
+      if (lane == 0 && bits) atomicOr(&mask, bits);
     }
     __syncthreads();
     const uint32_t m = mask;
-    for (int64_t r = z0; r < z1; ++r)
-      if (!((m >> uint32_t(r - z0)) & 1u))
-        for (int64_t c = tid; c < h; c += kEgThreads) out[r * h + c] = addend ? addend[r * h + c] + 0.0f : 0.0f;
-  }
-  if (b >= n) return;
-  const int32_t id = sid[b];
-  if (id < 0 || int64_t(id) >= rows) return;
-  int dup = 0;
-  for (int j = tid; j < int(b); j += kEgThreads) dup |= sid[j] == id ? 1 : 0;
-  if (__syncthreads_or(dup)) return;
-  // The positions of `id`, ascending.
-  int total = 0;
-  for (int j0 = int(b); j0 < n; j0 += kEgThreads) {
-    const int j = j0 + tid;
-    const bool hit = j < n && sid[j] == id;
-    const uint64_t bal = __ballot(hit);
-    if (lane == 0) wave_cnt[wave] = __popcll(bal);
-    __syncthreads();
-    int off = total;
-    for (int w = 0; w < wave; ++w) off += wave_cnt[w];
-    if (hit) list[off + __popcll(bal & ((uint64_t(1) << lane) - 1))] = j;
+    if (vec) {
+      // float4 cells of the stripe, four a thread in flight.
+      const int h4 = int(h >> 2), cells = int(z1 - z0) * h4;
+      float4* o4 = reinterpret_cast<float4*>(out + z0 * h);
+      const float4* a4 = addend ? reinterpret_cast<const float4*>(addend + z0 * h) : nullptr;
+      for (int e0 = tid; e0 < cells; e0 += kEgThreads * 4) {
+        float4 v[4];
 #pragma unroll
-    for (int w = 0; w < kEgThreads / 64; ++w) total += wave_cnt[w];
+        for (int u = 0; u < 4; ++u) {
+          const int e = e0 + u * kEgThreads;
+          v[u] = a4 ? a4[e < cells ? e : cells - 1] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = e0 + u * kEgThreads;
+          if (e < cells && !((m >> uint32_t(e / h4)) & 1u))
+            o4[e] = make_float4(v[u].x + 0.0f, v[u].y + 0.0f, v[u].z + 0.0f, v[u].w + 0.0f);
+        }
+      }
+    } else {
+      const int64_t cells = (z1 - z0) * h;
+      for (int64_t e = tid; e < cells; e += kEgThreads) {
+        const int64_t r = z0 + e / h;
+        if (!((m >> uint32_t(r - z0)) & 1u)) out[z0 * h + e] = addend ? addend[z0 * h + e] + 0.0f : 0.0f;
+      }
+    }
+    return;
+  }
+  const int b = int(blockIdx.x);
+  const int32_t id = ids[b];
+  if (id < 0 || int64_t(id) >= rows) return;
+  // One pass over the ids, kEgIds a thread a round with all loads in flight: an earlier position
+  // holding the id ends the block (only the first position goes on), and ballots in position order
+  // collect the positions k >= b holding it.
+  int total = 0;
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  for (int base = 0; base < n; base += kEgThreads * kEgIds) {
+    int32_t t[kEgIds];
+#pragma unroll
+    for (int u = 0; u < kEgIds; ++u) {
+      const int j = base + tid + u * kEgThreads;
+      t[u] = ids[j < n ? j : n - 1];
+    }
+    int dup = 0;
+#pragma unroll
+    for (int u = 0; u < kEgIds; ++u) {
+      const int j = base + tid + u * kEgThreads;
+      dup |= (j < b && t[u] == id) ? 1 : 0;
+    }
+    if (__syncthreads_or(dup)) return;
+    if (base + kEgThreads * kEgIds <= b) continue;
+#pragma unroll
+    for (int u = 0; u < kEgIds; ++u) {
+      const int j = base + tid + u * kEgThreads;
+      const uint64_t bal = __ballot(j < n && j >= b && t[u] == id);
+      if (lane == 0) cnt[u][wave] = __popcll(bal);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kEgIds; ++u) {
+      const int j = base + tid + u * kEgThreads;
+      const bool hit = j < n && j >= b && t[u] == id;
+      const uint64_t bal = __ballot(hit);
+      int off = total;
+      for (int w = 0; w < wave; ++w) off += cnt[u][w];
+      if (hit) list[off + __popcll(bal & below)] = j;
+#pragma unroll
+      for (int w = 0; w < kEgThreads / 64; ++w) total += cnt[u][w];
+    }
     __syncthreads();
   }
   // Thread tid adds columns tid, tid + 256, tid + 512, tid + 768 (h <= 1024).
@@ -872,13 +834,14 @@ void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* ou
   if (h > 1024) bad("embedding gradient rows wider than 1024");
   if (rows <= 0 || h <= 0) return;
   if (n <= 0 && !addend) { fill_zero(s, out, rows * h * 4); return; }
-  const int64_t blocks = std::max<int64_t>(n, (rows + 31) / 32);
+  const int64_t stripes = (rows + 31) / 32, stripe = (rows + stripes - 1) / stripes;  // stripe <= 32 rows
+  const int64_t blocks = std::max<int64_t>(n, 0) + stripes;
   if (blocks > 2147483647) bad("embedding gradient table too large");
-  const int64_t stripe = (rows + blocks - 1) / blocks;  // <= 32
-  const bool vec = h % 4 == 0 && reinterpret_cast<uintptr_t>(g) % 16 == 0;
+  auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  const bool vec = h % 4 == 0 && a16(g) && a16(out) && a16(addend);
   // A chunk fills the float4 registers of every thread (vec) or 4096 floats.
   const int ch = int(vec ? std::max<int64_t>(1, int64_t(kEgThreads) * kEgVec / (h / 4)) : std::max<int64_t>(1, 4096 / h));
-  const size_t lds = size_t(2 * n) * 4 + size_t(ch) * size_t(h) * 4;
+  const size_t lds = size_t(n) * 4 + size_t(ch) * size_t(h) * 4;
   hipLaunchKernelGGL(k_embedding_grad, dim3(unsigned(blocks)), dim3(kEgThreads), lds, s, ids, g, addend, out, int(n),
                      rows, h, stripe, ch, vec);
 }

@@ -534,9 +534,22 @@ void Executor::build() {
         if (ln_member.count(id)) goto layer_norm_backward;
         uint32_t a = o[0];
         int64_t rows = shape(a)[0], h = shape(a)[1];
-        int64_t pf = hk::column_workspace(rows, h);
-        void* part = R(size_t(pf) * 4);
-        push([=](hipStream_t s) { hk::column_sum(s, F(a), F(id), rows, h, static_cast<float*>(A(part)), pf); });
+        if (rows == 0) {
+          push([=](hipStream_t s) { hk::fill_zero(s, F(id), h * 4); });
+          break;
+        }
+        const int64_t chunks = hk::column_partial_chunks(rows, h);
+        void* part = R(size_t(chunks * h) * 4);
+        push([=](hipStream_t s) { hk::column_partial(s, F(a), static_cast<float*>(A(part)), rows, h); });
+        DeferredJob d{part, 0, int64_t(id), -1, int32_t(chunks), int32_t(h), int32_t(h)};
+        if (only_optimizer_reads(int64_t(id))) {
+          deferred.push_back(d);
+        } else {
+          push([=](hipStream_t s) {
+            hk::ColumnJob j{static_cast<float*>(A(d.tok)), F(uint32_t(d.lo)), nullptr, d.chunks, d.width, d.split, 0};
+            hk::column_finalize(s, &j, 1);
+          });
+        }
         break;
       }
       case Op::LayerNorm: case Op::LayerNormGradX: case Op::LayerNormGradGamma: {
