@@ -20,6 +20,7 @@ SOURCES = [
     "host/runner.cpp",
     "hip/runtime.cpp",
     "hip/kernels.hip",
+    "hip/gemm.hip",
     "hip/attention.hip",
 ]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

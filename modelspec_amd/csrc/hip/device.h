@@ -1,0 +1,58 @@
+// Device helpers shared by the kernel sources of the training step (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace msx::hk {
+
+namespace {
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+[[noreturn]] void bad(const std::string& what) { throw std::runtime_error("kernel launch refused: " + what); }
+
+inline unsigned blocks_for(int64_t n, int per) { return unsigned((n + per - 1) / per); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// The GELU of interpreter.rs:1539-1587 in device arithmetic: the nearest f32 constants, the same
+// operation order, the device expf.
+__device__ __forceinline__ float d_gelu_twice_inner(float x) {
+  const float scale = 0.797884560802865f, cubic = 0.044715f;
+  return 2.0f * scale * (x + cubic * x * x * x);
+}
+__device__ __forceinline__ float d_logistic(float v) { return 1.0f / (1.0f + expf(0.0f - v)); }
+__device__ __forceinline__ float d_gelu(float x) { return x * d_logistic(d_gelu_twice_inner(x)); }
+__device__ __forceinline__ float d_gelu_grad(float x, float g) {
+  const float scale = 0.797884560802865f, cubic = 0.044715f;
+  float v = d_gelu_twice_inner(x);
+  float s = d_logistic(v), r = d_logistic(0.0f - v);
+  float slope = scale * (1.0f + 3.0f * cubic * x * x);
+  return (s + 2.0f * (s * x) * r * slope) * g;
+}
+
+// Philox4x32-10 word 0 (train/init.rs:91-109), on the device for the dropout masks.
+__device__ __forceinline__ uint32_t philox_w0(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
+                                              uint32_t k1) {
+  const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+  for (int round = 0; round < 10; ++round) {
+    if (round > 0) { k0 += W0; k1 += W1; }
+    uint32_t hi0 = __umulhi(M0, c0), lo0 = M0 * c0, hi1 = __umulhi(M1, c2), lo1 = M1 * c2;
+    uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+  }
+  return c0;
+}
+}  // namespace
+
+}  // namespace msx::hk

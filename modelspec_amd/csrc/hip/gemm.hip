@@ -1,0 +1,448 @@
+// GEMM kernels of the training step on the gfx950 f32 MFMA (v_mfma_f32_16x16x4f32), with bias,
+// column-sum and split-K epilogues, and the shape-based choice of tile and split.
+#include "kernels.h"
+#include "device.h"
+
+#include <algorithm>
+
+namespace msx::hk {
+
+// ---------------------------------------------------------------------------------------------
+// GEMM on the f32 MFMA: a 64x64 output tile per 256-thread block, each wave a 32x32 quarter as
+// 2x2 MFMA 16x16x4 tiles. K advances 32 at a time through double-buffered LDS; the next K tile's
+// global loads (float4 where the operand's layout allows) are in flight while the MFMAs of the
+// current one run. Operands may be read transposed in place. Under split-K every slice writes its
+// partial tile to the workspace and k_splitk_sum adds the slices in ascending order, with every
+// slice's load in flight at once: deterministic.
+namespace {
+constexpr int BM = 64, BN = 64, BK = 32, LDP = 68;  // LDS row stride (floats)
+
+// Loads of one K tile of an operand into registers, branch-free: out-of-range elements read a
+// clamped in-range address and are zeroed by a select, so no load waits on another. The (r, k)
+// element is A[r * lda + k], or A[k * lda + r] when T; thread t takes the float4 groups t and
+// t + 256 of the tile along the operand's contiguous dimension. V: the groups are 16-byte aligned
+// and the contiguous extent is a multiple of 4, so a group is wholly in or out of range.
+template <bool T, bool V>
+__device__ __forceinline__ void load_tile(const float* __restrict__ A, int64_t lda, int64_t rows, int64_t kend,
+                                          int64_t r0, int64_t k0, int tid, float (&reg)[8]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = tid + h * 256;
+    int r, k;
+    if (!T) { r = e >> 3; k = (e & 7) * 4; } else { k = e >> 4; r = (e & 15) * 4; }
+    const int64_t gr = r0 + r, gk = k0 + k;
+    if (V) {
+      const bool ok = !T ? (gr < rows && gk < kend) : (gk < kend && gr < rows);
+      const int64_t cr = gr < rows ? gr : rows - 1;
+      const int64_t ck = gk < kend ? gk : kend - 4;
+      const int64_t crr = !T ? cr : (gr < rows ? gr : rows - 4);
+      const int64_t ckk = !T ? ck : (gk < kend ? gk : kend - 1);
+      const float4 f = *reinterpret_cast<const float4*>(!T ? A + crr * lda + ckk : A + ckk * lda + crr);
+      reg[4 * h] = ok ? f.x : 0.0f;
+      reg[4 * h + 1] = ok ? f.y : 0.0f;
+      reg[4 * h + 2] = ok ? f.z : 0.0f;
+      reg[4 * h + 3] = ok ? f.w : 0.0f;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t rr = !T ? gr : gr + j, kk = !T ? gk + j : gk;
+        const bool ok = rr < rows && kk < kend;
+        const int64_t cr = rr < rows ? rr : rows - 1, ck = kk < kend ? kk : kend - 1;
+        const float x = !T ? A[cr * lda + ck] : A[ck * lda + cr];
+        reg[4 * h + j] = ok ? x : 0.0f;
+      }
+    }
+  }
+}
+
+// Stores a K tile into LDS as S[k][r].
+template <bool T>
+__device__ __forceinline__ void store_tile(float* S, int tid, const float (&reg)[8]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = tid + h * 256;
+    if (!T) {
+      const int r = e >> 3, k = (e & 7) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) S[(k + j) * LDP + r] = reg[4 * h + j];
+    } else {
+      const int k = e >> 4, r = (e & 15) * 4;
+      *reinterpret_cast<float4*>(S + k * LDP + r) = make_float4(reg[4 * h], reg[4 * h + 1], reg[4 * h + 2], reg[4 * h + 3]);
+    }
+  }
+}
+}  // namespace
+
+template <bool TA, bool TB, bool VA, bool VB>
+__global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
+                                              float* __restrict__ C, const float* __restrict__ bias, int64_t M,
+                                              int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                                              int64_t kchunk, float* __restrict__ ws, float* __restrict__ colsum,
+                                              bool sum_a) {
+  __shared__ float As[2][BK * LDP];
+  __shared__ float Bs[2][BK * LDP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t m0 = int64_t(blockIdx.y) * BM, n0 = int64_t(blockIdx.x) * BN;
+  const int64_t kbeg = int64_t(blockIdx.z) * kchunk;
+  const int64_t kend = K < kbeg + kchunk ? K : kbeg + kchunk;
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+  v4f acc00 = {0, 0, 0, 0}, acc01 = acc00, acc10 = acc00, acc11 = acc00;
+  float ra[8], rb[8];
+  // Column sums of op(B) over K (or, with sum_a, row sums of op(A)): a bias gradient beside its
+  // weight gradient, taken from the LDS tiles by the first row (column) of blocks: thread t adds
+  // tile column t mod 64 over K rows 8 (t / 64) .. + 8 of each K tile.
+  const bool sums = colsum != nullptr && (sum_a ? blockIdx.x == 0 : blockIdx.y == 0);
+  float csum = 0.0f;
+  // B's (k, j) element is B[k * ldb + j], or B[j * ldb + k] when TB: the same loader with the
+  // roles of "row" and "contiguous" swapped.
+  load_tile<TA, VA>(A, lda, M, kend, m0, kbeg, tid, ra);
+  load_tile<!TB, VB>(B, ldb, N, kend, n0, kbeg, tid, rb);
+  int buf = 0;
+  for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
+    store_tile<TA>(As[buf], tid, ra);
+    store_tile<!TB>(Bs[buf], tid, rb);
+    __syncthreads();
+    if (k0 + BK < kend) {
+      load_tile<TA, VA>(A, lda, M, kend, m0, k0 + BK, tid, ra);
+      load_tile<!TB, VB>(B, ldb, N, kend, n0, k0 + BK, tid, rb);
+    }
+    const float* as = As[buf];
+    const float* bs = Bs[buf];
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 4) {
+      const int kr = (kk + (lane >> 4)) * LDP, c = lane & 15;
+      const float a0 = as[kr + wm + c], a1 = as[kr + wm + 16 + c];
+      const float b0 = bs[kr + wn + c], b1 = bs[kr + wn + 16 + c];
+      acc00 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc00, 0, 0, 0);
+      acc01 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc01, 0, 0, 0);
+      acc10 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc10, 0, 0, 0);
+      acc11 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc11, 0, 0, 0);
+    }
+    if (sums) {
+      const int c = tid & 63, kg = (tid >> 6) * 8;
+      const float* ss = sum_a ? as : bs;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) csum += ss[(kg + j) * LDP + c];
+    }
+    buf ^= 1;
+  }
+  if (sums) {
+    __syncthreads();
+    float* red = As[0];
+    red[tid] = csum;
+    __syncthreads();
+    const int64_t base = sum_a ? m0 : n0, width = sum_a ? M : N;
+    if (tid < 64 && base + tid < width) {
+      const float v = ((red[tid] + red[64 + tid]) + red[128 + tid]) + red[192 + tid];
+      colsum[(ws ? int64_t(blockIdx.z) * width : 0) + base + tid] = v;
+    }
+  }
+  const v4f* accs[4] = {&acc00, &acc01, &acc10, &acc11};
+  if (!ws) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int64_t col = n0 + wn + (t & 1) * 16 + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = m0 + wm + (t >> 1) * 16 + 4 * (lane >> 4) + r;
+        if (row < M && col < N) C[row * ldc + col] = bias ? (*accs[t])[r] + bias[col] : (*accs[t])[r];
+      }
+    }
+    return;
+  }
+  // Split-K: this slice's partial product, [M, N] row-major at slice z; the slices are added in
+  // order by k_splitk_sum or a deferred column_finalize job.
+  float* part = ws + int64_t(blockIdx.z) * M * N;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int64_t col = n0 + wn + (t & 1) * 16 + (lane & 15);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t row = m0 + wm + (t >> 1) * 16 + 4 * (lane >> 4) + r;
+      if (row < M && col < N) part[row * N + col] = (*accs[t])[r];
+    }
+  }
+}
+
+// Sums the split-K partial products in ascending slice order, one output element a thread, every
+// slice's load issued before the adds; the threads past M * N do the same for the slices' column
+// (row) sums.
+template <int SPLIT>
+__global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ ws, float* __restrict__ C,
+                                                    const float* __restrict__ bias, int64_t M, int64_t N, int64_t ldc,
+                                                    int splits, float* __restrict__ colsum, int64_t width) {
+  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t mn = M * N;
+  const bool cs = e >= mn;
+  if (cs && (!colsum || e - mn >= width)) return;
+  const float* src = cs ? ws + int64_t(splits) * mn + (e - mn) : ws + e;
+  const int64_t stride = cs ? width : mn;
+  // SPLIT slices' loads in flight at a time, added in slice order.
+  float s = 0.0f;
+  for (int z0 = 0; z0 < splits; z0 += SPLIT) {
+    float t[SPLIT];
+#pragma unroll
+    for (int u = 0; u < SPLIT; ++u) t[u] = src[int64_t(z0 + u < splits ? z0 + u : splits - 1) * stride];
+#pragma unroll
+    for (int u = 0; u < SPLIT; ++u)
+      if (z0 + u < splits) s = (z0 + u == 0) ? t[u] : s + t[u];
+  }
+  if (cs) {
+    colsum[e - mn] = s;
+  } else {
+    const int64_t row = e / N, col = e - row * N;
+    C[row * ldc + col] = bias ? s + bias[col] : s;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// The wide-tile GEMM for float4-aligned operands: a block of 2 x 2 waves, each wave a
+// (16 WM) x (16 WN) tile as WM x WN MFMA 16x16x4 accumulators, K advancing WK at a time through
+// double-buffered LDS whose row strides (tile width + 16 floats) keep the fragment reads of a
+// wave's two half-groups in disjoint banks. Epilogues as in k_gemm: bias, split-K partials,
+// column (row) sums from the LDS tiles.
+namespace {
+// One float4 group e of a K tile: the (row, k) element of a KC operand is P[row * ld + k] (four
+// consecutive k), else P[k * ld + row] (four consecutive rows). Out-of-range groups read a
+// clamped address and are zeroed, branch-free.
+template <bool KC, int R, int WK>
+__device__ __forceinline__ float4 wide_load(const float* __restrict__ P, int64_t ld, int64_t rows, int64_t kend,
+                                            int64_t r0, int64_t k0, int e) {
+  int r, k;
+  if (KC) { r = e / (WK / 4); k = (e % (WK / 4)) * 4; } else { k = e / (R / 4); r = (e % (R / 4)) * 4; }
+  const int64_t gr = r0 + r, gk = k0 + k;
+  const bool ok = gr < rows && gk < kend;
+  const int64_t cr = KC ? (gr < rows ? gr : rows - 1) : (gr < rows ? gr : rows - 4);
+  const int64_t ck = KC ? (gk < kend ? gk : kend - 4) : (gk < kend ? gk : kend - 1);
+  const float4 f = *reinterpret_cast<const float4*>(KC ? P + cr * ld + ck : P + ck * ld + cr);
+  return ok ? f : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+template <bool KC, int R, int L, int WK>
+__device__ __forceinline__ void wide_store(float* S, int e, float4 v) {
+  if (KC) {
+    const int r = e / (WK / 4), k = (e % (WK / 4)) * 4;
+    S[(k + 0) * L + r] = v.x;
+    S[(k + 1) * L + r] = v.y;
+    S[(k + 2) * L + r] = v.z;
+    S[(k + 3) * L + r] = v.w;
+  } else {
+    const int k = e / (R / 4), r = (e % (R / 4)) * 4;
+    *reinterpret_cast<float4*>(S + k * L + r) = v;
+  }
+}
+}  // namespace
+
+template <bool TA, bool TB, int WM, int WN, int WK>
+__global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, const float* __restrict__ B,
+                                                float* __restrict__ C, const float* __restrict__ bias, int64_t M,
+                                                int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                                                int64_t kchunk, float* __restrict__ ws, float* __restrict__ colsum,
+                                                bool sum_a) {
+  constexpr int TM = 32 * WM, TN = 32 * WN, LA = TM + 16, LB = TN + 16;
+  constexpr int GA = TM * WK / 4, GB = TN * WK / 4;              // float4 groups a K tile
+  constexpr int HA = (GA + 255) / 256, HB = (GB + 255) / 256;     // a thread's groups
+  __shared__ float As[2][WK * LA];
+  __shared__ float Bs[2][WK * LB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t m0 = int64_t(blockIdx.y) * TM, n0 = int64_t(blockIdx.x) * TN;
+  const int64_t kbeg = int64_t(blockIdx.z) * kchunk;
+  const int64_t kend = K < kbeg + kchunk ? K : kbeg + kchunk;
+  const int wm = (wave >> 1) * 16 * WM, wn = (wave & 1) * 16 * WN;
+  v4f acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  // op(A) is KC (contiguous along k) unless TA; op(B)^T is KC when TB.
+  float4 ra[HA], rb[HB];
+#pragma unroll
+  for (int h = 0; h < HA; ++h)
+    if (tid + 256 * h < GA) ra[h] = wide_load<!TA, TM, WK>(A, lda, M, kend, m0, kbeg, tid + 256 * h);
+#pragma unroll
+  for (int h = 0; h < HB; ++h)
+    if (tid + 256 * h < GB) rb[h] = wide_load<TB, TN, WK>(B, ldb, N, kend, n0, kbeg, tid + 256 * h);
+  // Column sums: thread t adds tile column t mod T over the K rows (t / T) per .. + per of each
+  // K tile, per = WK / (256 / T).
+  const int T = sum_a ? TM : TN;
+  const bool sums = colsum != nullptr && (sum_a ? blockIdx.x == 0 : blockIdx.y == 0);
+  const int sum_per = WK / (256 / T), sum_ld = sum_a ? LA : LB;
+  const int sum_off = (tid / T) * sum_per * sum_ld + tid % T;
+  float csum = 0.0f;
+  int buf = 0;
+  for (int64_t k0 = kbeg; k0 < kend; k0 += WK) {
+#pragma unroll
+    for (int h = 0; h < HA; ++h)
+      if (tid + 256 * h < GA) wide_store<!TA, TM, LA, WK>(As[buf], tid + 256 * h, ra[h]);
+#pragma unroll
+    for (int h = 0; h < HB; ++h)
+      if (tid + 256 * h < GB) wide_store<TB, TN, LB, WK>(Bs[buf], tid + 256 * h, rb[h]);
+    __syncthreads();
+    if (k0 + WK < kend) {
+#pragma unroll
+      for (int h = 0; h < HA; ++h)
+        if (tid + 256 * h < GA) ra[h] = wide_load<!TA, TM, WK>(A, lda, M, kend, m0, k0 + WK, tid + 256 * h);
+#pragma unroll
+      for (int h = 0; h < HB; ++h)
+        if (tid + 256 * h < GB) rb[h] = wide_load<TB, TN, WK>(B, ldb, N, kend, n0, k0 + WK, tid + 256 * h);
+    }
+    const float* as = As[buf];
+    const float* bs = Bs[buf];
+#pragma unroll
+    for (int kk = 0; kk < WK; kk += 4) {
+      const int ka = (kk + (lane >> 4)) * LA + wm + (lane & 15), kb = (kk + (lane >> 4)) * LB + wn + (lane & 15);
+      float a[WM], b[WN];
+#pragma unroll
+      for (int i = 0; i < WM; ++i) a[i] = as[ka + 16 * i];
+#pragma unroll
+      for (int j = 0; j < WN; ++j) b[j] = bs[kb + 16 * j];
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (sums) {
+      const float* ss = (sum_a ? as : bs) + sum_off;
+      for (int j = 0; j < sum_per; ++j) csum += ss[j * sum_ld];
+    }
+    buf ^= 1;
+  }
+  if (sums) {
+    __syncthreads();
+    float* red = As[0];
+    red[tid] = csum;
+    __syncthreads();
+    const int64_t base = sum_a ? m0 : n0, width = sum_a ? M : N;
+    if (tid < T && base + tid < width) {
+      float v = red[tid];
+      for (int g = 1; g < 256 / T; ++g) v += red[g * T + tid];
+      colsum[(ws ? int64_t(blockIdx.z) * width : 0) + base + tid] = v;
+    }
+  }
+  float* out = ws ? ws + int64_t(blockIdx.z) * M * N : C;
+  const int64_t ldo = ws ? N : ldc;
+  const float* bz = ws ? nullptr : bias;
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int64_t col = n0 + wn + 16 * j + (lane & 15);
+      const float bv = bz && col < N ? bz[col] : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = m0 + wm + 16 * i + 4 * (lane >> 4) + r;
+        if (row < M && col < N) out[row * ldo + col] = bz ? acc[i][j][r] + bv : acc[i][j][r];
+      }
+    }
+  }
+}
+
+namespace {
+// The tile shape and split-K of a GEMM, from measured MI355X timings of the step's shapes: large
+// outputs (and very deep K) take 64 x 64 tiles, outputs up to 2^19 elements 32 x 32, the rest
+// 32 x 64. Split-K, whose slice sum costs a launch unless deferred to a batched finalize, is used
+// when deferred or when K is deep, to fill the chip. Each slice is a multiple of 32 deep (BK of
+// the fallback kernel).
+struct SplitPlan { int wm, wn, wk, split; int64_t chunk; };
+SplitPlan split_plan(int64_t m, int64_t n, int64_t k, bool defer) {
+  const int64_t mn = m * n;
+  SplitPlan p{};
+  if (mn >= (int64_t(1) << 21) || k >= 8192) { p.wm = 2; p.wn = 2; p.wk = 16; }
+  else if (mn <= (int64_t(1) << 19)) { p.wm = 1; p.wn = 1; p.wk = 32; }
+  else { p.wm = 1; p.wn = 2; p.wk = 16; }
+  const int64_t tiles = ((m + 32 * p.wm - 1) / (32 * p.wm)) * ((n + 32 * p.wn - 1) / (32 * p.wn));
+  int64_t want = 1;
+  if (defer || k >= 1024) {
+    const int64_t blocks = p.wm == 2 ? 2048 : 1024;
+    want = tiles < blocks / 4 ? (blocks + tiles - 1) / tiles : 1;
+  }
+  const int64_t split = std::max<int64_t>(1, std::min(want, k / 64));
+  p.chunk = ((k + split - 1) / split + BK - 1) / BK * BK;
+  p.split = int((k + p.chunk - 1) / p.chunk);
+  return p;
+}
+}  // namespace
+
+int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer) { return split_plan(m, n, k, defer).split; }
+
+int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum, bool sum_a, bool defer) {
+  const int split = gemm_split_for(m, n, k, defer);
+  if (split <= 1) return 0;
+  return int64_t(split) * m * n + (colsum ? int64_t(split) * (sum_a ? m : n) : 0);  // partials, then sums
+}
+
+int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs) {
+  const int split = gemm_split_for(g.m, g.n, g.k, g.defer);
+  if (split <= 1) return 0;
+  if (g.bias || g.ldc != g.n) bad("deferred split-K needs a dense output without bias");
+  if (g.m * g.n > INT32_MAX) bad("deferred split-K output too large");
+  jobs[0] = ColumnJob{g.workspace, g.c, nullptr, split, int32_t(g.m * g.n), int32_t(g.m * g.n), 0};
+  if (!g.colsum) return 1;
+  const int64_t width = g.sum_a ? g.m : g.n;
+  jobs[1] = ColumnJob{g.workspace + int64_t(split) * g.m * g.n, g.colsum, nullptr, split, int32_t(width), int32_t(width), 0};
+  return 2;
+}
+
+void gemm(hipStream_t s, const GemmArgs& g) {
+  if (g.m <= 0 || g.n <= 0) return;
+  if (g.k <= 0) bad("gemm with k = 0");
+  const SplitPlan plan = split_plan(g.m, g.n, g.k, g.defer);
+  const int split = plan.split;
+  const int64_t chunk = plan.chunk;
+  float* ws = nullptr;
+  if (split > 1) {
+    if (!g.workspace || g.workspace_floats < gemm_workspace(g.m, g.n, g.k, g.colsum != nullptr, g.sum_a, g.defer))
+      bad("gemm split-K workspace too small");
+    ws = g.workspace;
+  }
+  dim3 grid(unsigned((g.n + BN - 1) / BN), unsigned((g.m + BM - 1) / BM), unsigned(split));
+  if (grid.y > 65535) bad("gemm M too large");
+  const dim3 wgrid(unsigned((g.n + 32 * plan.wn - 1) / (32 * plan.wn)), unsigned((g.m + 32 * plan.wm - 1) / (32 * plan.wm)),
+                   unsigned(split));
+  const int64_t width = g.sum_a ? g.m : g.n;
+  float* csum = g.colsum ? (ws ? ws + int64_t(split) * g.m * g.n : g.colsum) : nullptr;
+  // float4 loads need 16-byte aligned groups and a contiguous extent that is a multiple of 4.
+  auto aligned = [](const float* p, int64_t ld, int64_t extent) {
+    return (reinterpret_cast<uintptr_t>(p) % 16 == 0) && ld % 4 == 0 && extent % 4 == 0;
+  };
+  const bool va = aligned(g.a, g.lda, g.ta ? g.m : g.k), vb = aligned(g.b, g.ldb, g.tb ? g.k : g.n);
+#define MSX_GEMM(TA, TB, VA, VB)                                                                                 \
+  hipLaunchKernelGGL((k_gemm<TA, TB, VA, VB>), grid, dim3(256), 0, s, g.a, g.b, g.c, g.bias, g.m, g.n, g.k, g.lda, \
+                     g.ldb, g.ldc, chunk, ws, csum, g.sum_a)
+#define MSX_GEMM_V(TA, TB)                  \
+  if (va && vb) MSX_GEMM(TA, TB, true, true);        \
+  else if (va) MSX_GEMM(TA, TB, true, false);        \
+  else if (vb) MSX_GEMM(TA, TB, false, true);        \
+  else MSX_GEMM(TA, TB, false, false);
+#define MSX_WIDE(TA, TB, WM, WN, WK)                                                                              \
+  hipLaunchKernelGGL((k_gemm_w<TA, TB, WM, WN, WK>), wgrid, dim3(256), 0, s, g.a, g.b, g.c, g.bias, g.m, g.n, g.k, g.lda, \
+                     g.ldb, g.ldc, chunk, ws, csum, g.sum_a)
+#define MSX_WIDE_T(TA, TB)                                  \
+  if (plan.wm == 2) MSX_WIDE(TA, TB, 2, 2, 16);             \
+  else if (plan.wn == 2) MSX_WIDE(TA, TB, 1, 2, 16);        \
+  else MSX_WIDE(TA, TB, 1, 1, 32);
+  if (va && vb) {
+    if (!g.ta && !g.tb) { MSX_WIDE_T(false, false) }
+    else if (g.ta && !g.tb) { MSX_WIDE_T(true, false) }
+    else if (!g.ta && g.tb) { MSX_WIDE_T(false, true) }
+    else { MSX_WIDE_T(true, true) }
+  } else if (!g.ta && !g.tb) { MSX_GEMM_V(false, false) }
+  else if (g.ta && !g.tb) { MSX_GEMM_V(true, false) }
+  else if (!g.ta && g.tb) { MSX_GEMM_V(false, true) }
+  else { MSX_GEMM_V(true, true) }
+#undef MSX_WIDE_T
+#undef MSX_WIDE
+#undef MSX_GEMM_V
+#undef MSX_GEMM
+  if (split > 1 && !g.defer) {
+    const int64_t total = g.m * g.n + (g.colsum ? width : 0);
+    const unsigned blocks = unsigned((total + 255) / 256);
+#define MSX_SPLITK(S) hipLaunchKernelGGL(k_splitk_sum<S>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, \
+                                         split, g.colsum, width)
+    if (split <= 8) MSX_SPLITK(8);
+    else if (split <= 16) MSX_SPLITK(16);
+    else MSX_SPLITK(32);
+#undef MSX_SPLITK
+  }
+}
+
+}  // namespace msx::hk

@@ -1,8 +1,9 @@
-// CDNA4 (gfx950) kernels of the training step. Wave64 throughout; reductions use cross-lane
-// shuffles within a wave and LDS across waves; matrix contractions use the f32 MFMA
-// (v_mfma_f32_16x16x4f32). Built with -ffp-contract=off: every f32 expression rounds as written,
-// and fused multiply-adds appear only where a kernel calls __builtin_fmaf.
+// CDNA4 (gfx950) kernels of the training step other than the GEMMs (gemm.hip) and attention
+// (attention.hip). Wave64 throughout; reductions use cross-lane shuffles within a wave and LDS
+// across waves. Built with -ffp-contract=off: every f32 expression rounds as written, and fused
+// multiply-adds appear only where a kernel calls __builtin_fmaf.
 #include "kernels.h"
+#include "device.h"
 
 #include <algorithm>
 #include <stdexcept>
@@ -10,52 +11,6 @@
 
 namespace msx::hk {
 
-namespace {
-typedef float v4f __attribute__((ext_vector_type(4)));
-
-[[noreturn]] void bad(const std::string& what) { throw std::runtime_error("kernel launch refused: " + what); }
-
-inline unsigned blocks_for(int64_t n, int per) { return unsigned((n + per - 1) / per); }
-
-__device__ __forceinline__ float wave_sum(float v) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-
-// The GELU of interpreter.rs:1539-1587 in device arithmetic: the nearest f32 constants, the same
-// operation order, the device expf.
-__device__ __forceinline__ float d_gelu_twice_inner(float x) {
-  const float scale = 0.797884560802865f, cubic = 0.044715f;
-  return 2.0f * scale * (x + cubic * x * x * x);
-}
-__device__ __forceinline__ float d_logistic(float v) { return 1.0f / (1.0f + expf(0.0f - v)); }
-__device__ __forceinline__ float d_gelu(float x) { return x * d_logistic(d_gelu_twice_inner(x)); }
-__device__ __forceinline__ float d_gelu_grad(float x, float g) {
-  const float scale = 0.797884560802865f, cubic = 0.044715f;
-  float v = d_gelu_twice_inner(x);
-  float s = d_logistic(v), r = d_logistic(0.0f - v);
-  float slope = scale * (1.0f + 3.0f * cubic * x * x);
-  return (s + 2.0f * (s * x) * r * slope) * g;
-}
-
-// Philox4x32-10 word 0 (train/init.rs:91-109), on the device for the dropout masks.
-__device__ __forceinline__ uint32_t philox_w0(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
-                                              uint32_t k1) {
-  const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
-#pragma unroll
-  for (int round = 0; round < 10; ++round) {
-    if (round > 0) { k0 += W0; k1 += W1; }
-    uint32_t hi0 = __umulhi(M0, c0), lo0 = M0 * c0, hi1 = __umulhi(M1, c2), lo1 = M1 * c2;
-    uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
-    c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
-  }
-  return c0;
-}
-}  // namespace
 
 // ---------------------------------------------------------------------------------------------
 // Elementwise.
@@ -115,271 +70,6 @@ void fill_zero(hipStream_t s, void* o, int64_t bytes) {
   int64_t words = bytes / 4;
   hipLaunchKernelGGL(k_fill_zero, dim3(std::min<unsigned>(blocks_for(words / 4 + 1, 256), 8192)), dim3(256), 0, s,
                      static_cast<uint32_t*>(o), words);
-}
-
-// ---------------------------------------------------------------------------------------------
-// GEMM on the f32 MFMA: a 64x64 output tile per 256-thread block, each wave a 32x32 quarter as
-// 2x2 MFMA 16x16x4 tiles. K advances 32 at a time through double-buffered LDS; the next K tile's
-// global loads (float4 where the operand's layout allows) are in flight while the MFMAs of the
-// current one run. Operands may be read transposed in place. Under split-K every slice writes its
-// partial tile to the workspace and k_splitk_sum adds the slices in ascending order, with every
-// slice's load in flight at once: deterministic.
-namespace {
-constexpr int BM = 64, BN = 64, BK = 32, LDP = 68;  // LDS row stride (floats)
-
-// Loads of one K tile of an operand into registers, branch-free: out-of-range elements read a
-// clamped in-range address and are zeroed by a select, so no load waits on another. The (r, k)
-// element is A[r * lda + k], or A[k * lda + r] when T; thread t takes the float4 groups t and
-// t + 256 of the tile along the operand's contiguous dimension. V: the groups are 16-byte aligned
-// and the contiguous extent is a multiple of 4, so a group is wholly in or out of range.
-template <bool T, bool V>
-__device__ __forceinline__ void load_tile(const float* __restrict__ A, int64_t lda, int64_t rows, int64_t kend,
-                                          int64_t r0, int64_t k0, int tid, float (&reg)[8]) {
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int e = tid + h * 256;
-    int r, k;
-    if (!T) { r = e >> 3; k = (e & 7) * 4; } else { k = e >> 4; r = (e & 15) * 4; }
-    const int64_t gr = r0 + r, gk = k0 + k;
-    if (V) {
-      const bool ok = !T ? (gr < rows && gk < kend) : (gk < kend && gr < rows);
-      const int64_t cr = gr < rows ? gr : rows - 1;
-      const int64_t ck = gk < kend ? gk : kend - 4;
-      const int64_t crr = !T ? cr : (gr < rows ? gr : rows - 4);
-      const int64_t ckk = !T ? ck : (gk < kend ? gk : kend - 1);
-      const float4 f = *reinterpret_cast<const float4*>(!T ? A + crr * lda + ckk : A + ckk * lda + crr);
-      reg[4 * h] = ok ? f.x : 0.0f;
-      reg[4 * h + 1] = ok ? f.y : 0.0f;
-      reg[4 * h + 2] = ok ? f.z : 0.0f;
-      reg[4 * h + 3] = ok ? f.w : 0.0f;
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t rr = !T ? gr : gr + j, kk = !T ? gk + j : gk;
-        const bool ok = rr < rows && kk < kend;
-        const int64_t cr = rr < rows ? rr : rows - 1, ck = kk < kend ? kk : kend - 1;
-        const float x = !T ? A[cr * lda + ck] : A[ck * lda + cr];
-        reg[4 * h + j] = ok ? x : 0.0f;
-      }
-    }
-  }
-}
-
-// Stores a K tile into LDS as S[k][r].
-template <bool T>
-__device__ __forceinline__ void store_tile(float* S, int tid, const float (&reg)[8]) {
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int e = tid + h * 256;
-    if (!T) {
-      const int r = e >> 3, k = (e & 7) * 4;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) S[(k + j) * LDP + r] = reg[4 * h + j];
-    } else {
-      const int k = e >> 4, r = (e & 15) * 4;
-      *reinterpret_cast<float4*>(S + k * LDP + r) = make_float4(reg[4 * h], reg[4 * h + 1], reg[4 * h + 2], reg[4 * h + 3]);
-    }
-  }
-}
-}  // namespace
-
-template <bool TA, bool TB, bool VA, bool VB>
-__global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
-                                              float* __restrict__ C, const float* __restrict__ bias, int64_t M,
-                                              int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-                                              int64_t kchunk, float* __restrict__ ws, float* __restrict__ colsum,
-                                              bool sum_a) {
-  __shared__ float As[2][BK * LDP];
-  __shared__ float Bs[2][BK * LDP];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t m0 = int64_t(blockIdx.y) * BM, n0 = int64_t(blockIdx.x) * BN;
-  const int64_t kbeg = int64_t(blockIdx.z) * kchunk;
-  const int64_t kend = K < kbeg + kchunk ? K : kbeg + kchunk;
-  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
-  v4f acc00 = {0, 0, 0, 0}, acc01 = acc00, acc10 = acc00, acc11 = acc00;
-  float ra[8], rb[8];
-  // Column sums of op(B) over K (or, with sum_a, row sums of op(A)): a bias gradient beside its
-  // weight gradient, taken from the LDS tiles by the first row (column) of blocks: thread t adds
-  // tile column t mod 64 over K rows 8 (t / 64) .. + 8 of each K tile.
-  const bool sums = colsum != nullptr && (sum_a ? blockIdx.x == 0 : blockIdx.y == 0);
-  float csum = 0.0f;
-  // B's (k, j) element is B[k * ldb + j], or B[j * ldb + k] when TB: the same loader with the
-  // roles of "row" and "contiguous" swapped.
-  load_tile<TA, VA>(A, lda, M, kend, m0, kbeg, tid, ra);
-  load_tile<!TB, VB>(B, ldb, N, kend, n0, kbeg, tid, rb);
-  int buf = 0;
-  for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
-    store_tile<TA>(As[buf], tid, ra);
-    store_tile<!TB>(Bs[buf], tid, rb);
-    __syncthreads();
-    if (k0 + BK < kend) {
-      load_tile<TA, VA>(A, lda, M, kend, m0, k0 + BK, tid, ra);
-      load_tile<!TB, VB>(B, ldb, N, kend, n0, k0 + BK, tid, rb);
-    }
-    const float* as = As[buf];
-    const float* bs = Bs[buf];
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 4) {
-      const int kr = (kk + (lane >> 4)) * LDP, c = lane & 15;
-      const float a0 = as[kr + wm + c], a1 = as[kr + wm + 16 + c];
-      const float b0 = bs[kr + wn + c], b1 = bs[kr + wn + 16 + c];
-      acc00 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc00, 0, 0, 0);
-      acc01 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc01, 0, 0, 0);
-      acc10 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc10, 0, 0, 0);
-      acc11 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc11, 0, 0, 0);
-    }
-    if (sums) {
-      const int c = tid & 63, kg = (tid >> 6) * 8;
-      const float* ss = sum_a ? as : bs;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) csum += ss[(kg + j) * LDP + c];
-    }
-    buf ^= 1;
-  }
-  if (sums) {
-    __syncthreads();
-    float* red = As[0];
-    red[tid] = csum;
-    __syncthreads();
-    const int64_t base = sum_a ? m0 : n0, width = sum_a ? M : N;
-    if (tid < 64 && base + tid < width) {
-      const float v = ((red[tid] + red[64 + tid]) + red[128 + tid]) + red[192 + tid];
-      colsum[(ws ? int64_t(blockIdx.z) * width : 0) + base + tid] = v;
-    }
-  }
-  const v4f* accs[4] = {&acc00, &acc01, &acc10, &acc11};
-  if (!ws) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int64_t col = n0 + wn + (t & 1) * 16 + (lane & 15);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = m0 + wm + (t >> 1) * 16 + 4 * (lane >> 4) + r;
-        if (row < M && col < N) C[row * ldc + col] = bias ? (*accs[t])[r] + bias[col] : (*accs[t])[r];
-      }
-    }
-    return;
-  }
-  // Split-K: this slice's partial product, [M, N] row-major at slice z; the slices are added in
-  // order by k_splitk_sum or a deferred column_finalize job.
-  float* part = ws + int64_t(blockIdx.z) * M * N;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int64_t col = n0 + wn + (t & 1) * 16 + (lane & 15);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t row = m0 + wm + (t >> 1) * 16 + 4 * (lane >> 4) + r;
-      if (row < M && col < N) part[row * N + col] = (*accs[t])[r];
-    }
-  }
-}
-
-// Sums the split-K partial products in ascending slice order, one output element a thread, every
-// slice's load issued before the adds; the threads past M * N do the same for the slices' column
-// (row) sums.
-template <int SPLIT>
-__global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ ws, float* __restrict__ C,
-                                                    const float* __restrict__ bias, int64_t M, int64_t N, int64_t ldc,
-                                                    int splits, float* __restrict__ colsum, int64_t width) {
-  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t mn = M * N;
-  const bool cs = e >= mn;
-  if (cs && (!colsum || e - mn >= width)) return;
-  const float* src = cs ? ws + int64_t(splits) * mn + (e - mn) : ws + e;
-  const int64_t stride = cs ? width : mn;
-  float t[SPLIT];
-#pragma unroll
-  for (int z = 0; z < SPLIT; ++z) t[z] = z < splits ? src[z * stride] : 0.0f;
-  float s = t[0];
-#pragma unroll
-  for (int z = 1; z < SPLIT; ++z)
-    if (z < splits) s += t[z];
-  for (int z = SPLIT; z < splits; ++z) s += src[z * stride];
-  if (cs) {
-    colsum[e - mn] = s;
-  } else {
-    const int64_t row = e / N, col = e - row * N;
-    C[row * ldc + col] = bias ? s + bias[col] : s;
-  }
-}
-
-namespace {
-// The split-K factor and the K extent of a slice (a multiple of BK).
-struct SplitPlan { int split; int64_t chunk; };
-SplitPlan split_plan(int64_t m, int64_t n, int64_t k) {
-  const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  int64_t split = 1;
-  if (tiles < 256 && k >= 512) split = std::max<int64_t>(1, std::min((1024 + tiles - 1) / tiles, k / 128));
-  int64_t chunk = ((k + split - 1) / split + BK - 1) / BK * BK;
-  return {int((k + chunk - 1) / chunk), chunk};
-}
-}  // namespace
-
-int gemm_split_for(int64_t m, int64_t n, int64_t k) { return split_plan(m, n, k).split; }
-
-int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum, bool sum_a) {
-  const int split = gemm_split_for(m, n, k);
-  if (split <= 1) return 0;
-  return int64_t(split) * m * n + (colsum ? int64_t(split) * (sum_a ? m : n) : 0);  // partials, then sums
-}
-
-int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs) {
-  const int split = gemm_split_for(g.m, g.n, g.k);
-  if (split <= 1) return 0;
-  if (g.bias || g.ldc != g.n) bad("deferred split-K needs a dense output without bias");
-  if (g.m * g.n > INT32_MAX) bad("deferred split-K output too large");
-  jobs[0] = ColumnJob{g.workspace, g.c, nullptr, split, int32_t(g.m * g.n), int32_t(g.m * g.n), 0};
-  if (!g.colsum) return 1;
-  const int64_t width = g.sum_a ? g.m : g.n;
-  jobs[1] = ColumnJob{g.workspace + int64_t(split) * g.m * g.n, g.colsum, nullptr, split, int32_t(width), int32_t(width), 0};
-  return 2;
-}
-
-void gemm(hipStream_t s, const GemmArgs& g) {
-  if (g.m <= 0 || g.n <= 0) return;
-  if (g.k <= 0) bad("gemm with k = 0");
-  const SplitPlan plan = split_plan(g.m, g.n, g.k);
-  const int split = plan.split;
-  const int64_t chunk = plan.chunk;
-  float* ws = nullptr;
-  if (split > 1) {
-    if (!g.workspace || g.workspace_floats < gemm_workspace(g.m, g.n, g.k, g.colsum != nullptr, g.sum_a))
-      bad("gemm split-K workspace too small");
-    ws = g.workspace;
-  }
-  dim3 grid(unsigned((g.n + BN - 1) / BN), unsigned((g.m + BM - 1) / BM), unsigned(split));
-  if (grid.y > 65535) bad("gemm M too large");
-  const int64_t width = g.sum_a ? g.m : g.n;
-  float* csum = g.colsum ? (ws ? ws + int64_t(split) * g.m * g.n : g.colsum) : nullptr;
-  // float4 loads need 16-byte aligned groups and a contiguous extent that is a multiple of 4.
-  auto aligned = [](const float* p, int64_t ld, int64_t extent) {
-    return (reinterpret_cast<uintptr_t>(p) % 16 == 0) && ld % 4 == 0 && extent % 4 == 0;
-  };
-  const bool va = aligned(g.a, g.lda, g.ta ? g.m : g.k), vb = aligned(g.b, g.ldb, g.tb ? g.k : g.n);
-#define MSX_GEMM(TA, TB, VA, VB)                                                                                 \
-  hipLaunchKernelGGL((k_gemm<TA, TB, VA, VB>), grid, dim3(256), 0, s, g.a, g.b, g.c, g.bias, g.m, g.n, g.k, g.lda, \
-                     g.ldb, g.ldc, chunk, ws, csum, g.sum_a)
-#define MSX_GEMM_V(TA, TB)                  \
-  if (va && vb) MSX_GEMM(TA, TB, true, true);        \
-  else if (va) MSX_GEMM(TA, TB, true, false);        \
-  else if (vb) MSX_GEMM(TA, TB, false, true);        \
-  else MSX_GEMM(TA, TB, false, false);
-  if (!g.ta && !g.tb) { MSX_GEMM_V(false, false) }
-  else if (g.ta && !g.tb) { MSX_GEMM_V(true, false) }
-  else if (!g.ta && g.tb) { MSX_GEMM_V(false, true) }
-  else { MSX_GEMM_V(true, true) }
-#undef MSX_GEMM_V
-#undef MSX_GEMM
-  if (split > 1 && !g.defer) {
-    const int64_t total = g.m * g.n + (g.colsum ? width : 0);
-    const unsigned blocks = unsigned((total + 255) / 256);
-#define MSX_SPLITK(S) hipLaunchKernelGGL(k_splitk_sum<S>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, \
-                                         split, g.colsum, width)
-    if (split <= 8) MSX_SPLITK(8);
-    else if (split <= 16) MSX_SPLITK(16);
-    else MSX_SPLITK(32);
-#undef MSX_SPLITK
-  }
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -448,12 +448,12 @@ void Executor::build() {
         }
         const int64_t cs_id = x.op == Op::MatMul && colsum_of.count(id) ? int64_t(colsum_of.at(id)) : -1;
         g.sum_a = swap;  // the column sums of B are the row sums of the swapped left operand
-        int64_t wsf = hk::gemm_workspace(g.m, g.n, g.k, cs_id >= 0, g.sum_a);
-        void* ws = wsf > 0 ? R(size_t(wsf) * 4) : nullptr;
-        g.workspace_floats = wsf;
         int64_t bias_id = fused ? int64_t(o[1]) : -1;
         // Split-K partials only the optimizer reads are summed by the batched column finalize.
-        g.defer = wsf > 0 && bias_id < 0 && only_optimizer_reads(int64_t(out_id)) && only_optimizer_reads(cs_id);
+        g.defer = bias_id < 0 && only_optimizer_reads(int64_t(out_id)) && only_optimizer_reads(cs_id);
+        int64_t wsf = hk::gemm_workspace(g.m, g.n, g.k, cs_id >= 0, g.sum_a, g.defer);
+        void* ws = wsf > 0 ? R(size_t(wsf) * 4) : nullptr;
+        g.workspace_floats = wsf;
         push([=](hipStream_t s) {
           hk::GemmArgs a = g;
           a.a = F(asrc);
@@ -464,8 +464,8 @@ void Executor::build() {
           a.colsum = cs_id >= 0 ? F(uint32_t(cs_id)) : nullptr;
           hk::gemm(s, a);
         });
-        if (g.defer) {
-          const int split = hk::gemm_split_for(g.m, g.n, g.k);
+        if (g.defer && wsf > 0) {
+          const int split = hk::gemm_split_for(g.m, g.n, g.k, true);
           const int32_t mn = int32_t(g.m * g.n);
           deferred.push_back({ws, 0, int64_t(out_id), -1, split, mn, mn});
           if (cs_id >= 0) {
