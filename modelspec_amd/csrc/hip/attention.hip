@@ -193,6 +193,59 @@ __global__ __launch_bounds__(256) void k_attn_bwd_scalar(const float* __restrict
 // ---------------------------------------------------------------------------------------------
 // MFMA path. Row stride of every LDS tile is D + 4 floats: the 16 rows x 4 columns an MFMA
 // operand read touches fall in distinct banks.
+constexpr int kU = 4;      // row tiles whose MFMA chains interleave
+constexpr int kWaves = 2;  // waves (16 rows each) a block: a block's K/V (or Q/dO) LDS copy limits
+                           // a CU to two blocks, so smaller blocks spread a sequence over more CUs
+
+// Stages rows [0, rows) of two [., H] head slices (x at xs + row H, y likewise, D floats each)
+// into LDS tiles of row stride D + 4, eight float4 of each a thread in flight before any store.
+template <int D>
+__device__ __forceinline__ void stage_pair(float* X, float* Y, const float* __restrict__ xs,
+                                           const float* __restrict__ ys, int rows, int H) {
+  constexpr int DP = D + 4, Q = D / 4;
+  const int total = rows * Q;
+  for (int e0 = threadIdx.x; e0 < total; e0 += 8 * int(blockDim.x)) {
+    float4 xv[8], yv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      int e = e0 + u * int(blockDim.x);
+      e = e < total ? e : total - 1;
+      const int64_t off = int64_t(e / Q) * H + (e % Q) * 4;
+      xv[u] = *reinterpret_cast<const float4*>(xs + off);
+      yv[u] = *reinterpret_cast<const float4*>(ys + off);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + u * int(blockDim.x);
+      if (e < total) {
+        float* xd = X + (e / Q) * DP + (e % Q) * 4;
+        float* yd = Y + (e / Q) * DP + (e % Q) * 4;
+        xd[0] = xv[u].x; xd[1] = xv[u].y; xd[2] = xv[u].z; xd[3] = xv[u].w;
+        yd[0] = yv[u].x; yd[1] = yv[u].y; yd[2] = yv[u].z; yd[3] = yv[u].w;
+      }
+    }
+  }
+}
+
+
+// Scores of kU tiles of 16 LDS rows R (tiles t0 .. t0 + kU, the ones past nt repeat the last
+// tile and are ignored by the caller) against the 16 columns whose operand fragments xb a lane
+// holds: acc[u][r] = sum over d of R[(t0 + u) 16 + c][d] x[4 g + r][d], each in d order.
+template <int D>
+__device__ __forceinline__ void score_tiles(const float* R, const float (&xb)[D / 4], int t0, int nt, int c, int g,
+                                            v4f (&acc)[kU]) {
+  constexpr int DP = D + 4;
+  const float* rr[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    acc[u] = v4f{0, 0, 0, 0};
+    rr[u] = R + ((t0 + u < nt ? t0 + u : nt - 1) * 16 + c) * DP + g;
+  }
+#pragma unroll
+  for (int t = 0; t < D / 4; ++t)
+#pragma unroll
+    for (int u = 0; u < kU; ++u) acc[u] = mfma4(rr[u][4 * t], xb[t], acc[u]);
+}
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_fwd_mfma(const float* __restrict__ q, const float* __restrict__ k,
                                                        const float* __restrict__ v, const float* __restrict__ mask,
@@ -205,34 +258,28 @@ __global__ __launch_bounds__(256) void k_attn_fwd_mfma(const float* __restrict__
   float* Ms = sm + 2 * S * DP;
   const int b = blockIdx.x / heads, head = blockIdx.x % heads;
   const int64_t kbase = int64_t(b) * S * H + head * D;
-  for (int e = threadIdx.x; e < S * (D / 4); e += blockDim.x) {
-    int j = e / (D / 4), c4 = (e % (D / 4)) * 4;
-    float4 kv = *reinterpret_cast<const float4*>(k + kbase + int64_t(j) * H + c4);
-    float4 vv = *reinterpret_cast<const float4*>(v + kbase + int64_t(j) * H + c4);
-    float* kd = Ks + j * DP + c4;
-    float* vd = Vs + j * DP + c4;
-    kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
-    vd[0] = vv.x; vd[1] = vv.y; vd[2] = vv.z; vd[3] = vv.w;
-  }
+  stage_pair<D>(Ks, Vs, k + kbase, v + kbase, S, H);
   for (int j = threadIdx.x; j < S; j += blockDim.x) Ms[j] = mask[int64_t(b) * S + j];
   __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  const int i0 = blockIdx.y * 64 + wave * 16;
+  const int i0 = blockIdx.y * int(blockDim.x / 4) + wave * 16;
   if (i0 >= L) return;
   const int64_t qrow = (int64_t(b) * L + i0 + c) * H + head * D;
   float qb[D / 4];
 #pragma unroll
   for (int t = 0; t < D / 4; ++t) qb[t] = q[qrow + 4 * t + g];
-  // Pass 1: the maximum score of query i0 + c over the unmasked keys.
+  // Pass 1: the maximum score of query i0 + c over the unmasked keys. kU key tiles at a time, so
+  // that kU independent MFMA chains interleave.
+  const int nt = S / 16;
   float mx = -INFINITY;
-  for (int jt = 0; jt < S / 16; ++jt) {
-    v4f acc = {0, 0, 0, 0};
-    const float* kr = Ks + (jt * 16 + c) * DP + g;
+  for (int jt0 = 0; jt0 < nt; jt0 += kU) {
+    v4f acc[kU];
+    score_tiles<D>(Ks, qb, jt0, nt, c, g, acc);
 #pragma unroll
-    for (int t = 0; t < D / 4; ++t) acc = mfma4(kr[4 * t], qb[t], acc);
+    for (int u = 0; u < kU; ++u)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (Ms[jt * 16 + 4 * g + r] != 0.0f) mx = fmaxf(mx, acc[r] * scale);
+      for (int r = 0; r < 4; ++r)
+        if (jt0 + u < nt && Ms[(jt0 + u) * 16 + 4 * g + r] != 0.0f) mx = fmaxf(mx, acc[u][r] * scale);
   }
   mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
   mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -241,22 +288,25 @@ __global__ __launch_bounds__(256) void k_attn_fwd_mfma(const float* __restrict__
   v4f oacc[D / 16];
 #pragma unroll
   for (int ct = 0; ct < D / 16; ++ct) oacc[ct] = v4f{0, 0, 0, 0};
-  for (int jt = 0; jt < S / 16; ++jt) {
-    v4f acc = {0, 0, 0, 0};
-    const float* kr = Ks + (jt * 16 + c) * DP + g;
+  for (int jt0 = 0; jt0 < nt; jt0 += kU) {
+    v4f acc[kU];
+    score_tiles<D>(Ks, qb, jt0, nt, c, g, acc);
 #pragma unroll
-    for (int t = 0; t < D / 4; ++t) acc = mfma4(kr[4 * t], qb[t], acc);
-    float p[4];
+    for (int u = 0; u < kU; ++u) {
+      if (jt0 + u >= nt) break;
+      const int jt = jt0 + u;
+      float p[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = Ms[jt * 16 + 4 * g + r] != 0.0f ? expf(acc[r] * scale - mx) : 0.0f;
-      total += p[r];
-    }
+      for (int r = 0; r < 4; ++r) {
+        p[r] = Ms[jt * 16 + 4 * g + r] != 0.0f ? expf(acc[u][r] * scale - mx) : 0.0f;
+        total += p[r];
+      }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float* vr = Vs + (jt * 16 + 4 * g + r) * DP + c;
+      for (int r = 0; r < 4; ++r) {
+        const float* vr = Vs + (jt * 16 + 4 * g + r) * DP + c;
 #pragma unroll
-      for (int ct = 0; ct < D / 16; ++ct) oacc[ct] = mfma4(p[r], vr[ct * 16], oacc[ct]);
+        for (int ct = 0; ct < D / 16; ++ct) oacc[ct] = mfma4(p[r], vr[ct * 16], oacc[ct]);
+      }
     }
   }
   total += __shfl_xor(total, 16, 64);
@@ -290,19 +340,11 @@ __global__ __launch_bounds__(256) void k_attn_bwd_q_mfma(const float* __restrict
   float* Ms = sm + 2 * S * DP;
   const int b = blockIdx.x / heads, head = blockIdx.x % heads;
   const int64_t kbase = int64_t(b) * S * H + head * D;
-  for (int e = threadIdx.x; e < S * (D / 4); e += blockDim.x) {
-    int j = e / (D / 4), c4 = (e % (D / 4)) * 4;
-    float4 kv = *reinterpret_cast<const float4*>(k + kbase + int64_t(j) * H + c4);
-    float4 vv = *reinterpret_cast<const float4*>(v + kbase + int64_t(j) * H + c4);
-    float* kd = Ks + j * DP + c4;
-    float* vd = Vs + j * DP + c4;
-    kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
-    vd[0] = vv.x; vd[1] = vv.y; vd[2] = vv.z; vd[3] = vv.w;
-  }
+  stage_pair<D>(Ks, Vs, k + kbase, v + kbase, S, H);
   for (int j = threadIdx.x; j < S; j += blockDim.x) Ms[j] = mask[int64_t(b) * S + j];
   __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  const int i0 = blockIdx.y * 64 + wave * 16;
+  const int i0 = blockIdx.y * int(blockDim.x / 4) + wave * 16;
   if (i0 >= L) return;
   const int64_t row = (int64_t(b) * L + i0 + c) * H + head * D;
   // d_i for query i0 + c: lane group g sums columns [g D/4, (g + 1) D/4).
@@ -320,26 +362,27 @@ __global__ __launch_bounds__(256) void k_attn_bwd_q_mfma(const float* __restrict
   v4f acc[D / 16];
 #pragma unroll
   for (int ct = 0; ct < D / 16; ++ct) acc[ct] = v4f{0, 0, 0, 0};
-  for (int jt = 0; jt < S / 16; ++jt) {
-    v4f st = {0, 0, 0, 0}, dpt = {0, 0, 0, 0};
-    const float* kr = Ks + (jt * 16 + c) * DP + g;
-    const float* vr = Vs + (jt * 16 + c) * DP + g;
+  const int nt = S / 16;
+  for (int jt0 = 0; jt0 < nt; jt0 += kU) {
+    v4f st[kU], dpt[kU];
+    score_tiles<D>(Ks, qb, jt0, nt, c, g, st);
+    score_tiles<D>(Vs, gb, jt0, nt, c, g, dpt);
 #pragma unroll
-    for (int t = 0; t < D / 4; ++t) {
-      st = mfma4(kr[4 * t], qb[t], st);
-      dpt = mfma4(vr[4 * t], gb[t], dpt);
-    }
-    float ds[4];
+    for (int u = 0; u < kU; ++u) {
+      if (jt0 + u >= nt) break;
+      const int jt = jt0 + u;
+      float ds[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float p = Ms[jt * 16 + 4 * g + r] != 0.0f ? expf(st[r] * scale - mx) / total : 0.0f;
-      ds[r] = p * (dpt[r] - dd);
-    }
+      for (int r = 0; r < 4; ++r) {
+        float p = Ms[jt * 16 + 4 * g + r] != 0.0f ? expf(st[u][r] * scale - mx) / total : 0.0f;
+        ds[r] = p * (dpt[u][r] - dd);
+      }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float* kk = Ks + (jt * 16 + 4 * g + r) * DP + c;
+      for (int r = 0; r < 4; ++r) {
+        const float* kk = Ks + (jt * 16 + 4 * g + r) * DP + c;
 #pragma unroll
-      for (int ct = 0; ct < D / 16; ++ct) acc[ct] = mfma4(ds[r], kk[ct * 16], acc[ct]);
+        for (int ct = 0; ct < D / 16; ++ct) acc[ct] = mfma4(ds[r], kk[ct * 16], acc[ct]);
+      }
     }
   }
 #pragma unroll
@@ -365,15 +408,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_kv_mfma(const float* __restric
   float* Sm = sm + 2 * L * DP;  // max, sum, d per query
   const int b = blockIdx.x / heads, head = blockIdx.x % heads;
   const int64_t qbase = int64_t(b) * L * H + head * D;
-  for (int e = threadIdx.x; e < L * (D / 4); e += blockDim.x) {
-    int i = e / (D / 4), c4 = (e % (D / 4)) * 4;
-    float4 qv = *reinterpret_cast<const float4*>(q + qbase + int64_t(i) * H + c4);
-    float4 gv = *reinterpret_cast<const float4*>(go + qbase + int64_t(i) * H + c4);
-    float* qd = Qs + i * DP + c4;
-    float* gd = Gs + i * DP + c4;
-    qd[0] = qv.x; qd[1] = qv.y; qd[2] = qv.z; qd[3] = qv.w;
-    gd[0] = gv.x; gd[1] = gv.y; gd[2] = gv.z; gd[3] = gv.w;
-  }
+  stage_pair<D>(Qs, Gs, q + qbase, go + qbase, L, H);
   for (int i = threadIdx.x; i < L; i += blockDim.x) {
     const int64_t srow = int64_t(blockIdx.x) * L + i;
     Sm[3 * i] = stats[2 * srow];
@@ -382,7 +417,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_kv_mfma(const float* __restric
   }
   __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  const int j0 = blockIdx.y * 64 + wave * 16;
+  const int j0 = blockIdx.y * int(blockDim.x / 4) + wave * 16;
   if (j0 >= S) return;
   const int64_t krow = (int64_t(b) * S + j0 + c) * H + head * D;
   const bool live = mask[int64_t(b) * S + j0 + c] != 0.0f;
@@ -392,30 +427,31 @@ __global__ __launch_bounds__(256) void k_attn_bwd_kv_mfma(const float* __restric
   v4f dka[D / 16], dva[D / 16];
 #pragma unroll
   for (int ct = 0; ct < D / 16; ++ct) { dka[ct] = v4f{0, 0, 0, 0}; dva[ct] = v4f{0, 0, 0, 0}; }
-  for (int it = 0; it < L / 16; ++it) {
-    v4f s = {0, 0, 0, 0}, dp = {0, 0, 0, 0};
-    const float* qr = Qs + (it * 16 + c) * DP + g;
-    const float* gr = Gs + (it * 16 + c) * DP + g;
+  const int nt = L / 16;
+  for (int it0 = 0; it0 < nt; it0 += kU) {
+    v4f s[kU], dp[kU];
+    score_tiles<D>(Qs, kb, it0, nt, c, g, s);
+    score_tiles<D>(Gs, vb, it0, nt, c, g, dp);
 #pragma unroll
-    for (int t = 0; t < D / 4; ++t) {
-      s = mfma4(qr[4 * t], kb[t], s);
-      dp = mfma4(gr[4 * t], vb[t], dp);
-    }
-    float p[4], ds[4];
+    for (int u = 0; u < kU; ++u) {
+      if (it0 + u >= nt) break;
+      const int it = it0 + u;
+      float p[4], ds[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float* st = Sm + 3 * (it * 16 + 4 * g + r);
-      p[r] = live ? expf(s[r] * scale - st[0]) / st[1] : 0.0f;
-      ds[r] = p[r] * (dp[r] - st[2]);
-    }
+      for (int r = 0; r < 4; ++r) {
+        const float* st = Sm + 3 * (it * 16 + 4 * g + r);
+        p[r] = live ? expf(s[u][r] * scale - st[0]) / st[1] : 0.0f;
+        ds[r] = p[r] * (dp[u][r] - st[2]);
+      }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float* gq = Gs + (it * 16 + 4 * g + r) * DP + c;
-      const float* qq = Qs + (it * 16 + 4 * g + r) * DP + c;
+      for (int r = 0; r < 4; ++r) {
+        const float* gq = Gs + (it * 16 + 4 * g + r) * DP + c;
+        const float* qq = Qs + (it * 16 + 4 * g + r) * DP + c;
 #pragma unroll
-      for (int ct = 0; ct < D / 16; ++ct) {
-        dva[ct] = mfma4(p[r], gq[ct * 16], dva[ct]);
-        dka[ct] = mfma4(ds[r], qq[ct * 16], dka[ct]);
+        for (int ct = 0; ct < D / 16; ++ct) {
+          dva[ct] = mfma4(p[r], gq[ct * 16], dva[ct]);
+          dka[ct] = mfma4(ds[r], qq[ct * 16], dka[ct]);
+        }
       }
     }
   }
@@ -466,9 +502,9 @@ void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v
   if (!head_ok(d) || L > S) refuse("attention head width or query rows");
   float scale = 1.0f / sqrtf(float(d));
   if (attention_mfma(L, S, d)) {
-    dim3 grid(unsigned(B * heads), unsigned((L + 63) / 64));
+    dim3 grid(unsigned(B * heads), unsigned((L + 16 * kWaves - 1) / (16 * kWaves)));
     size_t lds = mfma_fwd_lds(S, d);
-#define GO(D) hipLaunchKernelGGL(k_attn_fwd_mfma<D>, grid, dim3(256), lds, s, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale)
+#define GO(D) hipLaunchKernelGGL(k_attn_fwd_mfma<D>, grid, dim3(64 * kWaves), lds, s, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale)
     MSX_BY_D(d, GO)
 #undef GO
     return;
@@ -489,20 +525,20 @@ void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v
   float scale = 1.0f / sqrtf(float(d));
   if (attention_mfma(L, S, d)) {
     if (!o || !stats || !dsum) refuse("the MFMA attention backward needs the forward output and statistics");
-    dim3 gq(unsigned(B * heads), unsigned((L + 63) / 64));
+    dim3 gq(unsigned(B * heads), unsigned((L + 16 * kWaves - 1) / (16 * kWaves)));
     if (dq || dk || dv) {
       // dQ (written only when asked) and the d_i the key pass reads.
       float* dq_out = dq;
       size_t lq = mfma_fwd_lds(S, d);
-#define GO(D) hipLaunchKernelGGL(k_attn_bwd_q_mfma<D>, gq, dim3(256), lq, s, q, k, v, mask, o, stats, g, dq_out, dsum, int(L), int(S), int(H), int(heads), scale)
+#define GO(D) hipLaunchKernelGGL(k_attn_bwd_q_mfma<D>, gq, dim3(64 * kWaves), lq, s, q, k, v, mask, o, stats, g, dq_out, dsum, int(L), int(S), int(H), int(heads), scale)
       if (dq_out) { MSX_BY_D(d, GO) }
 #undef GO
       if (!dq_out) refuse("the MFMA attention backward computes d_i in its dQ pass: dQ is required");
     }
     if (dk || dv) {
-      dim3 gk(unsigned(B * heads), unsigned((S + 63) / 64));
+      dim3 gk(unsigned(B * heads), unsigned((S + 16 * kWaves - 1) / (16 * kWaves)));
       size_t lk = mfma_kv_lds(L, d);
-#define GO(D) hipLaunchKernelGGL(k_attn_bwd_kv_mfma<D>, gk, dim3(256), lk, s, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale)
+#define GO(D) hipLaunchKernelGGL(k_attn_bwd_kv_mfma<D>, gk, dim3(64 * kWaves), lk, s, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale)
       MSX_BY_D(d, GO)
 #undef GO
     }
