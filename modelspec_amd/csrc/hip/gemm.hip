@@ -8,161 +8,9 @@
 namespace msx::hk {
 
 // ---------------------------------------------------------------------------------------------
-// GEMM on the f32 MFMA: a 64x64 output tile per 256-thread block, each wave a 32x32 quarter as
-// 2x2 MFMA 16x16x4 tiles. K advances 32 at a time through double-buffered LDS; the next K tile's
-// global loads (float4 where the operand's layout allows) are in flight while the MFMAs of the
-// current one run. Operands may be read transposed in place. Under split-K every slice writes its
-// partial tile to the workspace and k_splitk_sum adds the slices in ascending order, with every
-// slice's load in flight at once: deterministic.
 namespace {
-constexpr int BM = 64, BN = 64, BK = 32, LDP = 68;  // LDS row stride (floats)
-
-// Loads of one K tile of an operand into registers, branch-free: out-of-range elements read a
-// clamped in-range address and are zeroed by a select, so no load waits on another. The (r, k)
-// element is A[r * lda + k], or A[k * lda + r] when T; thread t takes the float4 groups t and
-// t + 256 of the tile along the operand's contiguous dimension. V: the groups are 16-byte aligned
-// and the contiguous extent is a multiple of 4, so a group is wholly in or out of range.
-template <bool T, bool V>
-__device__ __forceinline__ void load_tile(const float* __restrict__ A, int64_t lda, int64_t rows, int64_t kend,
-                                          int64_t r0, int64_t k0, int tid, float (&reg)[8]) {
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int e = tid + h * 256;
-    int r, k;
-    if (!T) { r = e >> 3; k = (e & 7) * 4; } else { k = e >> 4; r = (e & 15) * 4; }
-    const int64_t gr = r0 + r, gk = k0 + k;
-    if (V) {
-      const bool ok = !T ? (gr < rows && gk < kend) : (gk < kend && gr < rows);
-      const int64_t cr = gr < rows ? gr : rows - 1;
-      const int64_t ck = gk < kend ? gk : kend - 4;
-      const int64_t crr = !T ? cr : (gr < rows ? gr : rows - 4);
-      const int64_t ckk = !T ? ck : (gk < kend ? gk : kend - 1);
-      const float4 f = *reinterpret_cast<const float4*>(!T ? A + crr * lda + ckk : A + ckk * lda + crr);
-      reg[4 * h] = ok ? f.x : 0.0f;
-      reg[4 * h + 1] = ok ? f.y : 0.0f;
-      reg[4 * h + 2] = ok ? f.z : 0.0f;
-      reg[4 * h + 3] = ok ? f.w : 0.0f;
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t rr = !T ? gr : gr + j, kk = !T ? gk + j : gk;
-        const bool ok = rr < rows && kk < kend;
-        const int64_t cr = rr < rows ? rr : rows - 1, ck = kk < kend ? kk : kend - 1;
-        const float x = !T ? A[cr * lda + ck] : A[ck * lda + cr];
-        reg[4 * h + j] = ok ? x : 0.0f;
-      }
-    }
-  }
-}
-
-// Stores a K tile into LDS as S[k][r].
-template <bool T>
-__device__ __forceinline__ void store_tile(float* S, int tid, const float (&reg)[8]) {
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int e = tid + h * 256;
-    if (!T) {
-      const int r = e >> 3, k = (e & 7) * 4;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) S[(k + j) * LDP + r] = reg[4 * h + j];
-    } else {
-      const int k = e >> 4, r = (e & 15) * 4;
-      *reinterpret_cast<float4*>(S + k * LDP + r) = make_float4(reg[4 * h], reg[4 * h + 1], reg[4 * h + 2], reg[4 * h + 3]);
-    }
-  }
-}
+constexpr int kSliceAlign = 32;  // split-K slices are multiples of this many K steps
 }  // namespace
-
-template <bool TA, bool TB, bool VA, bool VB>
-__global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
-                                              float* __restrict__ C, const float* __restrict__ bias, int64_t M,
-                                              int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-                                              int64_t kchunk, float* __restrict__ ws, float* __restrict__ colsum,
-                                              bool sum_a) {
-  __shared__ float As[2][BK * LDP];
-  __shared__ float Bs[2][BK * LDP];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t m0 = int64_t(blockIdx.y) * BM, n0 = int64_t(blockIdx.x) * BN;
-  const int64_t kbeg = int64_t(blockIdx.z) * kchunk;
-  const int64_t kend = K < kbeg + kchunk ? K : kbeg + kchunk;
-  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
-  v4f acc00 = {0, 0, 0, 0}, acc01 = acc00, acc10 = acc00, acc11 = acc00;
-  float ra[8], rb[8];
-  // Column sums of op(B) over K (or, with sum_a, row sums of op(A)): a bias gradient beside its
-  // weight gradient, taken from the LDS tiles by the first row (column) of blocks: thread t adds
-  // tile column t mod 64 over K rows 8 (t / 64) .. + 8 of each K tile.
-  const bool sums = colsum != nullptr && (sum_a ? blockIdx.x == 0 : blockIdx.y == 0);
-  float csum = 0.0f;
-  // B's (k, j) element is B[k * ldb + j], or B[j * ldb + k] when TB: the same loader with the
-  // roles of "row" and "contiguous" swapped.
-  load_tile<TA, VA>(A, lda, M, kend, m0, kbeg, tid, ra);
-  load_tile<!TB, VB>(B, ldb, N, kend, n0, kbeg, tid, rb);
-  int buf = 0;
-  for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
-    store_tile<TA>(As[buf], tid, ra);
-    store_tile<!TB>(Bs[buf], tid, rb);
-    __syncthreads();
-    if (k0 + BK < kend) {
-      load_tile<TA, VA>(A, lda, M, kend, m0, k0 + BK, tid, ra);
-      load_tile<!TB, VB>(B, ldb, N, kend, n0, k0 + BK, tid, rb);
-    }
-    const float* as = As[buf];
-    const float* bs = Bs[buf];
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 4) {
-      const int kr = (kk + (lane >> 4)) * LDP, c = lane & 15;
-      const float a0 = as[kr + wm + c], a1 = as[kr + wm + 16 + c];
-      const float b0 = bs[kr + wn + c], b1 = bs[kr + wn + 16 + c];
-      acc00 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc00, 0, 0, 0);
-      acc01 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc01, 0, 0, 0);
-      acc10 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc10, 0, 0, 0);
-      acc11 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc11, 0, 0, 0);
-    }
-    if (sums) {
-      const int c = tid & 63, kg = (tid >> 6) * 8;
-      const float* ss = sum_a ? as : bs;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) csum += ss[(kg + j) * LDP + c];
-    }
-    buf ^= 1;
-  }
-  if (sums) {
-    __syncthreads();
-    float* red = As[0];
-    red[tid] = csum;
-    __syncthreads();
-    const int64_t base = sum_a ? m0 : n0, width = sum_a ? M : N;
-    if (tid < 64 && base + tid < width) {
-      const float v = ((red[tid] + red[64 + tid]) + red[128 + tid]) + red[192 + tid];
-      colsum[(ws ? int64_t(blockIdx.z) * width : 0) + base + tid] = v;
-    }
-  }
-  const v4f* accs[4] = {&acc00, &acc01, &acc10, &acc11};
-  if (!ws) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int64_t col = n0 + wn + (t & 1) * 16 + (lane & 15);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = m0 + wm + (t >> 1) * 16 + 4 * (lane >> 4) + r;
-        if (row < M && col < N) C[row * ldc + col] = bias ? (*accs[t])[r] + bias[col] : (*accs[t])[r];
-      }
-    }
-    return;
-  }
-  // Split-K: this slice's partial product, [M, N] row-major at slice z; the slices are added in
-  // order by k_splitk_sum or a deferred column_finalize job.
-  float* part = ws + int64_t(blockIdx.z) * M * N;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int64_t col = n0 + wn + (t & 1) * 16 + (lane & 15);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t row = m0 + wm + (t >> 1) * 16 + 4 * (lane >> 4) + r;
-      if (row < M && col < N) part[row * N + col] = (*accs[t])[r];
-    }
-  }
-}
 
 // Sums the split-K partial products in ascending slice order, one output element a thread, every
 // slice's load issued before the adds; the threads past M * N do the same for the slices' column
@@ -196,26 +44,40 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ ws
 }
 
 // ---------------------------------------------------------------------------------------------
-// The wide-tile GEMM for float4-aligned operands: a block of 2 x 2 waves, each wave a
+// The GEMM: a block of 2 x 2 waves, each wave a
 // (16 WM) x (16 WN) tile as WM x WN MFMA 16x16x4 accumulators, K advancing WK at a time through
 // double-buffered LDS whose row strides (tile width + 16 floats) keep the fragment reads of a
-// wave's two half-groups in disjoint banks. Epilogues as in k_gemm: bias, split-K partials,
-// column (row) sums from the LDS tiles.
+// wave's two half-groups in disjoint banks. Operands may be read transposed in place. Epilogues:
+// bias, split-K partials (summed in slice order by k_splitk_sum or a deferred column finalize:
+// deterministic), column (row) sums from the LDS tiles.
 namespace {
 // One float4 group e of a K tile: the (row, k) element of a KC operand is P[row * ld + k] (four
 // consecutive k), else P[k * ld + row] (four consecutive rows). Out-of-range groups read a
 // clamped address and are zeroed, branch-free.
-template <bool KC, int R, int WK>
+// V: the group is 16-byte aligned and wholly in or out of range, one float4 load; otherwise four
+// clamped scalar loads.
+template <bool KC, int R, int WK, bool V>
 __device__ __forceinline__ float4 wide_load(const float* __restrict__ P, int64_t ld, int64_t rows, int64_t kend,
                                             int64_t r0, int64_t k0, int e) {
   int r, k;
   if (KC) { r = e / (WK / 4); k = (e % (WK / 4)) * 4; } else { k = e / (R / 4); r = (e % (R / 4)) * 4; }
   const int64_t gr = r0 + r, gk = k0 + k;
-  const bool ok = gr < rows && gk < kend;
-  const int64_t cr = KC ? (gr < rows ? gr : rows - 1) : (gr < rows ? gr : rows - 4);
-  const int64_t ck = KC ? (gk < kend ? gk : kend - 4) : (gk < kend ? gk : kend - 1);
-  const float4 f = *reinterpret_cast<const float4*>(KC ? P + cr * ld + ck : P + ck * ld + cr);
-  return ok ? f : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (V) {
+    const bool ok = gr < rows && gk < kend;
+    const int64_t cr = KC ? (gr < rows ? gr : rows - 1) : (gr < rows ? gr : rows - 4);
+    const int64_t ck = KC ? (gk < kend ? gk : kend - 4) : (gk < kend ? gk : kend - 1);
+    const float4 f = *reinterpret_cast<const float4*>(KC ? P + cr * ld + ck : P + ck * ld + cr);
+    return ok ? f : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t rr = KC ? gr : gr + j, kk = KC ? gk + j : gk;
+    const int64_t cr = rr < rows ? rr : rows - 1, ck = kk < kend ? kk : kend - 1;
+    const float x = KC ? P[cr * ld + ck] : P[ck * ld + cr];
+    v[j] = rr < rows && kk < kend ? x : 0.0f;
+  }
+  return make_float4(v[0], v[1], v[2], v[3]);
 }
 template <bool KC, int R, int L, int WK>
 __device__ __forceinline__ void wide_store(float* S, int e, float4 v) {
@@ -232,7 +94,7 @@ __device__ __forceinline__ void wide_store(float* S, int e, float4 v) {
 }
 }  // namespace
 
-template <bool TA, bool TB, int WM, int WN, int WK>
+template <bool TA, bool TB, int WM, int WN, int WK, bool VA, bool VB>
 __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, const float* __restrict__ B,
                                                 float* __restrict__ C, const float* __restrict__ bias, int64_t M,
                                                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
@@ -257,10 +119,10 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   float4 ra[HA], rb[HB];
 #pragma unroll
   for (int h = 0; h < HA; ++h)
-    if (tid + 256 * h < GA) ra[h] = wide_load<!TA, TM, WK>(A, lda, M, kend, m0, kbeg, tid + 256 * h);
+    if (tid + 256 * h < GA) ra[h] = wide_load<!TA, TM, WK, VA>(A, lda, M, kend, m0, kbeg, tid + 256 * h);
 #pragma unroll
   for (int h = 0; h < HB; ++h)
-    if (tid + 256 * h < GB) rb[h] = wide_load<TB, TN, WK>(B, ldb, N, kend, n0, kbeg, tid + 256 * h);
+    if (tid + 256 * h < GB) rb[h] = wide_load<TB, TN, WK, VB>(B, ldb, N, kend, n0, kbeg, tid + 256 * h);
   // Column sums: thread t adds tile column t mod T over the K rows (t / T) per .. + per of each
   // K tile, per = WK / (256 / T).
   const int T = sum_a ? TM : TN;
@@ -280,10 +142,10 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
     if (k0 + WK < kend) {
 #pragma unroll
       for (int h = 0; h < HA; ++h)
-        if (tid + 256 * h < GA) ra[h] = wide_load<!TA, TM, WK>(A, lda, M, kend, m0, k0 + WK, tid + 256 * h);
+        if (tid + 256 * h < GA) ra[h] = wide_load<!TA, TM, WK, VA>(A, lda, M, kend, m0, k0 + WK, tid + 256 * h);
 #pragma unroll
       for (int h = 0; h < HB; ++h)
-        if (tid + 256 * h < GB) rb[h] = wide_load<TB, TN, WK>(B, ldb, N, kend, n0, k0 + WK, tid + 256 * h);
+        if (tid + 256 * h < GB) rb[h] = wide_load<TB, TN, WK, VB>(B, ldb, N, kend, n0, k0 + WK, tid + 256 * h);
     }
     const float* as = As[buf];
     const float* bs = Bs[buf];
@@ -318,9 +180,9 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
       colsum[(ws ? int64_t(blockIdx.z) * width : 0) + base + tid] = v;
     }
   }
+  const float* bz = ws ? nullptr : bias;
   float* out = ws ? ws + int64_t(blockIdx.z) * M * N : C;
   const int64_t ldo = ws ? N : ldc;
-  const float* bz = ws ? nullptr : bias;
 #pragma unroll
   for (int i = 0; i < WM; ++i) {
 #pragma unroll
@@ -340,8 +202,7 @@ namespace {
 // The tile shape and split-K of a GEMM, from measured MI355X timings of the step's shapes: large
 // outputs (and very deep K) take 64 x 64 tiles, outputs up to 2^19 elements 32 x 32, the rest
 // 32 x 64. Split-K, whose slice sum costs a launch unless deferred to a batched finalize, is used
-// when deferred or when K is deep, to fill the chip. Each slice is a multiple of 32 deep (BK of
-// the fallback kernel).
+// when deferred or when K is deep, to fill the chip.
 struct SplitPlan { int wm, wn, wk, split; int64_t chunk; };
 SplitPlan split_plan(int64_t m, int64_t n, int64_t k, bool defer) {
   const int64_t mn = m * n;
@@ -356,7 +217,7 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k, bool defer) {
     want = tiles < blocks / 4 ? (blocks + tiles - 1) / tiles : 1;
   }
   const int64_t split = std::max<int64_t>(1, std::min(want, k / 64));
-  p.chunk = ((k + split - 1) / split + BK - 1) / BK * BK;
+  p.chunk = ((k + split - 1) / split + kSliceAlign - 1) / kSliceAlign * kSliceAlign;
   p.split = int((k + p.chunk - 1) / p.chunk);
   return p;
 }
@@ -394,10 +255,9 @@ void gemm(hipStream_t s, const GemmArgs& g) {
       bad("gemm split-K workspace too small");
     ws = g.workspace;
   }
-  dim3 grid(unsigned((g.n + BN - 1) / BN), unsigned((g.m + BM - 1) / BM), unsigned(split));
-  if (grid.y > 65535) bad("gemm M too large");
   const dim3 wgrid(unsigned((g.n + 32 * plan.wn - 1) / (32 * plan.wn)), unsigned((g.m + 32 * plan.wm - 1) / (32 * plan.wm)),
                    unsigned(split));
+  if (wgrid.y > 65535) bad("gemm M too large");
   const int64_t width = g.sum_a ? g.m : g.n;
   float* csum = g.colsum ? (ws ? ws + int64_t(split) * g.m * g.n : g.colsum) : nullptr;
   // float4 loads need 16-byte aligned groups and a contiguous extent that is a multiple of 4.
@@ -405,34 +265,25 @@ void gemm(hipStream_t s, const GemmArgs& g) {
     return (reinterpret_cast<uintptr_t>(p) % 16 == 0) && ld % 4 == 0 && extent % 4 == 0;
   };
   const bool va = aligned(g.a, g.lda, g.ta ? g.m : g.k), vb = aligned(g.b, g.ldb, g.tb ? g.k : g.n);
-#define MSX_GEMM(TA, TB, VA, VB)                                                                                 \
-  hipLaunchKernelGGL((k_gemm<TA, TB, VA, VB>), grid, dim3(256), 0, s, g.a, g.b, g.c, g.bias, g.m, g.n, g.k, g.lda, \
-                     g.ldb, g.ldc, chunk, ws, csum, g.sum_a)
-#define MSX_GEMM_V(TA, TB)                  \
-  if (va && vb) MSX_GEMM(TA, TB, true, true);        \
-  else if (va) MSX_GEMM(TA, TB, true, false);        \
-  else if (vb) MSX_GEMM(TA, TB, false, true);        \
-  else MSX_GEMM(TA, TB, false, false);
-#define MSX_WIDE(TA, TB, WM, WN, WK)                                                                              \
-  hipLaunchKernelGGL((k_gemm_w<TA, TB, WM, WN, WK>), wgrid, dim3(256), 0, s, g.a, g.b, g.c, g.bias, g.m, g.n, g.k, g.lda, \
-                     g.ldb, g.ldc, chunk, ws, csum, g.sum_a)
+#define MSX_WIDE_V(TA, TB, WM, WN, WK, VA, VB)                                                              \
+  hipLaunchKernelGGL((k_gemm_w<TA, TB, WM, WN, WK, VA, VB>), wgrid, dim3(256), 0, s, g.a, g.b, g.c, g.bias, g.m, g.n, \
+                     g.k, g.lda, g.ldb, g.ldc, chunk, ws, csum, g.sum_a)
+  // float4 variants for both operands aligned, or the right one only; scalar loads otherwise.
+#define MSX_WIDE(TA, TB, WM, WN, WK)                                \
+  if (va && vb) MSX_WIDE_V(TA, TB, WM, WN, WK, true, true);         \
+  else if (vb) MSX_WIDE_V(TA, TB, WM, WN, WK, false, true);         \
+  else MSX_WIDE_V(TA, TB, WM, WN, WK, false, false)
 #define MSX_WIDE_T(TA, TB)                                  \
   if (plan.wm == 2) MSX_WIDE(TA, TB, 2, 2, 16);             \
   else if (plan.wn == 2) MSX_WIDE(TA, TB, 1, 2, 16);        \
   else MSX_WIDE(TA, TB, 1, 1, 32);
-  if (va && vb) {
-    if (!g.ta && !g.tb) { MSX_WIDE_T(false, false) }
-    else if (g.ta && !g.tb) { MSX_WIDE_T(true, false) }
-    else if (!g.ta && g.tb) { MSX_WIDE_T(false, true) }
-    else { MSX_WIDE_T(true, true) }
-  } else if (!g.ta && !g.tb) { MSX_GEMM_V(false, false) }
-  else if (g.ta && !g.tb) { MSX_GEMM_V(true, false) }
-  else if (!g.ta && g.tb) { MSX_GEMM_V(false, true) }
-  else { MSX_GEMM_V(true, true) }
+  if (!g.ta && !g.tb) { MSX_WIDE_T(false, false) }
+  else if (g.ta && !g.tb) { MSX_WIDE_T(true, false) }
+  else if (!g.ta && g.tb) { MSX_WIDE_T(false, true) }
+  else { MSX_WIDE_T(true, true) }
 #undef MSX_WIDE_T
 #undef MSX_WIDE
-#undef MSX_GEMM_V
-#undef MSX_GEMM
+#undef MSX_WIDE_V
   if (split > 1 && !g.defer) {
     const int64_t total = g.m * g.n + (g.colsum ? width : 0);
     const unsigned blocks = unsigned((total + 255) / 256);

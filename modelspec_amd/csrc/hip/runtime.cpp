@@ -520,7 +520,7 @@ void Executor::build() {
           id_bounds_[p.node(ids).name] = it == id_bounds_.end() ? rows : std::min(it->second, rows);
         }
         if (eg_add.count(id)) {
-          const auto [sum_id, addend] = eg_add.at(id);
+          const uint32_t sum_id = eg_add.at(id).first, addend = eg_add.at(id).second;
           what = "EmbeddingGrad+Add %" + std::to_string(id) + " %" + std::to_string(sum_id) + " " + type_string(x.ty);
           push([=](hipStream_t s) { hk::embedding_grad(s, I(ids), F(g), F(sum_id), nn, rows, h, F(addend)); });
           bytes += 8.0 * double(count);

@@ -98,6 +98,45 @@ def test_tied_decoder_gradients(ctx, oracle, v, h, r, n):
     assert within(got[3], want[3], ((ax.T @ adl).T + seg).reshape(-1))[0]
 
 
+@pytest.mark.parametrize("v,h,r,n,g_const", [(1000, 64, 96, 256, True), (1000, 64, 96, 256, False),
+                                             (30522, 128, 832, 4096, True)])
+def test_decoder_cross_entropy_head(ctx, oracle, v, h, r, n, g_const):
+    """The masked-LM head as the step has it: logits = x E^T + b, the cross-entropy loss and
+    gradient, dX, the transposed dW with the bias sums as row sums, added to the embedding
+    gradient; the upstream gradient a constant or computed."""
+    E, x, b = fast_values(61, v * h).reshape(v, h), fast_values(62, r * h).reshape(r, h), fast_values(63, v, 0.5)
+    G = fast_values(64, n * h).reshape(n, h)
+    rng = np.random.default_rng(7)
+    labels = rng.integers(0, v, r).astype(np.int32)
+    w = (rng.random(r) < 0.8).astype(np.float32)
+    ids = embedding_ids("zipf", v, n, rng)
+    p = Prog()
+    Ei, xi, bi = p.input("E", (v, h)), p.input("x", (r, h)), p.input("b", (v,))
+    li, wi, ii, Gi = p.input("labels", (r,), "i32"), p.input("w", (r,)), p.input("ids", (n,), "i32"), p.input("G", (n, h))
+    t1 = p.op("Transpose", [Ei], (h, v))
+    logits = p.op("AddRows", [p.op("MatMul", [xi, t1], (r, v)), bi], (r, v))
+    loss = p.op("CrossEntropy", [logits, li, wi], ())
+    gs = p.scalar(1.0) if g_const else p.op("Mul", [p.scalar(0.5), p.scalar(2.0)], ())
+    dl = p.op("CrossEntropyGrad", [logits, li, wi, gs], (r, v))
+    db = p.op("SumRows", [dl], (v,))
+    dx = p.op("MatMul", [dl, p.op("Transpose", [t1], (v, h))], (r, h))
+    dw = p.op("MatMul", [p.op("Transpose", [xi], (h, r)), dl], (h, v))
+    total = p.op("Add", [p.op("Transpose", [dw], (v, h)), p.op("EmbeddingGrad", [ii, Gi], (v, h), f"[{v}]")], (v, h))
+    inputs = {"E": E, "x": x, "b": b, "labels": labels, "w": w, "ids": ids, "G": G}
+    got, want = both(ctx, oracle, p.out(loss, dx, db, total), inputs, (0, 1, 2, 3))
+    lg = x.astype(np.float64) @ E.T.astype(np.float64) + b
+    pr = np.exp(lg - lg.max(1, keepdims=True))
+    pr /= pr.sum(1, keepdims=True)
+    adl = (pr + (np.arange(v)[None, :] == labels[:, None])) * w[:, None] / w.sum()
+    aE, ax = np.abs(E).astype(np.float64), np.abs(x).astype(np.float64)
+    assert within(got[0], want[0], np.abs(want[0]) + 10)[0]
+    assert within(got[1], want[1], (adl @ aE).reshape(-1) + 1e-3)[0]
+    assert within(got[2], want[2], adl.sum(0) + 1e-3)[0]
+    seg = np.zeros((v, h))
+    np.add.at(seg, ids, np.abs(G).astype(np.float64))
+    assert within(got[3], want[3], ((ax.T @ adl).T + seg).reshape(-1) + 1e-3)[0]
+
+
 @pytest.mark.parametrize("rows,h", [(6, 8), (4096, 128), (832, 128), (33, 200), (100, 768)])
 def test_layer_norm_family(ctx, oracle, rows, h):
     x = fast_values(6, rows * h).reshape(rows, h)
