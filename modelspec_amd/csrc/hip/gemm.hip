@@ -54,8 +54,8 @@ namespace {
 // One float4 group e of a K tile: the (row, k) element of a KC operand is P[row * ld + k] (four
 // consecutive k), else P[k * ld + row] (four consecutive rows). Out-of-range groups read a
 // clamped address and are zeroed, branch-free.
-// V: the group is 16-byte aligned and wholly in or out of range, one float4 load; otherwise four
-// clamped scalar loads.
+// V: the group is 16-byte aligned and wholly in or out of range, or its out-of-range part lies in
+// zero padding of the rows: one float4 load; otherwise four clamped scalar loads.
 template <bool KC, int R, int WK, bool V>
 __device__ __forceinline__ float4 wide_load(const float* __restrict__ P, int64_t ld, int64_t rows, int64_t kend,
                                             int64_t r0, int64_t k0, int e) {
@@ -64,8 +64,9 @@ __device__ __forceinline__ float4 wide_load(const float* __restrict__ P, int64_t
   const int64_t gr = r0 + r, gk = k0 + k;
   if (V) {
     const bool ok = gr < rows && gk < kend;
-    const int64_t cr = KC ? (gr < rows ? gr : rows - 1) : (gr < rows ? gr : rows - 4);
-    const int64_t ck = KC ? (gk < kend ? gk : kend - 4) : (gk < kend ? gk : kend - 1);
+    // A group past the end reads the aligned group holding the last element instead.
+    const int64_t cr = KC ? (gr < rows ? gr : rows - 1) : (gr < rows ? gr : (rows - 1) & ~int64_t(3));
+    const int64_t ck = KC ? (gk < kend ? gk : (kend - 1) & ~int64_t(3)) : (gk < kend ? gk : kend - 1);
     const float4 f = *reinterpret_cast<const float4*>(KC ? P + cr * ld + ck : P + ck * ld + cr);
     return ok ? f : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
@@ -261,10 +262,12 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   const int64_t width = g.sum_a ? g.m : g.n;
   float* csum = g.colsum ? (ws ? ws + int64_t(split) * g.m * g.n : g.colsum) : nullptr;
   // float4 loads need 16-byte aligned groups and a contiguous extent that is a multiple of 4.
+  // (A zero-padded operand may be read up to its leading dimension.)
   auto aligned = [](const float* p, int64_t ld, int64_t extent) {
     return (reinterpret_cast<uintptr_t>(p) % 16 == 0) && ld % 4 == 0 && extent % 4 == 0;
   };
-  const bool va = aligned(g.a, g.lda, g.ta ? g.m : g.k), vb = aligned(g.b, g.ldb, g.tb ? g.k : g.n);
+  const bool va = aligned(g.a, g.lda, g.pad_a ? g.lda : (g.ta ? g.m : g.k));
+  const bool vb = aligned(g.b, g.ldb, g.pad_b ? g.ldb : (g.tb ? g.k : g.n));
 #define MSX_WIDE_V(TA, TB, WM, WN, WK, VA, VB)                                                              \
   hipLaunchKernelGGL((k_gemm_w<TA, TB, WM, WN, WK, VA, VB>), wgrid, dim3(256), 0, s, g.a, g.b, g.c, g.bias, g.m, g.n, \
                      g.k, g.lda, g.ldb, g.ldc, chunk, ws, csum, g.sum_a)

@@ -33,6 +33,8 @@ struct GemmArgs {
   float* workspace; int64_t workspace_floats;
   float* colsum;
   bool sum_a, defer;
+  // The operand's rows are zero from its contiguous extent up to its leading dimension.
+  bool pad_a, pad_b;
 };
 // The split-K factor the launcher uses (with `defer` as in GemmArgs).
 int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer = false);
@@ -92,12 +94,13 @@ void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v
                    int64_t L, int64_t S, int64_t H, int64_t heads);
 void prepare_attention();
 
-// Cross-entropy: stats = [rows, 2] (max, total); den = [1] f32 weight sum rounded from f64.
-void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, int64_t v);
+// Cross-entropy over logits [rows, v] with row pitch ld (>= v): stats = [rows, 2] (max, total);
+// den = [1] f32 weight sum rounded from f64; the gradient o has row pitch ld too.
+void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, int64_t v, int64_t ld);
 void ce_loss(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats,
-             float* loss, float* den, int64_t rows, int64_t v);
+             float* loss, float* den, int64_t rows, int64_t v, int64_t ld);
 void ce_grad(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats,
-             const float* den, const float* g, float* o, int64_t rows, int64_t v);
+             const float* den, const float* g, float* o, int64_t rows, int64_t v, int64_t ld);
 
 void softmax(hipStream_t s, const float* x, float* o, int64_t rows, int64_t k);
 void softmax_grad(hipStream_t s, const float* y, const float* g, float* o, int64_t rows, int64_t k);

@@ -559,10 +559,11 @@ void dropout(hipStream_t s, const float* x, float* o, int64_t n, const int32_t* 
 // ---------------------------------------------------------------------------------------------
 // Cross-entropy. Row statistics once per logits tensor; the loss sums in f64 in one block.
 // Row maximum, then the sum of exp(x - max), each pass with eight loads in flight per thread.
-__global__ __launch_bounds__(256) void k_ce_stats(const float* __restrict__ x, float* __restrict__ stats, int64_t v) {
+__global__ __launch_bounds__(256) void k_ce_stats(const float* __restrict__ x, float* __restrict__ stats, int64_t v,
+                                                  int64_t ld) {
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
-  const float* row = x + r * v;
+  const float* row = x + r * ld;
   const int tid = threadIdx.x;
   float m = -INFINITY;
   for (int64_t c0 = 0; c0 < v; c0 += 256 * 8) {
@@ -596,21 +597,22 @@ __global__ __launch_bounds__(256) void k_ce_stats(const float* __restrict__ x, f
   __syncthreads();
   if (tid == 0) { stats[2 * r] = m; stats[2 * r + 1] = (red[0] + red[1]) + (red[2] + red[3]); }
 }
-void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, int64_t v) {
+void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, int64_t v, int64_t ld) {
   if (rows <= 0) return;
   if (rows > 2147483647) bad("cross_entropy rows");
-  hipLaunchKernelGGL(k_ce_stats, dim3(unsigned(rows)), dim3(256), 0, s, logits, stats, v);
+  if (ld < v) bad("cross_entropy row pitch");
+  hipLaunchKernelGGL(k_ce_stats, dim3(unsigned(rows)), dim3(256), 0, s, logits, stats, v, ld);
 }
 
 __global__ __launch_bounds__(256) void k_ce_loss(const float* __restrict__ x, const int32_t* __restrict__ labels,
                                                  const float* __restrict__ w, const float* __restrict__ stats,
                                                  float* __restrict__ loss, float* __restrict__ den_out, int64_t rows,
-                                                 int64_t v) {
+                                                 int64_t v, int64_t ld) {
   __shared__ double num_s[256], den_s[256];
   double num = 0.0, den = 0.0;
   for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) {
     int32_t lab = labels[r];
-    float xl = (lab >= 0 && lab < v) ? x[r * v + lab] : 0.0f;
+    float xl = (lab >= 0 && lab < v) ? x[r * ld + lab] : 0.0f;
     float l = stats[2 * r] + logf(stats[2 * r + 1]) - xl;
     num = __builtin_fma(double(w[r]), double(l), num);
     den += double(w[r]);
@@ -632,13 +634,13 @@ __global__ __launch_bounds__(256) void k_ce_loss(const float* __restrict__ x, co
   }
 }
 void ce_loss(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats, float* loss,
-             float* den, int64_t rows, int64_t v) {
-  hipLaunchKernelGGL(k_ce_loss, dim3(1), dim3(256), 0, s, logits, labels, w, stats, loss, den, rows, v);
+             float* den, int64_t rows, int64_t v, int64_t ld) {
+  hipLaunchKernelGGL(k_ce_loss, dim3(1), dim3(256), 0, s, logits, labels, w, stats, loss, den, rows, v, ld);
 }
 
 __global__ void k_ce_grad(const float* __restrict__ x, const int32_t* __restrict__ labels, const float* __restrict__ w,
                           const float* __restrict__ stats, const float* __restrict__ den, const float* __restrict__ g,
-                          float* __restrict__ o, int64_t v) {
+                          float* __restrict__ o, int64_t v, int64_t ld) {
   const int64_t r = blockIdx.y;
   const float d = den[0];
   const float scale = d == 0.0f ? 0.0f : g[0] * w[r] / d;
@@ -646,15 +648,15 @@ __global__ void k_ce_grad(const float* __restrict__ x, const int32_t* __restrict
   const int32_t lab = labels[r];
   for (int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; c < v; c += int64_t(gridDim.x) * blockDim.x) {
     float target = c == lab ? 1.0f : 0.0f;
-    o[r * v + c] = d == 0.0f ? 0.0f : scale * (expf(x[r * v + c] - mx) / total - target);
+    o[r * ld + c] = d == 0.0f ? 0.0f : scale * (expf(x[r * ld + c] - mx) / total - target);
   }
 }
 void ce_grad(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats,
-             const float* den, const float* g, float* o, int64_t rows, int64_t v) {
+             const float* den, const float* g, float* o, int64_t rows, int64_t v, int64_t ld) {
   if (rows <= 0) return;
   if (rows > 65535) bad("cross_entropy gradient rows");
   dim3 grid(unsigned(std::min<int64_t>((v + 255) / 256, 64)), unsigned(rows));
-  hipLaunchKernelGGL(k_ce_grad, grid, dim3(256), 0, s, logits, labels, w, stats, den, g, o, v);
+  hipLaunchKernelGGL(k_ce_grad, grid, dim3(256), 0, s, logits, labels, w, stats, den, g, o, v, ld);
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -286,6 +286,42 @@ void Executor::build() {
     it->second[size_t(slot)] = int64_t(x.id);
   }
 
+  // Row pitch: a wide 2-D value whose rows are not a whole number of float4 groups gets its rows
+  // padded to 64 floats when its producer and every reader take a leading dimension (GEMMs, the
+  // cross-entropy kernels), so that GEMMs load it with aligned float4s.
+  std::set<uint32_t> grad_values;
+  if (is_step_)
+    for (auto& pg : st.gradients) grad_values.insert(pg.second);
+  std::map<uint32_t, int64_t> pitch;
+  for (size_t k = 0; k < n; ++k) {
+    const Node& x = p.nodes[k];
+    if (!need[k] || x.ty.rank() != 2 || x.ty.dtype != DType::F32 || outputs.count(x.id) || grad_values.count(x.id)) continue;
+    const int64_t rows = x.ty.shape[0], cols = x.ty.shape[1];
+    if (cols % 4 == 0 || rows * cols < (int64_t(1) << 16)) continue;
+    const bool producer = (x.op == Op::AddRows && mm_fused.count(x.operands[0])) ||
+                          (x.op == Op::MatMul && !mm_fused.count(x.id) && !mm_transposed.count(x.id)) ||
+                          x.op == Op::CrossEntropyGrad;
+    if (!producer) continue;
+    bool readers = true;
+    for (auto c : consumers[k]) {
+      const Node& cn = p.nodes[c];
+      if (cn.op == Op::CrossEntropy || cn.op == Op::CrossEntropyGrad) {
+        readers = readers && cn.operands[0] == x.id && cn.operands[1] != x.id && cn.operands[2] != x.id;
+      } else if (cn.op == Op::MatMul) {
+      } else if (cn.op == Op::Transpose && folded.count(cn.id)) {
+        for (auto c2 : consumers[c]) readers = readers && p.nodes[c2].op == Op::MatMul;
+      } else if (cn.op == Op::SumRows && colsum_fused.count(cn.id)) {
+      } else {
+        readers = false;
+      }
+    }
+    if (readers) pitch[x.id] = (cols + 63) / 64 * 64;
+  }
+  auto ld_of = [&](uint32_t v) {
+    auto it = pitch.find(v);
+    return it != pitch.end() ? it->second : p.node(v).ty.shape.back();
+  };
+
   // --- storage ------------------------------------------------------------------------------
   std::map<uint32_t, float> constants;
   for (size_t k = 0; k < n; ++k) {
@@ -315,7 +351,7 @@ void Executor::build() {
         break;
       default:
         if (folded.count(x.id) || mm_fused.count(x.id) || mm_transposed.count(x.id) || eg_add.count(x.id)) break;
-        token_[x.id] = arena_.reserve(size_t(x.ty.count()) * 4);
+        token_[x.id] = arena_.reserve(size_t(pitch.count(x.id) ? x.ty.shape[0] * pitch.at(x.id) : x.ty.count()) * 4);
         break;
     }
   }
@@ -435,17 +471,23 @@ void Executor::build() {
         int64_t M = m.ty.shape[0], N = m.ty.shape[1], K = shape(m.operands[0])[1];
         hk::GemmArgs g{};
         uint32_t asrc = ra.src, bsrc = rb.src;
+        // Leading dimensions are the sources' row pitches (their widths unless padded).
         if (!swap) {
-          g.m = M; g.n = N; g.k = K; g.ldc = N;
-          g.ta = ra.flip; g.lda = ra.flip ? M : K;
-          g.tb = rb.flip; g.ldb = rb.flip ? K : N;
+          g.m = M; g.n = N; g.k = K;
+          g.ta = ra.flip;
+          g.tb = rb.flip;
         } else {
           // C^T [N, M] = op(B)^T op(A)^T: B's source becomes the left operand, A's the right.
-          g.m = N; g.n = M; g.k = K; g.ldc = M;
-          g.ta = !rb.flip; g.lda = rb.flip ? K : N;
-          g.tb = !ra.flip; g.ldb = ra.flip ? M : K;
+          g.m = N; g.n = M; g.k = K;
+          g.ta = !rb.flip;
+          g.tb = !ra.flip;
           std::swap(asrc, bsrc);
         }
+        g.lda = ld_of(asrc);
+        g.ldb = ld_of(bsrc);
+        g.ldc = ld_of(out_id);
+        g.pad_a = pitch.count(asrc) != 0;
+        g.pad_b = pitch.count(bsrc) != 0;
         const int64_t cs_id = x.op == Op::MatMul && colsum_of.count(id) ? int64_t(colsum_of.at(id)) : -1;
         g.sum_a = swap;  // the column sums of B are the row sums of the swapped left operand
         int64_t bias_id = fused ? int64_t(o[1]) : -1;
@@ -678,13 +720,15 @@ void Executor::build() {
       case Op::CrossEntropy: case Op::CrossEntropyGrad: {
         uint32_t lg = o[0], lab = o[1], w = o[2];
         int64_t rows = shape(lg)[0], v = shape(lg)[1];
+        const int64_t ld = ld_of(lg);
+        if (x.op == Op::CrossEntropyGrad && ld_of(id) != ld) throw IrError("cross-entropy gradient pitch differs from its logits'");
         if (p.node(lab).op == Op::Input) id_bounds_["#labels:" + p.node(lab).name] = v;
         if (p.node(w).op == Op::Input) id_bounds_["#weights:" + p.node(w).name] = 0;
         bool have = ce_stats_tok.count(lg) != 0;
         if (!have) {
           ce_stats_tok[lg] = R(size_t(rows) * 8);
           void* st2 = ce_stats_tok[lg];
-          push([=](hipStream_t s) { hk::ce_stats(s, F(lg), static_cast<float*>(A(st2)), rows, v); });
+          push([=](hipStream_t s) { hk::ce_stats(s, F(lg), static_cast<float*>(A(st2)), rows, v, ld); });
         }
         void* stats = ce_stats_tok[lg];
         auto dkey = std::make_pair(lg, w);
@@ -693,19 +737,19 @@ void Executor::build() {
         void* den = ce_den_tok[dkey];
         if (x.op == Op::CrossEntropy) {
           push([=](hipStream_t s) {
-            hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(stats)), F(id), static_cast<float*>(A(den)), rows, v);
+            hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(stats)), F(id), static_cast<float*>(A(den)), rows, v, ld);
           });
         } else {
           if (!have_den) {
             void* scratch = R(4);
             push([=](hipStream_t s) {
               hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(stats)), static_cast<float*>(A(scratch)),
-                          static_cast<float*>(A(den)), rows, v);
+                          static_cast<float*>(A(den)), rows, v, ld);
             });
           }
           uint32_t g = o[3];
           push([=](hipStream_t s) {
-            hk::ce_grad(s, F(lg), I(lab), F(w), static_cast<float*>(A(stats)), static_cast<float*>(A(den)), F(g), F(id), rows, v);
+            hk::ce_grad(s, F(lg), I(lab), F(w), static_cast<float*>(A(stats)), static_cast<float*>(A(den)), F(g), F(id), rows, v, ld);
           });
         }
         break;
