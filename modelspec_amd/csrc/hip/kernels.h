@@ -97,8 +97,14 @@ void prepare_attention();
 // Cross-entropy over logits [rows, v] with row pitch ld (>= v): stats = [rows, 2] (max, total);
 // den = [1] f32 weight sum rounded from f64; the gradient o has row pitch ld too.
 void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, int64_t v, int64_t ld);
+// With rowloss non-null the per-row loss terms come from there (ce_rows) instead of stats and logits.
 void ce_loss(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats,
-             float* loss, float* den, int64_t rows, int64_t v, int64_t ld);
+             float* loss, float* den, int64_t rows, int64_t v, int64_t ld, const float* rowloss = nullptr);
+// One pass per row: stats, the row loss terms (rowloss non-null) and the gradient (grad non-null,
+// with the upstream gradient scalar g). Needs ce_rows_fits and 16-byte aligned logits and grad.
+bool ce_rows_fits(int64_t v, int64_t ld);
+void ce_rows(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* g, float* stats,
+             float* rowloss, float* grad, int64_t rows, int64_t v, int64_t ld);
 void ce_grad(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats,
              const float* den, const float* g, float* o, int64_t rows, int64_t v, int64_t ld);
 

@@ -607,13 +607,18 @@ void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, in
 __global__ __launch_bounds__(256) void k_ce_loss(const float* __restrict__ x, const int32_t* __restrict__ labels,
                                                  const float* __restrict__ w, const float* __restrict__ stats,
                                                  float* __restrict__ loss, float* __restrict__ den_out, int64_t rows,
-                                                 int64_t v, int64_t ld) {
+                                                 int64_t v, int64_t ld, const float* __restrict__ rowloss) {
   __shared__ double num_s[256], den_s[256];
   double num = 0.0, den = 0.0;
   for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) {
-    int32_t lab = labels[r];
-    float xl = (lab >= 0 && lab < v) ? x[r * ld + lab] : 0.0f;
-    float l = stats[2 * r] + logf(stats[2 * r + 1]) - xl;
+    float l;
+    if (rowloss) {
+      l = rowloss[r];
+    } else {
+      int32_t lab = labels[r];
+      float xl = (lab >= 0 && lab < v) ? x[r * ld + lab] : 0.0f;
+      l = stats[2 * r] + logf(stats[2 * r + 1]) - xl;
+    }
     num = __builtin_fma(double(w[r]), double(l), num);
     den += double(w[r]);
   }
@@ -634,8 +639,8 @@ __global__ __launch_bounds__(256) void k_ce_loss(const float* __restrict__ x, co
   }
 }
 void ce_loss(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats, float* loss,
-             float* den, int64_t rows, int64_t v, int64_t ld) {
-  hipLaunchKernelGGL(k_ce_loss, dim3(1), dim3(256), 0, s, logits, labels, w, stats, loss, den, rows, v, ld);
+             float* den, int64_t rows, int64_t v, int64_t ld, const float* rowloss) {
+  hipLaunchKernelGGL(k_ce_loss, dim3(1), dim3(256), 0, s, logits, labels, w, stats, loss, den, rows, v, ld, rowloss);
 }
 
 __global__ void k_ce_grad(const float* __restrict__ x, const int32_t* __restrict__ labels, const float* __restrict__ w,
@@ -657,6 +662,109 @@ void ce_grad(hipStream_t s, const float* logits, const int32_t* labels, const fl
   if (rows > 65535) bad("cross_entropy gradient rows");
   dim3 grid(unsigned(std::min<int64_t>((v + 255) / 256, 64)), unsigned(rows));
   hipLaunchKernelGGL(k_ce_grad, grid, dim3(256), 0, s, logits, labels, w, stats, den, g, o, v, ld);
+}
+
+// Cross-entropy of whole rows in one pass over the logits: a block of kCeThreads holds its row in
+// registers (NV float4 a thread), takes the max and the sum of exp, writes them to stats, the
+// row's loss term max + log(sum) - x[label] to rowloss (when non-null) and, when grad is
+// non-null, the gradient g w / den (exp(x - max) / sum - onehot), the quotient taken as a product
+// with the reciprocal of the sum, zero in the padding columns. den is formed in each block exactly
+// as k_ce_loss forms it.
+constexpr int kCeThreads = 1024;
+template <int NV>
+__global__ __launch_bounds__(kCeThreads) void k_ce_rows(const float* __restrict__ x, const int32_t* __restrict__ labels,
+                                                        const float* __restrict__ w, const float* __restrict__ g,
+                                                        float* __restrict__ stats, float* __restrict__ rowloss,
+                                                        float* __restrict__ grad, int64_t rows, int64_t v, int64_t ld) {
+  constexpr int W = kCeThreads / 64;
+  __shared__ float red[W];
+  __shared__ double dred[256];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float4* row = reinterpret_cast<const float4*>(x + r * ld);
+  const int64_t nq = (v + 3) / 4;
+  float e[NV][4];
+#pragma unroll
+  for (int u = 0; u < NV; ++u) {
+    const int64_t q = tid + int64_t(kCeThreads) * u;
+    const float4 f = row[q < nq ? q : nq - 1];
+    e[u][0] = f.x; e[u][1] = f.y; e[u][2] = f.z; e[u][3] = f.w;
+  }
+  auto col = [&](int u, int c) { return 4 * (tid + int64_t(kCeThreads) * u) + c; };
+  float m = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < NV; ++u)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (col(u, c) < v) m = fmaxf(m, e[u][c]);
+  m = wave_max(m);
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  m = red[0];
+#pragma unroll
+  for (int i = 1; i < W; ++i) m = fmaxf(m, red[i]);
+  __syncthreads();
+  float sum = 0.0f;
+#pragma unroll
+  for (int u = 0; u < NV; ++u)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      e[u][c] = col(u, c) < v ? expf(e[u][c] - m) : 0.0f;
+      sum += e[u][c];
+    }
+  sum = wave_sum(sum);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < W; i += 2) total += red[i] + red[i + 1];
+  const int32_t lab = labels[r];
+  if (tid == 0) {
+    stats[2 * r] = m;
+    stats[2 * r + 1] = total;
+    if (rowloss) rowloss[r] = m + logf(total) - ((lab >= 0 && lab < v) ? x[r * ld + lab] : 0.0f);
+  }
+  if (!grad) return;
+  double dd = 0.0;
+  if (tid < 256)
+    for (int64_t i = tid; i < rows; i += 256) dd += double(w[i]);
+  if (tid < 256) dred[tid] = dd;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (tid < o) dred[tid] += dred[tid + o];
+    __syncthreads();
+  }
+  const float d = float(dred[0]);
+  const float scale = d == 0.0f ? 0.0f : g[0] * w[r] / d, inv = 1.0f / total;
+  float4* out = reinterpret_cast<float4*>(grad + r * ld);
+  auto gv = [&](int u, int c) {
+    const int64_t cc = col(u, c);
+    if (cc >= v || d == 0.0f) return 0.0f;
+    return scale * (e[u][c] * inv - (cc == lab ? 1.0f : 0.0f));
+  };
+#pragma unroll
+  for (int u = 0; u < NV; ++u) {
+    const int64_t q = tid + int64_t(kCeThreads) * u;
+    if (q < nq) out[q] = make_float4(gv(u, 0), gv(u, 1), gv(u, 2), gv(u, 3));
+  }
+}
+
+bool ce_rows_fits(int64_t v, int64_t ld) { return ld % 4 == 0 && (v + 3) / 4 <= int64_t(kCeThreads) * 8; }
+
+void ce_rows(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* g, float* stats,
+             float* rowloss, float* grad, int64_t rows, int64_t v, int64_t ld) {
+  if (rows <= 0) return;
+  if (rows > 2147483647) bad("cross_entropy rows");
+  if (!ce_rows_fits(v, ld) || reinterpret_cast<uintptr_t>(logits) % 16 || (grad && reinterpret_cast<uintptr_t>(grad) % 16))
+    bad("cross_entropy row kernel needs float4-aligned rows of at most 32768 classes");
+  if (grad && !g) bad("cross_entropy gradient without the upstream gradient");
+  const int64_t per = ((v + 3) / 4 + kCeThreads - 1) / kCeThreads;
+#define MSX_CER(NV) hipLaunchKernelGGL(k_ce_rows<NV>, dim3(unsigned(rows)), dim3(kCeThreads), 0, s, logits, labels, w, g, \
+                                       stats, rowloss, grad, rows, v, ld)
+  if (per <= 2) MSX_CER(2);
+  else if (per <= 4) MSX_CER(4);
+  else MSX_CER(8);
+#undef MSX_CER
 }
 
 // ---------------------------------------------------------------------------------------------

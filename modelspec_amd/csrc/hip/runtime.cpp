@@ -286,6 +286,16 @@ void Executor::build() {
     it->second[size_t(slot)] = int64_t(x.id);
   }
 
+  // Cross-entropy nodes over the same (logits, labels, weights): the loss and the gradient.
+  struct CeGroup { int64_t loss = -1, grad = -1; bool done = false, grad_done = false; };
+  std::map<std::array<uint32_t, 3>, CeGroup> ce_groups;
+  for (size_t k = 0; k < n; ++k) {
+    const Node& x = p.nodes[k];
+    if (!need[k] || (x.op != Op::CrossEntropy && x.op != Op::CrossEntropyGrad)) continue;
+    auto& grp = ce_groups[{x.operands[0], x.operands[1], x.operands[2]}];
+    if (x.op == Op::CrossEntropy && grp.loss < 0) grp.loss = x.id;
+    if (x.op == Op::CrossEntropyGrad && grp.grad < 0) grp.grad = x.id;
+  }
   // Row pitch: a wide 2-D value whose rows are not a whole number of float4 groups gets its rows
   // padded to 64 floats when its producer and every reader take a leading dimension (GEMMs, the
   // cross-entropy kernels), so that GEMMs load it with aligned float4s.
@@ -724,6 +734,43 @@ void Executor::build() {
         if (x.op == Op::CrossEntropyGrad && ld_of(id) != ld) throw IrError("cross-entropy gradient pitch differs from its logits'");
         if (p.node(lab).op == Op::Input) id_bounds_["#labels:" + p.node(lab).name] = v;
         if (p.node(w).op == Op::Input) id_bounds_["#weights:" + p.node(w).name] = 0;
+        // One pass over the rows where the kernel fits: at the group's first node, the statistics,
+        // the loss terms when the group has a loss, and the gradient when it has one whose upstream
+        // gradient is available (a constant, or this node's own operand).
+        auto& grp = ce_groups.at({lg, lab, w});
+        if (hk::ce_rows_fits(v, ld) && (grp.loss == int64_t(id) || grp.grad == int64_t(id))) {
+          if (x.op == Op::CrossEntropyGrad && grp.grad_done) break;
+          if (!grp.done || (x.op == Op::CrossEntropyGrad && !grp.grad_done)) {
+            const int64_t gnode = grp.grad;
+            const bool with_grad = gnode >= 0 && !grp.grad_done &&
+                                   (x.op == Op::CrossEntropyGrad || p.node(p.node(uint32_t(gnode)).operands[3]).op == Op::Scalar);
+            const bool with_loss = grp.loss >= 0 && !grp.done;
+            if (!ce_stats_tok.count(lg)) ce_stats_tok[lg] = R(size_t(rows) * 8);
+            void* st2 = ce_stats_tok.at(lg);
+            void* rl = with_loss ? R(size_t(rows) * 4) : nullptr;
+            const uint32_t gsc = with_grad ? p.node(uint32_t(gnode)).operands[3] : 0;
+            const int64_t gout = with_grad ? gnode : -1;
+            what = std::string("CrossEntropyRows") + (with_loss ? " loss %" + std::to_string(grp.loss) : "") +
+                   (with_grad ? " grad %" + std::to_string(gnode) : "") + " " + type_string(p.node(lg).ty);
+            push([=](hipStream_t s) {
+              hk::ce_rows(s, F(lg), I(lab), F(w), with_grad ? F(gsc) : nullptr, static_cast<float*>(A(st2)),
+                          rl ? static_cast<float*>(A(rl)) : nullptr, gout >= 0 ? F(uint32_t(gout)) : nullptr, rows, v, ld);
+            });
+            if (with_loss) {
+              auto dkey = std::make_pair(lg, w);
+              if (!ce_den_tok.count(dkey)) ce_den_tok[dkey] = R(4);
+              void* den = ce_den_tok.at(dkey);
+              const uint32_t lid = uint32_t(grp.loss);
+              push([=](hipStream_t s) {
+                hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(st2)), F(lid), static_cast<float*>(A(den)), rows,
+                            v, ld, static_cast<float*>(A(rl)));
+              });
+            }
+            grp.done = true;
+            grp.grad_done = grp.grad_done || with_grad;
+          }
+          break;
+        }
         bool have = ce_stats_tok.count(lg) != 0;
         if (!have) {
           ce_stats_tok[lg] = R(size_t(rows) * 8);
