@@ -15,10 +15,62 @@ constexpr int kSliceAlign = 32;  // split-K slices are multiples of this many K 
 // Sums the split-K partial products in ascending slice order, one output element a thread, every
 // slice's load issued before the adds; the threads past M * N do the same for the slices' column
 // (row) sums.
+// The output epilogue of element (row, col) of a product v: + bias[col], then the activation
+// (GELU or ReLU, the pre-activation value also stored to pre_out when asked; or their gradient
+// with respect to the pre-activation pre_in[row, col], v the incoming gradient), then addend[row,
+// col] + v. Every step rounds as the separate kernel would (the same operation order).
+__device__ __forceinline__ float gemm_epilogue(const GemmEpi& e, float v, int64_t row, int64_t col, int64_t ldc) {
+  if (e.bias) v = v + e.bias[col];
+  const int64_t at = row * ldc + col;
+  switch (e.act) {
+    case EPI_GELU: if (e.pre_out) e.pre_out[at] = v; v = d_gelu(v); break;
+    case EPI_RELU: if (e.pre_out) e.pre_out[at] = v; v = v > 0.0f ? v : 0.0f; break;
+    case EPI_GELU_GRAD: v = d_gelu_grad(e.pre_in[at], v); break;
+    case EPI_RELU_GRAD: v = e.pre_in[at] > 0.0f ? v : 0.0f; break;
+    default: break;
+  }
+  if (e.addend) v = e.addend[at] + v;
+  return v;
+}
+// The same on four consecutive columns (col a multiple of 4, 16-byte aligned rows).
+__device__ __forceinline__ float4 gemm_epilogue4(const GemmEpi& e, float4 v, int64_t row, int64_t col, int64_t ldc) {
+  if (e.bias) {
+    const float4 b = *reinterpret_cast<const float4*>(e.bias + col);
+    v = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
+  }
+  const int64_t at = row * ldc + col;
+  switch (e.act) {
+    case EPI_GELU:
+      if (e.pre_out) *reinterpret_cast<float4*>(e.pre_out + at) = v;
+      v = make_float4(d_gelu(v.x), d_gelu(v.y), d_gelu(v.z), d_gelu(v.w));
+      break;
+    case EPI_RELU:
+      if (e.pre_out) *reinterpret_cast<float4*>(e.pre_out + at) = v;
+      v = make_float4(v.x > 0.0f ? v.x : 0.0f, v.y > 0.0f ? v.y : 0.0f, v.z > 0.0f ? v.z : 0.0f, v.w > 0.0f ? v.w : 0.0f);
+      break;
+    case EPI_GELU_GRAD: {
+      const float4 p = *reinterpret_cast<const float4*>(e.pre_in + at);
+      v = make_float4(d_gelu_grad(p.x, v.x), d_gelu_grad(p.y, v.y), d_gelu_grad(p.z, v.z), d_gelu_grad(p.w, v.w));
+      break;
+    }
+    case EPI_RELU_GRAD: {
+      const float4 p = *reinterpret_cast<const float4*>(e.pre_in + at);
+      v = make_float4(p.x > 0.0f ? v.x : 0.0f, p.y > 0.0f ? v.y : 0.0f, p.z > 0.0f ? v.z : 0.0f, p.w > 0.0f ? v.w : 0.0f);
+      break;
+    }
+    default: break;
+  }
+  if (e.addend) {
+    const float4 a = *reinterpret_cast<const float4*>(e.addend + at);
+    v = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
+  }
+  return v;
+}
+
 template <int SPLIT>
-__global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ ws, float* __restrict__ C,
-                                                    const float* __restrict__ bias, int64_t M, int64_t N, int64_t ldc,
-                                                    int splits, float* __restrict__ colsum, int64_t width) {
+__global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ ws, float* __restrict__ C, GemmEpi epi,
+                                                    int64_t M, int64_t N, int64_t ldc, int splits,
+                                                    float* __restrict__ colsum, int64_t width) {
   const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
   const int64_t mn = M * N;
   const bool cs = e >= mn;
@@ -39,7 +91,7 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ ws
     colsum[e - mn] = s;
   } else {
     const int64_t row = e / N, col = e - row * N;
-    C[row * ldc + col] = bias ? s + bias[col] : s;
+    C[row * ldc + col] = gemm_epilogue(epi, s, row, col, ldc);
   }
 }
 
@@ -97,15 +149,18 @@ __device__ __forceinline__ void wide_store(float* S, int e, float4 v) {
 
 template <bool TA, bool TB, int WM, int WN, int WK, bool VA, bool VB>
 __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, const float* __restrict__ B,
-                                                float* __restrict__ C, const float* __restrict__ bias, int64_t M,
+                                                float* __restrict__ C, GemmEpi epi, int64_t M,
                                                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                                                 int64_t kchunk, float* __restrict__ ws, float* __restrict__ colsum,
-                                                bool sum_a) {
-  constexpr int TM = 32 * WM, TN = 32 * WN, LA = TM + 16, LB = TN + 16;
+                                                bool sum_a, bool vo) {
+  constexpr int TM = 32 * WM, TN = 32 * WN, LA = TM + 16, LB = TN + 16, LC = TN + 4;
   constexpr int GA = TM * WK / 4, GB = TN * WK / 4;              // float4 groups a K tile
   constexpr int HA = (GA + 255) / 256, HB = (GB + 255) / 256;     // a thread's groups
-  __shared__ float As[2][WK * LA];
-  __shared__ float Bs[2][WK * LB];
+  // The K tiles (double-buffered), and afterwards the output tile on its way to memory.
+  __shared__ float smem[2 * WK * LA + 2 * WK * LB];
+  static_assert(TM * LC <= 2 * WK * LA + 2 * WK * LB, "output tile exceeds the LDS of the K tiles");
+  float* const As0 = smem;                 // As(buf) = As0 + buf WK LA
+  float* const Bs0 = smem + 2 * WK * LA;   // Bs(buf) = Bs0 + buf WK LB
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t m0 = int64_t(blockIdx.y) * TM, n0 = int64_t(blockIdx.x) * TN;
   const int64_t kbeg = int64_t(blockIdx.z) * kchunk;
@@ -135,10 +190,10 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   for (int64_t k0 = kbeg; k0 < kend; k0 += WK) {
 #pragma unroll
     for (int h = 0; h < HA; ++h)
-      if (tid + 256 * h < GA) wide_store<!TA, TM, LA, WK>(As[buf], tid + 256 * h, ra[h]);
+      if (tid + 256 * h < GA) wide_store<!TA, TM, LA, WK>(As0 + buf * (WK * LA), tid + 256 * h, ra[h]);
 #pragma unroll
     for (int h = 0; h < HB; ++h)
-      if (tid + 256 * h < GB) wide_store<TB, TN, LB, WK>(Bs[buf], tid + 256 * h, rb[h]);
+      if (tid + 256 * h < GB) wide_store<TB, TN, LB, WK>(Bs0 + buf * (WK * LB), tid + 256 * h, rb[h]);
     __syncthreads();
     if (k0 + WK < kend) {
 #pragma unroll
@@ -148,8 +203,8 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
       for (int h = 0; h < HB; ++h)
         if (tid + 256 * h < GB) rb[h] = wide_load<TB, TN, WK, VB>(B, ldb, N, kend, n0, k0 + WK, tid + 256 * h);
     }
-    const float* as = As[buf];
-    const float* bs = Bs[buf];
+    const float* as = As0 + buf * (WK * LA);
+    const float* bs = Bs0 + buf * (WK * LB);
 #pragma unroll
     for (int kk = 0; kk < WK; kk += 4) {
       const int ka = (kk + (lane >> 4)) * LA + wm + (lane & 15), kb = (kk + (lane >> 4)) * LB + wn + (lane & 15);
@@ -171,7 +226,7 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   }
   if (sums) {
     __syncthreads();
-    float* red = As[0];
+    float* red = smem;
     red[tid] = csum;
     __syncthreads();
     const int64_t base = sum_a ? m0 : n0, width = sum_a ? M : N;
@@ -181,20 +236,42 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
       colsum[(ws ? int64_t(blockIdx.z) * width : 0) + base + tid] = v;
     }
   }
-  const float* bz = ws ? nullptr : bias;
+  // The output tile goes through LDS so that each row leaves as whole float4 groups (when `vo`:
+  // 16-byte aligned rows whose width is a multiple of 4, or padded to one), the epilogue applied
+  // on the way.
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) smem[(wm + 16 * i + 4 * (lane >> 4) + r) * LC + wn + 16 * j + (lane & 15)] = acc[i][j][r];
+  __syncthreads();
   float* out = ws ? ws + int64_t(blockIdx.z) * M * N : C;
   const int64_t ldo = ws ? N : ldc;
+  constexpr int Q = TN / 4;
 #pragma unroll
-  for (int i = 0; i < WM; ++i) {
+  for (int e0 = 0; e0 < TM * Q; e0 += 256) {
+    const int e = e0 + tid;
+    if (TM * Q % 256 != 0 && e >= TM * Q) break;
+    const int rl = e / Q, c4 = (e % Q) * 4;
+    const int64_t row = m0 + rl, col = n0 + c4;
+    if (row >= M) continue;
+    const float4 v = *reinterpret_cast<const float4*>(smem + rl * LC + c4);
+    if (vo && col + 3 < N) {
+      *reinterpret_cast<float4*>(out + row * ldo + col) = ws ? v : gemm_epilogue4(epi, v, row, col, ldo);
+    } else if (vo && col < N) {
+      // The last group of a row padded to a multiple of 4: zeros in the padding.
+      const float vs[4] = {v.x, v.y, v.z, v.w};
+      float r4[4];
 #pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int64_t col = n0 + wn + 16 * j + (lane & 15);
-      const float bv = bz && col < N ? bz[col] : 0.0f;
+      for (int c = 0; c < 4; ++c) r4[c] = col + c < N ? (ws ? vs[c] : gemm_epilogue(epi, vs[c], row, col + c, ldo)) : 0.0f;
+      *reinterpret_cast<float4*>(out + row * ldo + col) = make_float4(r4[0], r4[1], r4[2], r4[3]);
+    } else {
+      const float vs[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = m0 + wm + 16 * i + 4 * (lane >> 4) + r;
-        if (row < M && col < N) out[row * ldo + col] = bz ? acc[i][j][r] + bv : acc[i][j][r];
-      }
+      for (int c = 0; c < 4; ++c)
+        if (col + c < N) out[row * ldo + col + c] = ws ? vs[c] : gemm_epilogue(epi, vs[c], row, col + c, ldo);
     }
   }
 }
@@ -235,7 +312,7 @@ int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum, bool sum_a,
 int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs) {
   const int split = gemm_split_for(g.m, g.n, g.k, g.defer);
   if (split <= 1) return 0;
-  if (g.bias || g.ldc != g.n) bad("deferred split-K needs a dense output without bias");
+  if (g.bias || g.addend || g.act || g.ldc != g.n) bad("deferred split-K needs a dense output without epilogue");
   if (g.m * g.n > INT32_MAX) bad("deferred split-K output too large");
   jobs[0] = ColumnJob{g.workspace, g.c, nullptr, split, int32_t(g.m * g.n), int32_t(g.m * g.n), 0};
   if (!g.colsum) return 1;
@@ -260,6 +337,13 @@ void gemm(hipStream_t s, const GemmArgs& g) {
                    unsigned(split));
   if (wgrid.y > 65535) bad("gemm M too large");
   const int64_t width = g.sum_a ? g.m : g.n;
+  if ((g.act == EPI_GELU_GRAD || g.act == EPI_RELU_GRAD) && !g.pre_in) bad("gemm activation gradient without its input");
+  const GemmEpi epi{g.bias, g.addend, g.pre_in, g.pre_out, g.act};
+  // float4 output groups: every row the epilogue touches 16-byte aligned.
+  auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  const bool vo = ws ? (g.n % 4 == 0 && a16(ws))
+                     : ((g.n % 4 == 0 || (g.pad_c && !g.act && !g.addend)) && g.ldc % 4 == 0 && a16(g.c) && a16(g.bias) &&
+                        a16(g.addend) && a16(g.pre_in) && a16(g.pre_out));
   float* csum = g.colsum ? (ws ? ws + int64_t(split) * g.m * g.n : g.colsum) : nullptr;
   // float4 loads need 16-byte aligned groups and a contiguous extent that is a multiple of 4.
   // (A zero-padded operand may be read up to its leading dimension.)
@@ -269,8 +353,8 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   const bool va = aligned(g.a, g.lda, g.pad_a ? g.lda : (g.ta ? g.m : g.k));
   const bool vb = aligned(g.b, g.ldb, g.pad_b ? g.ldb : (g.tb ? g.k : g.n));
 #define MSX_WIDE_V(TA, TB, WM, WN, WK, VA, VB)                                                              \
-  hipLaunchKernelGGL((k_gemm_w<TA, TB, WM, WN, WK, VA, VB>), wgrid, dim3(256), 0, s, g.a, g.b, g.c, g.bias, g.m, g.n, \
-                     g.k, g.lda, g.ldb, g.ldc, chunk, ws, csum, g.sum_a)
+  hipLaunchKernelGGL((k_gemm_w<TA, TB, WM, WN, WK, VA, VB>), wgrid, dim3(256), 0, s, g.a, g.b, g.c, epi, g.m, g.n,   \
+                     g.k, g.lda, g.ldb, g.ldc, chunk, ws, csum, g.sum_a, vo)
   // float4 variants for both operands aligned, or the right one only; scalar loads otherwise.
 #define MSX_WIDE(TA, TB, WM, WN, WK)                                \
   if (va && vb) MSX_WIDE_V(TA, TB, WM, WN, WK, true, true);         \
@@ -290,7 +374,7 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   if (split > 1 && !g.defer) {
     const int64_t total = g.m * g.n + (g.colsum ? width : 0);
     const unsigned blocks = unsigned((total + 255) / 256);
-#define MSX_SPLITK(S) hipLaunchKernelGGL(k_splitk_sum<S>, dim3(blocks), dim3(256), 0, s, ws, g.c, g.bias, g.m, g.n, g.ldc, \
+#define MSX_SPLITK(S) hipLaunchKernelGGL(k_splitk_sum<S>, dim3(blocks), dim3(256), 0, s, ws, g.c, epi, g.m, g.n, g.ldc, \
                                          split, g.colsum, width)
     if (split <= 8) MSX_SPLITK(8);
     else if (split <= 16) MSX_SPLITK(16);

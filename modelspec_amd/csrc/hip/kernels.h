@@ -33,9 +33,19 @@ struct GemmArgs {
   float* workspace; int64_t workspace_floats;
   float* colsum;
   bool sum_a, defer;
-  // The operand's rows are zero from its contiguous extent up to its leading dimension.
-  bool pad_a, pad_b;
+  // The operand's rows are zero from its contiguous extent up to its leading dimension (pad_c:
+  // the output's rows are kept so).
+  bool pad_a, pad_b, pad_c;
+  // Epilogue after the bias: an activation (EPI_*: writing the pre-activation to pre_out when
+  // non-null) or an activation gradient (pre_in the pre-activation), then addend + value.
+  // addend, pre_in and pre_out share the output's leading dimension.
+  const float* addend;
+  const float* pre_in;
+  float* pre_out;
+  int act;
 };
+enum GemmAct : int { EPI_NONE, EPI_GELU, EPI_RELU, EPI_GELU_GRAD, EPI_RELU_GRAD };
+struct GemmEpi { const float* bias; const float* addend; const float* pre_in; float* pre_out; int act; };
 // The split-K factor the launcher uses (with `defer` as in GemmArgs).
 int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer = false);
 // Floats of workspace a gemm of this shape needs (0 without split-K): the slices' partial

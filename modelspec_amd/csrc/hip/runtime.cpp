@@ -231,6 +231,47 @@ void Executor::build() {
     eg_add[x.id] = {a.id, other};
     eg_add_nodes.insert(a.id);
   }
+  // GEMM epilogues. A GEMM's value (an unswapped MatMul, or the AddRows taking one as a biased
+  // GEMM) that is read only by Add(X, value) with X computed earlier, or only as the incoming
+  // gradient of GeluGrad/ReluGrad, is not materialized: the GEMM writes the consumer's value. A
+  // Gelu/Relu of a GEMM's value is written by the GEMM beside the value itself.
+  struct Epi { uint32_t node; int act; int64_t aux; };  // consumer, hk::GemmAct, addend or pre-activation
+  std::map<uint32_t, Epi> gemm_epi;                     // GEMM value -> consumer it writes
+  std::set<uint32_t> epi_nodes;                         // consumers written by their GEMM
+  for (size_t k = 0; k < n; ++k) {
+    const Node& x = p.nodes[k];
+    if (!need[k] || outputs.count(x.id)) continue;
+    const bool gemm_value = (x.op == Op::MatMul && !mm_fused.count(x.id) && !mm_transposed.count(x.id) &&
+                             !colsum_of.count(x.id)) ||
+                            (x.op == Op::AddRows && mm_fused.count(x.operands[0]));
+    if (!gemm_value) continue;
+    std::vector<size_t> cs = consumers[k];
+    if (cs.size() == 1) {
+      const Node& c = p.nodes[cs[0]];
+      if (c.op == Op::Add && !eg_add_nodes.count(c.id) && c.operands[0] != c.operands[1] && !epi_nodes.count(c.id)) {
+        const uint32_t other = c.operands[0] == x.id ? c.operands[1] : c.operands[0];
+        if (p.pos.at(other) < k && p.node(other).ty.shape == x.ty.shape) {
+          gemm_epi[x.id] = {c.id, hk::EPI_NONE, int64_t(other)};
+          epi_nodes.insert(c.id);
+          continue;
+        }
+      }
+      if ((c.op == Op::GeluGrad || c.op == Op::ReluGrad) && c.operands[1] == x.id && c.operands[0] != x.id &&
+          p.pos.at(c.operands[0]) < k) {
+        gemm_epi[x.id] = {c.id, c.op == Op::GeluGrad ? hk::EPI_GELU_GRAD : hk::EPI_RELU_GRAD, int64_t(c.operands[0])};
+        epi_nodes.insert(c.id);
+        continue;
+      }
+    }
+    for (auto c : cs) {
+      const Node& cn = p.nodes[c];
+      if ((cn.op == Op::Gelu || cn.op == Op::Relu) && !epi_nodes.count(cn.id)) {
+        gemm_epi[x.id] = {cn.id, cn.op == Op::Gelu ? hk::EPI_GELU : hk::EPI_RELU, -1};
+        epi_nodes.insert(cn.id);
+        break;
+      }
+    }
+  }
   // The LayerNorm gradients of one (input, output gradient) pair run as one pass: dx, and block
   // partials of the gamma and beta sums, finished by a batched column reduction, deferred to the
   // end of the step when only the optimizer reads them. The pass runs at its first member.
@@ -361,6 +402,7 @@ void Executor::build() {
         break;
       default:
         if (folded.count(x.id) || mm_fused.count(x.id) || mm_transposed.count(x.id) || eg_add.count(x.id)) break;
+        if (gemm_epi.count(x.id) && gemm_epi.at(x.id).act != hk::EPI_GELU && gemm_epi.at(x.id).act != hk::EPI_RELU) break;
         token_[x.id] = arena_.reserve(size_t(pitch.count(x.id) ? x.ty.shape[0] * pitch.at(x.id) : x.ty.count()) * 4);
         break;
     }
@@ -445,7 +487,7 @@ void Executor::build() {
     switch (x.op) {
       case Op::Input: case Op::ParamRead: case Op::Scalar: break;
       case Op::Add: case Op::Sub: case Op::Mul: case Op::Div: {
-        if (eg_add_nodes.count(id)) break;  // written by its EmbeddingGrad
+        if (eg_add_nodes.count(id) || epi_nodes.count(id)) break;  // written by its EmbeddingGrad or GEMM
         int op = x.op == Op::Add ? hk::EW_ADD : x.op == Op::Sub ? hk::EW_SUB : x.op == Op::Mul ? hk::EW_MUL : hk::EW_DIV;
         bool as = p.node(o[0]).ty.rank() == 0 && count > 1, bs = p.node(o[1]).ty.rank() == 0 && count > 1;
         uint32_t a = o[0], b = o[1];
@@ -453,12 +495,14 @@ void Executor::build() {
         break;
       }
       case Op::Relu: case Op::Gelu: case Op::Sqrt: case Op::StopGradient: {
+        if (epi_nodes.count(id)) break;  // written by its GEMM
         int op = x.op == Op::Relu ? hk::EW_RELU : x.op == Op::Gelu ? hk::EW_GELU : x.op == Op::Sqrt ? hk::EW_SQRT : hk::EW_COPY;
         uint32_t a = o[0];
         push([=](hipStream_t s) { hk::elementwise(s, op, F(a), nullptr, F(id), count, false, false); });
         break;
       }
       case Op::ReluGrad: case Op::GeluGrad: {
+        if (epi_nodes.count(id)) break;  // written by its GEMM
         int op = x.op == Op::ReluGrad ? hk::EW_RELU_GRAD : hk::EW_GELU_GRAD;
         uint32_t a = o[0], g = o[1];
         push([=](hipStream_t s) { hk::elementwise(s, op, F(a), F(g), F(id), count, false, false); });
@@ -469,7 +513,10 @@ void Executor::build() {
         if (x.op == Op::MatMul && mm_fused.count(id)) break;
         bool fused = x.op == Op::AddRows && mm_fused.count(o[0]);
         const bool swap = x.op == Op::MatMul && mm_transposed.count(id);
-        const uint32_t out_id = swap ? mm_transposed.at(id) : id;
+        // The value the GEMM writes: its own, the Transpose's (swapped), or an epilogue consumer's.
+        const Epi epi = gemm_epi.count(id) ? gemm_epi.at(id) : Epi{id, hk::EPI_NONE, -1};
+        const uint32_t out_id = swap ? mm_transposed.at(id) : epi.node;
+        if (epi.node != id) what += " +" + std::string(op_name(p.node(epi.node).op)) + " %" + std::to_string(epi.node);
         if (x.op == Op::AddRows && !fused) {
           uint32_t a = o[0], b = o[1];
           int64_t rows = x.ty.shape[0], h = x.ty.shape[1];
@@ -498,11 +545,12 @@ void Executor::build() {
         g.ldc = ld_of(out_id);
         g.pad_a = pitch.count(asrc) != 0;
         g.pad_b = pitch.count(bsrc) != 0;
+        g.pad_c = pitch.count(out_id) != 0;
         const int64_t cs_id = x.op == Op::MatMul && colsum_of.count(id) ? int64_t(colsum_of.at(id)) : -1;
         g.sum_a = swap;  // the column sums of B are the row sums of the swapped left operand
         int64_t bias_id = fused ? int64_t(o[1]) : -1;
         // Split-K partials only the optimizer reads are summed by the batched column finalize.
-        g.defer = bias_id < 0 && only_optimizer_reads(int64_t(out_id)) && only_optimizer_reads(cs_id);
+        g.defer = bias_id < 0 && epi.node == id && only_optimizer_reads(int64_t(out_id)) && only_optimizer_reads(cs_id);
         int64_t wsf = hk::gemm_workspace(g.m, g.n, g.k, cs_id >= 0, g.sum_a, g.defer);
         void* ws = wsf > 0 ? R(size_t(wsf) * 4) : nullptr;
         g.workspace_floats = wsf;
@@ -514,6 +562,10 @@ void Executor::build() {
           a.bias = bias_id >= 0 ? F(uint32_t(bias_id)) : nullptr;
           a.workspace = ws ? static_cast<float*>(A(ws)) : nullptr;
           a.colsum = cs_id >= 0 ? F(uint32_t(cs_id)) : nullptr;
+          a.act = epi.act;
+          if (epi.node != id && epi.act == hk::EPI_NONE) a.addend = F(uint32_t(epi.aux));
+          if (epi.act == hk::EPI_GELU_GRAD || epi.act == hk::EPI_RELU_GRAD) a.pre_in = F(uint32_t(epi.aux));
+          if (epi.act == hk::EPI_GELU || epi.act == hk::EPI_RELU) a.pre_out = F(id);
           hk::gemm(s, a);
         });
         if (g.defer && wsf > 0) {

@@ -138,6 +138,27 @@ def test_decoder_cross_entropy_head(ctx, oracle, v, h, r, n, g_const):
     assert within(got[3], want[3], ((ax.T @ adl).T + seg).reshape(-1) + 1e-3)[0]
 
 
+@pytest.mark.parametrize("act,m,k,n", [("Gelu", 4096, 128, 512), ("Relu", 64, 784, 256), ("Gelu", 33, 70, 129)])
+def test_gemm_epilogues(ctx, oracle, act, m, k, n):
+    """Activation, activation gradient and residual add written by the GEMM that produces their
+    input: y = x W + b, a = act(y) (y kept for the gradient), act'(y) (r W), q + dy W^T."""
+    x, W, b = fast_values(71, m * k).reshape(m, k), fast_values(72, k * n, 0.1).reshape(k, n), fast_values(73, n)
+    dy, r, q = fast_values(74, m * n).reshape(m, n), fast_values(75, m * k).reshape(m, k), fast_values(76, m * k).reshape(m, k)
+    p = Prog()
+    xi, wi, bi = p.input("x", (m, k)), p.input("W", (k, n)), p.input("b", (n,))
+    di, ri, qi = p.input("dy", (m, n)), p.input("r", (m, k)), p.input("q", (m, k))
+    y = p.op("AddRows", [p.op("MatMul", [xi, wi], (m, n)), bi], (m, n))
+    a = p.op(act, [y], (m, n))
+    g = p.op(act + "Grad", [y, p.op("MatMul", [ri, wi], (m, n))], (m, n))
+    z = p.op("Add", [qi, p.op("MatMul", [di, p.op("Transpose", [wi], (n, k))], (m, k))], (m, k))
+    got, want = both(ctx, oracle, p.out(a, g, z), {"x": x, "W": W, "b": b, "dy": dy, "r": r, "q": q}, (0, 1, 2))
+    aW = np.abs(W).astype(np.float64)
+    ry = np.abs(x) @ aW + np.abs(b)
+    assert within(got[0], want[0], (ry * 1.2 + 1e-3).reshape(-1))[0]
+    assert within(got[1], want[1], ((np.abs(r) @ aW) * 1.2 * (1 + ry) + 1e-3).reshape(-1))[0]
+    assert within(got[2], want[2], (np.abs(q) + np.abs(dy) @ aW.T).reshape(-1))[0]
+
+
 @pytest.mark.parametrize("rows,h", [(6, 8), (4096, 128), (832, 128), (33, 200), (100, 768)])
 def test_layer_norm_family(ctx, oracle, rows, h):
     x = fast_values(6, rows * h).reshape(rows, h)
