@@ -26,22 +26,10 @@ PEAK_FP32_MFMA = 157.3e12  # flop/s, dense
 CONFIG = "bert_tiny"
 TOKENS = 32 * 128
 
-# The HIP kernels each planned launch runs (the names rocprofv3 reports).
-SYMBOLS = {
-    "MatMul": "k_gemm", "MatMul+AddRows": "k_gemm", "EmbeddingGrad": "k_fill_zero+k_sort_ids+k_segment_sum",
-    "CrossEntropy": "k_ce_stats+k_ce_loss", "CrossEntropyGrad": "k_ce_grad", "Attention": "k_attn_fwd_mfma",
-    "AttentionGradQ": "k_attn_bwd_q_mfma+k_attn_bwd_kv_mfma", "AttentionGradK": "k_attn_bwd_q_mfma+k_attn_bwd_kv_mfma",
-    "AttentionGradV": "k_attn_bwd_q_mfma+k_attn_bwd_kv_mfma", "LayerNorm": "k_layer_norm", "LayerNormGradX": "k_ln_grad_x",
-    "LayerNormGradGamma": "k_column_partial+k_column_final", "SumRows": "k_column_partial+k_column_final",
-    "Dropout": "k_dropout", "DropoutGrad": "k_dropout", "AdamW": "k_adamw", "Embedding": "k_embedding",
-    "Transpose": "k_transpose", "AddRows": "k_add_rows",
-}
-
-
 def roofline(rows):
     """The launch with the largest mean time, and every launch's fraction of its roofline."""
     table = []
-    for what, ms, flop, nbytes in rows:
+    for what, ms, flop, nbytes, kernels in rows:
         if ms <= 0:
             continue
         if flop > 0:
@@ -52,9 +40,39 @@ def roofline(rows):
             achieved, peak = achieved / 1e9, peak / 1e9
         table.append({"launch": what, "ms": ms, "bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
                       "frac": achieved / peak, "flop": flop, "bytes": nbytes,
-                      "kernel": SYMBOLS.get(what.split()[0], "k_elementwise")})
+                      "kernel": kernels})
     table.sort(key=lambda r: -r["ms"])
     return table
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "dominant_launch_traffic.md")
+
+
+def measured_traffic(launch):
+    """HBM bytes per dispatch of `launch` from the committed rocprofv3 counter summary (FETCH_SIZE +
+    WRITE_SIZE, each scaled by the counters' reading of a copy of known size), when it covers this
+    launch; else None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("| traffic |"):
+                    cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                    if cells[1].strip("`") == launch:
+                        return float(cells[4])
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
+
+
+def copy_once(ctx, mib):
+    """One elementwise copy of `mib` MiB on the device (StopGradient: read n floats, write n)."""
+    import numpy as np
+    n = mib * (1 << 20) // 4
+    prog = ctx.program(f'%0: Tensor<f32, [{n}]> = Input "x"\n%1: Tensor<f32, [{n}]> = StopGradient %0\noutput %1\n')
+    try:
+        prog.run({"x": np.zeros(n, np.float32)})
+    finally:
+        prog.close()
 
 
 def cpu_baseline(steps):
@@ -90,6 +108,11 @@ def main():
     ap.add_argument("--profile-reps", type=int, default=5)
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--launches", metavar="FILE", help="write every profiled launch (order, time, work, "
+                    "kernels) to FILE as JSON lines")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after the bench, copy MIB MiB once with the elementwise kernel (a known-size "
+                         "reference dispatch for the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -103,7 +126,22 @@ def main():
     median_ms = statistics.median(per_step)
     table = roofline(rows)
     top = table[0]
+    if args.launches:
+        with open(args.launches, "w") as f:
+            for what, ms, flop, nbytes, kernels in rows:
+                f.write(json.dumps({"launch": what, "ms": ms, "flop": flop, "bytes": nbytes, "kernels": kernels}) + "\n")
+    # Where the dominant launch's dispatches sit in a profiled step (rocprofv3 counter runs).
+    first = 0
+    for what, _, _, _, kernels in rows:
+        if what == top["launch"]:
+            break
+        first += len(kernels.split("+")) if kernels else 0
+    dispatches = {"step_dispatches": sum(len(r[4].split("+")) if r[4] else 0 for r in rows), "first": first,
+                  "count": len(top["kernel"].split("+")) if top["kernel"] else 0}
+    traffic = measured_traffic(top["launch"])
     stats = ctx.stats()
+    if args.copy_calibration > 0:
+        copy_once(ctx, args.copy_calibration)
     ctx.close()
     out = {
         "metric": "BERT-tiny b32 s128 train ms/step (median) + per-kernel % of MFMA/HBM roofline",
@@ -126,7 +164,8 @@ def main():
         "last_loss": last_loss,
         "kernels_per_step": stats["kernels_per_step"],
         "roofline": {"bound": top["bound"], "achieved": round(top["achieved"], 2), "peak": top["peak"],
-                     "unit": top["unit"], "frac": round(top["frac"], 4), "traffic": None,
+                     "unit": top["unit"], "frac": round(top["frac"], 4), "traffic": traffic,
+                     "dispatches": dispatches,
                      "kernel": top["kernel"], "launch": top["launch"], "launch_ms": round(top["ms"], 5),
                      "algorithmic": top["flop"] if top["bound"] == "mfma" else top["bytes"]},
         "top_kernels": [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()

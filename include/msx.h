@@ -99,8 +99,9 @@ int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t ma
 /* Times `steps` graph-launched training steps of a built-in config after `warmup` (HIP events on
  * the run's stream after every step into step_ms[steps], may be null; host inputs made before the
  * timed region), then runs `profile_reps` more steps eagerly with an event pair around every
- * launch into `profile` ("launch\tms\tflop\tbytes" lines, ms the mean over the reps, flop and
- * bytes the reference's algorithmic count; free with msx_free). Replaces `train --clock
+ * launch into `profile` ("launch\tms\tflop\tbytes\tkernels" lines, ms the mean over the reps,
+ * flop and bytes the reference's algorithmic count, kernels the HIP kernels the launch dispatched
+ * joined by '+'; free with msx_free). Replaces `train --clock
  * --profile` (crates/modelspec-cli/src/train.rs:17-31, vulkan/profile.rs:1-14). */
 int msx_bench_config(msx_ctx* ctx, const char* config, int64_t masked_rows, uint32_t warmup, uint32_t steps,
                      double* ms_per_step, double* step_ms, float* last_loss, uint32_t profile_reps, char** profile);

@@ -235,7 +235,8 @@ def config_steps(name):
 
 
 def bench_config(ctx, name, warmup, steps, masked_rows=-1, profile_reps=1):
-    """(mean ms per step, [ms of each timed step], last loss, [(launch, ms, flop, bytes)])."""
+    """(mean ms per step, [ms of each timed step], last loss, [(launch, ms, flop, bytes, kernels)]), kernels
+    the HIP kernels the launch dispatched, '+'-joined."""
     L = lib()
     L.msx_bench_config.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint32,
                                    ctypes.POINTER(ctypes.c_double), ctypes.c_void_p, ctypes.POINTER(ctypes.c_float),
@@ -250,8 +251,8 @@ def bench_config(ctx, name, warmup, steps, masked_rows=-1, profile_reps=1):
         text = ctypes.string_at(rep).decode()
         L.msx_free(rep)
         for line in text.splitlines():
-            what, t, flop, nbytes = line.rsplit("\t", 3)
-            rows.append((what, float(t), float(flop), float(nbytes)))
+            what, t, flop, nbytes, kernels = line.rsplit("\t", 4)
+            rows.append((what, float(t), float(flop), float(nbytes), kernels))
     return ms.value, per_step[:steps].tolist(), loss.value, rows
 
 

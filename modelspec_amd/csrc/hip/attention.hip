@@ -13,6 +13,7 @@
 #include <string>
 
 #include "kernels.h"
+#include "device.h"
 
 namespace msx::hk {
 
@@ -504,7 +505,7 @@ void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v
   if (attention_mfma(L, S, d)) {
     dim3 grid(unsigned(B * heads), unsigned((L + 16 * kWaves - 1) / (16 * kWaves)));
     size_t lds = mfma_fwd_lds(S, d);
-#define GO(D) hipLaunchKernelGGL(k_attn_fwd_mfma<D>, grid, dim3(64 * kWaves), lds, s, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale)
+#define GO(D) MSX_LAUNCH(k_attn_fwd_mfma<D>, grid, dim3(64 * kWaves), lds, s, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale)
     MSX_BY_D(d, GO)
 #undef GO
     return;
@@ -512,7 +513,7 @@ void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v
   if (scalar_fwd_lds(S, d) > kLdsMax || stats) refuse("attention shape outside the kernels' LDS budget");
   dim3 grid(unsigned(B * heads), unsigned((L + 63) / 64));
   size_t lds = scalar_fwd_lds(S, d);
-#define GO(D) hipLaunchKernelGGL(k_attn_fwd_scalar<D>, grid, dim3(64), lds, s, q, k, v, mask, o, int(L), int(S), int(H), int(heads), scale)
+#define GO(D) MSX_LAUNCH(k_attn_fwd_scalar<D>, grid, dim3(64), lds, s, q, k, v, mask, o, int(L), int(S), int(H), int(heads), scale)
   MSX_BY_D(d, GO)
 #undef GO
 }
@@ -530,7 +531,7 @@ void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v
       // dQ (written only when asked) and the d_i the key pass reads.
       float* dq_out = dq;
       size_t lq = mfma_fwd_lds(S, d);
-#define GO(D) hipLaunchKernelGGL(k_attn_bwd_q_mfma<D>, gq, dim3(64 * kWaves), lq, s, q, k, v, mask, o, stats, g, dq_out, dsum, int(L), int(S), int(H), int(heads), scale)
+#define GO(D) MSX_LAUNCH(k_attn_bwd_q_mfma<D>, gq, dim3(64 * kWaves), lq, s, q, k, v, mask, o, stats, g, dq_out, dsum, int(L), int(S), int(H), int(heads), scale)
       if (dq_out) { MSX_BY_D(d, GO) }
 #undef GO
       if (!dq_out) refuse("the MFMA attention backward computes d_i in its dQ pass: dQ is required");
@@ -538,7 +539,7 @@ void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v
     if (dk || dv) {
       dim3 gk(unsigned(B * heads), unsigned((S + 16 * kWaves - 1) / (16 * kWaves)));
       size_t lk = mfma_kv_lds(L, d);
-#define GO(D) hipLaunchKernelGGL(k_attn_bwd_kv_mfma<D>, gk, dim3(64 * kWaves), lk, s, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale)
+#define GO(D) MSX_LAUNCH(k_attn_bwd_kv_mfma<D>, gk, dim3(64 * kWaves), lk, s, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale)
       MSX_BY_D(d, GO)
 #undef GO
     }
@@ -547,7 +548,7 @@ void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v
   if (scalar_bwd_lds(L, S, d) > kLdsMax) refuse("attention shape outside the kernels' LDS budget");
   size_t lds = scalar_bwd_lds(L, S, d);
   int threads = int(std::min<int64_t>(256, std::max<int64_t>(64, (S + 63) / 64 * 64)));
-#define GO(D) hipLaunchKernelGGL(k_attn_bwd_scalar<D>, dim3(unsigned(B * heads)), dim3(threads), lds, s, q, k, v, mask, g, dq, dk, dv, int(L), int(S), int(H), int(heads), scale)
+#define GO(D) MSX_LAUNCH(k_attn_bwd_scalar<D>, dim3(unsigned(B * heads)), dim3(threads), lds, s, q, k, v, mask, g, dq, dk, dv, int(L), int(S), int(H), int(heads), scale)
   MSX_BY_D(d, GO)
 #undef GO
 }

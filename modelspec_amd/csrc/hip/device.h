@@ -8,6 +8,15 @@
 
 namespace msx::hk {
 
+// The kernels a host thread dispatches are noted while a log is attached (profiling: which HIP
+// kernels one planned launch ran).
+void note_kernel(const char* expr);
+#define MSX_LAUNCH(KERNEL, ...)                 \
+  do {                                          \
+    ::msx::hk::note_kernel(#KERNEL);            \
+    hipLaunchKernelGGL(KERNEL, __VA_ARGS__);    \
+  } while (0)
+
 namespace {
 typedef float v4f __attribute__((ext_vector_type(4)));
 

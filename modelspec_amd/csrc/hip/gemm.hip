@@ -353,7 +353,7 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   const bool va = aligned(g.a, g.lda, g.pad_a ? g.lda : (g.ta ? g.m : g.k));
   const bool vb = aligned(g.b, g.ldb, g.pad_b ? g.ldb : (g.tb ? g.k : g.n));
 #define MSX_WIDE_V(TA, TB, WM, WN, WK, VA, VB)                                                              \
-  hipLaunchKernelGGL((k_gemm_w<TA, TB, WM, WN, WK, VA, VB>), wgrid, dim3(256), 0, s, g.a, g.b, g.c, epi, g.m, g.n,   \
+  MSX_LAUNCH((k_gemm_w<TA, TB, WM, WN, WK, VA, VB>), wgrid, dim3(256), 0, s, g.a, g.b, g.c, epi, g.m, g.n,   \
                      g.k, g.lda, g.ldb, g.ldc, chunk, ws, csum, g.sum_a, vo)
   // float4 variants for both operands aligned, or the right one only; scalar loads otherwise.
 #define MSX_WIDE(TA, TB, WM, WN, WK)                                \
@@ -374,7 +374,7 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   if (split > 1 && !g.defer) {
     const int64_t total = g.m * g.n + (g.colsum ? width : 0);
     const unsigned blocks = unsigned((total + 255) / 256);
-#define MSX_SPLITK(S) hipLaunchKernelGGL(k_splitk_sum<S>, dim3(blocks), dim3(256), 0, s, ws, g.c, epi, g.m, g.n, g.ldc, \
+#define MSX_SPLITK(S) MSX_LAUNCH(k_splitk_sum<S>, dim3(blocks), dim3(256), 0, s, ws, g.c, epi, g.m, g.n, g.ldc, \
                                          split, g.colsum, width)
     if (split <= 8) MSX_SPLITK(8);
     else if (split <= 16) MSX_SPLITK(16);

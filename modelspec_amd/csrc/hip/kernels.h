@@ -4,12 +4,18 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <string>
+#include <vector>
 
 namespace msx::hk {
 
 // Sets the launch attributes some kernels need (large dynamic LDS). Call once per process and
 // device before launching, never during stream capture.
 void prepare();
+
+// While `log` is attached (non-null), the names of the kernels this thread dispatches are appended
+// to it (profiling).
+void kernel_log(std::vector<std::string>* log);
 
 enum EwOp : int { EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_RELU, EW_RELU_GRAD, EW_GELU, EW_GELU_GRAD, EW_SQRT, EW_COPY };
 

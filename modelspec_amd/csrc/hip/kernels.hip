@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 namespace msx::hk {
 
@@ -40,7 +41,7 @@ __global__ void k_elementwise(int op, const float* __restrict__ a, const float* 
 void elementwise(hipStream_t s, int op, const float* a, const float* b, float* o, int64_t n, bool as, bool bs) {
   if (n <= 0) return;
   unsigned grid = std::min<unsigned>(blocks_for(n, 256), 8192);
-  hipLaunchKernelGGL(k_elementwise, dim3(grid), dim3(256), 0, s, op, a, b, o, n, int(as), int(bs));
+  MSX_LAUNCH(k_elementwise, dim3(grid), dim3(256), 0, s, op, a, b, o, n, int(as), int(bs));
 }
 
 void copy(hipStream_t s, const float* a, float* o, int64_t n) { elementwise(s, EW_COPY, a, nullptr, o, n, false, false); }
@@ -52,7 +53,7 @@ __global__ void k_fill_from(const float* __restrict__ v, float* __restrict__ o, 
 }
 void fill_from(hipStream_t s, const float* v, float* o, int64_t n) {
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_fill_from, dim3(std::min<unsigned>(blocks_for(n, 256), 8192)), dim3(256), 0, s, v, o, n);
+  MSX_LAUNCH(k_fill_from, dim3(std::min<unsigned>(blocks_for(n, 256), 8192)), dim3(256), 0, s, v, o, n);
 }
 
 __global__ void k_fill_zero(uint32_t* __restrict__ o, int64_t words) {
@@ -68,7 +69,7 @@ void fill_zero(hipStream_t s, void* o, int64_t bytes) {
   if (bytes <= 0) return;
   if (bytes % 4 || reinterpret_cast<uintptr_t>(o) % 16) bad("fill_zero needs 16-byte aligned whole words");
   int64_t words = bytes / 4;
-  hipLaunchKernelGGL(k_fill_zero, dim3(std::min<unsigned>(blocks_for(words / 4 + 1, 256), 8192)), dim3(256), 0, s,
+  MSX_LAUNCH(k_fill_zero, dim3(std::min<unsigned>(blocks_for(words / 4 + 1, 256), 8192)), dim3(256), 0, s,
                      static_cast<uint32_t*>(o), words);
 }
 
@@ -90,7 +91,7 @@ void transpose(hipStream_t s, const float* a, float* o, int64_t rows, int64_t co
   if (rows <= 0 || cols <= 0) return;
   dim3 grid(unsigned((cols + 31) / 32), unsigned((rows + 31) / 32));
   if (grid.y > 65535) bad("transpose too tall");
-  hipLaunchKernelGGL(k_transpose, grid, dim3(32, 8), 0, s, a, o, rows, cols);
+  MSX_LAUNCH(k_transpose, grid, dim3(32, 8), 0, s, a, o, rows, cols);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -102,7 +103,7 @@ __global__ void k_add_rows(const float* __restrict__ x, const float* __restrict_
 void add_rows(hipStream_t s, const float* x, const float* b, float* o, int64_t rows, int64_t h) {
   int64_t n = rows * h;
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_add_rows, dim3(std::min<unsigned>(blocks_for(n, 256), 8192)), dim3(256), 0, s, x, b, o, n, h);
+  MSX_LAUNCH(k_add_rows, dim3(std::min<unsigned>(blocks_for(n, 256), 8192)), dim3(256), 0, s, x, b, o, n, h);
 }
 
 // Partial column sums: block (x, y) adds columns 256 x + t over the rows of chunk y, eight rows in
@@ -133,7 +134,7 @@ void column_partial(hipStream_t s, const float* x, float* partial, int64_t rows,
   const int64_t chunks = column_partial_chunks(rows, h);
   const int64_t per = (rows + chunks - 1) / chunks;
   if ((rows + per - 1) / per != chunks) bad("column partial chunking");
-  hipLaunchKernelGGL(k_column_partial, dim3(unsigned((h + 255) / 256), unsigned(chunks)), dim3(256), 0, s, x, partial,
+  MSX_LAUNCH(k_column_partial, dim3(unsigned((h + 255) / 256), unsigned(chunks)), dim3(256), 0, s, x, partial,
                      rows, h, per);
 }
 
@@ -154,7 +155,7 @@ __global__ void k_ln_stats(const float* __restrict__ x, float* __restrict__ stat
 }
 void ln_stats(hipStream_t s, const float* x, float* stats, int64_t rows, int64_t h) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(k_ln_stats, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, stats, rows, h);
+  MSX_LAUNCH(k_ln_stats, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, stats, rows, h);
 }
 
 __global__ void k_layer_norm(const float* __restrict__ x, const float* __restrict__ gamma,
@@ -177,7 +178,7 @@ __global__ void k_layer_norm(const float* __restrict__ x, const float* __restric
 void layer_norm(hipStream_t s, const float* x, const float* gamma, const float* beta, float* y, float* stats,
                 int64_t rows, int64_t h) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(k_layer_norm, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, gamma, beta, y, stats, rows, h);
+  MSX_LAUNCH(k_layer_norm, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, gamma, beta, y, stats, rows, h);
 }
 
 // The LayerNorm backward of one input in one pass: dx (LayerNormGradX) and, per block of rows, the
@@ -257,7 +258,7 @@ void ln_backward(hipStream_t s, const float* x, const float* gamma, const float*
   const int64_t per = (rows + blocks - 1) / blocks;
   const size_t lds = size_t(8 * h) * 4;
   const int cpl = int((h + 63) / 64);
-#define MSX_LNB(C) hipLaunchKernelGGL(k_ln_backward<C>, dim3(unsigned(blocks)), dim3(256), lds, s, x, gamma, g, stats, dx, \
+#define MSX_LNB(C) MSX_LAUNCH(k_ln_backward<C>, dim3(unsigned(blocks)), dim3(256), lds, s, x, gamma, g, stats, dx, \
                                       partial, rows, h, per)
   if (cpl <= 1) MSX_LNB(1);
   else if (cpl <= 2) MSX_LNB(2);
@@ -306,7 +307,7 @@ void column_finalize(hipStream_t s, const ColumnJob* jobs, int count) {
       b.job[j].first = blocks;
       blocks += int((b.job[j].width + 255) / 256);
     }
-    hipLaunchKernelGGL(k_column_finalize, dim3(unsigned(blocks)), dim3(256), 0, s, b);
+    MSX_LAUNCH(k_column_finalize, dim3(unsigned(blocks)), dim3(256), 0, s, b);
   }
 }
 
@@ -321,7 +322,7 @@ __global__ void k_embedding(const float* __restrict__ table, const int32_t* __re
 void embedding(hipStream_t s, const float* table, const int32_t* ids, float* o, int64_t n, int64_t rows, int64_t h) {
   if (n <= 0) return;
   if (n > 2147483647) bad("embedding rows");
-  hipLaunchKernelGGL(k_embedding, dim3(unsigned(n)), dim3(h >= 256 ? 256 : (h >= 128 ? 128 : 64)), 0, s, table, ids,
+  MSX_LAUNCH(k_embedding, dim3(unsigned(n)), dim3(h >= 256 ? 256 : (h >= 128 ? 128 : 64)), 0, s, table, ids,
                      o, n, rows, h);
 }
 
@@ -532,7 +533,7 @@ void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* ou
   // A chunk fills the float4 registers of every thread (vec) or 4096 floats.
   const int ch = int(vec ? std::max<int64_t>(1, int64_t(kEgThreads) * kEgVec / (h / 4)) : std::max<int64_t>(1, 4096 / h));
   const size_t lds = size_t(n) * 4 + size_t(ch) * size_t(h) * 4;
-  hipLaunchKernelGGL(k_embedding_grad, dim3(unsigned(blocks)), dim3(kEgThreads), lds, s, ids, g, addend, out, int(n),
+  MSX_LAUNCH(k_embedding_grad, dim3(unsigned(blocks)), dim3(kEgThreads), lds, s, ids, g, addend, out, int(n),
                      rows, h, stripe, ch, vec);
 }
 
@@ -551,7 +552,7 @@ void dropout(hipStream_t s, const float* x, float* o, int64_t n, const int32_t* 
              uint64_t threshold, float scale) {
   if (n <= 0) return;
   if (n > (int64_t(1) << 32)) bad("dropout over more than 2^32 elements");
-  hipLaunchKernelGGL(k_dropout, dim3(std::min<unsigned>(blocks_for(n, 256), 8192)), dim3(256), 0, s, x, o, n, token,
+  MSX_LAUNCH(k_dropout, dim3(std::min<unsigned>(blocks_for(n, 256), 8192)), dim3(256), 0, s, x, o, n, token,
                      uint32_t(seed), uint32_t(seed >> 32), threshold, scale);
 }
 
@@ -601,7 +602,7 @@ void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, in
   if (rows <= 0) return;
   if (rows > 2147483647) bad("cross_entropy rows");
   if (ld < v) bad("cross_entropy row pitch");
-  hipLaunchKernelGGL(k_ce_stats, dim3(unsigned(rows)), dim3(256), 0, s, logits, stats, v, ld);
+  MSX_LAUNCH(k_ce_stats, dim3(unsigned(rows)), dim3(256), 0, s, logits, stats, v, ld);
 }
 
 __global__ __launch_bounds__(256) void k_ce_loss(const float* __restrict__ x, const int32_t* __restrict__ labels,
@@ -640,7 +641,7 @@ __global__ __launch_bounds__(256) void k_ce_loss(const float* __restrict__ x, co
 }
 void ce_loss(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats, float* loss,
              float* den, int64_t rows, int64_t v, int64_t ld, const float* rowloss) {
-  hipLaunchKernelGGL(k_ce_loss, dim3(1), dim3(256), 0, s, logits, labels, w, stats, loss, den, rows, v, ld, rowloss);
+  MSX_LAUNCH(k_ce_loss, dim3(1), dim3(256), 0, s, logits, labels, w, stats, loss, den, rows, v, ld, rowloss);
 }
 
 __global__ void k_ce_grad(const float* __restrict__ x, const int32_t* __restrict__ labels, const float* __restrict__ w,
@@ -661,7 +662,7 @@ void ce_grad(hipStream_t s, const float* logits, const int32_t* labels, const fl
   if (rows <= 0) return;
   if (rows > 65535) bad("cross_entropy gradient rows");
   dim3 grid(unsigned(std::min<int64_t>((v + 255) / 256, 64)), unsigned(rows));
-  hipLaunchKernelGGL(k_ce_grad, grid, dim3(256), 0, s, logits, labels, w, stats, den, g, o, v, ld);
+  MSX_LAUNCH(k_ce_grad, grid, dim3(256), 0, s, logits, labels, w, stats, den, g, o, v, ld);
 }
 
 // Cross-entropy of whole rows in one pass over the logits: a block of kCeThreads holds its row in
@@ -759,7 +760,7 @@ void ce_rows(hipStream_t s, const float* logits, const int32_t* labels, const fl
     bad("cross_entropy row kernel needs float4-aligned rows of at most 32768 classes");
   if (grad && !g) bad("cross_entropy gradient without the upstream gradient");
   const int64_t per = ((v + 3) / 4 + kCeThreads - 1) / kCeThreads;
-#define MSX_CER(NV) hipLaunchKernelGGL(k_ce_rows<NV>, dim3(unsigned(rows)), dim3(kCeThreads), 0, s, logits, labels, w, g, \
+#define MSX_CER(NV) MSX_LAUNCH(k_ce_rows<NV>, dim3(unsigned(rows)), dim3(kCeThreads), 0, s, logits, labels, w, g, \
                                        stats, rowloss, grad, rows, v, ld)
   if (per <= 2) MSX_CER(2);
   else if (per <= 4) MSX_CER(4);
@@ -789,7 +790,7 @@ __global__ void k_softmax(const float* __restrict__ x, float* __restrict__ o, in
 }
 void softmax(hipStream_t s, const float* x, float* o, int64_t rows, int64_t k) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(k_softmax, dim3(unsigned(rows)), dim3(256), 0, s, x, o, k);
+  MSX_LAUNCH(k_softmax, dim3(unsigned(rows)), dim3(256), 0, s, x, o, k);
 }
 __global__ void k_softmax_grad(const float* __restrict__ y, const float* __restrict__ g, float* __restrict__ o,
                                int64_t k) {
@@ -805,7 +806,7 @@ __global__ void k_softmax_grad(const float* __restrict__ y, const float* __restr
 }
 void softmax_grad(hipStream_t s, const float* y, const float* g, float* o, int64_t rows, int64_t k) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(k_softmax_grad, dim3(unsigned(rows)), dim3(256), 0, s, y, g, o, k);
+  MSX_LAUNCH(k_softmax_grad, dim3(unsigned(rows)), dim3(256), 0, s, y, g, o, k);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -830,10 +831,10 @@ __global__ __launch_bounds__(1024) void k_reduce(const float* __restrict__ a, co
   if (threadIdx.x == 0) o[0] = float(mode == 0 ? red[0] : red[0] / double(n));
 }
 void reduce_sum(hipStream_t s, const float* a, float* o, int64_t n, bool mean) {
-  hipLaunchKernelGGL(k_reduce, dim3(1), dim3(1024), 0, s, a, nullptr, o, n, mean ? 1 : 0);
+  MSX_LAUNCH(k_reduce, dim3(1), dim3(1024), 0, s, a, nullptr, o, n, mean ? 1 : 0);
 }
 void mse(hipStream_t s, const float* a, const float* b, float* o, int64_t n) {
-  hipLaunchKernelGGL(k_reduce, dim3(1), dim3(1024), 0, s, a, b, o, n, 2);
+  MSX_LAUNCH(k_reduce, dim3(1), dim3(1024), 0, s, a, b, o, n, 2);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -856,7 +857,7 @@ __global__ void k_adamw(float* __restrict__ p, const float* __restrict__ g, floa
 void adamw(hipStream_t s, float* p, const float* g, float* m, float* v, int64_t n, AdamWConsts k, const float* lr_t,
            const float* c1, const float* c2) {
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_adamw, dim3(std::min<unsigned>(blocks_for(n, 256), 16384)), dim3(256), 0, s, p, g, m, v, n, k,
+  MSX_LAUNCH(k_adamw, dim3(std::min<unsigned>(blocks_for(n, 256), 16384)), dim3(256), 0, s, p, g, m, v, n, k,
                      lr_t, c1, c2);
 }
 
@@ -867,7 +868,7 @@ __global__ void k_sgd(float* __restrict__ p, const float* __restrict__ g, int64_
 }
 void sgd(hipStream_t s, float* p, const float* g, int64_t n, const float* lr) {
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_sgd, dim3(std::min<unsigned>(blocks_for(n, 256), 16384)), dim3(256), 0, s, p, g, n, lr);
+  MSX_LAUNCH(k_sgd, dim3(std::min<unsigned>(blocks_for(n, 256), 16384)), dim3(256), 0, s, p, g, n, lr);
 }
 
 __global__ void k_record_loss(const float* __restrict__ loss, float* __restrict__ losses, uint32_t* __restrict__ counter,
@@ -876,6 +877,19 @@ __global__ void k_record_loss(const float* __restrict__ loss, float* __restrict_
   if (c < capacity) losses[c] = loss[0];
   counter[0] = c + 1;
 }
+namespace {
+thread_local std::vector<std::string>* g_kernel_log = nullptr;
+}  // namespace
+void kernel_log(std::vector<std::string>* log) { g_kernel_log = log; }
+void note_kernel(const char* expr) {
+  if (!g_kernel_log) return;
+  // "(k_name<...>)" or "k_name<...>": the name.
+  std::string s(expr);
+  size_t b = s.find_first_not_of("( ");
+  size_t e = s.find_first_of("<( )", b);
+  g_kernel_log->push_back(s.substr(b, e == std::string::npos ? std::string::npos : e - b));
+}
+
 void prepare() {
   // Kernels whose dynamic LDS may exceed the 64 KiB default; set once, outside any capture.
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_embedding_grad),
@@ -885,7 +899,7 @@ void prepare() {
 }
 
 void record_loss(hipStream_t s, const float* loss, float* losses, uint32_t* counter, uint32_t capacity) {
-  hipLaunchKernelGGL(k_record_loss, dim3(1), dim3(1), 0, s, loss, losses, counter, capacity);
+  MSX_LAUNCH(k_record_loss, dim3(1), dim3(1), 0, s, loss, losses, counter, capacity);
 }
 
 }  // namespace msx::hk

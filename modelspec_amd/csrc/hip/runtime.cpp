@@ -1146,8 +1146,11 @@ std::vector<Session::Timed> Session::profile_step(const StepInputs& in) {
   std::vector<hipEvent_t> ev(ls.size() + 1);
   for (auto& e : ev) hip_check(hipEventCreate(&e), "hipEventCreate");
   hip_check(hipEventRecord(ev[0], stream_), "hipEventRecord");
+  std::vector<std::vector<std::string>> kernels(ls.size());
   for (size_t i = 0; i < ls.size(); ++i) {
+    hk::kernel_log(&kernels[i]);
     ls[i].run(stream_);
+    hk::kernel_log(nullptr);
     hip_check(hipEventRecord(ev[i + 1], stream_), "hipEventRecord");
   }
   sync();
@@ -1155,7 +1158,9 @@ std::vector<Session::Timed> Session::profile_step(const StepInputs& in) {
   for (size_t i = 0; i < ls.size(); ++i) {
     float ms = 0;
     hip_check(hipEventElapsedTime(&ms, ev[i], ev[i + 1]), "hipEventElapsedTime");
-    out.push_back({ls[i].what, ms, ls[i].flop, ls[i].bytes});
+    std::string names;
+    for (auto& kname : kernels[i]) names += (names.empty() ? "" : "+") + kname;
+    out.push_back({ls[i].what, ms, ls[i].flop, ls[i].bytes, names});
   }
   for (auto& e : ev) (void)hipEventDestroy(e);
   stats_.steps += 1;

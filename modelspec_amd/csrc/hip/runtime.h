@@ -70,7 +70,7 @@ class Session : public Engine {
 
   // Runs the step plan eagerly (no graph) with one event pair around every launch; returns the
   // launches and their milliseconds for the current inputs (the step's update is applied).
-  struct Timed { std::string what; float ms; double flop, bytes; };
+  struct Timed { std::string what; float ms; double flop, bytes; std::string kernels; };
   std::vector<Timed> profile_step(const StepInputs& in);
   void use_graph(bool on) { use_graph_ = on; }
   void sync();
