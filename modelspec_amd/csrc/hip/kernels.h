@@ -73,6 +73,14 @@ void column_partial(hipStream_t s, const float* x, float* partial, int64_t rows,
 void ln_stats(hipStream_t s, const float* x, float* stats, int64_t rows, int64_t h);
 void layer_norm(hipStream_t s, const float* x, const float* gamma, const float* beta, float* y, float* stats,
                 int64_t rows, int64_t h);
+// LayerNorm with its neighbours: s = [a +] [dropout](b) (a may be null; din_token null: no
+// dropout), y = LayerNorm(s; gamma, beta), yd = dropout(y) (dout_token non-null); each of s_out,
+// y_out, stats, yd_out written when non-null. Dropout as `dropout` (threshold, scale, seed).
+void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_token, uint64_t din_threshold,
+              float din_scale, const float* gamma, const float* beta, float* s_out, float* y_out, float* stats,
+              const int32_t* dout_token, uint64_t dout_threshold, float dout_scale, float* yd_out, int64_t rows,
+              int64_t h, uint64_t seed);
+
 // LayerNorm backward in one pass: dx when non-null, and when `partial` is non-null the per-block
 // partial sums [ln_backward_blocks, 2 h] of g * xhat (gamma gradient) then g (beta gradient), to be
 // added by column_finalize. gamma may be null when dx is.

@@ -272,6 +272,49 @@ void Executor::build() {
       }
     }
   }
+  // A LayerNorm with its neighbours in one pass: its input X = Add(A, B) (B possibly a Dropout read
+  // only there, not materialized) written beside the normalized value, and a Dropout that is the
+  // LayerNorm output's only reader applied on the way out (the output then not materialized).
+  struct LnFused { int64_t add = -1, a = -1, b = -1, din = -1, dout = -1; };
+  std::map<uint32_t, LnFused> ln_fused;  // LayerNorm -> parts
+  std::set<uint32_t> ln_fused_nodes;     // the Add and Dropouts a fused LayerNorm writes or applies
+  std::set<uint32_t> ln_skip_storage;    // values of those never materialized
+  for (size_t k = 0; k < n; ++k) {
+    const Node& y = p.nodes[k];
+    if (!need[k] || y.op != Op::LayerNorm) continue;
+    LnFused f;
+    const uint32_t xv = y.operands[0];
+    const size_t xk = p.pos.at(xv);
+    const Node& xn = p.node(xv);
+    bool later = true;
+    for (auto c : consumers[xk]) later = later && (c == k || c > k);
+    if (xn.op == Op::Add && xn.operands[0] != xn.operands[1] && later && !epi_nodes.count(xv) && !eg_add_nodes.count(xv) &&
+        xn.ty.shape == y.ty.shape) {
+      f.add = xv;
+      f.a = xn.operands[0];
+      f.b = xn.operands[1];
+      for (int side = 1; side >= 0; --side) {
+        const uint32_t d = xn.operands[size_t(side)];
+        const Node& dn = p.node(d);
+        if (dn.op == Op::Dropout && consumers[p.pos.at(d)].size() == 1 && !outputs.count(d)) {
+          f.din = d;
+          f.b = dn.operands[0];
+          f.a = xn.operands[size_t(1 - side)];
+          break;
+        }
+      }
+    }
+    if (consumers[k].size() == 1 && !outputs.count(y.id)) {
+      const Node& d = p.nodes[consumers[k][0]];
+      if (d.op == Op::Dropout && d.operands[0] == y.id) f.dout = d.id;
+    }
+    if (f.add < 0 && f.dout < 0) continue;
+    ln_fused[y.id] = f;
+    for (auto v : {f.add, f.din, f.dout})
+      if (v >= 0) ln_fused_nodes.insert(uint32_t(v));
+    if (f.din >= 0) ln_skip_storage.insert(uint32_t(f.din));
+    if (f.dout >= 0) ln_skip_storage.insert(y.id);
+  }
   // The LayerNorm gradients of one (input, output gradient) pair run as one pass: dx, and block
   // partials of the gamma and beta sums, finished by a batched column reduction, deferred to the
   // end of the step when only the optimizer reads them. The pass runs at its first member.
@@ -403,6 +446,7 @@ void Executor::build() {
       default:
         if (folded.count(x.id) || mm_fused.count(x.id) || mm_transposed.count(x.id) || eg_add.count(x.id)) break;
         if (gemm_epi.count(x.id) && gemm_epi.at(x.id).act != hk::EPI_GELU && gemm_epi.at(x.id).act != hk::EPI_RELU) break;
+        if (ln_skip_storage.count(x.id)) break;
         token_[x.id] = arena_.reserve(size_t(pitch.count(x.id) ? x.ty.shape[0] * pitch.at(x.id) : x.ty.count()) * 4);
         break;
     }
@@ -487,7 +531,7 @@ void Executor::build() {
     switch (x.op) {
       case Op::Input: case Op::ParamRead: case Op::Scalar: break;
       case Op::Add: case Op::Sub: case Op::Mul: case Op::Div: {
-        if (eg_add_nodes.count(id) || epi_nodes.count(id)) break;  // written by its EmbeddingGrad or GEMM
+        if (eg_add_nodes.count(id) || epi_nodes.count(id) || ln_fused_nodes.count(id)) break;  // written by a fused launch
         int op = x.op == Op::Add ? hk::EW_ADD : x.op == Op::Sub ? hk::EW_SUB : x.op == Op::Mul ? hk::EW_MUL : hk::EW_DIV;
         bool as = p.node(o[0]).ty.rank() == 0 && count > 1, bs = p.node(o[1]).ty.rank() == 0 && count > 1;
         uint32_t a = o[0], b = o[1];
@@ -663,6 +707,34 @@ void Executor::build() {
         bool have = ln_stats_tok.count(xv) != 0;
         if (!have) ln_stats_tok[xv] = R(size_t(rows) * 8);
         void* stats = ln_stats_tok[xv];
+        if (x.op == Op::LayerNorm && ln_fused.count(id)) {
+          const LnFused f = ln_fused.at(id);
+          const uint32_t gm = o[1], bt = o[2];
+          const bool write_stats = !have;
+          // (threshold, scale) of a Dropout node, as its own launch would use them.
+          auto spec = [&](int64_t d) {
+            if (d < 0) return std::make_pair(uint64_t(0), 1.0f);
+            const float pr = p.node(uint32_t(d)).scalar;
+            return std::make_pair(dropout_threshold(pr), 1.0f / (1.0f - pr));
+          };
+          const auto si = spec(f.din), so = spec(f.dout);
+          const int64_t tin = f.din >= 0 ? int64_t(p.node(uint32_t(f.din)).operands[size_t(token_operand(Op::Dropout))]) : -1;
+          const int64_t tout = f.dout >= 0 ? int64_t(p.node(uint32_t(f.dout)).operands[size_t(token_operand(Op::Dropout))]) : -1;
+          const int64_t av = f.add >= 0 ? f.a : -1, bv = f.add >= 0 ? f.b : int64_t(xv);
+          const int64_t yv = f.dout >= 0 ? -1 : int64_t(id);
+          what = "LayerNorm+fused %" + std::to_string(id);
+          for (auto [tag, v] : {std::pair<const char*, int64_t>{" add %", f.add}, {" dropout-in %", f.din}, {" dropout-out %", f.dout}})
+            if (v >= 0) what += tag + std::to_string(v);
+          what += " " + type_string(x.ty);
+          push([=](hipStream_t s) {
+            auto fp = [&](int64_t v2) { return v2 >= 0 ? F(uint32_t(v2)) : nullptr; };
+            hk::ln_fused(s, fp(av), F(uint32_t(bv)), tin >= 0 ? I(uint32_t(tin)) : nullptr, si.first, si.second, F(gm), F(bt),
+                         f.add >= 0 ? F(uint32_t(f.add)) : nullptr, fp(yv), write_stats ? static_cast<float*>(A(stats)) : nullptr,
+                         tout >= 0 ? I(uint32_t(tout)) : nullptr, so.first, so.second, fp(f.dout), rows, h, seed);
+          });
+          bytes = 4.0 * double(count) * (2 + (av >= 0) + (f.add >= 0) + (yv >= 0) + (f.dout >= 0));
+          break;
+        }
         if (x.op == Op::LayerNorm) {
           uint32_t gm = o[1], bt = o[2];
           bool write_stats = !have;
@@ -854,6 +926,7 @@ void Executor::build() {
         break;
       }
       case Op::Dropout: case Op::DropoutGrad: {
+        if (ln_fused_nodes.count(id)) break;  // applied by its fused LayerNorm
         uint32_t tok = o[size_t(token_operand(x.op))], a = o[x.op == Op::Dropout ? 0 : 1];
         uint64_t threshold = dropout_threshold(x.scalar);
         float scale = 1.0f / (1.0f - x.scalar);

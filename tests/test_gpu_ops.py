@@ -299,6 +299,36 @@ def test_dropout_masks_are_bit_exact_at_full_size(ctx, oracle):
     assert 0.88 < kept < 0.92
 
 
+@pytest.mark.parametrize("rows,h", [(4096, 128), (37, 200)])
+def test_fused_layer_norm_neighbours(ctx, oracle, rows, h):
+    """LayerNorm(e1 + e2) followed by a Dropout, and LayerNorm(a + Dropout(b)) with the residual sum
+    kept for the backward, as the fused pass runs them: values within the per-kernel tolerance of
+    the oracle, dropout masks bit for bit."""
+    e1, e2 = fast_values(81, rows * h).reshape(rows, h), fast_values(82, rows * h).reshape(rows, h)
+    a, b = fast_values(83, rows * h).reshape(rows, h), fast_values(84, rows * h).reshape(rows, h)
+    gamma, beta, G = fast_values(85, h, 0.5), fast_values(86, h, 0.5), fast_values(87, rows * h).reshape(rows, h)
+    t1, t2 = np.array([11, -3], np.int32), np.array([0x7123, 99], np.int32)
+    p = Prog()
+    ei, fi, ai, bi = (p.input(nm, (rows, h)) for nm in ("e1", "e2", "a", "b"))
+    gi, be, Gi = p.input("gamma", (h,)), p.input("beta", (h,)), p.input("G", (rows, h))
+    ti1, ti2 = p.input("t1", (2,), "i32"), p.input("t2", (2,), "i32")
+    x1 = p.op("Add", [ei, fi], (rows, h))
+    y1 = p.op("Dropout", [p.op("LayerNorm", [x1, gi, be], (rows, h)), ti1], (rows, h), "[p = 0.1, site = t1]")
+    d2 = p.op("Dropout", [bi, ti2], (rows, h), "[p = 0.1, site = t2]")
+    s2 = p.op("Add", [ai, d2], (rows, h))
+    y2 = p.op("LayerNorm", [s2, gi, be], (rows, h))
+    dx2 = p.op("LayerNormGradX", [s2, gi, Gi], (rows, h))
+    inputs = {"e1": e1, "e2": e2, "a": a, "b": b, "gamma": gamma, "beta": beta, "G": G, "t1": t1, "t2": t2}
+    got, want = both(ctx, oracle, p.out(y1, y2, dx2, s2), inputs, (0, 1, 2, 3), seed=5)
+    r_ln = (4 * np.abs(gamma) + np.abs(beta) + 1)[None, :] * np.ones((rows, 1))
+    assert np.array_equal(got[0] == 0, want[0] == 0)
+    assert within(got[0], want[0], (r_ln / 0.9).reshape(-1))[0]
+    assert within(got[1], want[1], r_ln.reshape(-1))[0]
+    assert np.array_equal(got[3].view(np.uint32), want[3].view(np.uint32))  # a + dropout(b): exact
+    rx = (np.abs(G) * np.abs(gamma)).sum(1, keepdims=True) / h * 8 / np.abs(want[3].reshape(rows, h)).std(1, keepdims=True)
+    assert within(got[2], want[2], (np.abs(want[2].reshape(rows, h)) + rx).reshape(-1))[0]
+
+
 def test_whole_tensor_sums(ctx, oracle):
     n = 1 << 16
     a, b = fast_values(20, n), fast_values(21, n)
