@@ -84,14 +84,19 @@ void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_
 // LayerNorm backward in one pass: dx when non-null, and when `partial` is non-null the per-block
 // partial sums [ln_backward_blocks, 2 h] of g * xhat (gamma gradient) then g (beta gradient), to be
 // added by column_finalize. gamma may be null when dx is.
+// dx2, when non-null, gets a function of dx on the way out: the dropout gradient (LNB_DROPOUT, with
+// token, threshold, scale and seed as `dropout`) or the GELU / ReLU gradient with respect to
+// pre-activation `pre` (LNB_GELU_GRAD / LNB_RELU_GRAD); dx itself may then be null.
+enum LnbPost : int { LNB_DROPOUT, LNB_GELU_GRAD, LNB_RELU_GRAD };
 int64_t ln_backward_blocks(int64_t rows, int64_t h);
 void ln_backward(hipStream_t s, const float* x, const float* gamma, const float* g, const float* stats, float* dx,
-                 float* partial, int64_t rows, int64_t h);
+                 float* partial, int64_t rows, int64_t h, float* dx2 = nullptr, int post = 0, const float* pre = nullptr,
+                 const int32_t* token = nullptr, uint64_t threshold = 0, float scale = 1.0f, uint64_t seed = 0);
 
 // Sums of block partials [chunks, width] over the blocks, columns below `split` to out_lo and the
 // rest to out_hi; up to kColumnJobs reductions a launch (`first` is set by column_finalize).
 struct ColumnJob { const float* partial; float* out_lo; float* out_hi; int32_t chunks, width, split, first; };
-constexpr int kColumnJobs = 16;
+constexpr int kColumnJobs = 48;
 struct ColumnJobs { ColumnJob job[kColumnJobs]; int32_t count; };
 void column_finalize(hipStream_t s, const ColumnJob* jobs, int count);
 

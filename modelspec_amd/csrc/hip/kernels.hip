@@ -258,7 +258,9 @@ template <int CPL>
 __global__ __launch_bounds__(256) void k_ln_backward(const float* __restrict__ x, const float* __restrict__ gamma,
                                                      const float* __restrict__ g, const float* __restrict__ stats,
                                                      float* __restrict__ dx, float* __restrict__ partial, int64_t rows,
-                                                     int64_t h, int64_t rows_per) {
+                                                     int64_t h, int64_t rows_per, float* __restrict__ dx2, int post,
+                                                     const float* __restrict__ pre, DropoutSpec dsp, uint32_t seed_lo,
+                                                     uint32_t seed_hi) {
   extern __shared__ float red[];  // [4 waves][2 h]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t r0 = int64_t(blockIdx.x) * rows_per, r1 = std::min<int64_t>(rows, r0 + rows_per);
@@ -290,14 +292,29 @@ __global__ __launch_bounds__(256) void k_ln_backward(const float* __restrict__ x
       pg[j] += gv[j] * xhat;
       pb[j] += gv[j];
     }
-    if (dx) {
+    if (dx || dx2) {
       const float mean_gx = wave_sum(s1) / width, mean_gx_xhat = wave_sum(s2) / width;
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int64_t c = lane + 64 * j;
         const float xhat = (xv[j] - mean) * rstd;
         const float gx = gv[j] * gm[j];
-        if (c < h) dx[row * h + c] = rstd * ((gx - mean_gx) - xhat * mean_gx_xhat);
+        if (c < h) {
+          const int64_t i = row * h + c;
+          const float v = rstd * ((gx - mean_gx) - xhat * mean_gx_xhat);
+          if (dx) dx[i] = v;
+          if (dx2) {
+            if (post == LNB_DROPOUT)
+              dx2[i] = uint64_t(philox_w0(uint32_t(i), 4u, uint32_t(dsp.token[0]), uint32_t(dsp.token[1]), seed_lo, seed_hi)) >=
+                               dsp.threshold
+                           ? v * dsp.scale
+                           : 0.0f;
+            else if (post == LNB_GELU_GRAD)
+              dx2[i] = d_gelu_grad(pre[i], v);
+            else
+              dx2[i] = pre[i] > 0.0f ? v : 0.0f;
+          }
+        }
       }
     }
   }
@@ -320,7 +337,11 @@ int64_t ln_backward_blocks(int64_t rows, int64_t h) {
   return std::max<int64_t>(1, std::min<int64_t>((rows + 15) / 16, 256));
 }
 void ln_backward(hipStream_t s, const float* x, const float* gamma, const float* g, const float* stats, float* dx,
-                 float* partial, int64_t rows, int64_t h) {
+                 float* partial, int64_t rows, int64_t h, float* dx2, int post, const float* pre,
+                 const int32_t* token, uint64_t threshold, float scale, uint64_t seed) {
+  if (dx2 && post == LNB_DROPOUT && !token) bad("LayerNorm backward dropout without its token");
+  if (dx2 && post != LNB_DROPOUT && !pre) bad("LayerNorm backward activation gradient without its input");
+  const DropoutSpec dsp{token, threshold, scale};
   if (rows <= 0 || h <= 0) return;
   if (h > 1024) bad("LayerNorm backward rows wider than 1024");
   const int64_t blocks = ln_backward_blocks(rows, h);
@@ -328,7 +349,7 @@ void ln_backward(hipStream_t s, const float* x, const float* gamma, const float*
   const size_t lds = size_t(8 * h) * 4;
   const int cpl = int((h + 63) / 64);
 #define MSX_LNB(C) MSX_LAUNCH(k_ln_backward<C>, dim3(unsigned(blocks)), dim3(256), lds, s, x, gamma, g, stats, dx, \
-                                      partial, rows, h, per)
+                              partial, rows, h, per, dx2, post, pre, dsp, uint32_t(seed), uint32_t(seed >> 32))
   if (cpl <= 1) MSX_LNB(1);
   else if (cpl <= 2) MSX_LNB(2);
   else if (cpl <= 4) MSX_LNB(4);

@@ -231,6 +231,9 @@ void Executor::build() {
     eg_add[x.id] = {a.id, other};
     eg_add_nodes.insert(a.id);
   }
+  std::set<uint32_t> grad_values_pre;  // values the optimizer reads as gradients
+  if (is_step_)
+    for (auto& pg : st.gradients) grad_values_pre.insert(pg.second);
   // GEMM epilogues. A GEMM's value (an unswapped MatMul, or the AddRows taking one as a biased
   // GEMM) that is read only by Add(X, value) with X computed earlier, or only as the incoming
   // gradient of GeluGrad/ReluGrad, is not materialized: the GEMM writes the consumer's value. A
@@ -238,6 +241,10 @@ void Executor::build() {
   struct Epi { uint32_t node; int act; int64_t aux; };  // consumer, hk::GemmAct, addend or pre-activation
   std::map<uint32_t, Epi> gemm_epi;                     // GEMM value -> consumer it writes
   std::set<uint32_t> epi_nodes;                         // consumers written by their GEMM
+  // Where a value is written: a fused writer's position when it runs before the value's own node.
+  std::map<uint32_t, size_t> written_at;
+  for (auto& [eg, add] : eg_add) written_at[add.first] = p.pos.at(eg);
+  auto ready = [&](uint32_t v) { return written_at.count(v) ? written_at.at(v) : p.pos.at(v); };
   for (size_t k = 0; k < n; ++k) {
     const Node& x = p.nodes[k];
     if (!need[k] || outputs.count(x.id)) continue;
@@ -250,16 +257,18 @@ void Executor::build() {
       const Node& c = p.nodes[cs[0]];
       if (c.op == Op::Add && !eg_add_nodes.count(c.id) && c.operands[0] != c.operands[1] && !epi_nodes.count(c.id)) {
         const uint32_t other = c.operands[0] == x.id ? c.operands[1] : c.operands[0];
-        if (p.pos.at(other) < k && p.node(other).ty.shape == x.ty.shape) {
+        if (ready(other) < k && p.node(other).ty.shape == x.ty.shape) {
           gemm_epi[x.id] = {c.id, hk::EPI_NONE, int64_t(other)};
           epi_nodes.insert(c.id);
+          written_at[c.id] = k;
           continue;
         }
       }
       if ((c.op == Op::GeluGrad || c.op == Op::ReluGrad) && c.operands[1] == x.id && c.operands[0] != x.id &&
-          p.pos.at(c.operands[0]) < k) {
+          ready(c.operands[0]) < k) {
         gemm_epi[x.id] = {c.id, c.op == Op::GeluGrad ? hk::EPI_GELU_GRAD : hk::EPI_RELU_GRAD, int64_t(c.operands[0])};
         epi_nodes.insert(c.id);
+        written_at[c.id] = k;
         continue;
       }
     }
@@ -268,6 +277,7 @@ void Executor::build() {
       if ((cn.op == Op::Gelu || cn.op == Op::Relu) && !epi_nodes.count(cn.id)) {
         gemm_epi[x.id] = {cn.id, cn.op == Op::Gelu ? hk::EPI_GELU : hk::EPI_RELU, -1};
         epi_nodes.insert(cn.id);
+        written_at[cn.id] = k;
         break;
       }
     }
@@ -286,8 +296,10 @@ void Executor::build() {
     const uint32_t xv = y.operands[0];
     const size_t xk = p.pos.at(xv);
     const Node& xn = p.node(xv);
+    // X is written at the LayerNorm: no reader may run earlier (a GEMM epilogue reading it runs at
+    // its GEMM).
     bool later = true;
-    for (auto c : consumers[xk]) later = later && (c == k || c > k);
+    for (auto c : consumers[xk]) later = later && (c == k || c > k) && !epi_nodes.count(p.nodes[c].id);
     if (xn.op == Op::Add && xn.operands[0] != xn.operands[1] && later && !epi_nodes.count(xv) && !eg_add_nodes.count(xv) &&
         xn.ty.shape == y.ty.shape) {
       f.add = xv;
@@ -318,7 +330,13 @@ void Executor::build() {
   // The LayerNorm gradients of one (input, output gradient) pair run as one pass: dx, and block
   // partials of the gamma and beta sums, finished by a batched column reduction, deferred to the
   // end of the step when only the optimizer reads them. The pass runs at its first member.
-  struct LnGroup { int64_t dx = -1, gamma = -1, beta = -1, gm = -1; size_t first = SIZE_MAX; };
+  struct LnGroup {
+    int64_t dx = -1, gamma = -1, beta = -1, gm = -1;
+    size_t first = SIZE_MAX;
+    int64_t post = -1, aux = -1;  // a DropoutGrad / GeluGrad / ReluGrad of dx the pass writes; token or input
+    int kind = 0;                 // hk::LnbPost
+    bool keep_dx = true;          // dx has readers besides the post
+  };
   std::map<std::pair<uint32_t, uint32_t>, LnGroup> ln_groups;
   for (size_t k = 0; k < n; ++k) {
     if (!need[k]) continue;
@@ -332,6 +350,28 @@ void Executor::build() {
       auto& gr = ln_groups[{x.operands[0], x.operands[1]}];
       gr.gamma = x.id;
       gr.first = std::min(gr.first, k);
+    }
+  }
+  // The dropout or activation gradient of dx written by the same pass.
+  std::set<uint32_t> ln_post_nodes;
+  for (auto& [key, gr] : ln_groups) {
+    if (gr.dx < 0) continue;
+    const size_t dk = p.pos.at(uint32_t(gr.dx));
+    for (auto c : consumers[dk]) {
+      const Node& cn = p.nodes[c];
+      if (epi_nodes.count(cn.id) || ln_fused_nodes.count(cn.id) || cn.operands[1] != uint32_t(gr.dx)) continue;
+      if (cn.op == Op::DropoutGrad && cn.operands[0] != uint32_t(gr.dx)) {
+        gr.post = cn.id; gr.kind = hk::LNB_DROPOUT; gr.aux = cn.operands[0];
+      } else if ((cn.op == Op::GeluGrad || cn.op == Op::ReluGrad) && cn.operands[0] != uint32_t(gr.dx) &&
+                 p.pos.at(cn.operands[0]) < gr.first) {
+        gr.post = cn.id; gr.kind = cn.op == Op::GeluGrad ? hk::LNB_GELU_GRAD : hk::LNB_RELU_GRAD; gr.aux = cn.operands[0];
+      } else {
+        continue;
+      }
+      ln_post_nodes.insert(cn.id);
+      gr.keep_dx = consumers[dk].size() > 1 || outputs.count(uint32_t(gr.dx)) || grad_values_pre.count(uint32_t(gr.dx));
+      if (!gr.keep_dx) ln_skip_storage.insert(uint32_t(gr.dx));
+      break;
     }
   }
   std::map<uint32_t, std::pair<uint32_t, uint32_t>> ln_member;  // member -> group key
@@ -546,7 +586,7 @@ void Executor::build() {
         break;
       }
       case Op::ReluGrad: case Op::GeluGrad: {
-        if (epi_nodes.count(id)) break;  // written by its GEMM
+        if (epi_nodes.count(id) || ln_post_nodes.count(id)) break;  // written by its GEMM or LayerNorm backward
         int op = x.op == Op::ReluGrad ? hk::EW_RELU_GRAD : hk::EW_GELU_GRAD;
         uint32_t a = o[0], g = o[1];
         push([=](hipStream_t s) { hk::elementwise(s, op, F(a), F(g), F(id), count, false, false); });
@@ -759,14 +799,26 @@ void Executor::build() {
         const bool sums = gr.gamma >= 0 || gr.beta >= 0;
         const int64_t chunks = hk::ln_backward_blocks(rows, h);
         void* part = sums ? R(size_t(chunks * 2 * h) * 4) : nullptr;
-        const int64_t dxv = gr.dx, gmv = gr.gm;
+        const int64_t dxv = gr.keep_dx ? gr.dx : -1, gmv = gr.gm, post = gr.post, aux = gr.aux;
+        const int kind = gr.kind;
         what = "LayerNormBackward";
-        for (auto [tag, v] : {std::pair<const char*, int64_t>{" dx %", gr.dx}, {" gamma %", gr.gamma}, {" beta %", gr.beta}})
+        for (auto [tag, v] : {std::pair<const char*, int64_t>{" dx %", gr.dx}, {" gamma %", gr.gamma}, {" beta %", gr.beta},
+                              {" post %", gr.post}})
           if (v >= 0) what += tag + std::to_string(v);
         what += " " + type_string(p.node(xv).ty);
+        uint64_t thr = 0;
+        float scl = 1.0f;
+        if (post >= 0 && kind == hk::LNB_DROPOUT) {
+          const float pr = p.node(uint32_t(post)).scalar;
+          thr = dropout_threshold(pr);
+          scl = 1.0f / (1.0f - pr);
+        }
         push([=](hipStream_t s) {
           hk::ln_backward(s, F(xv), gmv >= 0 ? F(uint32_t(gmv)) : nullptr, F(g), static_cast<float*>(A(stats)),
-                          dxv >= 0 ? F(uint32_t(dxv)) : nullptr, part ? static_cast<float*>(A(part)) : nullptr, rows, h);
+                          dxv >= 0 ? F(uint32_t(dxv)) : nullptr, part ? static_cast<float*>(A(part)) : nullptr, rows, h,
+                          post >= 0 ? F(uint32_t(post)) : nullptr, kind,
+                          post >= 0 && kind != hk::LNB_DROPOUT ? F(uint32_t(aux)) : nullptr,
+                          post >= 0 && kind == hk::LNB_DROPOUT ? I(uint32_t(aux)) : nullptr, thr, scl, seed);
         });
         bytes = 4.0 * double(rows * h * (dxv >= 0 ? 3 : 2) + (gmv >= 0 ? h : 0) + (sums ? 2 * h : 0));
         if (sums) {
@@ -926,7 +978,7 @@ void Executor::build() {
         break;
       }
       case Op::Dropout: case Op::DropoutGrad: {
-        if (ln_fused_nodes.count(id)) break;  // applied by its fused LayerNorm
+        if (ln_fused_nodes.count(id) || ln_post_nodes.count(id)) break;  // applied by a fused LayerNorm pass
         uint32_t tok = o[size_t(token_operand(x.op))], a = o[x.op == Op::Dropout ? 0 : 1];
         uint64_t threshold = dropout_threshold(x.scalar);
         float scale = 1.0f / (1.0f - x.scalar);

@@ -318,8 +318,17 @@ def test_fused_layer_norm_neighbours(ctx, oracle, rows, h):
     s2 = p.op("Add", [ai, d2], (rows, h))
     y2 = p.op("LayerNorm", [s2, gi, be], (rows, h))
     dx2 = p.op("LayerNormGradX", [s2, gi, Gi], (rows, h))
-    inputs = {"e1": e1, "e2": e2, "a": a, "b": b, "gamma": gamma, "beta": beta, "G": G, "t1": t1, "t2": t2}
-    got, want = both(ctx, oracle, p.out(y1, y2, dx2, s2), inputs, (0, 1, 2, 3), seed=5)
+    # LayerNorm backward passes that also write the dropout / GELU gradient of their dx.
+    Gb = p.input("Gb", (rows, h))
+    da = p.op("DropoutGrad", [ti1, p.op("LayerNormGradX", [x1, gi, Gi], (rows, h))], (rows, h), "[p = 0.1, site = t1]")
+    dxb = p.op("LayerNormGradX", [s2, gi, Gb], (rows, h))
+    gb = p.op("GeluGrad", [ai, dxb], (rows, h))
+    inputs = {"e1": e1, "e2": e2, "a": a, "b": b, "gamma": gamma, "beta": beta, "G": G, "t1": t1, "t2": t2,
+              "Gb": fast_values(88, rows * h).reshape(rows, h)}
+    got, want = both(ctx, oracle, p.out(y1, y2, dx2, s2, da, dxb, gb), inputs, (0, 1, 2, 3, 4, 5, 6), seed=5)
+    for gg, ww in zip(got[4:], want[4:]):
+        assert np.array_equal(gg == 0, ww == 0) or gg is got[5]
+        assert within(gg, ww, np.abs(ww) * 0.01 + 0.05 * np.abs(ww).max())[0]
     r_ln = (4 * np.abs(gamma) + np.abs(beta) + 1)[None, :] * np.ones((rows, 1))
     assert np.array_equal(got[0] == 0, want[0] == 0)
     assert within(got[0], want[0], (r_ln / 0.9).reshape(-1))[0]
