@@ -75,11 +75,12 @@ void layer_norm(hipStream_t s, const float* x, const float* gamma, const float* 
                 int64_t rows, int64_t h);
 // LayerNorm with its neighbours: s = [a +] [dropout](b) (a may be null; din_token null: no
 // dropout), y = LayerNorm(s; gamma, beta), yd = dropout(y) (dout_token non-null); each of s_out,
-// y_out, stats, yd_out written when non-null. Dropout as `dropout` (threshold, scale, seed).
+// y_out, stats, yd_out written when non-null. Dropout as `dropout` (threshold, scale, seed). With
+// `gather` ([rows] ids into the src_rows rows of a and b), row r of s is the sum's row gather[r].
 void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_token, uint64_t din_threshold,
               float din_scale, const float* gamma, const float* beta, float* s_out, float* y_out, float* stats,
               const int32_t* dout_token, uint64_t dout_threshold, float dout_scale, float* yd_out, int64_t rows,
-              int64_t h, uint64_t seed);
+              int64_t h, uint64_t seed, const int32_t* gather = nullptr, int64_t src_rows = 0);
 
 // LayerNorm backward in one pass: dx when non-null, and when `partial` is non-null the per-block
 // partial sums [ln_backward_blocks, 2 h] of g * xhat (gamma gradient) then g (beta gradient), to be

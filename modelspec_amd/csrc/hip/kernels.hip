@@ -184,6 +184,8 @@ void layer_norm(hipStream_t s, const float* x, const float* gamma, const float* 
 // LayerNorm with its neighbours in one pass, a wave a row: s = [a +] [dropout](b), y = LN(s) (the
 // arithmetic of k_layer_norm), optionally yd = dropout(y); s, y, yd and the statistics each
 // written when asked. The dropout keep rule is k_dropout's (Philox word 0 of the element index).
+// With `gather`, output row r takes its a, b and input dropout from row gather[r] of those
+// (an Embedding of the sum: element indices are the source rows'; an id out of range gives 0).
 struct DropoutSpec { const int32_t* token; uint64_t threshold; float scale; };
 template <int CPL>
 __global__ __launch_bounds__(256) void k_ln_fused(const float* __restrict__ a, const float* __restrict__ b,
@@ -191,10 +193,13 @@ __global__ __launch_bounds__(256) void k_ln_fused(const float* __restrict__ a, c
                                                   const float* __restrict__ beta, float* __restrict__ s_out,
                                                   float* __restrict__ y_out, float* __restrict__ stats,
                                                   DropoutSpec dout, float* __restrict__ yd_out, int64_t rows, int64_t h,
-                                                  uint32_t seed_lo, uint32_t seed_hi) {
+                                                  uint32_t seed_lo, uint32_t seed_hi, const int32_t* __restrict__ gather,
+                                                  int64_t src_rows) {
   const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
+  const int64_t src = gather ? int64_t(gather[row]) : row;
+  const bool src_ok = src >= 0 && src < src_rows;
   const uint32_t il = din.token ? uint32_t(din.token[0]) : 0u, ih = din.token ? uint32_t(din.token[1]) : 0u;
   float sv[CPL];
   float sum = 0.0f;
@@ -203,10 +208,12 @@ __global__ __launch_bounds__(256) void k_ln_fused(const float* __restrict__ a, c
     const int64_t c = lane + 64 * j;
     sv[j] = 0.0f;
     if (c < h) {
-      const int64_t i = row * h + c;
-      float v = b[i];
-      if (din.token) v = uint64_t(philox_w0(uint32_t(i), 4u, il, ih, seed_lo, seed_hi)) >= din.threshold ? v * din.scale : 0.0f;
-      sv[j] = a ? a[i] + v : v;
+      if (src_ok) {
+        const int64_t i = src * h + c;
+        float v = b[i];
+        if (din.token) v = uint64_t(philox_w0(uint32_t(i), 4u, il, ih, seed_lo, seed_hi)) >= din.threshold ? v * din.scale : 0.0f;
+        sv[j] = a ? a[i] + v : v;
+      }
       sum += sv[j];
     }
   }
@@ -234,14 +241,15 @@ __global__ __launch_bounds__(256) void k_ln_fused(const float* __restrict__ a, c
 void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_token, uint64_t din_threshold,
               float din_scale, const float* gamma, const float* beta, float* s_out, float* y_out, float* stats,
               const int32_t* dout_token, uint64_t dout_threshold, float dout_scale, float* yd_out, int64_t rows,
-              int64_t h, uint64_t seed) {
+              int64_t h, uint64_t seed, const int32_t* gather, int64_t src_rows) {
   if (rows <= 0 || h <= 0) return;
+  if (!gather) src_rows = rows;
   if (h > 1024) bad("fused LayerNorm rows wider than 1024");
   if (rows * h > (int64_t(1) << 32)) bad("fused LayerNorm over more than 2^32 elements");
   const DropoutSpec din{din_token, din_threshold, din_scale}, dout{dout_token, dout_threshold, dout_scale};
   const int cpl = int((h + 63) / 64);
 #define MSX_LNF(C) MSX_LAUNCH(k_ln_fused<C>, dim3(blocks_for(rows, 4)), dim3(256), 0, s, a, b, din, gamma, beta, s_out, y_out, \
-                              stats, dout, yd_out, rows, h, uint32_t(seed), uint32_t(seed >> 32))
+                              stats, dout, yd_out, rows, h, uint32_t(seed), uint32_t(seed >> 32), gather, src_rows)
   if (cpl <= 1) MSX_LNF(1);
   else if (cpl <= 2) MSX_LNF(2);
   else if (cpl <= 4) MSX_LNF(4);

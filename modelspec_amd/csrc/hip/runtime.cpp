@@ -285,7 +285,7 @@ void Executor::build() {
   // A LayerNorm with its neighbours in one pass: its input X = Add(A, B) (B possibly a Dropout read
   // only there, not materialized) written beside the normalized value, and a Dropout that is the
   // LayerNorm output's only reader applied on the way out (the output then not materialized).
-  struct LnFused { int64_t add = -1, a = -1, b = -1, din = -1, dout = -1; };
+  struct LnFused { int64_t add = -1, a = -1, b = -1, din = -1, dout = -1, gather = -1; };
   std::map<uint32_t, LnFused> ln_fused;  // LayerNorm -> parts
   std::set<uint32_t> ln_fused_nodes;     // the Add and Dropouts a fused LayerNorm writes or applies
   std::set<uint32_t> ln_skip_storage;    // values of those never materialized
@@ -293,15 +293,30 @@ void Executor::build() {
     const Node& y = p.nodes[k];
     if (!need[k] || y.op != Op::LayerNorm) continue;
     LnFused f;
-    const uint32_t xv = y.operands[0];
-    const size_t xk = p.pos.at(xv);
-    const Node& xn = p.node(xv);
+    uint32_t xv = y.operands[0];
     // X is written at the LayerNorm: no reader may run earlier (a GEMM epilogue reading it runs at
     // its GEMM).
-    bool later = true;
-    for (auto c : consumers[xk]) later = later && (c == k || c > k) && !epi_nodes.count(p.nodes[c].id);
+    auto later_readers = [&](uint32_t v) {
+      bool ok = true;
+      for (auto c : consumers[p.pos.at(v)]) ok = ok && (c == k || c > k) && !epi_nodes.count(p.nodes[c].id);
+      return ok;
+    };
+    bool later = later_readers(xv);
+    // LayerNorm(Embedding(Add(..), ids)) with the Add read only by that gather: the pass sums the
+    // gathered rows only.
+    if (p.node(xv).op == Op::Embedding && later && !outputs.count(p.node(xv).operands[0])) {
+      const uint32_t tv = p.node(xv).operands[0];
+      const Node& tn = p.node(tv);
+      if (tn.op == Op::Add && consumers[p.pos.at(tv)].size() == 1 && !epi_nodes.count(tv) && !eg_add_nodes.count(tv) &&
+          tn.ty.rank() == 2 && tn.ty.shape[1] == y.ty.shape[1]) {
+        f.gather = xv;
+        xv = tv;
+        later = true;
+      }
+    }
+    const Node& xn = p.node(xv);
     if (xn.op == Op::Add && xn.operands[0] != xn.operands[1] && later && !epi_nodes.count(xv) && !eg_add_nodes.count(xv) &&
-        xn.ty.shape == y.ty.shape) {
+        xn.ty.shape[1] == y.ty.shape[1]) {
       f.add = xv;
       f.a = xn.operands[0];
       f.b = xn.operands[1];
@@ -320,11 +335,13 @@ void Executor::build() {
       const Node& d = p.nodes[consumers[k][0]];
       if (d.op == Op::Dropout && d.operands[0] == y.id) f.dout = d.id;
     }
+    if (f.gather >= 0 && f.add < 0) f.gather = -1;
     if (f.add < 0 && f.dout < 0) continue;
     ln_fused[y.id] = f;
-    for (auto v : {f.add, f.din, f.dout})
+    for (auto v : {f.add, f.din, f.dout, f.gather})
       if (v >= 0) ln_fused_nodes.insert(uint32_t(v));
     if (f.din >= 0) ln_skip_storage.insert(uint32_t(f.din));
+    if (f.gather >= 0) ln_skip_storage.insert(uint32_t(f.add));  // only the gathered rows are formed
     if (f.dout >= 0) ln_skip_storage.insert(y.id);
   }
   // The LayerNorm gradients of one (input, output gradient) pair run as one pass: dx, and block
@@ -694,6 +711,7 @@ void Executor::build() {
         break;
       }
       case Op::Embedding: {
+        if (ln_fused_nodes.count(id)) break;  // gathered by its fused LayerNorm
         uint32_t t = o[0], ids = o[1];
         int64_t rows = shape(t)[0], h = shape(t)[1], nn = shape(ids)[0];
         if (p.node(ids).op == Op::Input) id_bounds_[p.node(ids).name] = rows;
@@ -761,16 +779,25 @@ void Executor::build() {
           const int64_t tin = f.din >= 0 ? int64_t(p.node(uint32_t(f.din)).operands[size_t(token_operand(Op::Dropout))]) : -1;
           const int64_t tout = f.dout >= 0 ? int64_t(p.node(uint32_t(f.dout)).operands[size_t(token_operand(Op::Dropout))]) : -1;
           const int64_t av = f.add >= 0 ? f.a : -1, bv = f.add >= 0 ? f.b : int64_t(xv);
+          const int64_t s_val = f.gather >= 0 ? f.gather : f.add;  // the LayerNorm input as stored
+          const int64_t gids = f.gather >= 0 ? int64_t(p.node(uint32_t(f.gather)).operands[1]) : -1;
+          const int64_t src_rows = f.gather >= 0 ? shape(uint32_t(f.add))[0] : rows;
+          if (gids >= 0 && p.node(uint32_t(gids)).op == Op::Input) {
+            auto it = id_bounds_.find(p.node(uint32_t(gids)).name);
+            id_bounds_[p.node(uint32_t(gids)).name] = it == id_bounds_.end() ? src_rows : std::min(it->second, src_rows);
+          }
           const int64_t yv = f.dout >= 0 ? -1 : int64_t(id);
           what = "LayerNorm+fused %" + std::to_string(id);
-          for (auto [tag, v] : {std::pair<const char*, int64_t>{" add %", f.add}, {" dropout-in %", f.din}, {" dropout-out %", f.dout}})
+          for (auto [tag, v] : {std::pair<const char*, int64_t>{" add %", f.add}, {" dropout-in %", f.din},
+                                {" dropout-out %", f.dout}, {" gather %", f.gather}})
             if (v >= 0) what += tag + std::to_string(v);
           what += " " + type_string(x.ty);
           push([=](hipStream_t s) {
             auto fp = [&](int64_t v2) { return v2 >= 0 ? F(uint32_t(v2)) : nullptr; };
             hk::ln_fused(s, fp(av), F(uint32_t(bv)), tin >= 0 ? I(uint32_t(tin)) : nullptr, si.first, si.second, F(gm), F(bt),
-                         f.add >= 0 ? F(uint32_t(f.add)) : nullptr, fp(yv), write_stats ? static_cast<float*>(A(stats)) : nullptr,
-                         tout >= 0 ? I(uint32_t(tout)) : nullptr, so.first, so.second, fp(f.dout), rows, h, seed);
+                         fp(s_val), fp(yv), write_stats ? static_cast<float*>(A(stats)) : nullptr,
+                         tout >= 0 ? I(uint32_t(tout)) : nullptr, so.first, so.second, fp(f.dout), rows, h, seed,
+                         gids >= 0 ? I(uint32_t(gids)) : nullptr, src_rows);
           });
           bytes = 4.0 * double(count) * (2 + (av >= 0) + (f.add >= 0) + (yv >= 0) + (f.dout >= 0));
           break;

@@ -323,9 +323,20 @@ def test_fused_layer_norm_neighbours(ctx, oracle, rows, h):
     da = p.op("DropoutGrad", [ti1, p.op("LayerNormGradX", [x1, gi, Gi], (rows, h))], (rows, h), "[p = 0.1, site = t1]")
     dxb = p.op("LayerNormGradX", [s2, gi, Gb], (rows, h))
     gb = p.op("GeluGrad", [ai, dxb], (rows, h))
+    # LayerNorm of a gather of a residual sum (the masked rows of the last layer): only those rows.
+    nr = max(1, rows // 5)
+    ids = np.random.default_rng(9).permutation(rows)[:nr].astype(np.int32)
+    ii, ti3, G3 = p.input("ids", (nr,), "i32"), p.input("t3", (2,), "i32"), p.input("G3", (nr, h))
+    e3 = p.op("Embedding", [p.op("Add", [ai, p.op("Dropout", [bi, ti3], (rows, h), "[p = 0.1, site = t3]")], (rows, h)), ii],
+              (nr, h))
+    y3 = p.op("LayerNorm", [e3, gi, be], (nr, h))
+    dx3 = p.op("LayerNormGradX", [e3, gi, G3], (nr, h))
     inputs = {"e1": e1, "e2": e2, "a": a, "b": b, "gamma": gamma, "beta": beta, "G": G, "t1": t1, "t2": t2,
-              "Gb": fast_values(88, rows * h).reshape(rows, h)}
-    got, want = both(ctx, oracle, p.out(y1, y2, dx2, s2, da, dxb, gb), inputs, (0, 1, 2, 3, 4, 5, 6), seed=5)
+              "Gb": fast_values(88, rows * h).reshape(rows, h), "ids": ids, "t3": np.array([5, 6], np.int32),
+              "G3": fast_values(89, nr * h).reshape(nr, h)}
+    got, want = both(ctx, oracle, p.out(y1, y2, dx2, s2, da, dxb, gb, y3, dx3), inputs, tuple(range(9)), seed=5)
+    assert within(got[7], want[7], np.ones(nr * h) * (4 * np.abs(gamma).max() + np.abs(beta).max() + 1))[0]
+    assert within(got[8], want[8], np.abs(want[8]) * 0.01 + 0.05 * np.abs(want[8]).max())[0]
     for gg, ww in zip(got[4:], want[4:]):
         assert np.array_equal(gg == 0, ww == 0) or gg is got[5]
         assert within(gg, ww, np.abs(ww) * 0.01 + 0.05 * np.abs(ww).max())[0]
