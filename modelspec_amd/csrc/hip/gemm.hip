@@ -157,10 +157,12 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   constexpr int GA = TM * WK / 4, GB = TN * WK / 4;              // float4 groups a K tile
   constexpr int HA = (GA + 255) / 256, HB = (GB + 255) / 256;     // a thread's groups
   // The K tiles (double-buffered), and afterwards the output tile on its way to memory.
-  __shared__ float smem[2 * WK * LA + 2 * WK * LB];
-  static_assert(TM * LC <= 2 * WK * LA + 2 * WK * LB, "output tile exceeds the LDS of the K tiles");
-  float* const As0 = smem;                 // As(buf) = As0 + buf WK LA
-  float* const Bs0 = smem + 2 * WK * LA;   // Bs(buf) = Bs0 + buf WK LB
+  // Deep K tiles (WK >= 128, meant for K <= WK: one tile) are single-buffered.
+  constexpr int NB = WK >= 128 ? 1 : 2;
+  __shared__ float smem[NB * WK * LA + NB * WK * LB];
+  static_assert(TM * LC <= NB * WK * LA + NB * WK * LB, "output tile exceeds the LDS of the K tiles");
+  float* const As0 = smem;                  // As(buf) = As0 + buf WK LA
+  float* const Bs0 = smem + NB * WK * LA;   // Bs(buf) = Bs0 + buf WK LB
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t m0 = int64_t(blockIdx.y) * TM, n0 = int64_t(blockIdx.x) * TN;
   const int64_t kbeg = int64_t(blockIdx.z) * kchunk;
@@ -188,6 +190,7 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   float csum = 0.0f;
   int buf = 0;
   for (int64_t k0 = kbeg; k0 < kend; k0 += WK) {
+    if (NB == 1 && k0 != kbeg) __syncthreads();  // the single buffer is free again
 #pragma unroll
     for (int h = 0; h < HA; ++h)
       if (tid + 256 * h < GA) wide_store<!TA, TM, LA, WK>(As0 + buf * (WK * LA), tid + 256 * h, ra[h]);
@@ -222,7 +225,7 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
       const float* ss = (sum_a ? as : bs) + sum_off;
       for (int j = 0; j < sum_per; ++j) csum += ss[j * sum_ld];
     }
-    buf ^= 1;
+    buf = NB == 2 ? buf ^ 1 : 0;
   }
   if (sums) {
     __syncthreads();
