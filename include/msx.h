@@ -89,12 +89,44 @@ int msx_forward(msx_ctx* ctx, const msx_tensor* inputs, uint32_t n_inputs, float
 
 int msx_stats(msx_ctx* ctx, msx_run_stats* out);
 
+/* Held-out metrics (crates/modelspec-runtime/src/train/eval.rs:27-39, HeldOutMetrics at :94-98):
+ * loss = sum(w nll) / sum(w) over every row of every batch (f64 sums, rounded to f32 once, 0 when
+ * the weight sum is 0); accuracy = correct / selected over the rows of positive weight. The
+ * numerator and the correct count are the device's sums, the denominator and the selected count
+ * the host's sums of the batches' weights (HeldOut::metrics_of_sums, eval.rs:299-339). */
+typedef struct {
+  float loss;
+  float accuracy;
+  double numerator;
+  double denominator;
+  uint64_t correct;
+  uint64_t selected;
+} msx_heldout;
+
+/* Evaluates the loaded forward program on the current parameters (after every step run so far)
+ * over `n` held-out batches: batch i is the n_inputs[i] tensors at inputs[i], its labels and
+ * weights the inputs named `labels` and `weights`. The logits of each batch are reduced on the
+ * device; one host wait. A label outside the classes is MSX_E_DATA. Replaces HeldOut::evaluate
+ * (eval.rs:211-262) and the device reduction of vulkan/stepwise.rs:1635-1760. */
+int msx_evaluate(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, const uint32_t* n_inputs,
+                 const char* labels, const char* weights, msx_heldout* out);
+
 /* A whole run of a built-in config on the context's device: initial parameters from the seed,
  * synthetic batches, `steps` steps (negative: the config's own), the final loss. Writes steps + 1
  * losses and the final parameters concatenated in ParamId order. Replaces the device branch of
  * crates/modelspec-cli/src/train.rs:1045-1200 with runner::run_checked's loop semantics. */
 int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t masked_rows, float* losses,
                      uint64_t losses_len, float* params, uint64_t params_len, double* train_seconds);
+
+/* msx_train_config with held-out evaluation (`train --eval-every`, crates/modelspec-cli/src/
+ * train.rs:1293-1312): before step k with k % eval_every == 0 and after the last step, the
+ * forward program over `eval_batches` synthetic held-out batches (batch b drawn at step id
+ * 2^63 + b). Writes the evaluated steps and their metrics (at most evals_len) and their count to
+ * *n_evals; eval_seconds (may be null) is the evaluations' wall clock, which train_seconds
+ * excludes. */
+int msx_train_config_eval(msx_ctx* ctx, const char* config, int64_t steps, uint64_t eval_every, uint64_t eval_batches,
+                          float* losses, uint64_t losses_len, uint64_t* eval_steps, msx_heldout* evals,
+                          uint64_t evals_len, uint64_t* n_evals, double* train_seconds, double* eval_seconds);
 
 /* Times `steps` graph-launched training steps of a built-in config after `warmup` (HIP events on
  * the run's stream after every step into step_ms[steps], may be null; host inputs made before the

@@ -33,6 +33,14 @@ class RunStats(ctypes.Structure):
                 ("device_bytes", ctypes.c_uint64)]
 
 
+class HeldOutMetrics(ctypes.Structure):
+    _fields_ = [("loss", ctypes.c_float), ("accuracy", ctypes.c_float), ("numerator", ctypes.c_double),
+                ("denominator", ctypes.c_double), ("correct", ctypes.c_uint64), ("selected", ctypes.c_uint64)]
+
+    def as_dict(self):
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
 _lib = None
 
 
@@ -56,6 +64,11 @@ def lib():
         L.msx_forward.argtypes = [vp, ctypes.POINTER(Tensor), u32, vp, vp, u64]
         L.msx_stats.argtypes = [vp, ctypes.POINTER(RunStats)]
         L.msx_train_config.argtypes = [vp, ctypes.c_char_p, c64, c64, vp, u64, vp, u64, ctypes.POINTER(ctypes.c_double)]
+        L.msx_evaluate.argtypes = [vp, u32, ctypes.POINTER(ctypes.POINTER(Tensor)), ctypes.POINTER(u32),
+                                   ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(HeldOutMetrics)]
+        L.msx_train_config_eval.argtypes = [vp, ctypes.c_char_p, c64, u64, u64, vp, u64, vp,
+                                            ctypes.POINTER(HeldOutMetrics), u64, ctypes.POINTER(u64),
+                                            ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
         L.msx_prog_new.argtypes = [vp, ctypes.c_char_p, u64, ctypes.POINTER(vp)]
         L.msx_prog_run.argtypes = [vp, ctypes.POINTER(Tensor), u32, ctypes.POINTER(vp), ctypes.POINTER(u64), u32]
         L.msx_prog_output.argtypes = [vp, u32, vp, u64]
@@ -166,16 +179,22 @@ class Context:
         _check(lib().msx_read_moment(self._h, k, ord(which), out.ctypes.data, count))
         return out
 
-    def run_steps(self, per_step):
-        """per_step: list of {name: ndarray}; returns the losses."""
+    @staticmethod
+    def _batches(per_step):
         n = len(per_step)
         arrs, keep = [], []
         for named in per_step:
             a, k = _tensors(named)
             arrs.append(a)
             keep += k
-        ptrs = (ctypes.POINTER(Tensor) * n)(*[ctypes.cast(a, ctypes.POINTER(Tensor)) for a in arrs])
-        counts = (ctypes.c_uint32 * n)(*[len(d) for d in per_step])
+        ptrs = (ctypes.POINTER(Tensor) * max(1, n))(*[ctypes.cast(a, ctypes.POINTER(Tensor)) for a in arrs])
+        counts = (ctypes.c_uint32 * max(1, n))(*[len(d) for d in per_step])
+        return ptrs, counts, (arrs, keep)
+
+    def run_steps(self, per_step):
+        """per_step: list of {name: ndarray}; returns the losses."""
+        n = len(per_step)
+        ptrs, counts, keep = self._batches(per_step)
         losses = np.empty(n, np.float32)
         _check(lib().msx_run_steps(self._h, n, ptrs, counts, losses.ctypes.data))
         return losses
@@ -187,6 +206,28 @@ class Context:
         _check(lib().msx_forward(self._h, arr, len(inputs), ctypes.addressof(loss),
                                  pred.ctypes.data if pred is not None else None, prediction_count))
         return loss.value, pred
+
+    def evaluate(self, batches, labels, weights):
+        """Held-out metrics of the forward program on the current parameters over `batches`
+        ({name: ndarray} each): a dict of loss, accuracy, numerator, denominator, correct, selected."""
+        ptrs, counts, keep = self._batches(batches)
+        out = HeldOutMetrics()
+        _check(lib().msx_evaluate(self._h, len(batches), ptrs, counts, labels.encode(), weights.encode(),
+                                  ctypes.byref(out)))
+        return out.as_dict()
+
+    def train_config_eval(self, name, eval_every, eval_batches, steps=-1):
+        """A synthetic run with held-out evaluation: (losses, [(step, metrics dict)], train s, eval s)."""
+        n_steps = steps if steps >= 0 else config_steps(name)
+        losses = np.zeros(n_steps + 1, np.float32)
+        cap = n_steps // eval_every + 2
+        at = np.zeros(cap, np.uint64)
+        evals = (HeldOutMetrics * cap)()
+        n, ts, es = ctypes.c_uint64(), ctypes.c_double(), ctypes.c_double()
+        _check(lib().msx_train_config_eval(self._h, name.encode(), steps, eval_every, eval_batches, losses.ctypes.data,
+                                           losses.size, at.ctypes.data, evals, cap, ctypes.byref(n), ctypes.byref(ts),
+                                           ctypes.byref(es)))
+        return losses, [(int(at[k]), evals[k].as_dict()) for k in range(n.value)], ts.value, es.value
 
     def stats(self):
         s = RunStats()

@@ -24,6 +24,8 @@ int guarded(F&& f) {
     return f();
   } catch (const msx::HipError& e) {
     return fail(MSX_E_DEVICE, e.what());
+  } catch (const msx::HeldOutLabelError& e) {
+    return fail(MSX_E_DATA, e.what());
   } catch (const msx::IrError& e) {
     std::string w = e.what();
     if (w.find("E-DATA-") != std::string::npos || w.find("key mask") != std::string::npos ||
@@ -74,6 +76,7 @@ struct msx_ctx {
   std::unique_ptr<msx::Session> session;
   msx::TrainingStep step;
   msx::Program forward;
+  uint32_t prediction = 0;  // the forward program's prediction value
 };
 
 struct msx_prog {
@@ -137,6 +140,7 @@ int msx_load(msx_ctx* ctx, const char* step_ir, const char* forward_ir, uint64_t
     if (!ctx->step.has_optimizer) return fail(MSX_E_INVALID, "the step IR has no optimizer");
     ctx->forward = msx::parse_program(forward_ir);
     if (prediction_output >= ctx->forward.outputs.size()) return fail(MSX_E_INVALID, "no such forward output");
+    ctx->prediction = ctx->forward.outputs[prediction_output];
     ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, seed,
                                                   ctx->forward.outputs[prediction_output]);
     return MSX_OK;
@@ -200,9 +204,7 @@ int msx_forward(msx_ctx* ctx, const msx_tensor* inputs, uint32_t n_inputs, float
     float loss = ctx->session->final_loss(b);
     if (loss_out) *loss_out = loss;
     if (prediction_out) {
-      uint32_t pred = 0;
-      for (auto o : ctx->forward.outputs)
-        if (o != ctx->forward.outputs[0]) pred = o;
+      const uint32_t pred = ctx->prediction;
       if (ctx->forward.node(pred).ty.count() != int64_t(prediction_count)) return fail(MSX_E_INVALID, "prediction count");
       msx::hip_check(hipMemcpy(prediction_out, ctx->session->forward_value(pred), prediction_count * 4, hipMemcpyDeviceToHost),
                      "hipMemcpy (prediction)");
@@ -224,6 +226,88 @@ int msx_stats(msx_ctx* ctx, msx_run_stats* out) {
   });
 }
 
+namespace {
+// The metrics of `sums` with the host's own sums of `h`'s weights beside them.
+msx_heldout heldout_of(const msx::HeldOut& h, const msx::HeldOutSums& sums) {
+  msx::HeldOutMetrics m = h.metrics_of_sums(sums);
+  msx_heldout out{};
+  out.loss = m.loss;
+  out.accuracy = m.accuracy;
+  out.numerator = sums.numerator;
+  out.correct = sums.correct;
+  bool first = true;
+  for (auto& b : h.batches())
+    for (float w : b.f32.at(h.weights_name())) {
+      out.denominator = first ? double(w) : out.denominator + double(w);
+      first = false;
+      if (w > 0.0f) ++out.selected;
+    }
+  return out;
+}
+}  // namespace
+
+int msx_evaluate(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, const uint32_t* n_inputs,
+                 const char* labels, const char* weights, msx_heldout* out) {
+  return guarded([&] {
+    if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
+    if (!labels || !weights || !out || (n && (!inputs || !n_inputs))) return fail(MSX_E_INVALID, "null argument");
+    std::vector<msx::Batch> batches;
+    for (uint32_t i = 0; i < n; ++i) batches.push_back(batch_of(inputs[i], n_inputs[i]));
+    msx::HeldOut h(ctx->forward, ctx->prediction, labels, weights, std::move(batches));
+    *out = heldout_of(h, ctx->session->held_out(h));
+    return MSX_OK;
+  });
+}
+
+int msx_train_config_eval(msx_ctx* ctx, const char* config, int64_t steps, uint64_t eval_every, uint64_t eval_batches,
+                          float* losses, uint64_t losses_len, uint64_t* eval_steps, msx_heldout* evals,
+                          uint64_t evals_len, uint64_t* n_evals, double* train_seconds, double* eval_seconds) {
+  return guarded([&] {
+    if (eval_every == 0) return fail(MSX_E_INVALID, "eval_every takes a step count of at least 1, not 0");
+    msx::Compiled c = msx::compile_config(config, -1, steps);
+    ctx->session.reset();
+    ctx->step = c.step;
+    ctx->forward = c.forward;
+    ctx->prediction = c.prediction;
+    ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction);
+    // Sums of each evaluation, finished with the host's weight sums as msx_evaluate does.
+    struct Recording : msx::Engine {
+      msx::Session& s;
+      std::vector<msx::HeldOutSums> sums;
+      const msx::HeldOut* h = nullptr;
+      explicit Recording(msx::Session& x) : s(x) {}
+      void set_params(const std::vector<std::vector<float>>& v) override { s.set_params(v); }
+      std::vector<std::vector<float>> params() override { return s.params(); }
+      std::vector<std::vector<float>> moments(char w) override { return s.moments(w); }
+      std::vector<float> predict(const std::vector<std::vector<float>>& v, const msx::Batch& b) override { return s.predict(v, b); }
+      void train_step(const msx::StepInputs& in) override { s.train_step(in); }
+      float final_loss(const msx::Batch& b) override { return s.final_loss(b); }
+      std::vector<float> losses() override { return s.losses(); }
+      msx::HeldOutSums held_out(const msx::HeldOut& x) override {
+        h = &x;
+        sums.push_back(s.held_out(x));
+        return sums.back();
+      }
+    } rec(*ctx->session);
+    msx::RunResult r = msx::run(c, rec, c.config.steps, eval_every, eval_batches);
+    if (losses_len < r.losses.size()) return fail(MSX_E_INVALID, "losses buffer too small");
+    if (losses) std::memcpy(losses, r.losses.data(), r.losses.size() * 4);
+    if (r.evals.size() > evals_len) return fail(MSX_E_INVALID, "evals buffer too small");
+    msx::Feed feed(c);
+    msx::HeldOut h(c, feed, eval_batches);
+    for (size_t k = 0; k < r.evals.size(); ++k) {
+      if (eval_steps) eval_steps[k] = r.evals[k].first;
+      if (evals) evals[k] = heldout_of(h, rec.sums[k]);
+    }
+    if (n_evals) *n_evals = r.evals.size();
+    if (train_seconds) *train_seconds = r.train_seconds;
+    if (eval_seconds) *eval_seconds = r.eval_seconds;
+    if (r.nonfinite_step >= 0)
+      return fail(MSX_E_NONFINITE, "E-TRAIN-001: the loss of step " + std::to_string(r.nonfinite_step) + " is not finite");
+    return MSX_OK;
+  });
+}
+
 int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t masked_rows, float* losses,
                      uint64_t losses_len, float* params, uint64_t params_len, double* train_seconds) {
   return guarded([&] {
@@ -231,6 +315,7 @@ int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t ma
     ctx->session.reset();
     ctx->step = c.step;
     ctx->forward = c.forward;
+    ctx->prediction = c.prediction;
     ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction);
     msx::RunResult r = msx::run(c, *ctx->session, c.config.steps);
     if (losses_len < r.losses.size()) return fail(MSX_E_INVALID, "losses buffer too small");
@@ -256,6 +341,7 @@ int msx_bench_config(msx_ctx* ctx, const char* config, int64_t masked_rows, uint
     ctx->session.reset();
     ctx->step = c.step;
     ctx->forward = c.forward;
+    ctx->prediction = c.prediction;
     ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction);
     msx::Session& s = *ctx->session;
     msx::Feed feed(c);

@@ -138,6 +138,19 @@ void ce_rows(hipStream_t s, const float* logits, const int32_t* labels, const fl
 void ce_grad(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats,
              const float* den, const float* g, float* o, int64_t rows, int64_t v, int64_t ld);
 
+// Held-out evaluation (train/eval.rs). held_out_rows: per row r of logits [rows, v] (row pitch
+// ld), out[2r] = max + ln(sum exp(x - max)) - x[label] and out[2r + 1] = 1 when the row holds no
+// NaN and its first largest logit (lowest id among ties) is its label, else 0. Labels must lie in
+// [0, v) (the host checks them). held_out_sum: adds sum_r w_r out[2r] in f64 and the count of rows
+// with w_r > 0 and a hit to `state` (HeldOutState), which the caller zeroes before the first batch.
+struct HeldOutState {
+  double numerator;
+  unsigned long long correct;
+};
+void held_out_rows(hipStream_t s, const float* logits, const int32_t* labels, float* out, int64_t rows, int64_t v,
+                   int64_t ld);
+void held_out_sum(hipStream_t s, const float* rows_in, const float* w, int64_t rows, HeldOutState* state);
+
 void softmax(hipStream_t s, const float* x, float* o, int64_t rows, int64_t k);
 void softmax_grad(hipStream_t s, const float* y, const float* g, float* o, int64_t rows, int64_t k);
 

@@ -867,6 +867,127 @@ void ce_rows(hipStream_t s, const float* logits, const int32_t* labels, const fl
 }
 
 // ---------------------------------------------------------------------------------------------
+// Held-out evaluation: one block of 256 per row. The first pass finds the largest logit and its
+// first index (each thread scans its columns ascending, and equal maxima of different threads
+// resolve to the lower index, which is the first largest of the row) and whether a NaN occurs;
+// the second sums exp(x - max). A NaN or an infinity among the logits makes the nll NaN through
+// the arithmetic itself, as the sequential restatement does.
+__device__ __forceinline__ void better_of(float& m, int64_t& at, float m2, int64_t at2) {
+  if (m2 > m || (m2 == m && at2 < at)) {
+    m = m2;
+    at = at2;
+  }
+}
+__global__ __launch_bounds__(256) void k_held_out_rows(const float* __restrict__ x, const int32_t* __restrict__ labels,
+                                                       float* __restrict__ out, int64_t v, int64_t ld) {
+  __shared__ float red_m[4];
+  __shared__ int64_t red_at[4];
+  __shared__ int red_nan[4];
+  const int64_t r = blockIdx.x;
+  const float* row = x + r * ld;
+  const int tid = threadIdx.x;
+  float m = -INFINITY;
+  int64_t at = v;  // no column yet: loses every tie
+  bool nan = false;
+  for (int64_t c0 = 0; c0 < v; c0 += 256 * 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t c = c0 + tid + 256 * u;
+      t[u] = c < v ? row[c] : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      nan = nan || (t[u] != t[u]);
+      if (t[u] > m) {
+        m = t[u];
+        at = c0 + tid + 256 * u;
+      }
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float m2 = __shfl_xor(m, o, 64);
+    const int64_t at2 = __shfl_xor(at, o, 64);
+    better_of(m, at, m2, at2);
+  }
+  const bool wave_nan = __any(nan);
+  if ((tid & 63) == 0) {
+    red_m[tid >> 6] = m;
+    red_at[tid >> 6] = at;
+    red_nan[tid >> 6] = wave_nan;
+  }
+  __syncthreads();
+  m = red_m[0];
+  at = red_at[0];
+  for (int k = 1; k < 4; ++k) better_of(m, at, red_m[k], red_at[k]);
+  const bool row_nan = red_nan[0] | red_nan[1] | red_nan[2] | red_nan[3];
+  if (at >= v) at = 0;  // every logit -inf: the first column is the first largest
+  float total = 0.0f;
+  for (int64_t c0 = 0; c0 < v; c0 += 256 * 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t c = c0 + tid + 256 * u;
+      t[u] = c < v ? row[c] : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) total += expf(t[u] - m);
+  }
+  total = wave_sum(total);
+  __syncthreads();
+  if ((tid & 63) == 0) red_m[tid >> 6] = total;
+  __syncthreads();
+  if (tid == 0) {
+    const int32_t label = labels[r];
+    total = (red_m[0] + red_m[1]) + (red_m[2] + red_m[3]);
+    out[2 * r] = m + logf(total) - row[label];
+    out[2 * r + 1] = (!row_nan && at == int64_t(label)) ? 1.0f : 0.0f;
+  }
+}
+void held_out_rows(hipStream_t s, const float* logits, const int32_t* labels, float* out, int64_t rows, int64_t v,
+                   int64_t ld) {
+  if (rows <= 0) return;
+  if (rows > 2147483647) bad("held-out rows");
+  if (v <= 0 || ld < v) bad("held-out logits pitch");
+  MSX_LAUNCH(k_held_out_rows, dim3(unsigned(rows)), dim3(256), 0, s, logits, labels, out, v, ld);
+}
+
+__global__ __launch_bounds__(1024) void k_held_out_sum(const float* __restrict__ rows_in, const float* __restrict__ w,
+                                                       int64_t rows, HeldOutState* __restrict__ state) {
+  __shared__ double num_s[16];
+  __shared__ unsigned long long hit_s[16];
+  double num = 0.0;
+  unsigned long long hits = 0;
+  for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) {
+    const float wr = w[r];
+    num = __builtin_fma(double(wr), double(rows_in[2 * r]), num);
+    hits += (wr > 0.0f && rows_in[2 * r + 1] == 1.0f) ? 1 : 0;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    num += __shfl_xor(num, o, 64);
+    hits += __shfl_xor(hits, o, 64);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    num_s[wave] = num;
+    hit_s[wave] = hits;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < int(blockDim.x >> 6); ++k) {
+      num += num_s[k];
+      hits += hit_s[k];
+    }
+    state->numerator += num;
+    state->correct += hits;
+  }
+}
+void held_out_sum(hipStream_t s, const float* rows_in, const float* w, int64_t rows, HeldOutState* state) {
+  if (rows <= 0) return;
+  MSX_LAUNCH(k_held_out_sum, dim3(1), dim3(1024), 0, s, rows_in, w, rows, state);
+}
+
+// ---------------------------------------------------------------------------------------------
 __global__ void k_softmax(const float* __restrict__ x, float* __restrict__ o, int64_t k) {
   __shared__ float red[4];
   const int64_t r = blockIdx.x;

@@ -1196,6 +1196,7 @@ Session::~Session() {
   step_exec_.reset();
   fwd_exec_.reset();
   if (state_mem_) (void)hipFree(state_mem_);
+  if (eval_mem_) (void)hipFree(eval_mem_);
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
@@ -1327,6 +1328,41 @@ float Session::final_loss(const Batch& batch) {
   float loss = 0;
   hip_check(hipMemcpy(&loss, fwd_exec_->value(fwd_exec_->loss_value), 4, hipMemcpyDeviceToHost), "hipMemcpy (loss)");
   return loss;
+}
+
+HeldOutSums Session::held_out(const HeldOut& h) {
+  h.check_labels();
+  const Node* lab = forward_.input(h.labels_name());
+  const Node* w = forward_.input(h.weights_name());
+  const Node& pred = forward_.node(prediction_);
+  if (!lab || !w || lab->ty.dtype != DType::I32 || w->ty.dtype != DType::F32 || pred.ty.rank() != 2 ||
+      pred.ty.shape[1] != h.classes() || pred.ty.shape[0] != lab->ty.count() || w->ty.count() != lab->ty.count())
+    throw IrError("held-out evaluation: the forward program's prediction, labels and weights do not match");
+  const int64_t rows = lab->ty.count(), v = h.classes();
+  // Row results first, the state at the next 256-byte boundary behind them.
+  const size_t state_at = (size_t(rows) * 8 + 255) / 256 * 256;
+  if (rows > eval_rows_) {
+    sync();
+    if (eval_mem_) hip_check(hipFree(eval_mem_), "hipFree (held-out)");
+    eval_mem_ = nullptr;
+    eval_rows_ = 0;
+    hip_check(hipMalloc(&eval_mem_, state_at + 256), "hipMalloc (held-out)");
+    eval_rows_ = rows;
+  }
+  float* row_out = static_cast<float*>(eval_mem_);
+  auto* state = reinterpret_cast<hk::HeldOutState*>(static_cast<char*>(eval_mem_) + state_at);
+  hk::fill_zero(stream_, state, 16);
+  for (auto& batch : h.batches()) {
+    fwd_exec_->stage(batch);
+    fwd_exec_->run(stream_);
+    hk::held_out_rows(stream_, static_cast<const float*>(fwd_exec_->value(prediction_)),
+                      static_cast<const int32_t*>(fwd_exec_->value(lab->id)), row_out, rows, v, v);
+    hk::held_out_sum(stream_, row_out, static_cast<const float*>(fwd_exec_->value(w->id)), rows, state);
+  }
+  sync();
+  hk::HeldOutState got{};
+  hip_check(hipMemcpy(&got, state, sizeof(got), hipMemcpyDeviceToHost), "hipMemcpy (held-out state)");
+  return {got.numerator, uint64_t(got.correct)};
 }
 
 std::vector<float> Session::losses() {

@@ -66,6 +66,11 @@ class Session : public Engine {
   std::vector<float> predict(const std::vector<std::vector<float>>& values, const Batch& batch) override;
   void train_step(const StepInputs& in) override;
   float final_loss(const Batch& batch) override;
+  // The forward program over every held-out batch, each batch's logits reduced on the device to
+  // the row losses and hits (held_out_rows) and added into one f64 sum and one count
+  // (held_out_sum); one host wait at the end (vulkan/stepwise.rs:1635-1760 does the same with its
+  // HeldOutRows / HeldOutSum modules).
+  HeldOutSums held_out(const HeldOut& h) override;
   std::vector<float> losses() override;
 
   // Runs the step plan eagerly (no graph) with one event pair around every launch; returns the
@@ -102,6 +107,8 @@ class Session : public Engine {
   uint32_t* counter_ = nullptr;
   uint32_t loss_capacity_ = 1u << 20;
   void* state_mem_ = nullptr;
+  void* eval_mem_ = nullptr;     // held-out row results [rows, 2] and the HeldOutState behind them
+  int64_t eval_rows_ = 0;
 
   std::unique_ptr<Executor> step_exec_, fwd_exec_;
   hipGraph_t graph_ = nullptr;

@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <memory>
 
 namespace msx {
 
@@ -149,6 +150,73 @@ void masked_gather(const std::vector<int32_t>& labels, const std::vector<float>&
   out_weights.resize(capacity, 0.0f);
 }
 
+HeldOut::HeldOut(const Compiled& c, const Feed& feed, uint64_t batches)
+    : labels_(c.config.labels), weights_(c.config.weights) {
+  if (batches == 0) throw IrError("held-out evaluation needs at least one batch");
+  check_program(c.forward, c.prediction);
+  batches_.reserve(size_t(batches));
+  for (uint64_t b = 0; b < batches; ++b) batches_.push_back(feed.held_out(b));
+}
+
+HeldOut::HeldOut(const Program& forward, uint32_t prediction, std::string labels, std::string weights,
+                 std::vector<Batch> batches)
+    : batches_(std::move(batches)), labels_(std::move(labels)), weights_(std::move(weights)) {
+  if (batches_.empty()) throw IrError("held-out evaluation needs at least one batch");
+  check_program(forward, prediction);
+  const int64_t rows = forward.input(labels_)->ty.count();
+  for (size_t b = 0; b < batches_.size(); ++b) {
+    auto l = batches_[b].i32.find(labels_);
+    auto w = batches_[b].f32.find(weights_);
+    if (l == batches_[b].i32.end() || w == batches_[b].f32.end() || int64_t(l->second.size()) != rows ||
+        int64_t(w->second.size()) != rows)
+      throw IrError("held-out batch " + std::to_string(b) + " lacks " + std::to_string(rows) + " labels `" + labels_ +
+                    "` and weights `" + weights_ + "`");
+  }
+}
+
+void HeldOut::check_program(const Program& forward, uint32_t prediction) {
+  const Node& pred = forward.node(prediction);
+  const Node* lab = forward.input(labels_);
+  const Node* w = forward.input(weights_);
+  if (labels_.empty() || weights_.empty() || !lab || !w || lab->ty.dtype != DType::I32 || w->ty.dtype != DType::F32)
+    throw IrError("held-out evaluation reads the i32 labels and f32 weights of a cross-entropy loss");
+  const int64_t rows = lab->ty.count();
+  if (pred.ty.dtype != DType::F32 || pred.ty.rank() != 2 || pred.ty.shape[0] != rows || pred.ty.shape[1] <= 0 ||
+      w->ty.count() != rows)
+    throw IrError("held-out evaluation reads the prediction as f32 logits [" + std::to_string(rows) +
+                  ", V], one row per position of the batch; the prediction is " + type_string(pred.ty));
+  classes_ = pred.ty.shape[1];
+}
+
+void HeldOut::check_labels() const {
+  for (size_t b = 0; b < batches_.size(); ++b) {
+    const auto& labels = batches_[b].i32.at(labels_);
+    for (size_t n = 0; n < labels.size(); ++n)
+      if (labels[n] < 0 || labels[n] >= classes_)
+        throw HeldOutLabelError("held-out batch " + std::to_string(b) + ", row " + std::to_string(n) + ": label " +
+                                std::to_string(labels[n]) + " is not below the " + std::to_string(classes_) +
+                                " classes");
+  }
+}
+
+HeldOutMetrics HeldOut::metrics_of_sums(const HeldOutSums& sums) const {
+  check_labels();
+  // eval.rs:430-449: the denominator summed from its first term in batch and row order.
+  double den = 0;
+  bool first = true;
+  uint64_t selected = 0;
+  for (auto& b : batches_)
+    for (float w : b.f32.at(weights_)) {
+      den = first ? double(w) : den + double(w);
+      first = false;
+      if (w > 0.0f) ++selected;
+    }
+  HeldOutMetrics m;
+  m.loss = den == 0.0 ? 0.0f : float(sums.numerator / den);
+  m.accuracy = selected == 0 ? 0.0f : float(sums.correct) / float(selected);
+  return m;
+}
+
 StepInputs step_inputs(const Compiled& c, const Feed& feed, uint64_t step, uint64_t end) {
   StepInputs in;
   in.batch = feed.batch(step);
@@ -176,7 +244,7 @@ StepInputs step_inputs(const Compiled& c, const Feed& feed, uint64_t step, uint6
   return in;
 }
 
-RunResult run(const Compiled& c, Engine& engine, uint64_t steps) {
+RunResult run(const Compiled& c, Engine& engine, uint64_t steps, uint64_t eval_every, uint64_t eval_batches) {
   RunResult out;
   const uint64_t end = steps;
   if (c.step.rule == Rule::AdamW && steps > 0 && c.step.adamw.warmup_steps >= end)
@@ -188,12 +256,27 @@ RunResult run(const Compiled& c, Engine& engine, uint64_t steps) {
     auto teacher = initialize(c.forward, c.config.seed, Stream::Teacher);
     feed.set_target(engine.predict(teacher, feed.batch(0)));
   }
+  // Drawn once, before the first step, so a split the evaluation refuses stops the run first.
+  std::unique_ptr<HeldOut> held_out;
+  if (eval_every) {
+    held_out = std::make_unique<HeldOut>(c, feed, eval_batches);
+    held_out->check_labels();
+  }
+  auto evaluate = [&](uint64_t step) {
+    auto e0 = std::chrono::steady_clock::now();
+    out.evals.emplace_back(step, held_out->metrics_of_sums(engine.held_out(*held_out)));
+    out.eval_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - e0).count();
+  };
   engine.set_params(out.initial);
   auto t0 = std::chrono::steady_clock::now();
-  for (uint64_t step = 0; step < end; ++step) engine.train_step(step_inputs(c, feed, step, end));
+  for (uint64_t step = 0; step < end; ++step) {
+    if (held_out && step % eval_every == 0) evaluate(step);
+    engine.train_step(step_inputs(c, feed, step, end));
+  }
   out.losses = engine.losses();
   auto t1 = std::chrono::steady_clock::now();
-  out.train_seconds = std::chrono::duration<double>(t1 - t0).count();
+  out.train_seconds = std::chrono::duration<double>(t1 - t0).count() - out.eval_seconds;
+  if (held_out) evaluate(end);
   Batch last = feed.batch(end);
   if (const Node* rows = c.step.program.input(kMaskedRowsInput)) {
     std::vector<int32_t> r, l;

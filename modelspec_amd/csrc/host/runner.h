@@ -30,6 +30,9 @@ class Feed {
   explicit Feed(const Compiled& c);
   // The batch of step `step` (Teacher and Classifier data are the same every step).
   Batch batch(uint64_t step) const;
+  // Batch `b` of the held-out split: the batch drawn at step id 2^63 + b, the id the reference
+  // gives the masking of held-out batch b (train/eval.rs:6-10), so no training step draws it.
+  Batch held_out(uint64_t b) const { return batch((uint64_t(1) << 63) + b); }
   // Teacher data: the input tensor and the (zero) target before set_target.
   void set_target(std::vector<float> y) { target_ = std::move(y); }
   bool needs_teacher() const { return cfg_.feed == FeedKind::Teacher; }
@@ -49,6 +52,56 @@ class Feed {
 void masked_gather(const std::vector<int32_t>& labels, const std::vector<float>& weights, uint64_t capacity,
                    uint64_t step, std::vector<int32_t>& rows, std::vector<int32_t>& out_labels,
                    std::vector<float>& out_weights);
+
+// Held-out evaluation (crates/modelspec-runtime/src/train/eval.rs): the forward program, the one
+// without dropout, over every held-out batch; the loss is sum(w_n nll_n) / sum(w_n) over every row
+// of every batch, both sums in f64, rounded to f32 once (0 when the weight sum is 0); the
+// accuracy is correct / selected over the rows of positive weight, a row correct when the first
+// largest logit of its row (lowest id among ties) is its label and the row holds no NaN.
+struct HeldOutMetrics {
+  float loss = 0, accuracy = 0;
+};
+
+// What a device reduces the logits of an evaluation to (eval.rs:299-339, metrics_of_sums): the
+// weighted sum of the row losses and the count of correct rows of positive weight.
+struct HeldOutSums {
+  double numerator = 0;
+  uint64_t correct = 0;
+};
+
+// The held-out batches of a run, drawn once (HeldOut::new, eval.rs:166-198): their labels and
+// weights are what the reduction reads, by the config's input names.
+class HeldOut {
+ public:
+  // Draws `batches` held-out batches of `feed`; the prediction must be f32 logits [rows, V] with
+  // one row per label of a batch (eval.rs:148-163), else an IrError.
+  HeldOut(const Compiled& c, const Feed& feed, uint64_t batches);
+  // Batches the caller drew (HeldOut::batch hands the reference's own to a device, eval.rs:290),
+  // with the labels and weights under the given input names of `forward`.
+  HeldOut(const Program& forward, uint32_t prediction, std::string labels, std::string weights,
+          std::vector<Batch> batches);
+  const std::vector<Batch>& batches() const { return batches_; }
+  const std::string& labels_name() const { return labels_; }
+  const std::string& weights_name() const { return weights_; }
+  int64_t classes() const { return classes_; }
+  // The metrics of sums reduced elsewhere (eval.rs:299-339): the denominator and the selected
+  // rows from the batches' own weights; a label outside [0, classes) is refused, the first in
+  // batch and row order (DataError naming the batch and row).
+  HeldOutMetrics metrics_of_sums(const HeldOutSums& sums) const;
+  // The same label check alone, before any batch runs.
+  void check_labels() const;
+
+ private:
+  std::vector<Batch> batches_;
+  std::string labels_, weights_;
+  int64_t classes_ = 0;
+  void check_program(const Program& forward, uint32_t prediction);
+};
+
+// A held-out label outside the classes (EvalError::Label, eval.rs:84-91).
+struct HeldOutLabelError : IrError {
+  using IrError::IrError;
+};
 
 // Everything one training step reads besides parameters and moments.
 struct StepInputs {
@@ -76,6 +129,8 @@ class Engine {
   virtual float final_loss(const Batch& batch) = 0;
   // The losses of the train steps run since set_params, in order.
   virtual std::vector<float> losses() = 0;
+  // The held-out sums of the forward program on the current parameters, after every queued step.
+  virtual HeldOutSums held_out(const HeldOut& h) = 0;
 };
 
 struct RunResult {
@@ -84,8 +139,13 @@ struct RunResult {
   std::vector<std::vector<float>> params;
   double train_seconds = 0;   // wall clock of the step loop (runner.rs loop; train.rs:17-31 --clock)
   int64_t nonfinite_step = -1;
+  // Held-out metrics at every step k with k % eval_every == 0 and at the last step, on the
+  // parameters after k updates (crates/modelspec-cli/src/train.rs:1293-1312).
+  std::vector<std::pair<uint64_t, HeldOutMetrics>> evals;
+  double eval_seconds = 0;    // wall clock of the evaluations, outside train_seconds
 };
 
-RunResult run(const Compiled& c, Engine& engine, uint64_t steps);
+// eval_every = 0: no evaluation; else `eval_batches` held-out batches (at least 1).
+RunResult run(const Compiled& c, Engine& engine, uint64_t steps, uint64_t eval_every = 0, uint64_t eval_batches = 0);
 
 }  // namespace msx

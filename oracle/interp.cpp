@@ -516,4 +516,39 @@ void Interpreter::eval(size_t at, const std::map<std::string, std::vector<float>
   fail(std::string("the oracle has no rule for ") + msx::op_name(n.op));
 }
 
+float row_nll(const float* row, size_t v, size_t label) {
+  float max, total;
+  row_softmax(row, v, max, total);
+  return max + std::log(total) - row[label];
+}
+
+int64_t first_argmax(const float* row, size_t v) {
+  for (size_t c = 0; c < v; ++c)
+    if (std::isnan(row[c])) return -1;
+  size_t best = 0;
+  for (size_t c = 1; c < v; ++c)
+    if (row[c] > row[best]) best = c;
+  return int64_t(best);
+}
+
+bool HeldOutTally::add(const float* logits, const int32_t* labels, const float* weights, size_t rows, size_t v) {
+  for (size_t n = 0; n < rows; ++n)
+    if (labels[n] < 0 || size_t(labels[n]) >= v) return false;
+  for (size_t n = 0; n < rows; ++n) {
+    const float* row = logits + n * v;
+    const double wide = double(weights[n]), nll = double(row_nll(row, v, size_t(labels[n])));
+    numerator = started ? std::fma(wide, nll, numerator) : wide * nll;
+    denominator = started ? denominator + wide : wide;
+    started = true;
+    if (weights[n] > 0.0f) {
+      ++selected;
+      if (first_argmax(row, v) == int64_t(labels[n])) ++correct;
+    }
+  }
+  return true;
+}
+
+float HeldOutTally::loss() const { return denominator == 0.0 ? 0.0f : float(numerator / denominator); }
+float HeldOutTally::accuracy() const { return selected == 0 ? 0.0f : float(correct) / float(selected); }
+
 }  // namespace oracle

@@ -41,4 +41,23 @@ class Interpreter {
   const Tensor& arg(size_t at, size_t k) const;
 };
 
+// The held-out tally of crates/modelspec-runtime/src/train/eval.rs:520-575 (Tally::add and
+// Tally::metrics), every row's nll computed (the reference skips rows of weight +0 whose nll is
+// finite, which adds +0 to each sum and leaves its bits unchanged, eval.rs:531-537).
+struct HeldOutTally {
+  bool started = false;           // a first term was added (the sums are Options in eval.rs)
+  double numerator = 0, denominator = 0;
+  uint64_t correct = 0, selected = 0;
+  // Adds `rows` rows of `v` logits; false (and nothing added) when a label is outside [0, v).
+  bool add(const float* logits, const int32_t* labels, const float* weights, size_t rows, size_t v);
+  float loss() const;
+  float accuracy() const;
+};
+
+// max + ln(sum exp(x - max)) - row[label], the sum from its first term in ascending order
+// (eval.rs:593-601).
+float row_nll(const float* row, size_t v, size_t label);
+// The first largest logit, lowest id among ties; -1 when the row holds a NaN (runner.rs:633-638).
+int64_t first_argmax(const float* row, size_t v);
+
 }  // namespace oracle

@@ -63,6 +63,26 @@ class OracleEngine : public msx::Engine {
     return it.value(c_.forward.outputs[0])[0];
   }
   std::vector<float> losses() override { return losses_; }
+  msx::HeldOutSums held_out(const msx::HeldOut& h) override {
+    tally = tally_of(h, params_);
+    return {tally.numerator, tally.correct};
+  }
+  // The forward program over every held-out batch on `values`, tallied (eval.rs:263-287).
+  oracle::HeldOutTally tally_of(const msx::HeldOut& h, const std::vector<std::vector<float>>& values) const {
+    oracle::HeldOutTally t;
+    size_t b = 0;
+    for (auto& batch : h.batches()) {
+      oracle::Interpreter it(c_.forward, true, c_.config.seed);
+      it.run(batch.f32, batch.i32, values);
+      const auto& labels = batch.i32.at(h.labels_name());
+      if (!t.add(it.value(c_.prediction).data(), labels.data(), batch.f32.at(h.weights_name()).data(), labels.size(),
+                 size_t(h.classes())))
+        throw msx::HeldOutLabelError("held-out batch " + std::to_string(b) + ": a label is not below the classes");
+      ++b;
+    }
+    return t;
+  }
+  oracle::HeldOutTally tally;  // of the last held_out call
 
  private:
   const msx::Compiled& c_;
@@ -182,6 +202,68 @@ int orc_train(const char* config, int64_t steps, int64_t masked_rows, float* los
     g_error = ex.what();
     return -1;
   }
+}
+
+// A run of `config` with a held-out evaluation every `eval_every` steps over `eval_batches`
+// batches: writes the evaluated steps and, per evaluation, [loss, accuracy] as the host finishes
+// them from the sums (eval.rs:299-339) and [loss, accuracy] of the oracle's own tally
+// (eval.rs:520-575) into metrics[4 * k ..]. Returns the number of evaluations, or -1.
+int orc_train_eval(const char* config, int64_t steps, uint64_t eval_every, uint64_t eval_batches, uint64_t* eval_steps,
+                   float* metrics, uint64_t evals_len) {
+  try {
+    msx::Compiled c = msx::compile_config(config, -1, steps);
+    OracleEngine e(c);
+    struct Both : msx::Engine {
+      OracleEngine& e;
+      std::vector<std::pair<float, float>> own;
+      explicit Both(OracleEngine& x) : e(x) {}
+      void set_params(const std::vector<std::vector<float>>& v) override { e.set_params(v); }
+      std::vector<std::vector<float>> params() override { return e.params(); }
+      std::vector<std::vector<float>> moments(char w) override { return e.moments(w); }
+      std::vector<float> predict(const std::vector<std::vector<float>>& v, const msx::Batch& b) override { return e.predict(v, b); }
+      void train_step(const msx::StepInputs& in) override { e.train_step(in); }
+      float final_loss(const msx::Batch& b) override { return e.final_loss(b); }
+      std::vector<float> losses() override { return e.losses(); }
+      msx::HeldOutSums held_out(const msx::HeldOut& h) override {
+        msx::HeldOutSums s = e.held_out(h);
+        own.emplace_back(e.tally.loss(), e.tally.accuracy());
+        return s;
+      }
+    } both(e);
+    msx::RunResult r = msx::run(c, both, c.config.steps, eval_every, eval_batches);
+    if (r.evals.size() > evals_len) { g_error = "evals buffer too small"; return -1; }
+    for (size_t k = 0; k < r.evals.size(); ++k) {
+      eval_steps[k] = r.evals[k].first;
+      metrics[4 * k] = r.evals[k].second.loss;
+      metrics[4 * k + 1] = r.evals[k].second.accuracy;
+      metrics[4 * k + 2] = both.own[k].first;
+      metrics[4 * k + 3] = both.own[k].second;
+    }
+    return int(r.evals.size());
+  } catch (const std::exception& ex) {
+    g_error = ex.what();
+    return -1;
+  }
+}
+
+// The held-out tally over explicit logits (eval.rs Tally): `batches` batches of `rows` rows of `v`
+// logits each; out = [loss, accuracy, numerator, denominator, correct, selected]. Returns 0, or
+// -1 for a label outside the classes.
+int orc_held_out_tally(const float* logits, const int32_t* labels, const float* weights, uint64_t batches,
+                       uint64_t rows, uint64_t v, double out[6]) {
+  oracle::HeldOutTally t;
+  for (uint64_t b = 0; b < batches; ++b)
+    if (!t.add(logits + b * rows * v, labels + b * rows, weights + b * rows, rows, v)) {
+      g_error = "label outside the classes";
+      return -1;
+    }
+  out[0] = t.loss();
+  out[1] = t.accuracy();
+  out[2] = t.numerator;
+  out[3] = t.denominator;
+  out[4] = double(t.correct);
+  out[5] = double(t.selected);
+  return 0;
 }
 
 // Times `steps` training steps of `config` on this thread; writes seconds per step.

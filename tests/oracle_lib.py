@@ -39,6 +39,8 @@ class Oracle:
                                       ctypes.POINTER(u64)]
         L.orc_free.argtypes = [vp]
         L.orc_init_params.argtypes = [ctypes.c_char_p, vp, u64]
+        L.orc_train_eval.argtypes = [ctypes.c_char_p, i64, u64, u64, vp, vp, u64]
+        L.orc_held_out_tally.argtypes = [vp, vp, vp, u64, u64, u64, vp]
         self.L = L
 
     def err(self):
@@ -57,6 +59,30 @@ class Oracle:
         if rc != 0:
             raise RuntimeError(self.err())
         return losses, params, secs.value
+
+    def train_eval(self, config, steps, eval_every, eval_batches):
+        """[(step, host-finished (loss, accuracy), the oracle tally's own (loss, accuracy))]."""
+        cap = steps // eval_every + 2
+        at = np.zeros(cap, np.uint64)
+        m = np.zeros(4 * cap, np.float32)
+        n = self.L.orc_train_eval(config.encode(), steps, eval_every, eval_batches, at.ctypes.data, m.ctypes.data, cap)
+        if n < 0:
+            raise RuntimeError(self.err())
+        return [(int(at[k]), (m[4 * k], m[4 * k + 1]), (m[4 * k + 2], m[4 * k + 3])) for k in range(n)]
+
+    def held_out_tally(self, logits, labels, weights):
+        """logits [batches, rows, v] f32, labels [batches, rows] i32, weights [batches, rows] f32 ->
+        dict(loss, accuracy, numerator, denominator, correct, selected), the eval.rs tally."""
+        logits = np.ascontiguousarray(logits, np.float32)
+        labels = np.ascontiguousarray(labels, np.int32)
+        weights = np.ascontiguousarray(weights, np.float32)
+        b, r, v = logits.shape
+        out = np.zeros(6, np.float64)
+        if self.L.orc_held_out_tally(logits.ctypes.data, labels.ctypes.data, weights.ctypes.data, b, r, v,
+                                     out.ctypes.data) != 0:
+            raise ValueError(self.err())
+        keys = ("loss", "accuracy", "numerator", "denominator", "correct", "selected")
+        return {k: (np.float32(x) if k in ("loss", "accuracy") else x) for k, x in zip(keys, out)}
 
     def seconds_per_step(self, config, steps, masked_rows=-1):
         s = ctypes.c_double()
