@@ -959,6 +959,10 @@ void Executor::build() {
               hk::ce_rows(s, F(lg), I(lab), F(w), with_grad ? F(gsc) : nullptr, static_cast<float*>(A(st2)),
                           rl ? static_cast<float*>(A(rl)) : nullptr, gout >= 0 ? F(uint32_t(gout)) : nullptr, rows, v, ld);
             });
+            // The row pass reads the logits, labels and weights and writes the gradient and the
+            // row statistics; the loss launch behind it reads the row terms and weights.
+            pending.back().bytes = 4.0 * double(rows * v * (with_grad ? 2 : 1) + rows * (2 + 2 + (with_loss ? 1 : 0)));
+            const size_t rows_launch = pending.size() - 1;
             if (with_loss) {
               auto dkey = std::make_pair(lg, w);
               if (!ce_den_tok.count(dkey)) ce_den_tok[dkey] = R(4);
@@ -968,6 +972,9 @@ void Executor::build() {
                 hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(st2)), F(lid), static_cast<float*>(A(den)), rows,
                             v, ld, static_cast<float*>(A(rl)));
               });
+              bytes = 4.0 * double(2 * rows + 2);
+            } else {
+              bytes = pending[rows_launch].bytes;
             }
             grp.done = true;
             grp.grad_done = grp.grad_done || with_grad;

@@ -95,6 +95,9 @@ def test_non_finite_logits_poison_the_loss_as_in_the_tally(ctx, oracle):
         want = oracle.held_out_tally(bad, labels, w)
         assert np.isnan(got["loss"]) and np.isnan(want["loss"]), case
         assert got["correct"] == want["correct"], case
+    # Nothing selected: 0 and 0, not NaN (tests/adversary_heldout.rs:1-6).
+    got = ctx.evaluate(batches_of(logits, labels, np.zeros_like(weights)), "labels", "weights")
+    assert got["loss"] == 0.0 and got["accuracy"] == 0.0 and got["selected"] == 0
     every = np.full((1, rows, v), -np.inf, np.float32)
     got = ctx.evaluate(batches_of(every, labels, weights), "labels", "weights")
     assert np.isnan(got["loss"]) and np.isnan(oracle.held_out_tally(every, labels, weights)["loss"])
