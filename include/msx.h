@@ -89,6 +89,12 @@ int msx_forward(msx_ctx* ctx, const msx_tensor* inputs, uint32_t n_inputs, float
 
 int msx_stats(msx_ctx* ctx, msx_run_stats* out);
 
+/* The device copy of input `name` of the step program (program 0) or the forward program (1) as
+ * the last step or forward pass read it: what the host staged, or what the device drew from a
+ * packed corpus. `count` elements of 4 bytes. For tests and inspection; no counterpart in the
+ * reference, whose host builds every input itself. */
+int msx_read_input(msx_ctx* ctx, int32_t program, const char* name, void* out, uint64_t count);
+
 /* Held-out metrics (crates/modelspec-runtime/src/train/eval.rs:27-39, HeldOutMetrics at :94-98):
  * loss = sum(w nll) / sum(w) over every row of every batch (f64 sums, rounded to f32 once, 0 when
  * the weight sum is 0); accuracy = correct / selected over the rows of positive weight. The
@@ -127,6 +133,38 @@ int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t ma
 int msx_train_config_eval(msx_ctx* ctx, const char* config, int64_t steps, uint64_t eval_every, uint64_t eval_batches,
                           float* losses, uint64_t losses_len, uint64_t* eval_steps, msx_heldout* evals,
                           uint64_t evals_len, uint64_t* n_evals, double* train_seconds, double* eval_seconds);
+
+/* Reads a packed masked-language-model directory (binding.json, packed.json, train.tokens,
+ * heldout.tokens; crates/modelspec-runtime/src/dataset/mlm.rs:588-662, checks of
+ * train/data.rs:1448-1640) into the context; the next msx_load binds it to the forward program's
+ * batch tensors (ids, positions, key_mask, labels, weights; E-DATA-005/006 when they do not fit)
+ * and keeps both splits in device memory. Every batch is then drawn on the device: a step's
+ * inputs name `data.step` (i32 [low, high] of the step) in place of the batch and the masked-row
+ * gather, and the library draws the step's sequences (epoch order, Philox tag 5), masks them
+ * 80/10/10 (tag 3) and gathers the selected rows on the device (mlm_batch, mlm.rs:717-788;
+ * train/masked.rs:58-118). msx_evaluate with n = 0 evaluates every whole batch of the HeldOut
+ * split. A refused directory is MSX_E_DATA naming the file; a step that selects more rows than
+ * the gather holds is MSX_E_DATA (E-DATA-012) at the next call that waits on the device.
+ * dir = NULL unbinds the corpus: the next msx_load takes its batches from the host again. */
+int msx_load_packed(msx_ctx* ctx, const char* dir);
+
+/* Writes a packed directory of the given ids, whole sequences of seq_len, with the BERT masking
+ * policy (its selection rate replaced by `selection_rate`; BERT's is 0.15) and the records pack()
+ * writes (mlm.rs:395-535) for the dataset and tokenizer UUIDs given. No device is needed. */
+int msx_write_packed(const char* dir, const int32_t* train, uint64_t train_count, const int32_t* heldout,
+                     uint64_t heldout_count, uint64_t seq_len, uint64_t vocabulary_size, const char* dataset_id,
+                     const char* tokenizer_id, double selection_rate);
+
+/* A run of a built-in config on the packed directory `dir` (msx_load_packed): `steps` steps
+ * (negative: the config's own), a held-out evaluation every `eval_every` steps (0: none) over
+ * `eval_batches` batches (0: the whole HeldOut split). Writes steps + 1 losses, the final
+ * parameters in ParamId order (params may be null), and the evaluations as
+ * msx_train_config_eval does. Replaces `train --data <dir> --eval-every n`
+ * (crates/modelspec-cli/src/train.rs:1084-1312). */
+int msx_train_packed(msx_ctx* ctx, const char* config, const char* dir, int64_t steps, uint64_t eval_every,
+                     uint64_t eval_batches, float* losses, uint64_t losses_len, float* params, uint64_t params_len,
+                     uint64_t* eval_steps, msx_heldout* evals, uint64_t evals_len, uint64_t* n_evals,
+                     double* train_seconds, double* eval_seconds);
 
 /* Times `steps` graph-launched training steps of a built-in config after `warmup` (HIP events on
  * the run's stream after every step into step_ms[steps], may be null; host inputs made before the

@@ -69,6 +69,13 @@ def lib():
         L.msx_train_config_eval.argtypes = [vp, ctypes.c_char_p, c64, u64, u64, vp, u64, vp,
                                             ctypes.POINTER(HeldOutMetrics), u64, ctypes.POINTER(u64),
                                             ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
+        L.msx_load_packed.argtypes = [vp, ctypes.c_char_p]
+        L.msx_write_packed.argtypes = [ctypes.c_char_p, vp, u64, vp, u64, u64, u64, ctypes.c_char_p, ctypes.c_char_p,
+                                       ctypes.c_double]
+        L.msx_train_packed.argtypes = [vp, ctypes.c_char_p, ctypes.c_char_p, c64, u64, u64, vp, u64, vp, u64, vp,
+                                       ctypes.POINTER(HeldOutMetrics), u64, ctypes.POINTER(u64),
+                                       ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
+        L.msx_read_input.argtypes = [vp, i32, ctypes.c_char_p, vp, u64]
         L.msx_prog_new.argtypes = [vp, ctypes.c_char_p, u64, ctypes.POINTER(vp)]
         L.msx_prog_run.argtypes = [vp, ctypes.POINTER(Tensor), u32, ctypes.POINTER(vp), ctypes.POINTER(u64), u32]
         L.msx_prog_output.argtypes = [vp, u32, vp, u64]
@@ -229,6 +236,30 @@ class Context:
                                            ctypes.byref(es)))
         return losses, [(int(at[k]), evals[k].as_dict()) for k in range(n.value)], ts.value, es.value
 
+    def load_packed(self, path):
+        """Binds a packed directory to the next load; None unbinds it."""
+        _check(lib().msx_load_packed(self._h, None if path is None else str(path).encode()))
+
+    def read_input(self, program, name, count, dtype=np.int32):
+        """The device copy of an input of the step (program 0) or forward (1) program."""
+        out = np.zeros(count, dtype)
+        _check(lib().msx_read_input(self._h, program, name.encode(), out.ctypes.data, count))
+        return out
+
+    def train_packed(self, name, path, steps, eval_every=0, eval_batches=0):
+        """A run of a built-in config on a packed directory: (losses, flat params, [(step, metrics)])."""
+        step_ir, _ = compile_config(name, -1, steps)
+        losses = np.zeros(steps + 1, np.float32)
+        params = np.zeros(param_count(step_ir), np.float32)
+        cap = (steps // eval_every + 2) if eval_every else 1
+        at = np.zeros(cap, np.uint64)
+        evals = (HeldOutMetrics * cap)()
+        n, ts, es = ctypes.c_uint64(), ctypes.c_double(), ctypes.c_double()
+        _check(lib().msx_train_packed(self._h, name.encode(), str(path).encode(), steps, eval_every, eval_batches,
+                                      losses.ctypes.data, losses.size, params.ctypes.data, params.size, at.ctypes.data,
+                                      evals, cap, ctypes.byref(n), ctypes.byref(ts), ctypes.byref(es)))
+        return losses, params, [(int(at[k]), evals[k].as_dict()) for k in range(n.value)]
+
     def stats(self):
         s = RunStats()
         _check(lib().msx_stats(self._h, ctypes.byref(s)))
@@ -249,6 +280,19 @@ class Context:
 
     def program(self, text, seed=0):
         return Program(self, text, seed)
+
+
+DATASET_ID = "0c5a3f9e-2b71-8d40-9e6a-51f2c7d8a903"
+TOKENIZER_ID = "7e19b4c2-a5d3-8f60-8b21-c4e7d9a0f518"
+
+
+def write_packed(path, train, heldout, seq_len, vocabulary_size, dataset_id=DATASET_ID, tokenizer_id=TOKENIZER_ID,
+                 selection_rate=0.15):
+    """Writes a packed directory of the given ids (whole sequences of seq_len each); no device."""
+    tr = np.ascontiguousarray(train, np.int32)
+    ho = np.ascontiguousarray(heldout, np.int32)
+    _check(lib().msx_write_packed(str(path).encode(), tr.ctypes.data, tr.size, ho.ctypes.data, ho.size, seq_len,
+                                  vocabulary_size, dataset_id.encode(), tokenizer_id.encode(), selection_rate))
 
 
 def param_shapes(step_ir):

@@ -18,10 +18,13 @@ SOURCES = [
     "host/rng.cpp",
     "host/models.cpp",
     "host/runner.cpp",
+    "host/json.cpp",
+    "host/packed.cpp",
     "hip/runtime.cpp",
     "hip/kernels.hip",
     "hip/gemm.hip",
     "hip/attention.hip",
+    "hip/data.hip",
 ]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -6,6 +6,7 @@
 #include "../../include/msx.h"
 #include "hip/runtime.h"
 #include "host/models.h"
+#include "host/packed.h"
 #include "host/runner.h"
 
 namespace {
@@ -25,6 +26,8 @@ int guarded(F&& f) {
   } catch (const msx::HipError& e) {
     return fail(MSX_E_DEVICE, e.what());
   } catch (const msx::HeldOutLabelError& e) {
+    return fail(MSX_E_DATA, e.what());
+  } catch (const msx::PackedError& e) {
     return fail(MSX_E_DATA, e.what());
   } catch (const msx::IrError& e) {
     std::string w = e.what();
@@ -77,7 +80,26 @@ struct msx_ctx {
   msx::TrainingStep step;
   msx::Program forward;
   uint32_t prediction = 0;  // the forward program's prediction value
+  // A packed corpus msx_load_packed read; msx_load then draws every batch from it on the device.
+  std::unique_ptr<msx::PackedCorpus> corpus;
+  msx::EpochOrders orders;
+  uint64_t seed = 0;
 };
+
+namespace {
+// With a corpus loaded, a batch that names `data.step` (i32 [low, high] of the step) is the
+// corpus batch of that step: its sequences are drawn here and the device draws its rows.
+void corpus_draw(msx_ctx* ctx, msx::Batch& b, msx::SplitRole role) {
+  auto it = b.i32.find("data.step");
+  if (it == b.i32.end()) return;
+  if (!ctx->corpus || !ctx->session) throw msx::IrError("`data.step` names a corpus batch, and no corpus is loaded");
+  if (it->second.size() != 2) throw msx::IrError("`data.step` is i32 [low, high]");
+  const uint64_t step = uint64_t(uint32_t(it->second[0])) | (uint64_t(uint32_t(it->second[1])) << 32);
+  b.i32.erase(it);
+  b.i32[msx::kDrawInput] =
+      msx::draw_words(role, ctx->orders.draw(*ctx->corpus, role, ctx->seed, step, ctx->session->corpus_batch()));
+}
+}  // namespace
 
 struct msx_prog {
   std::unique_ptr<msx::Session> session;
@@ -141,8 +163,9 @@ int msx_load(msx_ctx* ctx, const char* step_ir, const char* forward_ir, uint64_t
     ctx->forward = msx::parse_program(forward_ir);
     if (prediction_output >= ctx->forward.outputs.size()) return fail(MSX_E_INVALID, "no such forward output");
     ctx->prediction = ctx->forward.outputs[prediction_output];
+    ctx->seed = seed;
     ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, seed,
-                                                  ctx->forward.outputs[prediction_output]);
+                                                  ctx->forward.outputs[prediction_output], ctx->corpus.get());
     return MSX_OK;
   });
 }
@@ -184,6 +207,7 @@ int msx_run_steps(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, con
     for (uint32_t i = 0; i < n; ++i) {
       msx::StepInputs in;
       in.batch = batch_of(inputs[i], n_inputs[i]);
+      corpus_draw(ctx, in.batch, msx::SplitRole::Train);
       ctx->session->train_step(in);
     }
     auto all = ctx->session->losses();
@@ -201,6 +225,7 @@ int msx_forward(msx_ctx* ctx, const msx_tensor* inputs, uint32_t n_inputs, float
   return guarded([&] {
     if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
     msx::Batch b = batch_of(inputs, n_inputs);
+    corpus_draw(ctx, b, msx::SplitRole::Train);
     float loss = ctx->session->final_loss(b);
     if (loss_out) *loss_out = loss;
     if (prediction_out) {
@@ -209,6 +234,21 @@ int msx_forward(msx_ctx* ctx, const msx_tensor* inputs, uint32_t n_inputs, float
       msx::hip_check(hipMemcpy(prediction_out, ctx->session->forward_value(pred), prediction_count * 4, hipMemcpyDeviceToHost),
                      "hipMemcpy (prediction)");
     }
+    return MSX_OK;
+  });
+}
+
+int msx_read_input(msx_ctx* ctx, int32_t program, const char* name, void* out, uint64_t count) {
+  return guarded([&] {
+    if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
+    if (!name || !out) return fail(MSX_E_INVALID, "null argument");
+    const msx::Program& p = program == 0 ? ctx->step.program : ctx->forward;
+    const msx::Node* in = p.input(name);
+    if (!in) return fail(MSX_E_INVALID, std::string("the program has no input `") + name + "`");
+    if (in->ty.count() != int64_t(count)) return fail(MSX_E_INVALID, std::string("input `") + name + "` count");
+    ctx->session->sync();
+    const void* src = program == 0 ? ctx->session->step_value(in->id) : ctx->session->forward_value(in->id);
+    msx::hip_check(hipMemcpy(out, src, count * 4, hipMemcpyDeviceToHost), "hipMemcpy (input)");
     return MSX_OK;
   });
 }
@@ -235,6 +275,13 @@ msx_heldout heldout_of(const msx::HeldOut& h, const msx::HeldOutSums& sums) {
   out.accuracy = m.accuracy;
   out.numerator = sums.numerator;
   out.correct = sums.correct;
+  bool host_weights = true;
+  for (auto& b : h.batches()) host_weights = host_weights && b.f32.count(h.weights_name());
+  if (!host_weights) {
+    out.denominator = sums.denominator;
+    out.selected = sums.selected;
+    return out;
+  }
   bool first = true;
   for (auto& b : h.batches())
     for (float w : b.f32.at(h.weights_name())) {
@@ -253,58 +300,128 @@ int msx_evaluate(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, cons
     if (!labels || !weights || !out || (n && (!inputs || !n_inputs))) return fail(MSX_E_INVALID, "null argument");
     std::vector<msx::Batch> batches;
     for (uint32_t i = 0; i < n; ++i) batches.push_back(batch_of(inputs[i], n_inputs[i]));
+    if (n == 0 && ctx->corpus) {
+      // Every whole batch of the corpus's HeldOut split, in stored order (eval.rs:6-12).
+      const uint64_t B = ctx->session->corpus_batch(), whole = ctx->corpus->sequences(msx::SplitRole::HeldOut) / B;
+      if (whole == 0) return fail(MSX_E_DATA, "the HeldOut split holds fewer sequences than one batch");
+      for (uint64_t b = 0; b < whole; ++b) {
+        msx::Batch x;
+        x.i32[msx::kDrawInput] =
+            msx::draw_words(msx::SplitRole::HeldOut, ctx->orders.draw(*ctx->corpus, msx::SplitRole::HeldOut, ctx->seed, b, B));
+        batches.push_back(std::move(x));
+      }
+    }
     msx::HeldOut h(ctx->forward, ctx->prediction, labels, weights, std::move(batches));
     *out = heldout_of(h, ctx->session->held_out(h));
     return MSX_OK;
   });
 }
 
+namespace {
+// One run of a built-in config, its batches synthetic or drawn from `corpus`, with a held-out
+// evaluation every `eval_every` steps (0: none).
+int train_run(msx_ctx* ctx, const char* config, int64_t steps, uint64_t eval_every, uint64_t eval_batches,
+              const msx::PackedCorpus* corpus, float* losses, uint64_t losses_len, float* params, uint64_t params_len,
+              uint64_t* eval_steps, msx_heldout* evals, uint64_t evals_len, uint64_t* n_evals, double* train_seconds,
+              double* eval_seconds) {
+  msx::Compiled c = msx::compile_config(config, -1, steps);
+  ctx->session.reset();
+  ctx->step = c.step;
+  ctx->forward = c.forward;
+  ctx->prediction = c.prediction;
+  ctx->seed = c.config.seed;
+  ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction, corpus);
+  // Each evaluation's metrics, finished with the host's weight sums as msx_evaluate does.
+  struct Recording : msx::Engine {
+    msx::Session& s;
+    std::vector<msx_heldout> metrics;
+    explicit Recording(msx::Session& x) : s(x) {}
+    void set_params(const std::vector<std::vector<float>>& v) override { s.set_params(v); }
+    std::vector<std::vector<float>> params() override { return s.params(); }
+    std::vector<std::vector<float>> moments(char w) override { return s.moments(w); }
+    std::vector<float> predict(const std::vector<std::vector<float>>& v, const msx::Batch& b) override { return s.predict(v, b); }
+    void train_step(const msx::StepInputs& in) override { s.train_step(in); }
+    float final_loss(const msx::Batch& b) override { return s.final_loss(b); }
+    std::vector<float> losses() override { return s.losses(); }
+    msx::HeldOutSums held_out(const msx::HeldOut& x) override {
+      msx::HeldOutSums sums = s.held_out(x);
+      metrics.push_back(heldout_of(x, sums));
+      return sums;
+    }
+  } rec(*ctx->session);
+  msx::RunResult r = msx::run(c, rec, c.config.steps, eval_every, eval_batches, corpus);
+  if (losses_len < r.losses.size()) return fail(MSX_E_INVALID, "losses buffer too small");
+  if (losses) std::memcpy(losses, r.losses.data(), r.losses.size() * 4);
+  if (params) {
+    uint64_t off = 0;
+    for (auto& p : r.params) {
+      if (off + p.size() > params_len) return fail(MSX_E_INVALID, "params buffer too small");
+      std::memcpy(params + off, p.data(), p.size() * 4);
+      off += p.size();
+    }
+  }
+  if (r.evals.size() > evals_len) return fail(MSX_E_INVALID, "evals buffer too small");
+  for (size_t k = 0; k < r.evals.size(); ++k) {
+    if (eval_steps) eval_steps[k] = r.evals[k].first;
+    if (evals) evals[k] = rec.metrics[k];
+  }
+  if (n_evals) *n_evals = r.evals.size();
+  if (train_seconds) *train_seconds = r.train_seconds;
+  if (eval_seconds) *eval_seconds = r.eval_seconds;
+  if (r.nonfinite_step >= 0)
+    return fail(MSX_E_NONFINITE, "E-TRAIN-001: the loss of step " + std::to_string(r.nonfinite_step) + " is not finite");
+  return MSX_OK;
+}
+}  // namespace
+
 int msx_train_config_eval(msx_ctx* ctx, const char* config, int64_t steps, uint64_t eval_every, uint64_t eval_batches,
                           float* losses, uint64_t losses_len, uint64_t* eval_steps, msx_heldout* evals,
                           uint64_t evals_len, uint64_t* n_evals, double* train_seconds, double* eval_seconds) {
   return guarded([&] {
     if (eval_every == 0) return fail(MSX_E_INVALID, "eval_every takes a step count of at least 1, not 0");
-    msx::Compiled c = msx::compile_config(config, -1, steps);
+    return train_run(ctx, config, steps, eval_every, eval_batches, nullptr, losses, losses_len, nullptr, 0, eval_steps,
+                     evals, evals_len, n_evals, train_seconds, eval_seconds);
+  });
+}
+
+int msx_load_packed(msx_ctx* ctx, const char* dir) {
+  return guarded([&] {
     ctx->session.reset();
-    ctx->step = c.step;
-    ctx->forward = c.forward;
-    ctx->prediction = c.prediction;
-    ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction);
-    // Sums of each evaluation, finished with the host's weight sums as msx_evaluate does.
-    struct Recording : msx::Engine {
-      msx::Session& s;
-      std::vector<msx::HeldOutSums> sums;
-      const msx::HeldOut* h = nullptr;
-      explicit Recording(msx::Session& x) : s(x) {}
-      void set_params(const std::vector<std::vector<float>>& v) override { s.set_params(v); }
-      std::vector<std::vector<float>> params() override { return s.params(); }
-      std::vector<std::vector<float>> moments(char w) override { return s.moments(w); }
-      std::vector<float> predict(const std::vector<std::vector<float>>& v, const msx::Batch& b) override { return s.predict(v, b); }
-      void train_step(const msx::StepInputs& in) override { s.train_step(in); }
-      float final_loss(const msx::Batch& b) override { return s.final_loss(b); }
-      std::vector<float> losses() override { return s.losses(); }
-      msx::HeldOutSums held_out(const msx::HeldOut& x) override {
-        h = &x;
-        sums.push_back(s.held_out(x));
-        return sums.back();
-      }
-    } rec(*ctx->session);
-    msx::RunResult r = msx::run(c, rec, c.config.steps, eval_every, eval_batches);
-    if (losses_len < r.losses.size()) return fail(MSX_E_INVALID, "losses buffer too small");
-    if (losses) std::memcpy(losses, r.losses.data(), r.losses.size() * 4);
-    if (r.evals.size() > evals_len) return fail(MSX_E_INVALID, "evals buffer too small");
-    msx::Feed feed(c);
-    msx::HeldOut h(c, feed, eval_batches);
-    for (size_t k = 0; k < r.evals.size(); ++k) {
-      if (eval_steps) eval_steps[k] = r.evals[k].first;
-      if (evals) evals[k] = heldout_of(h, rec.sums[k]);
-    }
-    if (n_evals) *n_evals = r.evals.size();
-    if (train_seconds) *train_seconds = r.train_seconds;
-    if (eval_seconds) *eval_seconds = r.eval_seconds;
-    if (r.nonfinite_step >= 0)
-      return fail(MSX_E_NONFINITE, "E-TRAIN-001: the loss of step " + std::to_string(r.nonfinite_step) + " is not finite");
+    ctx->corpus.reset();
+    if (!dir) return MSX_OK;
+    ctx->corpus = std::make_unique<msx::PackedCorpus>(msx::load_packed(dir));
+    ctx->orders = msx::EpochOrders();
     return MSX_OK;
+  });
+}
+
+int msx_write_packed(const char* dir, const int32_t* train, uint64_t train_count, const int32_t* heldout,
+                     uint64_t heldout_count, uint64_t seq_len, uint64_t vocabulary_size, const char* dataset_id,
+                     const char* tokenizer_id, double selection_rate) {
+  return guarded([&] {
+    if (!dir || !train || !heldout || !dataset_id || !tokenizer_id) return fail(MSX_E_INVALID, "null argument");
+    msx::MaskingPolicy policy;
+    policy.selection_rate = selection_rate;
+    msx::write_packed(dir, std::vector<int32_t>(train, train + train_count),
+                      std::vector<int32_t>(heldout, heldout + heldout_count), seq_len, vocabulary_size, dataset_id,
+                      tokenizer_id, policy);
+    return MSX_OK;
+  });
+}
+
+int msx_train_packed(msx_ctx* ctx, const char* config, const char* dir, int64_t steps, uint64_t eval_every,
+                     uint64_t eval_batches, float* losses, uint64_t losses_len, float* params, uint64_t params_len,
+                     uint64_t* eval_steps, msx_heldout* evals, uint64_t evals_len, uint64_t* n_evals,
+                     double* train_seconds, double* eval_seconds) {
+  return guarded([&] {
+    if (!dir) return fail(MSX_E_INVALID, "null directory");
+    ctx->session.reset();
+    // The run's own corpus; the context's msx_load_packed binding is left as it was.
+    auto corpus = std::make_unique<msx::PackedCorpus>(msx::load_packed(dir));
+    const int rc = train_run(ctx, config, steps, eval_every, eval_batches, corpus.get(), losses, losses_len, params,
+                             params_len, eval_steps, evals, evals_len, n_evals, train_seconds, eval_seconds);
+    ctx->session.reset();  // its feed pointed at the run's corpus
+    return rc;
   });
 }
 

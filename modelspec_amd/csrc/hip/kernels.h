@@ -141,11 +141,37 @@ void ce_grad(hipStream_t s, const float* logits, const int32_t* labels, const fl
 // Held-out evaluation (train/eval.rs). held_out_rows: per row r of logits [rows, v] (row pitch
 // ld), out[2r] = max + ln(sum exp(x - max)) - x[label] and out[2r + 1] = 1 when the row holds no
 // NaN and its first largest logit (lowest id among ties) is its label, else 0. Labels must lie in
-// [0, v) (the host checks them). held_out_sum: adds sum_r w_r out[2r] in f64 and the count of rows
-// with w_r > 0 and a hit to `state` (HeldOutState), which the caller zeroes before the first batch.
+// [0, v) (the host checks them). held_out_sum: adds sum_r w_r out[2r] in f64, the count of rows
+// with w_r > 0 and a hit, the weight sum in f64 and the count of rows with w_r > 0 to `state`
+// (HeldOutState), which the caller zeroes before the first batch.
+// A packed corpus resident on the device and the masking constants of its binding: the split
+// ids (sequence after sequence), the sequence length, the run seed, the integer thresholds of the
+// masking policy and V - 5 random tokens.
+constexpr uint32_t kMlmSpecials = 5;
+constexpr int32_t kMlmMask = 4;
+struct MlmCorpus {
+  const int32_t* train;
+  const int32_t* heldout;
+  int64_t seq_len;
+  uint64_t seed;
+  uint64_t select, mask, mask_or_random;
+  uint64_t random_tokens;
+};
+// The batch of one step: `draw` is [split (0 Train, 1 HeldOut), draw id low, draw id high,
+// sequence 0, ..., sequence batch-1] on the device. Any output may be null.
+void mlm_rows(hipStream_t s, const MlmCorpus& c, const int32_t* draw, int64_t batch, int32_t* ids, int32_t* positions,
+              float* key_mask, int32_t* labels, float* weights);
+// The masked-row gather of `rows` rows into `capacity` slots; `error` (4 words, zeroed by the
+// owner) records the first batch that selects more rows than the capacity: [1, count, draw id
+// low, draw id high].
+void masked_gather(hipStream_t s, const int32_t* labels, const float* weights, int64_t rows, int64_t capacity,
+                   const int32_t* draw, int32_t* out_rows, int32_t* out_labels, float* out_weights, uint32_t* error);
+
 struct HeldOutState {
   double numerator;
   unsigned long long correct;
+  double denominator;            // sum of the weights
+  unsigned long long selected;   // rows of positive weight
 };
 void held_out_rows(hipStream_t s, const float* logits, const int32_t* labels, float* out, int64_t rows, int64_t v,
                    int64_t ld);

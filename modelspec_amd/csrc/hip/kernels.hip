@@ -954,32 +954,42 @@ void held_out_rows(hipStream_t s, const float* logits, const int32_t* labels, fl
 
 __global__ __launch_bounds__(1024) void k_held_out_sum(const float* __restrict__ rows_in, const float* __restrict__ w,
                                                        int64_t rows, HeldOutState* __restrict__ state) {
-  __shared__ double num_s[16];
-  __shared__ unsigned long long hit_s[16];
-  double num = 0.0;
-  unsigned long long hits = 0;
+  __shared__ double num_s[16], den_s[16];
+  __shared__ unsigned long long hit_s[16], sel_s[16];
+  double num = 0.0, den = 0.0;
+  unsigned long long hits = 0, sel = 0;
   for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) {
     const float wr = w[r];
     num = __builtin_fma(double(wr), double(rows_in[2 * r]), num);
+    den += double(wr);
     hits += (wr > 0.0f && rows_in[2 * r + 1] == 1.0f) ? 1 : 0;
+    sel += wr > 0.0f ? 1 : 0;
   }
   for (int o = 32; o > 0; o >>= 1) {
     num += __shfl_xor(num, o, 64);
+    den += __shfl_xor(den, o, 64);
     hits += __shfl_xor(hits, o, 64);
+    sel += __shfl_xor(sel, o, 64);
   }
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     num_s[wave] = num;
+    den_s[wave] = den;
     hit_s[wave] = hits;
+    sel_s[wave] = sel;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int k = 1; k < int(blockDim.x >> 6); ++k) {
       num += num_s[k];
+      den += den_s[k];
       hits += hit_s[k];
+      sel += sel_s[k];
     }
     state->numerator += num;
     state->correct += hits;
+    state->denominator += den;
+    state->selected += sel;
   }
 }
 void held_out_sum(hipStream_t s, const float* rows_in, const float* w, int64_t rows, HeldOutState* state) {

@@ -490,9 +490,7 @@ void Executor::build() {
           if (param == UINT32_MAX) throw IrError("moment input of an unknown parameter: " + x.name);
           fixed_[x.id] = (x.name[10] == 'm' ? s_.m_ : s_.v_) + s_.offset_[param];
         } else {
-          InputSlot slot{x.name, x.ty.dtype, x.ty.count(), input_bytes_, x.id};
-          input_bytes_ += (size_t(std::max<int64_t>(x.ty.count(), 1)) * 4 + 255) / 256 * 256;
-          inputs_.push_back(slot);
+          inputs_.push_back(InputSlot{x.name, x.ty.dtype, x.ty.count(), 0, x.id, s_.corpus_fed(p, x.name)});
         }
         break;
       case Op::ParamRead: fixed_[x.id] = s_.param_ + s_.offset_[x.param]; break;
@@ -524,6 +522,23 @@ void Executor::build() {
       }
     }
   }
+  // The input block: the corpus draw of the step first (when a packed corpus feeds the batch),
+  // then every input the host stages, then the inputs the device writes, so that one copy of the
+  // block's head carries a step's host inputs.
+  auto slot_bytes = [](int64_t count) { return (size_t(std::max<int64_t>(count, 1)) * 4 + 255) / 256 * 256; };
+  input_bytes_ = 0;
+  if (s_.corpus_) {
+    draw_offset_ = 0;
+    input_bytes_ += slot_bytes(3 + int64_t(s_.corpus_batch_));
+  }
+  for (int device_pass = 0; device_pass < 2; ++device_pass) {
+    for (auto& slot : inputs_)
+      if (slot.device == (device_pass == 1)) {
+        slot.offset = input_bytes_;
+        input_bytes_ += slot_bytes(slot.count);
+      }
+    if (device_pass == 0) host_bytes_ = input_bytes_;
+  }
   input_token_ = arena_.reserve(std::max<size_t>(input_bytes_, 256));
 
   // Workspaces, reserved per launch now; resolved after commit.
@@ -544,6 +559,59 @@ void Executor::build() {
   auto I = [this](uint32_t id) { return static_cast<int32_t*>(ptr(id)); };
   auto shape = [&](uint32_t v) -> const std::vector<int64_t>& { return p.node(v).ty.shape; };
   const uint64_t seed = s_.seed_;
+
+  // A packed corpus feeds the batch: the step's rows drawn and masked on the device, then the
+  // masked-row gather of the selected rows, ahead of everything that reads them.
+  if (s_.corpus_) {
+    // An input the plan keeps (one no launch reads has no slot, and is not written).
+    auto slot_of = [&](const std::string& name) -> int64_t {
+      for (auto& slot : inputs_)
+        if (slot.name == name) return int64_t(slot.id);
+      return -1;
+    };
+    const int64_t ids = slot_of("ids"), positions = slot_of("positions"), key_mask = slot_of("key_mask");
+    int64_t labels = slot_of("labels"), weights = slot_of("weights");
+    const Node* rows_in = p.input(kMaskedRowsInput);
+    void* lab_tok = nullptr;
+    void* w_tok = nullptr;
+    const int64_t rows = int64_t(s_.corpus_batch_ * uint64_t(s_.corpus_->c.seq_len));
+    if (rows_in && labels < 0) lab_tok = R(size_t(rows) * 4);
+    if (rows_in && weights < 0) w_tok = R(size_t(rows) * 4);
+    const uint64_t batch = s_.corpus_batch_;
+    const hk::MlmCorpus mc = s_.corpus_->c;
+    auto draw = [this] { return static_cast<const int32_t*>(static_cast<void*>(static_cast<char*>(arena_.at(input_token_)) + draw_offset_)); };
+    auto opt_i = [this](int64_t v) { return v >= 0 ? static_cast<int32_t*>(ptr(uint32_t(v))) : nullptr; };
+    auto opt_f = [this](int64_t v) { return v >= 0 ? static_cast<float*>(ptr(uint32_t(v))) : nullptr; };
+    pending.push_back({[=] {
+      return Launch{"MlmBatch", [=](hipStream_t st) {
+                      hk::mlm_rows(st, mc, draw(), int64_t(batch), opt_i(ids), opt_i(positions), opt_f(key_mask),
+                                   lab_tok ? static_cast<int32_t*>(A(lab_tok)) : opt_i(labels),
+                                   w_tok ? static_cast<float*>(A(w_tok)) : opt_f(weights));
+                    }};
+    }});
+    pending.back().bytes = 4.0 * double(rows) * 6;
+    if (rows_in) {
+      const Node* ml = nullptr;
+      const Node* mw = nullptr;
+      for (auto& x : p.nodes)
+        if (x.op == Op::Input) {
+          if (x.name.rfind(kMaskedLabelsPrefix, 0) == 0) ml = &x;
+          if (x.name.rfind(kMaskedWeightsPrefix, 0) == 0) mw = &x;
+        }
+      if (!ml || !mw) throw IrError("the masked-row gather inputs are incomplete");
+      const uint32_t rid = rows_in->id, lid = ml->id, wid = mw->id;
+      const int64_t cap = rows_in->ty.count();
+      uint32_t* err = s_.corpus_->error;
+      pending.push_back({[=] {
+        return Launch{"MaskedGather", [=](hipStream_t st) {
+                        hk::masked_gather(st, lab_tok ? static_cast<int32_t*>(A(lab_tok)) : opt_i(labels),
+                                          w_tok ? static_cast<float*>(A(w_tok)) : opt_f(weights), rows, cap, draw(),
+                                          I(rid), I(lid), F(wid), err);
+                      }};
+      }});
+      pending.back().bytes = 4.0 * double(2 * rows + 3 * cap);
+    }
+  }
 
   for (size_t k = 0; k < n; ++k) {
     if (!need[k]) continue;
@@ -1088,13 +1156,18 @@ void Executor::build() {
 }
 
 void Executor::stage(const Batch& batch) {
+  auto fed = [&](const std::string& name) {
+    for (auto& in : inputs_)
+      if (in.device && in.name == name) return true;
+    return false;
+  };
   // The checks the reference makes before a step reads an id (interpreter.rs:700-715,
   // 1146-1262): ids inside their table, labels inside the classes, weights finite and not
   // negative, key masks of 0 and 1 with a 1 in every sequence.
   for (auto& [key, rows] : id_bounds_) {
     if (key.rfind("#weights:", 0) == 0) {
       auto it = batch.f32.find(key.substr(9));
-      if (it == batch.f32.end()) continue;
+      if (it == batch.f32.end() || fed(key.substr(9))) continue;
       for (size_t r = 0; r < it->second.size(); ++r) {
         float w = it->second[r];
         if (!(w * 0.0f == 0.0f) || w < 0.0f) throw IrError("loss weight " + std::to_string(r) + " is negative or not finite");
@@ -1103,6 +1176,7 @@ void Executor::stage(const Batch& batch) {
     }
     bool label = key.rfind("#labels:", 0) == 0;
     std::string name = label ? key.substr(8) : key;
+    if (fed(name)) continue;
     auto it = batch.i32.find(name);
     if (it == batch.i32.end()) continue;
     for (size_t r = 0; r < it->second.size(); ++r) {
@@ -1114,7 +1188,7 @@ void Executor::stage(const Batch& batch) {
   }
   for (auto& name : key_masks_) {
     auto it = batch.f32.find(name);
-    if (it == batch.f32.end()) continue;
+    if (it == batch.f32.end() || fed(name)) continue;
     const Node* in = p_.input(name);
     int64_t S = in->ty.shape[1];
     for (size_t b = 0; b * size_t(S) < it->second.size(); ++b) {
@@ -1131,7 +1205,15 @@ void Executor::stage(const Batch& batch) {
   next_slot_ = (next_slot_ + 1) % kRing;
   hip_check(hipEventSynchronize(slot_done_[slot]), "hipEventSynchronize (staging slot)");
   char* host = static_cast<char*>(pinned_[slot]);
+  if (s_.corpus_) {
+    auto it = batch.i32.find(kDrawInput);
+    if (it == batch.i32.end() || it->second.size() != 3 + s_.corpus_batch_)
+      throw IrError(std::string("a step on a packed corpus takes `") + kDrawInput + "` of " +
+                    std::to_string(3 + s_.corpus_batch_) + " words");
+    std::memcpy(host + draw_offset_, it->second.data(), it->second.size() * 4);
+  }
   for (auto& in : inputs_) {
+    if (in.device) continue;
     const void* src = nullptr;
     size_t have = 0;
     if (in.dtype == DType::F32) {
@@ -1145,9 +1227,9 @@ void Executor::stage(const Batch& batch) {
     if (int64_t(have) != in.count) throw IrError("input `" + in.name + "` has " + std::to_string(have) + " elements, not " + std::to_string(in.count));
     std::memcpy(host + in.offset, src, size_t(in.count) * 4);
   }
-  if (input_bytes_) {
-    hip_check(hipMemcpyAsync(arena_.at(input_token_), host, input_bytes_, hipMemcpyHostToDevice, s_.stream_), "hipMemcpyAsync (inputs)");
-    s_.stats_.bytes_uploaded += input_bytes_;
+  if (host_bytes_) {
+    hip_check(hipMemcpyAsync(arena_.at(input_token_), host, host_bytes_, hipMemcpyHostToDevice, s_.stream_), "hipMemcpyAsync (inputs)");
+    s_.stats_.bytes_uploaded += host_bytes_;
   }
   hip_check(hipEventRecord(slot_done_[slot], s_.stream_), "hipEventRecord");
 }
@@ -1161,12 +1243,54 @@ void Executor::run(hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------------
-Session::Session(int device, const TrainingStep& step, const Program& forward, uint64_t seed, uint32_t prediction)
+Session::DeviceCorpus::~DeviceCorpus() {
+  if (mem) (void)hipFree(mem);
+}
+
+bool Session::corpus_fed(const Program& p, const std::string& name) const {
+  if (!corpus_) return false;
+  for (const char* t : kBatchTensors)
+    if (name == t) return true;
+  return name == kMaskedRowsInput || name.rfind(kMaskedLabelsPrefix, 0) == 0 || name.rfind(kMaskedWeightsPrefix, 0) == 0;
+}
+
+void Session::check_data_error() {
+  if (!corpus_) return;
+  uint32_t e[4] = {};
+  hip_check(hipMemcpy(e, corpus_->error, sizeof e, hipMemcpyDeviceToHost), "hipMemcpy (gather error)");
+  if (!e[0]) return;
+  const uint64_t draw = uint64_t(e[2]) | (uint64_t(e[3]) << 32);
+  const bool held = draw >> 63;
+  throw IrError(std::string("E-DATA-012: the batch of ") + (held ? "held-out batch " : "step ") +
+                std::to_string(held ? draw - (uint64_t(1) << 63) : draw) + " has " + std::to_string(e[1]) +
+                " rows of non-zero weight, more than the rows the masked-row gather holds");
+}
+
+Session::Session(int device, const TrainingStep& step, const Program& forward, uint64_t seed, uint32_t prediction,
+                 const PackedCorpus* corpus)
     : device_(device), step_(step), forward_(forward), seed_(seed), prediction_(prediction) {
   step_.program.reindex();
   forward_.reindex();
   hip_check(hipSetDevice(device), "hipSetDevice");
   hk::prepare();
+  if (corpus) {
+    // Both splits resident in HBM for the whole run, and the four error words behind them.
+    corpus_batch_ = bind_corpus(forward_, *corpus);
+    corpus_ = std::make_unique<DeviceCorpus>();
+    const size_t tb = corpus->train.size() * 4, hb = corpus->heldout.size() * 4;
+    const size_t hoff = (tb + 255) / 256 * 256, eoff = hoff + (hb + 255) / 256 * 256;
+    hip_check(hipMalloc(&corpus_->mem, eoff + 256), "hipMalloc (packed corpus)");
+    char* base = static_cast<char*>(corpus_->mem);
+    hip_check(hipMemcpy(base, corpus->train.data(), tb, hipMemcpyHostToDevice), "hipMemcpy (train split)");
+    hip_check(hipMemcpy(base + hoff, corpus->heldout.data(), hb, hipMemcpyHostToDevice), "hipMemcpy (held-out split)");
+    hip_check(hipMemset(base + eoff, 0, 256), "hipMemset (gather error)");
+    const MaskingThresholds t = masking_thresholds(corpus->policy);
+    corpus_->c = hk::MlmCorpus{reinterpret_cast<const int32_t*>(base), reinterpret_cast<const int32_t*>(base + hoff),
+                               int64_t(corpus->seq_len), seed, t.select, t.mask, t.mask_or_random,
+                               corpus->vocabulary_size - kSpecialTokens};
+    corpus_->error = reinterpret_cast<uint32_t*>(base + eoff);
+    stats_.device_bytes += eoff + 256;
+  }
   hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
   const auto& params = step_.program.params;
   offset_.assign(params.size(), 0);
@@ -1193,7 +1317,7 @@ Session::Session(int device, const TrainingStep& step, const Program& forward, u
   counter_ = reinterpret_cast<uint32_t*>(base + 4 * total_ + loss_capacity_);
   if (step_.has_optimizer) step_exec_ = std::make_unique<Executor>(*this, step_.program, true);
   fwd_exec_ = std::make_unique<Executor>(*this, forward_, false);
-  stats_.device_bytes = floats * 4;
+  stats_.device_bytes += floats * 4;
 }
 
 Session::~Session() {
@@ -1202,6 +1326,7 @@ Session::~Session() {
   if (graph_) (void)hipGraphDestroy(graph_);
   step_exec_.reset();
   fwd_exec_.reset();
+  corpus_.reset();
   if (state_mem_) (void)hipFree(state_mem_);
   if (eval_mem_) (void)hipFree(eval_mem_);
   if (stream_) (void)hipStreamDestroy(stream_);
@@ -1210,6 +1335,10 @@ Session::~Session() {
 size_t Session::launches_per_step() const { return step_exec_ ? step_exec_->launches().size() : 0; }
 
 const void* Session::forward_value(uint32_t id) const { return fwd_exec_->value(id); }
+const void* Session::step_value(uint32_t id) const {
+  if (!step_exec_) throw IrError("no training step is loaded");
+  return step_exec_->value(id);
+}
 
 void Session::run_forward(const Batch& batch) {
   fwd_exec_->stage(batch);
@@ -1332,6 +1461,7 @@ float Session::final_loss(const Batch& batch) {
   fwd_exec_->stage(batch);
   fwd_exec_->run(stream_);
   sync();
+  check_data_error();
   float loss = 0;
   hip_check(hipMemcpy(&loss, fwd_exec_->value(fwd_exec_->loss_value), 4, hipMemcpyDeviceToHost), "hipMemcpy (loss)");
   return loss;
@@ -1358,7 +1488,7 @@ HeldOutSums Session::held_out(const HeldOut& h) {
   }
   float* row_out = static_cast<float*>(eval_mem_);
   auto* state = reinterpret_cast<hk::HeldOutState*>(static_cast<char*>(eval_mem_) + state_at);
-  hk::fill_zero(stream_, state, 16);
+  hk::fill_zero(stream_, state, sizeof(hk::HeldOutState));
   for (auto& batch : h.batches()) {
     fwd_exec_->stage(batch);
     fwd_exec_->run(stream_);
@@ -1367,15 +1497,23 @@ HeldOutSums Session::held_out(const HeldOut& h) {
     hk::held_out_sum(stream_, row_out, static_cast<const float*>(fwd_exec_->value(w->id)), rows, state);
   }
   sync();
+  check_data_error();
   hk::HeldOutState got{};
   hip_check(hipMemcpy(&got, state, sizeof(got), hipMemcpyDeviceToHost), "hipMemcpy (held-out state)");
-  return {got.numerator, uint64_t(got.correct)};
+  HeldOutSums out;
+  out.numerator = got.numerator;
+  out.correct = uint64_t(got.correct);
+  out.denominator = got.denominator;
+  out.selected = uint64_t(got.selected);
+  out.has_totals = true;
+  return out;
 }
 
 std::vector<float> Session::losses() {
   sync();
   uint32_t count = 0;
   hip_check(hipMemcpy(&count, counter_, 4, hipMemcpyDeviceToHost), "hipMemcpy (loss counter)");
+  check_data_error();
   count = std::min(count, loss_capacity_);
   std::vector<float> out(count);
   if (count) hip_check(hipMemcpy(out.data(), losses_dev_, count * 4, hipMemcpyDeviceToHost), "hipMemcpy (losses)");

@@ -13,6 +13,7 @@
 #include <string>
 #include <vector>
 
+#include "../host/packed.h"
 #include "../host/runner.h"
 #include "kernels.h"
 
@@ -57,7 +58,11 @@ class Executor;
 // A loaded training run on one device.
 class Session : public Engine {
  public:
-  Session(int device, const TrainingStep& step, const Program& forward, uint64_t seed, uint32_t prediction);
+  // With `corpus`, the batch tensors of both programs (ids, positions, key_mask, labels, weights)
+  // and the masked-row gather are drawn on the device from the corpus, resident in HBM; each
+  // step then stages kDrawInput instead of its batch.
+  Session(int device, const TrainingStep& step, const Program& forward, uint64_t seed, uint32_t prediction,
+          const PackedCorpus* corpus = nullptr);
   ~Session() override;
 
   void set_params(const std::vector<std::vector<float>>& values) override;
@@ -85,7 +90,13 @@ class Session : public Engine {
   // The forward program alone, on the current parameters (per-op tests, evaluation).
   void run_forward(const Batch& batch);
   const void* forward_value(uint32_t id) const;
+  // A value of the step program (its inputs among them) as the last step left it.
+  const void* step_value(uint32_t id) const;
   void load_params(const std::vector<std::vector<float>>& values) { upload_params(values); }
+  // Sequences per step of the bound corpus (0 without one).
+  uint64_t corpus_batch() const { return corpus_batch_; }
+  // Throws the E-DATA-012 refusal a device gather recorded (after a wait on the stream).
+  void check_data_error();
 
  private:
   friend class Executor;
@@ -107,6 +118,18 @@ class Session : public Engine {
   uint32_t* counter_ = nullptr;
   uint32_t loss_capacity_ = 1u << 20;
   void* state_mem_ = nullptr;
+  // The packed corpus on the device: both splits, the masking constants and the gather's error
+  // words.
+  struct DeviceCorpus {
+    hk::MlmCorpus c{};
+    void* mem = nullptr;
+    uint32_t* error = nullptr;
+    ~DeviceCorpus();
+  };
+  std::unique_ptr<DeviceCorpus> corpus_;
+  uint64_t corpus_batch_ = 0;
+  // Whether the corpus writes input `name` of `p` (a batch tensor or a masked-row gather input).
+  bool corpus_fed(const Program& p, const std::string& name) const;
   void* eval_mem_ = nullptr;     // held-out row results [rows, 2] and the HeldOutState behind them
   int64_t eval_rows_ = 0;
 
@@ -140,9 +163,10 @@ class Executor {
   std::map<uint32_t, void*> token_;   // arena reservation per value
   std::map<uint32_t, void*> fixed_;   // values living in the session's arenas
   std::vector<Launch> launches_;
-  struct InputSlot { std::string name; DType dtype; int64_t count; size_t offset; uint32_t id; };
+  // device: written on the device by the corpus prologue, never staged by the host.
+  struct InputSlot { std::string name; DType dtype; int64_t count; size_t offset; uint32_t id; bool device; };
   std::vector<InputSlot> inputs_;
-  size_t input_bytes_ = 0;
+  size_t input_bytes_ = 0, host_bytes_ = 0, draw_offset_ = 0;
   void* input_token_ = nullptr;
   static constexpr int kRing = 4;
   void* pinned_[kRing] = {};

@@ -69,8 +69,26 @@ int32_t Feed::zipf(uint64_t step, uint32_t row, uint64_t draw) const {
   return int32_t(cfg_.first_token + r);
 }
 
+Feed::Feed(const Compiled& c, const PackedCorpus* corpus, uint64_t batch)
+    : cfg_(c.config), corpus_(corpus), corpus_batch_(batch) {
+  if (!corpus || batch == 0) throw IrError("a corpus feed needs a corpus and a batch of at least one sequence");
+}
+
+Batch Feed::held_out(uint64_t b) const {
+  if (corpus_) {
+    Batch out;
+    out.i32[kDrawInput] = draw_words(SplitRole::HeldOut, orders_.draw(*corpus_, SplitRole::HeldOut, cfg_.seed, b, corpus_batch_));
+    return out;
+  }
+  return batch((uint64_t(1) << 63) + b);
+}
+
 Batch Feed::batch(uint64_t step) const {
   Batch b;
+  if (corpus_) {
+    b.i32[kDrawInput] = draw_words(SplitRole::Train, orders_.draw(*corpus_, SplitRole::Train, cfg_.seed, step, corpus_batch_));
+    return b;
+  }
   switch (cfg_.feed) {
     case FeedKind::Teacher:
       b.f32[cfg_.x] = x_;
@@ -152,6 +170,14 @@ void masked_gather(const std::vector<int32_t>& labels, const std::vector<float>&
 
 HeldOut::HeldOut(const Compiled& c, const Feed& feed, uint64_t batches)
     : labels_(c.config.labels), weights_(c.config.weights) {
+  if (const PackedCorpus* corpus = feed.corpus()) {
+    const uint64_t whole = corpus->sequences(SplitRole::HeldOut) / feed.corpus_batch();
+    if (whole == 0)
+      throw PackedError(corpus->dir + ": the HeldOut split holds " + std::to_string(corpus->sequences(SplitRole::HeldOut)) +
+                        " sequences, fewer than the batch of " + std::to_string(feed.corpus_batch()) +
+                        " that an evaluation reads");
+    batches = batches == 0 ? whole : std::min(batches, whole);
+  }
   if (batches == 0) throw IrError("held-out evaluation needs at least one batch");
   check_program(c.forward, c.prediction);
   batches_.reserve(size_t(batches));
@@ -165,6 +191,7 @@ HeldOut::HeldOut(const Program& forward, uint32_t prediction, std::string labels
   check_program(forward, prediction);
   const int64_t rows = forward.input(labels_)->ty.count();
   for (size_t b = 0; b < batches_.size(); ++b) {
+    if (batches_[b].i32.count(kDrawInput)) continue;  // drawn on the device
     auto l = batches_[b].i32.find(labels_);
     auto w = batches_[b].f32.find(weights_);
     if (l == batches_[b].i32.end() || w == batches_[b].f32.end() || int64_t(l->second.size()) != rows ||
@@ -190,7 +217,9 @@ void HeldOut::check_program(const Program& forward, uint32_t prediction) {
 
 void HeldOut::check_labels() const {
   for (size_t b = 0; b < batches_.size(); ++b) {
-    const auto& labels = batches_[b].i32.at(labels_);
+    auto it = batches_[b].i32.find(labels_);
+    if (it == batches_[b].i32.end()) continue;  // drawn on the device from a checked corpus
+    const auto& labels = it->second;
     for (size_t n = 0; n < labels.size(); ++n)
       if (labels[n] < 0 || labels[n] >= classes_)
         throw HeldOutLabelError("held-out batch " + std::to_string(b) + ", row " + std::to_string(n) + ": label " +
@@ -205,12 +234,20 @@ HeldOutMetrics HeldOut::metrics_of_sums(const HeldOutSums& sums) const {
   double den = 0;
   bool first = true;
   uint64_t selected = 0;
-  for (auto& b : batches_)
-    for (float w : b.f32.at(weights_)) {
-      den = first ? double(w) : den + double(w);
-      first = false;
-      if (w > 0.0f) ++selected;
-    }
+  bool host_weights = true;
+  for (auto& b : batches_) host_weights = host_weights && b.f32.count(weights_);
+  if (!host_weights) {
+    if (!sums.has_totals) throw IrError("held-out sums without the weight totals of batches drawn on the device");
+    den = sums.denominator;
+    selected = sums.selected;
+  } else {
+    for (auto& b : batches_)
+      for (float w : b.f32.at(weights_)) {
+        den = first ? double(w) : den + double(w);
+        first = false;
+        if (w > 0.0f) ++selected;
+      }
+  }
   HeldOutMetrics m;
   m.loss = den == 0.0 ? 0.0f : float(sums.numerator / den);
   m.accuracy = selected == 0 ? 0.0f : float(sums.correct) / float(selected);
@@ -221,7 +258,8 @@ StepInputs step_inputs(const Compiled& c, const Feed& feed, uint64_t step, uint6
   StepInputs in;
   in.batch = feed.batch(step);
   const Program& p = c.step.program;
-  if (const Node* rows = p.input(kMaskedRowsInput)) {
+  const bool on_device = in.batch.i32.count(kDrawInput) != 0;  // the device draws and gathers
+  if (const Node* rows = on_device ? nullptr : p.input(kMaskedRowsInput)) {
     const auto& cfg = c.config;
     std::vector<int32_t> r, l;
     std::vector<float> w;
@@ -244,14 +282,15 @@ StepInputs step_inputs(const Compiled& c, const Feed& feed, uint64_t step, uint6
   return in;
 }
 
-RunResult run(const Compiled& c, Engine& engine, uint64_t steps, uint64_t eval_every, uint64_t eval_batches) {
+RunResult run(const Compiled& c, Engine& engine, uint64_t steps, uint64_t eval_every, uint64_t eval_batches,
+              const PackedCorpus* corpus) {
   RunResult out;
   const uint64_t end = steps;
   if (c.step.rule == Rule::AdamW && steps > 0 && c.step.adamw.warmup_steps >= end)
     throw IrError("the warmup of " + std::to_string(c.step.adamw.warmup_steps) +
                   " steps is not shorter than the run of " + std::to_string(end) + " steps");
   out.initial = initialize(c.forward, c.config.seed, Stream::Init);
-  Feed feed(c);
+  Feed feed = corpus ? Feed(c, corpus, bind_corpus(c.forward, *corpus)) : Feed(c);
   if (feed.needs_teacher()) {
     auto teacher = initialize(c.forward, c.config.seed, Stream::Teacher);
     feed.set_target(engine.predict(teacher, feed.batch(0)));
@@ -278,7 +317,7 @@ RunResult run(const Compiled& c, Engine& engine, uint64_t steps, uint64_t eval_e
   out.train_seconds = std::chrono::duration<double>(t1 - t0).count() - out.eval_seconds;
   if (held_out) evaluate(end);
   Batch last = feed.batch(end);
-  if (const Node* rows = c.step.program.input(kMaskedRowsInput)) {
+  if (const Node* rows = last.i32.count(kDrawInput) ? nullptr : c.step.program.input(kMaskedRowsInput)) {
     std::vector<int32_t> r, l;
     std::vector<float> w;
     masked_gather(last.i32.at(c.config.labels), last.f32.at(c.config.weights), uint64_t(rows->ty.count()), end, r, l, w);

@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "models.h"
+#include "packed.h"
 #include "rng.h"
 
 namespace msx {
@@ -28,17 +29,25 @@ std::vector<std::vector<float>> initialize(const Program& p, uint64_t seed, Stre
 class Feed {
  public:
   explicit Feed(const Compiled& c);
+  // Batches drawn from a packed corpus on the device: each batch is only kDrawInput, the step's
+  // sequences of the epoch order (mlm.rs:717-760); `corpus` outlives the feed.
+  Feed(const Compiled& c, const PackedCorpus* corpus, uint64_t batch);
+  const PackedCorpus* corpus() const { return corpus_; }
+  uint64_t corpus_batch() const { return corpus_batch_; }
   // The batch of step `step` (Teacher and Classifier data are the same every step).
   Batch batch(uint64_t step) const;
   // Batch `b` of the held-out split: the batch drawn at step id 2^63 + b, the id the reference
   // gives the masking of held-out batch b (train/eval.rs:6-10), so no training step draws it.
-  Batch held_out(uint64_t b) const { return batch((uint64_t(1) << 63) + b); }
+  Batch held_out(uint64_t b) const;
   // Teacher data: the input tensor and the (zero) target before set_target.
   void set_target(std::vector<float> y) { target_ = std::move(y); }
   bool needs_teacher() const { return cfg_.feed == FeedKind::Teacher; }
 
  private:
   TrainConfig cfg_;
+  const PackedCorpus* corpus_ = nullptr;
+  uint64_t corpus_batch_ = 0;
+  mutable EpochOrders orders_;
   std::vector<double> zipf_cdf_;
   std::vector<float> x_, target_;
   std::vector<int32_t> labels_;
@@ -67,14 +76,20 @@ struct HeldOutMetrics {
 struct HeldOutSums {
   double numerator = 0;
   uint64_t correct = 0;
+  // The weight sum and the rows of positive weight, when the reducer summed them too (batches
+  // drawn on the device carry no weights on the host).
+  double denominator = 0;
+  uint64_t selected = 0;
+  bool has_totals = false;
 };
 
 // The held-out batches of a run, drawn once (HeldOut::new, eval.rs:166-198): their labels and
 // weights are what the reduction reads, by the config's input names.
 class HeldOut {
  public:
-  // Draws `batches` held-out batches of `feed`; the prediction must be f32 logits [rows, V] with
-  // one row per label of a batch (eval.rs:148-163), else an IrError.
+  // Draws `batches` held-out batches of `feed` (of a corpus feed: 0 draws every whole batch of
+  // the HeldOut split, eval.rs:6-12); the prediction must be f32 logits [rows, V] with one row per
+  // label of a batch (eval.rs:148-163), else an IrError.
   HeldOut(const Compiled& c, const Feed& feed, uint64_t batches);
   // Batches the caller drew (HeldOut::batch hands the reference's own to a device, eval.rs:290),
   // with the labels and weights under the given input names of `forward`.
@@ -145,7 +160,10 @@ struct RunResult {
   double eval_seconds = 0;    // wall clock of the evaluations, outside train_seconds
 };
 
-// eval_every = 0: no evaluation; else `eval_batches` held-out batches (at least 1).
-RunResult run(const Compiled& c, Engine& engine, uint64_t steps, uint64_t eval_every = 0, uint64_t eval_batches = 0);
+// eval_every = 0: no evaluation; else `eval_batches` held-out batches (at least 1; 0 with a corpus:
+// every whole batch of its HeldOut split). With `corpus`, the batches are drawn from it
+// (mlm_batch, mlm.rs:717-788) instead of the config's synthetic data.
+RunResult run(const Compiled& c, Engine& engine, uint64_t steps, uint64_t eval_every = 0, uint64_t eval_batches = 0,
+              const PackedCorpus* corpus = nullptr);
 
 }  // namespace msx

@@ -15,9 +15,77 @@
 namespace {
 thread_local std::string g_error;
 
+// The batch tensors of a corpus draw on the CPU: mlm_batch's rows (crates/modelspec-runtime/src/
+// dataset/mlm.rs:761-788), each comparison of a Philox word made as the reference makes it, in
+// f64 on uniform(w) = (w + 0.5) / 2^32; then, for a program with a masked-row gather, the gather
+// of train/masked.rs:97-118 (rows of non-zero weight ascending, padding row 0 / label 0 / +0).
+msx::Batch expand_draw(const msx::PackedCorpus& c, uint64_t seed, const msx::Batch& in, const msx::Program& p) {
+  auto it = in.i32.find(msx::kDrawInput);
+  if (it == in.i32.end()) return in;
+  const std::vector<int32_t>& d = it->second;
+  const bool held = d.at(0) != 0;
+  const uint64_t draw_id = uint64_t(uint32_t(d[1])) | (uint64_t(uint32_t(d[2])) << 32);
+  const std::vector<int32_t>& split = held ? c.heldout : c.train;
+  const uint64_t S = c.seq_len, B = d.size() - 3, random_tokens = c.vocabulary_size - 5;
+  msx::Batch out = in;
+  out.i32.erase(msx::kDrawInput);
+  std::vector<int32_t> ids, positions, labels;
+  std::vector<float> key_mask(size_t(B * S), 1.0f), weights;
+  for (uint64_t b = 0; b < B; ++b)
+    for (uint64_t q = 0; q < S; ++q) {
+      const uint32_t row = uint32_t(b * S + q);
+      const int32_t label = split.at(size_t(uint64_t(uint32_t(d[3 + b])) * S + q));
+      const msx::Philox4 w = msx::philox_block(seed, msx::Stream::Masking, draw_id, row);
+      const bool selected = label >= 5 && msx::uniform_word(w.w[0]) < c.policy.selection_rate;
+      int32_t id;
+      if (!selected) id = label;
+      else if (msx::uniform_word(w.w[1]) < c.policy.mask_fraction) id = 4;
+      else if (msx::uniform_word(w.w[1]) < c.policy.mask_fraction + c.policy.random_fraction)
+        id = int32_t(5 + ((uint64_t(w.w[2]) * random_tokens) >> 32));
+      else id = label;
+      ids.push_back(id);
+      positions.push_back(int32_t(q));
+      labels.push_back(label);
+      weights.push_back(selected ? 1.0f : 0.0f);
+    }
+  out.i32["ids"] = ids;
+  out.i32["positions"] = positions;
+  out.i32["labels"] = labels;
+  out.f32["key_mask"] = key_mask;
+  out.f32["weights"] = weights;
+  if (const msx::Node* rows_in = p.input(msx::kMaskedRowsInput)) {
+    const size_t cap = size_t(rows_in->ty.count());
+    std::vector<int32_t> rows, lab;
+    std::vector<float> wts;
+    for (size_t r = 0; r < weights.size(); ++r)
+      if (weights[r] != 0.0f) {
+        rows.push_back(int32_t(r));
+        lab.push_back(labels[r]);
+        wts.push_back(weights[r]);
+      }
+    if (rows.size() > cap)
+      throw msx::IrError("E-DATA-012: the batch of draw " + std::to_string(draw_id) + " has " + std::to_string(rows.size()) +
+                         " rows of non-zero weight, more than the " + std::to_string(cap) +
+                         " rows the masked-row gather holds");
+    rows.resize(cap, 0);
+    lab.resize(cap, 0);
+    wts.resize(cap, 0.0f);
+    for (auto& x : p.nodes)
+      if (x.op == msx::Op::Input) {
+        if (x.name.rfind(msx::kMaskedLabelsPrefix, 0) == 0) out.i32[x.name] = lab;
+        if (x.name.rfind(msx::kMaskedWeightsPrefix, 0) == 0) out.f32[x.name] = wts;
+      }
+    out.i32[msx::kMaskedRowsInput] = rows;
+  }
+  return out;
+}
+
 class OracleEngine : public msx::Engine {
  public:
-  explicit OracleEngine(const msx::Compiled& c) : c_(c) {}
+  explicit OracleEngine(const msx::Compiled& c, const msx::PackedCorpus* corpus = nullptr) : c_(c), corpus_(corpus) {}
+  msx::Batch expand(const msx::Batch& b, const msx::Program& p) const {
+    return corpus_ ? expand_draw(*corpus_, c_.config.seed, b, p) : b;
+  }
 
   void set_params(const std::vector<std::vector<float>>& values) override {
     params_ = values;
@@ -35,13 +103,16 @@ class OracleEngine : public msx::Engine {
     for (auto& [param, v] : which == 'm' ? m_ : v_) out[param] = v;
     return out;
   }
-  std::vector<float> predict(const std::vector<std::vector<float>>& values, const msx::Batch& b) override {
+  std::vector<float> predict(const std::vector<std::vector<float>>& values, const msx::Batch& b0) override {
+    const msx::Batch b = expand(b0, c_.forward);
     oracle::Interpreter it(c_.forward, true, c_.config.seed);
     it.run(b.f32, b.i32, values);
     return it.value(c_.prediction);
   }
-  void train_step(const msx::StepInputs& in) override {
+  void train_step(const msx::StepInputs& in0) override {
     const msx::TrainingStep& s = c_.step;
+    msx::StepInputs in;
+    in.batch = expand(in0.batch, s.program);
     auto f32 = in.batch.f32;
     for (auto& [param, mo] : s.moments) {
       const std::string& path = s.program.params[param].path;
@@ -57,7 +128,8 @@ class OracleEngine : public msx::Engine {
       v_[param] = it.value(mo.v_next);
     }
   }
-  float final_loss(const msx::Batch& b) override {
+  float final_loss(const msx::Batch& b0) override {
+    const msx::Batch b = expand(b0, c_.forward);
     oracle::Interpreter it(c_.forward, true, c_.config.seed);
     it.run(b.f32, b.i32, params_);
     return it.value(c_.forward.outputs[0])[0];
@@ -65,13 +137,20 @@ class OracleEngine : public msx::Engine {
   std::vector<float> losses() override { return losses_; }
   msx::HeldOutSums held_out(const msx::HeldOut& h) override {
     tally = tally_of(h, params_);
-    return {tally.numerator, tally.correct};
+    msx::HeldOutSums out;
+    out.numerator = tally.numerator;
+    out.correct = tally.correct;
+    out.denominator = tally.denominator;
+    out.selected = tally.selected;
+    out.has_totals = true;
+    return out;
   }
   // The forward program over every held-out batch on `values`, tallied (eval.rs:263-287).
   oracle::HeldOutTally tally_of(const msx::HeldOut& h, const std::vector<std::vector<float>>& values) const {
     oracle::HeldOutTally t;
     size_t b = 0;
-    for (auto& batch : h.batches()) {
+    for (auto& batch0 : h.batches()) {
+      const msx::Batch batch = expand(batch0, c_.forward);
       oracle::Interpreter it(c_.forward, true, c_.config.seed);
       it.run(batch.f32, batch.i32, values);
       const auto& labels = batch.i32.at(h.labels_name());
@@ -86,6 +165,7 @@ class OracleEngine : public msx::Engine {
 
  private:
   const msx::Compiled& c_;
+  const msx::PackedCorpus* corpus_;
   std::vector<std::vector<float>> params_;
   std::map<uint32_t, std::vector<float>> m_, v_;
   std::vector<float> losses_;
@@ -204,15 +284,20 @@ int orc_train(const char* config, int64_t steps, int64_t masked_rows, float* los
   }
 }
 
-// A run of `config` with a held-out evaluation every `eval_every` steps over `eval_batches`
-// batches: writes the evaluated steps and, per evaluation, [loss, accuracy] as the host finishes
-// them from the sums (eval.rs:299-339) and [loss, accuracy] of the oracle's own tally
-// (eval.rs:520-575) into metrics[4 * k ..]. Returns the number of evaluations, or -1.
-int orc_train_eval(const char* config, int64_t steps, uint64_t eval_every, uint64_t eval_batches, uint64_t* eval_steps,
-                   float* metrics, uint64_t evals_len) {
+// A run of `config`, its batches synthetic or drawn from the packed directory `packed_dir`
+// (may be null), with a held-out evaluation every `eval_every` steps (0: none) over
+// `eval_batches` batches: writes the losses and final parameters (either may be null), the
+// evaluated steps and, per evaluation, [loss, accuracy] as the host finishes them from the sums
+// (eval.rs:299-339) and [loss, accuracy] of the oracle's own tally (eval.rs:520-575) into
+// metrics[4 * k ..]. Returns the number of evaluations, or -1.
+int orc_train_run(const char* config, const char* packed_dir, int64_t steps, uint64_t eval_every, uint64_t eval_batches,
+                  float* losses, uint64_t losses_len, float* params_out, uint64_t params_len, uint64_t* eval_steps,
+                  float* metrics, uint64_t evals_len) {
   try {
     msx::Compiled c = msx::compile_config(config, -1, steps);
-    OracleEngine e(c);
+    std::unique_ptr<msx::PackedCorpus> corpus;
+    if (packed_dir) corpus = std::make_unique<msx::PackedCorpus>(msx::load_packed(packed_dir));
+    OracleEngine e(c, corpus.get());
     struct Both : msx::Engine {
       OracleEngine& e;
       std::vector<std::pair<float, float>> own;
@@ -230,8 +315,20 @@ int orc_train_eval(const char* config, int64_t steps, uint64_t eval_every, uint6
         return s;
       }
     } both(e);
-    msx::RunResult r = msx::run(c, both, c.config.steps, eval_every, eval_batches);
+    msx::RunResult r = msx::run(c, both, c.config.steps, eval_every, eval_batches, corpus.get());
     if (r.evals.size() > evals_len) { g_error = "evals buffer too small"; return -1; }
+    if (losses) {
+      if (losses_len < r.losses.size()) { g_error = "losses buffer too small"; return -1; }
+      std::memcpy(losses, r.losses.data(), r.losses.size() * sizeof(float));
+    }
+    if (params_out) {
+      uint64_t off = 0;
+      for (auto& p : r.params) {
+        if (off + p.size() > params_len) { g_error = "params buffer too small"; return -1; }
+        std::memcpy(params_out + off, p.data(), p.size() * sizeof(float));
+        off += p.size();
+      }
+    }
     for (size_t k = 0; k < r.evals.size(); ++k) {
       eval_steps[k] = r.evals[k].first;
       metrics[4 * k] = r.evals[k].second.loss;
@@ -244,6 +341,76 @@ int orc_train_eval(const char* config, int64_t steps, uint64_t eval_every, uint6
     g_error = ex.what();
     return -1;
   }
+}
+
+int orc_train_eval(const char* config, int64_t steps, uint64_t eval_every, uint64_t eval_batches, uint64_t* eval_steps,
+                   float* metrics, uint64_t evals_len) {
+  return orc_train_run(config, nullptr, steps, eval_every, eval_batches, nullptr, 0, nullptr, 0, eval_steps, metrics,
+                       evals_len);
+}
+
+// The rows of one corpus draw on the CPU (the checker of the device's MlmBatch and MaskedGather):
+// step `step` of split `role` (0 Train, 1 HeldOut) of the packed directory bound to `config`.
+// Writes ids, positions, labels (i32 [B*S]), weights (f32 [B*S]) and, when the step program
+// gathers, rows, labels and weights of the gather (i32/i32/f32 [C]) into caller buffers of the
+// right sizes (any may be null). Returns B, or -1.
+int64_t orc_corpus_draw(const char* config, const char* packed_dir, int role, uint64_t step, int32_t* ids,
+                        int32_t* positions, int32_t* labels, float* weights, int32_t* g_rows, int32_t* g_labels,
+                        float* g_weights) {
+  try {
+    msx::Compiled c = msx::compile_config(config, -1, -1);
+    msx::PackedCorpus corpus = msx::load_packed(packed_dir);
+    const uint64_t B = msx::bind_corpus(c.forward, corpus);
+    msx::EpochOrders orders;
+    const msx::SplitRole r = role ? msx::SplitRole::HeldOut : msx::SplitRole::Train;
+    msx::Batch in;
+    in.i32[msx::kDrawInput] = msx::draw_words(r, orders.draw(corpus, r, c.config.seed, step, B));
+    msx::Batch b = expand_draw(corpus, c.config.seed, in, c.step.program);
+    auto put_i = [&](int32_t* dst, const char* name) {
+      if (dst && b.i32.count(name)) std::memcpy(dst, b.i32.at(name).data(), b.i32.at(name).size() * 4);
+    };
+    put_i(ids, "ids");
+    put_i(positions, "positions");
+    put_i(labels, "labels");
+    if (weights) std::memcpy(weights, b.f32.at("weights").data(), b.f32.at("weights").size() * 4);
+    if (b.i32.count(msx::kMaskedRowsInput)) {
+      put_i(g_rows, msx::kMaskedRowsInput);
+      for (auto& [name, v] : b.i32)
+        if (g_labels && name.rfind(msx::kMaskedLabelsPrefix, 0) == 0) std::memcpy(g_labels, v.data(), v.size() * 4);
+      for (auto& [name, v] : b.f32)
+        if (g_weights && name.rfind(msx::kMaskedWeightsPrefix, 0) == 0) std::memcpy(g_weights, v.data(), v.size() * 4);
+    }
+    return int64_t(B);
+  } catch (const std::exception& ex) {
+    g_error = ex.what();
+    return -1;
+  }
+}
+
+// uuid_of (dataset/mod.rs:212-227) of a 32-byte hash into out[37].
+void orc_uuid_of(const uint8_t hash[32], char out[37]) {
+  std::string u = msx::uuid_of(hash);
+  std::memcpy(out, u.c_str(), u.size() + 1);
+}
+
+// binding_id (mlm.rs:161-185) into out[37]; returns 0, or -1 when an id is not a UUID.
+int orc_binding_id(const char* dataset_id, const char* tokenizer_id, uint64_t seq_len, const double rates[4],
+                   char out[37]) {
+  msx::MaskingPolicy p;
+  p.selection_rate = rates[0];
+  p.mask_fraction = rates[1];
+  p.random_fraction = rates[2];
+  p.keep_fraction = rates[3];
+  std::string id = msx::binding_id(dataset_id, tokenizer_id, seq_len, p);
+  if (id.empty()) return -1;
+  std::memcpy(out, id.c_str(), id.size() + 1);
+  return 0;
+}
+
+// epoch_order (mlm.rs:665-680) into out[n].
+void orc_epoch_order(uint64_t seed, uint64_t epoch, uint32_t n, uint32_t* out) {
+  auto o = msx::epoch_order(seed, epoch, n);
+  std::memcpy(out, o.data(), o.size() * 4);
 }
 
 // The held-out tally over explicit logits (eval.rs Tally): `batches` batches of `rows` rows of `v`

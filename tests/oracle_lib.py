@@ -40,6 +40,12 @@ class Oracle:
         L.orc_free.argtypes = [vp]
         L.orc_init_params.argtypes = [ctypes.c_char_p, vp, u64]
         L.orc_train_eval.argtypes = [ctypes.c_char_p, i64, u64, u64, vp, vp, u64]
+        L.orc_train_run.argtypes = [ctypes.c_char_p, ctypes.c_char_p, i64, u64, u64, vp, u64, vp, u64, vp, vp, u64]
+        L.orc_corpus_draw.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int, u64, vp, vp, vp, vp, vp, vp, vp]
+        L.orc_corpus_draw.restype = i64
+        L.orc_uuid_of.argtypes = [vp, vp]
+        L.orc_binding_id.argtypes = [ctypes.c_char_p, ctypes.c_char_p, u64, vp, vp]
+        L.orc_epoch_order.argtypes = [u64, u64, u32, vp]
         L.orc_held_out_tally.argtypes = [vp, vp, vp, u64, u64, u64, vp]
         self.L = L
 
@@ -69,6 +75,56 @@ class Oracle:
         if n < 0:
             raise RuntimeError(self.err())
         return [(int(at[k]), (m[4 * k], m[4 * k + 1]), (m[4 * k + 2], m[4 * k + 3])) for k in range(n)]
+
+    def train_packed(self, config, packed_dir, steps, eval_every=0, eval_batches=0):
+        """A run on a packed directory: (losses, flat params, [(step, host (loss, acc), tally (loss, acc))])."""
+        from modelspec_amd import api
+        step_ir, _ = api.compile_config(config, -1, steps)
+        losses = np.zeros(steps + 1, np.float32)
+        params = np.zeros(api.param_count(step_ir), np.float32)
+        cap = (steps // eval_every + 2) if eval_every else 1
+        at = np.zeros(cap, np.uint64)
+        m = np.zeros(4 * cap, np.float32)
+        n = self.L.orc_train_run(config.encode(), packed_dir.encode(), steps, eval_every, eval_batches,
+                                 losses.ctypes.data, losses.size, params.ctypes.data, params.size, at.ctypes.data,
+                                 m.ctypes.data, cap)
+        if n < 0:
+            raise RuntimeError(self.err())
+        evals = [(int(at[k]), (m[4 * k], m[4 * k + 1]), (m[4 * k + 2], m[4 * k + 3])) for k in range(n)]
+        return losses, params, evals
+
+    def corpus_draw(self, config, packed_dir, role, step, rows, capacity=0):
+        """The CPU rows of one corpus draw: dict of ids, positions, labels, weights (and the gather's
+        rows, labels, weights when capacity > 0)."""
+        out = {"ids": np.zeros(rows, np.int32), "positions": np.zeros(rows, np.int32),
+               "labels": np.zeros(rows, np.int32), "weights": np.zeros(rows, np.float32)}
+        if capacity:
+            out.update({"g_rows": np.zeros(capacity, np.int32), "g_labels": np.zeros(capacity, np.int32),
+                        "g_weights": np.zeros(capacity, np.float32)})
+        ptr = lambda k: out[k].ctypes.data if k in out else None
+        b = self.L.orc_corpus_draw(config.encode(), packed_dir.encode(), role, step, ptr("ids"), ptr("positions"),
+                                   ptr("labels"), ptr("weights"), ptr("g_rows"), ptr("g_labels"), ptr("g_weights"))
+        if b < 0:
+            raise RuntimeError(self.err())
+        return out
+
+    def uuid_of(self, digest):
+        buf = ctypes.create_string_buffer(37)
+        d = (ctypes.c_uint8 * 32)(*digest)
+        self.L.orc_uuid_of(d, buf)
+        return buf.value.decode()
+
+    def binding_id(self, dataset_id, tokenizer_id, seq_len, rates):
+        buf = ctypes.create_string_buffer(37)
+        r = np.array(rates, np.float64)
+        if self.L.orc_binding_id(dataset_id.encode(), tokenizer_id.encode(), seq_len, r.ctypes.data, buf) != 0:
+            return None
+        return buf.value.decode()
+
+    def epoch_order(self, seed, epoch, n):
+        out = np.zeros(n, np.uint32)
+        self.L.orc_epoch_order(seed, epoch, n, out.ctypes.data)
+        return out
 
     def held_out_tally(self, logits, labels, weights):
         """logits [batches, rows, v] f32, labels [batches, rows] i32, weights [batches, rows] f32 ->
