@@ -147,12 +147,19 @@ __device__ __forceinline__ void wide_store(float* S, int e, float4 v) {
 }
 }  // namespace
 
+// The order a GEMM's tiles are handed to blocks: mt x nt tiles a split slice, `tiles` in all,
+// M tiles adjacent when m_fastest.
+struct GemmOrder {
+  uint32_t mt, nt, tiles;
+  bool m_fastest;
+};
+
 template <bool TA, bool TB, int WM, int WN, int WK, bool VA, bool VB>
 __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, const float* __restrict__ B,
                                                 float* __restrict__ C, GemmEpi epi, int64_t M,
                                                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                                                 int64_t kchunk, float* __restrict__ ws, float* __restrict__ colsum,
-                                                bool sum_a, bool vo) {
+                                                bool sum_a, bool vo, GemmOrder order) {
   constexpr int TM = 32 * WM, TN = 32 * WN, LA = TM + 16, LB = TN + 16, LC = TN + 4;
   constexpr int GA = TM * WK / 4, GB = TN * WK / 4;              // float4 groups a K tile
   constexpr int HA = (GA + 255) / 256, HB = (GB + 255) / 256;     // a thread's groups
@@ -164,8 +171,21 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   float* const As0 = smem;                  // As(buf) = As0 + buf WK LA
   float* const Bs0 = smem + NB * WK * LA;   // Bs(buf) = Bs0 + buf WK LB
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t m0 = int64_t(blockIdx.y) * TM, n0 = int64_t(blockIdx.x) * TN;
-  const int64_t kbeg = int64_t(blockIdx.z) * kchunk;
+  // The tile of this block: consecutive blocks go to the 8 XCDs in turn, so block b takes tile
+  // (b mod 8) * per + b / 8 of the grouped order, and each XCD runs one contiguous run of it.
+  const uint32_t per = gridDim.x / 8, t = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (t >= order.tiles) return;
+  uint32_t tm, tn;
+  const uint32_t tz = t / (order.mt * order.nt), tr = t % (order.mt * order.nt);
+  if (order.m_fastest) {
+    tm = tr % order.mt;
+    tn = tr / order.mt;
+  } else {
+    tn = tr % order.nt;
+    tm = tr / order.nt;
+  }
+  const int64_t m0 = int64_t(tm) * TM, n0 = int64_t(tn) * TN;
+  const int64_t kbeg = int64_t(tz) * kchunk;
   const int64_t kend = K < kbeg + kchunk ? K : kbeg + kchunk;
   const int wm = (wave >> 1) * 16 * WM, wn = (wave & 1) * 16 * WN;
   v4f acc[WM][WN];
@@ -184,7 +204,7 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   // Column sums: thread t adds tile column t mod T over the K rows (t / T) per .. + per of each
   // K tile, per = WK / (256 / T).
   const int T = sum_a ? TM : TN;
-  const bool sums = colsum != nullptr && (sum_a ? blockIdx.x == 0 : blockIdx.y == 0);
+  const bool sums = colsum != nullptr && (sum_a ? tn == 0 : tm == 0);
   const int sum_per = WK / (256 / T), sum_ld = sum_a ? LA : LB;
   const int sum_off = (tid / T) * sum_per * sum_ld + tid % T;
   float csum = 0.0f;
@@ -236,7 +256,7 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
     if (tid < T && base + tid < width) {
       float v = red[tid];
       for (int g = 1; g < 256 / T; ++g) v += red[g * T + tid];
-      colsum[(ws ? int64_t(blockIdx.z) * width : 0) + base + tid] = v;
+      colsum[(ws ? int64_t(tz) * width : 0) + base + tid] = v;
     }
   }
   // The output tile goes through LDS so that each row leaves as whole float4 groups (when `vo`:
@@ -250,7 +270,7 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
 #pragma unroll
       for (int r = 0; r < 4; ++r) smem[(wm + 16 * i + 4 * (lane >> 4) + r) * LC + wn + 16 * j + (lane & 15)] = acc[i][j][r];
   __syncthreads();
-  float* out = ws ? ws + int64_t(blockIdx.z) * M * N : C;
+  float* out = ws ? ws + int64_t(tz) * M * N : C;
   const int64_t ldo = ws ? N : ldc;
   constexpr int Q = TN / 4;
 #pragma unroll
@@ -337,9 +357,14 @@ void gemm(hipStream_t s, const GemmArgs& g) {
       bad("gemm split-K workspace too small");
     ws = g.workspace;
   }
-  const dim3 wgrid(unsigned((g.n + 32 * plan.wn - 1) / (32 * plan.wn)), unsigned((g.m + 32 * plan.wm - 1) / (32 * plan.wm)),
-                   unsigned(split));
-  if (wgrid.y > 65535) bad("gemm M too large");
+  // Tiles in the grouped order: split slices outermost; within a slice the tiles that share the
+  // larger operand's panel are adjacent (M tiles of one column when B is the larger, N tiles of
+  // one row otherwise), so that each XCD's L2 serves the panel to all of them.
+  const int64_t nt = (g.n + 32 * plan.wn - 1) / (32 * plan.wn), mt = (g.m + 32 * plan.wm - 1) / (32 * plan.wm);
+  const int64_t tiles = nt * mt * split;
+  if (tiles > (int64_t(1) << 30)) bad("gemm has too many tiles");
+  const GemmOrder order{uint32_t(mt), uint32_t(nt), uint32_t(tiles), g.n * g.k >= g.m * g.k};
+  const dim3 wgrid(unsigned((tiles + 7) / 8 * 8));
   const int64_t width = g.sum_a ? g.m : g.n;
   if ((g.act == EPI_GELU_GRAD || g.act == EPI_RELU_GRAD) && !g.pre_in) bad("gemm activation gradient without its input");
   const GemmEpi epi{g.bias, g.addend, g.pre_in, g.pre_out, g.act};
@@ -358,7 +383,7 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   const bool vb = aligned(g.b, g.ldb, g.pad_b ? g.ldb : (g.tb ? g.k : g.n));
 #define MSX_WIDE_V(TA, TB, WM, WN, WK, VA, VB)                                                              \
   MSX_LAUNCH((k_gemm_w<TA, TB, WM, WN, WK, VA, VB>), wgrid, dim3(256), 0, s, g.a, g.b, g.c, epi, g.m, g.n,   \
-                     g.k, g.lda, g.ldb, g.ldc, chunk, ws, csum, g.sum_a, vo)
+                     g.k, g.lda, g.ldb, g.ldc, chunk, ws, csum, g.sum_a, vo, order)
   // float4 variants for both operands aligned, or the right one only; scalar loads otherwise.
 #define MSX_WIDE(TA, TB, WM, WN, WK)                                \
   if (va && vb) MSX_WIDE_V(TA, TB, WM, WN, WK, true, true);         \
