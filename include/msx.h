@@ -23,6 +23,7 @@ extern "C" {
 #define MSX_E_DEVICE -3      /* E-TARGET-002/003: no HIP runtime or no such device */
 #define MSX_E_NONFINITE -4   /* E-TRAIN-001: a loss stopped being finite */
 #define MSX_E_UNSUPPORTED -5 /* a step op or shape this backend has no kernel for */
+#define MSX_E_CHECKPOINT -6  /* E-CKPT-001..004: an unreadable, damaged or mismatched .msckpt */
 
 typedef struct msx_ctx msx_ctx;
 
@@ -165,6 +166,29 @@ int msx_train_packed(msx_ctx* ctx, const char* config, const char* dir, int64_t 
                      uint64_t eval_batches, float* losses, uint64_t losses_len, float* params, uint64_t params_len,
                      uint64_t* eval_steps, msx_heldout* evals, uint64_t evals_len, uint64_t* n_evals,
                      double* train_seconds, double* eval_seconds);
+
+/* Writes the loaded step's current parameters (and, under AdamW, its moments as optimizer slots
+ * "m" and "v") as a .msckpt v1 file recording `step` updates (crates/modelspec-runtime/src/train/
+ * checkpoint.rs; the reference writes no moments and so refuses to resume AdamW). The same
+ * state writes the same bytes. */
+int msx_checkpoint_write(msx_ctx* ctx, const char* path, uint64_t step);
+
+/* Reads a .msckpt v1 file, validated in the reference's order (E-CKPT-001/002/004 as
+ * MSX_E_CHECKPOINT), matches it against the loaded step (paths, shapes, schema hash; with
+ * `resume` the optimizer too: E-CKPT-003) and uploads its parameters; with `resume` under AdamW
+ * its moments too (a checkpoint of step 0 may carry none). Writes the checkpoint's step. */
+int msx_checkpoint_read(msx_ctx* ctx, const char* path, int32_t resume, uint64_t* step);
+
+/* A run of a built-in config (on a packed directory when packed_dir is not NULL) that may start
+ * from the checkpoint `resume` and write checkpoints: `<stem>-<k>.msckpt` beside
+ * checkpoint_path after every checkpoint_every updates before the end, and checkpoint_path at the
+ * end (train --resume / --checkpoint / --checkpoint-every, crates/modelspec-cli/src/train.rs:
+ * 538-542, 829-835, 1075, 1285). `steps` counts this invocation's steps (negative: to the config's
+ * end); a resumed run ends at its checkpoint's step + steps. Writes steps + 1 losses, the final
+ * parameters and the start step. */
+int msx_train_checkpointed(msx_ctx* ctx, const char* config, const char* packed_dir, int64_t steps, const char* resume,
+                           uint64_t checkpoint_every, const char* checkpoint_path, float* losses, uint64_t losses_len,
+                           float* params, uint64_t params_len, uint64_t* start_step);
 
 /* Times `steps` graph-launched training steps of a built-in config after `warmup` (HIP events on
  * the run's stream after every step into step_ms[steps], may be null; host inputs made before the

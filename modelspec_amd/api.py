@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(_HERE, "libmsx.so")
 CONFIGS = ("linear_regression", "mnist_mlp", "mlp_classifier", "transformer_block", "bert_tiny",
            "bert_cpu", "bert_micro", "block_micro", "mlp_micro")
 
-STATUS = {0: "ok", -1: "invalid", -2: "data", -3: "device", -4: "nonfinite", -5: "unsupported"}
+STATUS = {0: "ok", -1: "invalid", -2: "data", -3: "device", -4: "nonfinite", -5: "unsupported", -6: "checkpoint"}
 
 
 class MsxError(RuntimeError):
@@ -76,6 +76,10 @@ def lib():
                                        ctypes.POINTER(HeldOutMetrics), u64, ctypes.POINTER(u64),
                                        ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
         L.msx_read_input.argtypes = [vp, i32, ctypes.c_char_p, vp, u64]
+        L.msx_checkpoint_write.argtypes = [vp, ctypes.c_char_p, u64]
+        L.msx_checkpoint_read.argtypes = [vp, ctypes.c_char_p, i32, ctypes.POINTER(u64)]
+        L.msx_train_checkpointed.argtypes = [vp, ctypes.c_char_p, ctypes.c_char_p, c64, ctypes.c_char_p, u64,
+                                             ctypes.c_char_p, vp, u64, vp, u64, ctypes.POINTER(u64)]
         L.msx_prog_new.argtypes = [vp, ctypes.c_char_p, u64, ctypes.POINTER(vp)]
         L.msx_prog_run.argtypes = [vp, ctypes.POINTER(Tensor), u32, ctypes.POINTER(vp), ctypes.POINTER(u64), u32]
         L.msx_prog_output.argtypes = [vp, u32, vp, u64]
@@ -259,6 +263,27 @@ class Context:
                                       losses.ctypes.data, losses.size, params.ctypes.data, params.size, at.ctypes.data,
                                       evals, cap, ctypes.byref(n), ctypes.byref(ts), ctypes.byref(es)))
         return losses, params, [(int(at[k]), evals[k].as_dict()) for k in range(n.value)]
+
+    def checkpoint_write(self, path, step):
+        _check(lib().msx_checkpoint_write(self._h, str(path).encode(), step))
+
+    def checkpoint_read(self, path, resume=True):
+        """Uploads a checkpoint's parameters (and AdamW moments when resuming); returns its step."""
+        step = ctypes.c_uint64()
+        _check(lib().msx_checkpoint_read(self._h, str(path).encode(), int(resume), ctypes.byref(step)))
+        return step.value
+
+    def train_checkpointed(self, name, steps, packed=None, resume=None, every=0, path=None):
+        """A run that may resume from a checkpoint and write checkpoints: (losses, params, start step)."""
+        enc = lambda x: None if x is None else str(x).encode()
+        step_ir, _ = compile_config(name)
+        losses = np.zeros(steps + 1, np.float32)
+        params = np.zeros(param_count(step_ir), np.float32)
+        start = ctypes.c_uint64()
+        _check(lib().msx_train_checkpointed(self._h, name.encode(), enc(packed), steps, enc(resume), every, enc(path),
+                                            losses.ctypes.data, losses.size, params.ctypes.data, params.size,
+                                            ctypes.byref(start)))
+        return losses, params, start.value
 
     def stats(self):
         s = RunStats()

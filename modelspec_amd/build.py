@@ -20,6 +20,7 @@ SOURCES = [
     "host/runner.cpp",
     "host/json.cpp",
     "host/packed.cpp",
+    "host/checkpoint.cpp",
     "hip/runtime.cpp",
     "hip/kernels.hip",
     "hip/gemm.hip",

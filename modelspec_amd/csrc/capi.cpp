@@ -6,6 +6,7 @@
 #include "../../include/msx.h"
 #include "hip/runtime.h"
 #include "host/models.h"
+#include "host/checkpoint.h"
 #include "host/packed.h"
 #include "host/runner.h"
 
@@ -29,6 +30,8 @@ int guarded(F&& f) {
     return fail(MSX_E_DATA, e.what());
   } catch (const msx::PackedError& e) {
     return fail(MSX_E_DATA, e.what());
+  } catch (const msx::CheckpointError& e) {
+    return fail(MSX_E_CHECKPOINT, e.what());
   } catch (const msx::IrError& e) {
     std::string w = e.what();
     if (w.find("E-DATA-") != std::string::npos || w.find("key mask") != std::string::npos ||
@@ -339,6 +342,9 @@ int train_run(msx_ctx* ctx, const char* config, int64_t steps, uint64_t eval_eve
     void set_params(const std::vector<std::vector<float>>& v) override { s.set_params(v); }
     std::vector<std::vector<float>> params() override { return s.params(); }
     std::vector<std::vector<float>> moments(char w) override { return s.moments(w); }
+    void set_moments(const std::vector<std::vector<float>>& m, const std::vector<std::vector<float>>& v) override {
+      s.set_moments(m, v);
+    }
     std::vector<float> predict(const std::vector<std::vector<float>>& v, const msx::Batch& b) override { return s.predict(v, b); }
     void train_step(const msx::StepInputs& in) override { s.train_step(in); }
     float final_loss(const msx::Batch& b) override { return s.final_loss(b); }
@@ -422,6 +428,74 @@ int msx_train_packed(msx_ctx* ctx, const char* config, const char* dir, int64_t 
                              params_len, eval_steps, evals, evals_len, n_evals, train_seconds, eval_seconds);
     ctx->session.reset();  // its feed pointed at the run's corpus
     return rc;
+  });
+}
+
+int msx_checkpoint_write(msx_ctx* ctx, const char* path, uint64_t step) {
+  return guarded([&] {
+    if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
+    if (!path) return fail(MSX_E_INVALID, "null path");
+    msx::Session& s = *ctx->session;
+    msx::write_checkpoint(path, msx::checkpoint_of(ctx->step, ctx->seed, step, s.params(), s.moments('m'), s.moments('v')));
+    return MSX_OK;
+  });
+}
+
+int msx_checkpoint_read(msx_ctx* ctx, const char* path, int32_t resume, uint64_t* step) {
+  return guarded([&] {
+    if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
+    if (!path) return fail(MSX_E_INVALID, "null path");
+    msx::Checkpoint ck = msx::read_checkpoint(path);
+    if (resume) {
+      msx::ResumeState r = msx::resume_into(ck, ctx->step);
+      ctx->session->set_params(r.values);
+      if (ctx->step.rule == msx::Rule::AdamW) ctx->session->set_moments(r.m, r.v);
+    } else {
+      ctx->session->set_params(msx::parameters_for(ck, ctx->step));
+    }
+    if (step) *step = ck.step;
+    return MSX_OK;
+  });
+}
+
+int msx_train_checkpointed(msx_ctx* ctx, const char* config, const char* packed_dir, int64_t steps, const char* resume,
+                           uint64_t checkpoint_every, const char* checkpoint_path, float* losses, uint64_t losses_len,
+                           float* params, uint64_t params_len, uint64_t* start_step) {
+  return guarded([&] {
+    msx::Compiled c = msx::compile_config(config, -1, -1);
+    std::unique_ptr<msx::PackedCorpus> corpus;
+    if (packed_dir) corpus = std::make_unique<msx::PackedCorpus>(msx::load_packed(packed_dir));
+    std::unique_ptr<msx::ResumeState> from;
+    if (resume) from = std::make_unique<msx::ResumeState>(msx::resume_into(msx::read_checkpoint(resume), c.step));
+    const uint64_t n = steps >= 0 ? uint64_t(steps) : c.config.steps - (from ? std::min(from->step, c.config.steps) : 0);
+    ctx->session.reset();
+    ctx->step = c.step;
+    ctx->forward = c.forward;
+    ctx->prediction = c.prediction;
+    ctx->seed = c.config.seed;
+    ctx->session =
+        std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction, corpus.get());
+    msx::RunOptions o;
+    o.corpus = corpus.get();
+    o.resume = from.get();
+    o.checkpoint_every = checkpoint_every;
+    if (checkpoint_path) o.checkpoint_path = checkpoint_path;
+    msx::RunResult r = msx::run(c, *ctx->session, n, o);
+    if (corpus) ctx->session.reset();  // its feed pointed at this call's corpus
+    if (losses_len < r.losses.size()) return fail(MSX_E_INVALID, "losses buffer too small");
+    if (losses) std::memcpy(losses, r.losses.data(), r.losses.size() * 4);
+    if (params) {
+      uint64_t off = 0;
+      for (auto& p : r.params) {
+        if (off + p.size() > params_len) return fail(MSX_E_INVALID, "params buffer too small");
+        std::memcpy(params + off, p.data(), p.size() * 4);
+        off += p.size();
+      }
+    }
+    if (start_step) *start_step = r.start_step;
+    if (r.nonfinite_step >= 0)
+      return fail(MSX_E_NONFINITE, "E-TRAIN-001: the loss of step " + std::to_string(r.nonfinite_step) + " is not finite");
+    return MSX_OK;
   });
 }
 

@@ -1391,6 +1391,21 @@ std::vector<std::vector<float>> Session::moments(char which) {
   return out;
 }
 
+void Session::set_moments(const std::vector<std::vector<float>>& m, const std::vector<std::vector<float>>& v) {
+  sync();
+  for (auto& [q, mo] : step_.moments) {
+    const size_t n = size_t(step_.program.params[q].ty.count());
+    for (int k = 0; k < 2; ++k) {
+      const auto& src = k == 0 ? m : v;
+      if (q >= src.size() || src[q].size() != n)
+        throw IrError(std::string("set_moments: `") + step_.program.params[q].path + "` needs " + (k ? "v" : "m") +
+                      " of " + std::to_string(n) + " values");
+      hip_check(hipMemcpy((k == 0 ? m_ : v_) + offset_[q], src[q].data(), n * 4, hipMemcpyHostToDevice),
+                "hipMemcpy (moments)");
+    }
+  }
+}
+
 std::vector<float> Session::predict(const std::vector<std::vector<float>>& values, const Batch& batch) {
   upload_params(values);
   fwd_exec_->stage(batch);

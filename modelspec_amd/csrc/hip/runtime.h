@@ -68,6 +68,7 @@ class Session : public Engine {
   void set_params(const std::vector<std::vector<float>>& values) override;
   std::vector<std::vector<float>> params() override;
   std::vector<std::vector<float>> moments(char which) override;
+  void set_moments(const std::vector<std::vector<float>>& m, const std::vector<std::vector<float>>& v) override;
   std::vector<float> predict(const std::vector<std::vector<float>>& values, const Batch& batch) override;
   void train_step(const StepInputs& in) override;
   float final_loss(const Batch& batch) override;

@@ -1,6 +1,8 @@
 // Host side of a run. See runner.h.
 #include "runner.h"
 
+#include "checkpoint.h"
+
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -284,37 +286,71 @@ StepInputs step_inputs(const Compiled& c, const Feed& feed, uint64_t step, uint6
 
 RunResult run(const Compiled& c, Engine& engine, uint64_t steps, uint64_t eval_every, uint64_t eval_batches,
               const PackedCorpus* corpus) {
+  RunOptions o;
+  o.eval_every = eval_every;
+  o.eval_batches = eval_batches;
+  o.corpus = corpus;
+  return run(c, engine, steps, o);
+}
+
+std::string checkpoint_every_path(const std::string& path, uint64_t k) {
+  const size_t slash = path.find_last_of('/');
+  const size_t dot = path.find_last_of('.');
+  const std::string stem = dot != std::string::npos && (slash == std::string::npos || dot > slash + 1)
+                               ? path.substr(0, dot)
+                               : path;
+  return stem + "-" + std::to_string(k) + ".msckpt";
+}
+
+RunResult run(const Compiled& c, Engine& engine, uint64_t steps, const RunOptions& o) {
   RunResult out;
-  const uint64_t end = steps;
-  if (c.step.rule == Rule::AdamW && steps > 0 && c.step.adamw.warmup_steps >= end)
+  const uint64_t start = o.resume ? o.resume->step : 0;
+  const uint64_t end = start + steps;
+  out.start_step = start;
+  if (c.step.rule == Rule::AdamW && end > 0 && c.step.adamw.warmup_steps >= end)
     throw IrError("the warmup of " + std::to_string(c.step.adamw.warmup_steps) +
                   " steps is not shorter than the run of " + std::to_string(end) + " steps");
-  out.initial = initialize(c.forward, c.config.seed, Stream::Init);
-  Feed feed = corpus ? Feed(c, corpus, bind_corpus(c.forward, *corpus)) : Feed(c);
+  out.initial = o.resume ? o.resume->values : initialize(c.forward, c.config.seed, Stream::Init);
+  Feed feed = o.corpus ? Feed(c, o.corpus, bind_corpus(c.forward, *o.corpus)) : Feed(c);
   if (feed.needs_teacher()) {
     auto teacher = initialize(c.forward, c.config.seed, Stream::Teacher);
     feed.set_target(engine.predict(teacher, feed.batch(0)));
   }
   // Drawn once, before the first step, so a split the evaluation refuses stops the run first.
   std::unique_ptr<HeldOut> held_out;
-  if (eval_every) {
-    held_out = std::make_unique<HeldOut>(c, feed, eval_batches);
+  if (o.eval_every) {
+    held_out = std::make_unique<HeldOut>(c, feed, o.eval_batches);
     held_out->check_labels();
   }
+  double left_out = 0;  // evaluation and checkpoint time, outside the training clock
   auto evaluate = [&](uint64_t step) {
     auto e0 = std::chrono::steady_clock::now();
     out.evals.emplace_back(step, held_out->metrics_of_sums(engine.held_out(*held_out)));
-    out.eval_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - e0).count();
+    const double dt = std::chrono::duration<double>(std::chrono::steady_clock::now() - e0).count();
+    out.eval_seconds += dt;
+    left_out += dt;
+  };
+  // The state after k updates (train.rs:1075, 1285: `<stem>-<k>.msckpt` every n updates before
+  // the end, the checkpoint path itself at the end).
+  auto checkpoint = [&](uint64_t k, const std::string& path) {
+    auto w0 = std::chrono::steady_clock::now();
+    Checkpoint ck = checkpoint_of(c.step, c.config.seed, k, engine.params(), engine.moments('m'), engine.moments('v'));
+    write_checkpoint(path, ck);
+    out.checkpoints.push_back(path);
+    left_out += std::chrono::duration<double>(std::chrono::steady_clock::now() - w0).count();
   };
   engine.set_params(out.initial);
+  if (o.resume && c.step.rule == Rule::AdamW) engine.set_moments(o.resume->m, o.resume->v);
   auto t0 = std::chrono::steady_clock::now();
-  for (uint64_t step = 0; step < end; ++step) {
-    if (held_out && step % eval_every == 0) evaluate(step);
+  for (uint64_t step = start; step < end; ++step) {
+    if (held_out && step % o.eval_every == 0) evaluate(step);
+    if (o.checkpoint_every && step > start && step % o.checkpoint_every == 0 && !o.checkpoint_path.empty())
+      checkpoint(step, checkpoint_every_path(o.checkpoint_path, step));
     engine.train_step(step_inputs(c, feed, step, end));
   }
   out.losses = engine.losses();
   auto t1 = std::chrono::steady_clock::now();
-  out.train_seconds = std::chrono::duration<double>(t1 - t0).count() - out.eval_seconds;
+  out.train_seconds = std::chrono::duration<double>(t1 - t0).count() - left_out;
   if (held_out) evaluate(end);
   Batch last = feed.batch(end);
   if (const Node* rows = last.i32.count(kDrawInput) ? nullptr : c.step.program.input(kMaskedRowsInput)) {
@@ -324,9 +360,10 @@ RunResult run(const Compiled& c, Engine& engine, uint64_t steps, uint64_t eval_e
   }
   out.losses.push_back(engine.final_loss(last));
   out.params = engine.params();
+  if (!o.checkpoint_path.empty()) checkpoint(end, o.checkpoint_path);
   for (size_t k = 0; k < out.losses.size(); ++k)
     if (!std::isfinite(out.losses[k])) {
-      out.nonfinite_step = int64_t(k);
+      out.nonfinite_step = int64_t(start + k);
       out.losses.resize(k + 1);
       break;
     }

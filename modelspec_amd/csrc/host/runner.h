@@ -146,6 +146,8 @@ class Engine {
   virtual std::vector<float> losses() = 0;
   // The held-out sums of the forward program on the current parameters, after every queued step.
   virtual HeldOutSums held_out(const HeldOut& h) = 0;
+  // AdamW moments by ParamId (empty entries: parameters without moments), after set_params.
+  virtual void set_moments(const std::vector<std::vector<float>>& m, const std::vector<std::vector<float>>& v) = 0;
 };
 
 struct RunResult {
@@ -153,12 +155,32 @@ struct RunResult {
   std::vector<float> losses;  // steps + 1
   std::vector<std::vector<float>> params;
   double train_seconds = 0;   // wall clock of the step loop (runner.rs loop; train.rs:17-31 --clock)
-  int64_t nonfinite_step = -1;
+  int64_t nonfinite_step = -1;  // the step whose loss was not finite (absolute step number)
+  uint64_t start_step = 0;       // the step the run started at (a resumed run's checkpoint step)
+  std::vector<std::string> checkpoints;  // paths written, in order
   // Held-out metrics at every step k with k % eval_every == 0 and at the last step, on the
   // parameters after k updates (crates/modelspec-cli/src/train.rs:1293-1312).
   std::vector<std::pair<uint64_t, HeldOutMetrics>> evals;
   double eval_seconds = 0;    // wall clock of the evaluations, outside train_seconds
 };
+
+struct ResumeState;
+
+// What a run does besides training: held-out evaluation every `eval_every` steps over
+// `eval_batches` batches, batches drawn from `corpus`, a start from a checkpoint's state
+// (`resume`: `steps` then counts the steps of this invocation, which ends at resume->step +
+// steps, train.rs:549-550), and checkpoints: `<stem>-<k>.msckpt` after every `checkpoint_every`
+// updates before the end, `checkpoint_path` itself at the end (train.rs:538-542, 1075, 1285).
+struct RunOptions {
+  uint64_t eval_every = 0, eval_batches = 0;
+  const PackedCorpus* corpus = nullptr;
+  const ResumeState* resume = nullptr;
+  uint64_t checkpoint_every = 0;
+  std::string checkpoint_path;
+};
+RunResult run(const Compiled& c, Engine& engine, uint64_t steps, const RunOptions& options);
+// The path of the checkpoint after k updates: `<stem>-<k>.msckpt` beside `path`.
+std::string checkpoint_every_path(const std::string& path, uint64_t k);
 
 // eval_every = 0: no evaluation; else `eval_batches` held-out batches (at least 1; 0 with a corpus:
 // every whole batch of its HeldOut split). With `corpus`, the batches are drawn from it

@@ -9,6 +9,7 @@
 #include <cstring>
 #include <memory>
 
+#include "../modelspec_amd/csrc/host/checkpoint.h"
 #include "../modelspec_amd/csrc/host/runner.h"
 #include "interp.h"
 
@@ -102,6 +103,12 @@ class OracleEngine : public msx::Engine {
     std::vector<std::vector<float>> out(params_.size());
     for (auto& [param, v] : which == 'm' ? m_ : v_) out[param] = v;
     return out;
+  }
+  void set_moments(const std::vector<std::vector<float>>& m, const std::vector<std::vector<float>>& v) override {
+    for (auto& [param, mo] : c_.step.moments) {
+      m_[param] = m.at(param);
+      v_[param] = v.at(param);
+    }
   }
   std::vector<float> predict(const std::vector<std::vector<float>>& values, const msx::Batch& b0) override {
     const msx::Batch b = expand(b0, c_.forward);
@@ -305,6 +312,9 @@ int orc_train_run(const char* config, const char* packed_dir, int64_t steps, uin
       void set_params(const std::vector<std::vector<float>>& v) override { e.set_params(v); }
       std::vector<std::vector<float>> params() override { return e.params(); }
       std::vector<std::vector<float>> moments(char w) override { return e.moments(w); }
+      void set_moments(const std::vector<std::vector<float>>& m, const std::vector<std::vector<float>>& v) override {
+        e.set_moments(m, v);
+      }
       std::vector<float> predict(const std::vector<std::vector<float>>& v, const msx::Batch& b) override { return e.predict(v, b); }
       void train_step(const msx::StepInputs& in) override { e.train_step(in); }
       float final_loss(const msx::Batch& b) override { return e.final_loss(b); }
@@ -385,6 +395,64 @@ int64_t orc_corpus_draw(const char* config, const char* packed_dir, int role, ui
     g_error = ex.what();
     return -1;
   }
+}
+
+// A run of `config` (on `packed_dir` when not null) that may resume from `resume` and write
+// checkpoints as msx_train_checkpointed does. Writes the losses and final parameters; returns the
+// start step, or -1.
+int64_t orc_train_ckpt(const char* config, const char* packed_dir, int64_t steps, const char* resume,
+                       uint64_t checkpoint_every, const char* checkpoint_path, float* losses, uint64_t losses_len,
+                       float* params_out, uint64_t params_len) {
+  try {
+    msx::Compiled c = msx::compile_config(config, -1, -1);
+    std::unique_ptr<msx::PackedCorpus> corpus;
+    if (packed_dir) corpus = std::make_unique<msx::PackedCorpus>(msx::load_packed(packed_dir));
+    std::unique_ptr<msx::ResumeState> from;
+    if (resume) from = std::make_unique<msx::ResumeState>(msx::resume_into(msx::read_checkpoint(resume), c.step));
+    const uint64_t n = steps >= 0 ? uint64_t(steps) : c.config.steps - (from ? std::min(from->step, c.config.steps) : 0);
+    OracleEngine e(c, corpus.get());
+    msx::RunOptions o;
+    o.corpus = corpus.get();
+    o.resume = from.get();
+    o.checkpoint_every = checkpoint_every;
+    if (checkpoint_path) o.checkpoint_path = checkpoint_path;
+    msx::RunResult r = msx::run(c, e, n, o);
+    if (losses) {
+      if (losses_len < r.losses.size()) { g_error = "losses buffer too small"; return -1; }
+      std::memcpy(losses, r.losses.data(), r.losses.size() * sizeof(float));
+    }
+    if (params_out) {
+      uint64_t off = 0;
+      for (auto& p : r.params) {
+        if (off + p.size() > params_len) { g_error = "params buffer too small"; return -1; }
+        std::memcpy(params_out + off, p.data(), p.size() * sizeof(float));
+        off += p.size();
+      }
+    }
+    return int64_t(r.start_step);
+  } catch (const std::exception& ex) {
+    g_error = ex.what();
+    return -1;
+  }
+}
+
+// schema_hash (core/src/artifact.rs:169-193) of a config's step program, into out[65].
+int orc_schema_hash(const char* config, char out[65]) {
+  try {
+    msx::Compiled c = msx::compile_config(config, -1, -1);
+    std::string h = msx::schema_hash(c.step.program);
+    std::memcpy(out, h.c_str(), 65);
+    return 0;
+  } catch (const std::exception& ex) {
+    g_error = ex.what();
+    return -1;
+  }
+}
+
+// json_f64 of v into out[40].
+void orc_json_f64(double v, char out[40]) {
+  std::string s = msx::json_f64(v);
+  std::memcpy(out, s.c_str(), s.size() + 1);
 }
 
 // uuid_of (dataset/mod.rs:212-227) of a 32-byte hash into out[37].

@@ -46,6 +46,11 @@ class Oracle:
         L.orc_uuid_of.argtypes = [vp, vp]
         L.orc_binding_id.argtypes = [ctypes.c_char_p, ctypes.c_char_p, u64, vp, vp]
         L.orc_epoch_order.argtypes = [u64, u64, u32, vp]
+        L.orc_train_ckpt.argtypes = [ctypes.c_char_p, ctypes.c_char_p, i64, ctypes.c_char_p, u64, ctypes.c_char_p, vp,
+                                     u64, vp, u64]
+        L.orc_train_ckpt.restype = i64
+        L.orc_schema_hash.argtypes = [ctypes.c_char_p, vp]
+        L.orc_json_f64.argtypes = [ctypes.c_double, vp]
         L.orc_held_out_tally.argtypes = [vp, vp, vp, u64, u64, u64, vp]
         self.L = L
 
@@ -107,6 +112,30 @@ class Oracle:
         if b < 0:
             raise RuntimeError(self.err())
         return out
+
+    def train_ckpt(self, config, steps, packed=None, resume=None, every=0, path=None):
+        """A run that may resume from a checkpoint and write checkpoints: (losses, params, start step)."""
+        from modelspec_amd import api
+        enc = lambda x: None if x is None else str(x).encode()
+        step_ir, _ = api.compile_config(config)
+        losses = np.zeros(steps + 1, np.float32)
+        params = np.zeros(api.param_count(step_ir), np.float32)
+        start = self.L.orc_train_ckpt(config.encode(), enc(packed), steps, enc(resume), every, enc(path),
+                                      losses.ctypes.data, losses.size, params.ctypes.data, params.size)
+        if start < 0:
+            raise RuntimeError(self.err())
+        return losses, params, start
+
+    def schema_hash(self, config):
+        buf = ctypes.create_string_buffer(65)
+        if self.L.orc_schema_hash(config.encode(), buf) != 0:
+            raise RuntimeError(self.err())
+        return buf.value.decode()
+
+    def json_f64(self, v):
+        buf = ctypes.create_string_buffer(40)
+        self.L.orc_json_f64(v, buf)
+        return buf.value.decode()
 
     def uuid_of(self, digest):
         buf = ctypes.create_string_buffer(37)
