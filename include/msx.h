@@ -24,6 +24,7 @@ extern "C" {
 #define MSX_E_NONFINITE -4   /* E-TRAIN-001: a loss stopped being finite */
 #define MSX_E_UNSUPPORTED -5 /* a step op or shape this backend has no kernel for */
 #define MSX_E_CHECKPOINT -6  /* E-CKPT-001..004: an unreadable, damaged or mismatched .msckpt */
+#define MSX_E_ARTIFACT -7    /* E-ARTIFACT-001..004: an unreadable, altered or invalid artifact (005: MSX_E_DEVICE) */
 
 typedef struct msx_ctx msx_ctx;
 
@@ -166,6 +167,27 @@ int msx_train_packed(msx_ctx* ctx, const char* config, const char* dir, int64_t 
                      uint64_t eval_batches, float* losses, uint64_t losses_len, float* params, uint64_t params_len,
                      uint64_t* eval_steps, msx_heldout* evals, uint64_t evals_len, uint64_t* n_evals,
                      double* train_seconds, double* eval_seconds);
+
+/* Writes the loaded step as a compiled artifact of format 1 with the `Hip` backend
+ * (crates/modelspec-core/src/artifact.rs:210-290): dir/artifact.json (the manifest keys of
+ * format 1 in serde_json's pretty form, sealed by artifact_hash and artifact_id; the printed step
+ * and forward program it was planned from; its launch plans) and dir/kernels/<id>.hsaco, the
+ * gfx950 code objects of this library. `source_text` (may be NULL: the printed forward program)
+ * is what source_hash hashes. Writes the 64-hex-digit artifact hash to hash_out[65] (may be
+ * NULL). */
+int msx_write_artifact(msx_ctx* ctx, const char* dir, const char* source_text, char* hash_out);
+
+/* Reads and validates a Hip artifact in the reference's order (E-ARTIFACT-001 manifest, 004
+ * module files, 002 module hashes / artifact hash / id, 003 invariants: AMDGPU code objects,
+ * ir_hash, schema hash and parameters of the carried step), refuses code objects other than this
+ * library's (E-ARTIFACT-002) and a device other than the artifact's target (E-ARTIFACT-005,
+ * MSX_E_DEVICE), then loads its step and forward program as msx_load does (artifact::read_for_
+ * device, artifact.rs:340-346). */
+int msx_load_artifact(msx_ctx* ctx, const char* dir, uint64_t seed);
+
+/* The checks of msx_load_artifact without a device or a load; writes the artifact id to
+ * artifact_id_out[37] (may be NULL). */
+int msx_check_artifact(const char* dir, char* artifact_id_out);
 
 /* Writes the loaded step's current parameters (and, under AdamW, its moments as optimizer slots
  * "m" and "v") as a .msckpt v1 file recording `step` updates (crates/modelspec-runtime/src/train/

@@ -13,7 +13,8 @@ LIB_PATH = os.path.join(_HERE, "libmsx.so")
 CONFIGS = ("linear_regression", "mnist_mlp", "mlp_classifier", "transformer_block", "bert_tiny",
            "bert_cpu", "bert_micro", "block_micro", "mlp_micro")
 
-STATUS = {0: "ok", -1: "invalid", -2: "data", -3: "device", -4: "nonfinite", -5: "unsupported", -6: "checkpoint"}
+STATUS = {0: "ok", -1: "invalid", -2: "data", -3: "device", -4: "nonfinite", -5: "unsupported", -6: "checkpoint",
+          -7: "artifact"}
 
 
 class MsxError(RuntimeError):
@@ -77,6 +78,9 @@ def lib():
                                        ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
         L.msx_read_input.argtypes = [vp, i32, ctypes.c_char_p, vp, u64]
         L.msx_checkpoint_write.argtypes = [vp, ctypes.c_char_p, u64]
+        L.msx_write_artifact.argtypes = [vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]
+        L.msx_load_artifact.argtypes = [vp, ctypes.c_char_p, u64]
+        L.msx_check_artifact.argtypes = [ctypes.c_char_p, ctypes.c_char_p]
         L.msx_checkpoint_read.argtypes = [vp, ctypes.c_char_p, i32, ctypes.POINTER(u64)]
         L.msx_train_checkpointed.argtypes = [vp, ctypes.c_char_p, ctypes.c_char_p, c64, ctypes.c_char_p, u64,
                                              ctypes.c_char_p, vp, u64, vp, u64, ctypes.POINTER(u64)]
@@ -264,6 +268,16 @@ class Context:
                                       evals, cap, ctypes.byref(n), ctypes.byref(ts), ctypes.byref(es)))
         return losses, params, [(int(at[k]), evals[k].as_dict()) for k in range(n.value)]
 
+    def write_artifact(self, path, source_text=None):
+        """Writes the loaded step as a Hip artifact directory; returns the artifact hash."""
+        out = ctypes.create_string_buffer(65)
+        _check(lib().msx_write_artifact(self._h, str(path).encode(),
+                                        None if source_text is None else source_text.encode(), out))
+        return out.value.decode()
+
+    def load_artifact(self, path, seed):
+        _check(lib().msx_load_artifact(self._h, str(path).encode(), seed))
+
     def checkpoint_write(self, path, step):
         _check(lib().msx_checkpoint_write(self._h, str(path).encode(), step))
 
@@ -318,6 +332,13 @@ def write_packed(path, train, heldout, seq_len, vocabulary_size, dataset_id=DATA
     ho = np.ascontiguousarray(heldout, np.int32)
     _check(lib().msx_write_packed(str(path).encode(), tr.ctypes.data, tr.size, ho.ctypes.data, ho.size, seq_len,
                                   vocabulary_size, dataset_id.encode(), tokenizer_id.encode(), selection_rate))
+
+
+def check_artifact(path):
+    """Validates a Hip artifact directory (no device); returns its artifact id."""
+    out = ctypes.create_string_buffer(37)
+    _check(lib().msx_check_artifact(str(path).encode(), out))
+    return out.value.decode()
 
 
 def param_shapes(step_ir):

@@ -11,6 +11,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libmsx.so")
+CODE_OBJECTS = os.path.join(HERE, "kernels")
 SOURCES = [
     "capi.cpp",
     "host/ir.cpp",
@@ -21,6 +22,7 @@ SOURCES = [
     "host/json.cpp",
     "host/packed.cpp",
     "host/checkpoint.cpp",
+    "host/artifact.cpp",
     "hip/runtime.cpp",
     "hip/kernels.hip",
     "hip/gemm.hip",
@@ -50,6 +52,16 @@ def build(verbose=False):
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
         objs.append(obj)
+    # The gfx950 code object of each kernel source, beside the library: what an artifact of the
+    # library's plans records and hashes (host/artifact.cpp).
+    os.makedirs(CODE_OBJECTS, exist_ok=True)
+    for src in SOURCES:
+        if not src.endswith(".hip"):
+            continue
+        out = os.path.join(CODE_OBJECTS, os.path.basename(src).replace(".hip", ".hsaco"))
+        cmd = ([HIPCC] + [f for f in FLAGS if f not in ("-shared", "-fPIC")] +
+               ["--genco", "--offload-device-only", "--no-gpu-bundle-output", os.path.join(CSRC, src), "-o", out])
+        procs.append((src + " (code object)", subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
     failed = []
     for src, p in procs:
         out, _ = p.communicate()

@@ -1,4 +1,6 @@
 // The C ABI of libmsx.so (include/msx.h): status codes, no exception across the boundary.
+#include <dlfcn.h>
+
 #include <cstdlib>
 #include <cstring>
 #include <memory>
@@ -6,6 +8,7 @@
 #include "../../include/msx.h"
 #include "hip/runtime.h"
 #include "host/models.h"
+#include "host/artifact.h"
 #include "host/checkpoint.h"
 #include "host/packed.h"
 #include "host/runner.h"
@@ -32,6 +35,8 @@ int guarded(F&& f) {
     return fail(MSX_E_DATA, e.what());
   } catch (const msx::CheckpointError& e) {
     return fail(MSX_E_CHECKPOINT, e.what());
+  } catch (const msx::ArtifactError& e) {
+    return fail(e.code == "E-ARTIFACT-005" ? MSX_E_DEVICE : MSX_E_ARTIFACT, e.what());
   } catch (const msx::IrError& e) {
     std::string w = e.what();
     if (w.find("E-DATA-") != std::string::npos || w.find("key mask") != std::string::npos ||
@@ -428,6 +433,70 @@ int msx_train_packed(msx_ctx* ctx, const char* config, const char* dir, int64_t 
                              params_len, eval_steps, evals, evals_len, n_evals, train_seconds, eval_seconds);
     ctx->session.reset();  // its feed pointed at the run's corpus
     return rc;
+  });
+}
+
+namespace {
+// The directory of this library's gfx950 code objects: kernels/ beside libmsx.so.
+std::string code_object_dir() {
+  Dl_info info{};
+  if (!dladdr(reinterpret_cast<void*>(&msx_device_count), &info) || !info.dli_fname)
+    throw msx::IrError("cannot locate libmsx.so");
+  std::string lib = info.dli_fname;
+  const size_t slash = lib.find_last_of('/');
+  return (slash == std::string::npos ? std::string(".") : lib.substr(0, slash)) + "/kernels";
+}
+}  // namespace
+
+int msx_write_artifact(msx_ctx* ctx, const char* dir, const char* source_text, char* hash_out) {
+  return guarded([&] {
+    if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
+    if (!dir) return fail(MSX_E_INVALID, "null directory");
+    msx::ArtifactSource src;
+    src.step_ir = msx::print_step(ctx->step);
+    src.forward_ir = msx::print_program(ctx->forward);
+    src.source_text = source_text ? source_text : msx::print_program(ctx->forward);
+    for (size_t k = 0; k < ctx->forward.outputs.size(); ++k)
+      if (ctx->forward.outputs[k] == ctx->prediction) src.prediction_output = uint32_t(k);
+    src.param_offsets = ctx->session->param_offsets();
+    src.param_floats = ctx->session->param_floats();
+    for (auto& l : ctx->session->plan(true)) src.plan.push_back({l.what, l.flop, l.bytes});
+    for (auto& l : ctx->session->plan(false)) src.forward_plan.push_back({l.what, l.flop, l.bytes});
+    src.code_objects = code_object_dir();
+    src.compiler_version = "modelspec-hip 0.1 (hipcc, gfx950)";
+    const std::string h = msx::write_artifact(dir, src);
+    if (hash_out) std::memcpy(hash_out, h.c_str(), h.size() + 1);
+    return MSX_OK;
+  });
+}
+
+int msx_load_artifact(msx_ctx* ctx, const char* dir, uint64_t seed) {
+  return guarded([&] {
+    if (!dir) return fail(MSX_E_INVALID, "null directory");
+    msx::HipArtifact a = msx::read_artifact(dir, code_object_dir());
+    hipDeviceProp_t prop{};
+    msx::hip_check(hipGetDeviceProperties(&prop, ctx->device), "hipGetDeviceProperties");
+    const std::string arch = prop.gcnArchName;
+    if (arch.substr(0, a.target.size()) != a.target || (arch.size() > a.target.size() && arch[a.target.size()] != ':'))
+      throw msx::ArtifactError("E-ARTIFACT-005", "the artifact's code objects are for " + a.target + "; the device is " + arch);
+    ctx->session.reset();
+    ctx->step = msx::parse_step(a.step_ir);
+    if (!ctx->step.has_optimizer) return fail(MSX_E_INVALID, "the artifact's step has no optimizer");
+    ctx->forward = msx::parse_program(a.forward_ir);
+    if (a.prediction_output >= ctx->forward.outputs.size()) return fail(MSX_E_INVALID, "no such forward output");
+    ctx->prediction = ctx->forward.outputs[a.prediction_output];
+    ctx->seed = seed;
+    ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, seed, ctx->prediction, ctx->corpus.get());
+    return MSX_OK;
+  });
+}
+
+int msx_check_artifact(const char* dir, char* artifact_id_out) {
+  return guarded([&] {
+    if (!dir) return fail(MSX_E_INVALID, "null directory");
+    msx::HipArtifact a = msx::read_artifact(dir, code_object_dir());
+    if (artifact_id_out) std::memcpy(artifact_id_out, a.artifact_id.c_str(), a.artifact_id.size() + 1);
+    return MSX_OK;
   });
 }
 

@@ -1332,6 +1332,11 @@ Session::~Session() {
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
+const std::vector<Launch>& Session::plan(bool step) const {
+  if (step && !step_exec_) throw IrError("no training step is loaded");
+  return step ? step_exec_->launches() : fwd_exec_->launches();
+}
+
 size_t Session::launches_per_step() const { return step_exec_ ? step_exec_->launches().size() : 0; }
 
 const void* Session::forward_value(uint32_t id) const { return fwd_exec_->value(id); }

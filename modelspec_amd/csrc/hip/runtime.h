@@ -94,6 +94,11 @@ class Session : public Engine {
   // A value of the step program (its inputs among them) as the last step left it.
   const void* step_value(uint32_t id) const;
   void load_params(const std::vector<std::vector<float>>& values) { upload_params(values); }
+  // The launch plan of the step (or of the forward program): what each launch completes and its
+  // algorithmic FLOP and bytes.
+  const std::vector<Launch>& plan(bool step) const;
+  const std::vector<int64_t>& param_offsets() const { return offset_; }
+  int64_t param_floats() const { return total_; }
   // Sequences per step of the bound corpus (0 without one).
   uint64_t corpus_batch() const { return corpus_batch_; }
   // Throws the E-DATA-012 refusal a device gather recorded (after a wait on the stream).

@@ -183,6 +183,16 @@ std::string json_f64(double v) {
   return neg ? "-" + out : out;
 }
 
+namespace json {
+Value real(double v) {
+  Value x;
+  x.kind = Value::Number;
+  x.text = json_f64(v);
+  x.num = v;
+  return x;
+}
+}  // namespace json
+
 bool CheckpointOptimizer::operator==(const CheckpointOptimizer& o) const {
   if (adamw != o.adamw || learning_rate != o.learning_rate) return false;
   return !adamw || (weight_decay == o.weight_decay && beta1 == o.beta1 && beta2 == o.beta2 && epsilon == o.epsilon &&

@@ -232,4 +232,94 @@ std::string quote(const std::string& s) {
   return out + "\"";
 }
 
+Value uint(uint64_t v) {
+  Value x;
+  x.kind = Value::Number;
+  x.text = std::to_string(v);
+  x.num = double(v);
+  return x;
+}
+
+Value real(double v);  // defined with the checkpoint's f64 text
+
+Value str(const std::string& s) {
+  Value x;
+  x.kind = Value::String;
+  x.text = s;
+  return x;
+}
+
+Value boolean(bool b) {
+  Value x;
+  x.kind = Value::Bool;
+  x.b = b;
+  return x;
+}
+
+Value array() {
+  Value x;
+  x.kind = Value::Array;
+  return x;
+}
+
+Value object() {
+  Value x;
+  x.kind = Value::Object;
+  return x;
+}
+
+Value& push(Value& a, Value v) {
+  a.items.push_back(std::move(v));
+  return a.items.back();
+}
+
+Value& put(Value& o, const std::string& key, Value v) {
+  o.fields.emplace_back(key, std::move(v));
+  return o.fields.back().second;
+}
+
+namespace {
+void dump(const Value& v, int depth, std::string& out) {
+  const std::string pad(size_t(2 * (depth + 1)), ' '), close(size_t(2 * depth), ' ');
+  switch (v.kind) {
+    case Value::Null: out += "null"; break;
+    case Value::Bool: out += v.b ? "true" : "false"; break;
+    case Value::Number: out += v.text; break;
+    case Value::String: out += quote(v.text); break;
+    case Value::Array:
+      if (v.items.empty()) {
+        out += "[]";
+        break;
+      }
+      out += "[\n";
+      for (size_t i = 0; i < v.items.size(); ++i) {
+        out += pad;
+        dump(v.items[i], depth + 1, out);
+        out += i + 1 < v.items.size() ? ",\n" : "\n";
+      }
+      out += close + "]";
+      break;
+    case Value::Object:
+      if (v.fields.empty()) {
+        out += "{}";
+        break;
+      }
+      out += "{\n";
+      for (size_t i = 0; i < v.fields.size(); ++i) {
+        out += pad + quote(v.fields[i].first) + ": ";
+        dump(v.fields[i].second, depth + 1, out);
+        out += i + 1 < v.fields.size() ? ",\n" : "\n";
+      }
+      out += close + "}";
+      break;
+  }
+}
+}  // namespace
+
+std::string dump_pretty(const Value& v) {
+  std::string out;
+  dump(v, 0, out);
+  return out;
+}
+
 }  // namespace msx::json

@@ -30,6 +30,20 @@ struct Value {
 // Parses `text`; throws std::runtime_error with the byte offset of the first error.
 Value parse(const std::string& text);
 
+// Builders: a number keeps the text it was made with.
+Value uint(uint64_t v);
+Value real(double v);  // serde_json's text of an f64
+Value str(const std::string& s);
+Value boolean(bool b);
+Value array();
+Value object();
+// Appends to an array / object; returns the added value.
+Value& push(Value& array, Value v);
+Value& put(Value& object, const std::string& key, Value v);
+
+// serde_json's pretty form: two-space indent, "key": value, empty containers as [] and {}.
+std::string dump_pretty(const Value& v);
+
 // `s` as a JSON string literal.
 std::string quote(const std::string& s);
 
