@@ -247,40 +247,75 @@ __device__ __forceinline__ void score_tiles(const float* R, const float (&xb)[D 
 #pragma unroll
     for (int u = 0; u < kU; ++u) acc[u] = mfma4(rr[u][4 * t], xb[t], acc[u]);
 }
+// Stages rows [0, rows) of one [., H] head slice into an LDS tile of row stride D + 4.
+template <int D>
+__device__ __forceinline__ void stage_one(float* X, const float* __restrict__ xs, int rows, int H) {
+  constexpr int DP = D + 4, Q = D / 4;
+  const int total = rows * Q;
+  for (int e0 = threadIdx.x; e0 < total; e0 += 8 * int(blockDim.x)) {
+    float4 xv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      int e = e0 + u * int(blockDim.x);
+      e = e < total ? e : total - 1;
+      xv[u] = *reinterpret_cast<const float4*>(xs + int64_t(e / Q) * H + (e % Q) * 4);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + u * int(blockDim.x);
+      if (e < total) {
+        float* xd = X + (e / Q) * DP + (e % Q) * 4;
+        xd[0] = xv[u].x; xd[1] = xv[u].y; xd[2] = xv[u].z; xd[3] = xv[u].w;
+      }
+    }
+  }
+}
+
+// The kernels below stream the other side of the attention (keys for the forward and dQ, queries
+// for dK/dV) through LDS `chunk` rows at a time, in ascending order, so a sequence of any length
+// fits; a sequence that fits one chunk is staged once. Every wave of a block takes part in the
+// staging; waves past the last row tile compute nothing.
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_fwd_mfma(const float* __restrict__ q, const float* __restrict__ k,
                                                        const float* __restrict__ v, const float* __restrict__ mask,
                                                        float* __restrict__ o, float* __restrict__ stats, int L, int S,
-                                                       int H, int heads, float scale) {
+                                                       int H, int heads, float scale, int chunk) {
   constexpr int DP = D + 4;
   extern __shared__ float sm[];
   float* Ks = sm;
-  float* Vs = sm + S * DP;
-  float* Ms = sm + 2 * S * DP;
+  float* Vs = sm + chunk * DP;
+  float* Ms = sm + 2 * chunk * DP;
   const int b = blockIdx.x / heads, head = blockIdx.x % heads;
   const int64_t kbase = int64_t(b) * S * H + head * D;
-  stage_pair<D>(Ks, Vs, k + kbase, v + kbase, S, H);
-  for (int j = threadIdx.x; j < S; j += blockDim.x) Ms[j] = mask[int64_t(b) * S + j];
-  __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int i0 = blockIdx.y * int(blockDim.x / 4) + wave * 16;
-  if (i0 >= L) return;
-  const int64_t qrow = (int64_t(b) * L + i0 + c) * H + head * D;
+  const bool active = i0 < L;
+  const bool single = S <= chunk;
+  const int64_t qrow = (int64_t(b) * L + (active ? i0 : 0) + c) * H + head * D;
   float qb[D / 4];
 #pragma unroll
   for (int t = 0; t < D / 4; ++t) qb[t] = q[qrow + 4 * t + g];
   // Pass 1: the maximum score of query i0 + c over the unmasked keys. kU key tiles at a time, so
   // that kU independent MFMA chains interleave.
-  const int nt = S / 16;
   float mx = -INFINITY;
-  for (int jt0 = 0; jt0 < nt; jt0 += kU) {
-    v4f acc[kU];
-    score_tiles<D>(Ks, qb, jt0, nt, c, g, acc);
+  for (int s0 = 0; s0 < S; s0 += chunk) {
+    const int n = S - s0 < chunk ? S - s0 : chunk;
+    __syncthreads();
+    if (single) stage_pair<D>(Ks, Vs, k + kbase, v + kbase, n, H);
+    else stage_one<D>(Ks, k + kbase + int64_t(s0) * H, n, H);
+    for (int j = threadIdx.x; j < n; j += blockDim.x) Ms[j] = mask[int64_t(b) * S + s0 + j];
+    __syncthreads();
+    if (!active) continue;
+    const int nt = n / 16;
+    for (int jt0 = 0; jt0 < nt; jt0 += kU) {
+      v4f acc[kU];
+      score_tiles<D>(Ks, qb, jt0, nt, c, g, acc);
 #pragma unroll
-    for (int u = 0; u < kU; ++u)
+      for (int u = 0; u < kU; ++u)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (jt0 + u < nt && Ms[(jt0 + u) * 16 + 4 * g + r] != 0.0f) mx = fmaxf(mx, acc[u][r] * scale);
+        for (int r = 0; r < 4; ++r)
+          if (jt0 + u < nt && Ms[(jt0 + u) * 16 + 4 * g + r] != 0.0f) mx = fmaxf(mx, acc[u][r] * scale);
+    }
   }
   mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
   mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -289,27 +324,39 @@ __global__ __launch_bounds__(256) void k_attn_fwd_mfma(const float* __restrict__
   v4f oacc[D / 16];
 #pragma unroll
   for (int ct = 0; ct < D / 16; ++ct) oacc[ct] = v4f{0, 0, 0, 0};
-  for (int jt0 = 0; jt0 < nt; jt0 += kU) {
-    v4f acc[kU];
-    score_tiles<D>(Ks, qb, jt0, nt, c, g, acc);
+  for (int s0 = 0; s0 < S; s0 += chunk) {
+    const int n = S - s0 < chunk ? S - s0 : chunk;
+    if (!single) {
+      __syncthreads();
+      stage_pair<D>(Ks, Vs, k + kbase + int64_t(s0) * H, v + kbase + int64_t(s0) * H, n, H);
+      for (int j = threadIdx.x; j < n; j += blockDim.x) Ms[j] = mask[int64_t(b) * S + s0 + j];
+      __syncthreads();
+    }
+    if (!active) continue;
+    const int nt = n / 16;
+    for (int jt0 = 0; jt0 < nt; jt0 += kU) {
+      v4f acc[kU];
+      score_tiles<D>(Ks, qb, jt0, nt, c, g, acc);
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      if (jt0 + u >= nt) break;
-      const int jt = jt0 + u;
-      float p[4];
+      for (int u = 0; u < kU; ++u) {
+        if (jt0 + u >= nt) break;
+        const int jt = jt0 + u;
+        float p[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[r] = Ms[jt * 16 + 4 * g + r] != 0.0f ? expf(acc[u][r] * scale - mx) : 0.0f;
-        total += p[r];
-      }
+        for (int r = 0; r < 4; ++r) {
+          p[r] = Ms[jt * 16 + 4 * g + r] != 0.0f ? expf(acc[u][r] * scale - mx) : 0.0f;
+          total += p[r];
+        }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float* vr = Vs + (jt * 16 + 4 * g + r) * DP + c;
+        for (int r = 0; r < 4; ++r) {
+          const float* vr = Vs + (jt * 16 + 4 * g + r) * DP + c;
 #pragma unroll
-        for (int ct = 0; ct < D / 16; ++ct) oacc[ct] = mfma4(p[r], vr[ct * 16], oacc[ct]);
+          for (int ct = 0; ct < D / 16; ++ct) oacc[ct] = mfma4(p[r], vr[ct * 16], oacc[ct]);
+        }
       }
     }
   }
+  if (!active) return;
   total += __shfl_xor(total, 16, 64);
   total += __shfl_xor(total, 32, 64);
 #pragma unroll
@@ -333,29 +380,26 @@ __global__ __launch_bounds__(256) void k_attn_bwd_q_mfma(const float* __restrict
                                                          const float* __restrict__ o, const float* __restrict__ stats,
                                                          const float* __restrict__ go, float* __restrict__ dq,
                                                          float* __restrict__ dsum, int L, int S, int H, int heads,
-                                                         float scale) {
+                                                         float scale, int chunk) {
   constexpr int DP = D + 4;
   extern __shared__ float sm[];
   float* Ks = sm;
-  float* Vs = sm + S * DP;
-  float* Ms = sm + 2 * S * DP;
+  float* Vs = sm + chunk * DP;
+  float* Ms = sm + 2 * chunk * DP;
   const int b = blockIdx.x / heads, head = blockIdx.x % heads;
   const int64_t kbase = int64_t(b) * S * H + head * D;
-  stage_pair<D>(Ks, Vs, k + kbase, v + kbase, S, H);
-  for (int j = threadIdx.x; j < S; j += blockDim.x) Ms[j] = mask[int64_t(b) * S + j];
-  __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int i0 = blockIdx.y * int(blockDim.x / 4) + wave * 16;
-  if (i0 >= L) return;
-  const int64_t row = (int64_t(b) * L + i0 + c) * H + head * D;
+  const bool active = i0 < L;
+  const int64_t row = (int64_t(b) * L + (active ? i0 : 0) + c) * H + head * D;
   // d_i for query i0 + c: lane group g sums columns [g D/4, (g + 1) D/4).
   float dd = 0.0f;
 #pragma unroll
   for (int t = 0; t < D / 4; ++t) dd = __builtin_fmaf(go[row + g * (D / 4) + t], o[row + g * (D / 4) + t], dd);
   dd += __shfl_xor(dd, 16, 64);
   dd += __shfl_xor(dd, 32, 64);
-  const int64_t srow = int64_t(blockIdx.x) * L + i0 + c;
-  if (g == 0) dsum[srow] = dd;
+  const int64_t srow = int64_t(blockIdx.x) * L + (active ? i0 : 0) + c;
+  if (active && g == 0) dsum[srow] = dd;
   const float mx = stats[2 * srow], total = stats[2 * srow + 1];
   float qb[D / 4], gb[D / 4];
 #pragma unroll
@@ -363,29 +407,38 @@ __global__ __launch_bounds__(256) void k_attn_bwd_q_mfma(const float* __restrict
   v4f acc[D / 16];
 #pragma unroll
   for (int ct = 0; ct < D / 16; ++ct) acc[ct] = v4f{0, 0, 0, 0};
-  const int nt = S / 16;
-  for (int jt0 = 0; jt0 < nt; jt0 += kU) {
-    v4f st[kU], dpt[kU];
-    score_tiles<D>(Ks, qb, jt0, nt, c, g, st);
-    score_tiles<D>(Vs, gb, jt0, nt, c, g, dpt);
+  for (int s0 = 0; s0 < S; s0 += chunk) {
+    const int n = S - s0 < chunk ? S - s0 : chunk;
+    __syncthreads();
+    stage_pair<D>(Ks, Vs, k + kbase + int64_t(s0) * H, v + kbase + int64_t(s0) * H, n, H);
+    for (int j = threadIdx.x; j < n; j += blockDim.x) Ms[j] = mask[int64_t(b) * S + s0 + j];
+    __syncthreads();
+    if (!active) continue;
+    const int nt = n / 16;
+    for (int jt0 = 0; jt0 < nt; jt0 += kU) {
+      v4f st[kU], dpt[kU];
+      score_tiles<D>(Ks, qb, jt0, nt, c, g, st);
+      score_tiles<D>(Vs, gb, jt0, nt, c, g, dpt);
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      if (jt0 + u >= nt) break;
-      const int jt = jt0 + u;
-      float ds[4];
+      for (int u = 0; u < kU; ++u) {
+        if (jt0 + u >= nt) break;
+        const int jt = jt0 + u;
+        float ds[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float p = Ms[jt * 16 + 4 * g + r] != 0.0f ? expf(st[u][r] * scale - mx) / total : 0.0f;
-        ds[r] = p * (dpt[u][r] - dd);
-      }
+        for (int r = 0; r < 4; ++r) {
+          float p = Ms[jt * 16 + 4 * g + r] != 0.0f ? expf(st[u][r] * scale - mx) / total : 0.0f;
+          ds[r] = p * (dpt[u][r] - dd);
+        }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float* kk = Ks + (jt * 16 + 4 * g + r) * DP + c;
+        for (int r = 0; r < 4; ++r) {
+          const float* kk = Ks + (jt * 16 + 4 * g + r) * DP + c;
 #pragma unroll
-        for (int ct = 0; ct < D / 16; ++ct) acc[ct] = mfma4(ds[r], kk[ct * 16], acc[ct]);
+          for (int ct = 0; ct < D / 16; ++ct) acc[ct] = mfma4(ds[r], kk[ct * 16], acc[ct]);
+        }
       }
     }
   }
+  if (!active) return;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int64_t orow = (int64_t(b) * L + i0 + 4 * g + r) * H + head * D;
@@ -401,61 +454,67 @@ __global__ __launch_bounds__(256) void k_attn_bwd_kv_mfma(const float* __restric
                                                           const float* __restrict__ stats, const float* __restrict__ go,
                                                           const float* __restrict__ dsum, float* __restrict__ dk,
                                                           float* __restrict__ dv, int L, int S, int H, int heads,
-                                                          float scale) {
+                                                          float scale, int chunk) {
   constexpr int DP = D + 4;
   extern __shared__ float sm[];
   float* Qs = sm;
-  float* Gs = sm + L * DP;
-  float* Sm = sm + 2 * L * DP;  // max, sum, d per query
+  float* Gs = sm + chunk * DP;
+  float* Sm = sm + 2 * chunk * DP;  // max, sum, d per query of the chunk
   const int b = blockIdx.x / heads, head = blockIdx.x % heads;
   const int64_t qbase = int64_t(b) * L * H + head * D;
-  stage_pair<D>(Qs, Gs, q + qbase, go + qbase, L, H);
-  for (int i = threadIdx.x; i < L; i += blockDim.x) {
-    const int64_t srow = int64_t(blockIdx.x) * L + i;
-    Sm[3 * i] = stats[2 * srow];
-    Sm[3 * i + 1] = stats[2 * srow + 1];
-    Sm[3 * i + 2] = dsum[srow];
-  }
-  __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int j0 = blockIdx.y * int(blockDim.x / 4) + wave * 16;
-  if (j0 >= S) return;
-  const int64_t krow = (int64_t(b) * S + j0 + c) * H + head * D;
-  const bool live = mask[int64_t(b) * S + j0 + c] != 0.0f;
+  const bool active = j0 < S;
+  const int64_t krow = (int64_t(b) * S + (active ? j0 : 0) + c) * H + head * D;
+  const bool live = mask[int64_t(b) * S + (active ? j0 : 0) + c] != 0.0f;
   float kb[D / 4], vb[D / 4];
 #pragma unroll
   for (int t = 0; t < D / 4; ++t) { kb[t] = k[krow + 4 * t + g]; vb[t] = v[krow + 4 * t + g]; }
   v4f dka[D / 16], dva[D / 16];
 #pragma unroll
   for (int ct = 0; ct < D / 16; ++ct) { dka[ct] = v4f{0, 0, 0, 0}; dva[ct] = v4f{0, 0, 0, 0}; }
-  const int nt = L / 16;
-  for (int it0 = 0; it0 < nt; it0 += kU) {
-    v4f s[kU], dp[kU];
-    score_tiles<D>(Qs, kb, it0, nt, c, g, s);
-    score_tiles<D>(Gs, vb, it0, nt, c, g, dp);
+  for (int l0 = 0; l0 < L; l0 += chunk) {
+    const int n = L - l0 < chunk ? L - l0 : chunk;
+    __syncthreads();
+    stage_pair<D>(Qs, Gs, q + qbase + int64_t(l0) * H, go + qbase + int64_t(l0) * H, n, H);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const int64_t srow = int64_t(blockIdx.x) * L + l0 + i;
+      Sm[3 * i] = stats[2 * srow];
+      Sm[3 * i + 1] = stats[2 * srow + 1];
+      Sm[3 * i + 2] = dsum[srow];
+    }
+    __syncthreads();
+    if (!active) continue;
+    const int nt = n / 16;
+    for (int it0 = 0; it0 < nt; it0 += kU) {
+      v4f s[kU], dp[kU];
+      score_tiles<D>(Qs, kb, it0, nt, c, g, s);
+      score_tiles<D>(Gs, vb, it0, nt, c, g, dp);
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      if (it0 + u >= nt) break;
-      const int it = it0 + u;
-      float p[4], ds[4];
+      for (int u = 0; u < kU; ++u) {
+        if (it0 + u >= nt) break;
+        const int it = it0 + u;
+        float p[4], ds[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float* st = Sm + 3 * (it * 16 + 4 * g + r);
-        p[r] = live ? expf(s[u][r] * scale - st[0]) / st[1] : 0.0f;
-        ds[r] = p[r] * (dp[u][r] - st[2]);
-      }
+        for (int r = 0; r < 4; ++r) {
+          const float* st = Sm + 3 * (it * 16 + 4 * g + r);
+          p[r] = live ? expf(s[u][r] * scale - st[0]) / st[1] : 0.0f;
+          ds[r] = p[r] * (dp[u][r] - st[2]);
+        }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float* gq = Gs + (it * 16 + 4 * g + r) * DP + c;
-        const float* qq = Qs + (it * 16 + 4 * g + r) * DP + c;
+        for (int r = 0; r < 4; ++r) {
+          const float* gq = Gs + (it * 16 + 4 * g + r) * DP + c;
+          const float* qq = Qs + (it * 16 + 4 * g + r) * DP + c;
 #pragma unroll
-        for (int ct = 0; ct < D / 16; ++ct) {
-          dva[ct] = mfma4(p[r], gq[ct * 16], dva[ct]);
-          dka[ct] = mfma4(ds[r], qq[ct * 16], dka[ct]);
+          for (int ct = 0; ct < D / 16; ++ct) {
+            dva[ct] = mfma4(p[r], gq[ct * 16], dva[ct]);
+            dka[ct] = mfma4(ds[r], qq[ct * 16], dka[ct]);
+          }
         }
       }
     }
   }
+  if (!active) return;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int j = j0 + 4 * g + r;
@@ -473,8 +532,15 @@ __global__ __launch_bounds__(256) void k_attn_bwd_kv_mfma(const float* __restric
 namespace {
 size_t scalar_fwd_lds(int64_t S, int64_t d) { return size_t((2 * S * d + S) * 4); }
 size_t scalar_bwd_lds(int64_t L, int64_t S, int64_t d) { return size_t((2 * L * d + 2 * S * d + S + 3 * L) * 4); }
-size_t mfma_fwd_lds(int64_t S, int64_t d) { return size_t((2 * S * (d + 4) + S) * 4); }
-size_t mfma_kv_lds(int64_t L, int64_t d) { return size_t((2 * L * (d + 4) + 3 * L) * 4); }
+// The rows an MFMA kernel streams through LDS at a time: the fewest chunks of at most what fits
+// (two tiles of row stride d + 4 and three floats a row), of equal size in whole 16-row tiles.
+int64_t mfma_chunk(int64_t n, int64_t d) {
+  const int64_t most = int64_t(kLdsMax) / ((2 * (d + 4) + 3) * 4) / 16 * 16;
+  const int64_t chunks = (n + most - 1) / most;
+  return ((n + chunks - 1) / chunks + 15) / 16 * 16;
+}
+size_t mfma_fwd_lds(int64_t chunk, int64_t d) { return size_t((2 * chunk * (d + 4) + chunk) * 4); }
+size_t mfma_kv_lds(int64_t chunk, int64_t d) { return size_t((2 * chunk * (d + 4) + 3 * chunk) * 4); }
 bool head_ok(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128; }
 
 template <template <int> class K>
@@ -482,7 +548,7 @@ struct ByD;
 }  // namespace
 
 bool attention_mfma(int64_t L, int64_t S, int64_t d) {
-  return head_ok(d) && L % 16 == 0 && S % 16 == 0 && mfma_fwd_lds(S, d) <= kLdsMax && mfma_kv_lds(L, d) <= kLdsMax;
+  return head_ok(d) && L % 16 == 0 && S % 16 == 0;
 }
 
 bool attention_fits(int64_t s, int64_t d) {
@@ -504,8 +570,9 @@ void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v
   float scale = 1.0f / sqrtf(float(d));
   if (attention_mfma(L, S, d)) {
     dim3 grid(unsigned(B * heads), unsigned((L + 16 * kWaves - 1) / (16 * kWaves)));
-    size_t lds = mfma_fwd_lds(S, d);
-#define GO(D) MSX_LAUNCH(k_attn_fwd_mfma<D>, grid, dim3(64 * kWaves), lds, s, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale)
+    const int chunk = int(mfma_chunk(S, d));
+    size_t lds = mfma_fwd_lds(chunk, d);
+#define GO(D) MSX_LAUNCH(k_attn_fwd_mfma<D>, grid, dim3(64 * kWaves), lds, s, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale, chunk)
     MSX_BY_D(d, GO)
 #undef GO
     return;
@@ -530,16 +597,18 @@ void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v
     if (dq || dk || dv) {
       // dQ (written only when asked) and the d_i the key pass reads.
       float* dq_out = dq;
-      size_t lq = mfma_fwd_lds(S, d);
-#define GO(D) MSX_LAUNCH(k_attn_bwd_q_mfma<D>, gq, dim3(64 * kWaves), lq, s, q, k, v, mask, o, stats, g, dq_out, dsum, int(L), int(S), int(H), int(heads), scale)
+      const int chunk = int(mfma_chunk(S, d));
+      size_t lq = mfma_fwd_lds(chunk, d);
+#define GO(D) MSX_LAUNCH(k_attn_bwd_q_mfma<D>, gq, dim3(64 * kWaves), lq, s, q, k, v, mask, o, stats, g, dq_out, dsum, int(L), int(S), int(H), int(heads), scale, chunk)
       if (dq_out) { MSX_BY_D(d, GO) }
 #undef GO
       if (!dq_out) refuse("the MFMA attention backward computes d_i in its dQ pass: dQ is required");
     }
     if (dk || dv) {
       dim3 gk(unsigned(B * heads), unsigned((S + 16 * kWaves - 1) / (16 * kWaves)));
-      size_t lk = mfma_kv_lds(L, d);
-#define GO(D) MSX_LAUNCH(k_attn_bwd_kv_mfma<D>, gk, dim3(64 * kWaves), lk, s, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale)
+      const int chunk = int(mfma_chunk(L, d));
+      size_t lk = mfma_kv_lds(chunk, d);
+#define GO(D) MSX_LAUNCH(k_attn_bwd_kv_mfma<D>, gk, dim3(64 * kWaves), lk, s, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale, chunk)
       MSX_BY_D(d, GO)
 #undef GO
     }

@@ -210,6 +210,8 @@ def test_gelu_relu_elementwise(ctx, oracle):
     (2, 16, 32, 2, False), (2, 16, 32, 2, True), (32, 128, 128, 2, False), (4, 128, 128, 2, True),
     (2, 24, 32, 2, True),  # S not a multiple of 16: the scalar path
     (2, 64, 256, 2, False),  # head width 128
+    (2, 512, 128, 2, True),  # keys and queries streamed through LDS in two chunks
+    (1, 320, 256, 2, False),  # head width 128 in three chunks, the last one shorter
 ])
 def test_attention_and_gradients(ctx, oracle, B, S, H, heads, masked):
     n = B * S * H
