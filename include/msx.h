@@ -91,6 +91,16 @@ int msx_forward(msx_ctx* ctx, const msx_tensor* inputs, uint32_t n_inputs, float
 
 int msx_stats(msx_ctx* ctx, msx_run_stats* out);
 
+/* The precision of the next msx_load: mixed != 0 runs every GEMM on the f16 MFMA (operands
+ * rounded to f16, f32 accumulation) with dynamic loss scaling: the loss gradient is seeded with the
+ * scale (starting at loss_scale), the optimizer unscales the gradients and skips a step whose
+ * gradients overflowed (halving the scale), and the scale doubles after scale_window clean steps.
+ * No counterpart in the reference, which trains in f32 only. */
+int msx_set_precision(msx_ctx* ctx, int32_t mixed, float loss_scale, uint32_t scale_window);
+/* The loaded step's current loss scale and the number of steps skipped for an overflow (1 and 0
+ * without mixed precision). */
+int msx_loss_scale(msx_ctx* ctx, float* scale, uint64_t* skipped);
+
 /* The device copy of input `name` of the step program (program 0) or the forward program (1) as
  * the last step or forward pass read it: what the host staged, or what the device drew from a
  * packed corpus. `count` elements of 4 bytes. For tests and inspection; no counterpart in the

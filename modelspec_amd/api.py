@@ -11,7 +11,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmsx.so")
 
 CONFIGS = ("linear_regression", "mnist_mlp", "mlp_classifier", "transformer_block", "bert_tiny",
-           "bert_cpu", "bert_micro", "block_micro", "mlp_micro")
+           "bert_cpu", "bert_micro", "block_micro", "mlp_micro", "bert_base", "bert_micro_mixed", "bert_mini_mixed")
 
 STATUS = {0: "ok", -1: "invalid", -2: "data", -3: "device", -4: "nonfinite", -5: "unsupported", -6: "checkpoint",
           -7: "artifact"}
@@ -77,6 +77,8 @@ def lib():
                                        ctypes.POINTER(HeldOutMetrics), u64, ctypes.POINTER(u64),
                                        ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
         L.msx_read_input.argtypes = [vp, i32, ctypes.c_char_p, vp, u64]
+        L.msx_set_precision.argtypes = [vp, i32, ctypes.c_float, u32]
+        L.msx_loss_scale.argtypes = [vp, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(u64)]
         L.msx_checkpoint_write.argtypes = [vp, ctypes.c_char_p, u64]
         L.msx_write_artifact.argtypes = [vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]
         L.msx_load_artifact.argtypes = [vp, ctypes.c_char_p, u64]
@@ -299,6 +301,16 @@ class Context:
                                             ctypes.byref(start)))
         return losses, params, start.value
 
+    def set_precision(self, mixed, loss_scale=65536.0, scale_window=2000):
+        """The precision of the next load (and per-op program): f16 MFMA GEMMs with loss scaling."""
+        _check(lib().msx_set_precision(self._h, int(mixed), loss_scale, scale_window))
+
+    def loss_scale(self):
+        """(current loss scale, steps skipped for an overflow) of the loaded step."""
+        sc, sk = ctypes.c_float(), ctypes.c_uint64()
+        _check(lib().msx_loss_scale(self._h, ctypes.byref(sc), ctypes.byref(sk)))
+        return sc.value, sk.value
+
     def stats(self):
         s = RunStats()
         _check(lib().msx_stats(self._h, ctypes.byref(s)))
@@ -358,7 +370,8 @@ def param_count(step_ir):
 
 
 _STEPS = {"linear_regression": 500, "mnist_mlp": 1800, "mlp_classifier": 1000, "mlp_micro": 20,
-          "transformer_block": 500, "block_micro": 20, "bert_tiny": 1000, "bert_cpu": 800, "bert_micro": 20}
+          "transformer_block": 500, "block_micro": 20, "bert_tiny": 1000, "bert_cpu": 800, "bert_micro": 20,
+          "bert_base": 200, "bert_micro_mixed": 20, "bert_mini_mixed": 20}
 
 
 def config_steps(name):

@@ -92,9 +92,16 @@ struct msx_ctx {
   std::unique_ptr<msx::PackedCorpus> corpus;
   msx::EpochOrders orders;
   uint64_t seed = 0;
+  msx::SessionOptions options;  // msx_set_precision, for the next msx_load
 };
 
 namespace {
+msx::SessionOptions config_options(const msx::Compiled& c) {
+  msx::SessionOptions o;
+  o.mixed = c.config.mixed;
+  return o;
+}
+
 // With a corpus loaded, a batch that names `data.step` (i32 [low, high] of the step) is the
 // corpus batch of that step: its sequences are drawn here and the device draws its rows.
 void corpus_draw(msx_ctx* ctx, msx::Batch& b, msx::SplitRole role) {
@@ -173,7 +180,7 @@ int msx_load(msx_ctx* ctx, const char* step_ir, const char* forward_ir, uint64_t
     ctx->prediction = ctx->forward.outputs[prediction_output];
     ctx->seed = seed;
     ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, seed,
-                                                  ctx->forward.outputs[prediction_output], ctx->corpus.get());
+                                                  ctx->forward.outputs[prediction_output], ctx->corpus.get(), ctx->options);
     return MSX_OK;
   });
 }
@@ -261,6 +268,27 @@ int msx_read_input(msx_ctx* ctx, int32_t program, const char* name, void* out, u
   });
 }
 
+int msx_set_precision(msx_ctx* ctx, int32_t mixed, float loss_scale, uint32_t scale_window) {
+  return guarded([&] {
+    if (!(loss_scale >= 1.0f) || !std::isfinite(loss_scale) || scale_window == 0)
+      return fail(MSX_E_INVALID, "a loss scale of at least 1 and a window of at least one step");
+    ctx->options.mixed = mixed != 0;
+    ctx->options.loss_scale = loss_scale;
+    ctx->options.scale_window = scale_window;
+    return MSX_OK;
+  });
+}
+
+int msx_loss_scale(msx_ctx* ctx, float* scale, uint64_t* skipped) {
+  return guarded([&] {
+    if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
+    msx::hk::LossScaleState st = ctx->session->loss_scale();
+    if (scale) *scale = ctx->session->mixed() ? st.scale : 1.0f;
+    if (skipped) *skipped = ctx->session->mixed() ? st.skipped : 0;
+    return MSX_OK;
+  });
+}
+
 int msx_stats(msx_ctx* ctx, msx_run_stats* out) {
   return guarded([&] {
     if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
@@ -338,7 +366,8 @@ int train_run(msx_ctx* ctx, const char* config, int64_t steps, uint64_t eval_eve
   ctx->forward = c.forward;
   ctx->prediction = c.prediction;
   ctx->seed = c.config.seed;
-  ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction, corpus);
+  ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction, corpus,
+                                                config_options(c));
   // Each evaluation's metrics, finished with the host's weight sums as msx_evaluate does.
   struct Recording : msx::Engine {
     msx::Session& s;
@@ -486,7 +515,8 @@ int msx_load_artifact(msx_ctx* ctx, const char* dir, uint64_t seed) {
     if (a.prediction_output >= ctx->forward.outputs.size()) return fail(MSX_E_INVALID, "no such forward output");
     ctx->prediction = ctx->forward.outputs[a.prediction_output];
     ctx->seed = seed;
-    ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, seed, ctx->prediction, ctx->corpus.get());
+    ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, seed, ctx->prediction, ctx->corpus.get(),
+                                                  ctx->options);
     return MSX_OK;
   });
 }
@@ -543,7 +573,8 @@ int msx_train_checkpointed(msx_ctx* ctx, const char* config, const char* packed_
     ctx->prediction = c.prediction;
     ctx->seed = c.config.seed;
     ctx->session =
-        std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction, corpus.get());
+        std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction, corpus.get(),
+                                       config_options(c));
     msx::RunOptions o;
     o.corpus = corpus.get();
     o.resume = from.get();
@@ -576,7 +607,8 @@ int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t ma
     ctx->step = c.step;
     ctx->forward = c.forward;
     ctx->prediction = c.prediction;
-    ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction);
+    ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction, nullptr,
+                                                  config_options(c));
     msx::RunResult r = msx::run(c, *ctx->session, c.config.steps);
     if (losses_len < r.losses.size()) return fail(MSX_E_INVALID, "losses buffer too small");
     std::memcpy(losses, r.losses.data(), r.losses.size() * 4);
@@ -602,7 +634,8 @@ int msx_bench_config(msx_ctx* ctx, const char* config, int64_t masked_rows, uint
     ctx->step = c.step;
     ctx->forward = c.forward;
     ctx->prediction = c.prediction;
-    ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction);
+    ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction, nullptr,
+                                                  config_options(c));
     msx::Session& s = *ctx->session;
     msx::Feed feed(c);
     if (feed.needs_teacher())
@@ -660,7 +693,8 @@ int msx_prog_new(msx_ctx* ctx, const char* program_text, uint64_t seed, msx_prog
     msx::TrainingStep none;
     none.program = pr->program;
     none.loss = pr->program.outputs.at(0);
-    pr->session = std::make_unique<msx::Session>(ctx->device, none, pr->program, seed, pr->program.outputs.at(0));
+    pr->session = std::make_unique<msx::Session>(ctx->device, none, pr->program, seed, pr->program.outputs.at(0), nullptr,
+                                                 ctx->options);
     *out = pr.release();
     return MSX_OK;
   });

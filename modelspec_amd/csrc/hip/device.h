@@ -19,6 +19,8 @@ void note_kernel(const char* expr);
 
 namespace {
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 [[noreturn]] void bad(const std::string& what) { throw std::runtime_error("kernel launch refused: " + what); }
 

@@ -145,6 +145,21 @@ __device__ __forceinline__ void wide_store(float* S, int e, float4 v) {
     *reinterpret_cast<float4*>(S + k * L + r) = v;
   }
 }
+// The f16 K tiles of the mixed-precision GEMM: row r of the operand at S + r P, its K slice
+// contiguous (P halves a row), each f32 rounded to the nearest f16.
+template <bool KC, int R, int P, int WK>
+__device__ __forceinline__ void wide_store_h(_Float16* S, int e, float4 v) {
+  if (KC) {
+    const int r = e / (WK / 4), k = (e % (WK / 4)) * 4;
+    *reinterpret_cast<v4h*>(S + r * P + k) = v4h{_Float16(v.x), _Float16(v.y), _Float16(v.z), _Float16(v.w)};
+  } else {
+    const int k = e / (R / 4), r = (e % (R / 4)) * 4;
+    S[(r + 0) * P + k] = _Float16(v.x);
+    S[(r + 1) * P + k] = _Float16(v.y);
+    S[(r + 2) * P + k] = _Float16(v.z);
+    S[(r + 3) * P + k] = _Float16(v.w);
+  }
+}
 }  // namespace
 
 // The order a GEMM's tiles are handed to blocks: mt x nt tiles a split slice, `tiles` in all,
@@ -154,7 +169,10 @@ struct GemmOrder {
   bool m_fastest;
 };
 
-template <bool TA, bool TB, int WM, int WN, int WK, bool VA, bool VB>
+// H: the mixed-precision variant. The operands are rounded to f16 as they are staged into LDS
+// (rows of their K slice contiguous) and multiplied by v_mfma_f32_16x16x32_f16 with f32
+// accumulation; K tiles of 32; everything else (split-K, epilogues, output) as in f32.
+template <bool TA, bool TB, int WM, int WN, int WK, bool VA, bool VB, bool H = false>
 __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, const float* __restrict__ B,
                                                 float* __restrict__ C, GemmEpi epi, int64_t M,
                                                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
@@ -166,10 +184,14 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   // The K tiles (double-buffered), and afterwards the output tile on its way to memory.
   // Deep K tiles (WK >= 128, meant for K <= WK: one tile) are single-buffered.
   constexpr int NB = WK >= 128 ? 1 : 2;
-  __shared__ float smem[NB * WK * LA + NB * WK * LB];
-  static_assert(TM * LC <= NB * WK * LA + NB * WK * LB, "output tile exceeds the LDS of the K tiles");
+  constexpr int PH = WK + 8;  // f16 tile row: the K slice and 16 bytes of pad
+  constexpr int TILES = H ? (NB * (TM + TN) * PH + 1) / 2 : NB * WK * LA + NB * WK * LB;
+  static_assert(!H || WK % 32 == 0, "the f16 MFMA takes K 32 at a time");
+  __shared__ __align__(16) float smem[TILES > TM * LC ? TILES : TM * LC];
   float* const As0 = smem;                  // As(buf) = As0 + buf WK LA
   float* const Bs0 = smem + NB * WK * LA;   // Bs(buf) = Bs0 + buf WK LB
+  _Float16* const Ah0 = reinterpret_cast<_Float16*>(smem);  // Ah(buf) = Ah0 + buf TM PH
+  _Float16* const Bh0 = Ah0 + NB * TM * PH;                  // Bh(buf) = Bh0 + buf TN PH
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // The tile of this block: consecutive blocks go to the 8 XCDs in turn, so block b takes tile
   // (b mod 8) * per + b / 8 of the grouped order, and each XCD runs one contiguous run of it.
@@ -211,12 +233,21 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   int buf = 0;
   for (int64_t k0 = kbeg; k0 < kend; k0 += WK) {
     if (NB == 1 && k0 != kbeg) __syncthreads();  // the single buffer is free again
+    if constexpr (H) {
 #pragma unroll
-    for (int h = 0; h < HA; ++h)
-      if (tid + 256 * h < GA) wide_store<!TA, TM, LA, WK>(As0 + buf * (WK * LA), tid + 256 * h, ra[h]);
+      for (int h = 0; h < HA; ++h)
+        if (tid + 256 * h < GA) wide_store_h<!TA, TM, PH, WK>(Ah0 + buf * (TM * PH), tid + 256 * h, ra[h]);
 #pragma unroll
-    for (int h = 0; h < HB; ++h)
-      if (tid + 256 * h < GB) wide_store<TB, TN, LB, WK>(Bs0 + buf * (WK * LB), tid + 256 * h, rb[h]);
+      for (int h = 0; h < HB; ++h)
+        if (tid + 256 * h < GB) wide_store_h<TB, TN, PH, WK>(Bh0 + buf * (TN * PH), tid + 256 * h, rb[h]);
+    } else {
+#pragma unroll
+      for (int h = 0; h < HA; ++h)
+        if (tid + 256 * h < GA) wide_store<!TA, TM, LA, WK>(As0 + buf * (WK * LA), tid + 256 * h, ra[h]);
+#pragma unroll
+      for (int h = 0; h < HB; ++h)
+        if (tid + 256 * h < GB) wide_store<TB, TN, LB, WK>(Bs0 + buf * (WK * LB), tid + 256 * h, rb[h]);
+    }
     __syncthreads();
     if (k0 + WK < kend) {
 #pragma unroll
@@ -225,6 +256,24 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
 #pragma unroll
       for (int h = 0; h < HB; ++h)
         if (tid + 256 * h < GB) rb[h] = wide_load<TB, TN, WK, VB>(B, ldb, N, kend, n0, k0 + WK, tid + 256 * h);
+    }
+    if constexpr (H) {
+      const _Float16* ah = Ah0 + buf * (TM * PH) + (wm + (lane & 15)) * PH + 8 * (lane >> 4);
+      const _Float16* bh = Bh0 + buf * (TN * PH) + (wn + (lane & 15)) * PH + 8 * (lane >> 4);
+#pragma unroll
+      for (int kk = 0; kk < WK; kk += 32) {
+        v8h a[WM], b[WN];
+#pragma unroll
+        for (int i = 0; i < WM; ++i) a[i] = *reinterpret_cast<const v8h*>(ah + 16 * i * PH + kk);
+#pragma unroll
+        for (int j = 0; j < WN; ++j) b[j] = *reinterpret_cast<const v8h*>(bh + 16 * j * PH + kk);
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+          for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+      }
+      buf = NB == 2 ? buf ^ 1 : 0;
+      continue;
     }
     const float* as = As0 + buf * (WK * LA);
     const float* bs = Bs0 + buf * (WK * LB);
@@ -393,10 +442,31 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   if (plan.wm == 2) MSX_WIDE(TA, TB, 2, 2, 16);             \
   else if (plan.wn == 2) MSX_WIDE(TA, TB, 1, 2, 16);        \
   else MSX_WIDE(TA, TB, 1, 1, 32);
-  if (!g.ta && !g.tb) { MSX_WIDE_T(false, false) }
+  // The mixed-precision variants: the same tiles with f16 K tiles of 32.
+#define MSX_WIDE_HV(TA, TB, WM, WN, VA, VB)                                                                 \
+  MSX_LAUNCH((k_gemm_w<TA, TB, WM, WN, 32, VA, VB, true>), wgrid, dim3(256), 0, s, g.a, g.b, g.c, epi, g.m,  \
+             g.n, g.k, g.lda, g.ldb, g.ldc, chunk, ws, csum, g.sum_a, vo, order)
+#define MSX_WIDE_H(TA, TB, WM, WN)                                  \
+  if (va && vb) MSX_WIDE_HV(TA, TB, WM, WN, true, true);            \
+  else if (vb) MSX_WIDE_HV(TA, TB, WM, WN, false, true);            \
+  else MSX_WIDE_HV(TA, TB, WM, WN, false, false)
+#define MSX_WIDE_HT(TA, TB)                                 \
+  if (plan.wm == 2) MSX_WIDE_H(TA, TB, 2, 2);               \
+  else if (plan.wn == 2) MSX_WIDE_H(TA, TB, 1, 2);          \
+  else MSX_WIDE_H(TA, TB, 1, 1);
+  if (g.h16) {
+    if (g.colsum) bad("the mixed-precision GEMM takes no column sums");
+    if (!g.ta && !g.tb) { MSX_WIDE_HT(false, false) }
+    else if (g.ta && !g.tb) { MSX_WIDE_HT(true, false) }
+    else if (!g.ta && g.tb) { MSX_WIDE_HT(false, true) }
+    else { MSX_WIDE_HT(true, true) }
+  } else if (!g.ta && !g.tb) { MSX_WIDE_T(false, false) }
   else if (g.ta && !g.tb) { MSX_WIDE_T(true, false) }
   else if (!g.ta && g.tb) { MSX_WIDE_T(false, true) }
   else { MSX_WIDE_T(true, true) }
+#undef MSX_WIDE_HT
+#undef MSX_WIDE_H
+#undef MSX_WIDE_HV
 #undef MSX_WIDE_T
 #undef MSX_WIDE
 #undef MSX_WIDE_V

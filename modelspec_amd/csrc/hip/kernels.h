@@ -42,6 +42,8 @@ struct GemmArgs {
   // The operand's rows are zero from its contiguous extent up to its leading dimension (pad_c:
   // the output's rows are kept so).
   bool pad_a, pad_b, pad_c;
+  // Mixed precision: operands rounded to f16 for the f16 MFMA, f32 accumulation and output.
+  bool h16;
   // Epilogue after the bias: an activation (EPI_*: writing the pre-activation to pre_out when
   // non-null) or an activation gradient (pre_in the pre-activation), then addend + value.
   // addend, pre_in and pre_out share the output's leading dimension.
@@ -186,9 +188,20 @@ void mse(hipStream_t s, const float* a, const float* b, float* o, int64_t n);
 
 // The AdamW update of ir/training.rs:941-980 over one flat arena, in place.
 struct AdamWConsts { float beta1, rest1, beta2, rest2, eps, decay; };
+// Dynamic loss scaling of the mixed-precision step: the loss gradient is seeded with `scale`, the
+// optimizer multiplies each gradient by `inv` (exact: a power of two) and makes no update when
+// `overflow` is set; loss_scale_update then halves the scale on an overflow, doubles it after
+// `window` clean steps, and clears the flag.
+struct LossScaleState {
+  float scale, inv;
+  uint32_t good, overflow, skipped, window, pad0, pad1;
+};
+// ls may be null (no loss scaling).
 void adamw(hipStream_t s, float* p, const float* g, float* m, float* v, int64_t n, AdamWConsts k, const float* lr_t,
-           const float* c1, const float* c2);
-void sgd(hipStream_t s, float* p, const float* g, int64_t n, const float* lr);
+           const float* c1, const float* c2, const LossScaleState* ls = nullptr);
+void sgd(hipStream_t s, float* p, const float* g, int64_t n, const float* lr, const LossScaleState* ls = nullptr);
+void grad_check(hipStream_t s, const float* g, int64_t n, LossScaleState* ls);
+void loss_scale_update(hipStream_t s, LossScaleState* ls);
 
 void record_loss(hipStream_t s, const float* loss, float* losses, uint32_t* counter, uint32_t capacity);
 

@@ -1069,11 +1069,14 @@ void mse(hipStream_t s, const float* a, const float* b, float* o, int64_t n) {
 // ---------------------------------------------------------------------------------------------
 __global__ void k_adamw(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
                         float* __restrict__ v, int64_t n, AdamWConsts k, const float* __restrict__ lr_t,
-                        const float* __restrict__ c1, const float* __restrict__ c2) {
-  const float lr = lr_t[0], b1 = c1[0], b2 = c2[0];
+                        const float* __restrict__ c1, const float* __restrict__ c2,
+                        const LossScaleState* __restrict__ ls) {
+  // A step whose scaled gradients overflowed makes no update (the loss scale halves instead).
+  if (ls && ls->overflow) return;
+  const float lr = lr_t[0], b1 = c1[0], b2 = c2[0], inv = ls ? ls->inv : 1.0f;
   int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   for (; i < n; i += int64_t(gridDim.x) * blockDim.x) {
-    const float gi = g[i], pi = p[i];
+    const float gi = ls ? g[i] * inv : g[i], pi = p[i];
     const float m2 = k.beta1 * m[i] + k.rest1 * gi;
     const float v2 = k.beta2 * v[i] + (k.rest2 * gi) * gi;
     const float dir = (m2 * b1) / (sqrtf(v2 * b2) + k.eps);
@@ -1084,21 +1087,60 @@ __global__ void k_adamw(float* __restrict__ p, const float* __restrict__ g, floa
   }
 }
 void adamw(hipStream_t s, float* p, const float* g, float* m, float* v, int64_t n, AdamWConsts k, const float* lr_t,
-           const float* c1, const float* c2) {
+           const float* c1, const float* c2, const LossScaleState* ls) {
   if (n <= 0) return;
   MSX_LAUNCH(k_adamw, dim3(std::min<unsigned>(blocks_for(n, 256), 16384)), dim3(256), 0, s, p, g, m, v, n, k,
-                     lr_t, c1, c2);
+                     lr_t, c1, c2, ls);
 }
 
-__global__ void k_sgd(float* __restrict__ p, const float* __restrict__ g, int64_t n, const float* __restrict__ lr) {
-  const float r = lr[0];
+__global__ void k_sgd(float* __restrict__ p, const float* __restrict__ g, int64_t n, const float* __restrict__ lr,
+                      const LossScaleState* __restrict__ ls) {
+  if (ls && ls->overflow) return;
+  const float r = lr[0], inv = ls ? ls->inv : 1.0f;
   int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  for (; i < n; i += int64_t(gridDim.x) * blockDim.x) p[i] = p[i] - r * g[i];
+  for (; i < n; i += int64_t(gridDim.x) * blockDim.x) p[i] = p[i] - r * (ls ? g[i] * inv : g[i]);
 }
-void sgd(hipStream_t s, float* p, const float* g, int64_t n, const float* lr) {
+void sgd(hipStream_t s, float* p, const float* g, int64_t n, const float* lr, const LossScaleState* ls) {
   if (n <= 0) return;
-  MSX_LAUNCH(k_sgd, dim3(std::min<unsigned>(blocks_for(n, 256), 16384)), dim3(256), 0, s, p, g, n, lr);
+  MSX_LAUNCH(k_sgd, dim3(std::min<unsigned>(blocks_for(n, 256), 16384)), dim3(256), 0, s, p, g, n, lr, ls);
 }
+
+// Dynamic loss scaling: any non-finite scaled gradient marks the step as overflowed.
+__global__ __launch_bounds__(256) void k_grad_check(const float* __restrict__ g, int64_t n,
+                                                    LossScaleState* __restrict__ ls) {
+  bool bad = false;
+  const int64_t quads = n / 4;
+  const float4* g4 = reinterpret_cast<const float4*>(g);
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int64_t q = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; q < quads; q += stride) {
+    const float4 x = g4[q];
+    bad = bad || !isfinite(x.x) || !isfinite(x.y) || !isfinite(x.z) || !isfinite(x.w);
+  }
+  for (int64_t i = quads * 4 + int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    bad = bad || !isfinite(g[i]);
+  if (__any(bad) && (threadIdx.x & 63) == 0) ls->overflow = 1u;
+}
+// After the update: halve the scale on an overflow (and count the skipped step), double it after
+// `window` clean steps in a row; keep it in [1, 2^24].
+__global__ void k_loss_scale_update(LossScaleState* __restrict__ ls) {
+  if (threadIdx.x != 0) return;
+  if (ls->overflow) {
+    ls->scale = fmaxf(ls->scale * 0.5f, 1.0f);
+    ls->good = 0;
+    ls->skipped += 1;
+  } else if (++ls->good >= ls->window) {
+    ls->scale = fminf(ls->scale * 2.0f, 16777216.0f);
+    ls->good = 0;
+  }
+  ls->inv = 1.0f / ls->scale;
+  ls->overflow = 0;
+}
+void grad_check(hipStream_t s, const float* g, int64_t n, LossScaleState* ls) {
+  if (n <= 0) return;
+  if (reinterpret_cast<uintptr_t>(g) % 16) bad("grad_check needs 16-byte aligned gradients");
+  MSX_LAUNCH(k_grad_check, dim3(std::min<unsigned>(blocks_for(n / 4 + 1, 256), 4096)), dim3(256), 0, s, g, n, ls);
+}
+void loss_scale_update(hipStream_t s, LossScaleState* ls) { MSX_LAUNCH(k_loss_scale_update, dim3(1), dim3(64), 0, s, ls); }
 
 __global__ void k_record_loss(const float* __restrict__ loss, float* __restrict__ losses, uint32_t* __restrict__ counter,
                               uint32_t capacity) {

@@ -201,7 +201,7 @@ void Executor::build() {
   // is taken by that GEMM from its LDS tiles, when no reader of the sum comes before the GEMM.
   std::map<uint32_t, uint32_t> colsum_of;  // MatMul -> SumRows
   std::set<uint32_t> colsum_fused;
-  for (size_t k = 0; k < n; ++k) {
+  for (size_t k = 0; k < n && !s_.opt_.mixed; ++k) {
     if (!need[k] || p.nodes[k].op != Op::SumRows) continue;
     const uint32_t a = p.nodes[k].operands[0];
     for (auto c : consumers[p.pos.at(a)]) {
@@ -495,6 +495,13 @@ void Executor::build() {
         break;
       case Op::ParamRead: fixed_[x.id] = s_.param_ + s_.offset_[x.param]; break;
       case Op::Scalar:
+        // Under loss scaling the loss gradient's seed (the Scalar 1.0 of the loss subgraph) is
+        // the device's current loss scale.
+        if (is_step_ && s_.scaler_ && x.scalar == 1.0f && st.subgraphs.count(x.id) &&
+            st.subgraphs.at(x.id) == Subgraph::Loss) {
+          fixed_[x.id] = &s_.scaler_->scale;
+          break;
+        }
         token_[x.id] = arena_.reserve(4);
         constants[x.id] = x.scalar;
         break;
@@ -715,6 +722,7 @@ void Executor::build() {
         g.pad_a = pitch.count(asrc) != 0;
         g.pad_b = pitch.count(bsrc) != 0;
         g.pad_c = pitch.count(out_id) != 0;
+        g.h16 = s_.opt_.mixed;
         const int64_t cs_id = x.op == Op::MatMul && colsum_of.count(id) ? int64_t(colsum_of.at(id)) : -1;
         g.sum_a = swap;  // the column sums of B are the row sums of the swapped left operand
         int64_t bias_id = fused ? int64_t(o[1]) : -1;
@@ -1127,14 +1135,23 @@ void Executor::build() {
       st.adamw.constants(k);
       hk::AdamWConsts c{k[0], k[1], k[2], k[3], k[4], k[5]};
       uint32_t lr = *st.lr_t, c1 = *st.c1, c2 = *st.c2;
+      hk::LossScaleState* ls = s_.scaler_;
+      if (ls) {
+        pending.push_back({[=] { return Launch{"GradCheck", [=](hipStream_t s) { hk::grad_check(s, s_.grad_, nt, ls); }}; }});
+        pending.back().bytes = 4.0 * double(nt);
+      }
       pending.push_back({[=] {
-        return Launch{"AdamW", [=](hipStream_t s) { hk::adamw(s, s_.param_, s_.grad_, s_.m_, s_.v_, nt, c, F(lr), F(c1), F(c2)); }};
+        return Launch{"AdamW", [=](hipStream_t s) { hk::adamw(s, s_.param_, s_.grad_, s_.m_, s_.v_, nt, c, F(lr), F(c1), F(c2), ls); }};
       }});
       pending.back().bytes = 7.0 * 4.0 * double(nt);
+      if (ls) pending.push_back({[=] { return Launch{"LossScale", [=](hipStream_t s) { hk::loss_scale_update(s, ls); }}; }});
     } else if (st.rule == Rule::Sgd && !st.updates.empty()) {
       uint32_t rate = p.node(st.updates.begin()->second).operands[1];
       uint32_t lr_scalar = p.node(rate).operands[0];
-      pending.push_back({[=] { return Launch{"SGD", [=](hipStream_t s) { hk::sgd(s, s_.param_, s_.grad_, nt, F(lr_scalar)); }}; }});
+      hk::LossScaleState* ls = s_.scaler_;
+      if (ls) pending.push_back({[=] { return Launch{"GradCheck", [=](hipStream_t s) { hk::grad_check(s, s_.grad_, nt, ls); }}; }});
+      pending.push_back({[=] { return Launch{"SGD", [=](hipStream_t s) { hk::sgd(s, s_.param_, s_.grad_, nt, F(lr_scalar), ls); }}; }});
+      if (ls) pending.push_back({[=] { return Launch{"LossScale", [=](hipStream_t s) { hk::loss_scale_update(s, ls); }}; }});
     }
     loss_value = st.loss;
     uint32_t loss = st.loss;
@@ -1254,6 +1271,14 @@ bool Session::corpus_fed(const Program& p, const std::string& name) const {
   return name == kMaskedRowsInput || name.rfind(kMaskedLabelsPrefix, 0) == 0 || name.rfind(kMaskedWeightsPrefix, 0) == 0;
 }
 
+hk::LossScaleState Session::loss_scale() {
+  hk::LossScaleState out{};
+  if (!scaler_) return out;
+  sync();
+  hip_check(hipMemcpy(&out, scaler_, sizeof out, hipMemcpyDeviceToHost), "hipMemcpy (loss scale)");
+  return out;
+}
+
 void Session::check_data_error() {
   if (!corpus_) return;
   uint32_t e[4] = {};
@@ -1267,8 +1292,8 @@ void Session::check_data_error() {
 }
 
 Session::Session(int device, const TrainingStep& step, const Program& forward, uint64_t seed, uint32_t prediction,
-                 const PackedCorpus* corpus)
-    : device_(device), step_(step), forward_(forward), seed_(seed), prediction_(prediction) {
+                 const PackedCorpus* corpus, SessionOptions options)
+    : device_(device), step_(step), forward_(forward), seed_(seed), prediction_(prediction), opt_(options) {
   step_.program.reindex();
   forward_.reindex();
   hip_check(hipSetDevice(device), "hipSetDevice");
@@ -1315,6 +1340,12 @@ Session::Session(int device, const TrainingStep& step, const Program& forward, u
   v_ = base + 3 * total_;
   losses_dev_ = base + 4 * total_;
   counter_ = reinterpret_cast<uint32_t*>(base + 4 * total_ + loss_capacity_);
+  if (opt_.mixed) {
+    // The loss-scale state, in device memory for the whole run (read and written by the step).
+    hip_check(hipMalloc(&scaler_, sizeof(hk::LossScaleState)), "hipMalloc (loss scale)");
+    hk::LossScaleState init{opt_.loss_scale, 1.0f / opt_.loss_scale, 0, 0, 0, opt_.scale_window, 0, 0};
+    hip_check(hipMemcpy(scaler_, &init, sizeof init, hipMemcpyHostToDevice), "hipMemcpy (loss scale)");
+  }
   if (step_.has_optimizer) step_exec_ = std::make_unique<Executor>(*this, step_.program, true);
   fwd_exec_ = std::make_unique<Executor>(*this, forward_, false);
   stats_.device_bytes += floats * 4;
@@ -1327,6 +1358,7 @@ Session::~Session() {
   step_exec_.reset();
   fwd_exec_.reset();
   corpus_.reset();
+  if (scaler_) (void)hipFree(scaler_);
   if (state_mem_) (void)hipFree(state_mem_);
   if (eval_mem_) (void)hipFree(eval_mem_);
   if (stream_) (void)hipStreamDestroy(stream_);

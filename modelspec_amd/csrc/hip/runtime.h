@@ -56,13 +56,22 @@ struct RunStats {
 class Executor;
 
 // A loaded training run on one device.
+// How a session computes: `mixed` runs every GEMM on the f16 MFMA (operands rounded to f16, f32
+// accumulation, f32 values in HBM) with dynamic loss scaling of the gradients, starting at
+// `loss_scale` and doubling after `scale_window` steps without an overflow.
+struct SessionOptions {
+  bool mixed = false;
+  float loss_scale = 65536.0f;
+  uint32_t scale_window = 2000;
+};
+
 class Session : public Engine {
  public:
   // With `corpus`, the batch tensors of both programs (ids, positions, key_mask, labels, weights)
   // and the masked-row gather are drawn on the device from the corpus, resident in HBM; each
   // step then stages kDrawInput instead of its batch.
   Session(int device, const TrainingStep& step, const Program& forward, uint64_t seed, uint32_t prediction,
-          const PackedCorpus* corpus = nullptr);
+          const PackedCorpus* corpus = nullptr, SessionOptions options = SessionOptions());
   ~Session() override;
 
   void set_params(const std::vector<std::vector<float>>& values) override;
@@ -103,6 +112,9 @@ class Session : public Engine {
   uint64_t corpus_batch() const { return corpus_batch_; }
   // Throws the E-DATA-012 refusal a device gather recorded (after a wait on the stream).
   void check_data_error();
+  // The loss-scale state of a mixed-precision session (zeros otherwise), after every queued step.
+  hk::LossScaleState loss_scale();
+  bool mixed() const { return opt_.mixed; }
 
  private:
   friend class Executor;
@@ -112,6 +124,8 @@ class Session : public Engine {
   Program forward_;
   uint64_t seed_;
   uint32_t prediction_;
+  SessionOptions opt_;
+  hk::LossScaleState* scaler_ = nullptr;  // device memory, mixed precision only
   bool use_graph_ = true;
 
   // Parameter, gradient and moment arenas share offsets: element i of each is the same element

@@ -281,7 +281,7 @@ Compiled bert(const std::string& name, int64_t V, int64_t H, int64_t heads, int6
 
 std::vector<std::string> config_names() {
   return {"linear_regression", "mnist_mlp", "mlp_classifier", "transformer_block", "bert_tiny", "bert_cpu", "bert_micro",
-          "block_micro", "mlp_micro"};
+          "block_micro", "mlp_micro", "bert_base", "bert_micro_mixed", "bert_mini_mixed"};
 }
 
 Compiled compile_config(const std::string& name, int64_t masked_rows, int64_t steps_override) {
@@ -296,6 +296,20 @@ Compiled compile_config(const std::string& name, int64_t masked_rows, int64_t st
   else if (name == "bert_tiny") c = bert(name, 30522, 128, 2, 512, 32, 128, 2, 1e-4f, 100, 1000, masked_rows);
   else if (name == "bert_cpu") c = bert(name, 300, 32, 2, 64, 2, 16, 2, 3e-3f, 80, 800, masked_rows);
   else if (name == "bert_micro") c = bert(name, 300, 32, 2, 64, 8, 16, 2, 3e-3f, 4, 20, masked_rows);
+  else if (name == "bert_base") {
+    // BERT-base shape at seq 512, batch 32 (12 layers, hidden 768, 12 heads, FFN 3072), mixed
+    // precision, 200 steps with a 20-step warmup.
+    c = bert(name, 30522, 768, 12, 3072, 32, 512, 12, 1e-4f, 20, 200, masked_rows);
+    c.config.mixed = true;
+  } else if (name == "bert_micro_mixed") {
+    c = bert(name, 300, 32, 2, 64, 8, 16, 2, 3e-3f, 4, 20, masked_rows);
+    c.config.mixed = true;
+  } else if (name == "bert_mini_mixed") {
+    // A seq-512 BERT of two layers at hidden 256 (4 heads of 64), for tests of the mixed path at
+    // the sequence length of the BERT-base config.
+    c = bert(name, 1000, 256, 4, 1024, 4, 512, 2, 1e-3f, 4, 20, masked_rows);
+    c.config.mixed = true;
+  }
   else throw IrError("unknown config `" + name + "`");
   if (steps_override >= 0) {
     c.config.steps = steps(c.config.steps);

@@ -32,6 +32,9 @@ struct TrainConfig {
   uint64_t masked_rows = 0;  // masked-row gather capacity (0 = none)
   // names of the data inputs
   std::string x, y, ids, positions, key_mask, labels, weights;
+  // Mixed precision: GEMMs on the f16 MFMA with f32 accumulation and dynamic loss scaling (the
+  // BERT-base config); the step program itself is the f32 program.
+  bool mixed = false;
 };
 
 struct Compiled {

@@ -1,0 +1,104 @@
+"""Mixed precision on the MI355X (the BERT-base config's f16 MFMA with f32 accumulation and
+dynamic loss scaling). The reference trains in f32 only, so there is no reference oracle for this
+path: parity is pinned by what the arithmetic fixes and held against the f32 oracle at a stated
+looser tolerance.
+
+- A mixed GEMM equals the float64 product of its operands rounded to f16 (round to nearest even),
+  up to f32 accumulation: |g - c16| <= 1e-5 * sum |a16 b16| + 1e-30.
+- A mixed training run tracks the f32 oracle's run of the same program: every loss within
+  2e-2 |c| + 2e-3 (the f16 rounding of each GEMM operand, 2^-11 relative, through 20 AdamW steps).
+- Loss scaling: a step whose scaled gradients overflow changes no parameter and halves the scale."""
+import os
+
+import numpy as np
+import pytest
+
+from modelspec_amd import api
+from ops_lib import Prog, fast_values
+
+pytestmark = pytest.mark.gpu
+
+
+def f16(x):
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float64)
+
+
+@pytest.fixture
+def mixed(ctx):
+    ctx.set_precision(True)
+    yield ctx
+    ctx.set_precision(False)
+
+
+@pytest.mark.parametrize("m,k,n,ta,tb", [(128, 96, 80, False, False), (300, 770, 129, True, False),
+                                         (64, 4096, 128, False, True), (832, 128, 4001, True, True),
+                                         (33, 45, 17, False, False)])
+def test_a_mixed_gemm_is_the_product_of_f16_operands(mixed, m, k, n, ta, tb):
+    a = fast_values(21, m * k, 0.25).reshape((k, m) if ta else (m, k))
+    b = fast_values(22, k * n, 0.25).reshape((n, k) if tb else (k, n))
+    p = Prog()
+    ai, bi = p.input("a", a.shape), p.input("b", b.shape)
+    lhs = p.op("Transpose", [ai], (m, k)) if ta else ai
+    rhs = p.op("Transpose", [bi], (k, n)) if tb else bi
+    p.out(p.op("MatMul", [lhs, rhs], (m, n)))
+    prog = mixed.program(p.text())
+    prog.run({"a": a, "b": b})
+    got = prog.output(0, m * n).reshape(m, n).astype(np.float64)
+    A = f16(a.T if ta else a)
+    Bm = f16(b.T if tb else b)
+    want = A @ Bm
+    bound = 1e-5 * (np.abs(A) @ np.abs(Bm)) + 1e-30
+    assert np.all(np.abs(got - want) <= bound), float(np.max(np.abs(got - want) / bound))
+    # Against the f32 operands the error is the f16 rounding: 2^-11 of each operand's magnitude.
+    exact = (a.T if ta else a).astype(np.float64) @ (b.T if tb else b).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= 2.0 ** -10 * (np.abs(A) @ np.abs(Bm)) + 1e-6)
+
+
+def test_a_mixed_run_tracks_the_f32_oracle(ctx, oracle):
+    got_l, got_p, _ = ctx.train_config("bert_micro_mixed")
+    want_l, want_p, _ = oracle.train("bert_micro")
+    assert np.all(np.isfinite(got_l))
+    err = np.abs(got_l - want_l)
+    assert np.all(err <= 2e-2 * np.abs(want_l) + 2e-3), (got_l, want_l)
+    # Parameters: the bulk close to the f32 run (AdamW normalises each update, so an element with
+    # a near-zero gradient may move by up to lr per step either way).
+    close = np.abs(got_p - want_p) <= 1e-2 * np.abs(want_p) + 3e-3
+    assert close.mean() > 0.99, close.mean()
+    assert ctx.loss_scale() == (65536.0, 0)
+
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def test_the_seq_512_mixed_config_trains_and_tracks_the_f32_oracle(ctx):
+    # The oracle's f32 run of this config takes a minute on one core: its losses are a fixture
+    # written by tests/golden/make_oracle_losses.py.
+    print("bert_mini_mixed", flush=True)
+    got_l, _, _ = ctx.train_config("bert_mini_mixed", steps=2)
+    want_l = np.load(os.path.join(GOLDEN, "oracle_losses_bert_mini_mixed_2.npy"))
+    assert np.all(np.isfinite(got_l))
+    assert np.all(np.abs(got_l - want_l) <= 2e-2 * np.abs(want_l) + 2e-3), (got_l, want_l)
+    losses, _, _ = ctx.train_config("bert_mini_mixed")
+    assert np.all(np.isfinite(losses)) and losses[-1] < losses[0]
+
+
+def test_an_overflowing_step_is_skipped_and_halves_the_scale(ctx, oracle):
+    config = "bert_micro_mixed"
+    step_ir, fwd = api.compile_config(config)
+    ctx.load_packed(None)
+    ctx.set_precision(True, loss_scale=1e38)
+    try:
+        ctx.load(step_ir, fwd, 42, 1)
+    finally:
+        ctx.set_precision(False)
+    n = api.param_count(step_ir)
+    sizes = [int(np.prod(s)) for _, s in api.param_shapes(step_ir)]
+    init = oracle.init_params(config, n)
+    ctx.set_params(np.split(init, np.cumsum(sizes)[:-1]))
+    # The same batch three times: with no update in between, the three losses are one value.
+    losses = ctx.run_steps([oracle.step_inputs(config, 0, steps=20)] * 3)
+    after = np.concatenate([ctx.read_param(k, c) for k, c in enumerate(sizes)])
+    assert after.tobytes() == init.tobytes()
+    assert np.all(np.isfinite(losses)) and losses[0] == losses[1] == losses[2]
+    scale, skipped = ctx.loss_scale()
+    assert skipped == 3 and scale == np.float32(1e38) / 8
