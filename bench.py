@@ -1,4 +1,5 @@
-"""Benchmark of the BERT-tiny masked-LM training step on one MI355X.
+"""Benchmark of the BERT-tiny masked-LM training step on one MI355X;
+with `--config bert_base`, of the BERT-base mixed-precision step.
 
 One step = forward + backward + AdamW of BERT-tiny (2 layers, hidden 128, 2 heads, FFN 512,
 V = 30522, batch 32, seq 128, dropout 0.1, the masked-row gather of 832 rows) on synthetic Zipf
@@ -10,6 +11,12 @@ Prints one JSON line: the median ms/step (the metric), tokens/s, the roofline fr
 dominant kernel (algorithmic FLOP or bytes per launch over its mean launch time, timed with HIP
 events on the run's stream), and the CPU oracle (a single-threaded restatement of the reference
 interpreter) timed on a bounded sample of the same step on this host.
+
+BERT-base (12 layers, H 768, 12 heads, FFN 3072, V 30522, batch 32, seq 512) runs its GEMMs as f16
+MFMA with f32 accumulation, f32 master weights and activations, and dynamic loss scaling from
+2^16; its GEMM launches are priced against the f16 MFMA peak, attention (f32 MFMA) against the
+f32 one. One oracle step of it is ~10^13 flop of scalar code (hours), so that line carries no CPU
+baseline.
 """
 import argparse
 import json
@@ -23,17 +30,32 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM = 8.0e12          # bytes/s, MI355X
 PEAK_FP32_MFMA = 157.3e12  # flop/s, dense
-CONFIG = "bert_tiny"
-TOKENS = 32 * 128
+PEAK_FP16_MFMA = 2.5e15    # flop/s, dense
+WORKLOADS = {
+    "bert_tiny": {
+        "metric": "BERT-tiny b32 s128 train ms/step (median) + per-kernel % of MFMA/HBM roofline",
+        "tokens": 32 * 128, "dtype": "f32", "mixed": False,
+        "config": {"workload": "bert_tiny masked-LM train step (fwd + bwd + AdamW), 2 layers, H 128, 2 heads, "
+                               "FFN 512, V 30522, dropout 0.1, masked-row gather 832",
+                   "global_batch": 32, "seq_len": 128, "parallelism": "single-gpu"}},
+    "bert_base": {
+        "metric": "BERT-base b32 s512 mixed-precision train ms/step (median) + per-kernel % of MFMA/HBM roofline",
+        "tokens": 32 * 512, "dtype": "f16 MFMA / f32 accumulate, f32 master weights", "mixed": True,
+        "config": {"workload": "bert_base masked-LM train step (fwd + bwd + AdamW, dynamic loss scale from 2^16), "
+                               "12 layers, H 768, 12 heads, FFN 3072, V 30522, dropout 0.1, masked-row gather 15%",
+                   "global_batch": 32, "seq_len": 512, "parallelism": "single-gpu"}},
+}
 
-def roofline(rows):
-    """The launch with the largest mean time, and every launch's fraction of its roofline."""
+def roofline(rows, mixed=False):
+    """The launch with the largest mean time, and every launch's fraction of its roofline. Under
+    mixed precision a GEMM's peak is the f16 MFMA one; attention stays f32 MFMA."""
     table = []
     for what, ms, flop, nbytes, kernels in rows:
         if ms <= 0:
             continue
         if flop > 0:
-            achieved, peak, unit, bound = flop / (ms * 1e-3), PEAK_FP32_MFMA, "TFLOP/s", "mfma"
+            peak = PEAK_FP16_MFMA if mixed and "attn" not in kernels else PEAK_FP32_MFMA
+            achieved, unit, bound = flop / (ms * 1e-3), "TFLOP/s", "mfma"
             achieved, peak = achieved / 1e12, peak / 1e12
         else:
             achieved, peak, unit, bound = nbytes / (ms * 1e-3), PEAK_HBM, "GB/s", "hbm"
@@ -75,16 +97,16 @@ def copy_once(ctx, mib):
         prog.close()
 
 
-def cpu_baseline(steps):
+def cpu_baseline(steps, config="bert_tiny"):
     """The CPU oracle on `steps` steps of the same config, single-threaded."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib
     o = oracle_lib.Oracle()
     t0 = time.time()
-    s = o.seconds_per_step(CONFIG, steps)
+    s = o.seconds_per_step(config, steps)
     wall = time.time() - t0
     return {"value": s * 1e3, "unit": "ms/step", "cores": 1, "kind": "port",
-            "sample": f"{steps} training steps of {CONFIG} (b32 s128, V 30522, masked rows 832) on the "
+            "sample": f"{steps} training steps of {config} (b32 s128, V 30522, masked rows 832) on the "
                       f"single-threaded C++ oracle, {wall:.1f} s of CPU work, after input generation",
             "cpu": cpu_model(), "nproc": os.cpu_count()}
 
@@ -103,6 +125,7 @@ def cpu_model():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--config", choices=sorted(WORKLOADS), default="bert_tiny")
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--profile-reps", type=int, default=5)
@@ -119,12 +142,13 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    w = WORKLOADS[args.config]
     from modelspec_amd import api
     ctx = api.Context(0)
-    mean_ms, per_step, last_loss, rows = api.bench_config(ctx, CONFIG, args.warmup, args.steps,
+    mean_ms, per_step, last_loss, rows = api.bench_config(ctx, args.config, args.warmup, args.steps,
                                                           profile_reps=args.profile_reps)
     median_ms = statistics.median(per_step)
-    table = roofline(rows)
+    table = roofline(rows, w["mixed"])
     top = table[0]
     if args.launches:
         with open(args.launches, "w") as f:
@@ -138,13 +162,14 @@ def main():
         first += len(kernels.split("+")) if kernels else 0
     dispatches = {"step_dispatches": sum(len(r[4].split("+")) if r[4] else 0 for r in rows), "first": first,
                   "count": len(top["kernel"].split("+")) if top["kernel"] else 0}
-    traffic = measured_traffic(top["launch"])
+    traffic = measured_traffic(top["launch"]) if args.config == "bert_tiny" else None
     stats = ctx.stats()
+    ctx_scale = list(ctx.loss_scale()) if w["mixed"] else None
     if args.copy_calibration > 0:
         copy_once(ctx, args.copy_calibration)
     ctx.close()
     out = {
-        "metric": "BERT-tiny b32 s128 train ms/step (median) + per-kernel % of MFMA/HBM roofline",
+        "metric": w["metric"],
         "value": round(median_ms, 4),
         "unit": "ms/step",
         "n_gpus": 1,
@@ -152,15 +177,13 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(median_ms, 4),
         "mean_ms_per_step": round(mean_ms, 4),
-        "tokens_per_s": round(TOKENS / (median_ms * 1e-3), 1),
+        "tokens_per_s": round(w["tokens"] / (median_ms * 1e-3), 1),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": w["dtype"],
         "data": "synthetic: Zipf(1.1) token ids, BERT 80/10/10 masking at 0.15, random-init (xavier) weights",
-        "config": {"workload": "bert_tiny masked-LM train step (fwd + bwd + AdamW), 2 layers, H 128, 2 heads, "
-                               "FFN 512, V 30522, dropout 0.1, masked-row gather 832",
-                   "global_batch": 32, "seq_len": 128, "parallelism": "single-gpu"},
+        "config": w["config"],
         "last_loss": last_loss,
         "kernels_per_step": stats["kernels_per_step"],
         "roofline": {"bound": top["bound"], "achieved": round(top["achieved"], 2), "peak": top["peak"],
@@ -172,7 +195,9 @@ def main():
                          if k in ("launch", "ms", "bound", "frac", "kernel")} for r in table[:12]],
         "profiled_step_ms": round(sum(r[1] for r in rows), 4),
     }
-    if not args.no_cpu:
+    if w["mixed"]:
+        out["loss_scale"] = ctx_scale
+    if not args.no_cpu and args.config == "bert_tiny":
         out["cpu_baseline"] = cpu_baseline(args.cpu_steps)
     print(json.dumps(out), flush=True)
 

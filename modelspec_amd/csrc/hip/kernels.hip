@@ -127,7 +127,10 @@ __global__ __launch_bounds__(256) void k_column_partial(const float* __restrict_
 int64_t column_partial_chunks(int64_t rows, int64_t h) {
   const int64_t tiles = (h + 255) / 256;
   const int64_t want = std::max<int64_t>(1, 512 / tiles);  // about 512 blocks
-  return std::max<int64_t>(1, std::min<int64_t>(want, (rows + 15) / 16));
+  const int64_t chunks = std::max<int64_t>(1, std::min<int64_t>(want, (rows + 15) / 16));
+  // The chunks that rows of ceil(rows / chunks) each make: no empty last chunk.
+  const int64_t per = (rows + chunks - 1) / chunks;
+  return std::max<int64_t>(1, (rows + per - 1) / per);
 }
 void column_partial(hipStream_t s, const float* x, float* partial, int64_t rows, int64_t h) {
   if (rows <= 0 || h <= 0) return;

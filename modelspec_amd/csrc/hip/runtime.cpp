@@ -468,6 +468,17 @@ void Executor::build() {
     }
     if (readers) pitch[x.id] = (cols + 63) / 64 * 64;
   }
+  // The cross-entropy kernels walk the logits and their gradient with one pitch: both padded or
+  // neither (the gradient stays unpadded when a reader of it takes no leading dimension, as the
+  // unfused bias column sum does under mixed precision).
+  for (size_t k = 0; k < n; ++k) {
+    const Node& x = p.nodes[k];
+    if (!need[k] || x.op != Op::CrossEntropyGrad) continue;
+    if (pitch.count(x.id) != pitch.count(x.operands[0])) {
+      pitch.erase(x.id);
+      pitch.erase(x.operands[0]);
+    }
+  }
   auto ld_of = [&](uint32_t v) {
     auto it = pitch.find(v);
     return it != pitch.end() ? it->second : p.node(v).ty.shape.back();

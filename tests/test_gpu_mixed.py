@@ -102,3 +102,15 @@ def test_an_overflowing_step_is_skipped_and_halves_the_scale(ctx, oracle):
     assert np.all(np.isfinite(losses)) and losses[0] == losses[1] == losses[2]
     scale, skipped = ctx.loss_scale()
     assert skipped == 3 and scale == np.float32(1e38) / 8
+
+
+def test_the_bert_base_config_takes_two_steps(ctx):
+    """BERT-base (12 layers, H 768, V 30522, batch 32, seq 512) at its full shape: no oracle run
+    finishes at this size, so the check is what initialisation fixes. With xavier weights the first
+    loss is within 3 nats of ln V (logits of order one). The step after it is finite and the scale
+    has not overflowed."""
+    print("bert_base", flush=True)
+    losses, _, _ = ctx.train_config("bert_base", steps=2)
+    assert np.all(np.isfinite(losses)), losses
+    assert abs(losses[0] - np.log(30522)) < 3.0, losses
+    assert ctx.loss_scale() == (65536.0, 0)

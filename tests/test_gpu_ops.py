@@ -71,6 +71,17 @@ def test_weight_gradient_gemm_takes_the_bias_gradient(ctx, oracle, rows, m, n):
     assert within(gb, wb, np.abs(dy).astype(np.float64).sum(0))[0]
 
 
+@pytest.mark.parametrize("rows,h", [(16384, 768), (16384, 3072), (2458, 30522), (33, 5)])
+def test_column_sums_of_a_tall_matrix(ctx, oracle, rows, h):
+    """SumRows on its own (no GEMM to fuse into): partial column sums over row chunks, then the
+    chunk sums. 16384 x 768 is a shape where the requested chunk count leaves an empty last chunk."""
+    x = fast_values(35, rows * h).reshape(rows, h)
+    p = Prog()
+    xi = p.input("x", (rows, h))
+    (g,), (w,) = both(ctx, oracle, p.out(p.op("SumRows", [xi], (h,))), {"x": x}, (0,))
+    assert within(g, w, np.abs(x).astype(np.float64).sum(0))[0]
+
+
 @pytest.mark.parametrize("v,h,r,n", [(1000, 64, 96, 256), (30522, 128, 832, 4096)])
 def test_tied_decoder_gradients(ctx, oracle, v, h, r, n):
     """The tied-embedding decoder's graph: logits = h E^T, dX = dl E, the decoder weight gradient
