@@ -160,6 +160,30 @@ __device__ __forceinline__ void wide_store_h(_Float16* S, int e, float4 v) {
     S[(r + 3) * P + k] = _Float16(v.w);
   }
 }
+// The f16 tiles of an operand whose rows are not contiguous along K: a thread holds N float4
+// groups of 4 rows at N consecutive K (the groups hk_group numbers), and stores each of the 4 rows
+// as one vector of N halves.
+template <int R, int N>
+__device__ __forceinline__ int hk_group(int t, int h) {
+  return ((t / (R / 4)) * N + h) * (R / 4) + t % (R / 4);
+}
+template <int R, int P, int N>
+__device__ __forceinline__ void rows_store_h(_Float16* S, int t, const float4 (&v)[N]) {
+  const int r = (t % (R / 4)) * 4, k = (t / (R / 4)) * N;
+  typedef _Float16 vh __attribute__((ext_vector_type(N)));
+  vh x0, x1, x2, x3;
+#pragma unroll
+  for (int h = 0; h < N; ++h) {
+    x0[h] = _Float16(v[h].x);
+    x1[h] = _Float16(v[h].y);
+    x2[h] = _Float16(v[h].z);
+    x3[h] = _Float16(v[h].w);
+  }
+  *reinterpret_cast<vh*>(S + (r + 0) * P + k) = x0;
+  *reinterpret_cast<vh*>(S + (r + 1) * P + k) = x1;
+  *reinterpret_cast<vh*>(S + (r + 2) * P + k) = x2;
+  *reinterpret_cast<vh*>(S + (r + 3) * P + k) = x3;
+}
 }  // namespace
 
 // The order a GEMM's tiles are handed to blocks: mt x nt tiles a split slice, `tiles` in all,
@@ -187,7 +211,8 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   constexpr int PH = WK + 8;  // f16 tile row: the K slice and 16 bytes of pad
   constexpr int TILES = H ? (NB * (TM + TN) * PH + 1) / 2 : NB * WK * LA + NB * WK * LB;
   static_assert(!H || WK % 32 == 0, "the f16 MFMA takes K 32 at a time");
-  __shared__ __align__(16) float smem[TILES > TM * LC ? TILES : TM * LC];
+  constexpr int PASSES = TM > 64 ? TM / 64 : 1, PR = TM / PASSES;  // output rows staged at a time
+  __shared__ __align__(16) float smem[TILES > PR * LC ? TILES : PR * LC];
   float* const As0 = smem;                  // As(buf) = As0 + buf WK LA
   float* const Bs0 = smem + NB * WK * LA;   // Bs(buf) = Bs0 + buf WK LB
   _Float16* const Ah0 = reinterpret_cast<_Float16*>(smem);  // Ah(buf) = Ah0 + buf TM PH
@@ -215,14 +240,19 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   for (int i = 0; i < WM; ++i)
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  // op(A) is KC (contiguous along k) unless TA; op(B)^T is KC when TB.
+  // op(A) is KC (contiguous along k) unless TA; op(B)^T is KC when TB. Under H an operand that is
+  // not KC is loaded as consecutive K groups a thread (hk_group; GA and GB are multiples of 256).
+  constexpr bool RA = H && TA, RB = H && !TB;
+  static_assert((!RA || GA % 256 == 0) && (!RB || GB % 256 == 0), "row-vector staging takes whole groups a thread");
+  auto ga = [&](int h) { return RA ? hk_group<TM, HA>(tid, h) : tid + 256 * h; };
+  auto gb = [&](int h) { return RB ? hk_group<TN, HB>(tid, h) : tid + 256 * h; };
   float4 ra[HA], rb[HB];
 #pragma unroll
   for (int h = 0; h < HA; ++h)
-    if (tid + 256 * h < GA) ra[h] = wide_load<!TA, TM, WK, VA>(A, lda, M, kend, m0, kbeg, tid + 256 * h);
+    if (tid + 256 * h < GA) ra[h] = wide_load<!TA, TM, WK, VA>(A, lda, M, kend, m0, kbeg, ga(h));
 #pragma unroll
   for (int h = 0; h < HB; ++h)
-    if (tid + 256 * h < GB) rb[h] = wide_load<TB, TN, WK, VB>(B, ldb, N, kend, n0, kbeg, tid + 256 * h);
+    if (tid + 256 * h < GB) rb[h] = wide_load<TB, TN, WK, VB>(B, ldb, N, kend, n0, kbeg, gb(h));
   // Column sums: thread t adds tile column t mod T over the K rows (t / T) per .. + per of each
   // K tile, per = WK / (256 / T).
   const int T = sum_a ? TM : TN;
@@ -234,12 +264,20 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   for (int64_t k0 = kbeg; k0 < kend; k0 += WK) {
     if (NB == 1 && k0 != kbeg) __syncthreads();  // the single buffer is free again
     if constexpr (H) {
+      if constexpr (RA) {
+        rows_store_h<TM, PH, HA>(Ah0 + buf * (TM * PH), tid, ra);
+      } else {
 #pragma unroll
-      for (int h = 0; h < HA; ++h)
-        if (tid + 256 * h < GA) wide_store_h<!TA, TM, PH, WK>(Ah0 + buf * (TM * PH), tid + 256 * h, ra[h]);
+        for (int h = 0; h < HA; ++h)
+          if (tid + 256 * h < GA) wide_store_h<!TA, TM, PH, WK>(Ah0 + buf * (TM * PH), tid + 256 * h, ra[h]);
+      }
+      if constexpr (RB) {
+        rows_store_h<TN, PH, HB>(Bh0 + buf * (TN * PH), tid, rb);
+      } else {
 #pragma unroll
-      for (int h = 0; h < HB; ++h)
-        if (tid + 256 * h < GB) wide_store_h<TB, TN, PH, WK>(Bh0 + buf * (TN * PH), tid + 256 * h, rb[h]);
+        for (int h = 0; h < HB; ++h)
+          if (tid + 256 * h < GB) wide_store_h<TB, TN, PH, WK>(Bh0 + buf * (TN * PH), tid + 256 * h, rb[h]);
+      }
     } else {
 #pragma unroll
       for (int h = 0; h < HA; ++h)
@@ -252,10 +290,10 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
     if (k0 + WK < kend) {
 #pragma unroll
       for (int h = 0; h < HA; ++h)
-        if (tid + 256 * h < GA) ra[h] = wide_load<!TA, TM, WK, VA>(A, lda, M, kend, m0, k0 + WK, tid + 256 * h);
+        if (tid + 256 * h < GA) ra[h] = wide_load<!TA, TM, WK, VA>(A, lda, M, kend, m0, k0 + WK, ga(h));
 #pragma unroll
       for (int h = 0; h < HB; ++h)
-        if (tid + 256 * h < GB) rb[h] = wide_load<TB, TN, WK, VB>(B, ldb, N, kend, n0, k0 + WK, tid + 256 * h);
+        if (tid + 256 * h < GB) rb[h] = wide_load<TB, TN, WK, VB>(B, ldb, N, kend, n0, k0 + WK, gb(h));
     }
     if constexpr (H) {
       const _Float16* ah = Ah0 + buf * (TM * PH) + (wm + (lane & 15)) * PH + 8 * (lane >> 4);
@@ -310,40 +348,46 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   }
   // The output tile goes through LDS so that each row leaves as whole float4 groups (when `vo`:
   // 16-byte aligned rows whose width is a multiple of 4, or padded to one), the epilogue applied
-  // on the way.
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < WM; ++i)
-#pragma unroll
-    for (int j = 0; j < WN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) smem[(wm + 16 * i + 4 * (lane >> 4) + r) * LC + wn + 16 * j + (lane & 15)] = acc[i][j][r];
-  __syncthreads();
+  // on the way; a tile of more than 64 rows goes in passes of 64 rows (the waves of one half).
   float* out = ws ? ws + int64_t(tz) * M * N : C;
   const int64_t ldo = ws ? N : ldc;
   constexpr int Q = TN / 4;
 #pragma unroll
-  for (int e0 = 0; e0 < TM * Q; e0 += 256) {
-    const int e = e0 + tid;
-    if (TM * Q % 256 != 0 && e >= TM * Q) break;
-    const int rl = e / Q, c4 = (e % Q) * 4;
-    const int64_t row = m0 + rl, col = n0 + c4;
-    if (row >= M) continue;
-    const float4 v = *reinterpret_cast<const float4*>(smem + rl * LC + c4);
-    if (vo && col + 3 < N) {
-      *reinterpret_cast<float4*>(out + row * ldo + col) = ws ? v : gemm_epilogue4(epi, v, row, col, ldo);
-    } else if (vo && col < N) {
-      // The last group of a row padded to a multiple of 4: zeros in the padding.
-      const float vs[4] = {v.x, v.y, v.z, v.w};
-      float r4[4];
+  for (int pass = 0; pass < PASSES; ++pass) {
+    __syncthreads();
+    if (PASSES == 1 || wm / PR == pass) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) r4[c] = col + c < N ? (ws ? vs[c] : gemm_epilogue(epi, vs[c], row, col + c, ldo)) : 0.0f;
-      *reinterpret_cast<float4*>(out + row * ldo + col) = make_float4(r4[0], r4[1], r4[2], r4[3]);
-    } else {
-      const float vs[4] = {v.x, v.y, v.z, v.w};
+      for (int i = 0; i < WM; ++i)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (col + c < N) out[row * ldo + col + c] = ws ? vs[c] : gemm_epilogue(epi, vs[c], row, col + c, ldo);
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            smem[(wm - pass * PR + 16 * i + 4 * (lane >> 4) + r) * LC + wn + 16 * j + (lane & 15)] = acc[i][j][r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e0 = 0; e0 < PR * Q; e0 += 256) {
+      const int e = e0 + tid;
+      if (PR * Q % 256 != 0 && e >= PR * Q) break;
+      const int rl = e / Q, c4 = (e % Q) * 4;
+      const int64_t row = m0 + pass * PR + rl, col = n0 + c4;
+      if (row >= M) continue;
+      const float4 v = *reinterpret_cast<const float4*>(smem + rl * LC + c4);
+      if (vo && col + 3 < N) {
+        *reinterpret_cast<float4*>(out + row * ldo + col) = ws ? v : gemm_epilogue4(epi, v, row, col, ldo);
+      } else if (vo && col < N) {
+        // The last group of a row padded to a multiple of 4: zeros in the padding.
+        const float vs[4] = {v.x, v.y, v.z, v.w};
+        float r4[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) r4[c] = col + c < N ? (ws ? vs[c] : gemm_epilogue(epi, vs[c], row, col + c, ldo)) : 0.0f;
+        *reinterpret_cast<float4*>(out + row * ldo + col) = make_float4(r4[0], r4[1], r4[2], r4[3]);
+      } else {
+        const float vs[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (col + c < N) out[row * ldo + col + c] = ws ? vs[c] : gemm_epilogue(epi, vs[c], row, col + c, ldo);
+      }
     }
   }
 }
@@ -352,18 +396,21 @@ namespace {
 // The tile shape and split-K of a GEMM, from measured MI355X timings of the step's shapes: large
 // outputs (and very deep K) take 64 x 64 tiles, outputs up to 2^19 elements 32 x 32, the rest
 // 32 x 64. Split-K, whose slice sum costs a launch unless deferred to a batched finalize, is used
-// when deferred or when K is deep, to fill the chip.
+// when deferred or when K is deep, to fill the chip. The f16 MFMA does eight times the work of
+// the f32 one an instruction, so mixed-precision GEMMs of 2^21 outputs or more (or K of 8192 or
+// more) take 128 x 128 tiles: four times the MFMAs per operand byte staged.
 struct SplitPlan { int wm, wn, wk, split; int64_t chunk; };
-SplitPlan split_plan(int64_t m, int64_t n, int64_t k, bool defer) {
+SplitPlan split_plan(int64_t m, int64_t n, int64_t k, bool defer, bool h16) {
   const int64_t mn = m * n;
   SplitPlan p{};
-  if (mn >= (int64_t(1) << 21) || k >= 8192) { p.wm = 2; p.wn = 2; p.wk = 16; }
+  if (h16 && (mn >= (int64_t(1) << 21) || k >= 8192)) { p.wm = 4; p.wn = 4; p.wk = 32; }
+  else if (mn >= (int64_t(1) << 21) || k >= 8192) { p.wm = 2; p.wn = 2; p.wk = 16; }
   else if (mn <= (int64_t(1) << 19)) { p.wm = 1; p.wn = 1; p.wk = 32; }
   else { p.wm = 1; p.wn = 2; p.wk = 16; }
   const int64_t tiles = ((m + 32 * p.wm - 1) / (32 * p.wm)) * ((n + 32 * p.wn - 1) / (32 * p.wn));
   int64_t want = 1;
   if (defer || k >= 1024) {
-    const int64_t blocks = p.wm == 2 ? 2048 : 1024;
+    const int64_t blocks = p.wm == 2 ? 2048 : 1024;  // 128 x 128 tiles: 1024 (4 a CU)
     want = tiles < blocks / 4 ? (blocks + tiles - 1) / tiles : 1;
   }
   // Deferred slices keep 128 K steps or more: their partials all go through the finalize.
@@ -374,16 +421,16 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k, bool defer) {
 }
 }  // namespace
 
-int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer) { return split_plan(m, n, k, defer).split; }
+int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer, bool h16) { return split_plan(m, n, k, defer, h16).split; }
 
-int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum, bool sum_a, bool defer) {
-  const int split = gemm_split_for(m, n, k, defer);
+int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum, bool sum_a, bool defer, bool h16) {
+  const int split = gemm_split_for(m, n, k, defer, h16);
   if (split <= 1) return 0;
   return int64_t(split) * m * n + (colsum ? int64_t(split) * (sum_a ? m : n) : 0);  // partials, then sums
 }
 
 int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs) {
-  const int split = gemm_split_for(g.m, g.n, g.k, g.defer);
+  const int split = gemm_split_for(g.m, g.n, g.k, g.defer, g.h16);
   if (split <= 1) return 0;
   if (g.bias || g.addend || g.act || g.ldc != g.n) bad("deferred split-K needs a dense output without epilogue");
   if (g.m * g.n > INT32_MAX) bad("deferred split-K output too large");
@@ -397,12 +444,12 @@ int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs) {
 void gemm(hipStream_t s, const GemmArgs& g) {
   if (g.m <= 0 || g.n <= 0) return;
   if (g.k <= 0) bad("gemm with k = 0");
-  const SplitPlan plan = split_plan(g.m, g.n, g.k, g.defer);
+  const SplitPlan plan = split_plan(g.m, g.n, g.k, g.defer, g.h16);
   const int split = plan.split;
   const int64_t chunk = plan.chunk;
   float* ws = nullptr;
   if (split > 1) {
-    if (!g.workspace || g.workspace_floats < gemm_workspace(g.m, g.n, g.k, g.colsum != nullptr, g.sum_a, g.defer))
+    if (!g.workspace || g.workspace_floats < gemm_workspace(g.m, g.n, g.k, g.colsum != nullptr, g.sum_a, g.defer, g.h16))
       bad("gemm split-K workspace too small");
     ws = g.workspace;
   }
@@ -451,7 +498,8 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   else if (vb) MSX_WIDE_HV(TA, TB, WM, WN, false, true);            \
   else MSX_WIDE_HV(TA, TB, WM, WN, false, false)
 #define MSX_WIDE_HT(TA, TB)                                 \
-  if (plan.wm == 2) MSX_WIDE_H(TA, TB, 2, 2);               \
+  if (plan.wm == 4) MSX_WIDE_H(TA, TB, 4, 4);               \
+  else if (plan.wm == 2) MSX_WIDE_H(TA, TB, 2, 2);          \
   else if (plan.wn == 2) MSX_WIDE_H(TA, TB, 1, 2);          \
   else MSX_WIDE_H(TA, TB, 1, 1);
   if (g.h16) {

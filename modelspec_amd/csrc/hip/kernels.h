@@ -55,10 +55,11 @@ struct GemmArgs {
 enum GemmAct : int { EPI_NONE, EPI_GELU, EPI_RELU, EPI_GELU_GRAD, EPI_RELU_GRAD };
 struct GemmEpi { const float* bias; const float* addend; const float* pre_in; float* pre_out; int act; };
 // The split-K factor the launcher uses (with `defer` as in GemmArgs).
-int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer = false);
+int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer = false, bool h16 = false);
 // Floats of workspace a gemm of this shape needs (0 without split-K): the slices' partial
 // products, then the slices' column (row) sums when asked for.
-int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum = false, bool sum_a = false, bool defer = false);
+int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum = false, bool sum_a = false, bool defer = false,
+                       bool h16 = false);
 // The column_finalize jobs that finish a deferred split-K gemm (0, 1 or 2 written to jobs).
 int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs);
 void gemm(hipStream_t s, const GemmArgs& g);

@@ -739,7 +739,7 @@ void Executor::build() {
         int64_t bias_id = fused ? int64_t(o[1]) : -1;
         // Split-K partials only the optimizer reads are summed by the batched column finalize.
         g.defer = bias_id < 0 && epi.node == id && only_optimizer_reads(int64_t(out_id)) && only_optimizer_reads(cs_id);
-        int64_t wsf = hk::gemm_workspace(g.m, g.n, g.k, cs_id >= 0, g.sum_a, g.defer);
+        int64_t wsf = hk::gemm_workspace(g.m, g.n, g.k, cs_id >= 0, g.sum_a, g.defer, g.h16);
         void* ws = wsf > 0 ? R(size_t(wsf) * 4) : nullptr;
         g.workspace_floats = wsf;
         push([=](hipStream_t s) {
@@ -757,7 +757,7 @@ void Executor::build() {
           hk::gemm(s, a);
         });
         if (g.defer && wsf > 0) {
-          const int split = hk::gemm_split_for(g.m, g.n, g.k, true);
+          const int split = hk::gemm_split_for(g.m, g.n, g.k, true, g.h16);
           const int32_t mn = int32_t(g.m * g.n);
           deferred.push_back({ws, 0, int64_t(out_id), -1, split, mn, mn});
           if (cs_id >= 0) {

@@ -32,7 +32,8 @@ def mixed(ctx):
 
 @pytest.mark.parametrize("m,k,n,ta,tb", [(128, 96, 80, False, False), (300, 770, 129, True, False),
                                          (64, 4096, 128, False, True), (832, 128, 4001, True, True),
-                                         (33, 45, 17, False, False)])
+                                         (33, 45, 17, False, False), (1000, 2100, 3000, False, False),
+                                         (777, 2900, 520, True, True), (2880, 768, 4100, False, True)])
 def test_a_mixed_gemm_is_the_product_of_f16_operands(mixed, m, k, n, ta, tb):
     a = fast_values(21, m * k, 0.25).reshape((k, m) if ta else (m, k))
     b = fast_values(22, k * n, 0.25).reshape((n, k) if tb else (k, n))
