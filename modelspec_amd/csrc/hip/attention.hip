@@ -2,8 +2,9 @@
 // v, per (sequence, head). The main path runs on the f32 MFMA (v_mfma_f32_16x16x4f32) in a flash
 // layout: a wave owns 16 query rows (forward, dQ) or 16 key rows (dK, dV); the scores are
 // computed transposed (K Q^T) so that the probabilities of a query sit in the lanes that feed
-// them to the P V and dS K MFMAs without an LDS round trip. The forward saves each query's
-// softmax maximum and sum; the backward recomputes P from them and takes
+// them to the P V and dS K MFMAs without an LDS round trip. The forward is one pass over the keys
+// (online softmax) and saves each query's softmax maximum and sum; the backward recomputes P from
+// them and takes
 // d_i = sum_j P_ij dP_ij as rowsum(dO_i * O_i) from the forward's output. Shapes outside the MFMA
 // tiling run a scalar fallback (one thread per row). Semantics: interpreter.rs:1035-1119,
 // 1298-1510 (masked keys excluded; a masked key's dK and dV rows are +0).
@@ -192,204 +193,202 @@ __global__ __launch_bounds__(256) void k_attn_bwd_scalar(const float* __restrict
 }
 
 // ---------------------------------------------------------------------------------------------
-// MFMA path. Row stride of every LDS tile is D + 4 floats: the 16 rows x 4 columns an MFMA
-// operand read touches fall in distinct banks.
-constexpr int kU = 4;      // row tiles whose MFMA chains interleave
-constexpr int kWaves = 2;  // waves (16 rows each) a block: a block's K/V (or Q/dO) LDS copy limits
-                           // a CU to two blocks, so smaller blocks spread a sequence over more CUs
+// MFMA path. A block is four waves; each wave owns 16 rows of its side (queries for the forward
+// and dQ, keys for dK/dV) and the block streams the other side through LDS in tiles of T rows,
+// double-buffered: the next tile's global loads are in flight while the current one is in the
+// MFMAs, and one barrier a tile hands the buffers over. Row stride of every LDS tile is D + 4
+// floats: the 16 rows x 4 columns an MFMA operand read touches fall in distinct banks.
 
-// Stages rows [0, rows) of two [., H] head slices (x at xs + row H, y likewise, D floats each)
-// into LDS tiles of row stride D + 4, eight float4 of each a thread in flight before any store.
-template <int D>
-__device__ __forceinline__ void stage_pair(float* X, float* Y, const float* __restrict__ xs,
-                                           const float* __restrict__ ys, int rows, int H) {
-  constexpr int DP = D + 4, Q = D / 4;
-  const int total = rows * Q;
-  for (int e0 = threadIdx.x; e0 < total; e0 += 8 * int(blockDim.x)) {
-    float4 xv[8], yv[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      int e = e0 + u * int(blockDim.x);
-      e = e < total ? e : total - 1;
-      const int64_t off = int64_t(e / Q) * H + (e % Q) * 4;
-      xv[u] = *reinterpret_cast<const float4*>(xs + off);
-      yv[u] = *reinterpret_cast<const float4*>(ys + off);
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int e = e0 + u * int(blockDim.x);
-      if (e < total) {
-        float* xd = X + (e / Q) * DP + (e % Q) * 4;
-        float* yd = Y + (e / Q) * DP + (e % Q) * 4;
-        xd[0] = xv[u].x; xd[1] = xv[u].y; xd[2] = xv[u].z; xd[3] = xv[u].w;
-        yd[0] = yv[u].x; yd[1] = yv[u].y; yd[2] = yv[u].z; yd[3] = yv[u].w;
-      }
-    }
-  }
-}
-
-
-// Scores of kU tiles of 16 LDS rows R (tiles t0 .. t0 + kU, the ones past nt repeat the last
-// tile and are ignored by the caller) against the 16 columns whose operand fragments xb a lane
-// holds: acc[u][r] = sum over d of R[(t0 + u) 16 + c][d] x[4 g + r][d], each in d order.
-template <int D>
-__device__ __forceinline__ void score_tiles(const float* R, const float (&xb)[D / 4], int t0, int nt, int c, int g,
-                                            v4f (&acc)[kU]) {
+// Scores of U tiles of 16 LDS rows R against the 16 columns whose operand fragments xb a lane
+// holds: acc[u][r] = sum over d of R[16 u + c][d] x[4 g + r][d], each in d order. Tiles at or past
+// nt (a partial last tile) repeat tile nt - 1, branch-free; the caller ignores them.
+template <int D, int U>
+__device__ __forceinline__ void score_tiles(const float* R, const float (&xb)[D / 4], int nt, int c, int g,
+                                            v4f (&acc)[U]) {
   constexpr int DP = D + 4;
-  const float* rr[kU];
+  const float* rr[U];
 #pragma unroll
-  for (int u = 0; u < kU; ++u) {
+  for (int u = 0; u < U; ++u) {
     acc[u] = v4f{0, 0, 0, 0};
-    rr[u] = R + ((t0 + u < nt ? t0 + u : nt - 1) * 16 + c) * DP + g;
+    rr[u] = R + (16 * (u < nt ? u : nt - 1) + c) * DP + g;
   }
 #pragma unroll
   for (int t = 0; t < D / 4; ++t)
 #pragma unroll
-    for (int u = 0; u < kU; ++u) acc[u] = mfma4(rr[u][4 * t], xb[t], acc[u]);
+    for (int u = 0; u < U; ++u) acc[u] = mfma4(rr[u][4 * t], xb[t], acc[u]);
 }
-// Stages rows [0, rows) of one [., H] head slice into an LDS tile of row stride D + 4.
-template <int D>
-__device__ __forceinline__ void stage_one(float* X, const float* __restrict__ xs, int rows, int H) {
-  constexpr int DP = D + 4, Q = D / 4;
-  const int total = rows * Q;
-  for (int e0 = threadIdx.x; e0 < total; e0 += 8 * int(blockDim.x)) {
-    float4 xv[8];
+
+// One tile of two [., H] head slices (rows 0 .. n of x and y, D floats each) on its way to LDS
+// through registers: fetch_pair issues the global loads (rows past n repeat row n - 1), put_pair
+// stores them as tiles of row stride D + 4. NT threads take part, PT = tile_groups 4-float groups
+// of each slice a thread, held as native vectors (a float4 struct array is copied through private
+// memory).
+template <int D, int T, int NT>
+constexpr int tile_groups() { return (T * (D / 4) + NT - 1) / NT; }
+template <int D, int T, int NT, int PT>
+__device__ __forceinline__ void fetch_pair(v4f (&xv)[PT], v4f (&yv)[PT], const float* __restrict__ xs,
+                                           const float* __restrict__ ys, int64_t H, int n) {
+  constexpr int Q = D / 4, G = T * Q;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      int e = e0 + u * int(blockDim.x);
-      e = e < total ? e : total - 1;
-      xv[u] = *reinterpret_cast<const float4*>(xs + int64_t(e / Q) * H + (e % Q) * 4);
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int e = e0 + u * int(blockDim.x);
-      if (e < total) {
-        float* xd = X + (e / Q) * DP + (e % Q) * 4;
-        xd[0] = xv[u].x; xd[1] = xv[u].y; xd[2] = xv[u].z; xd[3] = xv[u].w;
-      }
+  for (int p = 0; p < PT; ++p) {
+    const int e = int(threadIdx.x) + NT * p;
+    int row = e / Q;
+    row = row < n ? row : n - 1;
+    const int64_t off = int64_t(row) * H + (e % Q) * 4;
+    if (G % NT == 0 || e < G) {
+      xv[p] = *reinterpret_cast<const v4f*>(xs + off);
+      yv[p] = *reinterpret_cast<const v4f*>(ys + off);
     }
   }
 }
+template <int D, int T, int NT, int PT>
+__device__ __forceinline__ void put_pair(float* X, float* Y, const v4f (&xv)[PT], const v4f (&yv)[PT]) {
+  constexpr int DP = D + 4, Q = D / 4, G = T * Q;
+#pragma unroll
+  for (int p = 0; p < PT; ++p) {
+    const int e = int(threadIdx.x) + NT * p;
+    if (G % NT == 0 || e < G) {
+      *reinterpret_cast<v4f*>(X + (e / Q) * DP + (e % Q) * 4) = xv[p];
+      *reinterpret_cast<v4f*>(Y + (e / Q) * DP + (e % Q) * 4) = yv[p];
+    }
+  }
+}
+// Floats of LDS a streaming kernel takes: two buffers of two T x (D + 4) tiles and E floats a row.
+constexpr int64_t stream_lds_floats(int64_t T, int64_t D, int64_t E) { return 2 * (2 * T * (D + 4) + E * T); }
 
-// The kernels below stream the other side of the attention (keys for the forward and dQ, queries
-// for dK/dV) through LDS `chunk` rows at a time, in ascending order, so a sequence of any length
-// fits; a sequence that fits one chunk is staged once. Every wave of a block takes part in the
-// staging; waves past the last row tile compute nothing.
-template <int D>
-__global__ __launch_bounds__(256) void k_attn_fwd_mfma(const float* __restrict__ q, const float* __restrict__ k,
+// The forward, in one pass over the keys (online softmax): per tile, the scores of the wave's 16
+// queries against the tile's unmasked keys raise the running maximum m; the running sum l and
+// output O are rescaled by exp(m_old - m_new); P = exp(s - m) feeds the P V MFMA and l. Saves m
+// and l (the sum relative to the final maximum) per query for the backward.
+template <int D, int T, int W>
+__global__ __launch_bounds__(64 * W) void k_attn_fwd_mfma(const float* __restrict__ q, const float* __restrict__ k,
                                                        const float* __restrict__ v, const float* __restrict__ mask,
                                                        float* __restrict__ o, float* __restrict__ stats, int L, int S,
-                                                       int H, int heads, float scale, int chunk) {
-  constexpr int DP = D + 4;
+                                                       int H, int heads, float scale) {
+  constexpr int DP = D + 4, U = T / 16;
   extern __shared__ float sm[];
-  float* Ks = sm;
-  float* Vs = sm + chunk * DP;
-  float* Ms = sm + 2 * chunk * DP;
+  float* const Kb = sm;                    // buffer j: Kb + j 2 T DP
+  float* const Vb = sm + T * DP;           // Vb + j 2 T DP
+  float* const Mb = sm + 4 * T * DP;       // Mb + j T
   const int b = blockIdx.x / heads, head = blockIdx.x % heads;
   const int64_t kbase = int64_t(b) * S * H + head * D;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  const int i0 = blockIdx.y * int(blockDim.x / 4) + wave * 16;
+  const int i0 = blockIdx.y * (16 * W) + wave * 16;
   const bool active = i0 < L;
-  const bool single = S <= chunk;
   const int64_t qrow = (int64_t(b) * L + (active ? i0 : 0) + c) * H + head * D;
   float qb[D / 4];
 #pragma unroll
   for (int t = 0; t < D / 4; ++t) qb[t] = q[qrow + 4 * t + g];
-  // Pass 1: the maximum score of query i0 + c over the unmasked keys. kU key tiles at a time, so
-  // that kU independent MFMA chains interleave.
-  float mx = -INFINITY;
-  for (int s0 = 0; s0 < S; s0 += chunk) {
-    const int n = S - s0 < chunk ? S - s0 : chunk;
-    __syncthreads();
-    if (single) stage_pair<D>(Ks, Vs, k + kbase, v + kbase, n, H);
-    else stage_one<D>(Ks, k + kbase + int64_t(s0) * H, n, H);
-    for (int j = threadIdx.x; j < n; j += blockDim.x) Ms[j] = mask[int64_t(b) * S + s0 + j];
-    __syncthreads();
-    if (!active) continue;
-    const int nt = n / 16;
-    for (int jt0 = 0; jt0 < nt; jt0 += kU) {
-      v4f acc[kU];
-      score_tiles<D>(Ks, qb, jt0, nt, c, g, acc);
-#pragma unroll
-      for (int u = 0; u < kU; ++u)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (jt0 + u < nt && Ms[(jt0 + u) * 16 + 4 * g + r] != 0.0f) mx = fmaxf(mx, acc[u][r] * scale);
-    }
+  const float* mrow = mask + int64_t(b) * S;
+  constexpr int NT = 64 * W, PT = tile_groups<D, T, NT>();
+  static_assert(NT >= T, "a thread a row of the mask");
+  const int ntiles = (S + T - 1) / T;
+  const int tid = int(threadIdx.x);
+  {
+    v4f kv[PT], vv[PT];
+    fetch_pair<D, T, NT>(kv, vv, k + kbase, v + kbase, H, S < T ? S : T);
+    const float mv = tid < T ? mrow[tid < S ? tid : S - 1] : 0.0f;
+    put_pair<D, T, NT>(Kb, Vb, kv, vv);
+    if (tid < T) Mb[tid] = mv;
   }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  // Pass 2: P = exp(s - max) into the P V MFMA, the sum of P alongside.
-  float total = 0.0f;
+  __syncthreads();
+  float m = -INFINITY, l = 0.0f;
   v4f oacc[D / 16];
 #pragma unroll
   for (int ct = 0; ct < D / 16; ++ct) oacc[ct] = v4f{0, 0, 0, 0};
-  for (int s0 = 0; s0 < S; s0 += chunk) {
-    const int n = S - s0 < chunk ? S - s0 : chunk;
-    if (!single) {
-      __syncthreads();
-      stage_pair<D>(Ks, Vs, k + kbase + int64_t(s0) * H, v + kbase + int64_t(s0) * H, n, H);
-      for (int j = threadIdx.x; j < n; j += blockDim.x) Ms[j] = mask[int64_t(b) * S + s0 + j];
-      __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int j = t & 1, s0 = t * T, n = S - s0 < T ? S - s0 : T;
+    const bool more = t + 1 < ntiles;
+    v4f kv[PT], vv[PT];
+    float mv = 0.0f;
+    if (more) {
+      const int s1 = s0 + T, n1 = S - s1 < T ? S - s1 : T;
+      fetch_pair<D, T, NT>(kv, vv, k + kbase + int64_t(s1) * H, v + kbase + int64_t(s1) * H, H, n1);
+      if (tid < T) mv = mrow[s1 + (tid < n1 ? tid : n1 - 1)];
     }
-    if (!active) continue;
-    const int nt = n / 16;
-    for (int jt0 = 0; jt0 < nt; jt0 += kU) {
-      v4f acc[kU];
-      score_tiles<D>(Ks, qb, jt0, nt, c, g, acc);
+    if (active) {
+      const float* Ks = Kb + j * 2 * T * DP;
+      const float* Vs = Vb + j * 2 * T * DP;
+      const float* Ms = Mb + j * T;
+      const int nt = n / 16;
+      v4f acc[U];
+      score_tiles<D, U>(Ks, qb, nt, c, g, acc);
+      float tmax = -INFINITY;
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        if (jt0 + u >= nt) break;
-        const int jt = jt0 + u;
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (u < nt && Ms[16 * u + 4 * g + r] != 0.0f) tmax = fmaxf(tmax, acc[u][r] * scale);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float mn = fmaxf(m, tmax);
+      // No unmasked key yet (mn = -inf): nothing has accumulated, nothing to rescale.
+      const float alpha = mn == -INFINITY ? 1.0f : expf(m - mn);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) oacc[ct][r] *= ar;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (u >= nt) break;
         float p[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          p[r] = Ms[jt * 16 + 4 * g + r] != 0.0f ? expf(acc[u][r] * scale - mx) : 0.0f;
-          total += p[r];
+          p[r] = Ms[16 * u + 4 * g + r] != 0.0f ? expf(acc[u][r] * scale - m) : 0.0f;
+          l += p[r];
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float* vr = Vs + (jt * 16 + 4 * g + r) * DP + c;
+          const float* vr = Vs + (16 * u + 4 * g + r) * DP + c;
 #pragma unroll
           for (int ct = 0; ct < D / 16; ++ct) oacc[ct] = mfma4(p[r], vr[ct * 16], oacc[ct]);
         }
       }
     }
+    if (more) {
+      put_pair<D, T, NT>(Kb + (j ^ 1) * 2 * T * DP, Vb + (j ^ 1) * 2 * T * DP, kv, vv);
+      if (tid < T) Mb[(j ^ 1) * T + tid] = mv;
+    }
+    __syncthreads();
   }
   if (!active) return;
-  total += __shfl_xor(total, 16, 64);
-  total += __shfl_xor(total, 32, 64);
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const float row_total = __shfl(total, 4 * g + r, 64);
+    const float row_total = __shfl(l, 4 * g + r, 64);
     const int64_t orow = (int64_t(b) * L + i0 + 4 * g + r) * H + head * D;
 #pragma unroll
     for (int ct = 0; ct < D / 16; ++ct) o[orow + ct * 16 + c] = oacc[ct][r] / row_total;
   }
   if (stats && g == 0) {
     const int64_t at = (int64_t(blockIdx.x) * L + i0 + c) * 2;
-    stats[at] = mx;
-    stats[at + 1] = total;
+    stats[at] = m;
+    stats[at + 1] = l;
   }
 }
 
-// dQ and d_i = rowsum(dO * O), per 16 query rows.
-template <int D>
-__global__ __launch_bounds__(256) void k_attn_bwd_q_mfma(const float* __restrict__ q, const float* __restrict__ k,
+// dQ and d_i = rowsum(dO * O), per 16 query rows, streaming key and value tiles.
+template <int D, int T, int W>
+__global__ __launch_bounds__(64 * W) void k_attn_bwd_q_mfma(const float* __restrict__ q, const float* __restrict__ k,
                                                          const float* __restrict__ v, const float* __restrict__ mask,
                                                          const float* __restrict__ o, const float* __restrict__ stats,
                                                          const float* __restrict__ go, float* __restrict__ dq,
                                                          float* __restrict__ dsum, int L, int S, int H, int heads,
-                                                         float scale, int chunk) {
-  constexpr int DP = D + 4;
+                                                         float scale) {
+  constexpr int DP = D + 4, U = T / 16;
   extern __shared__ float sm[];
-  float* Ks = sm;
-  float* Vs = sm + chunk * DP;
-  float* Ms = sm + 2 * chunk * DP;
+  float* const Kb = sm;
+  float* const Vb = sm + T * DP;
+  float* const Mb = sm + 4 * T * DP;
   const int b = blockIdx.x / heads, head = blockIdx.x % heads;
   const int64_t kbase = int64_t(b) * S * H + head * D;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  const int i0 = blockIdx.y * int(blockDim.x / 4) + wave * 16;
+  const int i0 = blockIdx.y * (16 * W) + wave * 16;
   const bool active = i0 < L;
   const int64_t row = (int64_t(b) * L + (active ? i0 : 0) + c) * H + head * D;
   // d_i for query i0 + c: lane group g sums columns [g D/4, (g + 1) D/4).
@@ -404,39 +403,62 @@ __global__ __launch_bounds__(256) void k_attn_bwd_q_mfma(const float* __restrict
   float qb[D / 4], gb[D / 4];
 #pragma unroll
   for (int t = 0; t < D / 4; ++t) { qb[t] = q[row + 4 * t + g]; gb[t] = go[row + 4 * t + g]; }
+  const float* mrow = mask + int64_t(b) * S;
+  constexpr int NT = 64 * W, PT = tile_groups<D, T, NT>();
+  static_assert(NT >= T, "a thread a row of the mask");
+  const int ntiles = (S + T - 1) / T;
+  const int tid = int(threadIdx.x);
+  {
+    v4f kv[PT], vv[PT];
+    fetch_pair<D, T, NT>(kv, vv, k + kbase, v + kbase, H, S < T ? S : T);
+    const float mv = tid < T ? mrow[tid < S ? tid : S - 1] : 0.0f;
+    put_pair<D, T, NT>(Kb, Vb, kv, vv);
+    if (tid < T) Mb[tid] = mv;
+  }
+  __syncthreads();
   v4f acc[D / 16];
 #pragma unroll
   for (int ct = 0; ct < D / 16; ++ct) acc[ct] = v4f{0, 0, 0, 0};
-  for (int s0 = 0; s0 < S; s0 += chunk) {
-    const int n = S - s0 < chunk ? S - s0 : chunk;
-    __syncthreads();
-    stage_pair<D>(Ks, Vs, k + kbase + int64_t(s0) * H, v + kbase + int64_t(s0) * H, n, H);
-    for (int j = threadIdx.x; j < n; j += blockDim.x) Ms[j] = mask[int64_t(b) * S + s0 + j];
-    __syncthreads();
-    if (!active) continue;
-    const int nt = n / 16;
-    for (int jt0 = 0; jt0 < nt; jt0 += kU) {
-      v4f st[kU], dpt[kU];
-      score_tiles<D>(Ks, qb, jt0, nt, c, g, st);
-      score_tiles<D>(Vs, gb, jt0, nt, c, g, dpt);
+  for (int t = 0; t < ntiles; ++t) {
+    const int j = t & 1, s0 = t * T, n = S - s0 < T ? S - s0 : T;
+    const bool more = t + 1 < ntiles;
+    v4f kv[PT], vv[PT];
+    float mv = 0.0f;
+    if (more) {
+      const int s1 = s0 + T, n1 = S - s1 < T ? S - s1 : T;
+      fetch_pair<D, T, NT>(kv, vv, k + kbase + int64_t(s1) * H, v + kbase + int64_t(s1) * H, H, n1);
+      if (tid < T) mv = mrow[s1 + (tid < n1 ? tid : n1 - 1)];
+    }
+    if (active) {
+      const float* Ks = Kb + j * 2 * T * DP;
+      const float* Vs = Vb + j * 2 * T * DP;
+      const float* Ms = Mb + j * T;
+      const int nt = n / 16;
+      v4f st[U], dpt[U];
+      score_tiles<D, U>(Ks, qb, nt, c, g, st);
+      score_tiles<D, U>(Vs, gb, nt, c, g, dpt);
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        if (jt0 + u >= nt) break;
-        const int jt = jt0 + u;
+      for (int u = 0; u < U; ++u) {
+        if (u >= nt) break;
         float ds[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float p = Ms[jt * 16 + 4 * g + r] != 0.0f ? expf(st[u][r] * scale - mx) / total : 0.0f;
+          const float p = Ms[16 * u + 4 * g + r] != 0.0f ? expf(st[u][r] * scale - mx) / total : 0.0f;
           ds[r] = p * (dpt[u][r] - dd);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float* kk = Ks + (jt * 16 + 4 * g + r) * DP + c;
+          const float* kk = Ks + (16 * u + 4 * g + r) * DP + c;
 #pragma unroll
           for (int ct = 0; ct < D / 16; ++ct) acc[ct] = mfma4(ds[r], kk[ct * 16], acc[ct]);
         }
       }
     }
+    if (more) {
+      put_pair<D, T, NT>(Kb + (j ^ 1) * 2 * T * DP, Vb + (j ^ 1) * 2 * T * DP, kv, vv);
+      if (tid < T) Mb[(j ^ 1) * T + tid] = mv;
+    }
+    __syncthreads();
   }
   if (!active) return;
 #pragma unroll
@@ -447,64 +469,95 @@ __global__ __launch_bounds__(256) void k_attn_bwd_q_mfma(const float* __restrict
   }
 }
 
-// dK and dV, per 16 key rows, over every query of the sequence.
-template <int D>
-__global__ __launch_bounds__(256) void k_attn_bwd_kv_mfma(const float* __restrict__ q, const float* __restrict__ k,
+// dK and dV, per 16 key rows, streaming query and output-gradient tiles (with each query's
+// maximum, sum and d).
+template <int D, int T, int W>
+__global__ __launch_bounds__(64 * W) void k_attn_bwd_kv_mfma(const float* __restrict__ q, const float* __restrict__ k,
                                                           const float* __restrict__ v, const float* __restrict__ mask,
                                                           const float* __restrict__ stats, const float* __restrict__ go,
                                                           const float* __restrict__ dsum, float* __restrict__ dk,
                                                           float* __restrict__ dv, int L, int S, int H, int heads,
-                                                          float scale, int chunk) {
-  constexpr int DP = D + 4;
+                                                          float scale) {
+  constexpr int DP = D + 4, U = T / 16;
   extern __shared__ float sm[];
-  float* Qs = sm;
-  float* Gs = sm + chunk * DP;
-  float* Sm = sm + 2 * chunk * DP;  // max, sum, d per query of the chunk
+  float* const Qb = sm;
+  float* const Gb = sm + T * DP;
+  float* const Sb = sm + 4 * T * DP;  // max, sum, d per query of the tile; buffer j at Sb + j 3 T
   const int b = blockIdx.x / heads, head = blockIdx.x % heads;
   const int64_t qbase = int64_t(b) * L * H + head * D;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  const int j0 = blockIdx.y * int(blockDim.x / 4) + wave * 16;
+  const int j0 = blockIdx.y * (16 * W) + wave * 16;
   const bool active = j0 < S;
   const int64_t krow = (int64_t(b) * S + (active ? j0 : 0) + c) * H + head * D;
   const bool live = mask[int64_t(b) * S + (active ? j0 : 0) + c] != 0.0f;
   float kb[D / 4], vb[D / 4];
 #pragma unroll
   for (int t = 0; t < D / 4; ++t) { kb[t] = k[krow + 4 * t + g]; vb[t] = v[krow + 4 * t + g]; }
+  const int64_t sbase = int64_t(blockIdx.x) * L;
+  constexpr int NT = 64 * W, PT = tile_groups<D, T, NT>();
+  static_assert(NT >= T, "a thread a row of the statistics");
+  const int ntiles = (L + T - 1) / T;
+  const int tid = int(threadIdx.x);
+  // The maximum, sum and d of query l0 + row (row clamped to the n rows of the tile).
+  auto fetch_stats = [&](float (&e)[3], int l0, int n) {
+    if (tid < T) {
+      const int64_t at = sbase + l0 + (tid < n ? tid : n - 1);
+      e[0] = stats[2 * at];
+      e[1] = stats[2 * at + 1];
+      e[2] = dsum[at];
+    }
+  };
+  auto put_stats = [&](float* X, const float (&e)[3]) {
+    if (tid < T) {
+      X[3 * tid] = e[0];
+      X[3 * tid + 1] = e[1];
+      X[3 * tid + 2] = e[2];
+    }
+  };
+  {
+    v4f qv[PT], gv[PT];
+    float e[3] = {0.0f, 0.0f, 0.0f};
+    fetch_pair<D, T, NT>(qv, gv, q + qbase, go + qbase, H, L < T ? L : T);
+    fetch_stats(e, 0, L < T ? L : T);
+    put_pair<D, T, NT>(Qb, Gb, qv, gv);
+    put_stats(Sb, e);
+  }
+  __syncthreads();
   v4f dka[D / 16], dva[D / 16];
 #pragma unroll
   for (int ct = 0; ct < D / 16; ++ct) { dka[ct] = v4f{0, 0, 0, 0}; dva[ct] = v4f{0, 0, 0, 0}; }
-  for (int l0 = 0; l0 < L; l0 += chunk) {
-    const int n = L - l0 < chunk ? L - l0 : chunk;
-    __syncthreads();
-    stage_pair<D>(Qs, Gs, q + qbase + int64_t(l0) * H, go + qbase + int64_t(l0) * H, n, H);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-      const int64_t srow = int64_t(blockIdx.x) * L + l0 + i;
-      Sm[3 * i] = stats[2 * srow];
-      Sm[3 * i + 1] = stats[2 * srow + 1];
-      Sm[3 * i + 2] = dsum[srow];
+  for (int t = 0; t < ntiles; ++t) {
+    const int j = t & 1, l0 = t * T, n = L - l0 < T ? L - l0 : T;
+    const bool more = t + 1 < ntiles;
+    v4f qv[PT], gv[PT];
+    float e[3] = {0.0f, 0.0f, 0.0f};
+    if (more) {
+      const int l1 = l0 + T, n1 = L - l1 < T ? L - l1 : T;
+      fetch_pair<D, T, NT>(qv, gv, q + qbase + int64_t(l1) * H, go + qbase + int64_t(l1) * H, H, n1);
+      fetch_stats(e, l1, n1);
     }
-    __syncthreads();
-    if (!active) continue;
-    const int nt = n / 16;
-    for (int it0 = 0; it0 < nt; it0 += kU) {
-      v4f s[kU], dp[kU];
-      score_tiles<D>(Qs, kb, it0, nt, c, g, s);
-      score_tiles<D>(Gs, vb, it0, nt, c, g, dp);
+    if (active) {
+      const float* Qs = Qb + j * 2 * T * DP;
+      const float* Gs = Gb + j * 2 * T * DP;
+      const float* Ss = Sb + j * 3 * T;
+      const int nt = n / 16;
+      v4f s[U], dp[U];
+      score_tiles<D, U>(Qs, kb, nt, c, g, s);
+      score_tiles<D, U>(Gs, vb, nt, c, g, dp);
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        if (it0 + u >= nt) break;
-        const int it = it0 + u;
+      for (int u = 0; u < U; ++u) {
+        if (u >= nt) break;
         float p[4], ds[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float* st = Sm + 3 * (it * 16 + 4 * g + r);
+          const float* st = Ss + 3 * (16 * u + 4 * g + r);
           p[r] = live ? expf(s[u][r] * scale - st[0]) / st[1] : 0.0f;
           ds[r] = p[r] * (dp[u][r] - st[2]);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float* gq = Gs + (it * 16 + 4 * g + r) * DP + c;
-          const float* qq = Qs + (it * 16 + 4 * g + r) * DP + c;
+          const float* gq = Gs + (16 * u + 4 * g + r) * DP + c;
+          const float* qq = Qs + (16 * u + 4 * g + r) * DP + c;
 #pragma unroll
           for (int ct = 0; ct < D / 16; ++ct) {
             dva[ct] = mfma4(p[r], gq[ct * 16], dva[ct]);
@@ -513,13 +566,18 @@ __global__ __launch_bounds__(256) void k_attn_bwd_kv_mfma(const float* __restric
         }
       }
     }
+    if (more) {
+      put_pair<D, T, NT>(Qb + (j ^ 1) * 2 * T * DP, Gb + (j ^ 1) * 2 * T * DP, qv, gv);
+      put_stats(Sb + (j ^ 1) * 3 * T, e);
+    }
+    __syncthreads();
   }
   if (!active) return;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int j = j0 + 4 * g + r;
-    const bool keep = mask[int64_t(b) * S + j] != 0.0f;
-    const int64_t orow = (int64_t(b) * S + j) * H + head * D;
+    const int jj = j0 + 4 * g + r;
+    const bool keep = mask[int64_t(b) * S + jj] != 0.0f;
+    const int64_t orow = (int64_t(b) * S + jj) * H + head * D;
 #pragma unroll
     for (int ct = 0; ct < D / 16; ++ct) {
       if (dv) dv[orow + ct * 16 + c] = keep ? dva[ct][r] : 0.0f;
@@ -532,19 +590,43 @@ __global__ __launch_bounds__(256) void k_attn_bwd_kv_mfma(const float* __restric
 namespace {
 size_t scalar_fwd_lds(int64_t S, int64_t d) { return size_t((2 * S * d + S) * 4); }
 size_t scalar_bwd_lds(int64_t L, int64_t S, int64_t d) { return size_t((2 * L * d + 2 * S * d + S + 3 * L) * 4); }
-// The rows an MFMA kernel streams through LDS at a time: the fewest chunks of at most what fits
-// (two tiles of row stride d + 4 and three floats a row), of equal size in whole 16-row tiles.
-int64_t mfma_chunk(int64_t n, int64_t d) {
-  const int64_t most = int64_t(kLdsMax) / ((2 * (d + 4) + 3) * 4) / 16 * 16;
-  const int64_t chunks = (n + most - 1) / most;
-  return ((n + chunks - 1) / chunks + 15) / 16 * 16;
-}
-size_t mfma_fwd_lds(int64_t chunk, int64_t d) { return size_t((2 * chunk * (d + 4) + chunk) * 4); }
-size_t mfma_kv_lds(int64_t chunk, int64_t d) { return size_t((2 * chunk * (d + 4) + 3 * chunk) * 4); }
 bool head_ok(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128; }
-
-template <template <int> class K>
-struct ByD;
+// The streaming shape, from measured MI355X timings: problems of 4096 or more 16-row wave tiles
+// (BERT-base: 12288) take blocks of four waves and tiles of 32 rows (35 KB of LDS a block at
+// D = 64, four blocks a CU); smaller ones (BERT-tiny: 512) blocks of two waves and tiles of 64
+// rows (32 for D = 128), so that the few waves spread over more CUs with longer MFMA chains.
+struct AttnPlan { int T, W; };
+AttnPlan attn_plan(int64_t bh, int64_t rows, int64_t d) {
+  const int64_t tiles = bh * ((rows + 15) / 16);
+  if (tiles >= 4096) return {32, 4};
+  return {d >= 128 ? 32 : 64, 2};
+}
+#define MSX_BY_PLAN(plan, GO_D)                                 \
+  if ((plan).W == 4) GO_D(32, 4);                               \
+  else if ((plan).T == 64) GO_D(64, 2);                         \
+  else GO_D(32, 2);
+template <int D, int T, int W>
+void launch_fwd(hipStream_t s, dim3 grid, const float* q, const float* k, const float* v, const float* mask,
+                float* o, float* stats, int L, int S, int H, int heads, float scale) {
+  const size_t lds = size_t(stream_lds_floats(T, D, 1)) * 4;
+  MSX_LAUNCH((k_attn_fwd_mfma<D, T, W>), grid, dim3(64 * W), lds, s, q, k, v, mask, o, stats, L, S, H, heads, scale);
+}
+template <int D, int T, int W>
+void launch_bwd_q(hipStream_t s, dim3 grid, const float* q, const float* k, const float* v, const float* mask,
+                  const float* o, const float* stats, const float* g, float* dq, float* dsum, int L, int S, int H,
+                  int heads, float scale) {
+  const size_t lds = size_t(stream_lds_floats(T, D, 1)) * 4;
+  MSX_LAUNCH((k_attn_bwd_q_mfma<D, T, W>), grid, dim3(64 * W), lds, s, q, k, v, mask, o, stats, g, dq, dsum, L, S, H,
+             heads, scale);
+}
+template <int D, int T, int W>
+void launch_bwd_kv(hipStream_t s, dim3 grid, const float* q, const float* k, const float* v, const float* mask,
+                   const float* stats, const float* g, const float* dsum, float* dk, float* dv, int L, int S, int H,
+                   int heads, float scale) {
+  const size_t lds = size_t(stream_lds_floats(T, D, 3)) * 4;
+  MSX_LAUNCH((k_attn_bwd_kv_mfma<D, T, W>), grid, dim3(64 * W), lds, s, q, k, v, mask, stats, g, dsum, dk, dv, L, S, H,
+             heads, scale);
+}
 }  // namespace
 
 bool attention_mfma(int64_t L, int64_t S, int64_t d) {
@@ -569,12 +651,13 @@ void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v
   if (!head_ok(d) || L > S) refuse("attention head width or query rows");
   float scale = 1.0f / sqrtf(float(d));
   if (attention_mfma(L, S, d)) {
-    dim3 grid(unsigned(B * heads), unsigned((L + 16 * kWaves - 1) / (16 * kWaves)));
-    const int chunk = int(mfma_chunk(S, d));
-    size_t lds = mfma_fwd_lds(chunk, d);
-#define GO(D) MSX_LAUNCH(k_attn_fwd_mfma<D>, grid, dim3(64 * kWaves), lds, s, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale, chunk)
+    const AttnPlan plan = attn_plan(B * heads, L, d);
+    dim3 grid(unsigned(B * heads), unsigned((L + 16 * plan.W - 1) / (16 * plan.W)));
+#define GO_TW(T, W) launch_fwd<D, T, W>(s, grid, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale)
+#define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(plan, GO_TW) }
     MSX_BY_D(d, GO)
 #undef GO
+#undef GO_TW
     return;
   }
   if (scalar_fwd_lds(S, d) > kLdsMax || stats) refuse("attention shape outside the kernels' LDS budget");
@@ -593,24 +676,22 @@ void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v
   float scale = 1.0f / sqrtf(float(d));
   if (attention_mfma(L, S, d)) {
     if (!o || !stats || !dsum) refuse("the MFMA attention backward needs the forward output and statistics");
-    dim3 gq(unsigned(B * heads), unsigned((L + 16 * kWaves - 1) / (16 * kWaves)));
-    if (dq || dk || dv) {
-      // dQ (written only when asked) and the d_i the key pass reads.
-      float* dq_out = dq;
-      const int chunk = int(mfma_chunk(S, d));
-      size_t lq = mfma_fwd_lds(chunk, d);
-#define GO(D) MSX_LAUNCH(k_attn_bwd_q_mfma<D>, gq, dim3(64 * kWaves), lq, s, q, k, v, mask, o, stats, g, dq_out, dsum, int(L), int(S), int(H), int(heads), scale, chunk)
-      if (dq_out) { MSX_BY_D(d, GO) }
+    if (!dq) refuse("the MFMA attention backward computes d_i in its dQ pass: dQ is required");
+    const AttnPlan pq = attn_plan(B * heads, L, d);
+    dim3 gq(unsigned(B * heads), unsigned((L + 16 * pq.W - 1) / (16 * pq.W)));
+#define GO_TW(T, W) launch_bwd_q<D, T, W>(s, gq, q, k, v, mask, o, stats, g, dq, dsum, int(L), int(S), int(H), int(heads), scale)
+#define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(pq, GO_TW) }
+    MSX_BY_D(d, GO)
 #undef GO
-      if (!dq_out) refuse("the MFMA attention backward computes d_i in its dQ pass: dQ is required");
-    }
+#undef GO_TW
     if (dk || dv) {
-      dim3 gk(unsigned(B * heads), unsigned((S + 16 * kWaves - 1) / (16 * kWaves)));
-      const int chunk = int(mfma_chunk(L, d));
-      size_t lk = mfma_kv_lds(chunk, d);
-#define GO(D) MSX_LAUNCH(k_attn_bwd_kv_mfma<D>, gk, dim3(64 * kWaves), lk, s, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale, chunk)
+      const AttnPlan pk = attn_plan(B * heads, S, d);
+      dim3 gk(unsigned(B * heads), unsigned((S + 16 * pk.W - 1) / (16 * pk.W)));
+#define GO_TW(T, W) launch_bwd_kv<D, T, W>(s, gk, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale)
+#define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(pk, GO_TW) }
       MSX_BY_D(d, GO)
 #undef GO
+#undef GO_TW
     }
     return;
   }
@@ -628,12 +709,14 @@ void prepare_attention() {
       reinterpret_cast<const void*>(k_attn_fwd_scalar<64>), reinterpret_cast<const void*>(k_attn_fwd_scalar<128>),
       reinterpret_cast<const void*>(k_attn_bwd_scalar<16>), reinterpret_cast<const void*>(k_attn_bwd_scalar<32>),
       reinterpret_cast<const void*>(k_attn_bwd_scalar<64>), reinterpret_cast<const void*>(k_attn_bwd_scalar<128>),
-      reinterpret_cast<const void*>(k_attn_fwd_mfma<16>),   reinterpret_cast<const void*>(k_attn_fwd_mfma<32>),
-      reinterpret_cast<const void*>(k_attn_fwd_mfma<64>),   reinterpret_cast<const void*>(k_attn_fwd_mfma<128>),
-      reinterpret_cast<const void*>(k_attn_bwd_q_mfma<16>), reinterpret_cast<const void*>(k_attn_bwd_q_mfma<32>),
-      reinterpret_cast<const void*>(k_attn_bwd_q_mfma<64>), reinterpret_cast<const void*>(k_attn_bwd_q_mfma<128>),
-      reinterpret_cast<const void*>(k_attn_bwd_kv_mfma<16>), reinterpret_cast<const void*>(k_attn_bwd_kv_mfma<32>),
-      reinterpret_cast<const void*>(k_attn_bwd_kv_mfma<64>), reinterpret_cast<const void*>(k_attn_bwd_kv_mfma<128>)};
+#define MSX_ATTN_W(D, T, W)                                         \
+  reinterpret_cast<const void*>(k_attn_fwd_mfma<D, T, W>),          \
+      reinterpret_cast<const void*>(k_attn_bwd_q_mfma<D, T, W>),    \
+      reinterpret_cast<const void*>(k_attn_bwd_kv_mfma<D, T, W>)
+#define MSX_ATTN_K(D) MSX_ATTN_W(D, 32, 4), MSX_ATTN_W(D, 64, 2), MSX_ATTN_W(D, 32, 2)
+      MSX_ATTN_K(16), MSX_ATTN_K(32), MSX_ATTN_K(64), MSX_ATTN_K(128)};
+#undef MSX_ATTN_K
+#undef MSX_ATTN_W
   for (const void* kern : kernels) {
     hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, int(kLdsMax));
     if (e != hipSuccess) throw std::runtime_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));

@@ -223,6 +223,9 @@ def test_gelu_relu_elementwise(ctx, oracle):
     (2, 64, 256, 2, False),  # head width 128
     (2, 512, 128, 2, True),  # keys and queries streamed through LDS in two chunks
     (1, 320, 256, 2, False),  # head width 128 in three chunks, the last one shorter
+    # 4096 or more 16-row tiles: blocks of four waves streaming 32-row tiles, the last one of 16 rows
+    (16, 272, 256, 16, True),  # head width 16
+    (32, 176, 768, 12, True),  # head width 64 (the BERT-base heads)
 ])
 def test_attention_and_gradients(ctx, oracle, B, S, H, heads, masked):
     n = B * S * H
