@@ -47,6 +47,10 @@ struct Launch {
   // (crates/modelspec-core/src/ir/kernel.rs:1221, 1565): 2mnk for a matmul, 4 / 8 B heads L S d
   // for attention forward / backward, bytes of the values read and written otherwise.
   double flop = 0, bytes = 0;
+  // A launch whose outputs only the optimizer reads (a weight gradient): in a step it runs on the
+  // session's side stream, after work launched before it on the main stream, so that it overlaps
+  // the rest of the backward; the main stream joins it before the optimizer.
+  bool side = false;
 };
 
 struct RunStats {
@@ -120,6 +124,8 @@ class Session : public Engine {
   friend class Executor;
   int device_;
   hipStream_t stream_ = nullptr;
+  hipStream_t side_ = nullptr;  // weight-gradient launches (default priority, like stream_)
+  hipEvent_t fork_ = nullptr, join_ = nullptr;
   TrainingStep step_;
   Program forward_;
   uint64_t seed_;
@@ -183,6 +189,7 @@ class Executor {
   std::map<uint32_t, void*> token_;   // arena reservation per value
   std::map<uint32_t, void*> fixed_;   // values living in the session's arenas
   std::vector<Launch> launches_;
+  size_t join_at_ = SIZE_MAX;  // the first launch after the backward (it waits for the side stream)
   // device: written on the device by the corpus prologue, never staged by the host.
   struct InputSlot { std::string name; DType dtype; int64_t count; size_t offset; uint32_t id; bool device; };
   std::vector<InputSlot> inputs_;
