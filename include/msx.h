@@ -51,10 +51,20 @@ const char* msx_last_error(void);
 int msx_device_count(void);
 
 /* Compiles a built-in config (linear_regression, mlp_classifier, transformer_block, bert_tiny,
- * bert_cpu, bert_micro, block_micro, mlp_micro) to the printed training step and forward program
- * (ir/print.rs text). masked_rows / steps < 0 take the config's own. Free both with msx_free.
- * Replaces compile::compile_training_with, crates/modelspec-core/src/compile.rs:85-118. */
+ * bert_cpu, bert_micro, block_micro, mlp_micro, ...) or, for a name ending in ".mspec", the source
+ * file at that path (the front-end's subset of the reference language: a model of params and
+ * functions and one train block) to the printed training step and forward program (ir/print.rs
+ * text). masked_rows / steps < 0 take the config's own. Free both with msx_free. Every entry point
+ * below that takes a config name takes such a path too. Replaces compile::compile_training_with,
+ * crates/modelspec-core/src/compile.rs:85-118 (and, for a path, syntax::parse, types::check and
+ * lower::lower before it, crates/modelspec-core/src/syntax/parser.rs, types.rs, lower.rs:95-160);
+ * a refused source is MSX_E_INVALID with its E-SYNTAX-001 / E-NAME-001 / E-TYPE-001 / E-TRAIN-002
+ * code and line:column in msx_last_error. */
 int msx_compile_config(const char* config, int64_t masked_rows, int64_t steps, char** step_ir, char** forward_ir);
+
+/* The `steps` and `seed` a config (or .mspec source) trains with. Replaces reading them off the
+ * checked train block (crates/modelspec-core/src/hir.rs, HirTrain). */
+int msx_config_steps(const char* config, uint64_t* steps, uint64_t* seed);
 void msx_free(void* p);
 
 /* Parses a printed training step and prints it back (msx_free the result): the validation

@@ -103,8 +103,17 @@ def device_count():
     return lib().msx_device_count()
 
 
+CONFIG_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "configs")
+
+
+def config_file(name):
+    """The path of the .mspec source of a config this package ships (modelspec_amd/configs)."""
+    return os.path.join(CONFIG_DIR, name + ".mspec")
+
+
 def compile_config(name, masked_rows=-1, steps=-1):
-    """The printed training step and forward program of a built-in config."""
+    """The printed training step and forward program of a built-in config, or of the .mspec source
+    at the path `name` (a name ending in ".mspec")."""
     s, f = ctypes.c_void_p(), ctypes.c_void_p()
     _check(lib().msx_compile_config(name.encode(), masked_rows, steps, ctypes.byref(s), ctypes.byref(f)))
     try:
@@ -375,7 +384,14 @@ _STEPS = {"linear_regression": 500, "mnist_mlp": 1800, "mlp_classifier": 1000, "
 
 
 def config_steps(name):
-    return _STEPS[name]
+    """The steps a config (or the .mspec file at the path `name`) trains for."""
+    if name in _STEPS:
+        return _STEPS[name]
+    steps, seed = ctypes.c_uint64(), ctypes.c_uint64()
+    L = lib()
+    L.msx_config_steps.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]
+    _check(L.msx_config_steps(name.encode(), ctypes.byref(steps), ctypes.byref(seed)))
+    return steps.value
 
 
 def bench_config(ctx, name, warmup, steps, masked_rows=-1, profile_reps=1):

@@ -18,6 +18,7 @@ SOURCES = [
     "host/passes.cpp",
     "host/rng.cpp",
     "host/models.cpp",
+    "host/mspec.cpp",
     "host/runner.cpp",
     "host/json.cpp",
     "host/packed.cpp",

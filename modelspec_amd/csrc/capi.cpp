@@ -140,6 +140,15 @@ int msx_compile_config(const char* config, int64_t masked_rows, int64_t steps, c
   });
 }
 
+int msx_config_steps(const char* config, uint64_t* steps, uint64_t* seed) {
+  return guarded([&] {
+    msx::Compiled c = msx::compile_config(config, -1, -1);
+    if (steps) *steps = c.config.steps;
+    if (seed) *seed = c.config.seed;
+    return MSX_OK;
+  });
+}
+
 void msx_free(void* p) { std::free(p); }
 
 int msx_check_ir(const char* step_ir, char** normalized) {

@@ -2,6 +2,8 @@
 #include "models.h"
 
 #include <cmath>
+
+#include "mspec.h"
 #include <functional>
 
 namespace msx {
@@ -279,13 +281,27 @@ Compiled bert(const std::string& name, int64_t V, int64_t H, int64_t heads, int6
 
 }  // namespace
 
+Compiled compile_lowered(TrainConfig cfg, Program lowered, uint32_t loss, uint32_t prediction, Rule rule, float lr,
+                         const AdamWConfig& adamw) {
+  return finish(std::move(cfg), std::move(lowered), loss, prediction, rule, lr, adamw);
+}
+
+void apply_steps_override(Compiled& c, int64_t steps) {
+  if (steps < 0) return;
+  c.config.steps = uint64_t(steps);
+  if (c.step.rule == Rule::AdamW && c.step.adamw.warmup_steps >= c.config.steps && c.config.steps > 0)
+    c.step.adamw.warmup_steps = c.config.steps / 10;
+}
+
 std::vector<std::string> config_names() {
   return {"linear_regression", "mnist_mlp", "mlp_classifier", "transformer_block", "bert_tiny", "bert_cpu", "bert_micro",
           "block_micro", "mlp_micro", "bert_base", "bert_micro_mixed", "bert_mini_mixed"};
 }
 
 Compiled compile_config(const std::string& name, int64_t masked_rows, int64_t steps_override) {
-  auto steps = [&](uint64_t d) { return steps_override >= 0 ? uint64_t(steps_override) : d; };
+  const std::string ext = ".mspec";
+  if (name.size() > ext.size() && name.compare(name.size() - ext.size(), ext.size(), ext) == 0)
+    return compile_mspec(read_mspec(name), name, masked_rows, steps_override);
   Compiled c;
   if (name == "linear_regression") c = linear_regression();
   else if (name == "mnist_mlp") c = mnist_mlp();
@@ -311,13 +327,7 @@ Compiled compile_config(const std::string& name, int64_t masked_rows, int64_t st
     c.config.mixed = true;
   }
   else throw IrError("unknown config `" + name + "`");
-  if (steps_override >= 0) {
-    c.config.steps = steps(c.config.steps);
-    if (c.step.rule == Rule::AdamW && c.step.adamw.warmup_steps >= c.config.steps && c.config.steps > 0) {
-      uint64_t w = c.config.steps / 10;
-      c.step.adamw.warmup_steps = w;
-    }
-  }
+  apply_steps_override(c, steps_override);
   return c;
 }
 

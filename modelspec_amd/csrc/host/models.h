@@ -45,10 +45,20 @@ struct Compiled {
 };
 
 // The configs of this build by name: "linear_regression", "mlp_classifier",
-// "transformer_block", "bert_tiny", and small variants used by tests ("bert_micro").
+// "transformer_block", "bert_tiny", and small variants used by tests ("bert_micro"). A name
+// ending in ".mspec" is the path of a source file, compiled by the front-end (mspec.h).
 std::vector<std::string> config_names();
 Compiled compile_config(const std::string& name, int64_t masked_rows_override = -1,
                         int64_t steps_override = -1);
+
+// The compile pipeline after lowering: dead-code elimination, the masked-row gather when
+// cfg.masked_rows, autodiff of `loss`, the optimizer, and the dropout-free forward program whose
+// outputs are [loss, prediction].
+Compiled compile_lowered(TrainConfig cfg, Program lowered, uint32_t loss, uint32_t prediction, Rule rule, float lr,
+                         const AdamWConfig& adamw);
+// A run of `steps` (>= 0) instead of the config's: an AdamW warm-up that would not end before it
+// becomes a tenth of it.
+void apply_steps_override(Compiled& c, int64_t steps);
 
 // default_masked_rows of crates/modelspec-cli/src/train.rs:380-389.
 uint64_t default_masked_rows(uint64_t rows, double rate);
