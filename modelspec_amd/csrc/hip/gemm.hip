@@ -186,8 +186,8 @@ __device__ __forceinline__ void rows_store_h(_Float16* S, int t, const float4 (&
 }
 }  // namespace
 
-// The order a GEMM's tiles are handed to blocks: mt x nt tiles a split slice, `tiles` in all,
-// M tiles adjacent when m_fastest.
+// The order a GEMM's tiles are handed to blocks: mt x nt tiles a split slice, `tiles` in all (of
+// one problem of the group), M tiles adjacent when m_fastest.
 struct GemmOrder {
   uint32_t mt, nt, tiles;
   bool m_fastest;
@@ -197,11 +197,9 @@ struct GemmOrder {
 // (rows of their K slice contiguous) and multiplied by v_mfma_f32_16x16x32_f16 with f32
 // accumulation; K tiles of 32; everything else (split-K, epilogues, output) as in f32.
 template <bool TA, bool TB, int WM, int WN, int WK, bool VA, bool VB, bool H = false>
-__global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, const float* __restrict__ B,
-                                                float* __restrict__ C, GemmEpi epi, int64_t M,
-                                                int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-                                                int64_t kchunk, float* __restrict__ ws, float* __restrict__ colsum,
-                                                bool sum_a, bool vo, GemmOrder order) {
+__global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_t N, int64_t K, int64_t lda,
+                                                int64_t ldb, int64_t ldc, int64_t kchunk, bool sum_a, bool vo,
+                                                GemmOrder order) {
   constexpr int TM = 32 * WM, TN = 32 * WN, LA = TM + 16, LB = TN + 16, LC = TN + 4;
   constexpr int GA = TM * WK / 4, GB = TN * WK / 4;              // float4 groups a K tile
   constexpr int HA = (GA + 255) / 256, HB = (GB + 255) / 256;     // a thread's groups
@@ -220,8 +218,17 @@ __global__ __launch_bounds__(256) void k_gemm_w(const float* __restrict__ A, con
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // The tile of this block: consecutive blocks go to the 8 XCDs in turn, so block b takes tile
   // (b mod 8) * per + b / 8 of the grouped order, and each XCD runs one contiguous run of it.
-  const uint32_t per = gridDim.x / 8, t = (blockIdx.x % 8) * per + blockIdx.x / 8;
-  if (t >= order.tiles) return;
+  const uint32_t per = gridDim.x / 8, tg = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (tg >= order.tiles * ptrs.count) return;
+  // The problem of the group this block works on, and its tile in that problem's order.
+  const int q = int(tg / order.tiles);
+  const uint32_t t = tg - uint32_t(q) * order.tiles;
+  const float* __restrict__ A = ptrs.a[q];
+  const float* __restrict__ B = ptrs.b[q];
+  float* __restrict__ C = ptrs.c[q];
+  const GemmEpi epi = ptrs.epi[q];
+  float* __restrict__ ws = ptrs.ws[q];
+  float* __restrict__ colsum = ptrs.colsum[q];
   uint32_t tm, tn;
   const uint32_t tz = t / (order.mt * order.nt), tr = t % (order.mt * order.nt);
   if (order.m_fastest) {
@@ -441,45 +448,76 @@ int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs) {
   return 2;
 }
 
-void gemm(hipStream_t s, const GemmArgs& g) {
+void gemm(hipStream_t s, const GemmArgs& g) { gemm_group(s, &g, 1); }
+
+// A group of problems of one shape and configuration (the first one's), one launch: every
+// problem's pointers differ, nothing else.
+void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
+  if (count < 1 || count > kGemmGroupMax) bad("gemm group size");
+  const GemmArgs& g = list[0];
   if (g.m <= 0 || g.n <= 0) return;
   if (g.k <= 0) bad("gemm with k = 0");
+  for (int q = 1; q < count; ++q) {
+    const GemmArgs& o = list[q];
+    if (o.m != g.m || o.n != g.n || o.k != g.k || o.lda != g.lda || o.ldb != g.ldb || o.ldc != g.ldc || o.ta != g.ta ||
+        o.tb != g.tb || o.sum_a != g.sum_a || o.defer != g.defer || o.pad_a != g.pad_a || o.pad_b != g.pad_b ||
+        o.pad_c != g.pad_c || o.h16 != g.h16 || o.act != g.act || (o.colsum == nullptr) != (g.colsum == nullptr) ||
+        (o.bias == nullptr) != (g.bias == nullptr) || (o.addend == nullptr) != (g.addend == nullptr) ||
+        (o.workspace == nullptr) != (g.workspace == nullptr))
+      bad("gemm group of unlike problems");
+  }
   const SplitPlan plan = split_plan(g.m, g.n, g.k, g.defer, g.h16);
   const int split = plan.split;
   const int64_t chunk = plan.chunk;
-  float* ws = nullptr;
-  if (split > 1) {
-    if (!g.workspace || g.workspace_floats < gemm_workspace(g.m, g.n, g.k, g.colsum != nullptr, g.sum_a, g.defer, g.h16))
-      bad("gemm split-K workspace too small");
-    ws = g.workspace;
+  if (split > 1 && count > 1 && !g.defer) bad("a gemm group sums split-K slices by deferral only");
+  GemmPtrs ptrs{};
+  ptrs.count = count;
+  for (int q = 0; q < count; ++q) {
+    const GemmArgs& o = list[q];
+    float* ws = nullptr;
+    if (split > 1) {
+      if (!o.workspace || o.workspace_floats < gemm_workspace(o.m, o.n, o.k, o.colsum != nullptr, o.sum_a, o.defer, o.h16))
+        bad("gemm split-K workspace too small");
+      ws = o.workspace;
+    }
+    ptrs.a[q] = o.a;
+    ptrs.b[q] = o.b;
+    ptrs.c[q] = o.c;
+    ptrs.epi[q] = GemmEpi{o.bias, o.addend, o.pre_in, o.pre_out, o.act};
+    ptrs.ws[q] = ws;
+    ptrs.colsum[q] = o.colsum ? (ws ? ws + int64_t(split) * o.m * o.n : o.colsum) : nullptr;
   }
+  float* ws = ptrs.ws[0];
   // Tiles in the grouped order: split slices outermost; within a slice the tiles that share the
   // larger operand's panel are adjacent (M tiles of one column when B is the larger, N tiles of
   // one row otherwise), so that each XCD's L2 serves the panel to all of them.
   const int64_t nt = (g.n + 32 * plan.wn - 1) / (32 * plan.wn), mt = (g.m + 32 * plan.wm - 1) / (32 * plan.wm);
   const int64_t tiles = nt * mt * split;
-  if (tiles > (int64_t(1) << 30)) bad("gemm has too many tiles");
+  if (tiles * count > (int64_t(1) << 30)) bad("gemm has too many tiles");
   const GemmOrder order{uint32_t(mt), uint32_t(nt), uint32_t(tiles), g.n * g.k >= g.m * g.k};
-  const dim3 wgrid(unsigned((tiles + 7) / 8 * 8));
+  const dim3 wgrid(unsigned((tiles * count + 7) / 8 * 8));
   const int64_t width = g.sum_a ? g.m : g.n;
   if ((g.act == EPI_GELU_GRAD || g.act == EPI_RELU_GRAD) && !g.pre_in) bad("gemm activation gradient without its input");
   const GemmEpi epi{g.bias, g.addend, g.pre_in, g.pre_out, g.act};
-  // float4 output groups: every row the epilogue touches 16-byte aligned.
+  // float4 output groups: every row the epilogue touches 16-byte aligned (in every problem).
   auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  const bool vo = ws ? (g.n % 4 == 0 && a16(ws))
-                     : ((g.n % 4 == 0 || (g.pad_c && !g.act && !g.addend)) && g.ldc % 4 == 0 && a16(g.c) && a16(g.bias) &&
-                        a16(g.addend) && a16(g.pre_in) && a16(g.pre_out));
-  float* csum = g.colsum ? (ws ? ws + int64_t(split) * g.m * g.n : g.colsum) : nullptr;
+  bool vo = true, va = true, vb = true;
   // float4 loads need 16-byte aligned groups and a contiguous extent that is a multiple of 4.
   // (A zero-padded operand may be read up to its leading dimension.)
   auto aligned = [](const float* p, int64_t ld, int64_t extent) {
     return (reinterpret_cast<uintptr_t>(p) % 16 == 0) && ld % 4 == 0 && extent % 4 == 0;
   };
-  const bool va = aligned(g.a, g.lda, g.pad_a ? g.lda : (g.ta ? g.m : g.k));
-  const bool vb = aligned(g.b, g.ldb, g.pad_b ? g.ldb : (g.tb ? g.k : g.n));
+  for (int q = 0; q < count; ++q) {
+    const GemmArgs& o = list[q];
+    vo = vo && (ptrs.ws[q] ? (o.n % 4 == 0 && a16(ptrs.ws[q]))
+                           : ((o.n % 4 == 0 || (o.pad_c && !o.act && !o.addend)) && o.ldc % 4 == 0 && a16(o.c) &&
+                              a16(o.bias) && a16(o.addend) && a16(o.pre_in) && a16(o.pre_out)));
+    va = va && aligned(o.a, o.lda, o.pad_a ? o.lda : (o.ta ? o.m : o.k));
+    vb = vb && aligned(o.b, o.ldb, o.pad_b ? o.ldb : (o.tb ? o.k : o.n));
+  }
 #define MSX_WIDE_V(TA, TB, WM, WN, WK, VA, VB)                                                              \
-  MSX_LAUNCH((k_gemm_w<TA, TB, WM, WN, WK, VA, VB>), wgrid, dim3(256), 0, s, g.a, g.b, g.c, epi, g.m, g.n,   \
-                     g.k, g.lda, g.ldb, g.ldc, chunk, ws, csum, g.sum_a, vo, order)
+  MSX_LAUNCH((k_gemm_w<TA, TB, WM, WN, WK, VA, VB>), wgrid, dim3(256), 0, s, ptrs, g.m, g.n, g.k, g.lda,     \
+             g.ldb, g.ldc, chunk, g.sum_a, vo, order)
   // float4 variants for both operands aligned, or the right one only; scalar loads otherwise.
 #define MSX_WIDE(TA, TB, WM, WN, WK)                                \
   if (va && vb) MSX_WIDE_V(TA, TB, WM, WN, WK, true, true);         \
@@ -491,8 +529,8 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   else MSX_WIDE(TA, TB, 1, 1, 32);
   // The mixed-precision variants: the same tiles with f16 K tiles of 32.
 #define MSX_WIDE_HV(TA, TB, WM, WN, VA, VB)                                                                 \
-  MSX_LAUNCH((k_gemm_w<TA, TB, WM, WN, 32, VA, VB, true>), wgrid, dim3(256), 0, s, g.a, g.b, g.c, epi, g.m,  \
-             g.n, g.k, g.lda, g.ldb, g.ldc, chunk, ws, csum, g.sum_a, vo, order)
+  MSX_LAUNCH((k_gemm_w<TA, TB, WM, WN, 32, VA, VB, true>), wgrid, dim3(256), 0, s, ptrs, g.m, g.n, g.k,     \
+             g.lda, g.ldb, g.ldc, chunk, g.sum_a, vo, order)
 #define MSX_WIDE_H(TA, TB, WM, WN)                                  \
   if (va && vb) MSX_WIDE_HV(TA, TB, WM, WN, true, true);            \
   else if (vb) MSX_WIDE_HV(TA, TB, WM, WN, false, true);            \

@@ -54,6 +54,18 @@ struct GemmArgs {
 };
 enum GemmAct : int { EPI_NONE, EPI_GELU, EPI_RELU, EPI_GELU_GRAD, EPI_RELU_GRAD };
 struct GemmEpi { const float* bias; const float* addend; const float* pre_in; float* pre_out; int act; };
+// The pointers of each problem of a GEMM group (problems of one shape and configuration, one
+// launch; block b works on problem b / tiles of the order).
+constexpr int kGemmGroupMax = 4;
+struct GemmPtrs {
+  const float* a[kGemmGroupMax];
+  const float* b[kGemmGroupMax];
+  float* c[kGemmGroupMax];
+  GemmEpi epi[kGemmGroupMax];
+  float* ws[kGemmGroupMax];
+  float* colsum[kGemmGroupMax];
+  int count;
+};
 // The split-K factor the launcher uses (with `defer` as in GemmArgs).
 int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer = false, bool h16 = false);
 // Floats of workspace a gemm of this shape needs (0 without split-K): the slices' partial
@@ -63,6 +75,9 @@ int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum = false, boo
 // The column_finalize jobs that finish a deferred split-K gemm (0, 1 or 2 written to jobs).
 int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs);
 void gemm(hipStream_t s, const GemmArgs& g);
+// `count` (1 .. kGemmGroupMax) independent GEMMs that differ only in their pointers, in one
+// launch; split-K slices of a group are summed by deferral only.
+void gemm_group(hipStream_t s, const GemmArgs* list, int count);
 
 void transpose(hipStream_t s, const float* a, float* o, int64_t rows, int64_t cols);  // a [rows,cols] -> o [cols,rows]
 

@@ -560,7 +560,22 @@ void Executor::build() {
   input_token_ = arena_.reserve(std::max<size_t>(input_bytes_, 256));
 
   // Workspaces, reserved per launch now; resolved after commit.
-  struct Pending { std::function<Launch()> make; double flop = 0, bytes = 0; bool side = false; };
+  // A GEMM of the plan as the grouping pass sees it: its arguments (pointers resolved at launch)
+  // and the values it reads and writes.
+  struct GemmJob {
+    hk::GemmArgs g;
+    uint32_t asrc = 0, bsrc = 0, out_id = 0, id = 0;
+    int64_t bias_id = -1, cs_id = -1;
+    Epi epi;
+    void* ws = nullptr;
+    std::string what;
+  };
+  struct Pending {
+    std::function<Launch()> make;
+    double flop = 0, bytes = 0;
+    bool side = false;
+    std::vector<std::shared_ptr<GemmJob>> gemm;  // the GEMM(s) this launch runs, for grouping
+  };
   std::vector<Pending> pending;
   std::map<uint32_t, void*> ln_stats_tok;             // LN input value -> stats [rows, 2]
   std::map<uint32_t, void*> ce_stats_tok;             // logits value -> stats [rows, 2]
@@ -577,6 +592,32 @@ void Executor::build() {
   auto I = [this](uint32_t id) { return static_cast<int32_t*>(ptr(id)); };
   auto shape = [&](uint32_t v) -> const std::vector<int64_t>& { return p.node(v).ty.shape; };
   const uint64_t seed = s_.seed_;
+  // The launch of one GEMM or a group of like GEMMs (one hk::gemm_group call).
+  auto gemm_launch = [this, F, A](std::vector<std::shared_ptr<GemmJob>> jobs) {
+    return [this, F, A, jobs]() {
+      std::string what = jobs[0]->what;
+      for (size_t q = 1; q < jobs.size(); ++q) what += " | %" + std::to_string(jobs[q]->id);
+      return Launch{what, [this, F, A, jobs](hipStream_t s) {
+                      hk::GemmArgs list[hk::kGemmGroupMax];
+                      for (size_t q = 0; q < jobs.size(); ++q) {
+                        const GemmJob& j = *jobs[q];
+                        hk::GemmArgs a = j.g;
+                        a.a = F(j.asrc);
+                        a.b = F(j.bsrc);
+                        a.c = F(j.out_id);
+                        a.bias = j.bias_id >= 0 ? F(uint32_t(j.bias_id)) : nullptr;
+                        a.workspace = j.ws ? static_cast<float*>(A(j.ws)) : nullptr;
+                        a.colsum = j.cs_id >= 0 ? F(uint32_t(j.cs_id)) : nullptr;
+                        a.act = j.epi.act;
+                        if (j.epi.node != j.id && j.epi.act == hk::EPI_NONE) a.addend = F(uint32_t(j.epi.aux));
+                        if (j.epi.act == hk::EPI_GELU_GRAD || j.epi.act == hk::EPI_RELU_GRAD) a.pre_in = F(uint32_t(j.epi.aux));
+                        if (j.epi.act == hk::EPI_GELU || j.epi.act == hk::EPI_RELU) a.pre_out = F(j.id);
+                        list[q] = a;
+                      }
+                      hk::gemm_group(s, list, int(jobs.size()));
+                    }};
+    };
+  };
 
   // A packed corpus feeds the batch: the step's rows drawn and masked on the device, then the
   // masked-row gather of the selected rows, ahead of everything that reads them.
@@ -742,21 +783,18 @@ void Executor::build() {
         int64_t wsf = hk::gemm_workspace(g.m, g.n, g.k, cs_id >= 0, g.sum_a, g.defer, g.h16);
         void* ws = wsf > 0 ? R(size_t(wsf) * 4) : nullptr;
         g.workspace_floats = wsf;
-        push([=](hipStream_t s) {
-          hk::GemmArgs a = g;
-          a.a = F(asrc);
-          a.b = F(bsrc);
-          a.c = F(out_id);
-          a.bias = bias_id >= 0 ? F(uint32_t(bias_id)) : nullptr;
-          a.workspace = ws ? static_cast<float*>(A(ws)) : nullptr;
-          a.colsum = cs_id >= 0 ? F(uint32_t(cs_id)) : nullptr;
-          a.act = epi.act;
-          if (epi.node != id && epi.act == hk::EPI_NONE) a.addend = F(uint32_t(epi.aux));
-          if (epi.act == hk::EPI_GELU_GRAD || epi.act == hk::EPI_RELU_GRAD) a.pre_in = F(uint32_t(epi.aux));
-          if (epi.act == hk::EPI_GELU || epi.act == hk::EPI_RELU) a.pre_out = F(id);
-          hk::gemm(s, a);
-        });
-        if (is_step_ && g.defer) pending.back().side = true;
+        auto job = std::make_shared<GemmJob>();
+        job->g = g;
+        job->asrc = asrc;
+        job->bsrc = bsrc;
+        job->out_id = out_id;
+        job->id = id;
+        job->bias_id = bias_id;
+        job->cs_id = cs_id;
+        job->epi = epi;
+        job->ws = ws;
+        job->what = what;
+        pending.push_back({gemm_launch({job}), 0, 0, is_step_ && g.defer, {job}});
         if (g.defer && wsf > 0) {
           const int split = hk::gemm_split_for(g.m, g.n, g.k, true, g.h16);
           const int32_t mn = int32_t(g.m * g.n);
@@ -1113,6 +1151,83 @@ void Executor::build() {
       pending.back().flop = flop;
       pending.back().bytes = bytes;
     }
+  }
+  // GEMM groups: like GEMMs (one shape and configuration, split-K slices only by deferral) that
+  // read nothing the others write run as one launch. Main-stream GEMMs group when adjacent in the
+  // launch order (the group takes the first one's place: nothing runs between them). Side-stream
+  // GEMMs, whose outputs only the optimizer reads, group with later ones up to the join and take
+  // the last one's place (every member's operands exist there; the arena reuses no buffer within
+  // a step). The Q, K and V projections of a layer and their weight gradients are such groups.
+  {
+    auto like = [](const GemmJob& x, const GemmJob& y) {
+      const hk::GemmArgs &a = x.g, &b = y.g;
+      const int split = hk::gemm_split_for(a.m, a.n, a.k, a.defer, a.h16);
+      return a.m == b.m && a.n == b.n && a.k == b.k && a.lda == b.lda && a.ldb == b.ldb && a.ldc == b.ldc &&
+             a.ta == b.ta && a.tb == b.tb && a.sum_a == b.sum_a && a.defer == b.defer && a.pad_a == b.pad_a &&
+             a.pad_b == b.pad_b && a.pad_c == b.pad_c && a.h16 == b.h16 && x.epi.act == y.epi.act &&
+             (x.bias_id >= 0) == (y.bias_id >= 0) && (x.cs_id >= 0) == (y.cs_id >= 0) &&
+             (x.epi.node != x.id) == (y.epi.node != y.id) && (x.ws != nullptr) == (y.ws != nullptr) &&
+             (split == 1 || a.defer);
+    };
+    auto reads = [](const GemmJob& j) {
+      std::vector<int64_t> r{int64_t(j.asrc), int64_t(j.bsrc), j.bias_id};
+      if (j.epi.node != j.id) r.push_back(j.epi.aux);
+      return r;
+    };
+    auto writes = [](const GemmJob& j) {
+      std::vector<int64_t> w{int64_t(j.out_id), j.cs_id};
+      if (j.epi.node != j.id) w.push_back(int64_t(j.id));
+      return w;
+    };
+    auto independent = [&](const std::vector<std::shared_ptr<GemmJob>>& group, const GemmJob& y) {
+      for (auto& x : group) {
+        for (int64_t w : writes(*x))
+          for (int64_t r : reads(y))
+            if (w >= 0 && w == r) return false;
+        for (int64_t w : writes(y))
+          for (int64_t r : reads(*x))
+            if (w >= 0 && w == r) return false;
+      }
+      return true;
+    };
+    std::vector<Pending> merged;
+    std::vector<bool> taken(pending.size(), false);
+    for (size_t i = 0; i < pending.size(); ++i) {
+      if (taken[i]) continue;
+      Pending pd = pending[i];
+      if (pd.gemm.size() == 1 && !pd.side) {
+        size_t j = i + 1;
+        while (j < pending.size() && pd.gemm.size() < size_t(hk::kGemmGroupMax) && pending[j].gemm.size() == 1 &&
+               !pending[j].side && like(*pd.gemm[0], *pending[j].gemm[0]) && independent(pd.gemm, *pending[j].gemm[0])) {
+          pd.gemm.push_back(pending[j].gemm[0]);
+          pd.flop += pending[j].flop;
+          pd.bytes += pending[j].bytes;
+          taken[j++] = true;
+        }
+      } else if (pd.gemm.size() == 1 && pd.side) {
+        // Later like side GEMMs join this one; the group runs at the last member's place.
+        size_t last = i;
+        for (size_t j = i + 1; j < pending.size() && pd.gemm.size() < size_t(hk::kGemmGroupMax); ++j)
+          if (!taken[j] && pending[j].gemm.size() == 1 && pending[j].side && like(*pd.gemm[0], *pending[j].gemm[0]) &&
+              independent(pd.gemm, *pending[j].gemm[0])) {
+            pd.gemm.push_back(pending[j].gemm[0]);
+            pd.flop += pending[j].flop;
+            pd.bytes += pending[j].bytes;
+            taken[j] = true;
+            last = j;
+          }
+        if (last != i) {
+          pd.make = gemm_launch(pd.gemm);
+          // Re-insert at the last member's place: mark it and emit when the scan reaches it.
+          pending[last] = pd;
+          taken[last] = false;
+          continue;
+        }
+      }
+      if (pd.gemm.size() > 1) pd.make = gemm_launch(pd.gemm);
+      merged.push_back(pd);
+    }
+    pending = std::move(merged);
   }
   const size_t join_at = pending.size();
   // The reductions only the optimizer reads (LayerNorm gamma and beta sums, split-K weight
