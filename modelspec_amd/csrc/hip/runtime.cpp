@@ -575,6 +575,7 @@ void Executor::build() {
     double flop = 0, bytes = 0;
     bool side = false;
     std::vector<std::shared_ptr<GemmJob>> gemm;  // the GEMM(s) this launch runs, for grouping
+    bool concat = false;                          // gemm[] are the pairs of one K-concatenation
   };
   std::vector<Pending> pending;
   std::map<uint32_t, void*> ln_stats_tok;             // LN input value -> stats [rows, 2]
@@ -1225,6 +1226,65 @@ void Executor::build() {
         }
       }
       if (pd.gemm.size() > 1) pd.make = gemm_launch(pd.gemm);
+      merged.push_back(pd);
+    }
+    pending = std::move(merged);
+  }
+  // Chains of accumulated products: GEMM j's output plus an addend is GEMM j+1's addend, and
+  // nothing else reads it (the adjoint sum of the inputs of the Q, K and V projections, x0 W0^T
+  // + x1 W1^T + x2 W2^T + r). Adjacent like GEMMs of such a chain run as one GEMM over the
+  // K-concatenation of their pairs, r its addend: one f32 accumulation instead of three rounded
+  // partial sums, within the run tolerance of the reference's sum order.
+  {
+    auto chains = [&](const GemmJob& x, const GemmJob& y) {
+      const hk::GemmArgs &a = x.g, &b = y.g;
+      if (!(x.epi.node != x.id && x.epi.act == hk::EPI_NONE && y.epi.node != y.id && y.epi.act == hk::EPI_NONE)) return false;
+      if (y.epi.aux != int64_t(x.out_id) || x.bias_id >= 0 || y.bias_id >= 0 || x.cs_id >= 0 || y.cs_id >= 0) return false;
+      if (x.ws || y.ws || a.defer || b.defer || a.k % 32 != 0) return false;
+      if (!(a.m == b.m && a.n == b.n && a.k == b.k && a.lda == b.lda && a.ldb == b.ldb && a.ldc == b.ldc && a.ta == b.ta &&
+            a.tb == b.tb && a.pad_a == b.pad_a && a.pad_b == b.pad_b && a.pad_c == b.pad_c && a.h16 == b.h16))
+        return false;
+      const auto& readers = consumers[p.pos.at(x.out_id)];
+      return readers.size() == 1 && p.nodes[readers[0]].id == y.epi.node && !outputs.count(x.out_id) &&
+             !grad_values.count(x.out_id);
+    };
+    std::vector<Pending> merged;
+    for (size_t i = 0; i < pending.size(); ++i) {
+      Pending pd = pending[i];
+      if (pd.gemm.size() == 1 && !pd.side) {
+        size_t j = i + 1;
+        while (j < pending.size() && pd.gemm.size() < size_t(hk::kGemmGroupMax) && pending[j].gemm.size() == 1 &&
+               !pending[j].side && !pending[j].concat && chains(*pd.gemm.back(), *pending[j].gemm[0])) {
+          const int64_t total = pd.gemm[0]->g.k * int64_t(pd.gemm.size() + 1);
+          if (hk::gemm_split_for(pd.gemm[0]->g.m, pd.gemm[0]->g.n, total, false, pd.gemm[0]->g.h16) != 1) break;
+          pd.gemm.push_back(pending[j].gemm[0]);
+          pd.flop += pending[j].flop;
+          pd.bytes += pending[j].bytes;
+          ++j;
+        }
+        if (pd.gemm.size() > 1) {
+          pd.concat = true;
+          auto jobs = pd.gemm;
+          pd.make = [this, F, A, jobs]() {
+            std::string what = jobs[0]->what;
+            for (size_t q = 1; q < jobs.size(); ++q) what += " ++ %" + std::to_string(jobs[q]->id);
+            return Launch{what, [this, F, A, jobs](hipStream_t s) {
+                            hk::GemmArgs list[hk::kGemmGroupMax];
+                            for (size_t q = 0; q < jobs.size(); ++q) {
+                              list[q] = jobs[q]->g;
+                              list[q].a = F(jobs[q]->asrc);
+                              list[q].b = F(jobs[q]->bsrc);
+                            }
+                            // The chain's output and its first addend.
+                            list[0].c = F(jobs.back()->out_id);
+                            list[0].addend = F(uint32_t(jobs[0]->epi.aux));
+                            list[0].act = hk::EPI_NONE;
+                            hk::gemm_concat(s, list, int(jobs.size()));
+                          }};
+          };
+          i = j - 1;
+        }
+      }
       merged.push_back(pd);
     }
     pending = std::move(merged);
