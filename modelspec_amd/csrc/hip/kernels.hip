@@ -851,6 +851,120 @@ __global__ __launch_bounds__(kCeThreads) void k_ce_rows(const float* __restrict_
   }
 }
 
+// The same, persistent: one block a CU walks rows blockIdx.x, + gridDim.x, ..., the next row's
+// loads in flight while the current row is reduced and its gradient written (rows of 30522
+// classes: a block alone on its CU otherwise waits out each row's load latency between its
+// reductions). The weight sum is taken once a block.
+template <int NV>
+__global__ __launch_bounds__(kCeThreads) void k_ce_rows_p(const float* __restrict__ x, const int32_t* __restrict__ labels,
+                                                          const float* __restrict__ w, const float* __restrict__ g,
+                                                          float* __restrict__ stats, float* __restrict__ rowloss,
+                                                          float* __restrict__ grad, int64_t rows, int64_t v, int64_t ld) {
+  constexpr int W = kCeThreads / 64;
+  __shared__ float redm[W], reds[W];
+  __shared__ double dred[256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // Columns in 32 bits (v < 2^31 is checked by the launcher).
+  const int nq = int((v + 3) / 4), vi = int(v);
+  auto col = [&](int u, int c) { return 4 * (tid + kCeThreads * u) + c; };
+  float d = 0.0f;
+  if (grad) {
+    double dd = 0.0;
+    if (tid < 256)
+      for (int64_t i = tid; i < rows; i += 256) dd += double(w[i]);
+    if (tid < 256) dred[tid] = dd;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+      if (tid < o) dred[tid] += dred[tid + o];
+      __syncthreads();
+    }
+    d = float(dred[0]);
+  }
+  const float gs = grad ? g[0] : 0.0f;
+  v4f cur[NV], nxt[NV];
+  // Columns past the row hold -inf from the load on: the maximum, exp and sum below then need no
+  // per-column masks (each one a live lane mask), exp(-inf - m) is +0, and so is their gradient.
+  auto fetch = [&](v4f (&e)[NV], int64_t r) {
+    const v4f* row = reinterpret_cast<const v4f*>(x + r * ld);
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int q = tid + kCeThreads * u;
+      const v4f f = row[q < nq ? q : nq - 1];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) e[u][c] = 4 * q + c < vi ? f[c] : -INFINITY;
+    }
+  };
+  int64_t r = blockIdx.x;
+  if (r < rows) fetch(cur, r);
+  for (; r < rows; r += gridDim.x) {
+    // The row's label, weight and labelled logit are loaded first, so that their latency passes
+    // under the row's reductions rather than after them.
+    const int32_t lab = labels[r];
+    const float wr = grad ? w[r] : 0.0f;
+    const float xlab = (tid == 0 && rowloss && lab >= 0 && lab < v) ? x[r * ld + lab] : 0.0f;
+    const int64_t rn = r + gridDim.x;
+    if (rn < rows) fetch(nxt, rn);
+    float m = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) m = fmaxf(m, cur[u][c]);
+    m = wave_max(m);
+    if (lane == 0) redm[wave] = m;
+    __syncthreads();
+    m = redm[0];
+#pragma unroll
+    for (int i = 1; i < W; ++i) m = fmaxf(m, redm[i]);
+    float sum = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        cur[u][c] = expf(cur[u][c] - m);
+        sum += cur[u][c];
+      }
+    sum = wave_sum(sum);
+    if (lane == 0) reds[wave] = sum;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < W; i += 2) total += reds[i] + reds[i + 1];
+    if (tid == 0) {
+      stats[2 * r] = m;
+      stats[2 * r + 1] = total;
+      if (rowloss) rowloss[r] = m + logf(total) - xlab;
+    }
+    if (grad) {
+      const float scale = d == 0.0f ? 0.0f : gs * wr / d, inv = 1.0f / total;
+      v4f* out = reinterpret_cast<v4f*>(grad + r * ld);
+#pragma unroll
+      for (int u = 0; u < NV; ++u) {
+        const int q = tid + kCeThreads * u;
+        v4f o;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          o[c] = d == 0.0f ? 0.0f : scale * (cur[u][c] * inv - (col(u, c) == lab ? 1.0f : 0.0f));
+        }
+        if (q < nq) out[q] = o;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NV; ++u) cur[u] = nxt[u];
+  }
+}
+
+int cu_count() {
+  static int counts[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!counts[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    counts[dev] = n;
+  }
+  return counts[dev];
+}
+
 bool ce_rows_fits(int64_t v, int64_t ld) { return ld % 4 == 0 && (v + 3) / 4 <= int64_t(kCeThreads) * 8; }
 
 void ce_rows(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* g, float* stats,
@@ -861,7 +975,8 @@ void ce_rows(hipStream_t s, const float* logits, const int32_t* labels, const fl
     bad("cross_entropy row kernel needs float4-aligned rows of at most 32768 classes");
   if (grad && !g) bad("cross_entropy gradient without the upstream gradient");
   const int64_t per = ((v + 3) / 4 + kCeThreads - 1) / kCeThreads;
-#define MSX_CER(NV) MSX_LAUNCH(k_ce_rows<NV>, dim3(unsigned(rows)), dim3(kCeThreads), 0, s, logits, labels, w, g, \
+  const unsigned blocks = unsigned(std::min<int64_t>(rows, cu_count()));
+#define MSX_CER(NV) MSX_LAUNCH(k_ce_rows_p<NV>, dim3(blocks), dim3(kCeThreads), 0, s, logits, labels, w, g, \
                                        stats, rowloss, grad, rows, v, ld)
   if (per <= 2) MSX_CER(2);
   else if (per <= 4) MSX_CER(4);
