@@ -597,7 +597,7 @@ void Executor::build() {
   auto gemm_launch = [this, F, A](std::vector<std::shared_ptr<GemmJob>> jobs) {
     return [this, F, A, jobs]() {
       std::string what = jobs[0]->what;
-      for (size_t q = 1; q < jobs.size(); ++q) what += " | %" + std::to_string(jobs[q]->id);
+      for (size_t q = 1; q < jobs.size(); ++q) what += " & %" + std::to_string(jobs[q]->id);
       return Launch{what, [this, F, A, jobs](hipStream_t s) {
                       hk::GemmArgs list[hk::kGemmGroupMax];
                       for (size_t q = 0; q < jobs.size(); ++q) {
