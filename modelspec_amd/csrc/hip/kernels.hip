@@ -1185,30 +1185,57 @@ void mse(hipStream_t s, const float* a, const float* b, float* o, int64_t n) {
 }
 
 // ---------------------------------------------------------------------------------------------
-__global__ void k_adamw(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
-                        float* __restrict__ v, int64_t n, AdamWConsts k, const float* __restrict__ lr_t,
-                        const float* __restrict__ c1, const float* __restrict__ c2,
-                        const LossScaleState* __restrict__ ls) {
+// One element of the update, every operation rounded on its own (compiled without contraction).
+__device__ __forceinline__ void adamw_one(float& p, float g, float& m, float& v, const AdamWConsts& k, float lr, float b1,
+                                          float b2) {
+  const float m2 = k.beta1 * m + k.rest1 * g;
+  const float v2 = k.beta2 * v + (k.rest2 * g) * g;
+  const float dir = (m2 * b1) / (sqrtf(v2 * b2) + k.eps);
+  const float step = dir + k.decay * p;
+  p = p - lr * step;
+  m = m2;
+  v = v2;
+}
+// Four elements a thread as native 16-byte vectors (the arenas are 256-byte aligned), the tail of
+// n mod 4 elements by the first threads.
+__global__ __launch_bounds__(256) void k_adamw(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
+                                               float* __restrict__ v, int64_t n, AdamWConsts k,
+                                               const float* __restrict__ lr_t, const float* __restrict__ c1,
+                                               const float* __restrict__ c2, const LossScaleState* __restrict__ ls) {
   // A step whose scaled gradients overflowed makes no update (the loss scale halves instead).
   if (ls && ls->overflow) return;
   const float lr = lr_t[0], b1 = c1[0], b2 = c2[0], inv = ls ? ls->inv : 1.0f;
-  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  for (; i < n; i += int64_t(gridDim.x) * blockDim.x) {
-    const float gi = ls ? g[i] * inv : g[i], pi = p[i];
-    const float m2 = k.beta1 * m[i] + k.rest1 * gi;
-    const float v2 = k.beta2 * v[i] + (k.rest2 * gi) * gi;
-    const float dir = (m2 * b1) / (sqrtf(v2 * b2) + k.eps);
-    const float step = dir + k.decay * pi;
-    p[i] = pi - lr * step;
-    m[i] = m2;
-    v[i] = v2;
+  const bool scaled = ls != nullptr;
+  const int64_t quads = n / 4, stride = int64_t(gridDim.x) * blockDim.x;
+  const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  v4f* p4 = reinterpret_cast<v4f*>(p);
+  const v4f* g4 = reinterpret_cast<const v4f*>(g);
+  v4f* m4 = reinterpret_cast<v4f*>(m);
+  v4f* v4 = reinterpret_cast<v4f*>(v);
+  for (int64_t q = t; q < quads; q += stride) {
+    v4f pq = p4[q], gq = g4[q], mq = m4[q], vq = v4[q];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float pc = pq[c], mc = mq[c], vc = vq[c];
+      adamw_one(pc, scaled ? gq[c] * inv : gq[c], mc, vc, k, lr, b1, b2);
+      pq[c] = pc;
+      mq[c] = mc;
+      vq[c] = vc;
+    }
+    p4[q] = pq;
+    m4[q] = mq;
+    v4[q] = vq;
   }
+  for (int64_t i = quads * 4 + t; i < n; i += stride) adamw_one(p[i], scaled ? g[i] * inv : g[i], m[i], v[i], k, lr, b1, b2);
 }
 void adamw(hipStream_t s, float* p, const float* g, float* m, float* v, int64_t n, AdamWConsts k, const float* lr_t,
            const float* c1, const float* c2, const LossScaleState* ls) {
   if (n <= 0) return;
-  MSX_LAUNCH(k_adamw, dim3(std::min<unsigned>(blocks_for(n, 256), 16384)), dim3(256), 0, s, p, g, m, v, n, k,
-                     lr_t, c1, c2, ls);
+  for (const void* a : {static_cast<const void*>(p), static_cast<const void*>(g), static_cast<const void*>(m),
+                        static_cast<const void*>(v)})
+    if (reinterpret_cast<uintptr_t>(a) % 16) bad("AdamW arenas must be 16-byte aligned");
+  MSX_LAUNCH(k_adamw, dim3(std::min<unsigned>(blocks_for((n + 3) / 4, 256), 16384)), dim3(256), 0, s, p, g, m, v, n,
+             k, lr_t, c1, c2, ls);
 }
 
 __global__ void k_sgd(float* __restrict__ p, const float* __restrict__ g, int64_t n, const float* __restrict__ lr,
