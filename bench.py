@@ -50,7 +50,7 @@ def roofline(rows, mixed=False):
     """The launch with the largest mean time, and every launch's fraction of its roofline. Under
     mixed precision a GEMM's peak is the f16 MFMA one; attention stays f32 MFMA."""
     table = []
-    for what, ms, flop, nbytes, kernels in rows:
+    for what, ms, flop, nbytes, kernels, _ in rows:
         if ms <= 0:
             continue
         if flop > 0:
@@ -152,15 +152,16 @@ def main():
     top = table[0]
     if args.launches:
         with open(args.launches, "w") as f:
-            for what, ms, flop, nbytes, kernels in rows:
-                f.write(json.dumps({"launch": what, "ms": ms, "flop": flop, "bytes": nbytes, "kernels": kernels}) + "\n")
+            for what, ms, flop, nbytes, kernels, runs in rows:
+                f.write(json.dumps({"launch": what, "ms": ms, "flop": flop, "bytes": nbytes, "kernels": kernels,
+                                    "runs": runs}) + "\n")
     # Where the dominant launch's dispatches sit in a profiled step (rocprofv3 counter runs).
     first = 0
-    for what, _, _, _, kernels in rows:
+    for what, _, _, _, kernels, runs in rows:
         if what == top["launch"]:
             break
-        first += len(kernels.split("+")) if kernels else 0
-    dispatches = {"step_dispatches": sum(len(r[4].split("+")) if r[4] else 0 for r in rows), "first": first,
+        first += (len(kernels.split("+")) if kernels else 0) * runs
+    dispatches = {"step_dispatches": sum((len(r[4].split("+")) if r[4] else 0) * r[5] for r in rows), "first": first,
                   "count": len(top["kernel"].split("+")) if top["kernel"] else 0}
     traffic = measured_traffic(top["launch"]) if args.config == "bert_tiny" else None
     stats = ctx.stats()

@@ -395,8 +395,9 @@ def config_steps(name):
 
 
 def bench_config(ctx, name, warmup, steps, masked_rows=-1, profile_reps=1):
-    """(mean ms per step, [ms of each timed step], last loss, [(launch, ms, flop, bytes, kernels)]), kernels
-    the HIP kernels the launch dispatched, '+'-joined."""
+    """(mean ms per step, [ms of each timed step], last loss, [(launch, ms, flop, bytes, kernels, runs)]), kernels
+    the HIP kernels the launch dispatched, '+'-joined, runs how many times a profiled step ran it (a pure
+    launch, such as a GEMM, is timed over back-to-back repeats)."""
     L = lib()
     L.msx_bench_config.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint32,
                                    ctypes.POINTER(ctypes.c_double), ctypes.c_void_p, ctypes.POINTER(ctypes.c_float),
@@ -411,8 +412,8 @@ def bench_config(ctx, name, warmup, steps, masked_rows=-1, profile_reps=1):
         text = ctypes.string_at(rep).decode()
         L.msx_free(rep)
         for line in text.splitlines():
-            what, t, flop, nbytes, kernels = line.rsplit("\t", 4)
-            rows.append((what, float(t), float(flop), float(nbytes), kernels))
+            what, t, flop, nbytes, kernels, runs = line.rsplit("\t", 5)
+            rows.append((what, float(t), float(flop), float(nbytes), kernels, int(runs)))
     return ms.value, per_step[:steps].tolist(), loss.value, rows
 
 

@@ -688,7 +688,7 @@ int msx_bench_config(msx_ctx* ctx, const char* config, int64_t masked_rows, uint
       std::string text;
       for (auto& t : acc)
         text += t.what + "\t" + std::to_string(t.ms / reps) + "\t" + std::to_string(t.flop) + "\t" + std::to_string(t.bytes) +
-                "\t" + t.kernels + "\n";
+                "\t" + t.kernels + "\t" + std::to_string(t.runs) + "\n";
       *profile = dup(text);
     }
     return MSX_OK;

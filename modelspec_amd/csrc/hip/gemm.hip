@@ -219,12 +219,9 @@ __global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_
   // The tile of this block: consecutive blocks go to the 8 XCDs in turn, so block b takes tile
   // (b mod 8) * per + b / 8 of the grouped order, and each XCD runs one contiguous run of it.
   const uint32_t per = gridDim.x / 8, tg = (blockIdx.x % 8) * per + blockIdx.x / 8;
-  // A group (kseg 0): count problems; a K-concatenation (kseg > 0): one problem whose K runs
-  // through the count (A, B) pairs, kseg of K each.
-  const int64_t kseg = ptrs.kseg;
-  if (tg >= order.tiles * (kseg > 0 ? 1 : ptrs.count)) return;
+  if (tg >= order.tiles * ptrs.count) return;
   // The problem of the group this block works on, and its tile in that problem's order.
-  const int q = kseg > 0 ? 0 : int(tg / order.tiles);
+  const int q = int(tg / order.tiles);
   const uint32_t t = tg - uint32_t(q) * order.tiles;
   const float* __restrict__ A = ptrs.a[q];
   const float* __restrict__ B = ptrs.b[q];
@@ -256,22 +253,8 @@ __global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_
   static_assert((!RA || GA % 256 == 0) && (!RB || GB % 256 == 0), "row-vector staging takes whole groups a thread");
   auto ga = [&](int h) { return RA ? hk_group<TM, HA>(tid, h) : tid + 256 * h; };
   auto gb = [&](int h) { return RB ? hk_group<TN, HB>(tid, h) : tid + 256 * h; };
-  // The K tile at k0 of either operand: in a K-concatenation, of the pair holding k0 (a K tile
-  // never straddles two: kseg is a multiple of WK), at k0's offset within it.
-  auto load_a = [&](int64_t k0, int h) {
-    if (kseg > 0) {
-      const int64_t sg = k0 / kseg;
-      return wide_load<!TA, TM, WK, VA>(ptrs.a[sg], lda, M, kseg, m0, k0 - sg * kseg, ga(h));
-    }
-    return wide_load<!TA, TM, WK, VA>(A, lda, M, kend, m0, k0, ga(h));
-  };
-  auto load_b = [&](int64_t k0, int h) {
-    if (kseg > 0) {
-      const int64_t sg = k0 / kseg;
-      return wide_load<TB, TN, WK, VB>(ptrs.b[sg], ldb, N, kseg, n0, k0 - sg * kseg, gb(h));
-    }
-    return wide_load<TB, TN, WK, VB>(B, ldb, N, kend, n0, k0, gb(h));
-  };
+  auto load_a = [&](int64_t k0, int h) { return wide_load<!TA, TM, WK, VA>(A, lda, M, kend, m0, k0, ga(h)); };
+  auto load_b = [&](int64_t k0, int h) { return wide_load<TB, TN, WK, VB>(B, ldb, N, kend, n0, k0, gb(h)); };
   float4 ra[HA], rb[HB];
 #pragma unroll
   for (int h = 0; h < HA; ++h)
@@ -467,47 +450,15 @@ int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs) {
   return 2;
 }
 
-namespace {
-void gemm_run(hipStream_t s, const GemmArgs* list, int count, int64_t kseg, const float* const* as, const float* const* bs);
-}
-
 void gemm(hipStream_t s, const GemmArgs& g) { gemm_group(s, &g, 1); }
 
-void gemm_concat(hipStream_t s, const GemmArgs* list, int count) {
-  if (count < 2 || count > kGemmGroupMax) bad("gemm K-concatenation size");
-  GemmArgs g = list[0];
-  for (int q = 1; q < count; ++q) {
-    const GemmArgs& o = list[q];
-    if (o.m != g.m || o.n != g.n || o.k != g.k || o.lda != g.lda || o.ldb != g.ldb || o.ta != g.ta || o.tb != g.tb ||
-        o.pad_a != g.pad_a || o.pad_b != g.pad_b || o.h16 != g.h16)
-      bad("gemm K-concatenation of unlike pairs");
-  }
-  if (g.colsum || g.defer) bad("a gemm K-concatenation takes no column sums or deferral");
-  if (g.k % 32 != 0) bad("a gemm K-concatenation takes pairs of K a multiple of 32");
-  const int64_t kseg = g.k;
-  g.k = kseg * count;
-  if (split_plan(g.m, g.n, g.k, false, g.h16).split != 1) bad("a gemm K-concatenation runs without split-K");
-  const float* as[kGemmGroupMax];
-  const float* bs[kGemmGroupMax];
-  for (int q = 0; q < count; ++q) {
-    as[q] = list[q].a;
-    bs[q] = list[q].b;
-  }
-  gemm_run(s, &g, count, kseg, as, bs);
-}
-
 // A group of problems of one shape and configuration (the first one's), one launch: every
-void gemm_group(hipStream_t s, const GemmArgs* list, int count) { gemm_run(s, list, count, 0, nullptr, nullptr); }
-
-namespace {
-// One launch of a group (kseg 0: `count` problems, list[0 .. count)) or of a K-concatenation
-// (kseg > 0: list[0] the problem with K = count kseg, its pairs as[q], bs[q]).
-void gemm_run(hipStream_t s, const GemmArgs* list, int count, int64_t kseg, const float* const* as, const float* const* bs) {
+void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
   if (count < 1 || count > kGemmGroupMax) bad("gemm group size");
   const GemmArgs& g = list[0];
   if (g.m <= 0 || g.n <= 0) return;
   if (g.k <= 0) bad("gemm with k = 0");
-  for (int q = 1; q < (kseg > 0 ? 1 : count); ++q) {
+  for (int q = 1; q < count; ++q) {
     const GemmArgs& o = list[q];
     if (o.m != g.m || o.n != g.n || o.k != g.k || o.lda != g.lda || o.ldb != g.ldb || o.ldc != g.ldc || o.ta != g.ta ||
         o.tb != g.tb || o.sum_a != g.sum_a || o.defer != g.defer || o.pad_a != g.pad_a || o.pad_b != g.pad_b ||
@@ -522,8 +473,7 @@ void gemm_run(hipStream_t s, const GemmArgs* list, int count, int64_t kseg, cons
   if (split > 1 && count > 1 && !g.defer) bad("a gemm group sums split-K slices by deferral only");
   GemmPtrs ptrs{};
   ptrs.count = count;
-  ptrs.kseg = kseg;
-  const int problems = kseg > 0 ? 1 : count;
+  const int problems = count;
   for (int q = 0; q < problems; ++q) {
     const GemmArgs& o = list[q];
     float* ws = nullptr;
@@ -539,11 +489,6 @@ void gemm_run(hipStream_t s, const GemmArgs* list, int count, int64_t kseg, cons
     ptrs.ws[q] = ws;
     ptrs.colsum[q] = o.colsum ? (ws ? ws + int64_t(split) * o.m * o.n : o.colsum) : nullptr;
   }
-  if (kseg > 0)
-    for (int q = 0; q < count; ++q) {
-      ptrs.a[q] = as[q];
-      ptrs.b[q] = bs[q];
-    }
   float* ws = ptrs.ws[0];
   // Tiles in the grouped order: split slices outermost; within a slice the tiles that share the
   // larger operand's panel are adjacent (M tiles of one column when B is the larger, N tiles of
@@ -569,14 +514,8 @@ void gemm_run(hipStream_t s, const GemmArgs* list, int count, int64_t kseg, cons
     vo = vo && (ptrs.ws[q] ? (o.n % 4 == 0 && a16(ptrs.ws[q]))
                            : ((o.n % 4 == 0 || (o.pad_c && !o.act && !o.addend)) && o.ldc % 4 == 0 && a16(o.c) &&
                               a16(o.bias) && a16(o.addend) && a16(o.pre_in) && a16(o.pre_out)));
-    if (kseg == 0) {
-      va = va && aligned(o.a, o.lda, o.pad_a ? o.lda : (o.ta ? o.m : o.k));
-      vb = vb && aligned(o.b, o.ldb, o.pad_b ? o.ldb : (o.tb ? o.k : o.n));
-    }
-  }
-  for (int q = 0; q < (kseg > 0 ? count : 0); ++q) {
-    va = va && aligned(as[q], g.lda, g.pad_a ? g.lda : (g.ta ? g.m : kseg));
-    vb = vb && aligned(bs[q], g.ldb, g.pad_b ? g.ldb : (g.tb ? kseg : g.n));
+    va = va && aligned(o.a, o.lda, o.pad_a ? o.lda : (o.ta ? o.m : o.k));
+    vb = vb && aligned(o.b, o.ldb, o.pad_b ? o.ldb : (o.tb ? o.k : o.n));
   }
 #define MSX_WIDE_V(TA, TB, WM, WN, WK, VA, VB)                                                              \
   MSX_LAUNCH((k_gemm_w<TA, TB, WM, WN, WK, VA, VB>), wgrid, dim3(256), 0, s, ptrs, g.m, g.n, g.k, g.lda,     \
@@ -630,7 +569,5 @@ void gemm_run(hipStream_t s, const GemmArgs* list, int count, int64_t kseg, cons
 #undef MSX_SPLITK
   }
 }
-
-}  // namespace
 
 }  // namespace msx::hk

@@ -65,7 +65,6 @@ struct GemmPtrs {
   float* ws[kGemmGroupMax];
   float* colsum[kGemmGroupMax];
   int count;
-  int64_t kseg;  // 0: a group; > 0: one problem whose K runs through count (a, b) pairs of kseg each
 };
 // The split-K factor the launcher uses (with `defer` as in GemmArgs).
 int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer = false, bool h16 = false);
@@ -79,11 +78,6 @@ void gemm(hipStream_t s, const GemmArgs& g);
 // `count` (1 .. kGemmGroupMax) independent GEMMs that differ only in their pointers, in one
 // launch; split-K slices of a group are summed by deferral only.
 void gemm_group(hipStream_t s, const GemmArgs* list, int count);
-// One GEMM over the K-concatenation of `count` (2 .. kGemmGroupMax) pairs: C = epilogue(sum over q
-// of op(list[q].a) op(list[q].b)), one f32 accumulation in K order, pair 0 first; list[0] carries
-// the output and the epilogue, every pair the same m, n, k (a multiple of 32) and layout; no
-// split-K, column sums or deferral.
-void gemm_concat(hipStream_t s, const GemmArgs* list, int count);
 
 void transpose(hipStream_t s, const float* a, float* o, int64_t rows, int64_t cols);  // a [rows,cols] -> o [cols,rows]
 

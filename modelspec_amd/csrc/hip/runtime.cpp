@@ -575,7 +575,7 @@ void Executor::build() {
     double flop = 0, bytes = 0;
     bool side = false;
     std::vector<std::shared_ptr<GemmJob>> gemm;  // the GEMM(s) this launch runs, for grouping
-    bool concat = false;                          // gemm[] are the pairs of one K-concatenation
+    bool pure = false;
   };
   std::vector<Pending> pending;
   std::map<uint32_t, void*> ln_stats_tok;             // LN input value -> stats [rows, 2]
@@ -796,6 +796,7 @@ void Executor::build() {
         job->ws = ws;
         job->what = what;
         pending.push_back({gemm_launch({job}), 0, 0, is_step_ && g.defer, {job}});
+        pending.back().pure = true;
         if (g.defer && wsf > 0) {
           const int split = hk::gemm_split_for(g.m, g.n, g.k, true, g.h16);
           const int32_t mn = int32_t(g.m * g.n);
@@ -1017,6 +1018,7 @@ void Executor::build() {
           push([=](hipStream_t s) {
             hk::attention_fwd(s, F(q), F(kv), F(v), F(mask), F(id), st2 ? static_cast<float*>(A(st2)) : nullptr, B, L, S, H, heads);
           });
+          pending.back().pure = true;
           break;
         }
         auto key = o;
@@ -1055,6 +1057,7 @@ void Executor::build() {
           hk::attention_bwd(s, F(q), F(kv), F(v), F(mask), fo, stats_tok ? static_cast<float*>(A(stats_tok)) : nullptr, F(g), dq,
                             out(members[1]), out(members[2]), dsum ? static_cast<float*>(A(dsum)) : nullptr, B, L, S, H, heads);
         });
+        pending.back().pure = true;
         break;
       }
       case Op::CrossEntropy: case Op::CrossEntropyGrad: {
@@ -1230,65 +1233,6 @@ void Executor::build() {
     }
     pending = std::move(merged);
   }
-  // Chains of accumulated products: GEMM j's output plus an addend is GEMM j+1's addend, and
-  // nothing else reads it (the adjoint sum of the inputs of the Q, K and V projections, x0 W0^T
-  // + x1 W1^T + x2 W2^T + r). Adjacent like GEMMs of such a chain run as one GEMM over the
-  // K-concatenation of their pairs, r its addend: one f32 accumulation instead of three rounded
-  // partial sums, within the run tolerance of the reference's sum order.
-  {
-    auto chains = [&](const GemmJob& x, const GemmJob& y) {
-      const hk::GemmArgs &a = x.g, &b = y.g;
-      if (!(x.epi.node != x.id && x.epi.act == hk::EPI_NONE && y.epi.node != y.id && y.epi.act == hk::EPI_NONE)) return false;
-      if (y.epi.aux != int64_t(x.out_id) || x.bias_id >= 0 || y.bias_id >= 0 || x.cs_id >= 0 || y.cs_id >= 0) return false;
-      if (x.ws || y.ws || a.defer || b.defer || a.k % 32 != 0) return false;
-      if (!(a.m == b.m && a.n == b.n && a.k == b.k && a.lda == b.lda && a.ldb == b.ldb && a.ldc == b.ldc && a.ta == b.ta &&
-            a.tb == b.tb && a.pad_a == b.pad_a && a.pad_b == b.pad_b && a.pad_c == b.pad_c && a.h16 == b.h16))
-        return false;
-      const auto& readers = consumers[p.pos.at(x.out_id)];
-      return readers.size() == 1 && p.nodes[readers[0]].id == y.epi.node && !outputs.count(x.out_id) &&
-             !grad_values.count(x.out_id);
-    };
-    std::vector<Pending> merged;
-    for (size_t i = 0; i < pending.size(); ++i) {
-      Pending pd = pending[i];
-      if (pd.gemm.size() == 1 && !pd.side) {
-        size_t j = i + 1;
-        while (j < pending.size() && pd.gemm.size() < size_t(hk::kGemmGroupMax) && pending[j].gemm.size() == 1 &&
-               !pending[j].side && !pending[j].concat && chains(*pd.gemm.back(), *pending[j].gemm[0])) {
-          const int64_t total = pd.gemm[0]->g.k * int64_t(pd.gemm.size() + 1);
-          if (hk::gemm_split_for(pd.gemm[0]->g.m, pd.gemm[0]->g.n, total, false, pd.gemm[0]->g.h16) != 1) break;
-          pd.gemm.push_back(pending[j].gemm[0]);
-          pd.flop += pending[j].flop;
-          pd.bytes += pending[j].bytes;
-          ++j;
-        }
-        if (pd.gemm.size() > 1) {
-          pd.concat = true;
-          auto jobs = pd.gemm;
-          pd.make = [this, F, A, jobs]() {
-            std::string what = jobs[0]->what;
-            for (size_t q = 1; q < jobs.size(); ++q) what += " ++ %" + std::to_string(jobs[q]->id);
-            return Launch{what, [this, F, A, jobs](hipStream_t s) {
-                            hk::GemmArgs list[hk::kGemmGroupMax];
-                            for (size_t q = 0; q < jobs.size(); ++q) {
-                              list[q] = jobs[q]->g;
-                              list[q].a = F(jobs[q]->asrc);
-                              list[q].b = F(jobs[q]->bsrc);
-                            }
-                            // The chain's output and its first addend.
-                            list[0].c = F(jobs.back()->out_id);
-                            list[0].addend = F(uint32_t(jobs[0]->epi.aux));
-                            list[0].act = hk::EPI_NONE;
-                            hk::gemm_concat(s, list, int(jobs.size()));
-                          }};
-          };
-          i = j - 1;
-        }
-      }
-      merged.push_back(pd);
-    }
-    pending = std::move(merged);
-  }
   const size_t join_at = pending.size();
   // The reductions only the optimizer reads (LayerNorm gamma and beta sums, split-K weight
   // gradients and their bias sums), in one launch.
@@ -1358,6 +1302,7 @@ void Executor::build() {
     launches_.back().flop = pd.flop;
     launches_.back().bytes = pd.bytes;
     launches_.back().side = pd.side;
+    launches_.back().pure = pd.pure;
   }
   join_at_ = join_at;
 }
@@ -1709,27 +1654,41 @@ void Session::train_step(const StepInputs& in) {
   steps_since_reset_ += 1;
 }
 
+// Each launch of one eager step between its own pair of events on the step's stream; a pure
+// launch is then run kRepeats more times back to back between a second pair, and its time is
+// their mean (one launch's events also hold the dispatch gap before it, a repeat run amortizes it).
 std::vector<Session::Timed> Session::profile_step(const StepInputs& in) {
+  constexpr int kRepeats = 10;
   step_exec_->stage(in.batch);
   const auto& ls = step_exec_->launches();
-  std::vector<hipEvent_t> ev(ls.size() + 1);
+  std::vector<hipEvent_t> ev(4 * ls.size());
   for (auto& e : ev) hip_check(hipEventCreate(&e), "hipEventCreate");
-  hip_check(hipEventRecord(ev[0], stream_), "hipEventRecord");
   std::vector<std::vector<std::string>> kernels(ls.size());
   for (size_t i = 0; i < ls.size(); ++i) {
+    hip_check(hipEventRecord(ev[4 * i], stream_), "hipEventRecord");
     hk::kernel_log(&kernels[i]);
     ls[i].run(stream_);
     hk::kernel_log(nullptr);
-    hip_check(hipEventRecord(ev[i + 1], stream_), "hipEventRecord");
+    hip_check(hipEventRecord(ev[4 * i + 1], stream_), "hipEventRecord");
+    if (ls[i].pure) {
+      hip_check(hipEventRecord(ev[4 * i + 2], stream_), "hipEventRecord");
+      for (int r = 0; r < kRepeats; ++r) ls[i].run(stream_);
+      hip_check(hipEventRecord(ev[4 * i + 3], stream_), "hipEventRecord");
+    }
   }
   sync();
   std::vector<Timed> out;
   for (size_t i = 0; i < ls.size(); ++i) {
     float ms = 0;
-    hip_check(hipEventElapsedTime(&ms, ev[i], ev[i + 1]), "hipEventElapsedTime");
+    if (ls[i].pure) {
+      hip_check(hipEventElapsedTime(&ms, ev[4 * i + 2], ev[4 * i + 3]), "hipEventElapsedTime");
+      ms /= kRepeats;
+    } else {
+      hip_check(hipEventElapsedTime(&ms, ev[4 * i], ev[4 * i + 1]), "hipEventElapsedTime");
+    }
     std::string names;
     for (auto& kname : kernels[i]) names += (names.empty() ? "" : "+") + kname;
-    out.push_back({ls[i].what, ms, ls[i].flop, ls[i].bytes, names});
+    out.push_back({ls[i].what, ms, ls[i].flop, ls[i].bytes, names, ls[i].pure ? 1 + kRepeats : 1});
   }
   for (auto& e : ev) (void)hipEventDestroy(e);
   stats_.steps += 1;

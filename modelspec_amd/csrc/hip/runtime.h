@@ -51,6 +51,9 @@ struct Launch {
   // session's side stream, after work launched before it on the main stream, so that it overlaps
   // the rest of the backward; the main stream joins it before the optimizer.
   bool side = false;
+  // A launch whose outputs are none of its inputs (a GEMM, attention): running it again recomputes
+  // the same values, so a profile may time it over back-to-back repeats.
+  bool pure = false;
 };
 
 struct RunStats {
@@ -94,7 +97,8 @@ class Session : public Engine {
 
   // Runs the step plan eagerly (no graph) with one event pair around every launch; returns the
   // launches and their milliseconds for the current inputs (the step's update is applied).
-  struct Timed { std::string what; float ms; double flop, bytes; std::string kernels; };
+  // runs: how many times the profiled step ran the launch (1, or 1 + the repeats of a pure one).
+  struct Timed { std::string what; float ms; double flop, bytes; std::string kernels; int runs; };
   std::vector<Timed> profile_step(const StepInputs& in);
   void use_graph(bool on) { use_graph_ = on; }
   void sync();
