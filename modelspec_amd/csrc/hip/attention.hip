@@ -587,6 +587,392 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_kv_mfma(const float* __rest
 }
 
 // ---------------------------------------------------------------------------------------------
+// Mixed precision: the same kernels with their QK^T, P V, dS K, P^T dO and dS^T Q contractions on
+// the f16 MFMA (v_mfma_f32_16x16x16f16, f32 accumulation). Its lane layout is the f32 one's with four
+// consecutive K values a lane group (K 4g .. 4g + 3 where the f32 instruction has K = g): the four
+// probabilities (or dS values) a lane holds after a score MFMA, keys 4g + r of a 16-key tile, are
+// the A operand of the next contraction as they stand, and that contraction's B operand is read
+// from a transposed f16 copy of its tile (8 bytes a lane). Tiles are staged from f32 into f16 LDS
+// tiles: row-major (row stride D + 8 halves) for score operands, transposed (row stride T + 8)
+// for the others. Softmax statistics, exp and the running sums stay f32.
+namespace {
+__device__ __forceinline__ v4f mfma16h(v4h a, v4h b, v4f c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+__device__ __forceinline__ v4h to_h4(float a, float b, float c, float d) {
+  return v4h{_Float16(a), _Float16(b), _Float16(c), _Float16(d)};
+}
+}  // namespace
+
+// Rows 0 .. T of a fetched tile (fetch_pair's registers) into a row-major f16 tile (row stride KP)
+// and, when Xt is non-null, a transposed one (row stride VP: column d of the tile is row d).
+template <int D, int T, int NT, int PT>
+__device__ __forceinline__ void put_h(_Float16* Xr, _Float16* Xt, const v4f (&xv)[PT]) {
+  constexpr int KP = D + 8, VP = T + 8, Q = D / 4, G = T * Q;
+#pragma unroll
+  for (int p = 0; p < PT; ++p) {
+    const int e = int(threadIdx.x) + NT * p;
+    if (G % NT == 0 || e < G) {
+      const int row = e / Q, col = (e % Q) * 4;
+      const v4f x = xv[p];
+      if (Xr) *reinterpret_cast<v4h*>(Xr + row * KP + col) = to_h4(x[0], x[1], x[2], x[3]);
+      if (Xt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Xt[(col + j) * VP + row] = _Float16(x[j]);
+      }
+    }
+  }
+}
+
+// f16 scores of U tiles of 16 rows of the row-major tile R against the 16 rows whose fragments xh
+// a lane holds: acc[u][r] = sum over d of R[16 u + 4 g + r][d] x[c][d] (the f32 score_tiles' layout).
+template <int D, int U>
+__device__ __forceinline__ void score_tiles_h(const _Float16* R, const v4h (&xh)[D / 16], int nt, int c, int g,
+                                              v4f (&acc)[U]) {
+  constexpr int KP = D + 8;
+  const _Float16* rr[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    acc[u] = v4f{0, 0, 0, 0};
+    rr[u] = R + (16 * (u < nt ? u : nt - 1) + c) * KP + 4 * g;
+  }
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[u] = mfma16h(*reinterpret_cast<const v4h*>(rr[u] + 16 * t), xh[t], acc[u]);
+}
+
+// A row's D values at x as the f16 B fragments of a score MFMA: xh[t] = x[16 t + 4 g .. + 3].
+template <int D>
+__device__ __forceinline__ void row_fragments_h(const float* __restrict__ x, int g, v4h (&xh)[D / 16]) {
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) {
+    const v4f f = *reinterpret_cast<const v4f*>(x + 16 * t + 4 * g);
+    xh[t] = to_h4(f[0], f[1], f[2], f[3]);
+  }
+}
+
+template <int D, int T>
+constexpr int h16_lds_bytes(int row_tiles, int col_tiles, int extras) {
+  return 2 * (row_tiles * T * (D + 8) + col_tiles * D * (T + 8)) * 2 + 2 * extras * T * 4;
+}
+
+template <int D, int T, int W>
+__global__ __launch_bounds__(64 * W) void k_attn_fwd_h16(const float* __restrict__ q, const float* __restrict__ k,
+                                                         const float* __restrict__ v, const float* __restrict__ mask,
+                                                         float* __restrict__ o, float* __restrict__ stats, int L, int S,
+                                                         int H, int heads, float scale) {
+  constexpr int KP = D + 8, VP = T + 8, U = T / 16, NT = 64 * W, PT = tile_groups<D, T, NT>();
+  static_assert(NT >= T, "a thread a row of the mask");
+  extern __shared__ float sm[];
+  _Float16* const Kh = reinterpret_cast<_Float16*>(sm);  // buffer j: + j T KP
+  _Float16* const Vt = Kh + 2 * T * KP;                     // buffer j: + j D VP
+  float* const Mb = reinterpret_cast<float*>(Vt + 2 * D * VP);
+  const int b = blockIdx.x / heads, head = blockIdx.x % heads;
+  const int64_t kbase = int64_t(b) * S * H + head * D;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const int i0 = blockIdx.y * (16 * W) + wave * 16;
+  const bool active = i0 < L;
+  v4h qh[D / 16];
+  row_fragments_h<D>(q + (int64_t(b) * L + (active ? i0 : 0) + c) * H + head * D, g, qh);
+  const float* mrow = mask + int64_t(b) * S;
+  const int ntiles = (S + T - 1) / T, tid = int(threadIdx.x);
+  {
+    v4f kv[PT], vv[PT];
+    fetch_pair<D, T, NT>(kv, vv, k + kbase, v + kbase, H, S < T ? S : T);
+    const float mv = tid < T ? mrow[tid < S ? tid : S - 1] : 0.0f;
+    put_h<D, T, NT>(Kh, nullptr, kv);
+    put_h<D, T, NT>(nullptr, Vt, vv);
+    if (tid < T) Mb[tid] = mv;
+  }
+  __syncthreads();
+  float m = -INFINITY, l = 0.0f;
+  v4f oacc[D / 16];
+#pragma unroll
+  for (int ct = 0; ct < D / 16; ++ct) oacc[ct] = v4f{0, 0, 0, 0};
+  for (int t = 0; t < ntiles; ++t) {
+    const int j = t & 1, s0 = t * T, n = S - s0 < T ? S - s0 : T;
+    const bool more = t + 1 < ntiles;
+    v4f kv[PT], vv[PT];
+    float mv = 0.0f;
+    if (more) {
+      const int s1 = s0 + T, n1 = S - s1 < T ? S - s1 : T;
+      fetch_pair<D, T, NT>(kv, vv, k + kbase + int64_t(s1) * H, v + kbase + int64_t(s1) * H, H, n1);
+      if (tid < T) mv = mrow[s1 + (tid < n1 ? tid : n1 - 1)];
+    }
+    if (active) {
+      const _Float16* Ks = Kh + j * T * KP;
+      const _Float16* Vs = Vt + j * D * VP;
+      const float* Ms = Mb + j * T;
+      const int nt = n / 16;
+      v4f acc[U];
+      score_tiles_h<D, U>(Ks, qh, nt, c, g, acc);
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (u < nt && Ms[16 * u + 4 * g + r] != 0.0f) tmax = fmaxf(tmax, acc[u][r] * scale);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float mn = fmaxf(m, tmax);
+      const float alpha = mn == -INFINITY ? 1.0f : expf(m - mn);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) oacc[ct][r] *= ar;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (u >= nt) break;
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[r] = Ms[16 * u + 4 * g + r] != 0.0f ? expf(acc[u][r] * scale - m) : 0.0f;
+          l += p[r];
+        }
+        const v4h ph = to_h4(p[0], p[1], p[2], p[3]);
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct)
+          oacc[ct] = mfma16h(ph, *reinterpret_cast<const v4h*>(Vs + (16 * ct + c) * VP + 16 * u + 4 * g), oacc[ct]);
+      }
+    }
+    if (more) {
+      put_h<D, T, NT>(Kh + (j ^ 1) * T * KP, nullptr, kv);
+      put_h<D, T, NT>(nullptr, Vt + (j ^ 1) * D * VP, vv);
+      if (tid < T) Mb[(j ^ 1) * T + tid] = mv;
+    }
+    __syncthreads();
+  }
+  if (!active) return;
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float row_total = __shfl(l, 4 * g + r, 64);
+    const int64_t orow = (int64_t(b) * L + i0 + 4 * g + r) * H + head * D;
+#pragma unroll
+    for (int ct = 0; ct < D / 16; ++ct) o[orow + ct * 16 + c] = oacc[ct][r] / row_total;
+  }
+  if (stats && g == 0) {
+    const int64_t at = (int64_t(blockIdx.x) * L + i0 + c) * 2;
+    stats[at] = m;
+    stats[at + 1] = l;
+  }
+}
+
+template <int D, int T, int W>
+__global__ __launch_bounds__(64 * W) void k_attn_bwd_q_h16(const float* __restrict__ q, const float* __restrict__ k,
+                                                           const float* __restrict__ v, const float* __restrict__ mask,
+                                                           const float* __restrict__ o, const float* __restrict__ stats,
+                                                           const float* __restrict__ go, float* __restrict__ dq,
+                                                           float* __restrict__ dsum, int L, int S, int H, int heads,
+                                                           float scale) {
+  constexpr int KP = D + 8, VP = T + 8, U = T / 16, NT = 64 * W, PT = tile_groups<D, T, NT>();
+  static_assert(NT >= T, "a thread a row of the mask");
+  extern __shared__ float sm[];
+  _Float16* const Kh = reinterpret_cast<_Float16*>(sm);  // keys, row-major; buffer j: + j T KP
+  _Float16* const Vh = Kh + 2 * T * KP;                    // values, row-major
+  _Float16* const Kt = Vh + 2 * T * KP;                    // keys, transposed; buffer j: + j D VP
+  float* const Mb = reinterpret_cast<float*>(Kt + 2 * D * VP);
+  const int b = blockIdx.x / heads, head = blockIdx.x % heads;
+  const int64_t kbase = int64_t(b) * S * H + head * D;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const int i0 = blockIdx.y * (16 * W) + wave * 16;
+  const bool active = i0 < L;
+  const int64_t row = (int64_t(b) * L + (active ? i0 : 0) + c) * H + head * D;
+  float dd = 0.0f;
+#pragma unroll
+  for (int t = 0; t < D / 4; ++t) dd = __builtin_fmaf(go[row + g * (D / 4) + t], o[row + g * (D / 4) + t], dd);
+  dd += __shfl_xor(dd, 16, 64);
+  dd += __shfl_xor(dd, 32, 64);
+  const int64_t srow = int64_t(blockIdx.x) * L + (active ? i0 : 0) + c;
+  if (active && g == 0) dsum[srow] = dd;
+  const float mx = stats[2 * srow], total = stats[2 * srow + 1];
+  v4h qh[D / 16], gh[D / 16];
+  row_fragments_h<D>(q + row, g, qh);
+  row_fragments_h<D>(go + row, g, gh);
+  const float* mrow = mask + int64_t(b) * S;
+  const int ntiles = (S + T - 1) / T, tid = int(threadIdx.x);
+  {
+    v4f kv[PT], vv[PT];
+    fetch_pair<D, T, NT>(kv, vv, k + kbase, v + kbase, H, S < T ? S : T);
+    const float mv = tid < T ? mrow[tid < S ? tid : S - 1] : 0.0f;
+    put_h<D, T, NT>(Kh, Kt, kv);
+    put_h<D, T, NT>(Vh, nullptr, vv);
+    if (tid < T) Mb[tid] = mv;
+  }
+  __syncthreads();
+  v4f acc[D / 16];
+#pragma unroll
+  for (int ct = 0; ct < D / 16; ++ct) acc[ct] = v4f{0, 0, 0, 0};
+  for (int t = 0; t < ntiles; ++t) {
+    const int j = t & 1, s0 = t * T, n = S - s0 < T ? S - s0 : T;
+    const bool more = t + 1 < ntiles;
+    v4f kv[PT], vv[PT];
+    float mv = 0.0f;
+    if (more) {
+      const int s1 = s0 + T, n1 = S - s1 < T ? S - s1 : T;
+      fetch_pair<D, T, NT>(kv, vv, k + kbase + int64_t(s1) * H, v + kbase + int64_t(s1) * H, H, n1);
+      if (tid < T) mv = mrow[s1 + (tid < n1 ? tid : n1 - 1)];
+    }
+    if (active) {
+      const _Float16* Ks = Kh + j * T * KP;
+      const _Float16* Vs = Vh + j * T * KP;
+      const _Float16* Kts = Kt + j * D * VP;
+      const float* Ms = Mb + j * T;
+      const int nt = n / 16;
+      v4f st[U], dpt[U];
+      score_tiles_h<D, U>(Ks, qh, nt, c, g, st);
+      score_tiles_h<D, U>(Vs, gh, nt, c, g, dpt);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (u >= nt) break;
+        float ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = Ms[16 * u + 4 * g + r] != 0.0f ? expf(st[u][r] * scale - mx) / total : 0.0f;
+          ds[r] = p * (dpt[u][r] - dd);
+        }
+        const v4h dh = to_h4(ds[0], ds[1], ds[2], ds[3]);
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct)
+          acc[ct] = mfma16h(dh, *reinterpret_cast<const v4h*>(Kts + (16 * ct + c) * VP + 16 * u + 4 * g), acc[ct]);
+      }
+    }
+    if (more) {
+      put_h<D, T, NT>(Kh + (j ^ 1) * T * KP, Kt + (j ^ 1) * D * VP, kv);
+      put_h<D, T, NT>(Vh + (j ^ 1) * T * KP, nullptr, vv);
+      if (tid < T) Mb[(j ^ 1) * T + tid] = mv;
+    }
+    __syncthreads();
+  }
+  if (!active) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t orow = (int64_t(b) * L + i0 + 4 * g + r) * H + head * D;
+#pragma unroll
+    for (int ct = 0; ct < D / 16; ++ct) dq[orow + ct * 16 + c] = acc[ct][r] * scale;
+  }
+}
+
+template <int D, int T, int W>
+__global__ __launch_bounds__(64 * W) void k_attn_bwd_kv_h16(const float* __restrict__ q, const float* __restrict__ k,
+                                                            const float* __restrict__ v, const float* __restrict__ mask,
+                                                            const float* __restrict__ stats, const float* __restrict__ go,
+                                                            const float* __restrict__ dsum, float* __restrict__ dk,
+                                                            float* __restrict__ dv, int L, int S, int H, int heads,
+                                                            float scale) {
+  constexpr int KP = D + 8, VP = T + 8, U = T / 16, NT = 64 * W, PT = tile_groups<D, T, NT>();
+  static_assert(NT >= T, "a thread a row of the statistics");
+  extern __shared__ float sm[];
+  _Float16* const Qh = reinterpret_cast<_Float16*>(sm);  // queries, row-major; buffer j: + j T KP
+  _Float16* const Gh = Qh + 2 * T * KP;                    // output gradients, row-major
+  _Float16* const Qt = Gh + 2 * T * KP;                    // queries, transposed; buffer j: + j D VP
+  _Float16* const Gt = Qt + 2 * D * VP;                    // output gradients, transposed
+  float* const Sb = reinterpret_cast<float*>(Gt + 2 * D * VP);  // max, sum, d a query; buffer j: + j 3 T
+  const int b = blockIdx.x / heads, head = blockIdx.x % heads;
+  const int64_t qbase = int64_t(b) * L * H + head * D;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const int j0 = blockIdx.y * (16 * W) + wave * 16;
+  const bool active = j0 < S;
+  const int64_t krow = (int64_t(b) * S + (active ? j0 : 0) + c) * H + head * D;
+  const bool live = mask[int64_t(b) * S + (active ? j0 : 0) + c] != 0.0f;
+  v4h kh[D / 16], vh[D / 16];
+  row_fragments_h<D>(k + krow, g, kh);
+  row_fragments_h<D>(v + krow, g, vh);
+  const int64_t sbase = int64_t(blockIdx.x) * L;
+  const int ntiles = (L + T - 1) / T, tid = int(threadIdx.x);
+  auto fetch_stats = [&](float (&e)[3], int l0, int n) {
+    if (tid < T) {
+      const int64_t at = sbase + l0 + (tid < n ? tid : n - 1);
+      e[0] = stats[2 * at];
+      e[1] = stats[2 * at + 1];
+      e[2] = dsum[at];
+    }
+  };
+  auto put_stats = [&](float* X, const float (&e)[3]) {
+    if (tid < T) {
+      X[3 * tid] = e[0];
+      X[3 * tid + 1] = e[1];
+      X[3 * tid + 2] = e[2];
+    }
+  };
+  {
+    v4f qv[PT], gv[PT];
+    float e[3] = {0.0f, 0.0f, 0.0f};
+    fetch_pair<D, T, NT>(qv, gv, q + qbase, go + qbase, H, L < T ? L : T);
+    fetch_stats(e, 0, L < T ? L : T);
+    put_h<D, T, NT>(Qh, Qt, qv);
+    put_h<D, T, NT>(Gh, Gt, gv);
+    put_stats(Sb, e);
+  }
+  __syncthreads();
+  v4f dka[D / 16], dva[D / 16];
+#pragma unroll
+  for (int ct = 0; ct < D / 16; ++ct) { dka[ct] = v4f{0, 0, 0, 0}; dva[ct] = v4f{0, 0, 0, 0}; }
+  for (int t = 0; t < ntiles; ++t) {
+    const int j = t & 1, l0 = t * T, n = L - l0 < T ? L - l0 : T;
+    const bool more = t + 1 < ntiles;
+    v4f qv[PT], gv[PT];
+    float e[3] = {0.0f, 0.0f, 0.0f};
+    if (more) {
+      const int l1 = l0 + T, n1 = L - l1 < T ? L - l1 : T;
+      fetch_pair<D, T, NT>(qv, gv, q + qbase + int64_t(l1) * H, go + qbase + int64_t(l1) * H, H, n1);
+      fetch_stats(e, l1, n1);
+    }
+    if (active) {
+      const _Float16* Qs = Qh + j * T * KP;
+      const _Float16* Gs = Gh + j * T * KP;
+      const _Float16* Qts = Qt + j * D * VP;
+      const _Float16* Gts = Gt + j * D * VP;
+      const float* Ss = Sb + j * 3 * T;
+      const int nt = n / 16;
+      v4f s[U], dp[U];
+      score_tiles_h<D, U>(Qs, kh, nt, c, g, s);
+      score_tiles_h<D, U>(Gs, vh, nt, c, g, dp);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (u >= nt) break;
+        float p[4], ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float* st = Ss + 3 * (16 * u + 4 * g + r);
+          p[r] = live ? expf(s[u][r] * scale - st[0]) / st[1] : 0.0f;
+          ds[r] = p[r] * (dp[u][r] - st[2]);
+        }
+        const v4h ph = to_h4(p[0], p[1], p[2], p[3]), dh = to_h4(ds[0], ds[1], ds[2], ds[3]);
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) {
+          const int at = (16 * ct + c) * VP + 16 * u + 4 * g;
+          dva[ct] = mfma16h(ph, *reinterpret_cast<const v4h*>(Gts + at), dva[ct]);
+          dka[ct] = mfma16h(dh, *reinterpret_cast<const v4h*>(Qts + at), dka[ct]);
+        }
+      }
+    }
+    if (more) {
+      put_h<D, T, NT>(Qh + (j ^ 1) * T * KP, Qt + (j ^ 1) * D * VP, qv);
+      put_h<D, T, NT>(Gh + (j ^ 1) * T * KP, Gt + (j ^ 1) * D * VP, gv);
+      put_stats(Sb + (j ^ 1) * 3 * T, e);
+    }
+    __syncthreads();
+  }
+  if (!active) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int jj = j0 + 4 * g + r;
+    const bool keep = mask[int64_t(b) * S + jj] != 0.0f;
+    const int64_t orow = (int64_t(b) * S + jj) * H + head * D;
+#pragma unroll
+    for (int ct = 0; ct < D / 16; ++ct) {
+      if (dv) dv[orow + ct * 16 + c] = keep ? dva[ct][r] : 0.0f;
+      if (dk) dk[orow + ct * 16 + c] = keep ? dka[ct][r] * scale : 0.0f;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 namespace {
 size_t scalar_fwd_lds(int64_t S, int64_t d) { return size_t((2 * S * d + S) * 4); }
 size_t scalar_bwd_lds(int64_t L, int64_t S, int64_t d) { return size_t((2 * L * d + 2 * S * d + S + 3 * L) * 4); }
@@ -620,6 +1006,28 @@ void launch_bwd_q(hipStream_t s, dim3 grid, const float* q, const float* k, cons
              heads, scale);
 }
 template <int D, int T, int W>
+void launch_fwd_h(hipStream_t s, dim3 grid, const float* q, const float* k, const float* v, const float* mask,
+                  float* o, float* stats, int L, int S, int H, int heads, float scale) {
+  const size_t lds = size_t(h16_lds_bytes<D, T>(1, 1, 1));
+  MSX_LAUNCH((k_attn_fwd_h16<D, T, W>), grid, dim3(64 * W), lds, s, q, k, v, mask, o, stats, L, S, H, heads, scale);
+}
+template <int D, int T, int W>
+void launch_bwd_q_h(hipStream_t s, dim3 grid, const float* q, const float* k, const float* v, const float* mask,
+                    const float* o, const float* stats, const float* g, float* dq, float* dsum, int L, int S, int H,
+                    int heads, float scale) {
+  const size_t lds = size_t(h16_lds_bytes<D, T>(2, 1, 1));
+  MSX_LAUNCH((k_attn_bwd_q_h16<D, T, W>), grid, dim3(64 * W), lds, s, q, k, v, mask, o, stats, g, dq, dsum, L, S, H,
+             heads, scale);
+}
+template <int D, int T, int W>
+void launch_bwd_kv_h(hipStream_t s, dim3 grid, const float* q, const float* k, const float* v, const float* mask,
+                     const float* stats, const float* g, const float* dsum, float* dk, float* dv, int L, int S, int H,
+                     int heads, float scale) {
+  const size_t lds = size_t(h16_lds_bytes<D, T>(2, 2, 3));
+  MSX_LAUNCH((k_attn_bwd_kv_h16<D, T, W>), grid, dim3(64 * W), lds, s, q, k, v, mask, stats, g, dsum, dk, dv, L, S, H,
+             heads, scale);
+}
+template <int D, int T, int W>
 void launch_bwd_kv(hipStream_t s, dim3 grid, const float* q, const float* k, const float* v, const float* mask,
                    const float* stats, const float* g, const float* dsum, float* dk, float* dv, int L, int S, int H,
                    int heads, float scale) {
@@ -646,14 +1054,16 @@ bool attention_fits(int64_t s, int64_t d) {
   }
 
 void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v, const float* mask, float* o,
-                   float* stats, int64_t B, int64_t L, int64_t S, int64_t H, int64_t heads) {
+                   float* stats, int64_t B, int64_t L, int64_t S, int64_t H, int64_t heads, bool h16) {
   int64_t d = H / heads;
   if (!head_ok(d) || L > S) refuse("attention head width or query rows");
   float scale = 1.0f / sqrtf(float(d));
   if (attention_mfma(L, S, d)) {
     const AttnPlan plan = attn_plan(B * heads, L, d);
     dim3 grid(unsigned(B * heads), unsigned((L + 16 * plan.W - 1) / (16 * plan.W)));
-#define GO_TW(T, W) launch_fwd<D, T, W>(s, grid, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale)
+#define GO_TW(T, W)                                                                                         \
+  if (h16) launch_fwd_h<D, T, W>(s, grid, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale); \
+  else launch_fwd<D, T, W>(s, grid, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale)
 #define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(plan, GO_TW) }
     MSX_BY_D(d, GO)
 #undef GO
@@ -670,7 +1080,7 @@ void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v
 
 void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v, const float* mask, const float* o,
                    const float* stats, const float* g, float* dq, float* dk, float* dv, float* dsum, int64_t B,
-                   int64_t L, int64_t S, int64_t H, int64_t heads) {
+                   int64_t L, int64_t S, int64_t H, int64_t heads, bool h16) {
   int64_t d = H / heads;
   if (!head_ok(d) || L > S) refuse("attention head width or query rows");
   float scale = 1.0f / sqrtf(float(d));
@@ -679,7 +1089,9 @@ void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v
     if (!dq) refuse("the MFMA attention backward computes d_i in its dQ pass: dQ is required");
     const AttnPlan pq = attn_plan(B * heads, L, d);
     dim3 gq(unsigned(B * heads), unsigned((L + 16 * pq.W - 1) / (16 * pq.W)));
-#define GO_TW(T, W) launch_bwd_q<D, T, W>(s, gq, q, k, v, mask, o, stats, g, dq, dsum, int(L), int(S), int(H), int(heads), scale)
+#define GO_TW(T, W)                                                                                                  \
+  if (h16) launch_bwd_q_h<D, T, W>(s, gq, q, k, v, mask, o, stats, g, dq, dsum, int(L), int(S), int(H), int(heads), scale); \
+  else launch_bwd_q<D, T, W>(s, gq, q, k, v, mask, o, stats, g, dq, dsum, int(L), int(S), int(H), int(heads), scale)
 #define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(pq, GO_TW) }
     MSX_BY_D(d, GO)
 #undef GO
@@ -687,7 +1099,9 @@ void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v
     if (dk || dv) {
       const AttnPlan pk = attn_plan(B * heads, S, d);
       dim3 gk(unsigned(B * heads), unsigned((S + 16 * pk.W - 1) / (16 * pk.W)));
-#define GO_TW(T, W) launch_bwd_kv<D, T, W>(s, gk, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale)
+#define GO_TW(T, W)                                                                                                   \
+  if (h16) launch_bwd_kv_h<D, T, W>(s, gk, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale); \
+  else launch_bwd_kv<D, T, W>(s, gk, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale)
 #define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(pk, GO_TW) }
       MSX_BY_D(d, GO)
 #undef GO
@@ -713,9 +1127,16 @@ void prepare_attention() {
   reinterpret_cast<const void*>(k_attn_fwd_mfma<D, T, W>),          \
       reinterpret_cast<const void*>(k_attn_bwd_q_mfma<D, T, W>),    \
       reinterpret_cast<const void*>(k_attn_bwd_kv_mfma<D, T, W>)
-#define MSX_ATTN_K(D) MSX_ATTN_W(D, 32, 4), MSX_ATTN_W(D, 64, 2), MSX_ATTN_W(D, 32, 2)
+#define MSX_ATTN_H(D, T, W)                                         \
+  reinterpret_cast<const void*>(k_attn_fwd_h16<D, T, W>),           \
+      reinterpret_cast<const void*>(k_attn_bwd_q_h16<D, T, W>),     \
+      reinterpret_cast<const void*>(k_attn_bwd_kv_h16<D, T, W>)
+#define MSX_ATTN_K(D)                                                                            \
+  MSX_ATTN_W(D, 32, 4), MSX_ATTN_W(D, 64, 2), MSX_ATTN_W(D, 32, 2), MSX_ATTN_H(D, 32, 4), \
+      MSX_ATTN_H(D, 64, 2), MSX_ATTN_H(D, 32, 2)
       MSX_ATTN_K(16), MSX_ATTN_K(32), MSX_ATTN_K(64), MSX_ATTN_K(128)};
 #undef MSX_ATTN_K
+#undef MSX_ATTN_H
 #undef MSX_ATTN_W
   for (const void* kern : kernels) {
     hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, int(kLdsMax));

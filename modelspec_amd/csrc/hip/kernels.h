@@ -133,13 +133,14 @@ bool attention_fits(int64_t s, int64_t d);
 bool attention_mfma(int64_t L, int64_t S, int64_t d);  // the MFMA path runs (else the scalar one)
 // stats: [B*heads*L, 2] softmax maximum and sum per query (written when non-null; required by the
 // MFMA backward).
+// h16 (mixed precision): the MFMA path's contractions on the f16 MFMA with f32 accumulation.
 void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v, const float* mask, float* o,
-                   float* stats, int64_t B, int64_t L, int64_t S, int64_t H, int64_t heads);
+                   float* stats, int64_t B, int64_t L, int64_t S, int64_t H, int64_t heads, bool h16 = false);
 // Any of dk/dv may be null; the MFMA path needs dq, o (the forward's output), stats and dsum
 // ([B*heads*L] scratch).
 void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v, const float* mask, const float* o,
                    const float* stats, const float* g, float* dq, float* dk, float* dv, float* dsum, int64_t B,
-                   int64_t L, int64_t S, int64_t H, int64_t heads);
+                   int64_t L, int64_t S, int64_t H, int64_t heads, bool h16 = false);
 void prepare_attention();
 
 // Cross-entropy over logits [rows, v] with row pitch ld (>= v): stats = [rows, 2] (max, total);

@@ -1012,11 +1012,13 @@ void Executor::build() {
         if (p.node(mask).op == Op::Input) key_masks_.push_back(p.node(mask).name);
         auto fkey = std::vector<uint32_t>{q, kv, v, mask, uint32_t(heads)};
         bool mfma = hk::attention_mfma(L, S, H / heads);
+        const bool h16 = s_.opt_.mixed;  // mixed precision: the f16 MFMA
         if (x.op == Op::Attention) {
           void* st2 = mfma ? R(size_t(B * heads * L) * 8) : nullptr;
           attn_fwd[fkey] = {id, st2};
           push([=](hipStream_t s) {
-            hk::attention_fwd(s, F(q), F(kv), F(v), F(mask), F(id), st2 ? static_cast<float*>(A(st2)) : nullptr, B, L, S, H, heads);
+            hk::attention_fwd(s, F(q), F(kv), F(v), F(mask), F(id), st2 ? static_cast<float*>(A(st2)) : nullptr, B, L, S, H, heads,
+                              h16);
           });
           pending.back().pure = true;
           break;
@@ -1044,7 +1046,7 @@ void Executor::build() {
             stats_tok = R(size_t(B * heads * L) * 8);
             push([=](hipStream_t s) {
               hk::attention_fwd(s, F(q), F(kv), F(v), F(mask), static_cast<float*>(A(scratch_o)),
-                                static_cast<float*>(A(stats_tok)), B, L, S, H, heads);
+                                static_cast<float*>(A(stats_tok)), B, L, S, H, heads, h16);
             });
           }
           dsum = R(size_t(B * heads * L) * 4);
@@ -1055,7 +1057,8 @@ void Executor::build() {
           float* dq = members[0] >= 0 ? F(uint32_t(members[0])) : (dq_scratch ? static_cast<float*>(A(dq_scratch)) : nullptr);
           const float* fo = fwd_out >= 0 ? F(uint32_t(fwd_out)) : (scratch_o ? static_cast<float*>(A(scratch_o)) : nullptr);
           hk::attention_bwd(s, F(q), F(kv), F(v), F(mask), fo, stats_tok ? static_cast<float*>(A(stats_tok)) : nullptr, F(g), dq,
-                            out(members[1]), out(members[2]), dsum ? static_cast<float*>(A(dsum)) : nullptr, B, L, S, H, heads);
+                            out(members[1]), out(members[2]), dsum ? static_cast<float*>(A(dsum)) : nullptr, B, L, S, H, heads,
+                            h16);
         });
         pending.back().pure = true;
         break;

@@ -55,6 +55,42 @@ def test_a_mixed_gemm_is_the_product_of_f16_operands(mixed, m, k, n, ta, tb):
     assert np.all(np.abs(got - exact) <= 2.0 ** -10 * (np.abs(A) @ np.abs(Bm)) + 1e-6)
 
 
+@pytest.mark.parametrize("B,S,H,heads,masked", [(2, 128, 128, 2, True), (32, 176, 768, 12, True), (16, 272, 256, 16, False),
+                                                (2, 64, 256, 2, True)])
+def test_mixed_attention_and_gradients(mixed, oracle, B, S, H, heads, masked):
+    """Attention on the f16 MFMA (q, k, v, P, dO and dS rounded to f16, f32 accumulation and softmax
+    statistics) against the oracle's f32 values: within 1e-3 + 4e-3 (|c| + r), r the f32 test's
+    magnitude bound, i.e. a few f16 roundings (2^-11 each) of the terms."""
+    from test_gpu_ops import both
+    n = B * S * H
+    q, k, v, G = (fast_values(s, n, 0.5).reshape(B * S, H) for s in (12, 13, 14, 15))
+    mask = np.ones((B, S), np.float32)
+    if masked:
+        rng = np.random.default_rng(1)
+        mask[rng.random((B, S)) < 0.3] = 0.0
+        mask[:, 0] = 1.0
+    p = Prog()
+    qi, ki, vi = p.input("q", (B * S, H)), p.input("k", (B * S, H)), p.input("v", (B * S, H))
+    mi, Gi = p.input("mask", (B, S)), p.input("G", (B * S, H))
+    attr = f"[heads = {heads}]"
+    outs = [p.op("Attention", [qi, ki, vi, mi], (B * S, H), attr)]
+    for op in ("AttentionGradQ", "AttentionGradK", "AttentionGradV"):
+        outs.append(p.op(op, [qi, ki, vi, mi, Gi], (B * S, H), attr))
+    got, want = both(mixed, oracle, p.out(*outs), {"q": q, "k": k, "v": v, "mask": mask, "G": G}, (0, 1, 2, 3))
+    d = H // heads
+    r = np.abs(v).max() + np.abs(G).max() * (np.abs(q).max() + np.abs(k).max()) * np.sqrt(d) * 2
+    for idx, (g, w) in enumerate(zip(got, want)):
+        err = np.abs(g.astype(np.float64) - w) / (1e-3 + 4e-3 * (np.abs(w) + r))
+        assert np.all(err <= 1.0), (idx, float(err.max()))
+        # Not the f32 path: f16 rounding shows (the f32 kernels agree to 1e-5 + 1e-4 (|c| + r)).
+        if idx == 0:
+            assert np.max(np.abs(g - w)) > 1e-6
+    if masked:
+        dead = np.flatnonzero(mask.reshape(-1) == 0)
+        for g in (got[2], got[3]):
+            assert np.all(g.reshape(B * S, H)[dead] == 0)
+
+
 def test_a_mixed_run_tracks_the_f32_oracle(ctx, oracle):
     got_l, got_p, _ = ctx.train_config("bert_micro_mixed")
     want_l, want_p, _ = oracle.train("bert_micro")
