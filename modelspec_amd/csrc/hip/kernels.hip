@@ -361,10 +361,13 @@ void ln_backward(hipStream_t s, const float* x, const float* gamma, const float*
   const int cpl = int((h + 63) / 64);
 #define MSX_LNB(C) MSX_LAUNCH(k_ln_backward<C>, dim3(unsigned(blocks)), dim3(256), lds, s, x, gamma, g, stats, dx, \
                               partial, rows, h, per, dx2, post, pre, dsp, uint32_t(seed), uint32_t(seed >> 32))
+  // 12 columns a lane for H = 768 (BERT-base): 16 would hold a third of the registers idle and
+  // cost a wave of occupancy on a bandwidth-bound pass.
   if (cpl <= 1) MSX_LNB(1);
   else if (cpl <= 2) MSX_LNB(2);
   else if (cpl <= 4) MSX_LNB(4);
   else if (cpl <= 8) MSX_LNB(8);
+  else if (cpl <= 12) MSX_LNB(12);
   else MSX_LNB(16);
 #undef MSX_LNB
 }
