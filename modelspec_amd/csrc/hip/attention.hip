@@ -254,26 +254,33 @@ __device__ __forceinline__ void put_pair(float* X, float* Y, const v4f (&xv)[PT]
   }
 }
 // Floats of LDS a streaming kernel takes: two buffers of two T x (D + 4) tiles and E floats a row.
-constexpr int64_t stream_lds_floats(int64_t T, int64_t D, int64_t E) { return 2 * (2 * T * (D + 4) + E * T); }
+// Floats of LDS a streaming kernel takes: E floats a row for two buffers (first), then `buffers`
+// buffers of two T x (D + 4) tiles.
+constexpr int64_t stream_lds_floats(int64_t T, int64_t D, int64_t E, int64_t buffers = 2) {
+  return 2 * E * T + buffers * 2 * T * (D + 4);
+}
 
 // The forward, in one pass over the keys (online softmax): per tile, the scores of the wave's 16
 // queries against the tile's unmasked keys raise the running maximum m; the running sum l and
 // output O are rescaled by exp(m_old - m_new); P = exp(s - m) feeds the P V MFMA and l. Saves m
 // and l (the sum relative to the final maximum) per query for the backward.
-template <int D, int T, int W>
+template <int D, int T, int W, int KS = 1>
 __global__ __launch_bounds__(64 * W) void k_attn_fwd_mfma(const float* __restrict__ q, const float* __restrict__ k,
                                                        const float* __restrict__ v, const float* __restrict__ mask,
                                                        float* __restrict__ o, float* __restrict__ stats, int L, int S,
                                                        int H, int heads, float scale) {
-  constexpr int DP = D + 4, U = T / 16;
+  constexpr int DP = D + 4, U = T / 16 / KS;
+  static_assert(T % (16 * KS) == 0, "a wave's share of a tile is whole 16-row tiles");
   extern __shared__ float sm[];
-  float* const Kb = sm;                    // buffer j: Kb + j 2 T DP
-  float* const Vb = sm + T * DP;           // Vb + j 2 T DP
-  float* const Mb = sm + 4 * T * DP;       // Mb + j T
+  float* const Mb = sm;                    // Mb + j T (first: a one-tile launch has one tile buffer)
+  float* const Kb = sm + 2 * T;            // buffer j: Kb + j 2 T DP
+  float* const Vb = Kb + T * DP;           // Vb + j 2 T DP
   const int b = blockIdx.x / heads, head = blockIdx.x % heads;
   const int64_t kbase = int64_t(b) * S * H + head * D;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  const int i0 = blockIdx.y * (16 * W) + wave * 16;
+  // KS waves share a query tile, each taking rows [half U 16, (half + 1) U 16) of every key tile.
+  const int half = wave % KS;
+  const int i0 = blockIdx.y * (16 * W / KS) + (wave / KS) * 16;
   const bool active = i0 < L;
   const int64_t qrow = (int64_t(b) * L + (active ? i0 : 0) + c) * H + head * D;
   float qb[D / 4];
@@ -306,11 +313,11 @@ __global__ __launch_bounds__(64 * W) void k_attn_fwd_mfma(const float* __restric
       fetch_pair<D, T, NT>(kv, vv, k + kbase + int64_t(s1) * H, v + kbase + int64_t(s1) * H, H, n1);
       if (tid < T) mv = mrow[s1 + (tid < n1 ? tid : n1 - 1)];
     }
-    if (active) {
-      const float* Ks = Kb + j * 2 * T * DP;
-      const float* Vs = Vb + j * 2 * T * DP;
-      const float* Ms = Mb + j * T;
-      const int nt = n / 16;
+    const int nt = KS == 1 ? n / 16 : std::min(U, n / 16 - half * U);
+    if (active && nt > 0) {
+      const float* Ks = Kb + j * 2 * T * DP + half * U * 16 * DP;
+      const float* Vs = Vb + j * 2 * T * DP + half * U * 16 * DP;
+      const float* Ms = Mb + j * T + half * U * 16;
       v4f acc[U];
       score_tiles<D, U>(Ks, qb, nt, c, g, acc);
       float tmax = -INFINITY;
@@ -355,9 +362,37 @@ __global__ __launch_bounds__(64 * W) void k_attn_fwd_mfma(const float* __restric
     }
     __syncthreads();
   }
-  if (!active) return;
   l += __shfl_xor(l, 16, 64);
   l += __shfl_xor(l, 32, 64);
+  if constexpr (KS > 1) {
+    // The pair's second wave hands its maximum, sum and output rows over through LDS (the tiles
+    // are done with: the loop ended on a barrier); the first rescales both to the larger maximum.
+    static_assert(KS == 2, "two waves a query tile");
+    float* cb = sm + (wave / KS) * (32 + 16 * D);
+    if (half == 1 && active) {
+      if (g == 0) {
+        cb[c] = m;
+        cb[16 + c] = l;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) cb[32 + (4 * g + r) * D + 16 * ct + c] = oacc[ct][r];
+    }
+    __syncthreads();
+    if (half == 1 || !active) return;
+    const float m1 = cb[c], l1 = cb[16 + c], mn = fmaxf(m, m1);
+    const float a0 = m == -INFINITY ? 0.0f : expf(m - mn), a1 = m1 == -INFINITY ? 0.0f : expf(m1 - mn);
+    l = l * a0 + l1 * a1;
+    m = mn;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float b0 = __shfl(a0, 4 * g + r, 64), b1 = __shfl(a1, 4 * g + r, 64);
+#pragma unroll
+      for (int ct = 0; ct < D / 16; ++ct) oacc[ct][r] = oacc[ct][r] * b0 + cb[32 + (4 * g + r) * D + 16 * ct + c] * b1;
+    }
+  }
+  if (!active) return;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const float row_total = __shfl(l, 4 * g + r, 64);
@@ -373,22 +408,24 @@ __global__ __launch_bounds__(64 * W) void k_attn_fwd_mfma(const float* __restric
 }
 
 // dQ and d_i = rowsum(dO * O), per 16 query rows, streaming key and value tiles.
-template <int D, int T, int W>
+template <int D, int T, int W, int KS = 1>
 __global__ __launch_bounds__(64 * W) void k_attn_bwd_q_mfma(const float* __restrict__ q, const float* __restrict__ k,
                                                          const float* __restrict__ v, const float* __restrict__ mask,
                                                          const float* __restrict__ o, const float* __restrict__ stats,
                                                          const float* __restrict__ go, float* __restrict__ dq,
                                                          float* __restrict__ dsum, int L, int S, int H, int heads,
                                                          float scale) {
-  constexpr int DP = D + 4, U = T / 16;
+  constexpr int DP = D + 4, U = T / 16 / KS;
+  static_assert(T % (16 * KS) == 0, "a wave's share of a tile is whole 16-row tiles");
   extern __shared__ float sm[];
-  float* const Kb = sm;
-  float* const Vb = sm + T * DP;
-  float* const Mb = sm + 4 * T * DP;
+  float* const Mb = sm;
+  float* const Kb = sm + 2 * T;
+  float* const Vb = Kb + T * DP;
   const int b = blockIdx.x / heads, head = blockIdx.x % heads;
   const int64_t kbase = int64_t(b) * S * H + head * D;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  const int i0 = blockIdx.y * (16 * W) + wave * 16;
+  const int half = wave % KS;  // KS waves share a query tile, each a share of every key tile
+  const int i0 = blockIdx.y * (16 * W / KS) + (wave / KS) * 16;
   const bool active = i0 < L;
   const int64_t row = (int64_t(b) * L + (active ? i0 : 0) + c) * H + head * D;
   // d_i for query i0 + c: lane group g sums columns [g D/4, (g + 1) D/4).
@@ -398,7 +435,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_q_mfma(const float* __restr
   dd += __shfl_xor(dd, 16, 64);
   dd += __shfl_xor(dd, 32, 64);
   const int64_t srow = int64_t(blockIdx.x) * L + (active ? i0 : 0) + c;
-  if (active && g == 0) dsum[srow] = dd;
+  if (active && g == 0 && half == 0) dsum[srow] = dd;
   const float mx = stats[2 * srow], total = stats[2 * srow + 1];
   float qb[D / 4], gb[D / 4];
 #pragma unroll
@@ -429,11 +466,11 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_q_mfma(const float* __restr
       fetch_pair<D, T, NT>(kv, vv, k + kbase + int64_t(s1) * H, v + kbase + int64_t(s1) * H, H, n1);
       if (tid < T) mv = mrow[s1 + (tid < n1 ? tid : n1 - 1)];
     }
-    if (active) {
-      const float* Ks = Kb + j * 2 * T * DP;
-      const float* Vs = Vb + j * 2 * T * DP;
-      const float* Ms = Mb + j * T;
-      const int nt = n / 16;
+    const int nt = KS == 1 ? n / 16 : std::min(U, n / 16 - half * U);
+    if (active && nt > 0) {
+      const float* Ks = Kb + j * 2 * T * DP + half * U * 16 * DP;
+      const float* Vs = Vb + j * 2 * T * DP + half * U * 16 * DP;
+      const float* Ms = Mb + j * T + half * U * 16;
       v4f st[U], dpt[U];
       score_tiles<D, U>(Ks, qb, nt, c, g, st);
       score_tiles<D, U>(Vs, gb, nt, c, g, dpt);
@@ -460,6 +497,23 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_q_mfma(const float* __restr
     }
     __syncthreads();
   }
+  if constexpr (KS > 1) {
+    // The pair's partial dQ, the first wave's plus the second's.
+    static_assert(KS == 2, "two waves a query tile");
+    float* cb = sm + (wave / KS) * (16 * D);
+    if (half == 1 && active)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) cb[(4 * g + r) * D + 16 * ct + c] = acc[ct][r];
+    __syncthreads();
+    if (half == 1) return;
+    if (active)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) acc[ct][r] += cb[(4 * g + r) * D + 16 * ct + c];
+  }
   if (!active) return;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -471,22 +525,24 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_q_mfma(const float* __restr
 
 // dK and dV, per 16 key rows, streaming query and output-gradient tiles (with each query's
 // maximum, sum and d).
-template <int D, int T, int W>
+template <int D, int T, int W, int KS = 1>
 __global__ __launch_bounds__(64 * W) void k_attn_bwd_kv_mfma(const float* __restrict__ q, const float* __restrict__ k,
                                                           const float* __restrict__ v, const float* __restrict__ mask,
                                                           const float* __restrict__ stats, const float* __restrict__ go,
                                                           const float* __restrict__ dsum, float* __restrict__ dk,
                                                           float* __restrict__ dv, int L, int S, int H, int heads,
                                                           float scale) {
-  constexpr int DP = D + 4, U = T / 16;
+  constexpr int DP = D + 4, U = T / 16 / KS;
+  static_assert(T % (16 * KS) == 0, "a wave's share of a tile is whole 16-row tiles");
   extern __shared__ float sm[];
-  float* const Qb = sm;
-  float* const Gb = sm + T * DP;
-  float* const Sb = sm + 4 * T * DP;  // max, sum, d per query of the tile; buffer j at Sb + j 3 T
+  float* const Sb = sm;  // max, sum, d per query of the tile; buffer j at Sb + j 3 T
+  float* const Qb = sm + 6 * T;
+  float* const Gb = Qb + T * DP;
   const int b = blockIdx.x / heads, head = blockIdx.x % heads;
   const int64_t qbase = int64_t(b) * L * H + head * D;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  const int j0 = blockIdx.y * (16 * W) + wave * 16;
+  const int half = wave % KS;  // KS waves share a key tile, each a share of every query tile
+  const int j0 = blockIdx.y * (16 * W / KS) + (wave / KS) * 16;
   const bool active = j0 < S;
   const int64_t krow = (int64_t(b) * S + (active ? j0 : 0) + c) * H + head * D;
   const bool live = mask[int64_t(b) * S + (active ? j0 : 0) + c] != 0.0f;
@@ -536,11 +592,11 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_kv_mfma(const float* __rest
       fetch_pair<D, T, NT>(qv, gv, q + qbase + int64_t(l1) * H, go + qbase + int64_t(l1) * H, H, n1);
       fetch_stats(e, l1, n1);
     }
-    if (active) {
-      const float* Qs = Qb + j * 2 * T * DP;
-      const float* Gs = Gb + j * 2 * T * DP;
-      const float* Ss = Sb + j * 3 * T;
-      const int nt = n / 16;
+    const int nt = KS == 1 ? n / 16 : std::min(U, n / 16 - half * U);
+    if (active && nt > 0) {
+      const float* Qs = Qb + j * 2 * T * DP + half * U * 16 * DP;
+      const float* Gs = Gb + j * 2 * T * DP + half * U * 16 * DP;
+      const float* Ss = Sb + j * 3 * T + half * U * 16 * 3;
       v4f s[U], dp[U];
       score_tiles<D, U>(Qs, kb, nt, c, g, s);
       score_tiles<D, U>(Gs, vb, nt, c, g, dp);
@@ -571,6 +627,29 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_kv_mfma(const float* __rest
       put_stats(Sb + (j ^ 1) * 3 * T, e);
     }
     __syncthreads();
+  }
+  if constexpr (KS > 1) {
+    // The pair's partial dK and dV, the first wave's plus the second's.
+    static_assert(KS == 2, "two waves a key tile");
+    float* cb = sm + (wave / KS) * (32 * D);
+    if (half == 1 && active)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) {
+          cb[(4 * g + r) * D + 16 * ct + c] = dka[ct][r];
+          cb[16 * D + (4 * g + r) * D + 16 * ct + c] = dva[ct][r];
+        }
+    __syncthreads();
+    if (half == 1) return;
+    if (active)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) {
+          dka[ct][r] += cb[(4 * g + r) * D + 16 * ct + c];
+          dva[ct][r] += cb[16 * D + (4 * g + r) * D + 16 * ct + c];
+        }
   }
   if (!active) return;
 #pragma unroll
@@ -981,29 +1060,35 @@ bool head_ok(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128; }
 // (BERT-base: 12288) take blocks of four waves and tiles of 32 rows (35 KB of LDS a block at
 // D = 64, four blocks a CU); smaller ones (BERT-tiny: 512) blocks of two waves and tiles of 64
 // rows (32 for D = 128), so that the few waves spread over more CUs with longer MFMA chains.
-struct AttnPlan { int T, W; };
-AttnPlan attn_plan(int64_t bh, int64_t rows, int64_t d) {
+// ks: waves sharing a row tile (each a share of every streamed tile); one: the streamed side fits
+// one tile, so one LDS buffer and no prefetch. Small problems whose streamed side is at most 128
+// rows (BERT-tiny: 512 wave tiles on 1024 SIMDs) take one 128-row tile shared by two waves a row
+// tile, twice the waves (f32 only; on BERT-tiny the backward pair went from 34 to 27 us a layer
+// and the step from 0.955 to 0.935 ms).
+struct AttnPlan { int T, W, KS; bool one; };
+AttnPlan attn_plan(int64_t bh, int64_t rows, int64_t streamed, int64_t d, bool h16) {
   const int64_t tiles = bh * ((rows + 15) / 16);
-  if (tiles >= 4096) return {32, 4};
-  return {d >= 128 ? 32 : 64, 2};
+  AttnPlan p;
+  if (tiles >= 4096) p = {32, 4, 1, false};
+  else if (!h16 && streamed <= 128 && d <= 64) p = {128, 4, 2, false};
+  else p = {d >= 128 ? 32 : 64, 2, 1, false};
+  p.one = streamed <= p.T;
+  return p;
 }
-#define MSX_BY_PLAN(plan, GO_D)                                 \
-  if ((plan).W == 4) GO_D(32, 4);                               \
-  else if ((plan).T == 64) GO_D(64, 2);                         \
-  else GO_D(32, 2);
-template <int D, int T, int W>
-void launch_fwd(hipStream_t s, dim3 grid, const float* q, const float* k, const float* v, const float* mask,
+unsigned row_blocks(int64_t rows, const AttnPlan& p) { return unsigned((rows + 16 * p.W / p.KS - 1) / (16 * p.W / p.KS)); }
+template <int D, int T, int W, int KS>
+void launch_fwd(hipStream_t s, dim3 grid, bool one, const float* q, const float* k, const float* v, const float* mask,
                 float* o, float* stats, int L, int S, int H, int heads, float scale) {
-  const size_t lds = size_t(stream_lds_floats(T, D, 1)) * 4;
-  MSX_LAUNCH((k_attn_fwd_mfma<D, T, W>), grid, dim3(64 * W), lds, s, q, k, v, mask, o, stats, L, S, H, heads, scale);
+  const size_t lds = size_t(stream_lds_floats(T, D, 1, one ? 1 : 2)) * 4;
+  MSX_LAUNCH((k_attn_fwd_mfma<D, T, W, KS>), grid, dim3(64 * W), lds, s, q, k, v, mask, o, stats, L, S, H, heads, scale);
 }
-template <int D, int T, int W>
-void launch_bwd_q(hipStream_t s, dim3 grid, const float* q, const float* k, const float* v, const float* mask,
+template <int D, int T, int W, int KS>
+void launch_bwd_q(hipStream_t s, dim3 grid, bool one, const float* q, const float* k, const float* v, const float* mask,
                   const float* o, const float* stats, const float* g, float* dq, float* dsum, int L, int S, int H,
                   int heads, float scale) {
-  const size_t lds = size_t(stream_lds_floats(T, D, 1)) * 4;
-  MSX_LAUNCH((k_attn_bwd_q_mfma<D, T, W>), grid, dim3(64 * W), lds, s, q, k, v, mask, o, stats, g, dq, dsum, L, S, H,
-             heads, scale);
+  const size_t lds = size_t(stream_lds_floats(T, D, 1, one ? 1 : 2)) * 4;
+  MSX_LAUNCH((k_attn_bwd_q_mfma<D, T, W, KS>), grid, dim3(64 * W), lds, s, q, k, v, mask, o, stats, g, dq, dsum, L, S,
+             H, heads, scale);
 }
 template <int D, int T, int W>
 void launch_fwd_h(hipStream_t s, dim3 grid, const float* q, const float* k, const float* v, const float* mask,
@@ -1027,14 +1112,26 @@ void launch_bwd_kv_h(hipStream_t s, dim3 grid, const float* q, const float* k, c
   MSX_LAUNCH((k_attn_bwd_kv_h16<D, T, W>), grid, dim3(64 * W), lds, s, q, k, v, mask, stats, g, dsum, dk, dv, L, S, H,
              heads, scale);
 }
-template <int D, int T, int W>
-void launch_bwd_kv(hipStream_t s, dim3 grid, const float* q, const float* k, const float* v, const float* mask,
+template <int D, int T, int W, int KS>
+void launch_bwd_kv(hipStream_t s, dim3 grid, bool one, const float* q, const float* k, const float* v, const float* mask,
                    const float* stats, const float* g, const float* dsum, float* dk, float* dv, int L, int S, int H,
                    int heads, float scale) {
-  const size_t lds = size_t(stream_lds_floats(T, D, 3)) * 4;
-  MSX_LAUNCH((k_attn_bwd_kv_mfma<D, T, W>), grid, dim3(64 * W), lds, s, q, k, v, mask, stats, g, dsum, dk, dv, L, S, H,
-             heads, scale);
+  const size_t lds = size_t(stream_lds_floats(T, D, 3, one ? 1 : 2)) * 4;
+  MSX_LAUNCH((k_attn_bwd_kv_mfma<D, T, W, KS>), grid, dim3(64 * W), lds, s, q, k, v, mask, stats, g, dsum, dk, dv, L,
+             S, H, heads, scale);
 }
+// Dispatch on a plan: the f16 kernels (never split) or the f32 ones.
+#define MSX_BY_PLAN(plan, h16, GO_H, GO_F)                 \
+  if (h16) {                                               \
+    if ((plan).W == 4) GO_H(32, 4);                        \
+    else if ((plan).T == 64) GO_H(64, 2);                  \
+    else GO_H(32, 2);                                      \
+  } else {                                                 \
+    if ((plan).KS == 2) GO_F(128, 4, 2);                   \
+    else if ((plan).W == 4) GO_F(32, 4, 1);                \
+    else if ((plan).T == 64) GO_F(64, 2, 1);               \
+    else GO_F(32, 2, 1);                                   \
+  }
 }  // namespace
 
 bool attention_mfma(int64_t L, int64_t S, int64_t d) {
@@ -1059,15 +1156,16 @@ void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v
   if (!head_ok(d) || L > S) refuse("attention head width or query rows");
   float scale = 1.0f / sqrtf(float(d));
   if (attention_mfma(L, S, d)) {
-    const AttnPlan plan = attn_plan(B * heads, L, d);
-    dim3 grid(unsigned(B * heads), unsigned((L + 16 * plan.W - 1) / (16 * plan.W)));
-#define GO_TW(T, W)                                                                                         \
-  if (h16) launch_fwd_h<D, T, W>(s, grid, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale); \
-  else launch_fwd<D, T, W>(s, grid, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale)
-#define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(plan, GO_TW) }
+    const AttnPlan plan = attn_plan(B * heads, L, S, d, h16);
+    dim3 grid(unsigned(B * heads), row_blocks(L, plan));
+#define GO_H(T, W) launch_fwd_h<D, T, W>(s, grid, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale)
+#define GO_F(T, W, KS) \
+  launch_fwd<D, T, W, KS>(s, grid, plan.one, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale)
+#define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(plan, h16, GO_H, GO_F) }
     MSX_BY_D(d, GO)
 #undef GO
-#undef GO_TW
+#undef GO_F
+#undef GO_H
     return;
   }
   if (scalar_fwd_lds(S, d) > kLdsMax || stats) refuse("attention shape outside the kernels' LDS budget");
@@ -1087,25 +1185,31 @@ void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v
   if (attention_mfma(L, S, d)) {
     if (!o || !stats || !dsum) refuse("the MFMA attention backward needs the forward output and statistics");
     if (!dq) refuse("the MFMA attention backward computes d_i in its dQ pass: dQ is required");
-    const AttnPlan pq = attn_plan(B * heads, L, d);
-    dim3 gq(unsigned(B * heads), unsigned((L + 16 * pq.W - 1) / (16 * pq.W)));
-#define GO_TW(T, W)                                                                                                  \
-  if (h16) launch_bwd_q_h<D, T, W>(s, gq, q, k, v, mask, o, stats, g, dq, dsum, int(L), int(S), int(H), int(heads), scale); \
-  else launch_bwd_q<D, T, W>(s, gq, q, k, v, mask, o, stats, g, dq, dsum, int(L), int(S), int(H), int(heads), scale)
-#define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(pq, GO_TW) }
+    const AttnPlan pq = attn_plan(B * heads, L, S, d, h16);
+    dim3 gq(unsigned(B * heads), row_blocks(L, pq));
+#define GO_H(T, W) \
+  launch_bwd_q_h<D, T, W>(s, gq, q, k, v, mask, o, stats, g, dq, dsum, int(L), int(S), int(H), int(heads), scale)
+#define GO_F(T, W, KS)                                                                                            \
+  launch_bwd_q<D, T, W, KS>(s, gq, pq.one, q, k, v, mask, o, stats, g, dq, dsum, int(L), int(S), int(H), int(heads), \
+                            scale)
+#define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(pq, h16, GO_H, GO_F) }
     MSX_BY_D(d, GO)
 #undef GO
-#undef GO_TW
+#undef GO_F
+#undef GO_H
     if (dk || dv) {
-      const AttnPlan pk = attn_plan(B * heads, S, d);
-      dim3 gk(unsigned(B * heads), unsigned((S + 16 * pk.W - 1) / (16 * pk.W)));
-#define GO_TW(T, W)                                                                                                   \
-  if (h16) launch_bwd_kv_h<D, T, W>(s, gk, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale); \
-  else launch_bwd_kv<D, T, W>(s, gk, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale)
-#define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(pk, GO_TW) }
+      const AttnPlan pk = attn_plan(B * heads, S, L, d, h16);
+      dim3 gk(unsigned(B * heads), row_blocks(S, pk));
+#define GO_H(T, W) \
+  launch_bwd_kv_h<D, T, W>(s, gk, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), scale)
+#define GO_F(T, W, KS)                                                                                             \
+  launch_bwd_kv<D, T, W, KS>(s, gk, pk.one, q, k, v, mask, stats, g, dsum, dk, dv, int(L), int(S), int(H), int(heads), \
+                             scale)
+#define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(pk, h16, GO_H, GO_F) }
       MSX_BY_D(d, GO)
 #undef GO
-#undef GO_TW
+#undef GO_F
+#undef GO_H
     }
     return;
   }
@@ -1126,7 +1230,10 @@ void prepare_attention() {
 #define MSX_ATTN_W(D, T, W)                                         \
   reinterpret_cast<const void*>(k_attn_fwd_mfma<D, T, W>),          \
       reinterpret_cast<const void*>(k_attn_bwd_q_mfma<D, T, W>),    \
-      reinterpret_cast<const void*>(k_attn_bwd_kv_mfma<D, T, W>)
+      reinterpret_cast<const void*>(k_attn_bwd_kv_mfma<D, T, W>),   \
+      reinterpret_cast<const void*>(k_attn_fwd_mfma<D, 128, 4, 2>), \
+      reinterpret_cast<const void*>(k_attn_bwd_q_mfma<D, 128, 4, 2>), \
+      reinterpret_cast<const void*>(k_attn_bwd_kv_mfma<D, 128, 4, 2>)
 #define MSX_ATTN_H(D, T, W)                                         \
   reinterpret_cast<const void*>(k_attn_fwd_h16<D, T, W>),           \
       reinterpret_cast<const void*>(k_attn_bwd_q_h16<D, T, W>),     \
