@@ -132,10 +132,18 @@ __device__ __forceinline__ float4 wide_load(const float* __restrict__ P, int64_t
   }
   return make_float4(v[0], v[1], v[2], v[3]);
 }
+// The column a KC operand's element (row r, k) takes in its [k][row] LDS tile: r XOR a multiple of
+// 128 / WK chosen by k / 4. A float4 group's four stores (k .. k + 3 of one row) go to four rows of
+// the tile, and the 32 lanes of a half-wave hold 32 / (WK / 4) rows at WK / 4 k offsets each:
+// without the XOR the lanes of one row all land in one bank; with it the half-wave's stores fill
+// 32 distinct banks. The fragment reads keep 16 consecutive columns a row (the XOR permutes a
+// 16-aligned segment or swaps it with its neighbour), so they stay conflict-free.
+template <int WK>
+__device__ __forceinline__ int kc_swizzle(int k) { return (k >> 2) * (128 / WK); }
 template <bool KC, int R, int L, int WK>
 __device__ __forceinline__ void wide_store(float* S, int e, float4 v) {
   if (KC) {
-    const int r = e / (WK / 4), k = (e % (WK / 4)) * 4;
+    const int k = (e % (WK / 4)) * 4, r = (e / (WK / 4)) ^ kc_swizzle<WK>(k);
     S[(k + 0) * L + r] = v.x;
     S[(k + 1) * L + r] = v.y;
     S[(k + 2) * L + r] = v.z;
@@ -267,7 +275,9 @@ __global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_
   const int T = sum_a ? TM : TN;
   const bool sums = colsum != nullptr && (sum_a ? tn == 0 : tm == 0);
   const int sum_per = WK / (256 / T), sum_ld = sum_a ? LA : LB;
-  const int sum_off = (tid / T) * sum_per * sum_ld + tid % T;
+  // (A KC operand's columns are swizzled by k: its reads take the row's swizzle.)
+  const bool sum_kc = sum_a ? !TA : TB;
+  const int sum_k0 = (tid / T) * sum_per, sum_col = tid % T;
   float csum = 0.0f;
   int buf = 0;
   for (int64_t k0 = kbeg; k0 < kend; k0 += WK) {
@@ -326,20 +336,25 @@ __global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_
     const float* bs = Bs0 + buf * (WK * LB);
 #pragma unroll
     for (int kk = 0; kk < WK; kk += 4) {
-      const int ka = (kk + (lane >> 4)) * LA + wm + (lane & 15), kb = (kk + (lane >> 4)) * LB + wn + (lane & 15);
+      // A is KC unless TA, B when TB: their columns carry the swizzle of k = kk .. kk + 3.
+      const int swa = !TA ? kc_swizzle<WK>(kk) : 0, swb = TB ? kc_swizzle<WK>(kk) : 0;
+      const int ka = (kk + (lane >> 4)) * LA, kb = (kk + (lane >> 4)) * LB;
       float a[WM], b[WN];
 #pragma unroll
-      for (int i = 0; i < WM; ++i) a[i] = as[ka + 16 * i];
+      for (int i = 0; i < WM; ++i) a[i] = as[ka + ((wm + 16 * i + (lane & 15)) ^ swa)];
 #pragma unroll
-      for (int j = 0; j < WN; ++j) b[j] = bs[kb + 16 * j];
+      for (int j = 0; j < WN; ++j) b[j] = bs[kb + ((wn + 16 * j + (lane & 15)) ^ swb)];
 #pragma unroll
       for (int i = 0; i < WM; ++i)
 #pragma unroll
         for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
     }
     if (sums) {
-      const float* ss = (sum_a ? as : bs) + sum_off;
-      for (int j = 0; j < sum_per; ++j) csum += ss[j * sum_ld];
+      const float* ss = sum_a ? as : bs;
+      for (int j = 0; j < sum_per; ++j) {
+        const int kr = sum_k0 + j;
+        csum += ss[kr * sum_ld + (sum_kc ? sum_col ^ kc_swizzle<WK>(kr) : sum_col)];
+      }
     }
     buf = NB == 2 ? buf ^ 1 : 0;
   }
