@@ -12,10 +12,9 @@ dominant kernel (algorithmic FLOP or bytes per launch over its mean launch time,
 events on the run's stream), and the CPU oracle (a single-threaded restatement of the reference
 interpreter) timed on a bounded sample of the same step on this host.
 
-BERT-base (12 layers, H 768, 12 heads, FFN 3072, V 30522, batch 32, seq 512) runs its GEMMs as f16
-MFMA with f32 accumulation, f32 master weights and activations, and dynamic loss scaling from
-2^16; its GEMM launches are priced against the f16 MFMA peak, attention (f32 MFMA) against the
-f32 one. One oracle step of it is ~10^13 flop of scalar code (hours), so that line carries no CPU
+BERT-base (12 layers, H 768, 12 heads, FFN 3072, V 30522, batch 32, seq 512) runs its GEMMs and
+attention as f16 MFMA with f32 accumulation, f32 master weights and activations, and dynamic loss
+scaling from 2^16; its GEMM and f16 attention launches are priced against the f16 MFMA peak. One oracle step of it is ~10^13 flop of scalar code (hours), so that line carries no CPU
 baseline.
 """
 import argparse
@@ -48,13 +47,15 @@ WORKLOADS = {
 
 def roofline(rows, mixed=False):
     """The launch with the largest mean time, and every launch's fraction of its roofline. Under
-    mixed precision a GEMM's peak is the f16 MFMA one; attention stays f32 MFMA."""
+    mixed precision a GEMM's and the f16 attention kernels' (`k_attn_*_h16`) peak is the f16 MFMA
+    one; an f32 attention kernel is priced at the f32 MFMA peak."""
     table = []
     for what, ms, flop, nbytes, kernels, _ in rows:
         if ms <= 0:
             continue
         if flop > 0:
-            peak = PEAK_FP16_MFMA if mixed and "attn" not in kernels else PEAK_FP32_MFMA
+            f32_attn = "attn" in kernels and "_h16" not in kernels
+            peak = PEAK_FP16_MFMA if mixed and not f32_attn else PEAK_FP32_MFMA
             achieved, unit, bound = flop / (ms * 1e-3), "TFLOP/s", "mfma"
             achieved, peak = achieved / 1e12, peak / 1e12
         else:

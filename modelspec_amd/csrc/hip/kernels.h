@@ -82,10 +82,10 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count);
 void transpose(hipStream_t s, const float* a, float* o, int64_t rows, int64_t cols);  // a [rows,cols] -> o [cols,rows]
 
 void add_rows(hipStream_t s, const float* x, const float* bias, float* o, int64_t rows, int64_t h);
-// Partial column sums of x [rows, h] into partial [column_partial_chunks, h], finished by
-// column_finalize (a SumRows).
+// Partial column sums of x [rows, h] (rows ld floats apart; ld < 0: h) into partial
+// [column_partial_chunks, h], finished by column_finalize (a SumRows).
 int64_t column_partial_chunks(int64_t rows, int64_t h);
-void column_partial(hipStream_t s, const float* x, float* partial, int64_t rows, int64_t h);
+void column_partial(hipStream_t s, const float* x, float* partial, int64_t rows, int64_t h, int64_t ld = -1);
 
 // LayerNorm family, eps 1e-12. stats = [rows, 2] (mean, rstd).
 void ln_stats(hipStream_t s, const float* x, float* stats, int64_t rows, int64_t h);

@@ -106,10 +106,10 @@ void add_rows(hipStream_t s, const float* x, const float* b, float* o, int64_t r
   MSX_LAUNCH(k_add_rows, dim3(std::min<unsigned>(blocks_for(n, 256), 8192)), dim3(256), 0, s, x, b, o, n, h);
 }
 
-// Partial column sums: block (x, y) adds columns 256 x + t over the rows of chunk y, eight rows in
-// flight a thread, into partial[y, c]; column_finalize adds the chunks.
+// Partial column sums: block (x, y) adds columns 256 x + t over the rows of chunk y (rows ld
+// floats apart), eight rows in flight a thread, into partial[y, c]; column_finalize adds the chunks.
 __global__ __launch_bounds__(256) void k_column_partial(const float* __restrict__ x, float* __restrict__ partial,
-                                                        int64_t rows, int64_t h, int64_t rows_per) {
+                                                        int64_t rows, int64_t h, int64_t ld, int64_t rows_per) {
   const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
   const int64_t r0 = int64_t(blockIdx.y) * rows_per, r1 = std::min<int64_t>(rows, r0 + rows_per);
   if (c >= h) return;
@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void k_column_partial(const float* __restrict_
   for (int64_t r = r0; r < r1; r += 8) {
     float t[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) t[u] = x[(r + u < r1 ? r + u : r1 - 1) * h + c];
+    for (int u = 0; u < 8; ++u) t[u] = x[(r + u < r1 ? r + u : r1 - 1) * ld + c];
 #pragma unroll
     for (int u = 0; u < 8; ++u)
       if (r + u < r1) s += t[u];
@@ -132,13 +132,15 @@ int64_t column_partial_chunks(int64_t rows, int64_t h) {
   const int64_t per = (rows + chunks - 1) / chunks;
   return std::max<int64_t>(1, (rows + per - 1) / per);
 }
-void column_partial(hipStream_t s, const float* x, float* partial, int64_t rows, int64_t h) {
+void column_partial(hipStream_t s, const float* x, float* partial, int64_t rows, int64_t h, int64_t ld) {
   if (rows <= 0 || h <= 0) return;
+  if (ld < 0) ld = h;
+  if (ld < h) bad("column partial pitch below its width");
   const int64_t chunks = column_partial_chunks(rows, h);
   const int64_t per = (rows + chunks - 1) / chunks;
   if ((rows + per - 1) / per != chunks) bad("column partial chunking");
   MSX_LAUNCH(k_column_partial, dim3(unsigned((h + 255) / 256), unsigned(chunks)), dim3(256), 0, s, x, partial,
-                     rows, h, per);
+                     rows, h, ld, per);
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -461,7 +461,8 @@ void Executor::build() {
       } else if (cn.op == Op::MatMul) {
       } else if (cn.op == Op::Transpose && folded.count(cn.id)) {
         for (auto c2 : consumers[c]) readers = readers && p.nodes[c2].op == Op::MatMul;
-      } else if (cn.op == Op::SumRows && colsum_fused.count(cn.id)) {
+      } else if (cn.op == Op::SumRows && (colsum_fused.count(cn.id) || !ln_member.count(cn.id))) {
+        // taken by its GEMM, or its own column-sum launch, which reads rows at a pitch
       } else {
         readers = false;
       }
@@ -469,8 +470,7 @@ void Executor::build() {
     if (readers) pitch[x.id] = (cols + 63) / 64 * 64;
   }
   // The cross-entropy kernels walk the logits and their gradient with one pitch: both padded or
-  // neither (the gradient stays unpadded when a reader of it takes no leading dimension, as the
-  // unfused bias column sum does under mixed precision).
+  // neither (the gradient stays unpadded when a reader of it takes no leading dimension).
   for (size_t k = 0; k < n; ++k) {
     const Node& x = p.nodes[k];
     if (!need[k] || x.op != Op::CrossEntropyGrad) continue;
@@ -874,7 +874,8 @@ void Executor::build() {
         }
         const int64_t chunks = hk::column_partial_chunks(rows, h);
         void* part = R(size_t(chunks * h) * 4);
-        push([=](hipStream_t s) { hk::column_partial(s, F(a), static_cast<float*>(A(part)), rows, h); });
+        const int64_t lda = ld_of(a);
+        push([=](hipStream_t s) { hk::column_partial(s, F(a), static_cast<float*>(A(part)), rows, h, lda); });
         DeferredJob d{part, 0, int64_t(id), -1, int32_t(chunks), int32_t(h), int32_t(h)};
         if (only_optimizer_reads(int64_t(id))) {
           deferred.push_back(d);

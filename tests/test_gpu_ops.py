@@ -82,6 +82,22 @@ def test_column_sums_of_a_tall_matrix(ctx, oracle, rows, h):
     assert within(g, w, np.abs(x).astype(np.float64).sum(0))[0]
 
 
+@pytest.mark.parametrize("r,k,v,h", [(832, 64, 1001, 32), (300, 128, 30522, 64)])
+def test_column_sums_of_a_row_padded_gemm_output(ctx, oracle, r, k, v, h):
+    """A GEMM output whose width is not a multiple of 4, read by GEMMs and by a column sum of its
+    own: its rows are padded in HBM, and the column-sum launch reads them at that pitch."""
+    x, w, w2 = fast_values(61, r * k).reshape(r, k), fast_values(62, k * v).reshape(k, v), fast_values(63, v * h).reshape(v, h)
+    p = Prog()
+    xi, wi, w2i = p.input("x", (r, k)), p.input("w", (k, v)), p.input("w2", (v, h))
+    y = p.op("MatMul", [xi, wi], (r, v))
+    cs = p.op("SumRows", [y], (v,))
+    z = p.op("MatMul", [y, w2i], (r, h))
+    (gs, gz), (ws, wz) = both(ctx, oracle, p.out(cs, z), {"x": x, "w": w, "w2": w2}, (0, 1))
+    ay = np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64)
+    assert within(gs, ws, ay.sum(0))[0]
+    assert within(gz, wz, (ay @ np.abs(w2)).reshape(-1))[0]
+
+
 @pytest.mark.parametrize("v,h,r,n", [(1000, 64, 96, 256), (30522, 128, 832, 4096)])
 def test_tied_decoder_gradients(ctx, oracle, v, h, r, n):
     """The tied-embedding decoder's graph: logits = h E^T, dX = dl E, the decoder weight gradient
