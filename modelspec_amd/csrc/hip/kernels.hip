@@ -124,6 +124,38 @@ __global__ __launch_bounds__(256) void k_column_partial(const float* __restrict_
   }
   partial[int64_t(blockIdx.y) * h + c] = s;
 }
+// The same sums four columns a thread: block (x, y) takes column groups 64 x + (t mod 64) (four
+// columns each, 16-byte loads) over the rows of chunk y, its four waves the rows r = r0 + w mod 4,
+// four such rows in flight a wave; the waves' sums are added in wave order through LDS.
+__global__ __launch_bounds__(256) void k_column_partial4(const float* __restrict__ x, float* __restrict__ partial,
+                                                         int64_t rows, int64_t h, int64_t ld, int64_t rows_per) {
+  __shared__ v4f part[3][64];
+  const int g = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c = (int64_t(blockIdx.x) * 64 + g) * 4;
+  const int64_t r0 = int64_t(blockIdx.y) * rows_per, r1 = std::min<int64_t>(rows, r0 + rows_per);
+  v4f s = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (c < h) {
+    for (int64_t r = r0 + w; r < r1; r += 16) {
+      v4f t[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t rr = r + 4 * u < r1 ? r + 4 * u : r;
+        t[u] = *reinterpret_cast<const v4f*>(x + rr * ld + c);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (r + 4 * u < r1) s += t[u];
+    }
+  }
+  if (w > 0) part[w - 1][g] = s;
+  __syncthreads();
+  if (w == 0 && c < h) {
+    s += part[0][g];
+    s += part[1][g];
+    s += part[2][g];
+    *reinterpret_cast<v4f*>(partial + int64_t(blockIdx.y) * h + c) = s;
+  }
+}
 int64_t column_partial_chunks(int64_t rows, int64_t h) {
   const int64_t tiles = (h + 255) / 256;
   const int64_t want = std::max<int64_t>(1, 512 / tiles);  // about 512 blocks
@@ -139,6 +171,12 @@ void column_partial(hipStream_t s, const float* x, float* partial, int64_t rows,
   const int64_t chunks = column_partial_chunks(rows, h);
   const int64_t per = (rows + chunks - 1) / chunks;
   if ((rows + per - 1) / per != chunks) bad("column partial chunking");
+  if (h % 4 == 0 && ld % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(partial) % 16 == 0) {
+    MSX_LAUNCH(k_column_partial4, dim3(unsigned((h + 255) / 256), unsigned(chunks)), dim3(256), 0, s, x, partial,
+               rows, h, ld, per);
+    return;
+  }
   MSX_LAUNCH(k_column_partial, dim3(unsigned((h + 255) / 256), unsigned(chunks)), dim3(256), 0, s, x, partial,
                      rows, h, ld, per);
 }
