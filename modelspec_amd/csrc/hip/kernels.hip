@@ -385,7 +385,10 @@ __global__ __launch_bounds__(256) void k_ln_backward(const float* __restrict__ x
 
 int64_t ln_backward_blocks(int64_t rows, int64_t h) {
   (void)h;
-  return std::max<int64_t>(1, std::min<int64_t>((rows + 15) / 16, 256));
+  // 16 rows a block, at most 1024 blocks (4 a CU): at BERT-base's 16384 rows, 1024 blocks take
+  // 1.2 ms a step against 2.0 ms for 256 (one block a CU); more blocks cost more in the finalize
+  // of their partials than they gain.
+  return std::max<int64_t>(1, std::min<int64_t>((rows + 15) / 16, 1024));
 }
 void ln_backward(hipStream_t s, const float* x, const float* gamma, const float* g, const float* stats, float* dx,
                  float* partial, int64_t rows, int64_t h, float* dx2, int post, const float* pre,
