@@ -80,3 +80,18 @@ def test_default_masked_rows_capacity():
     assert cap(4096, 0.15) == 832
     step_ir, _ = api.compile_config("bert_micro")
     assert f"Tensor<i32, [{cap(128, 0.15)}]> = Input \"masked.rows\"" in step_ir
+
+
+def test_the_1000_step_fixture_starts_where_the_oracle_does(oracle):
+    """tests/golden/oracle_losses_bert_tiny_1000.npy is the oracle's BERT-tiny run: its first loss
+    (before any update, so independent of the run's length) is the oracle's, bit for bit, and the
+    parameter-norm fixture has one norm per parameter tensor of the step program."""
+    from modelspec_amd import api
+    golden = os.path.join(os.path.dirname(__file__), "golden")
+    want = np.load(os.path.join(golden, "oracle_losses_bert_tiny_1000.npy"))
+    norms = np.load(os.path.join(golden, "oracle_param_norms_bert_tiny_1000.npy"))
+    assert want.shape == (1001,) and want.dtype == np.float32
+    step_ir, _ = api.compile_config("bert_tiny", -1, 1000)
+    assert norms.shape == (len(api.param_shapes(step_ir)),) and np.all(norms > 0)
+    got, _, _ = oracle.train("bert_tiny", steps=1)
+    assert np.float32(got[0]).tobytes() == want[0].tobytes()
