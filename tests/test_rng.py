@@ -28,6 +28,17 @@ def test_dropout_ids_differ_by_site_and_step(oracle):
     assert a != oracle.dropout_id("BertTiny.forward.dropout#1", 0)
 
 
+def test_dropout_id_is_the_first_8_le_bytes_of_blake3_of_site_then_le_step(oracle):
+    """train/init.rs:136-146: blake3(site bytes, then step as 8 little-endian bytes), its first 8
+    bytes read little-endian. BLAKE3 itself is pinned by the known answers above. Steps above
+    2^32 and with distinct bytes catch a 4-byte or big-endian step; two sites catch a dropped
+    site."""
+    for site in ("BertTiny.forward.dropout#0", "Block.forward.dropout#12", ""):
+        for step in (0, 1, 255, 256, 999, 0x0102030405060708, (1 << 32) + 7, (1 << 64) - 1):
+            digest = oracle.blake3(site.encode() + step.to_bytes(8, "little"))
+            assert oracle.dropout_id(site, step) == int.from_bytes(digest[:8], "little"), (site, step)
+
+
 def uniform(w):
     return (w + 0.5) / 4294967296.0
 
