@@ -75,8 +75,11 @@ def build(verbose=False):
         for src, text in failed:
             sys.stderr.write(f"--- {src}\n{text}\n")
         raise RuntimeError("hipcc failed for " + ", ".join(s for s, _ in failed))
-    cmd = [HIPCC] + FLAGS + objs + ["-o", LIB]
-    subprocess.run(cmd, check=True)
+    # Linked beside the library and renamed over it, so a process that has the old one mapped
+    # keeps its pages.
+    tmp = LIB + ".tmp"
+    subprocess.run([HIPCC] + FLAGS + objs + ["-o", tmp], check=True)
+    os.replace(tmp, LIB)
     return LIB
 
 

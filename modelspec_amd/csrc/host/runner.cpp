@@ -332,20 +332,48 @@ RunResult run(const Compiled& c, Engine& engine, uint64_t steps, const RunOption
   };
   // The state after k updates (train.rs:1075, 1285: `<stem>-<k>.msckpt` every n updates before
   // the end, the checkpoint path itself at the end).
+  // Losses stay on the device between read-backs, as the reference's Vulkan runner keeps them
+  // (cli/src/train.rs:39-44): every loss so far and the parameters are checked where they are
+  // read back, at each checkpoint and after the last step. A non-finite loss names its own step;
+  // a non-finite parameter under finite losses names the step of the read-back that showed it.
+  // Returns false, with out.nonfinite_step and the losses through that step set, on the first.
+  auto finite_through = [&](uint64_t k, const std::vector<float>& losses,
+                            const std::vector<std::vector<float>>& params) {
+    for (size_t i = 0; i < losses.size(); ++i)
+      if (!std::isfinite(losses[i])) {
+        out.nonfinite_step = int64_t(start + i);
+        out.losses.assign(losses.begin(), losses.begin() + i + 1);
+        return false;
+      }
+    for (const auto& p : params)
+      for (float x : p)
+        if (!std::isfinite(x)) {
+          out.nonfinite_step = int64_t(k);
+          out.losses = losses;
+          return false;
+        }
+    return true;
+  };
+  // Writes the state after k updates unless a loss or parameter read back is not finite; then
+  // nothing is written and the run stops (returns false).
   auto checkpoint = [&](uint64_t k, const std::string& path) {
     auto w0 = std::chrono::steady_clock::now();
-    Checkpoint ck = checkpoint_of(c.step, c.config.seed, k, engine.params(), engine.moments('m'), engine.moments('v'));
+    std::vector<std::vector<float>> params = engine.params();
+    if (!finite_through(k, engine.losses(), params)) return false;
+    Checkpoint ck = checkpoint_of(c.step, c.config.seed, k, params, engine.moments('m'), engine.moments('v'));
     write_checkpoint(path, ck);
     out.checkpoints.push_back(path);
     left_out += std::chrono::duration<double>(std::chrono::steady_clock::now() - w0).count();
+    return true;
   };
   engine.set_params(out.initial);
   if (o.resume && c.step.rule == Rule::AdamW) engine.set_moments(o.resume->m, o.resume->v);
   auto t0 = std::chrono::steady_clock::now();
   for (uint64_t step = start; step < end; ++step) {
     if (held_out && step % o.eval_every == 0) evaluate(step);
-    if (o.checkpoint_every && step > start && step % o.checkpoint_every == 0 && !o.checkpoint_path.empty())
-      checkpoint(step, checkpoint_every_path(o.checkpoint_path, step));
+    if (o.checkpoint_every && step > start && step % o.checkpoint_every == 0 && !o.checkpoint_path.empty() &&
+        !checkpoint(step, checkpoint_every_path(o.checkpoint_path, step)))
+      return out;
     engine.train_step(step_inputs(c, feed, step, end));
   }
   out.losses = engine.losses();
@@ -353,20 +381,19 @@ RunResult run(const Compiled& c, Engine& engine, uint64_t steps, const RunOption
   out.train_seconds = std::chrono::duration<double>(t1 - t0).count() - left_out;
   if (held_out) evaluate(end);
   Batch last = feed.batch(end);
+  // The final batch is held to the gather's capacity as every trained batch is (runner.rs:462):
+  // masked_gather throws E-DATA-012 on a batch the step's gather could not hold. Its rows are
+  // not used: the final loss runs the forward program over every row.
   if (const Node* rows = last.i32.count(kDrawInput) ? nullptr : c.step.program.input(kMaskedRowsInput)) {
     std::vector<int32_t> r, l;
     std::vector<float> w;
     masked_gather(last.i32.at(c.config.labels), last.f32.at(c.config.weights), uint64_t(rows->ty.count()), end, r, l, w);
   }
-  out.losses.push_back(engine.final_loss(last));
   out.params = engine.params();
+  if (!finite_through(end, out.losses, out.params)) return out;
+  out.losses.push_back(engine.final_loss(last));
+  if (!finite_through(end, out.losses, {})) return out;
   if (!o.checkpoint_path.empty()) checkpoint(end, o.checkpoint_path);
-  for (size_t k = 0; k < out.losses.size(); ++k)
-    if (!std::isfinite(out.losses[k])) {
-      out.nonfinite_step = int64_t(start + k);
-      out.losses.resize(k + 1);
-      break;
-    }
   return out;
 }
 

@@ -417,6 +417,10 @@ int64_t orc_train_ckpt(const char* config, const char* packed_dir, int64_t steps
     o.checkpoint_every = checkpoint_every;
     if (checkpoint_path) o.checkpoint_path = checkpoint_path;
     msx::RunResult r = msx::run(c, e, n, o);
+    if (r.nonfinite_step >= 0) {
+      g_error = "E-TRAIN-001: a loss or an updated parameter is not finite at step " + std::to_string(r.nonfinite_step);
+      return -1;
+    }
     if (losses) {
       if (losses_len < r.losses.size()) { g_error = "losses buffer too small"; return -1; }
       std::memcpy(losses, r.losses.data(), r.losses.size() * sizeof(float));

@@ -161,3 +161,41 @@ def test_another_model_is_refused(oracle, tmp_path):
     oracle.train_ckpt("linear_regression", 2, path=path)
     with pytest.raises(RuntimeError, match="E-CKPT-003.*path"):
         oracle.train_ckpt("mlp_micro", 1, resume=path)
+
+
+DIVERGING = """model LinearReg {
+    param w: Tensor<f32, [4, 1]> = xavier_uniform();
+
+    fn forward(x: Tensor<f32, [8, 4]>) -> Tensor<f32, [8, 1]> {
+        return matmul(x, w);
+    }
+}
+
+train Fit {
+    model = LinearReg;
+    input x: Tensor<f32, [8, 4]>;
+    target y: Tensor<f32, [8, 1]>;
+    loss = mse(model.forward(x), y);
+    optimizer = sgd(lr = 1e30);
+    steps = 6;
+    seed = 42;
+    device = cpu;
+}
+"""
+
+
+def test_a_diverged_run_stops_and_writes_no_later_checkpoint(oracle, tmp_path):
+    """cli/src/train.rs:39-44: a run whose loss stops being finite stops with E-TRAIN-001, and the
+    state is checked where it is read back, so no checkpoint holds a non-finite loss's state. At
+    lr 1e30 the first update leaves finite parameters of order 1e30 (written at step 1) and the
+    loss of step 1 overflows; the read-back before the step-2 checkpoint shows it."""
+    src = tmp_path / "diverge.mspec"
+    src.write_text(DIVERGING)
+    path = tmp_path / "run.msckpt"
+    with pytest.raises(RuntimeError, match=r"E-TRAIN-001.*step 1\b"):
+        oracle.train_ckpt(str(src), 6, every=1, path=str(path))
+    assert (tmp_path / "run-1.msckpt").exists()
+    assert not (tmp_path / "run-2.msckpt").exists()
+    assert not path.exists()
+    with pytest.raises(RuntimeError, match="E-TRAIN-001"):
+        oracle.train(str(src))
