@@ -67,6 +67,7 @@ def lib():
         L.msx_train_config.argtypes = [vp, ctypes.c_char_p, c64, c64, vp, u64, vp, u64, ctypes.POINTER(ctypes.c_double)]
         L.msx_evaluate.argtypes = [vp, u32, ctypes.POINTER(ctypes.POINTER(Tensor)), ctypes.POINTER(u32),
                                    ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(HeldOutMetrics)]
+        L.msx_evaluate_static.argtypes = L.msx_evaluate.argtypes
         L.msx_train_config_eval.argtypes = [vp, ctypes.c_char_p, c64, u64, u64, vp, u64, vp,
                                             ctypes.POINTER(HeldOutMetrics), u64, ctypes.POINTER(u64),
                                             ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
@@ -240,6 +241,14 @@ class Context:
         out = HeldOutMetrics()
         _check(lib().msx_evaluate(self._h, len(batches), ptrs, counts, labels.encode(), weights.encode(),
                                   ctypes.byref(out)))
+        return out.as_dict()
+
+    def evaluate_static(self, batches, labels, weights):
+        """`evaluate` through msx_evaluate_static: no device allocation, at most 65,536 rows a batch."""
+        ptrs, counts, keep = self._batches(batches)
+        out = HeldOutMetrics()
+        _check(lib().msx_evaluate_static(self._h, len(batches), ptrs, counts, labels.encode(), weights.encode(),
+                                         ctypes.byref(out)))
         return out.as_dict()
 
     def train_config_eval(self, name, eval_every, eval_batches, steps=-1):

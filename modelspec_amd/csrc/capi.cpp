@@ -338,8 +338,9 @@ msx_heldout heldout_of(const msx::HeldOut& h, const msx::HeldOutSums& sums) {
 }
 }  // namespace
 
-int msx_evaluate(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, const uint32_t* n_inputs,
-                 const char* labels, const char* weights, msx_heldout* out) {
+namespace {
+int evaluate(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, const uint32_t* n_inputs, const char* labels,
+             const char* weights, msx_heldout* out, bool no_alloc) {
   return guarded([&] {
     if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");
     if (!labels || !weights || !out || (n && (!inputs || !n_inputs))) return fail(MSX_E_INVALID, "null argument");
@@ -357,9 +358,20 @@ int msx_evaluate(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, cons
       }
     }
     msx::HeldOut h(ctx->forward, ctx->prediction, labels, weights, std::move(batches));
-    *out = heldout_of(h, ctx->session->held_out(h));
+    *out = heldout_of(h, no_alloc ? ctx->session->held_out_static(h) : ctx->session->held_out(h));
     return MSX_OK;
   });
+}
+}  // namespace
+
+int msx_evaluate(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, const uint32_t* n_inputs,
+                 const char* labels, const char* weights, msx_heldout* out) {
+  return evaluate(ctx, n, inputs, n_inputs, labels, weights, out, false);
+}
+
+int msx_evaluate_static(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, const uint32_t* n_inputs,
+                        const char* labels, const char* weights, msx_heldout* out) {
+  return evaluate(ctx, n, inputs, n_inputs, labels, weights, out, true);
 }
 
 namespace {

@@ -5,9 +5,38 @@
 #include <cmath>
 #include <cstring>
 #include <array>
+#include <map>
+#include <mutex>
 #include <set>
 
+// The device memory of Session::held_out_static: the row results [rows, 2] of at most
+// kStaticEvalRows rows, then the HeldOutState at the next 256-byte boundary (512 KiB + 256 bytes).
+// Each device holds its own copy until the process ends. In host code `scratch` names a host-side
+// stand-in, so its device address is looked up once per device (static_scratch) and only that
+// address is used.
+static constexpr size_t kStaticStateAt = size_t(msx::Session::kStaticEvalRows) * 8;
+static constexpr size_t kStaticScratchBytes = kStaticStateAt + 256;
+static __device__ __align__(256) char scratch[kStaticScratchBytes];
+
 namespace msx {
+
+namespace {
+std::mutex g_scratch_mu;
+std::map<int, void*> g_scratch_at;
+
+// The address of `scratch` on `device`, looked up with that device current on its first use.
+void* static_scratch(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  auto it = g_scratch_at.find(device);
+  if (it != g_scratch_at.end()) return it->second;
+  hip_check(hipSetDevice(device), "hipSetDevice (static scratch)");
+  void* ptr = nullptr;
+  hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (static scratch)");
+  if (!ptr) throw HipError("hipGetSymbolAddress (static scratch): no address");
+  g_scratch_at[device] = ptr;
+  return ptr;
+}
+}  // namespace
 
 void hip_check(hipError_t e, const char* what) {
   if (e != hipSuccess) throw HipError(std::string(what) + ": " + hipGetErrorString(e));
@@ -1710,7 +1739,11 @@ float Session::final_loss(const Batch& batch) {
   return loss;
 }
 
-HeldOutSums Session::held_out(const HeldOut& h) {
+HeldOutSums Session::held_out(const HeldOut& h) { return held_out_in(h, false); }
+
+HeldOutSums Session::held_out_static(const HeldOut& h) { return held_out_in(h, true); }
+
+HeldOutSums Session::held_out_in(const HeldOut& h, bool no_alloc) {
   h.check_labels();
   const Node* lab = forward_.input(h.labels_name());
   const Node* w = forward_.input(h.weights_name());
@@ -1721,7 +1754,16 @@ HeldOutSums Session::held_out(const HeldOut& h) {
   const int64_t rows = lab->ty.count(), v = h.classes();
   // Row results first, the state at the next 256-byte boundary behind them.
   const size_t state_at = (size_t(rows) * 8 + 255) / 256 * 256;
-  if (rows > eval_rows_) {
+  float* row_out = nullptr;
+  hk::HeldOutState* state = nullptr;
+  if (no_alloc) {
+    if (rows > kStaticEvalRows)
+      throw IrError("held-out evaluation without allocation: a batch of " + std::to_string(rows) + " rows exceeds " +
+                    std::to_string(kStaticEvalRows));
+    char* base = static_cast<char*>(static_scratch(device_));
+    row_out = reinterpret_cast<float*>(base);
+    state = reinterpret_cast<hk::HeldOutState*>(base + kStaticStateAt);
+  } else if (rows > eval_rows_) {
     sync();
     if (eval_mem_) hip_check(hipFree(eval_mem_), "hipFree (held-out)");
     eval_mem_ = nullptr;
@@ -1729,8 +1771,10 @@ HeldOutSums Session::held_out(const HeldOut& h) {
     hip_check(hipMalloc(&eval_mem_, state_at + 256), "hipMalloc (held-out)");
     eval_rows_ = rows;
   }
-  float* row_out = static_cast<float*>(eval_mem_);
-  auto* state = reinterpret_cast<hk::HeldOutState*>(static_cast<char*>(eval_mem_) + state_at);
+  if (!no_alloc) {
+    row_out = static_cast<float*>(eval_mem_);
+    state = reinterpret_cast<hk::HeldOutState*>(static_cast<char*>(eval_mem_) + state_at);
+  }
   hk::fill_zero(stream_, state, sizeof(hk::HeldOutState));
   for (auto& batch : h.batches()) {
     fwd_exec_->stage(batch);

@@ -93,6 +93,11 @@ class Session : public Engine {
   // (held_out_sum); one host wait at the end (vulkan/stepwise.rs:1635-1760 does the same with its
   // HeldOutRows / HeldOutSum modules).
   HeldOutSums held_out(const HeldOut& h) override;
+  // held_out with the row results and the sums in the library's static device array instead of
+  // a buffer of the session: no device memory is allocated. At most kStaticEvalRows rows a batch;
+  // every call on one device shares the array, so calls that overlap on a device race.
+  HeldOutSums held_out_static(const HeldOut& h);
+  static constexpr int64_t kStaticEvalRows = 65536;
   std::vector<float> losses() override;
 
   // Runs the step plan eagerly (no graph) with one event pair around every launch; returns the
@@ -160,6 +165,7 @@ class Session : public Engine {
   uint64_t corpus_batch_ = 0;
   // Whether the corpus writes input `name` of `p` (a batch tensor or a masked-row gather input).
   bool corpus_fed(const Program& p, const std::string& name) const;
+  HeldOutSums held_out_in(const HeldOut& h, bool no_alloc);
   void* eval_mem_ = nullptr;     // held-out row results [rows, 2] and the HeldOutState behind them
   int64_t eval_rows_ = 0;
 
