@@ -29,6 +29,7 @@ SOURCES = [
     "hip/gemm.hip",
     "hip/attention.hip",
     "hip/data.hip",
+    "hip/segments.hip",
 ]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -125,6 +125,23 @@ void embedding(hipStream_t s, const float* table, const int32_t* ids, float* o, 
 void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* out, int64_t n, int64_t rows,
                     int64_t h, const float* addend = nullptr);
 
+// EmbeddingGrad as a sorted-segment scatter (segments.hip), bit-exact with embedding_grad: a plan
+// per table (ids of at most 8192 positions, eg_sorted_fits) made by eg_plan into a buffer of
+// eg_plan_bytes, then eg_apply writes out = e (or addend + e) for up to kEgJobs tables a launch.
+constexpr int kEgJobs = 3;
+struct EgPlanJob { const int32_t* ids; int32_t* plan; int32_t n, rows, pos_bits, key_bits; };
+struct EgPlanSet { EgPlanJob job[kEgJobs]; int32_t count; };
+struct EgApplyJob {
+  const int32_t* plan; const float* g; const float* addend; float* out;
+  int32_t n, rows; int64_t h;
+  int32_t vec, blocks_short, blocks_long, blocks;  // set by eg_apply
+};
+struct EgApplySet { EgApplyJob job[kEgJobs]; int32_t count; };
+bool eg_sorted_fits(int64_t n, int64_t rows);
+size_t eg_plan_bytes(int64_t n, int64_t rows);
+void eg_plan(hipStream_t s, const EgPlanJob* jobs, int njobs);
+void eg_apply(hipStream_t s, const EgApplyJob* jobs, int njobs);
+
 void dropout(hipStream_t s, const float* x, float* o, int64_t n, const int32_t* token, uint64_t seed,
              uint64_t threshold, float scale);
 

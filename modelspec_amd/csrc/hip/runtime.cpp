@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <array>
 #include <map>
@@ -702,6 +703,76 @@ void Executor::build() {
     }
   }
 
+  // EmbeddingGrads whose ids are step inputs take the sorted-segment path: each distinct ids
+  // input is sorted once, by one launch at the head of the step (the ids exist before any
+  // kernel runs), and each EmbeddingGrad then reads its plan.
+  std::map<uint32_t, void*> eg_plan_tok;  // EmbeddingGrad node -> plan buffer of its ids
+  std::set<uint32_t> eg_deferred;                      // launched with a later EmbeddingGrad
+  std::map<uint32_t, std::vector<uint32_t>> eg_group;  // last EmbeddingGrad -> every one it launches
+  {
+    std::map<std::pair<uint32_t, int64_t>, void*> by_ids;
+    struct PlanJob { uint32_t ids; int64_t n, rows; void* tok; };
+    std::vector<PlanJob> jobs;
+    for (size_t k = 0; k < n; ++k) {
+      const Node& x = p.nodes[k];
+      if (!need[k] || x.op != Op::EmbeddingGrad || optimizer.count(x.id)) continue;
+      const uint32_t ids = x.operands[0];
+      const int64_t nn = shape(ids)[0], rows = x.rows;
+      if (p.node(ids).op != Op::Input || !hk::eg_sorted_fits(nn, rows)) continue;
+      auto key = std::make_pair(ids, rows);
+      if (!by_ids.count(key)) {
+        by_ids[key] = R(hk::eg_plan_bytes(nn, rows));
+        jobs.push_back({ids, nn, rows, by_ids[key]});
+      }
+      eg_plan_tok[x.id] = by_ids[key];
+    }
+    // EmbeddingGrads of one gradient (the token and position tables of the same embedding sum)
+    // share one launch, at the last of them, when nothing in between reads an earlier one's output.
+    std::map<uint32_t, std::vector<uint32_t>> by_g;
+    for (size_t k = 0; k < n; ++k) {
+      const Node& x = p.nodes[k];
+      if (need[k] && x.op == Op::EmbeddingGrad && eg_plan_tok.count(x.id)) by_g[x.operands[1]].push_back(x.id);
+    }
+    for (auto& [g, members] : by_g) {
+      std::vector<uint32_t> group;
+      for (uint32_t m : members) {
+        if (group.size() == size_t(hk::kEgJobs)) break;
+        group.push_back(m);
+      }
+      if (group.size() < 2) continue;
+      const size_t last = p.pos.at(group.back());
+      bool ok = true;
+      for (size_t q = 0; q + 1 < group.size() && ok; ++q) {
+        const uint32_t out = eg_add.count(group[q]) ? eg_add.at(group[q]).first : group[q];
+        for (size_t k = p.pos.at(group[q]) + 1; k < last && ok; ++k)
+          if (need[k] && !optimizer.count(p.nodes[k].id) && p.nodes[k].id != out)
+            for (uint32_t o : p.nodes[k].operands) ok = ok && o != out && o != group[q];
+      }
+      if (!ok) continue;
+      for (size_t q = 0; q + 1 < group.size(); ++q) eg_deferred.insert(group[q]);
+      eg_group[group.back()] = group;
+    }
+    for (size_t q0 = 0; q0 < jobs.size(); q0 += hk::kEgJobs) {
+      std::vector<PlanJob> part(jobs.begin() + q0, jobs.begin() + std::min(jobs.size(), q0 + hk::kEgJobs));
+      std::string what = "EmbeddingPlan";
+      double bytes = 0;
+      for (auto& j : part) {
+        what += " %" + std::to_string(j.ids);
+        bytes += double(j.n) * 4 + double(hk::eg_plan_bytes(j.n, j.rows));
+      }
+      pending.push_back({[=] {
+        return Launch{what, [=](hipStream_t st) {
+                        hk::EgPlanJob js[hk::kEgJobs];
+                        for (size_t q = 0; q < part.size(); ++q)
+                          js[q] = hk::EgPlanJob{I(part[q].ids), static_cast<int32_t*>(A(part[q].tok)), int32_t(part[q].n),
+                                                int32_t(part[q].rows), 0, 0};
+                        hk::eg_plan(st, js, int(part.size()));
+                      }};
+      }});
+      pending.back().bytes = bytes;
+    }
+  }
+
   for (size_t k = 0; k < n; ++k) {
     if (!need[k]) continue;
     const Node& x = p.nodes[k];
@@ -882,7 +953,41 @@ void Executor::build() {
           auto it = id_bounds_.find(p.node(ids).name);
           id_bounds_[p.node(ids).name] = it == id_bounds_.end() ? rows : std::min(it->second, rows);
         }
-        if (eg_add.count(id)) {
+        if (eg_deferred.count(id)) break;  // launched with a later EmbeddingGrad of the same gradient
+        if (eg_plan_tok.count(id)) {
+          struct Job { void* plan; uint32_t g, out; int64_t addend, n, rows, h; };
+          std::vector<Job> jobs;
+          const std::vector<uint32_t> members = eg_group.count(id) ? eg_group.at(id) : std::vector<uint32_t>{id};
+          what.clear();
+          bytes = 0;
+          for (uint32_t m : members) {
+            const Node& e = p.node(m);
+            const bool add = eg_add.count(m) != 0;
+            const uint32_t out = add ? eg_add.at(m).first : m;
+            jobs.push_back({eg_plan_tok.at(m), e.operands[1], out, add ? int64_t(eg_add.at(m).second) : -1,
+                            shape(e.operands[0])[0], e.rows, shape(e.operands[1])[1]});
+            what += (what.empty() ? "" : " & ") + std::string(add ? "EmbeddingGrad+Add %" : "EmbeddingGrad %") +
+                    std::to_string(m) + (add ? " %" + std::to_string(out) : "") + " " + type_string(e.ty);
+            const double cnt = double(e.ty.count());
+            bytes += 4.0 * (double(shape(e.operands[0])[0]) * (1 + double(shape(e.operands[1])[1])) + cnt) +
+                     (add ? 8.0 * cnt : 0.0);
+          }
+          push([=](hipStream_t s) {
+            hk::EgApplyJob js[hk::kEgJobs];
+            for (size_t q = 0; q < jobs.size(); ++q) {
+              hk::EgApplyJob j{};
+              j.plan = static_cast<const int32_t*>(A(jobs[q].plan));
+              j.g = F(jobs[q].g);
+              j.addend = jobs[q].addend >= 0 ? F(uint32_t(jobs[q].addend)) : nullptr;
+              j.out = F(jobs[q].out);
+              j.n = int32_t(jobs[q].n);
+              j.rows = int32_t(jobs[q].rows);
+              j.h = jobs[q].h;
+              js[q] = j;
+            }
+            hk::eg_apply(s, js, int(jobs.size()));
+          });
+        } else if (eg_add.count(id)) {
           const uint32_t sum_id = eg_add.at(id).first, addend = eg_add.at(id).second;
           what = "EmbeddingGrad+Add %" + std::to_string(id) + " %" + std::to_string(sum_id) + " " + type_string(x.ty);
           push([=](hipStream_t s) { hk::embedding_grad(s, I(ids), F(g), F(sum_id), nn, rows, h, F(addend)); });
@@ -1516,7 +1621,9 @@ Session::Session(int device, const TrainingStep& step, const Program& forward, u
     stats_.device_bytes += eoff + 256;
   }
   hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
-  hip_check(hipStreamCreateWithFlags(&side_, hipStreamNonBlocking), "hipStreamCreate (side)");
+  if (!std::getenv("MSX_NO_SIDE_STREAM"))
+    hip_check(hipStreamCreateWithFlags(&side_, hipStreamNonBlocking), "hipStreamCreate (side)");
+  if (std::getenv("MSX_NO_GRAPH")) use_graph_ = false;
   hip_check(hipEventCreateWithFlags(&fork_, hipEventDisableTiming), "hipEventCreate (fork)");
   hip_check(hipEventCreateWithFlags(&join_, hipEventDisableTiming), "hipEventCreate (join)");
   const auto& params = step_.program.params;

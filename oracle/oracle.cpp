@@ -526,6 +526,30 @@ int orc_time_steps(const char* config, int64_t steps, int64_t masked_rows, doubl
   }
 }
 
+// The wall-clock seconds of each of `steps` training steps of `config` on this thread, from the
+// initial parameters, inputs made beforehand: out[k] is step k's. Returns 0, or -1 with
+// orc_last_error().
+int orc_step_times(const char* config, int64_t steps, int64_t masked_rows, double* out) {
+  try {
+    msx::Compiled c = msx::compile_config(config, masked_rows, -1);
+    OracleEngine e(c);
+    msx::Feed feed(c);
+    if (feed.needs_teacher()) feed.set_target(e.predict(msx::initialize(c.forward, c.config.seed, msx::Stream::Teacher), feed.batch(0)));
+    e.set_params(msx::initialize(c.forward, c.config.seed, msx::Stream::Init));
+    std::vector<msx::StepInputs> ins;
+    for (int64_t s = 0; s < steps; ++s) ins.push_back(msx::step_inputs(c, feed, uint64_t(s), c.config.steps));
+    for (int64_t s = 0; s < steps; ++s) {
+      auto t0 = std::chrono::steady_clock::now();
+      e.train_step(ins[size_t(s)]);
+      out[s] = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    }
+    return 0;
+  } catch (const std::exception& ex) {
+    g_error = ex.what();
+    return -1;
+  }
+}
+
 void* orc_prog_new(const char* program_text, int has_seed, uint64_t seed) {
   try {
     auto* p = new Prog;

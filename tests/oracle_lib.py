@@ -20,6 +20,7 @@ class Oracle:
         L.orc_last_error.restype = ctypes.c_char_p
         L.orc_train.argtypes = [ctypes.c_char_p, i64, i64, vp, u64, vp, u64, ctypes.POINTER(ctypes.c_double)]
         L.orc_time_steps.argtypes = [ctypes.c_char_p, i64, i64, ctypes.POINTER(ctypes.c_double)]
+        L.orc_step_times.argtypes = [ctypes.c_char_p, i64, i64, vp]
         L.orc_prog_new.argtypes = [ctypes.c_char_p, ctypes.c_int, u64]
         L.orc_prog_new.restype = vp
         L.orc_prog_free.argtypes = [vp]
@@ -174,6 +175,13 @@ class Oracle:
         if self.L.orc_time_steps(config.encode(), steps, masked_rows, ctypes.byref(s)) != 0:
             raise RuntimeError(self.err())
         return s.value
+
+    def step_times(self, config, steps, masked_rows=-1):
+        """Seconds of each of `steps` training steps from the initial parameters, one thread."""
+        out = np.zeros(steps, np.float64)
+        if self.L.orc_step_times(config.encode(), steps, masked_rows, out.ctypes.data) != 0:
+            raise RuntimeError(self.err())
+        return out
 
     def philox(self, counter, key):
         c = np.array(counter, np.uint32)
