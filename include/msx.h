@@ -107,6 +107,15 @@ int msx_stats(msx_ctx* ctx, msx_run_stats* out);
  * gradients overflowed (halving the scale), and the scale doubles after scale_window clean steps.
  * No counterpart in the reference, which trains in f32 only. */
 int msx_set_precision(msx_ctx* ctx, int32_t mixed, float loss_scale, uint32_t scale_window);
+
+/* Optional fusions of the next msx_load or msx_prog_new. MSX_FUSE_CE_HEAD: a cross-entropy whose
+ * logits come from a GEMM and whose gradient only GEMMs read is folded into those GEMMs (the
+ * forward leaves per-tile row partials, the gradient is formed from the logits as it is loaded and
+ * never stored); off by default, as it measured slower on BERT-tiny. No counterpart in the
+ * reference: a plan choice of this backend (the reference's own fusion groups are fixed by its
+ * planner, crates/modelspec-core/src/ir/kernel.rs:1407). */
+#define MSX_FUSE_CE_HEAD 1u
+int msx_set_fusion(msx_ctx* ctx, uint32_t flags);
 /* The loaded step's current loss scale and the number of steps skipped for an overflow (1 and 0
  * without mixed precision). */
 int msx_loss_scale(msx_ctx* ctx, float* scale, uint64_t* skipped);

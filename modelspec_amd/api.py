@@ -68,6 +68,7 @@ def lib():
         L.msx_evaluate.argtypes = [vp, u32, ctypes.POINTER(ctypes.POINTER(Tensor)), ctypes.POINTER(u32),
                                    ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(HeldOutMetrics)]
         L.msx_evaluate_static.argtypes = L.msx_evaluate.argtypes
+        L.msx_set_fusion.argtypes = [vp, u32]
         L.msx_train_config_eval.argtypes = [vp, ctypes.c_char_p, c64, u64, u64, vp, u64, vp,
                                             ctypes.POINTER(HeldOutMetrics), u64, ctypes.POINTER(u64),
                                             ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
@@ -318,6 +319,11 @@ class Context:
                                             losses.ctypes.data, losses.size, params.ctypes.data, params.size,
                                             ctypes.byref(start)))
         return losses, params, start.value
+
+    def set_fusion(self, ce_head=False):
+        """Optional fusions of the next load (msx_set_fusion): ce_head folds the cross-entropy into
+        its decoder head GEMMs."""
+        _check(lib().msx_set_fusion(self._h, 1 if ce_head else 0))
 
     def set_precision(self, mixed, loss_scale=65536.0, scale_window=2000):
         """The precision of the next load (and per-op program): f16 MFMA GEMMs with loss scaling."""

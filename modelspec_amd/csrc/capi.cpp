@@ -277,6 +277,14 @@ int msx_read_input(msx_ctx* ctx, int32_t program, const char* name, void* out, u
   });
 }
 
+int msx_set_fusion(msx_ctx* ctx, uint32_t flags) {
+  return guarded([&] {
+    if (flags & ~uint32_t(MSX_FUSE_CE_HEAD)) return fail(MSX_E_INVALID, "unknown fusion flags");
+    ctx->options.fuse_ce_head = (flags & MSX_FUSE_CE_HEAD) != 0;
+    return MSX_OK;
+  });
+}
+
 int msx_set_precision(msx_ctx* ctx, int32_t mixed, float loss_scale, uint32_t scale_window) {
   return guarded([&] {
     if (!(loss_scale >= 1.0f) || !std::isfinite(loss_scale) || scale_window == 0)

@@ -108,9 +108,20 @@ namespace {
 // clamped address and are zeroed, branch-free.
 // V: the group is 16-byte aligned and wholly in or out of range, or its out-of-range part lies in
 // zero padding of the rows: one float4 load; otherwise four clamped scalar loads.
-template <bool KC, int R, int WK, bool V>
+// The cross-entropy gradient of logit x at column c of a row with entry t = (max, 1 / sum,
+// g w / sum(w), label): (g w / sum(w)) (exp(x - max) / sum - [c = label]), in k_ce_rows' operation
+// order; 0 past the row's `cols` columns and in a row of a batch whose weights sum to 0.
+__device__ __forceinline__ float ce_grad_of(float x, const float4 t, int64_t c, int64_t cols) {
+  const int lab = __float_as_int(t.w);
+  if (c >= cols || lab == -2) return 0.0f;
+  return t.z * (__expf(x - t.x) * t.y - (c == lab ? 1.0f : 0.0f));
+}
+// XF: the operand is a cross-entropy gradient formed from the logits P holds (tab, cols); its
+// stored element (row, column) is P[row * ld + column].
+template <bool KC, int R, int WK, bool V, bool XF = false>
 __device__ __forceinline__ float4 wide_load(const float* __restrict__ P, int64_t ld, int64_t rows, int64_t kend,
-                                            int64_t r0, int64_t k0, int e) {
+                                            int64_t r0, int64_t k0, int e, const float4* __restrict__ tab = nullptr,
+                                            int64_t cols = 0) {
   int r, k;
   if (KC) { r = e / (WK / 4); k = (e % (WK / 4)) * 4; } else { k = e / (R / 4); r = (e % (R / 4)) * 4; }
   const int64_t gr = r0 + r, gk = k0 + k;
@@ -119,7 +130,13 @@ __device__ __forceinline__ float4 wide_load(const float* __restrict__ P, int64_t
     // A group past the end reads the aligned group holding the last element instead.
     const int64_t cr = KC ? (gr < rows ? gr : rows - 1) : (gr < rows ? gr : (rows - 1) & ~int64_t(3));
     const int64_t ck = KC ? (gk < kend ? gk : (kend - 1) & ~int64_t(3)) : (gk < kend ? gk : kend - 1);
-    const float4 f = *reinterpret_cast<const float4*>(KC ? P + cr * ld + ck : P + ck * ld + cr);
+    float4 f = *reinterpret_cast<const float4*>(KC ? P + cr * ld + ck : P + ck * ld + cr);
+    if (XF) {
+      const int64_t srow = KC ? cr : ck, scol = KC ? ck : cr;
+      const float4 t = tab[srow];
+      f = make_float4(ce_grad_of(f.x, t, scol, cols), ce_grad_of(f.y, t, scol + 1, cols),
+                      ce_grad_of(f.z, t, scol + 2, cols), ce_grad_of(f.w, t, scol + 3, cols));
+    }
     return ok ? f : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
   float v[4];
@@ -127,7 +144,8 @@ __device__ __forceinline__ float4 wide_load(const float* __restrict__ P, int64_t
   for (int j = 0; j < 4; ++j) {
     const int64_t rr = KC ? gr : gr + j, kk = KC ? gk + j : gk;
     const int64_t cr = rr < rows ? rr : rows - 1, ck = kk < kend ? kk : kend - 1;
-    const float x = KC ? P[cr * ld + ck] : P[ck * ld + cr];
+    float x = KC ? P[cr * ld + ck] : P[ck * ld + cr];
+    if (XF) x = ce_grad_of(x, tab[KC ? cr : ck], KC ? ck : cr, cols);
     v[j] = rr < rows && kk < kend ? x : 0.0f;
   }
   return make_float4(v[0], v[1], v[2], v[3]);
@@ -204,7 +222,9 @@ struct GemmOrder {
 // H: the mixed-precision variant. The operands are rounded to f16 as they are staged into LDS
 // (rows of their K slice contiguous) and multiplied by v_mfma_f32_16x16x32_f16 with f32
 // accumulation; K tiles of 32; everything else (split-K, epilogues, output) as in f32.
-template <bool TA, bool TB, int WM, int WN, int WK, bool VA, bool VB, bool H = false>
+// CE: 1 or 2, operand A or B is a cross-entropy gradient formed from its logits (ce_grad_of);
+// 3, the row partials of a cross-entropy over the output (ce_part).
+template <bool TA, bool TB, int WM, int WN, int WK, bool VA, bool VB, bool H = false, int CE = 0>
 __global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_t N, int64_t K, int64_t lda,
                                                 int64_t ldb, int64_t ldc, int64_t kchunk, bool sum_a, bool vo,
                                                 GemmOrder order) {
@@ -261,8 +281,13 @@ __global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_
   static_assert((!RA || GA % 256 == 0) && (!RB || GB % 256 == 0), "row-vector staging takes whole groups a thread");
   auto ga = [&](int h) { return RA ? hk_group<TM, HA>(tid, h) : tid + 256 * h; };
   auto gb = [&](int h) { return RB ? hk_group<TN, HB>(tid, h) : tid + 256 * h; };
-  auto load_a = [&](int64_t k0, int h) { return wide_load<!TA, TM, WK, VA>(A, lda, M, kend, m0, k0, ga(h)); };
-  auto load_b = [&](int64_t k0, int h) { return wide_load<TB, TN, WK, VB>(B, ldb, N, kend, n0, k0, gb(h)); };
+  const float4* __restrict__ ce_tab = CE == 1 || CE == 2 ? ptrs.ce_tab[q] : nullptr;
+  auto load_a = [&](int64_t k0, int h) {
+    return wide_load<!TA, TM, WK, VA, CE == 1>(A, lda, M, kend, m0, k0, ga(h), ce_tab, ptrs.ce_cols);
+  };
+  auto load_b = [&](int64_t k0, int h) {
+    return wide_load<TB, TN, WK, VB, CE == 2>(B, ldb, N, kend, n0, k0, gb(h), ce_tab, ptrs.ce_cols);
+  };
   float4 ra[HA], rb[HB];
 #pragma unroll
   for (int h = 0; h < HA; ++h)
@@ -395,6 +420,31 @@ __global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_
       if (PR * Q % 256 != 0 && e >= PR * Q) break;
       const int rl = e / Q, c4 = (e % Q) * 4;
       const int64_t row = m0 + pass * PR + rl, col = n0 + c4;
+      if constexpr (CE == 3) {
+        // The row's (max, sum of exp(v - max)) over this tile's columns, after the epilogue: the Q
+        // lanes of a row are consecutive, reduced by shuffles in a fixed order.
+        static_assert(Q <= 64 && 256 % Q == 0, "a row's output groups lie in one wave");
+        const float4 raw = *reinterpret_cast<const float4*>(smem + rl * LC + c4);
+        float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (row < M && col < N) {
+          const float4 f = col + 3 < N ? gemm_epilogue4(epi, raw, row, col, ldo)
+                                       : make_float4(gemm_epilogue(epi, raw.x, row, col, ldo),
+                                                     col + 1 < N ? gemm_epilogue(epi, raw.y, row, col + 1, ldo) : 0.0f,
+                                                     col + 2 < N ? gemm_epilogue(epi, raw.z, row, col + 2, ldo) : 0.0f, 0.0f);
+          v = make_float4(f.x, col + 1 < N ? f.y : -INFINITY, col + 2 < N ? f.z : -INFINITY,
+                          col + 3 < N ? f.w : -INFINITY);
+        }
+        float mx = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+#pragma unroll
+        for (int o = Q / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        float sm = (__expf(v.x - mx) + __expf(v.y - mx)) + (__expf(v.z - mx) + __expf(v.w - mx));
+#pragma unroll
+        for (int o = Q / 2; o > 0; o >>= 1) sm += __shfl_xor(sm, o, 64);
+        if (c4 == 0 && row < M) {
+          const int64_t tiles = (N + TN - 1) / TN;
+          reinterpret_cast<float2*>(ptrs.ce_part[q])[row * tiles + tn] = make_float2(mx, sm);
+        }
+      }
       if (row >= M) continue;
       const float4 v = *reinterpret_cast<const float4*>(smem + rl * LC + c4);
       if (vo && col + 3 < N) {
@@ -424,11 +474,12 @@ namespace {
 // the f32 one an instruction, so mixed-precision GEMMs of 2^21 outputs or more (or K of 8192 or
 // more) take 128 x 128 tiles: four times the MFMAs per operand byte staged.
 struct SplitPlan { int wm, wn, wk, split; int64_t chunk; };
-SplitPlan split_plan(int64_t m, int64_t n, int64_t k, bool defer, bool h16) {
+SplitPlan split_plan(int64_t m, int64_t n, int64_t k, bool defer, bool h16, bool ce = false) {
   const int64_t mn = m * n;
   SplitPlan p{};
-  if (h16 && (mn >= (int64_t(1) << 21) || k >= 8192)) { p.wm = 4; p.wn = 4; p.wk = 32; }
-  else if (mn >= (int64_t(1) << 21) || k >= 8192) { p.wm = 2; p.wn = 2; p.wk = 16; }
+  // A cross-entropy head (ce) always takes the largest tile, the one its kernels are built for.
+  if (h16 && (ce || mn >= (int64_t(1) << 21) || k >= 8192)) { p.wm = 4; p.wn = 4; p.wk = 32; }
+  else if (ce || mn >= (int64_t(1) << 21) || k >= 8192) { p.wm = 2; p.wn = 2; p.wk = 16; }
   else if (mn <= (int64_t(1) << 19)) { p.wm = 1; p.wn = 1; p.wk = 32; }
   else { p.wm = 1; p.wn = 2; p.wk = 16; }
   const int64_t tiles = ((m + 32 * p.wm - 1) / (32 * p.wm)) * ((n + 32 * p.wn - 1) / (32 * p.wn));
@@ -446,16 +497,22 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k, bool defer, bool h16) {
 }
 }  // namespace
 
-int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer, bool h16) { return split_plan(m, n, k, defer, h16).split; }
+int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer, bool h16, bool ce) {
+  return split_plan(m, n, k, defer, h16, ce).split;
+}
 
-int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum, bool sum_a, bool defer, bool h16) {
-  const int split = gemm_split_for(m, n, k, defer, h16);
+int64_t gemm_tile_n(int64_t m, int64_t n, int64_t k, bool defer, bool h16) {
+  return 32 * split_plan(m, n, k, defer, h16, true).wn;
+}
+
+int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum, bool sum_a, bool defer, bool h16, bool ce) {
+  const int split = gemm_split_for(m, n, k, defer, h16, ce);
   if (split <= 1) return 0;
   return int64_t(split) * m * n + (colsum ? int64_t(split) * (sum_a ? m : n) : 0);  // partials, then sums
 }
 
 int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs) {
-  const int split = gemm_split_for(g.m, g.n, g.k, g.defer, g.h16);
+  const int split = gemm_split_for(g.m, g.n, g.k, g.defer, g.h16, g.ce_operand != 0 || g.ce_part);
   if (split <= 1) return 0;
   if (g.bias || g.addend || g.act || g.ldc != g.n) bad("deferred split-K needs a dense output without epilogue");
   if (g.m * g.n > INT32_MAX) bad("deferred split-K output too large");
@@ -483,7 +540,10 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
         (o.workspace == nullptr) != (g.workspace == nullptr))
       bad("gemm group of unlike problems");
   }
-  const SplitPlan plan = split_plan(g.m, g.n, g.k, g.defer, g.h16);
+  const int ce = g.ce_part ? 3 : g.ce_operand;
+  if (ce && (count != 1 || (ce == 3 && g.k > 0 && split_plan(g.m, g.n, g.k, g.defer, g.h16, true).split > 1)))
+    bad("a cross-entropy head GEMM runs alone, and its forward without split-K");
+  const SplitPlan plan = split_plan(g.m, g.n, g.k, g.defer, g.h16, ce != 0);
   const int split = plan.split;
   const int64_t chunk = plan.chunk;
   if (split > 1 && count > 1 && !g.defer) bad("a gemm group sums split-K slices by deferral only");
@@ -494,7 +554,8 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
     const GemmArgs& o = list[q];
     float* ws = nullptr;
     if (split > 1) {
-      if (!o.workspace || o.workspace_floats < gemm_workspace(o.m, o.n, o.k, o.colsum != nullptr, o.sum_a, o.defer, o.h16))
+      if (!o.workspace ||
+          o.workspace_floats < gemm_workspace(o.m, o.n, o.k, o.colsum != nullptr, o.sum_a, o.defer, o.h16, ce != 0))
         bad("gemm split-K workspace too small");
       ws = o.workspace;
     }
@@ -504,7 +565,10 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
     ptrs.epi[q] = GemmEpi{o.bias, o.addend, o.pre_in, o.pre_out, o.act};
     ptrs.ws[q] = ws;
     ptrs.colsum[q] = o.colsum ? (ws ? ws + int64_t(split) * o.m * o.n : o.colsum) : nullptr;
+    ptrs.ce_part[q] = o.ce_part;
+    ptrs.ce_tab[q] = o.ce_tab;
   }
+  ptrs.ce_cols = g.ce_cols;
   float* ws = ptrs.ws[0];
   // Tiles in the grouped order: split slices outermost; within a slice the tiles that share the
   // larger operand's panel are adjacent (M tiles of one column when B is the larger, N tiles of
@@ -558,7 +622,25 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
   else if (plan.wm == 2) MSX_WIDE_H(TA, TB, 2, 2);          \
   else if (plan.wn == 2) MSX_WIDE_H(TA, TB, 1, 2);          \
   else MSX_WIDE_H(TA, TB, 1, 1);
-  if (g.h16) {
+  // The cross-entropy head kernels: the largest tile of each precision, both operands float4.
+#define MSX_CE_V(TA, TB, WM, WN, WK, H, CE)                                                                    \
+  MSX_LAUNCH((k_gemm_w<TA, TB, WM, WN, WK, true, true, H, CE>), wgrid, dim3(256), 0, s, ptrs, g.m, g.n, g.k,  \
+             g.lda, g.ldb, g.ldc, chunk, g.sum_a, vo, order)
+#define MSX_CE_T(TA, TB, WM, WN, WK, H)                       \
+  if (ce == 1) MSX_CE_V(TA, TB, WM, WN, WK, H, 1);            \
+  else if (ce == 2) MSX_CE_V(TA, TB, WM, WN, WK, H, 2);       \
+  else MSX_CE_V(TA, TB, WM, WN, WK, H, 3);
+#define MSX_CE(WM, WN, WK, H)                                 \
+  if (!g.ta && !g.tb) { MSX_CE_T(false, false, WM, WN, WK, H) } \
+  else if (g.ta && !g.tb) { MSX_CE_T(true, false, WM, WN, WK, H) } \
+  else if (!g.ta && g.tb) { MSX_CE_T(false, true, WM, WN, WK, H) } \
+  else { MSX_CE_T(true, true, WM, WN, WK, H) }
+  if (ce) {
+    if (!va || !vb || (ce == 3 && !vo)) bad("a cross-entropy head GEMM needs aligned, padded operands");
+    if (g.h16 && g.colsum) bad("the mixed-precision GEMM takes no column sums");
+    if (g.h16) { MSX_CE(4, 4, 32, true) }
+    else { MSX_CE(2, 2, 16, false) }
+  } else if (g.h16) {
     if (g.colsum) bad("the mixed-precision GEMM takes no column sums");
     if (!g.ta && !g.tb) { MSX_WIDE_HT(false, false) }
     else if (g.ta && !g.tb) { MSX_WIDE_HT(true, false) }
@@ -568,6 +650,9 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
   else if (g.ta && !g.tb) { MSX_WIDE_T(true, false) }
   else if (!g.ta && g.tb) { MSX_WIDE_T(false, true) }
   else { MSX_WIDE_T(true, true) }
+#undef MSX_CE
+#undef MSX_CE_T
+#undef MSX_CE_V
 #undef MSX_WIDE_HT
 #undef MSX_WIDE_H
 #undef MSX_WIDE_HV

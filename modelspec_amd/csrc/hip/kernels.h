@@ -51,6 +51,14 @@ struct GemmArgs {
   const float* pre_in;
   float* pre_out;
   int act;
+  // Cross-entropy fused into a decoder head. ce_part (forward): each output row's (max, sum of
+  // exp(v - max)) over each TN-column tile after the epilogue, [m][gemm_tile_n columns tiles] float2.
+  // ce_operand 1 (A) or 2 (B): that operand is the loss gradient, formed from the logits it
+  // reads: stored element (r, c) becomes ce_grad_of(x, ce_tab[r], c, ce_cols) (ce_head_rows).
+  float* ce_part;
+  const float4* ce_tab;
+  int ce_operand;
+  int64_t ce_cols;
 };
 enum GemmAct : int { EPI_NONE, EPI_GELU, EPI_RELU, EPI_GELU_GRAD, EPI_RELU_GRAD };
 struct GemmEpi { const float* bias; const float* addend; const float* pre_in; float* pre_out; int act; };
@@ -64,14 +72,20 @@ struct GemmPtrs {
   GemmEpi epi[kGemmGroupMax];
   float* ws[kGemmGroupMax];
   float* colsum[kGemmGroupMax];
+  float* ce_part[kGemmGroupMax];
+  const float4* ce_tab[kGemmGroupMax];
+  int64_t ce_cols;
   int count;
 };
+// The output tile width of a GEMM of this shape (the column tiles of ce_part).
+int64_t gemm_tile_n(int64_t m, int64_t n, int64_t k, bool defer = false, bool h16 = false);
 // The split-K factor the launcher uses (with `defer` as in GemmArgs).
-int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer = false, bool h16 = false);
+// ce: a cross-entropy head GEMM (GemmArgs ce_part or ce_operand), which takes the largest tile.
+int gemm_split_for(int64_t m, int64_t n, int64_t k, bool defer = false, bool h16 = false, bool ce = false);
 // Floats of workspace a gemm of this shape needs (0 without split-K): the slices' partial
 // products, then the slices' column (row) sums when asked for.
 int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum = false, bool sum_a = false, bool defer = false,
-                       bool h16 = false);
+                       bool h16 = false, bool ce = false);
 // The column_finalize jobs that finish a deferred split-K gemm (0, 1 or 2 written to jobs).
 int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs);
 void gemm(hipStream_t s, const GemmArgs& g);
@@ -169,6 +183,12 @@ void ce_loss(hipStream_t s, const float* logits, const int32_t* labels, const fl
 // One pass per row: stats, the row loss terms (rowloss non-null) and the gradient (grad non-null,
 // with the upstream gradient scalar g). Needs ce_rows_fits and 16-byte aligned logits and grad.
 bool ce_rows_fits(int64_t v, int64_t ld);
+// The rows of a cross-entropy whose logits came from a GEMM with ce_part: from the `tiles`
+// column-tile partials of each row, its max and sum of exp (stats [rows, 2]), its loss term
+// (rowloss) and its gradient entry tab[r] = (max, 1 / sum, g * w_r / sum(w), label; label -2 when
+// sum(w) is 0) for the GEMMs that form the gradient from the logits.
+void ce_head_rows(hipStream_t s, const float* part, int64_t tiles, const float* logits, int64_t ld, const int32_t* labels,
+                  const float* w, const float* g, float* stats, float* rowloss, float4* tab, int64_t rows, int64_t v);
 void ce_rows(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* g, float* stats,
              float* rowloss, float* grad, int64_t rows, int64_t v, int64_t ld);
 void ce_grad(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats,

@@ -999,6 +999,55 @@ __global__ __launch_bounds__(kCeThreads) void k_ce_rows_p(const float* __restric
   }
 }
 
+// The rows of a cross-entropy whose logits came from a GEMM that left each row's column-tile
+// partials (max, sum of exp(v - max)): one wave a row combines them in tile order (the maximum,
+// then the partial sums rescaled to it), then writes the row's statistics and loss term as
+// k_ce_rows_p does, and its gradient entry for the GEMMs that form the gradient from the logits.
+// Every block sums the weights (f64, as k_ce_rows_p and k_ce_loss do) for the entries' scale.
+__global__ __launch_bounds__(256) void k_ce_head_rows(const float2* __restrict__ part, int64_t tiles,
+                                                      const float* __restrict__ x, int64_t ld,
+                                                      const int32_t* __restrict__ labels, const float* __restrict__ w,
+                                                      const float* __restrict__ g, float* __restrict__ stats,
+                                                      float* __restrict__ rowloss, float4* __restrict__ tab, int64_t rows,
+                                                      int64_t v) {
+  __shared__ double dred[256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  double dd = 0.0;
+  for (int64_t i = tid; i < rows; i += 256) dd += double(w[i]);
+  dred[tid] = dd;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (tid < o) dred[tid] += dred[tid + o];
+    __syncthreads();
+  }
+  const float d = float(dred[0]);
+  const int64_t r = int64_t(blockIdx.x) * 4 + wave;
+  if (r >= rows) return;
+  const int32_t lab = labels[r];
+  const float wr = w[r];
+  const float xl = (lab >= 0 && lab < v) ? x[r * ld + lab] : 0.0f;
+  const float2* pr = part + r * tiles;
+  float m = -INFINITY;
+  for (int64_t t = lane; t < tiles; t += 64) m = fmaxf(m, pr[t].x);
+  m = wave_max(m);
+  float s = 0.0f;
+  for (int64_t t = lane; t < tiles; t += 64) s += pr[t].y * expf(pr[t].x - m);
+  s = wave_sum(s);
+  if (lane == 0) {
+    stats[2 * r] = m;
+    stats[2 * r + 1] = s;
+    if (rowloss) rowloss[r] = m + logf(s) - xl;
+    const float scale = d == 0.0f ? 0.0f : g[0] * wr / d;
+    tab[r] = make_float4(m, 1.0f / s, scale, __int_as_float(d == 0.0f ? -2 : lab));
+  }
+}
+void ce_head_rows(hipStream_t s, const float* part, int64_t tiles, const float* logits, int64_t ld, const int32_t* labels,
+                  const float* w, const float* g, float* stats, float* rowloss, float4* tab, int64_t rows, int64_t v) {
+  if (rows <= 0) return;
+  MSX_LAUNCH(k_ce_head_rows, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, s, reinterpret_cast<const float2*>(part), tiles,
+             logits, ld, labels, w, g, stats, rowloss, tab, rows, v);
+}
+
 int cu_count() {
   static int counts[64] = {};
   int dev = 0;

@@ -514,6 +514,79 @@ void Executor::build() {
     return it != pitch.end() ? it->second : p.node(v).ty.shape.back();
   };
 
+  // Cross-entropy fused into its decoder head: when the logits come from one GEMM (with or
+  // without its bias) that nothing else follows, and the loss gradient is read only by GEMMs (and
+  // their fused column sums), the forward GEMM leaves each row's column-tile partials of max and
+  // sum of exp, one launch finishes the rows (statistics, loss terms, gradient entries), and the
+  // GEMMs that read the gradient form it from the logits as they load them: the gradient is never
+  // stored, and no separate pass reads the logits.
+  struct CeHead {
+    uint32_t logits, labels, weights, grad, seed;
+    int64_t loss, rows, cols, tiles;
+    size_t emit_at;  // the node position its rows launch takes
+    void* part = nullptr;
+    void* tab = nullptr;
+    bool done = false;
+  };
+  std::map<uint32_t, CeHead> ce_head;         // logits value -> its head
+  std::map<uint32_t, uint32_t> ce_head_grad;  // gradient value -> its logits
+  // Off by default: on BERT-tiny (one MI355X) the gradient formed at load costs the two backward
+  // GEMMs 20-24 us each (each element of it is loaded, and its exp taken, by two tiles) and the
+  // forward's partials 12 us, more than the 54 us row pass it replaces (0.917 against 0.900 ms a
+  // step). SessionOptions::fuse_ce_head turns it on.
+  if (s_.opt_.fuse_ce_head) {
+    for (auto& [key, grp] : ce_groups) {
+      if (grp.grad < 0) continue;
+      const uint32_t lg = key[0];
+      const Node& lx = p.node(lg);
+      const uint32_t gv = uint32_t(grp.grad);
+      if (lx.ty.rank() != 2 || outputs.count(lg) || grad_values.count(lg) || outputs.count(gv) || grad_values.count(gv))
+        continue;
+      // The producer: a MatMul, alone or with its bias (AddRows), written as itself.
+      const bool with_bias = lx.op == Op::AddRows && mm_fused.count(lx.operands[0]);
+      const uint32_t mm = with_bias ? lx.operands[0] : lg;
+      if (!with_bias && (lx.op != Op::MatMul || mm_fused.count(lg))) continue;
+      if (mm_transposed.count(mm) || (gemm_epi.count(lg) && gemm_epi.at(lg).node != lg)) continue;
+      const int64_t rows = lx.ty.shape[0], cols = lx.ty.shape[1];
+      if (ld_of(lg) % 4 != 0 || pitch.count(lg) != pitch.count(gv)) continue;
+      const uint32_t seed = p.node(gv).operands[3];
+      bool ok = true;
+      for (auto c : consumers[p.pos.at(lg)]) {
+        const Node& cn = p.nodes[c];
+        ok = ok && (cn.op == Op::CrossEntropy || cn.op == Op::CrossEntropyGrad) && cn.operands[0] == lg &&
+             cn.operands[1] == key[1] && cn.operands[2] == key[2];
+      }
+      auto gemm_reader = [&](uint32_t c) {
+        const Node& cn = p.nodes[c];
+        return cn.op == Op::MatMul && cn.operands[0] != cn.operands[1];
+      };
+      for (auto c : consumers[p.pos.at(gv)]) {
+        const Node& cn = p.nodes[c];
+        if (gemm_reader(c)) continue;
+        if (cn.op == Op::Transpose && folded.count(cn.id)) {
+          for (auto c2 : consumers[c]) ok = ok && gemm_reader(c2);
+          continue;
+        }
+        ok = ok && cn.op == Op::SumRows && colsum_fused.count(cn.id);
+      }
+      // The rows' launch goes where the group's first node is, or, when the upstream gradient is
+      // computed inside the step, at the gradient node (its operand exists there), provided
+      // nothing reads the loss before that.
+      const size_t at_grad = p.pos.at(gv);
+      size_t emit_at = grp.loss >= 0 ? std::min(at_grad, p.pos.at(uint32_t(grp.loss))) : at_grad;
+      const Op seed_op = p.node(seed).op;
+      if (seed_op != Op::Scalar && seed_op != Op::Input && p.pos.at(seed) > emit_at) {
+        emit_at = at_grad;
+        for (auto c : consumers[p.pos.at(uint32_t(grp.loss))]) ok = ok && c > at_grad;
+      }
+      if (!ok) continue;
+      const int64_t K = p.node(p.node(mm).operands[0]).ty.shape[1];
+      const int64_t tn = hk::gemm_tile_n(rows, cols, K, false, s_.opt_.mixed);
+      ce_head[lg] = CeHead{lg, key[1], key[2], gv, seed, grp.loss, rows, cols, (cols + tn - 1) / tn, emit_at};
+      ce_head_grad[gv] = lg;
+    }
+  }
+
   // --- storage ------------------------------------------------------------------------------
   std::map<uint32_t, float> constants;
   for (size_t k = 0; k < n; ++k) {
@@ -549,7 +622,7 @@ void Executor::build() {
       default:
         if (folded.count(x.id) || mm_fused.count(x.id) || mm_transposed.count(x.id) || eg_add.count(x.id)) break;
         if (gemm_epi.count(x.id) && gemm_epi.at(x.id).act != hk::EPI_GELU && gemm_epi.at(x.id).act != hk::EPI_RELU) break;
-        if (ln_skip_storage.count(x.id)) break;
+        if (ln_skip_storage.count(x.id) || ce_head_grad.count(x.id)) break;
         token_[x.id] = arena_.reserve(size_t(pitch.count(x.id) ? x.ty.shape[0] * pitch.at(x.id) : x.ty.count()) * 4);
         break;
     }
@@ -598,6 +671,8 @@ void Executor::build() {
     int64_t bias_id = -1, cs_id = -1;
     Epi epi;
     void* ws = nullptr;
+    void* ce_part = nullptr;  // a cross-entropy head: the forward's row partials
+    void* ce_tab = nullptr;   // or the gradient entries of the operand formed from logits
     std::string what;
   };
   struct Pending {
@@ -638,6 +713,8 @@ void Executor::build() {
                         a.c = F(j.out_id);
                         a.bias = j.bias_id >= 0 ? F(uint32_t(j.bias_id)) : nullptr;
                         a.workspace = j.ws ? static_cast<float*>(A(j.ws)) : nullptr;
+                        a.ce_part = j.ce_part ? static_cast<float*>(A(j.ce_part)) : nullptr;
+                        a.ce_tab = j.ce_tab ? static_cast<const float4*>(A(j.ce_tab)) : nullptr;
                         a.colsum = j.cs_id >= 0 ? F(uint32_t(j.cs_id)) : nullptr;
                         a.act = j.epi.act;
                         if (j.epi.node != j.id && j.epi.act == hk::EPI_NONE) a.addend = F(uint32_t(j.epi.aux));
@@ -869,6 +946,25 @@ void Executor::build() {
           g.tb = !ra.flip;
           std::swap(asrc, bsrc);
         }
+        // A cross-entropy head: an operand that is the loss gradient is formed from the logits.
+        void* ce_tab = nullptr;
+        for (int side = 0; side < 2; ++side) {
+          uint32_t& src = side == 0 ? asrc : bsrc;
+          if (!ce_head_grad.count(src)) continue;
+          CeHead& hd = ce_head.at(ce_head_grad.at(src));
+          if (!hd.tab) hd.tab = R(size_t(hd.rows) * 16);
+          ce_tab = hd.tab;
+          g.ce_operand = side + 1;
+          g.ce_cols = hd.cols;
+          src = hd.logits;
+          what += " (cross-entropy gradient of %" + std::to_string(hd.logits) + ")";
+        }
+        void* ce_part = nullptr;
+        if (ce_head.count(out_id)) {
+          CeHead& hd = ce_head.at(out_id);
+          hd.part = R(size_t(hd.rows * hd.tiles) * 8);
+          ce_part = hd.part;
+        }
         g.lda = ld_of(asrc);
         g.ldb = ld_of(bsrc);
         g.ldc = ld_of(out_id);
@@ -881,7 +977,7 @@ void Executor::build() {
         int64_t bias_id = fused ? int64_t(o[1]) : -1;
         // Split-K partials only the optimizer reads are summed by the batched column finalize.
         g.defer = bias_id < 0 && epi.node == id && only_optimizer_reads(int64_t(out_id)) && only_optimizer_reads(cs_id);
-        int64_t wsf = hk::gemm_workspace(g.m, g.n, g.k, cs_id >= 0, g.sum_a, g.defer, g.h16);
+        int64_t wsf = hk::gemm_workspace(g.m, g.n, g.k, cs_id >= 0, g.sum_a, g.defer, g.h16, g.ce_operand || ce_part);
         void* ws = wsf > 0 ? R(size_t(wsf) * 4) : nullptr;
         g.workspace_floats = wsf;
         auto job = std::make_shared<GemmJob>();
@@ -894,11 +990,13 @@ void Executor::build() {
         job->cs_id = cs_id;
         job->epi = epi;
         job->ws = ws;
+        job->ce_part = ce_part;
+        job->ce_tab = ce_tab;
         job->what = what;
         pending.push_back({gemm_launch({job}), 0, 0, is_step_ && g.defer, {job}});
         pending.back().pure = true;
         if (g.defer && wsf > 0) {
-          const int split = hk::gemm_split_for(g.m, g.n, g.k, true, g.h16);
+          const int split = hk::gemm_split_for(g.m, g.n, g.k, true, g.h16, g.ce_operand != 0);
           const int32_t mn = int32_t(g.m * g.n);
           deferred.push_back({ws, 0, int64_t(out_id), -1, split, mn, mn});
           if (cs_id >= 0) {
@@ -1202,6 +1300,45 @@ void Executor::build() {
         uint32_t lg = o[0], lab = o[1], w = o[2];
         int64_t rows = shape(lg)[0], v = shape(lg)[1];
         const int64_t ld = ld_of(lg);
+        if (ce_head.count(lg)) {
+          if (p.node(lab).op == Op::Input) id_bounds_["#labels:" + p.node(lab).name] = v;
+          if (p.node(w).op == Op::Input) id_bounds_["#weights:" + p.node(w).name] = 0;
+          CeHead& hd = ce_head.at(lg);
+          if (hd.done || k != hd.emit_at) break;
+          hd.done = true;
+          if (!hd.part) throw IrError("cross-entropy head: its forward GEMM was not planned first");
+          if (!hd.tab) hd.tab = R(size_t(rows) * 16);
+          if (!ce_stats_tok.count(lg)) ce_stats_tok[lg] = R(size_t(rows) * 8);
+          void* st2 = ce_stats_tok.at(lg);
+          void* rl = R(size_t(rows) * 4);
+          void* part = hd.part;
+          void* tab = hd.tab;
+          const int64_t tiles = hd.tiles;
+          const uint32_t seed = hd.seed;
+          what = "CrossEntropyHeadRows" + std::string(hd.loss >= 0 ? " loss %" + std::to_string(hd.loss) : "") + " grad %" +
+                 std::to_string(hd.grad) + " " + type_string(p.node(lg).ty);
+          push([=](hipStream_t s) {
+            hk::ce_head_rows(s, static_cast<const float*>(A(part)), tiles, F(lg), ld, I(lab), F(w), F(seed),
+                             static_cast<float*>(A(st2)), static_cast<float*>(A(rl)), static_cast<float4*>(A(tab)), rows,
+                             v);
+          });
+          pending.back().bytes = 4.0 * double(rows * tiles * 2 + rows * (3 + 2 + 1 + 4));
+          if (hd.loss >= 0) {
+            auto dkey = std::make_pair(lg, w);
+            if (!ce_den_tok.count(dkey)) ce_den_tok[dkey] = R(4);
+            void* den = ce_den_tok.at(dkey);
+            const uint32_t lid = uint32_t(hd.loss);
+            what = "CrossEntropyLoss %" + std::to_string(hd.loss);
+            push([=](hipStream_t s) {
+              hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(st2)), F(lid), static_cast<float*>(A(den)), rows, v,
+                          ld, static_cast<float*>(A(rl)));
+            });
+            bytes = 4.0 * double(2 * rows + 2);
+          } else {
+            bytes = pending.back().bytes;
+          }
+          break;
+        }
         if (x.op == Op::CrossEntropyGrad && ld_of(id) != ld) throw IrError("cross-entropy gradient pitch differs from its logits'");
         if (p.node(lab).op == Op::Input) id_bounds_["#labels:" + p.node(lab).name] = v;
         if (p.node(w).op == Op::Input) id_bounds_["#weights:" + p.node(w).name] = 0;
@@ -1309,7 +1446,7 @@ void Executor::build() {
              a.pad_b == b.pad_b && a.pad_c == b.pad_c && a.h16 == b.h16 && x.epi.act == y.epi.act &&
              (x.bias_id >= 0) == (y.bias_id >= 0) && (x.cs_id >= 0) == (y.cs_id >= 0) &&
              (x.epi.node != x.id) == (y.epi.node != y.id) && (x.ws != nullptr) == (y.ws != nullptr) &&
-             (split == 1 || a.defer);
+             (split == 1 || a.defer) && !x.ce_part && !x.ce_tab && !y.ce_part && !y.ce_tab;
     };
     auto reads = [](const GemmJob& j) {
       std::vector<int64_t> r{int64_t(j.asrc), int64_t(j.bsrc), j.bias_id};

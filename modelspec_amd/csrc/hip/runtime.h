@@ -70,6 +70,8 @@ struct SessionOptions {
   bool mixed = false;
   float loss_scale = 65536.0f;
   uint32_t scale_window = 2000;
+  // Cross-entropy fused into its decoder head GEMMs (Executor::build).
+  bool fuse_ce_head = false;
 };
 
 class Session : public Engine {

@@ -125,13 +125,17 @@ def test_tied_decoder_gradients(ctx, oracle, v, h, r, n):
     assert within(got[3], want[3], ((ax.T @ adl).T + seg).reshape(-1))[0]
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("v,h,r,n,g_const", [(1000, 64, 96, 256, True), (1001, 64, 96, 256, False),
                                              (30522, 128, 832, 4096, True)])
-def test_decoder_cross_entropy_head(ctx, oracle, v, h, r, n, g_const):
+def test_decoder_cross_entropy_head(ctx, oracle, request, v, h, r, n, g_const, fused):
     """The masked-LM head as the step has it: logits = x E^T + b, the cross-entropy loss and
     gradient, dX, the transposed dW with the bias sums as row sums, added to the embedding
     gradient; the upstream gradient a constant or computed. Vocabularies that are not a multiple of
-    4 keep the logits and their gradient in rows padded to 64 floats."""
+    4 keep the logits and their gradient in rows padded to 64 floats. `fused`: the cross-entropy
+    folded into the head GEMMs (msx_set_fusion)."""
+    ctx.set_fusion(ce_head=fused)
+    request.addfinalizer(lambda: ctx.set_fusion(ce_head=False))
     E, x, b = fast_values(61, v * h).reshape(v, h), fast_values(62, r * h).reshape(r, h), fast_values(63, v, 0.5)
     G = fast_values(64, n * h).reshape(n, h)
     rng = np.random.default_rng(7)
