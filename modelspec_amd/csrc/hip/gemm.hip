@@ -291,10 +291,10 @@ __global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_
   float4 ra[HA], rb[HB];
 #pragma unroll
   for (int h = 0; h < HA; ++h)
-    if (tid + 256 * h < GA) ra[h] = load_a(kbeg, h);
+    if (GA % 256 == 0 || tid + 256 * h < GA) ra[h] = load_a(kbeg, h);
 #pragma unroll
   for (int h = 0; h < HB; ++h)
-    if (tid + 256 * h < GB) rb[h] = load_b(kbeg, h);
+    if (GB % 256 == 0 || tid + 256 * h < GB) rb[h] = load_b(kbeg, h);
   // Column sums: thread t adds tile column t mod T over the K rows (t / T) per .. + per of each
   // K tile, per = WK / (256 / T).
   const int T = sum_a ? TM : TN;
@@ -313,31 +313,31 @@ __global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_
       } else {
 #pragma unroll
         for (int h = 0; h < HA; ++h)
-          if (tid + 256 * h < GA) wide_store_h<!TA, TM, PH, WK>(Ah0 + buf * (TM * PH), tid + 256 * h, ra[h]);
+          if (GA % 256 == 0 || tid + 256 * h < GA) wide_store_h<!TA, TM, PH, WK>(Ah0 + buf * (TM * PH), tid + 256 * h, ra[h]);
       }
       if constexpr (RB) {
         rows_store_h<TN, PH, HB>(Bh0 + buf * (TN * PH), tid, rb);
       } else {
 #pragma unroll
         for (int h = 0; h < HB; ++h)
-          if (tid + 256 * h < GB) wide_store_h<TB, TN, PH, WK>(Bh0 + buf * (TN * PH), tid + 256 * h, rb[h]);
+          if (GB % 256 == 0 || tid + 256 * h < GB) wide_store_h<TB, TN, PH, WK>(Bh0 + buf * (TN * PH), tid + 256 * h, rb[h]);
       }
     } else {
 #pragma unroll
       for (int h = 0; h < HA; ++h)
-        if (tid + 256 * h < GA) wide_store<!TA, TM, LA, WK>(As0 + buf * (WK * LA), tid + 256 * h, ra[h]);
+        if (GA % 256 == 0 || tid + 256 * h < GA) wide_store<!TA, TM, LA, WK>(As0 + buf * (WK * LA), tid + 256 * h, ra[h]);
 #pragma unroll
       for (int h = 0; h < HB; ++h)
-        if (tid + 256 * h < GB) wide_store<TB, TN, LB, WK>(Bs0 + buf * (WK * LB), tid + 256 * h, rb[h]);
+        if (GB % 256 == 0 || tid + 256 * h < GB) wide_store<TB, TN, LB, WK>(Bs0 + buf * (WK * LB), tid + 256 * h, rb[h]);
     }
     __syncthreads();
     if (k0 + WK < kend) {
 #pragma unroll
       for (int h = 0; h < HA; ++h)
-        if (tid + 256 * h < GA) ra[h] = load_a(k0 + WK, h);
+        if (GA % 256 == 0 || tid + 256 * h < GA) ra[h] = load_a(k0 + WK, h);
 #pragma unroll
       for (int h = 0; h < HB; ++h)
-        if (tid + 256 * h < GB) rb[h] = load_b(k0 + WK, h);
+        if (GB % 256 == 0 || tid + 256 * h < GB) rb[h] = load_b(k0 + WK, h);
     }
     if constexpr (H) {
       const _Float16* ah = Ah0 + buf * (TM * PH) + (wm + (lane & 15)) * PH + 8 * (lane >> 4);
