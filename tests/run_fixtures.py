@@ -1,0 +1,57 @@
+"""The committed oracle runs of tests/golden/ (written by tests/golden/make_oracle_losses.py) and
+the reference's run tolerance applied to them (crates/modelspec-runtime/tests/common/mod.rs:17-40):
+every loss and every kept parameter element within 1e-4 + 1e-3 |c|; an attention key bias, whose
+exact gradient is zero so that both backends carry only rounding noise there, within
+1e-4 + steps * lr * 1e-3 (zero_gradient_bound)."""
+import json
+import os
+
+import numpy as np
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+RUN_ATOL, RUN_RTOL = 1e-4, 1e-3
+
+
+def path(kind, config, steps, ext):
+    return os.path.join(GOLDEN, f"oracle_{kind}_{config}_{steps}.{ext}")
+
+
+def available(config, steps):
+    return all(os.path.exists(path(k, config, steps, e))
+               for k, e in (("losses", "npy"), ("param_norms", "npy"), ("params", "npz"), ("meta", "json")))
+
+
+def load(config, steps):
+    """(losses, norms, idx, val, meta) of a committed run; idx is every index when stored empty."""
+    losses = np.load(path("losses", config, steps, "npy"))
+    norms = np.load(path("param_norms", config, steps, "npy"))
+    with np.load(path("params", config, steps, "npz")) as z:
+        idx, val = z["idx"].astype(np.int64), z["val"]
+    if idx.size == 0:
+        idx = np.arange(val.size, dtype=np.int64)
+    with open(path("meta", config, steps, "json")) as f:
+        meta = json.load(f)
+    return losses, norms, idx, val, meta
+
+
+def param_tolerance(step_ir, steps, lr, key_biases):
+    """Per-element absolute tolerance of the flat parameter vector (before the relative term)."""
+    from modelspec_amd import api
+    atol = []
+    for p, shape in api.param_shapes(step_ir):
+        n = int(np.prod(shape))
+        atol.append(np.full(n, RUN_ATOL + (steps * lr * 1e-3 if p in key_biases else 0.0)))
+    return np.concatenate(atol)
+
+
+def check_run(got_losses, got_params, config, steps, lr, step_ir, key_biases):
+    """Asserts a device run against the committed oracle run of (config, steps)."""
+    want_l, want_n, idx, val, _ = load(config, steps)
+    assert got_losses.shape == want_l.shape, (got_losses.shape, want_l.shape)
+    assert np.all(np.isfinite(got_losses))
+    ok = np.abs(got_losses - want_l) <= RUN_ATOL + RUN_RTOL * np.abs(want_l)
+    assert ok.all(), (config, np.flatnonzero(~ok)[:5], got_losses[~ok][:5], want_l[~ok][:5])
+    atol = param_tolerance(step_ir, steps, lr, key_biases)
+    g = got_params[idx]
+    bad = np.abs(g - val) > atol[idx] + RUN_RTOL * np.abs(val)
+    assert not bad.any(), (config, int(bad.sum()), idx[bad][:5], g[bad][:5], val[bad][:5])

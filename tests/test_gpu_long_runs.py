@@ -1,0 +1,29 @@
+"""Full-length runs of the BASELINE configs on the MI355X against the CPU oracle's runs of the same
+seed and inputs: the MLP classifier for 1,000 steps, the transformer block for 500 and BERT-tiny
+for 1,000 ("Parity runs"). The oracle takes minutes to hours for them on one core, so
+its runs are fixtures (tests/golden/oracle_*_<config>_<steps>.*): every loss, and every parameter
+element (the MLP) or a seeded sample of at least 65,536 elements stratified over every tensor (the
+transformer block, BERT-tiny), is held to the reference's run tolerance (tests/run_fixtures.py)."""
+import numpy as np
+import pytest
+
+from modelspec_amd import api
+
+import run_fixtures
+from test_gpu_train import key_biases
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("config,steps,lr", [("mlp_classifier", 1000, 0.01), ("transformer_block", 500, 1e-3),
+                                             ("bert_tiny", 1000, 1e-4)])
+def test_full_run_tracks_the_oracle(ctx, config, steps, lr):
+    if not run_fixtures.available(config, steps):
+        pytest.skip(f"no committed oracle run of {config} for {steps} steps")
+    step_ir, _ = api.compile_config(config, -1, steps)
+    print(f"{config} {steps} steps", flush=True)
+    got_l, got_p, _ = ctx.train_config(config, steps=steps)
+    run_fixtures.check_run(got_l, got_p, config, steps, lr, step_ir, key_biases(step_ir))
+    # The run trains: the last losses are below the first.
+    want_l = run_fixtures.load(config, steps)[0]
+    assert want_l[-10:].mean() < want_l[:10].mean()
