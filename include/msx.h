@@ -84,6 +84,14 @@ int msx_load(msx_ctx* ctx, const char* step_ir, const char* forward_ir, uint64_t
 
 /* Uploads every parameter (ParamId order, `n` arrays of counts[i] floats) and zeroes the AdamW
  * moments and the loss log. Replaces the parameter upload of vulkan/stepwise.rs:343-400. */
+/* The launch plans this backend makes of a step and its forward program, without a device: for
+ * each program one line a launch (the values it completes, whether it runs on the side stream, its
+ * algorithmic flop and bytes), then its buffer plan (the arena size and each value's offset). The
+ * counterpart of the reference's printed Kernel IR (crates/modelspec-core/src/ir/kernel.rs:1407,
+ * the `*.kernel.ir` goldens): its fusion groups and buffers, as this backend plans them. The text
+ * is freed with msx_free. */
+int msx_plan(const char* step_ir, const char* forward_ir, uint32_t prediction_output, int32_t mixed, char** plan);
+
 int msx_set_params(msx_ctx* ctx, const float* const* values, const uint64_t* counts, uint32_t n);
 int msx_read_param(msx_ctx* ctx, uint32_t param, float* out, uint64_t count);
 /* which = 'm' or 'v'. */

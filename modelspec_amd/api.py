@@ -69,6 +69,7 @@ def lib():
                                    ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(HeldOutMetrics)]
         L.msx_evaluate_static.argtypes = L.msx_evaluate.argtypes
         L.msx_set_fusion.argtypes = [vp, u32]
+        L.msx_plan.argtypes = [ctypes.c_char_p, ctypes.c_char_p, u32, ctypes.c_int32, ctypes.POINTER(ctypes.c_void_p)]
         L.msx_train_config_eval.argtypes = [vp, ctypes.c_char_p, c64, u64, u64, vp, u64, vp,
                                             ctypes.POINTER(HeldOutMetrics), u64, ctypes.POINTER(u64),
                                             ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
@@ -111,6 +112,18 @@ CONFIG_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "configs")
 def config_file(name):
     """The path of the .mspec source of a config this package ships (modelspec_amd/configs)."""
     return os.path.join(CONFIG_DIR, name + ".mspec")
+
+
+def plan(step_ir, forward_ir, prediction_output=1, mixed=False):
+    """This backend's launch and buffer plans of a step and its forward program (msx_plan; no
+    device needed)."""
+    out = ctypes.c_void_p()
+    _check(lib().msx_plan(step_ir.encode(), forward_ir.encode(), prediction_output, 1 if mixed else 0,
+                          ctypes.byref(out)))
+    try:
+        return ctypes.string_at(out).decode()
+    finally:
+        lib().msx_free(out)
 
 
 def compile_config(name, masked_rows=-1, steps=-1):

@@ -194,6 +194,22 @@ int msx_load(msx_ctx* ctx, const char* step_ir, const char* forward_ir, uint64_t
   });
 }
 
+int msx_plan(const char* step_ir, const char* forward_ir, uint32_t prediction_output, int32_t mixed, char** plan) {
+  return guarded([&] {
+    if (!step_ir || !forward_ir || !plan) return fail(MSX_E_INVALID, "null argument");
+    msx::TrainingStep step = msx::parse_step(step_ir);
+    if (!step.has_optimizer) return fail(MSX_E_INVALID, "the step IR has no optimizer");
+    msx::Program forward = msx::parse_program(forward_ir);
+    if (prediction_output >= forward.outputs.size()) return fail(MSX_E_INVALID, "no such forward output");
+    msx::SessionOptions o;
+    o.plan_only = true;
+    o.mixed = mixed != 0;
+    msx::Session s(0, step, forward, 0, forward.outputs[prediction_output], nullptr, o);
+    *plan = dup(s.plan_text());
+    return MSX_OK;
+  });
+}
+
 int msx_set_params(msx_ctx* ctx, const float* const* values, const uint64_t* counts, uint32_t n) {
   return guarded([&] {
     if (!ctx->session) return fail(MSX_E_INVALID, "no step is loaded");

@@ -21,6 +21,10 @@ enum EwOp : int { EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_RELU, EW_RELU_GRAD, EW_GELU
 
 // o[i] = op(a[a_scalar ? 0 : i], b[b_scalar ? 0 : i]) for i < n (binary ops), op(a[i]) for unary.
 void elementwise(hipStream_t s, int op, const float* a, const float* b, float* o, int64_t n, bool a_scalar, bool b_scalar);
+// o = (a op1 b) op2 s, or s op2 (a op1 b) when !inner_left; s a single value; each op rounded as
+// elementwise rounds it.
+void elementwise2(hipStream_t s, int op1, const float* a, const float* b, int op2, const float* sc, bool inner_left,
+                  float* o, int64_t n);
 void fill_from(hipStream_t s, const float* scalar, float* o, int64_t n);  // BroadcastScalar
 void fill_zero(hipStream_t s, void* o, int64_t bytes);                     // kernel, not a memset
 void copy(hipStream_t s, const float* a, float* o, int64_t n);

@@ -44,6 +44,30 @@ void elementwise(hipStream_t s, int op, const float* a, const float* b, float* o
   MSX_LAUNCH(k_elementwise, dim3(grid), dim3(256), 0, s, op, a, b, o, n, int(as), int(bs));
 }
 
+__device__ __forceinline__ float ew_apply(int op, float x, float y) {
+  switch (op) {
+    case EW_ADD: return x + y;
+    case EW_SUB: return x - y;
+    case EW_MUL: return x * y;
+    default: return x / y;
+  }
+}
+__global__ void k_elementwise2(int op1, const float* __restrict__ a, const float* __restrict__ b, int op2,
+                               const float* __restrict__ sc, int inner_left, float* __restrict__ o, int64_t n) {
+  const float sv = sc[0];
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+    const float t = ew_apply(op1, a[i], b[i]);
+    o[i] = inner_left ? ew_apply(op2, t, sv) : ew_apply(op2, sv, t);
+  }
+}
+void elementwise2(hipStream_t s, int op1, const float* a, const float* b, int op2, const float* sc, bool inner_left,
+                  float* o, int64_t n) {
+  if (n <= 0) return;
+  if (op1 < EW_ADD || op1 > EW_DIV || op2 < EW_ADD || op2 > EW_DIV) bad("elementwise2 takes binary arithmetic");
+  unsigned grid = std::min<unsigned>(blocks_for(n, 256), 8192);
+  MSX_LAUNCH(k_elementwise2, dim3(grid), dim3(256), 0, s, op1, a, b, op2, sc, int(inner_left), o, n);
+}
+
 void copy(hipStream_t s, const float* a, float* o, int64_t n) { elementwise(s, EW_COPY, a, nullptr, o, n, false, false); }
 
 __global__ void k_fill_from(const float* __restrict__ v, float* __restrict__ o, int64_t n) {

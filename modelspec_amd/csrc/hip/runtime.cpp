@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <array>
@@ -84,6 +85,7 @@ Resolved resolve(const Program& p, uint32_t v) {
 // ---------------------------------------------------------------------------------------------
 Executor::Executor(Session& s, const Program& p, bool is_step) : s_(s), p_(p), is_step_(is_step) {
   build();
+  if (s_.opt_.plan_only) return;
   for (int i = 0; i < kRing; ++i) {
     hip_check(hipHostMalloc(&pinned_[i], std::max<size_t>(input_bytes_, 256), hipHostMallocDefault), "hipHostMalloc");
     hip_check(hipEventCreateWithFlags(&slot_done_[i], hipEventDisableTiming), "hipEventCreate");
@@ -587,6 +589,41 @@ void Executor::build() {
     }
   }
 
+  // Elementwise chains (the reference's elementwise fusion groups, spirv kernel "Sub>Mul@0"): a
+  // binary elementwise value read only by a binary elementwise op with a rank-0 other operand is
+  // computed inside that op's launch, y = (a op1 b) op2 s, and never stored.
+  struct EwChain { uint32_t inner; int op1, op2; bool inner_left; };
+  std::map<uint32_t, EwChain> ew_chain;  // outer value -> its inner op
+  std::set<uint32_t> ew_inner;           // inner values so computed
+  auto ew_code = [](Op op) {
+    return op == Op::Add ? hk::EW_ADD : op == Op::Sub ? hk::EW_SUB : op == Op::Mul ? hk::EW_MUL : hk::EW_DIV;
+  };
+  auto binary_ew = [](Op op) { return op == Op::Add || op == Op::Sub || op == Op::Mul || op == Op::Div; };
+  for (size_t k = 0; k < n; ++k) {
+    const Node& x = p.nodes[k];
+    if (!need[k] || !binary_ew(x.op) || optimizer.count(x.id) || x.ty.rank() == 0 || outputs.count(x.id) ||
+        grad_values.count(x.id) || consumers[k].size() != 1)
+      continue;
+    if (eg_add_nodes.count(x.id) || epi_nodes.count(x.id) || ln_fused_nodes.count(x.id) || ln_post_nodes.count(x.id))
+      continue;
+    const Node& a = p.node(x.operands[0]);
+    const Node& b = p.node(x.operands[1]);
+    if (a.ty.count() != x.ty.count() || b.ty.count() != x.ty.count()) continue;  // no broadcast inside
+    const Node& y = p.nodes[consumers[k][0]];
+    if (!binary_ew(y.op) || optimizer.count(y.id) || y.ty.count() != x.ty.count() || ew_inner.count(y.id)) continue;
+    if (eg_add_nodes.count(y.id) || epi_nodes.count(y.id) || ln_fused_nodes.count(y.id) || ln_post_nodes.count(y.id))
+      continue;
+    const bool left = y.operands[0] == x.id;
+    const uint32_t other = left ? y.operands[1] : y.operands[0];
+    if (other == x.id || p.node(other).ty.rank() != 0) continue;
+    ew_chain[y.id] = EwChain{x.id, ew_code(x.op), ew_code(y.op), left};
+    ew_inner.insert(x.id);
+  }
+  // Rank-0 arithmetic on constants is folded once, in f32 as the kernel would round it (the
+  // reference folds the mse gradient's 1.0 * 0.25 the same way); the loss-scaled seed is not a
+  // constant and is never folded.
+  std::set<uint32_t> folded_scalar;
+
   // --- storage ------------------------------------------------------------------------------
   std::map<uint32_t, float> constants;
   for (size_t k = 0; k < n; ++k) {
@@ -619,6 +656,18 @@ void Executor::build() {
         token_[x.id] = arena_.reserve(4);
         constants[x.id] = x.scalar;
         break;
+      case Op::Add: case Op::Sub: case Op::Mul: case Op::Div:
+        if (x.ty.rank() == 0 && constants.count(x.operands[0]) && constants.count(x.operands[1]) &&
+            !optimizer.count(x.id)) {
+          const float a = constants.at(x.operands[0]), b = constants.at(x.operands[1]);
+          const volatile float r = x.op == Op::Add ? a + b : x.op == Op::Sub ? a - b : x.op == Op::Mul ? a * b : a / b;
+          token_[x.id] = arena_.reserve(4);
+          constants[x.id] = r;
+          folded_scalar.insert(x.id);
+          break;
+        }
+        if (ew_inner.count(x.id)) break;  // computed inside its consumer's launch
+        [[fallthrough]];
       default:
         if (folded.count(x.id) || mm_fused.count(x.id) || mm_transposed.count(x.id) || eg_add.count(x.id)) break;
         if (gemm_epi.count(x.id) && gemm_epi.at(x.id).act != hk::EPI_GELU && gemm_epi.at(x.id).act != hk::EPI_RELU) break;
@@ -894,6 +943,20 @@ void Executor::build() {
       case Op::Input: case Op::ParamRead: case Op::Scalar: break;
       case Op::Add: case Op::Sub: case Op::Mul: case Op::Div: {
         if (eg_add_nodes.count(id) || epi_nodes.count(id) || ln_fused_nodes.count(id)) break;  // written by a fused launch
+        if (folded_scalar.count(id) || ew_inner.count(id)) break;  // a constant, or inside its consumer's launch
+        if (ew_chain.count(id)) {
+          const EwChain c = ew_chain.at(id);
+          const Node& in = p.node(c.inner);
+          const uint32_t a = in.operands[0], b = in.operands[1];
+          const uint32_t sc = c.inner_left ? o[1] : o[0];
+          const int op1 = c.op1, op2 = c.op2;
+          const bool left = c.inner_left;
+          what = std::string(op_name(in.op)) + ">" + op_name(x.op) + " %" + std::to_string(c.inner) + " %" +
+                 std::to_string(id) + " " + type_string(x.ty);
+          push([=](hipStream_t s) { hk::elementwise2(s, op1, F(a), F(b), op2, F(sc), left, F(id), count); });
+          bytes = 4.0 * (3.0 * double(count) + 1.0);
+          break;
+        }
         int op = x.op == Op::Add ? hk::EW_ADD : x.op == Op::Sub ? hk::EW_SUB : x.op == Op::Mul ? hk::EW_MUL : hk::EW_DIV;
         bool as = p.node(o[0]).ty.rank() == 0 && count > 1, bs = p.node(o[1]).ty.rank() == 0 && count > 1;
         uint32_t a = o[0], b = o[1];
@@ -1569,9 +1632,11 @@ void Executor::build() {
     loss_value = p.outputs.at(0);
   }
 
-  arena_.commit();
-  for (auto& [vid, val] : constants) hip_check(hipMemcpy(ptr(vid), &val, 4, hipMemcpyHostToDevice), "hipMemcpy (constants)");
-  for (auto& slot : inputs_) fixed_[slot.id] = static_cast<char*>(arena_.at(input_token_)) + slot.offset;
+  if (!s_.opt_.plan_only) {
+    arena_.commit();
+    for (auto& [vid, val] : constants) hip_check(hipMemcpy(ptr(vid), &val, 4, hipMemcpyHostToDevice), "hipMemcpy (constants)");
+    for (auto& slot : inputs_) fixed_[slot.id] = static_cast<char*>(arena_.at(input_token_)) + slot.offset;
+  }
   for (auto& pd : pending) {
     launches_.push_back(pd.make());
     launches_.back().flop = pd.flop;
@@ -1580,6 +1645,23 @@ void Executor::build() {
     launches_.back().pure = pd.pure;
   }
   join_at_ = join_at;
+}
+
+std::string Executor::plan_text() const {
+  std::string out;
+  size_t k = 0;
+  for (auto& l : launches_) {
+    char work[96];
+    std::snprintf(work, sizeof work, " flop %.0f bytes %.0f", l.flop, l.bytes);
+    out += "  " + std::to_string(k++) + ": " + l.what + (l.side ? " [side]" : "") + work + "\n";
+  }
+  std::vector<std::pair<size_t, uint32_t>> slices;
+  for (auto& [vid, tok] : token_) slices.push_back({DeviceArena::offset(tok), vid});
+  std::sort(slices.begin(), slices.end());
+  out += "  arena " + std::to_string(arena_.bytes()) + " bytes, " + std::to_string(slices.size()) + " values";
+  for (auto& [off, vid] : slices) out += " %" + std::to_string(vid) + "@" + std::to_string(off);
+  out += "\n";
+  return out;
 }
 
 void Executor::stage(const Batch& batch) {
@@ -1737,6 +1819,26 @@ Session::Session(int device, const TrainingStep& step, const Program& forward, u
     : device_(device), step_(step), forward_(forward), seed_(seed), prediction_(prediction), opt_(options) {
   step_.program.reindex();
   forward_.reindex();
+  if (opt_.plan_only) {
+    // No device: the plans only. Parameter, gradient and moment slices are offsets from a null
+    // base, never dereferenced.
+    if (corpus) throw IrError("a plan-only session takes no packed corpus");
+    const auto& params = step_.program.params;
+    offset_.assign(params.size(), 0);
+    int64_t at = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+      for (size_t q = 0; q < params.size(); ++q) {
+        if ((step_.updates.count(uint32_t(q)) != 0) != (pass == 0)) continue;
+        offset_[q] = at;
+        at += (params[q].ty.count() + 63) / 64 * 64;
+      }
+      if (pass == 0) trained_ = at;
+    }
+    total_ = std::max<int64_t>(at, 64);
+    if (step_.has_optimizer) step_exec_ = std::make_unique<Executor>(*this, step_.program, true);
+    fwd_exec_ = std::make_unique<Executor>(*this, forward_, false);
+    return;
+  }
   hip_check(hipSetDevice(device), "hipSetDevice");
   hk::prepare();
   if (corpus) {
@@ -2037,6 +2139,13 @@ HeldOutSums Session::held_out_in(const HeldOut& h, bool no_alloc) {
   out.denominator = got.denominator;
   out.selected = uint64_t(got.selected);
   out.has_totals = true;
+  return out;
+}
+
+std::string Session::plan_text() const {
+  std::string out;
+  if (step_exec_) out += "plan step (" + std::to_string(step_exec_->launches().size()) + " launches)\n" + step_exec_->plan_text();
+  out += "plan forward (" + std::to_string(fwd_exec_->launches().size()) + " launches)\n" + fwd_exec_->plan_text();
   return out;
 }
 

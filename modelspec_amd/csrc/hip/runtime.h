@@ -34,6 +34,7 @@ class DeviceArena {
   void commit();                // one hipMalloc of everything reserved
   void* at(void* token) const;  // device address of a reservation
   size_t bytes() const { return size_; }
+  static size_t offset(void* token) { return reinterpret_cast<size_t>(token) - 1; }
 
  private:
   size_t size_ = 0;
@@ -72,6 +73,9 @@ struct SessionOptions {
   uint32_t scale_window = 2000;
   // Cross-entropy fused into its decoder head GEMMs (Executor::build).
   bool fuse_ce_head = false;
+  // Plan only: the step and forward programs are planned (launches, fusions, buffer offsets) and
+  // nothing touches a device; such a session can print its plans and cannot run.
+  bool plan_only = false;
 };
 
 class Session : public Engine {
@@ -101,6 +105,8 @@ class Session : public Engine {
   HeldOutSums held_out_static(const HeldOut& h);
   static constexpr int64_t kStaticEvalRows = 65536;
   std::vector<float> losses() override;
+  // The plans of a plan-only (or any) session: the step's, then the forward program's.
+  std::string plan_text() const;
 
   // Runs the step plan eagerly (no graph) with one event pair around every launch; returns the
   // launches and their milliseconds for the current inputs (the step's update is applied).
@@ -190,6 +196,9 @@ class Executor {
   void stage(const Batch& batch);
   void run(hipStream_t s);  // every launch, in order
   const std::vector<Launch>& launches() const { return launches_; }
+  // The launch plan as text: one line a launch (its place, the values it completes, side stream,
+  // algorithmic flop and bytes), then the buffer plan (every value's arena slice).
+  std::string plan_text() const;
   const void* value(uint32_t id) const;
   uint32_t loss_value = 0;
 
