@@ -113,10 +113,13 @@ void layer_norm(hipStream_t s, const float* x, const float* gamma, const float* 
 // dropout), y = LayerNorm(s; gamma, beta), yd = dropout(y) (dout_token non-null); each of s_out,
 // y_out, stats, yd_out written when non-null. Dropout as `dropout` (threshold, scale, seed). With
 // `gather` ([rows] ids into the src_rows rows of a and b), row r of s is the sum's row gather[r].
+// With a_ids (b_ids), a (b) is a table of a_rows (b_rows) rows and its row r is the Embedding row
+// a_ids[r] (0 for an id out of range); not combined with `gather` or an input dropout.
 void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_token, uint64_t din_threshold,
               float din_scale, const float* gamma, const float* beta, float* s_out, float* y_out, float* stats,
               const int32_t* dout_token, uint64_t dout_threshold, float dout_scale, float* yd_out, int64_t rows,
-              int64_t h, uint64_t seed, const int32_t* gather = nullptr, int64_t src_rows = 0);
+              int64_t h, uint64_t seed, const int32_t* gather = nullptr, int64_t src_rows = 0,
+              const int32_t* a_ids = nullptr, int64_t a_rows = 0, const int32_t* b_ids = nullptr, int64_t b_rows = 0);
 
 // LayerNorm backward in one pass: dx when non-null, and when `partial` is non-null the per-block
 // partial sums [ln_backward_blocks, 2 h] of g * xhat (gamma gradient) then g (beta gradient), to be
@@ -181,9 +184,13 @@ void prepare_attention();
 // Cross-entropy over logits [rows, v] with row pitch ld (>= v): stats = [rows, 2] (max, total);
 // den = [1] f32 weight sum rounded from f64; the gradient o has row pitch ld too.
 void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, int64_t v, int64_t ld);
+// The step's loss log: record_loss appends losses[counter] (when counter < capacity) and counts.
+struct LossLog { float* losses = nullptr; uint32_t* counter = nullptr; uint32_t capacity = 0; };
 // With rowloss non-null the per-row loss terms come from there (ce_rows) instead of stats and logits.
+// With log.losses non-null the loss is also appended to the log, as record_loss would.
 void ce_loss(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats,
-             float* loss, float* den, int64_t rows, int64_t v, int64_t ld, const float* rowloss = nullptr);
+             float* loss, float* den, int64_t rows, int64_t v, int64_t ld, const float* rowloss = nullptr,
+             LossLog log = {});
 // One pass per row: stats, the row loss terms (rowloss non-null) and the gradient (grad non-null,
 // with the upstream gradient scalar g). Needs ce_rows_fits and 16-byte aligned logits and grad.
 bool ce_rows_fits(int64_t v, int64_t ld);

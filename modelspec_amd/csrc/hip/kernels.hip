@@ -253,7 +253,10 @@ void layer_norm(hipStream_t s, const float* x, const float* gamma, const float* 
 // written when asked. The dropout keep rule is k_dropout's (Philox word 0 of the element index).
 // With `gather`, output row r takes its a, b and input dropout from row gather[r] of those
 // (an Embedding of the sum: element indices are the source rows'; an id out of range gives 0).
+// With `ga` (`gb`), a (b) is itself an Embedding: row r of a is row ga.ids[r] of the table `a`, 0
+// for an id outside [0, ga.rows) (k_embedding's rule), and the gathered rows are not written.
 struct DropoutSpec { const int32_t* token; uint64_t threshold; float scale; };
+struct RowGather { const int32_t* ids; int64_t rows; };
 template <int CPL>
 __global__ __launch_bounds__(256) void k_ln_fused(const float* __restrict__ a, const float* __restrict__ b,
                                                   DropoutSpec din, const float* __restrict__ gamma,
@@ -261,13 +264,15 @@ __global__ __launch_bounds__(256) void k_ln_fused(const float* __restrict__ a, c
                                                   float* __restrict__ y_out, float* __restrict__ stats,
                                                   DropoutSpec dout, float* __restrict__ yd_out, int64_t rows, int64_t h,
                                                   uint32_t seed_lo, uint32_t seed_hi, const int32_t* __restrict__ gather,
-                                                  int64_t src_rows) {
+                                                  int64_t src_rows, RowGather ga, RowGather gb) {
   const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
   const int64_t src = gather ? int64_t(gather[row]) : row;
   const bool src_ok = src >= 0 && src < src_rows;
   const uint32_t il = din.token ? uint32_t(din.token[0]) : 0u, ih = din.token ? uint32_t(din.token[1]) : 0u;
+  const int64_t ra = ga.ids ? int64_t(ga.ids[row]) : src, rb = gb.ids ? int64_t(gb.ids[row]) : src;
+  const bool a_ok = ga.ids ? ra >= 0 && ra < ga.rows : src_ok, b_ok = gb.ids ? rb >= 0 && rb < gb.rows : src_ok;
   float sv[CPL];
   float sum = 0.0f;
 #pragma unroll
@@ -275,7 +280,10 @@ __global__ __launch_bounds__(256) void k_ln_fused(const float* __restrict__ a, c
     const int64_t c = lane + 64 * j;
     sv[j] = 0.0f;
     if (c < h) {
-      if (src_ok) {
+      if (ga.ids || gb.ids) {
+        const float v = b_ok ? b[rb * h + c] : 0.0f;
+        sv[j] = a ? (a_ok ? a[ra * h + c] : 0.0f) + v : v;
+      } else if (src_ok) {
         const int64_t i = src * h + c;
         float v = b[i];
         if (din.token) v = uint64_t(philox_w0(uint32_t(i), 4u, il, ih, seed_lo, seed_hi)) >= din.threshold ? v * din.scale : 0.0f;
@@ -308,15 +316,18 @@ __global__ __launch_bounds__(256) void k_ln_fused(const float* __restrict__ a, c
 void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_token, uint64_t din_threshold,
               float din_scale, const float* gamma, const float* beta, float* s_out, float* y_out, float* stats,
               const int32_t* dout_token, uint64_t dout_threshold, float dout_scale, float* yd_out, int64_t rows,
-              int64_t h, uint64_t seed, const int32_t* gather, int64_t src_rows) {
+              int64_t h, uint64_t seed, const int32_t* gather, int64_t src_rows, const int32_t* a_ids, int64_t a_rows,
+              const int32_t* b_ids, int64_t b_rows) {
   if (rows <= 0 || h <= 0) return;
   if (!gather) src_rows = rows;
+  if ((a_ids || b_ids) && (gather || din_token)) bad("fused LayerNorm: gathered operands with a row gather or an input dropout");
   if (h > 1024) bad("fused LayerNorm rows wider than 1024");
   if (rows * h > (int64_t(1) << 32)) bad("fused LayerNorm over more than 2^32 elements");
   const DropoutSpec din{din_token, din_threshold, din_scale}, dout{dout_token, dout_threshold, dout_scale};
   const int cpl = int((h + 63) / 64);
 #define MSX_LNF(C) MSX_LAUNCH(k_ln_fused<C>, dim3(blocks_for(rows, 4)), dim3(256), 0, s, a, b, din, gamma, beta, s_out, y_out, \
-                              stats, dout, yd_out, rows, h, uint32_t(seed), uint32_t(seed >> 32), gather, src_rows)
+                              stats, dout, yd_out, rows, h, uint32_t(seed), uint32_t(seed >> 32), gather, src_rows, \
+                              RowGather{a_ids, a_rows}, RowGather{b_ids, b_rows})
   if (cpl <= 1) MSX_LNF(1);
   else if (cpl <= 2) MSX_LNF(2);
   else if (cpl <= 4) MSX_LNF(4);
@@ -779,7 +790,7 @@ void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, in
 __global__ __launch_bounds__(256) void k_ce_loss(const float* __restrict__ x, const int32_t* __restrict__ labels,
                                                  const float* __restrict__ w, const float* __restrict__ stats,
                                                  float* __restrict__ loss, float* __restrict__ den_out, int64_t rows,
-                                                 int64_t v, int64_t ld, const float* __restrict__ rowloss) {
+                                                 int64_t v, int64_t ld, const float* __restrict__ rowloss, LossLog log) {
   __shared__ double num_s[256], den_s[256];
   double num = 0.0, den = 0.0;
   for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) {
@@ -806,13 +817,19 @@ __global__ __launch_bounds__(256) void k_ce_loss(const float* __restrict__ x, co
   }
   if (threadIdx.x == 0) {
     double n = num_s[0], d = den_s[0];
-    loss[0] = d == 0.0 ? 0.0f : float(n / d);
+    const float l = d == 0.0 ? 0.0f : float(n / d);
+    loss[0] = l;
     if (den_out) den_out[0] = float(d);
+    if (log.losses) {  // k_record_loss's append
+      const uint32_t c = log.counter[0];
+      if (c < log.capacity) log.losses[c] = l;
+      log.counter[0] = c + 1;
+    }
   }
 }
 void ce_loss(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats, float* loss,
-             float* den, int64_t rows, int64_t v, int64_t ld, const float* rowloss) {
-  MSX_LAUNCH(k_ce_loss, dim3(1), dim3(256), 0, s, logits, labels, w, stats, loss, den, rows, v, ld, rowloss);
+             float* den, int64_t rows, int64_t v, int64_t ld, const float* rowloss, LossLog log) {
+  MSX_LAUNCH(k_ce_loss, dim3(1), dim3(256), 0, s, logits, labels, w, stats, loss, den, rows, v, ld, rowloss, log);
 }
 
 __global__ void k_ce_grad(const float* __restrict__ x, const int32_t* __restrict__ labels, const float* __restrict__ w,

@@ -317,7 +317,7 @@ void Executor::build() {
   // A LayerNorm with its neighbours in one pass: its input X = Add(A, B) (B possibly a Dropout read
   // only there, not materialized) written beside the normalized value, and a Dropout that is the
   // LayerNorm output's only reader applied on the way out (the output then not materialized).
-  struct LnFused { int64_t add = -1, a = -1, b = -1, din = -1, dout = -1, gather = -1; };
+  struct LnFused { int64_t add = -1, a = -1, b = -1, din = -1, dout = -1, gather = -1, ea = -1, eb = -1; };
   std::map<uint32_t, LnFused> ln_fused;  // LayerNorm -> parts
   std::set<uint32_t> ln_fused_nodes;     // the Add and Dropouts a fused LayerNorm writes or applies
   std::set<uint32_t> ln_skip_storage;    // values of those never materialized
@@ -363,6 +363,19 @@ void Executor::build() {
         }
       }
     }
+    // Add(Embedding(T, ids), Embedding(U, ids2)) summed by this pass: the pass gathers the table
+    // rows itself and the Embedding outputs, read only by the Add, are never formed.
+    if (f.add >= 0 && f.din < 0 && f.gather < 0) {
+      for (int side = 0; side < 2; ++side) {
+        const uint32_t e = uint32_t(side == 0 ? f.a : f.b);
+        const Node& en = p.node(e);
+        if (en.op != Op::Embedding || consumers[p.pos.at(e)].size() != 1 || outputs.count(e) || f.a == f.b) continue;
+        const Node& tn = p.node(en.operands[0]);
+        if (tn.ty.rank() != 2 || tn.ty.shape[1] != y.ty.shape[1] || p.node(en.operands[1]).ty.count() != y.ty.shape[0])
+          continue;
+        (side == 0 ? f.ea : f.eb) = e;
+      }
+    }
     if (consumers[k].size() == 1 && !outputs.count(y.id)) {
       const Node& d = p.nodes[consumers[k][0]];
       if (d.op == Op::Dropout && d.operands[0] == y.id) f.dout = d.id;
@@ -370,8 +383,10 @@ void Executor::build() {
     if (f.gather >= 0 && f.add < 0) f.gather = -1;
     if (f.add < 0 && f.dout < 0) continue;
     ln_fused[y.id] = f;
-    for (auto v : {f.add, f.din, f.dout, f.gather})
+    for (auto v : {f.add, f.din, f.dout, f.gather, f.ea, f.eb})
       if (v >= 0) ln_fused_nodes.insert(uint32_t(v));
+    for (auto v : {f.ea, f.eb})
+      if (v >= 0) ln_skip_storage.insert(uint32_t(v));
     if (f.din >= 0) ln_skip_storage.insert(uint32_t(f.din));
     if (f.gather >= 0) ln_skip_storage.insert(uint32_t(f.add));  // only the gathered rows are formed
     if (f.dout >= 0) ln_skip_storage.insert(y.id);
@@ -899,6 +914,20 @@ void Executor::build() {
     }
   }
 
+  // A step's loss formed by a cross-entropy loss launch is appended to the loss log by that launch,
+  // in place of a RecordLoss launch after the optimizer (the value is the same: nothing between
+  // writes it).
+  bool loss_logged = false;
+  auto logs_loss = [&](uint32_t v, std::string& what) {
+    if (!is_step_ || v != st.loss || loss_logged) return false;
+    loss_logged = true;
+    what += " +RecordLoss";
+    return true;
+  };
+  auto loss_log = [this](bool rec) {
+    return rec ? hk::LossLog{s_.losses_dev_, s_.counter_, s_.loss_capacity_} : hk::LossLog{};
+  };
+
   for (size_t k = 0; k < n; ++k) {
     if (!need[k]) continue;
     const Node& x = p.nodes[k];
@@ -1202,7 +1231,6 @@ void Executor::build() {
           const auto si = spec(f.din), so = spec(f.dout);
           const int64_t tin = f.din >= 0 ? int64_t(p.node(uint32_t(f.din)).operands[size_t(token_operand(Op::Dropout))]) : -1;
           const int64_t tout = f.dout >= 0 ? int64_t(p.node(uint32_t(f.dout)).operands[size_t(token_operand(Op::Dropout))]) : -1;
-          const int64_t av = f.add >= 0 ? f.a : -1, bv = f.add >= 0 ? f.b : int64_t(xv);
           const int64_t s_val = f.gather >= 0 ? f.gather : f.add;  // the LayerNorm input as stored
           const int64_t gids = f.gather >= 0 ? int64_t(p.node(uint32_t(f.gather)).operands[1]) : -1;
           const int64_t src_rows = f.gather >= 0 ? shape(uint32_t(f.add))[0] : rows;
@@ -1210,10 +1238,28 @@ void Executor::build() {
             auto it = id_bounds_.find(p.node(uint32_t(gids)).name);
             id_bounds_[p.node(uint32_t(gids)).name] = it == id_bounds_.end() ? src_rows : std::min(it->second, src_rows);
           }
+          // An Embedding operand: its table, its ids and the table's rows.
+          struct Emb { int64_t table = -1, ids = -1, rows = 0; };
+          auto emb = [&](int64_t e) {
+            Emb r;
+            if (e < 0) return r;
+            r.table = p.node(uint32_t(e)).operands[0];
+            r.ids = p.node(uint32_t(e)).operands[1];
+            r.rows = shape(uint32_t(r.table))[0];
+            if (p.node(uint32_t(r.ids)).op == Op::Input) {
+              auto it = id_bounds_.find(p.node(uint32_t(r.ids)).name);
+              id_bounds_[p.node(uint32_t(r.ids)).name] = it == id_bounds_.end() ? r.rows : std::min(it->second, r.rows);
+            }
+            return r;
+          };
+          const Emb ea = emb(f.ea), eb = emb(f.eb);
+          const int64_t av = f.add >= 0 ? (ea.table >= 0 ? ea.table : f.a) : -1;
+          const int64_t bv = f.add >= 0 ? (eb.table >= 0 ? eb.table : f.b) : int64_t(xv);
           const int64_t yv = f.dout >= 0 ? -1 : int64_t(id);
           what = "LayerNorm+fused %" + std::to_string(id);
           for (auto [tag, v] : {std::pair<const char*, int64_t>{" add %", f.add}, {" dropout-in %", f.din},
-                                {" dropout-out %", f.dout}, {" gather %", f.gather}})
+                                {" dropout-out %", f.dout}, {" gather %", f.gather}, {" embedding %", f.ea},
+                                {" embedding %", f.eb}})
             if (v >= 0) what += tag + std::to_string(v);
           what += " " + type_string(x.ty);
           push([=](hipStream_t s) {
@@ -1221,7 +1267,8 @@ void Executor::build() {
             hk::ln_fused(s, fp(av), F(uint32_t(bv)), tin >= 0 ? I(uint32_t(tin)) : nullptr, si.first, si.second, F(gm), F(bt),
                          fp(s_val), fp(yv), write_stats ? static_cast<float*>(A(stats)) : nullptr,
                          tout >= 0 ? I(uint32_t(tout)) : nullptr, so.first, so.second, fp(f.dout), rows, h, seed,
-                         gids >= 0 ? I(uint32_t(gids)) : nullptr, src_rows);
+                         gids >= 0 ? I(uint32_t(gids)) : nullptr, src_rows, ea.ids >= 0 ? I(uint32_t(ea.ids)) : nullptr,
+                         ea.rows, eb.ids >= 0 ? I(uint32_t(eb.ids)) : nullptr, eb.rows);
           });
           bytes = 4.0 * double(count) * (2 + (av >= 0) + (f.add >= 0) + (yv >= 0) + (f.dout >= 0));
           break;
@@ -1392,9 +1439,11 @@ void Executor::build() {
             void* den = ce_den_tok.at(dkey);
             const uint32_t lid = uint32_t(hd.loss);
             what = "CrossEntropyLoss %" + std::to_string(hd.loss);
+            const bool rec = logs_loss(lid, what);
             push([=](hipStream_t s) {
+              const hk::LossLog log = loss_log(rec);
               hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(st2)), F(lid), static_cast<float*>(A(den)), rows, v,
-                          ld, static_cast<float*>(A(rl)));
+                          ld, static_cast<float*>(A(rl)), log);
             });
             bytes = 4.0 * double(2 * rows + 2);
           } else {
@@ -1436,9 +1485,11 @@ void Executor::build() {
               if (!ce_den_tok.count(dkey)) ce_den_tok[dkey] = R(4);
               void* den = ce_den_tok.at(dkey);
               const uint32_t lid = uint32_t(grp.loss);
+              const bool rec = logs_loss(lid, what);
               push([=](hipStream_t s) {
+                const hk::LossLog log = loss_log(rec);
                 hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(st2)), F(lid), static_cast<float*>(A(den)), rows,
-                            v, ld, static_cast<float*>(A(rl)));
+                            v, ld, static_cast<float*>(A(rl)), log);
               });
               bytes = 4.0 * double(2 * rows + 2);
             } else {
@@ -1461,8 +1512,11 @@ void Executor::build() {
         if (!have_den) ce_den_tok[dkey] = R(4);
         void* den = ce_den_tok[dkey];
         if (x.op == Op::CrossEntropy) {
+          const bool rec = logs_loss(id, what);
           push([=](hipStream_t s) {
-            hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(stats)), F(id), static_cast<float*>(A(den)), rows, v, ld);
+            const hk::LossLog log = loss_log(rec);
+            hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(stats)), F(id), static_cast<float*>(A(den)), rows, v, ld,
+                        nullptr, log);
           });
         } else {
           if (!have_den) {
@@ -1625,9 +1679,10 @@ void Executor::build() {
     }
     loss_value = st.loss;
     uint32_t loss = st.loss;
-    pending.push_back({[=] {
-      return Launch{"RecordLoss", [=](hipStream_t s) { hk::record_loss(s, F(loss), s_.losses_dev_, s_.counter_, s_.loss_capacity_); }};
-    }});
+    if (!loss_logged)
+      pending.push_back({[=] {
+        return Launch{"RecordLoss", [=](hipStream_t s) { hk::record_loss(s, F(loss), s_.losses_dev_, s_.counter_, s_.loss_capacity_); }};
+      }});
   } else {
     loss_value = p.outputs.at(0);
   }
