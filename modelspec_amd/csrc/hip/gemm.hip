@@ -18,7 +18,13 @@ constexpr int kSliceAlign = 32;  // split-K slices are multiples of this many K 
 // The output epilogue of element (row, col) of a product v: + bias[col], then the activation
 // (GELU or ReLU, the pre-activation value also stored to pre_out when asked; or their gradient
 // with respect to the pre-activation pre_in[row, col], v the incoming gradient), then addend[row,
-// col] + v. Every step rounds as the separate kernel would (the same operation order).
+// col] + v, then the dropout gradient (kept or zeroed by the dropout kernel's rule at the
+// element's index). Every step rounds as the separate kernel would (the same operation order).
+__device__ __forceinline__ float epi_drop(const GemmEpi& e, float v, int64_t at) {
+  const uint32_t w = philox_w0(uint32_t(at), 4u, uint32_t(e.drop_token[0]), uint32_t(e.drop_token[1]),
+                               uint32_t(e.drop_seed), uint32_t(e.drop_seed >> 32));
+  return uint64_t(w) >= e.drop_threshold ? v * e.drop_scale : 0.0f;
+}
 __device__ __forceinline__ float gemm_epilogue(const GemmEpi& e, float v, int64_t row, int64_t col, int64_t ldc) {
   if (e.bias) v = v + e.bias[col];
   const int64_t at = row * ldc + col;
@@ -30,6 +36,7 @@ __device__ __forceinline__ float gemm_epilogue(const GemmEpi& e, float v, int64_
     default: break;
   }
   if (e.addend) v = e.addend[at] + v;
+  if (e.drop_token) v = epi_drop(e, v, at);
   return v;
 }
 // The same on four consecutive columns (col a multiple of 4, 16-byte aligned rows).
@@ -64,6 +71,8 @@ __device__ __forceinline__ float4 gemm_epilogue4(const GemmEpi& e, float4 v, int
     const float4 a = *reinterpret_cast<const float4*>(e.addend + at);
     v = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
   }
+  if (e.drop_token)
+    v = make_float4(epi_drop(e, v.x, at), epi_drop(e, v.y, at + 1), epi_drop(e, v.z, at + 2), epi_drop(e, v.w, at + 3));
   return v;
 }
 
@@ -514,7 +523,7 @@ int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum, bool sum_a,
 int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs) {
   const int split = gemm_split_for(g.m, g.n, g.k, g.defer, g.h16, g.ce_operand != 0 || g.ce_part);
   if (split <= 1) return 0;
-  if (g.bias || g.addend || g.act || g.ldc != g.n) bad("deferred split-K needs a dense output without epilogue");
+  if (g.bias || g.addend || g.act || g.drop_token || g.ldc != g.n) bad("deferred split-K needs a dense output without epilogue");
   if (g.m * g.n > INT32_MAX) bad("deferred split-K output too large");
   jobs[0] = ColumnJob{g.workspace, g.c, nullptr, split, int32_t(g.m * g.n), int32_t(g.m * g.n), 0};
   if (!g.colsum) return 1;
@@ -537,7 +546,7 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
         o.tb != g.tb || o.sum_a != g.sum_a || o.defer != g.defer || o.pad_a != g.pad_a || o.pad_b != g.pad_b ||
         o.pad_c != g.pad_c || o.h16 != g.h16 || o.act != g.act || (o.colsum == nullptr) != (g.colsum == nullptr) ||
         (o.bias == nullptr) != (g.bias == nullptr) || (o.addend == nullptr) != (g.addend == nullptr) ||
-        (o.workspace == nullptr) != (g.workspace == nullptr))
+        (o.workspace == nullptr) != (g.workspace == nullptr) || (o.drop_token == nullptr) != (g.drop_token == nullptr))
       bad("gemm group of unlike problems");
   }
   const int ce = g.ce_part ? 3 : g.ce_operand;
@@ -562,7 +571,7 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
     ptrs.a[q] = o.a;
     ptrs.b[q] = o.b;
     ptrs.c[q] = o.c;
-    ptrs.epi[q] = GemmEpi{o.bias, o.addend, o.pre_in, o.pre_out, o.act};
+    ptrs.epi[q] = GemmEpi{o.bias, o.addend, o.pre_in, o.pre_out, o.act, o.drop_token, o.drop_threshold, o.drop_scale, o.drop_seed};
     ptrs.ws[q] = ws;
     ptrs.colsum[q] = o.colsum ? (ws ? ws + int64_t(split) * o.m * o.n : o.colsum) : nullptr;
     ptrs.ce_part[q] = o.ce_part;
@@ -580,7 +589,9 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
   const dim3 wgrid(unsigned((tiles * problems + 7) / 8 * 8));
   const int64_t width = g.sum_a ? g.m : g.n;
   if ((g.act == EPI_GELU_GRAD || g.act == EPI_RELU_GRAD) && !g.pre_in) bad("gemm activation gradient without its input");
-  const GemmEpi epi{g.bias, g.addend, g.pre_in, g.pre_out, g.act};
+  const GemmEpi epi{g.bias, g.addend, g.pre_in, g.pre_out, g.act, g.drop_token, g.drop_threshold, g.drop_scale, g.drop_seed};
+  if (g.drop_token && (g.ldc != g.n || g.m * g.n > (int64_t(1) << 32)))
+    bad("a GEMM's dropout epilogue needs a dense output of at most 2^32 elements");
   // float4 output groups: every row the epilogue touches 16-byte aligned (in every problem).
   auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   bool vo = true, va = true, vb = true;

@@ -55,6 +55,13 @@ struct GemmArgs {
   const float* pre_in;
   float* pre_out;
   int act;
+  // Then, with drop_token, the dropout gradient of the result: element (r, c) (index r ldc + c;
+  // ldc == n) kept when Philox word 0 of (index, drop_token, drop_seed) >= drop_threshold, then
+  // times drop_scale, else 0 (the dropout kernel's rule).
+  const int32_t* drop_token;
+  uint64_t drop_threshold;
+  float drop_scale;
+  uint64_t drop_seed;
   // Cross-entropy fused into a decoder head. ce_part (forward): each output row's (max, sum of
   // exp(v - max)) over each TN-column tile after the epilogue, [m][gemm_tile_n columns tiles] float2.
   // ce_operand 1 (A) or 2 (B): that operand is the loss gradient, formed from the logits it
@@ -65,7 +72,10 @@ struct GemmArgs {
   int64_t ce_cols;
 };
 enum GemmAct : int { EPI_NONE, EPI_GELU, EPI_RELU, EPI_GELU_GRAD, EPI_RELU_GRAD };
-struct GemmEpi { const float* bias; const float* addend; const float* pre_in; float* pre_out; int act; };
+struct GemmEpi {
+  const float* bias; const float* addend; const float* pre_in; float* pre_out; int act;
+  const int32_t* drop_token; uint64_t drop_threshold; float drop_scale; uint64_t drop_seed;
+};
 // The pointers of each problem of a GEMM group (problems of one shape and configuration, one
 // launch; block b works on problem b / tiles of the order).
 constexpr int kGemmGroupMax = 4;
@@ -135,7 +145,7 @@ void ln_backward(hipStream_t s, const float* x, const float* gamma, const float*
 
 // Sums of block partials [chunks, width] over the blocks, columns below `split` to out_lo and the
 // rest to out_hi; up to kColumnJobs reductions a launch (`first` is set by column_finalize).
-struct ColumnJob { const float* partial; float* out_lo; float* out_hi; int32_t chunks, width, split, first; };
+struct ColumnJob { const float* partial; float* out_lo; float* out_hi; int32_t chunks, width, split, first, parts; };
 constexpr int kColumnJobs = 48;
 struct ColumnJobs { ColumnJob job[kColumnJobs]; int32_t count; };
 void column_finalize(hipStream_t s, const ColumnJob* jobs, int count);
@@ -152,9 +162,12 @@ void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* ou
 constexpr int kEgJobs = 3;
 struct EgPlanJob { const int32_t* ids; int32_t* plan; int32_t n, rows, pos_bits, key_bits; };
 struct EgPlanSet { EgPlanJob job[kEgJobs]; int32_t count; };
+// With out2, the job also writes out2 = DropoutGrad(out) (dropout's rule: element i kept when
+// Philox word 0 of (i, drop_token, seed) >= drop_threshold, then times drop_scale, else 0).
 struct EgApplyJob {
   const int32_t* plan; const float* g; const float* addend; float* out;
   int32_t n, rows; int64_t h;
+  float* out2; const int32_t* drop_token; uint64_t drop_threshold; float drop_scale; uint64_t seed;
   int32_t vec, blocks_short, blocks_long, blocks;  // set by eg_apply
 };
 struct EgApplySet { EgApplyJob job[kEgJobs]; int32_t count; };

@@ -450,28 +450,46 @@ void ln_backward(hipStream_t s, const float* x, const float* gamma, const float*
 #undef MSX_LNB
 }
 
-// Column sums of block partials for several reductions in one launch: job j owns blocks
-// [first, first + ceil(width / 256)); a thread adds one column's partials in ascending block order,
-// 16 loads in flight, and writes it to out_lo[c] (c < split) or out_hi[c - split] (a null output
-// is skipped).
+// Column sums of block partials for several reductions in one launch. Job j owns blocks [first,
+// first + ceil(width / cols)), cols = 256 / parts: a block takes cols columns, and its `parts`
+// thread groups each add a contiguous share of a column's chunks in ascending order (8 loads in
+// flight); the shares' sums are then added in share order. The order is fixed, so the result does
+// not depend on timing. A job of many chunks (a LayerNorm's gamma and beta partials: few columns)
+// takes up to 8 parts so that no thread walks all of them; one of few chunks takes 1. The sum
+// goes to out_lo[c] (c < split) or out_hi[c - split] (a null output is skipped).
+int finalize_parts(int chunks) { return std::min(8, std::max(1, chunks / 16)); }
 __global__ __launch_bounds__(256) void k_column_finalize(ColumnJobs jobs) {
+  __shared__ float red[256];
   int j = 0;
   while (j + 1 < jobs.count && int(blockIdx.x) >= jobs.job[j + 1].first) ++j;
   const ColumnJob& J = jobs.job[j];
-  const int64_t c = int64_t(int(blockIdx.x) - J.first) * 256 + threadIdx.x;
-  if (c >= J.width) return;
+  const int parts = J.parts, cols = 256 / parts;
+  const int lc = threadIdx.x % cols, part = threadIdx.x / cols;
+  const int64_t c = int64_t(int(blockIdx.x) - J.first) * cols + lc;
+  const int per = (J.chunks + parts - 1) / parts;
+  const int z_beg = part * per, z_end = min(J.chunks, z_beg + per);
   float s = 0.0f;
-  for (int z0 = 0; z0 < J.chunks; z0 += 16) {
-    float t[16];
+  if (c < J.width) {
+    for (int z0 = z_beg; z0 < z_end; z0 += 8) {
+      float t[8];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int z = z0 + u < J.chunks ? z0 + u : J.chunks - 1;
-      t[u] = J.partial[int64_t(z) * J.width + c];
+      for (int u = 0; u < 8; ++u) {
+        const int z = z0 + u < z_end ? z0 + u : z_end - 1;
+        t[u] = J.partial[int64_t(z) * J.width + c];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (z0 + u < z_end) s = (z0 + u == z_beg) ? t[u] : s + t[u];
     }
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-      if (z0 + u < J.chunks) s += t[u];
   }
+  if (parts > 1) {
+    red[threadIdx.x] = s;
+    __syncthreads();
+    if (part != 0) return;
+    // Shares past the last chunk hold nothing and are not added.
+    for (int q = 1; q < parts && q * per < J.chunks; ++q) s += red[q * cols + lc];
+  }
+  if (c >= J.width) return;
   if (c < J.split) {
     if (J.out_lo) J.out_lo[c] = s;
   } else if (J.out_hi) {
@@ -487,7 +505,8 @@ void column_finalize(hipStream_t s, const ColumnJob* jobs, int count) {
       b.job[j] = jobs[base + j];
       if (b.job[j].chunks <= 0 || b.job[j].width <= 0) bad("column finalize job without partials");
       b.job[j].first = blocks;
-      blocks += int((b.job[j].width + 255) / 256);
+      b.job[j].parts = finalize_parts(b.job[j].chunks);
+      blocks += int((b.job[j].width + 256 / b.job[j].parts - 1) / (256 / b.job[j].parts));
     }
     MSX_LAUNCH(k_column_finalize, dim3(unsigned(blocks)), dim3(256), 0, s, b);
   }

@@ -270,9 +270,12 @@ void Executor::build() {
   // GEMM) that is read only by Add(X, value) with X computed earlier, or only as the incoming
   // gradient of GeluGrad/ReluGrad, is not materialized: the GEMM writes the consumer's value. A
   // Gelu/Relu of a GEMM's value is written by the GEMM beside the value itself.
-  struct Epi { uint32_t node; int act; int64_t aux; };  // consumer, hk::GemmAct, addend or pre-activation
+  // consumer, hk::GemmAct, addend or pre-activation; `drop`: a DropoutGrad of the Add consumer (its
+  // only reader) whose value the GEMM writes instead, the Add then not materialized.
+  struct Epi { uint32_t node; int act; int64_t aux; int64_t drop = -1; };
   std::map<uint32_t, Epi> gemm_epi;                     // GEMM value -> consumer it writes
   std::set<uint32_t> epi_nodes;                         // consumers written by their GEMM
+  std::set<uint32_t> epi_unstored;                      // epilogue values never materialized
   // Where a value is written: a fused writer's position when it runs before the value's own node.
   std::map<uint32_t, size_t> written_at;
   for (auto& [eg, add] : eg_add) written_at[add.first] = p.pos.at(eg);
@@ -293,6 +296,16 @@ void Executor::build() {
           gemm_epi[x.id] = {c.id, hk::EPI_NONE, int64_t(other)};
           epi_nodes.insert(c.id);
           written_at[c.id] = k;
+          const std::vector<size_t>& dc = consumers[cs[0]];
+          if (dc.size() == 1 && !outputs.count(c.id) && !grad_values_pre.count(c.id)) {
+            const Node& d = p.nodes[dc[0]];
+            if (d.op == Op::DropoutGrad && d.operands[1] == c.id && d.ty.count() == c.ty.count() && c.ty.rank() == 2) {
+              gemm_epi[x.id].drop = d.id;
+              epi_nodes.insert(d.id);
+              written_at[d.id] = k;
+              epi_unstored.insert(c.id);
+            }
+          }
           continue;
         }
       }
@@ -686,7 +699,7 @@ void Executor::build() {
       default:
         if (folded.count(x.id) || mm_fused.count(x.id) || mm_transposed.count(x.id) || eg_add.count(x.id)) break;
         if (gemm_epi.count(x.id) && gemm_epi.at(x.id).act != hk::EPI_GELU && gemm_epi.at(x.id).act != hk::EPI_RELU) break;
-        if (ln_skip_storage.count(x.id) || ce_head_grad.count(x.id)) break;
+        if (ln_skip_storage.count(x.id) || ce_head_grad.count(x.id) || epi_unstored.count(x.id)) break;
         token_[x.id] = arena_.reserve(size_t(pitch.count(x.id) ? x.ty.shape[0] * pitch.at(x.id) : x.ty.count()) * 4);
         break;
     }
@@ -737,6 +750,9 @@ void Executor::build() {
     void* ws = nullptr;
     void* ce_part = nullptr;  // a cross-entropy head: the forward's row partials
     void* ce_tab = nullptr;   // or the gradient entries of the operand formed from logits
+    uint32_t drop_tok = 0;    // the DropoutGrad epilogue's token, threshold and scale
+    uint64_t drop_thr = 0;
+    float drop_scale = 1.0f;
     std::string what;
   };
   struct Pending {
@@ -763,11 +779,11 @@ void Executor::build() {
   auto shape = [&](uint32_t v) -> const std::vector<int64_t>& { return p.node(v).ty.shape; };
   const uint64_t seed = s_.seed_;
   // The launch of one GEMM or a group of like GEMMs (one hk::gemm_group call).
-  auto gemm_launch = [this, F, A](std::vector<std::shared_ptr<GemmJob>> jobs) {
-    return [this, F, A, jobs]() {
+  auto gemm_launch = [this, F, A, I](std::vector<std::shared_ptr<GemmJob>> jobs) {
+    return [this, F, A, I, jobs]() {
       std::string what = jobs[0]->what;
       for (size_t q = 1; q < jobs.size(); ++q) what += " & %" + std::to_string(jobs[q]->id);
-      return Launch{what, [this, F, A, jobs](hipStream_t s) {
+      return Launch{what, [this, F, A, I, jobs](hipStream_t s) {
                       hk::GemmArgs list[hk::kGemmGroupMax];
                       for (size_t q = 0; q < jobs.size(); ++q) {
                         const GemmJob& j = *jobs[q];
@@ -784,6 +800,12 @@ void Executor::build() {
                         if (j.epi.node != j.id && j.epi.act == hk::EPI_NONE) a.addend = F(uint32_t(j.epi.aux));
                         if (j.epi.act == hk::EPI_GELU_GRAD || j.epi.act == hk::EPI_RELU_GRAD) a.pre_in = F(uint32_t(j.epi.aux));
                         if (j.epi.act == hk::EPI_GELU || j.epi.act == hk::EPI_RELU) a.pre_out = F(j.id);
+                        if (j.epi.drop >= 0) {
+                          a.drop_token = I(j.drop_tok);
+                          a.drop_threshold = j.drop_thr;
+                          a.drop_scale = j.drop_scale;
+                          a.drop_seed = s_.seed_;
+                        }
                         list[q] = a;
                       }
                       hk::gemm_group(s, list, int(jobs.size()));
@@ -850,6 +872,8 @@ void Executor::build() {
   std::map<uint32_t, void*> eg_plan_tok;  // EmbeddingGrad node -> plan buffer of its ids
   std::set<uint32_t> eg_deferred;                      // launched with a later EmbeddingGrad
   std::map<uint32_t, std::vector<uint32_t>> eg_group;  // last EmbeddingGrad -> every one it launches
+  std::map<uint32_t, uint32_t> eg_drop;                // EmbeddingGrad -> the DropoutGrad of it written beside
+  std::set<uint32_t> eg_drop_nodes;
   {
     std::map<std::pair<uint32_t, int64_t>, void*> by_ids;
     struct PlanJob { uint32_t ids; int64_t n, rows; void* tok; };
@@ -892,6 +916,16 @@ void Executor::build() {
       if (!ok) continue;
       for (size_t q = 0; q + 1 < group.size(); ++q) eg_deferred.insert(group[q]);
       eg_group[group.back()] = group;
+    }
+    // A DropoutGrad of such an EmbeddingGrad's own output is written by the same apply pass, beside
+    // it (the pass holds each element; the mask is the dropout's, by element index).
+    for (size_t k = 0; k < n; ++k) {
+      const Node& x = p.nodes[k];
+      if (!need[k] || x.op != Op::DropoutGrad || optimizer.count(x.id)) continue;
+      const uint32_t e = x.operands[1];
+      if (!eg_plan_tok.count(e) || eg_add.count(e) || eg_drop.count(e) || p.node(e).ty.count() != x.ty.count()) continue;
+      eg_drop[e] = x.id;
+      eg_drop_nodes.insert(x.id);
     }
     for (size_t q0 = 0; q0 < jobs.size(); q0 += hk::kEgJobs) {
       std::vector<PlanJob> part(jobs.begin() + q0, jobs.begin() + std::min(jobs.size(), q0 + hk::kEgJobs));
@@ -1013,8 +1047,9 @@ void Executor::build() {
         const bool swap = x.op == Op::MatMul && mm_transposed.count(id);
         // The value the GEMM writes: its own, the Transpose's (swapped), or an epilogue consumer's.
         const Epi epi = gemm_epi.count(id) ? gemm_epi.at(id) : Epi{id, hk::EPI_NONE, -1};
-        const uint32_t out_id = swap ? mm_transposed.at(id) : epi.node;
+        const uint32_t out_id = swap ? mm_transposed.at(id) : epi.drop >= 0 ? uint32_t(epi.drop) : epi.node;
         if (epi.node != id) what += " +" + std::string(op_name(p.node(epi.node).op)) + " %" + std::to_string(epi.node);
+        if (epi.drop >= 0) what += " +DropoutGrad %" + std::to_string(epi.drop);
         if (x.op == Op::AddRows && !fused) {
           uint32_t a = o[0], b = o[1];
           int64_t rows = x.ty.shape[0], h = x.ty.shape[1];
@@ -1081,6 +1116,12 @@ void Executor::build() {
         job->bias_id = bias_id;
         job->cs_id = cs_id;
         job->epi = epi;
+        if (epi.drop >= 0) {
+          const Node& d = p.node(uint32_t(epi.drop));
+          job->drop_tok = d.operands[size_t(token_operand(Op::DropoutGrad))];
+          job->drop_thr = dropout_threshold(d.scalar);
+          job->drop_scale = 1.0f / (1.0f - d.scalar);
+        }
         job->ws = ws;
         job->ce_part = ce_part;
         job->ce_tab = ce_tab;
@@ -1145,7 +1186,7 @@ void Executor::build() {
         }
         if (eg_deferred.count(id)) break;  // launched with a later EmbeddingGrad of the same gradient
         if (eg_plan_tok.count(id)) {
-          struct Job { void* plan; uint32_t g, out; int64_t addend, n, rows, h; };
+          struct Job { void* plan; uint32_t g, out; int64_t addend, n, rows, h, drop = -1, drop_tok = -1; uint64_t thr = 0; float scale = 1; };
           std::vector<Job> jobs;
           const std::vector<uint32_t> members = eg_group.count(id) ? eg_group.at(id) : std::vector<uint32_t>{id};
           what.clear();
@@ -1158,6 +1199,16 @@ void Executor::build() {
                             shape(e.operands[0])[0], e.rows, shape(e.operands[1])[1]});
             what += (what.empty() ? "" : " & ") + std::string(add ? "EmbeddingGrad+Add %" : "EmbeddingGrad %") +
                     std::to_string(m) + (add ? " %" + std::to_string(out) : "") + " " + type_string(e.ty);
+            if (eg_drop.count(m)) {
+              const Node& d = p.node(eg_drop.at(m));
+              Job& jb = jobs.back();
+              jb.drop = d.id;
+              jb.drop_tok = d.operands[size_t(token_operand(Op::DropoutGrad))];
+              jb.thr = dropout_threshold(d.scalar);
+              jb.scale = 1.0f / (1.0f - d.scalar);
+              what += " +DropoutGrad %" + std::to_string(d.id);
+              bytes += 4.0 * double(e.ty.count());
+            }
             const double cnt = double(e.ty.count());
             bytes += 4.0 * (double(shape(e.operands[0])[0]) * (1 + double(shape(e.operands[1])[1])) + cnt) +
                      (add ? 8.0 * cnt : 0.0);
@@ -1173,6 +1224,13 @@ void Executor::build() {
               j.n = int32_t(jobs[q].n);
               j.rows = int32_t(jobs[q].rows);
               j.h = jobs[q].h;
+              if (jobs[q].drop >= 0) {
+                j.out2 = F(uint32_t(jobs[q].drop));
+                j.drop_token = I(uint32_t(jobs[q].drop_tok));
+                j.drop_threshold = jobs[q].thr;
+                j.drop_scale = jobs[q].scale;
+                j.seed = seed;
+              }
               js[q] = j;
             }
             hk::eg_apply(s, js, int(jobs.size()));
@@ -1535,6 +1593,8 @@ void Executor::build() {
       }
       case Op::Dropout: case Op::DropoutGrad: {
         if (ln_fused_nodes.count(id) || ln_post_nodes.count(id)) break;  // applied by a fused LayerNorm pass
+        if (eg_drop_nodes.count(id)) break;  // written by its EmbeddingGrad's apply pass
+        if (epi_nodes.count(id)) break;      // written by its GEMM's epilogue
         uint32_t tok = o[size_t(token_operand(x.op))], a = o[x.op == Op::Dropout ? 0 : 1];
         uint64_t threshold = dropout_threshold(x.scalar);
         float scale = 1.0f / (1.0f - x.scalar);
@@ -1563,7 +1623,8 @@ void Executor::build() {
              a.pad_b == b.pad_b && a.pad_c == b.pad_c && a.h16 == b.h16 && x.epi.act == y.epi.act &&
              (x.bias_id >= 0) == (y.bias_id >= 0) && (x.cs_id >= 0) == (y.cs_id >= 0) &&
              (x.epi.node != x.id) == (y.epi.node != y.id) && (x.ws != nullptr) == (y.ws != nullptr) &&
-             (split == 1 || a.defer) && !x.ce_part && !x.ce_tab && !y.ce_part && !y.ce_tab;
+             (split == 1 || a.defer) && !x.ce_part && !x.ce_tab && !y.ce_part && !y.ce_tab && x.epi.drop < 0 &&
+             y.epi.drop < 0;
     };
     auto reads = [](const GemmJob& j) {
       std::vector<int64_t> r{int64_t(j.asrc), int64_t(j.bsrc), j.bias_id};

@@ -315,6 +315,22 @@ template <> struct Vec<4> {
   static __device__ __forceinline__ T add(T a, T b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
 };
 
+// out2 = DropoutGrad(out) for the V consecutive elements from `at` (their values v), when asked.
+template <int V>
+__device__ __forceinline__ void put_dropped(const EgApplyJob& j, int64_t at, const float* v) {
+  if (!j.out2) return;
+  const uint32_t tl = uint32_t(j.drop_token[0]), th = uint32_t(j.drop_token[1]);
+  float o[V];
+#pragma unroll
+  for (int u = 0; u < V; ++u) {
+    const uint32_t w = philox_w0(uint32_t(at + u), 4u, tl, th, uint32_t(j.seed), uint32_t(j.seed >> 32));
+    o[u] = uint64_t(w) >= j.drop_threshold ? v[u] * j.drop_scale : 0.0f;
+  }
+  if constexpr (V == 4) *reinterpret_cast<float4*>(j.out2 + at) = make_float4(o[0], o[1], o[2], o[3]);
+  else if constexpr (V == 2) *reinterpret_cast<float2*>(j.out2 + at) = make_float2(o[0], o[1]);
+  else j.out2[at] = o[0];
+}
+
 // A short segment: one wave; lane l takes columns c0 + l*V .. + V - 1 of each 64*V-column pass.
 template <int V>
 __device__ __forceinline__ void short_segment(const EgApplyJob& j, const int32_t* plan, const PlanLayout& L, int q,
@@ -353,6 +369,7 @@ __device__ __forceinline__ void short_segment(const EgApplyJob& j, const int32_t
       if (k < len) acc = W::add(acc, v[k]);
     if (j.addend) acc = W::add(*reinterpret_cast<const T*>(j.addend + id * h + c), acc);
     *reinterpret_cast<T*>(j.out + id * h + c) = acc;
+    put_dropped<V>(j, id * h + c, reinterpret_cast<const float*>(&acc));
   }
 }
 
@@ -466,7 +483,9 @@ __global__ __launch_bounds__(kApplyThreads) void k_eg_apply(EgApplySet set) {
     }
     if (tid < cw) {
       const int64_t at = id * h + c_lo + tid;
-      j.out[at] = j.addend ? j.addend[at] + acc : acc;
+      const float v = j.addend ? j.addend[at] + acc : acc;
+      j.out[at] = v;
+      put_dropped<1>(j, at, &v);
     }
     return;
   }
@@ -489,12 +508,15 @@ __global__ __launch_bounds__(kApplyThreads) void k_eg_apply(EgApplySet set) {
         v = make_float4(a.x + 0.0f, a.y + 0.0f, a.z + 0.0f, a.w + 0.0f);
       }
       o4[e] = v;
+      put_dropped<4>(j, z0 * h + 4 * e, reinterpret_cast<const float*>(&v));
     }
   } else {
     const int64_t cells = (z1 - z0) * h;
     for (int64_t e = tid; e < cells; e += kApplyThreads) {
       if ((m >> uint32_t(e / h)) & 1u) continue;
-      j.out[z0 * h + e] = j.addend ? j.addend[z0 * h + e] + 0.0f : 0.0f;
+      const float v = j.addend ? j.addend[z0 * h + e] + 0.0f : 0.0f;
+      j.out[z0 * h + e] = v;
+      put_dropped<1>(j, z0 * h + e, &v);
     }
   }
 }
@@ -507,6 +529,8 @@ void eg_apply(hipStream_t s, const EgApplyJob* jobs, int njobs) {
   for (int q = 0; q < njobs; ++q) {
     EgApplyJob j = jobs[q];
     if (!eg_sorted_fits(j.n, j.rows) || j.h <= 0) bad("eg_apply: shape outside the sorted-segment path");
+    if (j.out2 && (!j.drop_token || int64_t(j.rows) * j.h > (int64_t(1) << 32)))
+      bad("eg_apply: a dropout output needs its token and at most 2^32 elements");
     const int64_t groups = (j.h + kLongCols - 1) / kLongCols;
     j.vec = (j.h % 256 == 0) ? 4 : (j.h % 128 == 0) ? 2 : 1;
     j.blocks_short = int(blocks_for(std::min<int64_t>(j.n, j.rows), kApplyThreads / 64));
