@@ -9,8 +9,9 @@ place here too (no Transpose launch); every value a reference dispatch writes ha
 
 Where this backend plans differently, by design: the reference's one sgd_update kernel a parameter
 is one optimizer launch over the flat parameter arena; a RecordLoss launch appends the step's loss
-to the device loss log (the reference's loss slots, kernel.rs:1515); weight-gradient GEMMs that only
-the optimizer reads run on the side stream."""
+to the device loss log (the reference's loss slots, kernel.rs:1515; where a cross-entropy loss
+launch forms the loss, that launch appends it); weight-gradient GEMMs that only the optimizer reads
+run on the side stream."""
 import os
 
 import pytest
