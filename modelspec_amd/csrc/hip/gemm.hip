@@ -233,7 +233,8 @@ struct GemmOrder {
 // accumulation; K tiles of 32; everything else (split-K, epilogues, output) as in f32.
 // CE: 1 or 2, operand A or B is a cross-entropy gradient formed from its logits (ce_grad_of);
 // 3, the row partials of a cross-entropy over the output (ce_part).
-template <bool TA, bool TB, int WM, int WN, int WK, bool VA, bool VB, bool H = false, int CE = 0>
+// KS: the product is a sum of K segments (GemmPtrs::ksegs), read in place segment by segment.
+template <bool TA, bool TB, int WM, int WN, int WK, bool VA, bool VB, bool H = false, int CE = 0, bool KS = false>
 __global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_t N, int64_t K, int64_t lda,
                                                 int64_t ldb, int64_t ldc, int64_t kchunk, bool sum_a, bool vo,
                                                 GemmOrder order) {
@@ -291,11 +292,32 @@ __global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_
   auto ga = [&](int h) { return RA ? hk_group<TM, HA>(tid, h) : tid + 256 * h; };
   auto gb = [&](int h) { return RB ? hk_group<TN, HB>(tid, h) : tid + 256 * h; };
   const float4* __restrict__ ce_tab = CE == 1 || CE == 2 ? ptrs.ce_tab[q] : nullptr;
+  // K segments: the tiles are loaded in ascending k0, so the segment (its operands and K offset)
+  // advances when k0 reaches its end (kseg a multiple of WK; one segment: never).
+  const float* sa = A;
+  const float* sb = B;
+  int64_t s_lo = 0, s_hi = KS ? ptrs.kseg : INT64_MAX;
+  int sn = 0;
+  auto advance = [&](int64_t k0) {
+    if (KS && k0 >= s_hi) {
+      ++sn;
+      s_lo = s_hi;
+      s_hi += ptrs.kseg;
+      sa = ptrs.a[sn];
+      sb = ptrs.b[sn];
+    }
+  };
   auto load_a = [&](int64_t k0, int h) {
-    return wide_load<!TA, TM, WK, VA, CE == 1>(A, lda, M, kend, m0, k0, ga(h), ce_tab, ptrs.ce_cols);
+    if constexpr (KS)
+      return wide_load<!TA, TM, WK, VA, CE == 1>(sa, lda, M, kend - s_lo, m0, k0 - s_lo, ga(h), ce_tab, ptrs.ce_cols);
+    else
+      return wide_load<!TA, TM, WK, VA, CE == 1>(A, lda, M, kend, m0, k0, ga(h), ce_tab, ptrs.ce_cols);
   };
   auto load_b = [&](int64_t k0, int h) {
-    return wide_load<TB, TN, WK, VB, CE == 2>(B, ldb, N, kend, n0, k0, gb(h), ce_tab, ptrs.ce_cols);
+    if constexpr (KS)
+      return wide_load<TB, TN, WK, VB, CE == 2>(sb, ldb, N, kend - s_lo, n0, k0 - s_lo, gb(h), ce_tab, ptrs.ce_cols);
+    else
+      return wide_load<TB, TN, WK, VB, CE == 2>(B, ldb, N, kend, n0, k0, gb(h), ce_tab, ptrs.ce_cols);
   };
   float4 ra[HA], rb[HB];
 #pragma unroll
@@ -341,6 +363,7 @@ __global__ __launch_bounds__(256) void k_gemm_w(GemmPtrs ptrs, int64_t M, int64_
     }
     __syncthreads();
     if (k0 + WK < kend) {
+      if constexpr (KS) advance(k0 + WK);
 #pragma unroll
       for (int h = 0; h < HA; ++h)
         if (GA % 256 == 0 || tid + 256 * h < GA) ra[h] = load_a(k0 + WK, h);
@@ -554,6 +577,11 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
     bad("a cross-entropy head GEMM runs alone, and its forward without split-K");
   const SplitPlan plan = split_plan(g.m, g.n, g.k, g.defer, g.h16, ce != 0);
   const int split = plan.split;
+  const int ksegs = g.ksegs > 1 ? g.ksegs : 1;
+  if (ksegs > 1 && (count != 1 || ksegs > kGemmGroupMax || g.k % ksegs != 0 || (g.k / ksegs) % 32 != 0 || split != 1 ||
+                    g.colsum || ce))
+    bad("K segments need one problem, at most 4 segments of a multiple of 32 K, no split-K, column sums or "
+        "cross-entropy");
   const int64_t chunk = plan.chunk;
   if (split > 1 && count > 1 && !g.defer) bad("a gemm group sums split-K slices by deferral only");
   GemmPtrs ptrs{};
@@ -578,6 +606,13 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
     ptrs.ce_tab[q] = o.ce_tab;
   }
   ptrs.ce_cols = g.ce_cols;
+  ptrs.ksegs = ksegs;
+  ptrs.kseg = g.k / ksegs;
+  if (ksegs > 1)
+    for (int q = 0; q < ksegs; ++q) {
+      ptrs.a[q] = g.seg_a[q];
+      ptrs.b[q] = g.seg_b[q];
+    }
   float* ws = ptrs.ws[0];
   // Tiles in the grouped order: split slices outermost; within a slice the tiles that share the
   // larger operand's panel are adjacent (M tiles of one column when B is the larger, N tiles of
@@ -605,8 +640,12 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
     vo = vo && (ptrs.ws[q] ? (o.n % 4 == 0 && a16(ptrs.ws[q]))
                            : ((o.n % 4 == 0 || (o.pad_c && !o.act && !o.addend)) && o.ldc % 4 == 0 && a16(o.c) &&
                               a16(o.bias) && a16(o.addend) && a16(o.pre_in) && a16(o.pre_out)));
-    va = va && aligned(o.a, o.lda, o.pad_a ? o.lda : (o.ta ? o.m : o.k));
-    vb = vb && aligned(o.b, o.ldb, o.pad_b ? o.ldb : (o.tb ? o.k : o.n));
+    va = va && aligned(o.a, o.lda, o.pad_a ? o.lda : (o.ta ? o.m : o.k / ksegs));
+    vb = vb && aligned(o.b, o.ldb, o.pad_b ? o.ldb : (o.tb ? o.k / ksegs : o.n));
+  }
+  for (int q = 0; q < ksegs && ksegs > 1; ++q) {
+    va = va && aligned(ptrs.a[q], g.lda, g.pad_a ? g.lda : (g.ta ? g.m : g.k / ksegs));
+    vb = vb && aligned(ptrs.b[q], g.ldb, g.pad_b ? g.ldb : (g.tb ? g.k / ksegs : g.n));
   }
 #define MSX_WIDE_V(TA, TB, WM, WN, WK, VA, VB)                                                              \
   MSX_LAUNCH((k_gemm_w<TA, TB, WM, WN, WK, VA, VB>), wgrid, dim3(256), 0, s, ptrs, g.m, g.n, g.k, g.lda,     \
@@ -646,7 +685,21 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
   else if (g.ta && !g.tb) { MSX_CE_T(true, false, WM, WN, WK, H) } \
   else if (!g.ta && g.tb) { MSX_CE_T(false, true, WM, WN, WK, H) } \
   else { MSX_CE_T(true, true, WM, WN, WK, H) }
-  if (ce) {
+  // K segments: the f32 kernels with both operands float4.
+#define MSX_KS_V(TA, TB, WM, WN, WK)                                                                           \
+  MSX_LAUNCH((k_gemm_w<TA, TB, WM, WN, WK, true, true, false, 0, true>), wgrid, dim3(256), 0, s, ptrs, g.m, g.n, \
+             g.k, g.lda, g.ldb, g.ldc, chunk, g.sum_a, vo, order)
+#define MSX_KS_T(TA, TB)                                    \
+  if (plan.wm == 2) MSX_KS_V(TA, TB, 2, 2, 16);             \
+  else if (plan.wn == 2) MSX_KS_V(TA, TB, 1, 2, 16);        \
+  else MSX_KS_V(TA, TB, 1, 1, 32);
+  if (ksegs > 1) {
+    if (!va || !vb || g.h16) bad("K segments need aligned f32 operands");
+    if (!g.ta && !g.tb) { MSX_KS_T(false, false) }
+    else if (g.ta && !g.tb) { MSX_KS_T(true, false) }
+    else if (!g.ta && g.tb) { MSX_KS_T(false, true) }
+    else { MSX_KS_T(true, true) }
+  } else if (ce) {
     if (!va || !vb || (ce == 3 && !vo)) bad("a cross-entropy head GEMM needs aligned, padded operands");
     if (g.h16 && g.colsum) bad("the mixed-precision GEMM takes no column sums");
     if (g.h16) { MSX_CE(4, 4, 32, true) }
@@ -661,6 +714,8 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
   else if (g.ta && !g.tb) { MSX_WIDE_T(true, false) }
   else if (!g.ta && g.tb) { MSX_WIDE_T(false, true) }
   else { MSX_WIDE_T(true, true) }
+#undef MSX_KS_T
+#undef MSX_KS_V
 #undef MSX_CE
 #undef MSX_CE_T
 #undef MSX_CE_V

@@ -70,6 +70,12 @@ struct GemmArgs {
   const float4* ce_tab;
   int ce_operand;
   int64_t ce_cols;
+  // K segments: with ksegs > 1 the product is the sum over s < ksegs of seg_a[s] seg_b[s], each
+  // pair of the shape (m, k / ksegs, n) with a and b's transposes and leading dimensions, as one
+  // contraction over k (a chain of like GEMMs added into one value); a and b are ignored then.
+  int ksegs;
+  const float* seg_a[4];
+  const float* seg_b[4];
 };
 enum GemmAct : int { EPI_NONE, EPI_GELU, EPI_RELU, EPI_GELU_GRAD, EPI_RELU_GRAD };
 struct GemmEpi {
@@ -90,6 +96,10 @@ struct GemmPtrs {
   const float4* ce_tab[kGemmGroupMax];
   int64_t ce_cols;
   int count;
+  // K segments (GemmArgs::ksegs): one problem whose K tile at k0 reads a[k0 / kseg] and
+  // b[k0 / kseg] at K offset k0 mod kseg.
+  int ksegs;
+  int64_t kseg;
 };
 // The output tile width of a GEMM of this shape (the column tiles of ce_part).
 int64_t gemm_tile_n(int64_t m, int64_t n, int64_t k, bool defer = false, bool h16 = false);

@@ -753,6 +753,8 @@ void Executor::build() {
     uint32_t drop_tok = 0;    // the DropoutGrad epilogue's token, threshold and scale
     uint64_t drop_thr = 0;
     float drop_scale = 1.0f;
+    // Further K segments (A, B sources) of a chain of like GEMMs added into one value.
+    std::vector<std::pair<uint32_t, uint32_t>> segs;
     std::string what;
   };
   struct Pending {
@@ -797,6 +799,15 @@ void Executor::build() {
                         a.ce_tab = j.ce_tab ? static_cast<const float4*>(A(j.ce_tab)) : nullptr;
                         a.colsum = j.cs_id >= 0 ? F(uint32_t(j.cs_id)) : nullptr;
                         a.act = j.epi.act;
+                        if (!j.segs.empty()) {
+                          a.ksegs = int(1 + j.segs.size());
+                          a.seg_a[0] = a.a;
+                          a.seg_b[0] = a.b;
+                          for (size_t t = 0; t < j.segs.size(); ++t) {
+                            a.seg_a[t + 1] = F(j.segs[t].first);
+                            a.seg_b[t + 1] = F(j.segs[t].second);
+                          }
+                        }
                         if (j.epi.node != j.id && j.epi.act == hk::EPI_NONE) a.addend = F(uint32_t(j.epi.aux));
                         if (j.epi.act == hk::EPI_GELU_GRAD || j.epi.act == hk::EPI_RELU_GRAD) a.pre_in = F(uint32_t(j.epi.aux));
                         if (j.epi.act == hk::EPI_GELU || j.epi.act == hk::EPI_RELU) a.pre_out = F(j.id);
@@ -1608,6 +1619,69 @@ void Executor::build() {
       pending.back().bytes = bytes;
     }
   }
+  // GEMM chains: Add(..Add(Add(X, A1 B1), A2 B2).., An Bn), each product a GEMM of one shape and
+  // configuration whose sum only the next Add reads, is one GEMM over the concatenated K (the
+  // K tiles of segment s read As and Bs in place) with X added in its epilogue, at the last
+  // GEMM's place. The sum is one contraction instead of n rounded partial products: within the
+  // per-kernel tolerance of the reference's order, not bit-identical to it. (The backward of the
+  // Q, K and V projections: the three input gradients added into the residual gradient.)
+  {
+    auto chainable = [&](const GemmJob& j) {
+      return j.epi.node != j.id && j.epi.act == hk::EPI_NONE && j.bias_id < 0 && j.cs_id < 0 && !j.ws &&
+             !j.ce_part && !j.ce_tab && j.segs.empty() && !j.g.defer && !j.g.h16 && j.g.k % 32 == 0 &&
+             hk::gemm_split_for(j.g.m, j.g.n, j.g.k, false, j.g.h16) == 1;
+    };
+    auto same = [](const hk::GemmArgs& a, const hk::GemmArgs& b) {
+      return a.m == b.m && a.n == b.n && a.k == b.k && a.lda == b.lda && a.ldb == b.ldb && a.ldc == b.ldc &&
+             a.ta == b.ta && a.tb == b.tb && a.pad_a == b.pad_a && a.pad_b == b.pad_b && a.pad_c == b.pad_c &&
+             a.h16 == b.h16;
+    };
+    std::vector<bool> gone(pending.size(), false);
+    for (size_t i = 0; i < pending.size(); ++i) {
+      if (gone[i] || pending[i].gemm.size() != 1 || pending[i].side) continue;
+      const GemmJob& head = *pending[i].gemm[0];
+      if (!chainable(head) || head.epi.drop >= 0) continue;
+      std::vector<size_t> chain{i};
+      while (chain.size() < size_t(hk::kGemmGroupMax)) {
+        const GemmJob& cur = *pending[chain.back()].gemm[0];
+        if (cur.epi.drop >= 0 || consumers[p.pos.at(cur.out_id)].size() != 1) break;
+        size_t nxt = SIZE_MAX;
+        for (size_t j = chain.back() + 1; j < pending.size() && nxt == SIZE_MAX; ++j)
+          if (!gone[j] && pending[j].gemm.size() == 1 && !pending[j].side && chainable(*pending[j].gemm[0]) &&
+              pending[j].gemm[0]->epi.aux == int64_t(cur.out_id) && same(pending[j].gemm[0]->g, head.g))
+            nxt = j;
+        if (nxt == SIZE_MAX) break;
+        chain.push_back(nxt);
+      }
+      if (chain.size() < 2) continue;
+      auto job = std::make_shared<GemmJob>(*pending[chain.back()].gemm[0]);
+      job->asrc = head.asrc;
+      job->bsrc = head.bsrc;
+      job->epi.aux = head.epi.aux;
+      job->g.k = head.g.k * int64_t(chain.size());
+      job->what = head.what;
+      Pending merged = pending[chain.back()];
+      merged.flop = 0;
+      merged.bytes = 0;
+      for (size_t c = 0; c < chain.size(); ++c) {
+        const GemmJob& m = *pending[chain[c]].gemm[0];
+        if (c > 0) {
+          job->segs.push_back({m.asrc, m.bsrc});
+          job->what += " (+) " + m.what.substr(m.what.find('%'));
+        }
+        merged.flop += pending[chain[c]].flop;
+        merged.bytes += pending[chain[c]].bytes;
+        if (c + 1 < chain.size()) gone[chain[c]] = true;
+      }
+      merged.gemm = {job};
+      merged.make = gemm_launch({job});
+      pending[chain.back()] = merged;
+    }
+    std::vector<Pending> kept;
+    for (size_t i = 0; i < pending.size(); ++i)
+      if (!gone[i]) kept.push_back(pending[i]);
+    pending = std::move(kept);
+  }
   // GEMM groups: like GEMMs (one shape and configuration, split-K slices only by deferral) that
   // read nothing the others write run as one launch. Main-stream GEMMs group when adjacent in the
   // launch order (the group takes the first one's place: nothing runs between them). Side-stream
@@ -1624,7 +1698,7 @@ void Executor::build() {
              (x.bias_id >= 0) == (y.bias_id >= 0) && (x.cs_id >= 0) == (y.cs_id >= 0) &&
              (x.epi.node != x.id) == (y.epi.node != y.id) && (x.ws != nullptr) == (y.ws != nullptr) &&
              (split == 1 || a.defer) && !x.ce_part && !x.ce_tab && !y.ce_part && !y.ce_tab && x.epi.drop < 0 &&
-             y.epi.drop < 0;
+             y.epi.drop < 0 && x.segs.empty() && y.segs.empty();
     };
     auto reads = [](const GemmJob& j) {
       std::vector<int64_t> r{int64_t(j.asrc), int64_t(j.bsrc), j.bias_id};
