@@ -190,6 +190,47 @@ def test_gemm_epilogues(ctx, oracle, act, m, k, n):
     assert within(got[2], want[2], (np.abs(q) + np.abs(dy) @ aW.T).reshape(-1))[0]
 
 
+@pytest.mark.parametrize("m,k,n", [(4096, 128, 128), (37, 64, 40)])
+def test_gemm_chain_with_dropout_gradient(ctx, oracle, m, k, n):
+    """q + d1 W1^T + d2 W2^T + d3 W3^T (a chain of like GEMMs added into one value, run as one
+    GEMM over three K segments) followed by the DropoutGrad that is its only reader (applied in
+    the GEMM's epilogue): values within the per-kernel tolerance of the oracle, zeros exactly where
+    the mask drops."""
+    q = fast_values(91, m * n).reshape(m, n)
+    ds = [fast_values(92 + i, m * k).reshape(m, k) for i in range(3)]
+    Ws = [fast_values(95 + i, n * k, 0.1).reshape(n, k) for i in range(3)]
+    token = np.array([0x13579, -0x2468], np.int32)
+    p = Prog()
+    qi, ti = p.input("q", (m, n)), p.input("tok", (2,), "i32")
+    acc = qi
+    for i in range(3):
+        di, wi = p.input(f"d{i}", (m, k)), p.input(f"W{i}", (n, k))
+        acc = p.op("Add", [acc, p.op("MatMul", [di, p.op("Transpose", [wi], (k, n))], (m, n))], (m, n))
+    z = p.op("DropoutGrad", [ti, acc], (m, n), "[p = 0.1, site = tok]")
+    inputs = {"q": q, "tok": token, **{f"d{i}": ds[i] for i in range(3)}, **{f"W{i}": Ws[i] for i in range(3)}}
+    (g,), (w,) = both(ctx, oracle, p.out(z), inputs, (0,), seed=7)
+    r = np.abs(q).astype(np.float64) + sum(np.abs(d).astype(np.float64) @ np.abs(W).T.astype(np.float64) for d, W in zip(ds, Ws))
+    assert np.array_equal(g == 0, w == 0)
+    assert within(g, w, (r / 0.9).reshape(-1))[0]
+
+
+def test_embedding_gradient_with_its_dropout_gradient(ctx, oracle):
+    """EmbeddingGrad over step-input ids (the sorted-segment path) and a DropoutGrad of it written by
+    the same apply pass: both bit for bit."""
+    n, rows, h = 832, 4096, 128
+    ids = np.random.default_rng(5).integers(0, rows, n).astype(np.int32)
+    ids[700:] = 0  # padding slots all naming row 0: one long segment
+    G = fast_values(98, n * h).reshape(n, h)
+    token = np.array([0x2222, 0x7777], np.int32)
+    p = Prog()
+    ii, gi, ti = p.input("ids", (n,), "i32"), p.input("G", (n, h)), p.input("tok", (2,), "i32")
+    e = p.op("EmbeddingGrad", [ii, gi], (rows, h), "[%d]" % rows)
+    d = p.op("DropoutGrad", [ti, e], (rows, h), "[p = 0.1, site = tok]")
+    got, want = both(ctx, oracle, p.out(e, d), {"ids": ids, "G": G, "tok": token}, (0, 1), seed=3)
+    for g, w in zip(got, want):
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
+
+
 @pytest.mark.parametrize("rows,h", [(6, 8), (4096, 128), (832, 128), (33, 200), (100, 768)])
 def test_layer_norm_family(ctx, oracle, rows, h):
     x = fast_values(6, rows * h).reshape(rows, h)
