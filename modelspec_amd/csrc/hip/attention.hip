@@ -407,17 +407,17 @@ __global__ __launch_bounds__(64 * W) void k_attn_fwd_mfma(const float* __restric
   }
 }
 
-// dQ and d_i = rowsum(dO * O), per 16 query rows, streaming key and value tiles.
-template <int D, int T, int W, int KS = 1>
-__global__ __launch_bounds__(64 * W) void k_attn_bwd_q_mfma(const float* __restrict__ q, const float* __restrict__ k,
-                                                         const float* __restrict__ v, const float* __restrict__ mask,
-                                                         const float* __restrict__ o, const float* __restrict__ stats,
-                                                         const float* __restrict__ go, float* __restrict__ dq,
-                                                         float* __restrict__ dsum, int L, int S, int H, int heads,
-                                                         float scale) {
+// dQ and d_i = rowsum(dO * O), per 16 query rows, streaming key and value tiles; `by` is the
+// block's query-tile index (blockIdx.y of its own launch).
+template <int D, int T, int W, int KS>
+__device__ __forceinline__ void attn_bwd_q_body(const float* __restrict__ q, const float* __restrict__ k,
+                                                const float* __restrict__ v, const float* __restrict__ mask,
+                                                const float* __restrict__ o, const float* __restrict__ stats,
+                                                const float* __restrict__ go, float* __restrict__ dq,
+                                                float* __restrict__ dsum, int L, int S, int H, int heads, float scale,
+                                                int by, float* sm) {
   constexpr int DP = D + 4, U = T / 16 / KS;
   static_assert(T % (16 * KS) == 0, "a wave's share of a tile is whole 16-row tiles");
-  extern __shared__ float sm[];
   float* const Mb = sm;
   float* const Kb = sm + 2 * T;
   float* const Vb = Kb + T * DP;
@@ -425,7 +425,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_q_mfma(const float* __restr
   const int64_t kbase = int64_t(b) * S * H + head * D;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int half = wave % KS;  // KS waves share a query tile, each a share of every key tile
-  const int i0 = blockIdx.y * (16 * W / KS) + (wave / KS) * 16;
+  const int i0 = by * (16 * W / KS) + (wave / KS) * 16;
   const bool active = i0 < L;
   const int64_t row = (int64_t(b) * L + (active ? i0 : 0) + c) * H + head * D;
   // d_i for query i0 + c: lane group g sums columns [g D/4, (g + 1) D/4).
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_q_mfma(const float* __restr
   dd += __shfl_xor(dd, 16, 64);
   dd += __shfl_xor(dd, 32, 64);
   const int64_t srow = int64_t(blockIdx.x) * L + (active ? i0 : 0) + c;
-  if (active && g == 0 && half == 0) dsum[srow] = dd;
+  if (dsum && active && g == 0 && half == 0) dsum[srow] = dd;
   const float mx = stats[2 * srow], total = stats[2 * srow + 1];
   float qb[D / 4], gb[D / 4];
 #pragma unroll
@@ -522,19 +522,30 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_q_mfma(const float* __restr
     for (int ct = 0; ct < D / 16; ++ct) dq[orow + ct * 16 + c] = acc[ct][r] * scale;
   }
 }
+template <int D, int T, int W, int KS = 1>
+__global__ __launch_bounds__(64 * W) void k_attn_bwd_q_mfma(const float* __restrict__ q, const float* __restrict__ k,
+                                                         const float* __restrict__ v, const float* __restrict__ mask,
+                                                         const float* __restrict__ o, const float* __restrict__ stats,
+                                                         const float* __restrict__ go, float* __restrict__ dq,
+                                                         float* __restrict__ dsum, int L, int S, int H, int heads,
+                                                         float scale) {
+  extern __shared__ float sm[];
+  attn_bwd_q_body<D, T, W, KS>(q, k, v, mask, o, stats, go, dq, dsum, L, S, H, heads, scale, int(blockIdx.y), sm);
+}
 
 // dK and dV, per 16 key rows, streaming query and output-gradient tiles (with each query's
-// maximum, sum and d).
-template <int D, int T, int W, int KS = 1>
-__global__ __launch_bounds__(64 * W) void k_attn_bwd_kv_mfma(const float* __restrict__ q, const float* __restrict__ k,
-                                                          const float* __restrict__ v, const float* __restrict__ mask,
-                                                          const float* __restrict__ stats, const float* __restrict__ go,
-                                                          const float* __restrict__ dsum, float* __restrict__ dk,
-                                                          float* __restrict__ dv, int L, int S, int H, int heads,
-                                                          float scale) {
+// maximum, sum and d). d is read from dsum, or, when dsum is null, formed here from dO and O in
+// the dQ pass's order (so the two passes can run in one launch); `by` is the block's key-tile
+// index.
+template <int D, int T, int W, int KS>
+__device__ __forceinline__ void attn_bwd_kv_body(const float* __restrict__ q, const float* __restrict__ k,
+                                                 const float* __restrict__ v, const float* __restrict__ mask,
+                                                 const float* __restrict__ o, const float* __restrict__ stats,
+                                                 const float* __restrict__ go, const float* __restrict__ dsum,
+                                                 float* __restrict__ dk, float* __restrict__ dv, int L, int S, int H,
+                                                 int heads, float scale, int by, float* sm) {
   constexpr int DP = D + 4, U = T / 16 / KS;
   static_assert(T % (16 * KS) == 0, "a wave's share of a tile is whole 16-row tiles");
-  extern __shared__ float sm[];
   float* const Sb = sm;  // max, sum, d per query of the tile; buffer j at Sb + j 3 T
   float* const Qb = sm + 6 * T;
   float* const Gb = Qb + T * DP;
@@ -542,7 +553,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_kv_mfma(const float* __rest
   const int64_t qbase = int64_t(b) * L * H + head * D;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int half = wave % KS;  // KS waves share a key tile, each a share of every query tile
-  const int j0 = blockIdx.y * (16 * W / KS) + (wave / KS) * 16;
+  const int j0 = by * (16 * W / KS) + (wave / KS) * 16;
   const bool active = j0 < S;
   const int64_t krow = (int64_t(b) * S + (active ? j0 : 0) + c) * H + head * D;
   const bool live = mask[int64_t(b) * S + (active ? j0 : 0) + c] != 0.0f;
@@ -560,7 +571,22 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_kv_mfma(const float* __rest
       const int64_t at = sbase + l0 + (tid < n ? tid : n - 1);
       e[0] = stats[2 * at];
       e[1] = stats[2 * at + 1];
-      e[2] = dsum[at];
+      if (dsum) {
+        e[2] = dsum[at];
+      } else {
+        // d = rowsum(dO * O) as the dQ pass forms it: four sequential fma chains over a quarter
+        // of the columns each, then (p0 + p1) + (p2 + p3).
+        const int64_t qrow = qbase + int64_t(l0 + (tid < n ? tid : n - 1)) * H;
+        float pg[4];
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) {
+          float a = 0.0f;
+#pragma unroll
+          for (int t = 0; t < D / 4; ++t) a = __builtin_fmaf(go[qrow + gg * (D / 4) + t], o[qrow + gg * (D / 4) + t], a);
+          pg[gg] = a;
+        }
+        e[2] = (pg[0] + pg[1]) + (pg[2] + pg[3]);
+      }
     }
   };
   auto put_stats = [&](float* X, const float (&e)[3]) {
@@ -663,6 +689,35 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_kv_mfma(const float* __rest
       if (dk) dk[orow + ct * 16 + c] = keep ? dka[ct][r] * scale : 0.0f;
     }
   }
+}
+template <int D, int T, int W, int KS = 1>
+__global__ __launch_bounds__(64 * W) void k_attn_bwd_kv_mfma(const float* __restrict__ q, const float* __restrict__ k,
+                                                          const float* __restrict__ v, const float* __restrict__ mask,
+                                                          const float* __restrict__ stats, const float* __restrict__ go,
+                                                          const float* __restrict__ dsum, float* __restrict__ dk,
+                                                          float* __restrict__ dv, int L, int S, int H, int heads,
+                                                          float scale) {
+  extern __shared__ float sm[];
+  attn_bwd_kv_body<D, T, W, KS>(q, k, v, mask, nullptr, stats, go, dsum, dk, dv, L, S, H, heads, scale,
+                                int(blockIdx.y), sm);
+}
+// Both backward passes in one launch (self-attention, one plan for both): blocks with
+// blockIdx.y < qy take query tiles (dQ), the rest key tiles (dK, dV, forming each query's d
+// themselves), so that the two passes' blocks share the chip instead of each leaving most of it
+// idle in turn.
+template <int D, int T, int W, int KS = 1>
+__global__ __launch_bounds__(64 * W, 2) void k_attn_bwd_mfma(const float* __restrict__ q, const float* __restrict__ k,
+                                                       const float* __restrict__ v, const float* __restrict__ mask,
+                                                       const float* __restrict__ o, const float* __restrict__ stats,
+                                                       const float* __restrict__ go, float* __restrict__ dq,
+                                                       float* __restrict__ dk, float* __restrict__ dv, int L, int S,
+                                                       int H, int heads, float scale, int qy) {
+  extern __shared__ float sm[];
+  if (int(blockIdx.y) < qy)
+    attn_bwd_q_body<D, T, W, KS>(q, k, v, mask, o, stats, go, dq, nullptr, L, S, H, heads, scale, int(blockIdx.y), sm);
+  else
+    attn_bwd_kv_body<D, T, W, KS>(q, k, v, mask, o, stats, go, nullptr, dk, dv, L, S, H, heads, scale,
+                                  int(blockIdx.y) - qy, sm);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1120,6 +1175,15 @@ void launch_bwd_kv(hipStream_t s, dim3 grid, bool one, const float* q, const flo
   MSX_LAUNCH((k_attn_bwd_kv_mfma<D, T, W, KS>), grid, dim3(64 * W), lds, s, q, k, v, mask, stats, g, dsum, dk, dv, L,
              S, H, heads, scale);
 }
+template <int D, int T, int W, int KS>
+void launch_bwd(hipStream_t s, dim3 grid, unsigned qy, bool one, const float* q, const float* k, const float* v,
+                const float* mask, const float* o, const float* stats, const float* g, float* dq, float* dk, float* dv,
+                int L, int S, int H, int heads, float scale) {
+  const size_t lds =
+      size_t(std::max(stream_lds_floats(T, D, 1, one ? 1 : 2), stream_lds_floats(T, D, 3, one ? 1 : 2))) * 4;
+  MSX_LAUNCH((k_attn_bwd_mfma<D, T, W, KS>), grid, dim3(64 * W), lds, s, q, k, v, mask, o, stats, g, dq, dk, dv, L, S,
+             H, heads, scale, int(qy));
+}
 // Dispatch on a plan: the f16 kernels (never split) or the f32 ones.
 #define MSX_BY_PLAN(plan, h16, GO_H, GO_F)                 \
   if (h16) {                                               \
@@ -1187,6 +1251,20 @@ void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v
     if (!dq) refuse("the MFMA attention backward computes d_i in its dQ pass: dQ is required");
     const AttnPlan pq = attn_plan(B * heads, L, S, d, h16);
     dim3 gq(unsigned(B * heads), row_blocks(L, pq));
+    if (!h16 && dk && dv && L == S) {
+      // Self-attention in f32: one launch for both passes (the key pass plans as the query pass).
+      dim3 gb(unsigned(B * heads), 2 * row_blocks(L, pq));
+#define GO_H(T, W)
+#define GO_F(T, W, KS)                                                                                              \
+  launch_bwd<D, T, W, KS>(s, gb, row_blocks(L, pq), pq.one, q, k, v, mask, o, stats, g, dq, dk, dv, int(L), int(S), \
+                          int(H), int(heads), scale)
+#define GO(D_) { constexpr int D = D_; MSX_BY_PLAN(pq, false, GO_H, GO_F) }
+      MSX_BY_D(d, GO)
+#undef GO
+#undef GO_F
+#undef GO_H
+      return;
+    }
 #define GO_H(T, W) \
   launch_bwd_q_h<D, T, W>(s, gq, q, k, v, mask, o, stats, g, dq, dsum, int(L), int(S), int(H), int(heads), scale)
 #define GO_F(T, W, KS)                                                                                            \
@@ -1233,7 +1311,9 @@ void prepare_attention() {
       reinterpret_cast<const void*>(k_attn_bwd_kv_mfma<D, T, W>),   \
       reinterpret_cast<const void*>(k_attn_fwd_mfma<D, 128, 4, 2>), \
       reinterpret_cast<const void*>(k_attn_bwd_q_mfma<D, 128, 4, 2>), \
-      reinterpret_cast<const void*>(k_attn_bwd_kv_mfma<D, 128, 4, 2>)
+      reinterpret_cast<const void*>(k_attn_bwd_kv_mfma<D, 128, 4, 2>), \
+      reinterpret_cast<const void*>(k_attn_bwd_mfma<D, T, W>),      \
+      reinterpret_cast<const void*>(k_attn_bwd_mfma<D, 128, 4, 2>)
 #define MSX_ATTN_H(D, T, W)                                         \
   reinterpret_cast<const void*>(k_attn_fwd_h16<D, T, W>),           \
       reinterpret_cast<const void*>(k_attn_bwd_q_h16<D, T, W>),     \
