@@ -33,6 +33,10 @@ constexpr int kShortMax = 16;    // positions a short segment holds at most
 constexpr int kLongCols = 32;    // columns of one long-segment block
 constexpr int kLongRows = 256;   // positions a long-segment block stages a round (one a thread)
 constexpr int kTilePitch = 36;   // floats a staged row takes in LDS (32 + 4: float4 stores spread over banks)
+#ifndef MSX_EG_ADD_BATCH
+#define MSX_EG_ADD_BATCH 32
+#endif
+constexpr int kAddBatch = MSX_EG_ADD_BATCH;  // staged values a column reads ahead of its adds
 constexpr int kApplyThreads = 256;
 constexpr int kCountRows = 36864;
 constexpr int kMaxPositions = 8192;  // ids a table's EmbeddingGrad takes on this path  // rows an LDS histogram of u32 counts holds (144 KiB)
@@ -423,15 +427,16 @@ __global__ __launch_bounds__(kApplyThreads) void k_eg_apply(EgApplySet set) {
   const int32_t* plan = j.plan;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t h = j.h;
-  if (b < j.blocks_short) {
-    const int s = b * (kApplyThreads / 64) + wave;
+  // The long segments' blocks come first in the job's range: their order-keeping add chains are
+  // the longest work of the launch, so they start before the short segments and stripes.
+  if (b >= j.blocks_long && b < j.blocks_long + j.blocks_short) {
+    const int s = (b - j.blocks_long) * (kApplyThreads / 64) + wave;
     if (s >= plan[L.counts + 1]) return;
     if (j.vec == 4) short_segment<4>(j, plan, L, s, lane);
     else if (j.vec == 2) short_segment<2>(j, plan, L, s, lane);
     else short_segment<1>(j, plan, L, s, lane);
     return;
   }
-  b -= j.blocks_short;
   if (b < j.blocks_long) {
     const int groups = int((h + kLongCols - 1) / kLongCols);
     if (b >= plan[L.counts + 2] * groups) return;
@@ -471,12 +476,14 @@ __global__ __launch_bounds__(kApplyThreads) void k_eg_apply(EgApplySet set) {
       if (tid < cw) {
         const int cnt = min(kLongRows, len - r0);
         int rr = 0;
-        for (; rr + 8 <= cnt; rr += 8) {
-          float t[8];
+        // kAddBatch staged values read ahead of their adds: the adds are one dependent chain, and
+        // the reads' latency is paid once a batch.
+        for (; rr + kAddBatch <= cnt; rr += kAddBatch) {
+          float t[kAddBatch];
 #pragma unroll
-          for (int u = 0; u < 8; ++u) t[u] = tile[(rr + u) * kTilePitch + tid];
+          for (int u = 0; u < kAddBatch; ++u) t[u] = tile[(rr + u) * kTilePitch + tid];
 #pragma unroll
-          for (int u = 0; u < 8; ++u) acc = acc + t[u];
+          for (int u = 0; u < kAddBatch; ++u) acc = acc + t[u];
         }
         for (; rr < cnt; ++rr) acc = acc + tile[rr * kTilePitch + tid];
       }
@@ -489,7 +496,7 @@ __global__ __launch_bounds__(kApplyThreads) void k_eg_apply(EgApplySet set) {
     }
     return;
   }
-  b -= j.blocks_long;
+  b -= j.blocks_long + j.blocks_short;
   // A stripe of 32 rows: the rows no id names are +0, or the addend's row + 0 (-0 becomes +0 as
   // the reference's zero-initialised sum added to it would make it).
   const int64_t z0 = int64_t(b) * 32, z1 = std::min<int64_t>(j.rows, z0 + 32);
