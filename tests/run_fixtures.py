@@ -55,3 +55,8 @@ def check_run(got_losses, got_params, config, steps, lr, step_ir, key_biases):
     g = got_params[idx]
     bad = np.abs(g - val) > atol[idx] + RUN_RTOL * np.abs(val)
     assert not bad.any(), (config, int(bad.sum()), idx[bad][:5], g[bad][:5], val[bad][:5])
+    # The margins, for the record: the largest difference of each kind as a fraction of its bound.
+    loss_frac = float(np.max(np.abs(got_losses - want_l) / (RUN_ATOL + RUN_RTOL * np.abs(want_l))))
+    param_frac = float(np.max(np.abs(g - val) / (atol[idx] + RUN_RTOL * np.abs(val))))
+    print(f"{config} {steps} steps: worst loss {loss_frac:.3f}, worst parameter {param_frac:.3f} of the tolerance "
+          f"({len(idx)} parameter elements)", flush=True)
