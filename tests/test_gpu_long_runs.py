@@ -3,7 +3,9 @@ seed and inputs: the MLP classifier for 1,000 steps, the transformer block for 5
 for 1,000 ("Parity runs"). The oracle takes minutes to hours for them on one core, so
 its runs are fixtures (tests/golden/oracle_*_<config>_<steps>.*): every loss, and every parameter
 element (the MLP) or a seeded sample of at least 65,536 elements stratified over every tensor (the
-transformer block, BERT-tiny), is held to the reference's run tolerance (tests/run_fixtures.py)."""
+transformer block, BERT-tiny), is held to the reference's run tolerance, and every tensor of the
+transformer block and BERT-tiny to the reference's whole-run bound ||g - c|| <= 1e-4 ||c||
+(run_within, tests/common/mod.rs:469-485), estimated from the kept elements (tests/run_fixtures.py)."""
 import numpy as np
 import pytest
 
@@ -23,7 +25,14 @@ def test_full_run_tracks_the_oracle(ctx, config, steps, lr):
     step_ir, _ = api.compile_config(config, -1, steps)
     print(f"{config} {steps} steps", flush=True)
     got_l, got_p, _ = ctx.train_config(config, steps=steps)
-    run_fixtures.check_run(got_l, got_p, config, steps, lr, step_ir, key_biases(step_ir))
+    # The MLP classifier's two biases end 7x and 3.8x past the whole-tensor bound: trained on
+    # uniform random labels, their gradients are batch sums of terms that nearly cancel, so the
+    # differences the two summation orders leave are large next to their small norms (0.037 and
+    # 0.018, against 19.9 and 5.5 for the weights, which hold the bound at 0.37 and 0.24). Every
+    # element still holds the per-element run tolerance (worst 0.41 of it). The transformer block
+    # and BERT-tiny hold the whole-tensor bound on every tensor, at 0.014 of it or less.
+    run_fixtures.check_run(got_l, got_p, config, steps, lr, step_ir, key_biases(step_ir),
+                           l2_bound=config != "mlp_classifier")
     # The run trains: the last losses are below the first.
     want_l = run_fixtures.load(config, steps)[0]
     assert want_l[-10:].mean() < want_l[:10].mean()
