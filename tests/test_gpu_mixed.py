@@ -151,3 +151,16 @@ def test_the_bert_base_config_takes_two_steps(ctx):
     assert np.all(np.isfinite(losses)), losses
     assert abs(losses[0] - np.log(30522)) < 3.0, losses
     assert ctx.loss_scale() == (65536.0, 0)
+
+
+def test_the_bert_base_config_trains_for_its_whole_run(ctx):
+    """BERT-base mixed for the config's whole run (200 steps, AdamW with warm-up, dynamic loss
+    scale): every loss finite, the run learning (the last ten losses below the first ten), and at
+    most a few steps skipped for an overflow of the scaled gradients (the scale starts at 2^16)."""
+    steps = api.config_steps("bert_base")
+    print("bert_base", steps, flush=True)
+    losses, _, _ = ctx.train_config("bert_base")
+    assert len(losses) == steps + 1 and np.all(np.isfinite(losses)), losses
+    assert losses[-10:].mean() < losses[:10].mean(), (losses[:10], losses[-10:])
+    scale, skipped = ctx.loss_scale()
+    assert skipped <= 8 and scale >= 1.0, (scale, skipped)
