@@ -123,6 +123,12 @@ int msx_set_precision(msx_ctx* ctx, int32_t mixed, float loss_scale, uint32_t sc
  * reference: a plan choice of this backend (the reference's own fusion groups are fixed by its
  * planner, crates/modelspec-core/src/ir/kernel.rs:1407). */
 #define MSX_FUSE_CE_HEAD 1u
+/* MSX_FUSE_OPTIMIZER (on by default): without loss scaling, the batched finalize of the reductions
+ * only the optimizer reads (split-K weight gradients, LayerNorm gamma/beta sums) runs inside the
+ * AdamW launch, each finished gradient updated by the block that sums it; results are identical to
+ * the two launches'. A plan choice of this backend, no counterpart in the reference. */
+#define MSX_FUSE_OPTIMIZER 2u
+#define MSX_FUSE_DEFAULT MSX_FUSE_OPTIMIZER
 int msx_set_fusion(msx_ctx* ctx, uint32_t flags);
 /* The loaded step's current loss scale and the number of steps skipped for an overflow (1 and 0
  * without mixed precision). */

@@ -333,10 +333,11 @@ class Context:
                                             ctypes.byref(start)))
         return losses, params, start.value
 
-    def set_fusion(self, ce_head=False):
+    def set_fusion(self, ce_head=False, optimizer=True):
         """Optional fusions of the next load (msx_set_fusion): ce_head folds the cross-entropy into
-        its decoder head GEMMs."""
-        _check(lib().msx_set_fusion(self._h, 1 if ce_head else 0))
+        its decoder head GEMMs; optimizer (the default) runs the deferred column finalize inside
+        the AdamW launch."""
+        _check(lib().msx_set_fusion(self._h, (1 if ce_head else 0) | (2 if optimizer else 0)))
 
     def set_precision(self, mixed, loss_scale=65536.0, scale_window=2000):
         """The precision of the next load (and per-op program): f16 MFMA GEMMs with loss scaling."""

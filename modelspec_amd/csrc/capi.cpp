@@ -295,8 +295,9 @@ int msx_read_input(msx_ctx* ctx, int32_t program, const char* name, void* out, u
 
 int msx_set_fusion(msx_ctx* ctx, uint32_t flags) {
   return guarded([&] {
-    if (flags & ~uint32_t(MSX_FUSE_CE_HEAD)) return fail(MSX_E_INVALID, "unknown fusion flags");
+    if (flags & ~uint32_t(MSX_FUSE_CE_HEAD | MSX_FUSE_OPTIMIZER)) return fail(MSX_E_INVALID, "unknown fusion flags");
     ctx->options.fuse_ce_head = (flags & MSX_FUSE_CE_HEAD) != 0;
+    ctx->options.fuse_optimizer = (flags & MSX_FUSE_OPTIMIZER) != 0;
     return MSX_OK;
   });
 }

@@ -288,6 +288,12 @@ struct LossScaleState {
 void adamw(hipStream_t s, float* p, const float* g, float* m, float* v, int64_t n, AdamWConsts k, const float* lr_t,
            const float* c1, const float* c2, const LossScaleState* ls = nullptr);
 void sgd(hipStream_t s, float* p, const float* g, int64_t n, const float* lr, const LossScaleState* ls = nullptr);
+// column_finalize and adamw in one launch, for a step without loss scaling whose deferred
+// reductions are all gradients in the arena g[0, n): the blocks of the finalize jobs write each
+// finished gradient and update its parameter and moments at once; the other blocks run the
+// AdamW update over the rest of the arena. Results equal the two launches'.
+void finalize_adamw(hipStream_t s, const ColumnJob* jobs, int count, float* p, float* g, float* m, float* v, int64_t n,
+                    AdamWConsts k, const float* lr_t, const float* c1, const float* c2);
 void grad_check(hipStream_t s, const float* g, int64_t n, LossScaleState* ls);
 void loss_scale_update(hipStream_t s, LossScaleState* ls);
 

@@ -1393,6 +1393,162 @@ void adamw(hipStream_t s, float* p, const float* g, float* m, float* v, int64_t 
              k, lr_t, c1, c2, ls);
 }
 
+// The arena outside the finalize jobs' outputs: `segs` runs of whole 16-byte quads (first quad,
+// quads before it in the list), then up to kFaLoose single elements.
+constexpr int kFaSegs = 2 * kColumnJobs + 1;
+constexpr int kFaLoose = 64;
+struct FaRest {  // (32-bit indices: the launch's arguments stay under 4 KiB)
+  uint32_t quad0[kFaSegs], before[kFaSegs];
+  int64_t quads;
+  int32_t segs, loose;
+  uint32_t loose_at[kFaLoose];
+};
+__global__ __launch_bounds__(256) void k_finalize_adamw(ColumnJobs jobs, int fin_blocks, FaRest rest, float* __restrict__ p,
+                                                        float* __restrict__ g, float* __restrict__ m, float* __restrict__ v,
+                                                        AdamWConsts k, const float* __restrict__ lr_t,
+                                                        const float* __restrict__ c1, const float* __restrict__ c2) {
+  const float lr = lr_t[0], b1 = c1[0], b2 = c2[0];
+  if (int(blockIdx.x) < fin_blocks) {
+    // A finalize block (k_column_finalize's arithmetic), then the update of each finished element.
+    __shared__ float red[256];
+    int j = 0;
+    while (j + 1 < jobs.count && int(blockIdx.x) >= jobs.job[j + 1].first) ++j;
+    const ColumnJob& J = jobs.job[j];
+    const int parts = J.parts, cols = 256 / parts;
+    const int lc = threadIdx.x % cols, part = threadIdx.x / cols;
+    const int64_t c = int64_t(int(blockIdx.x) - J.first) * cols + lc;
+    const int per = (J.chunks + parts - 1) / parts;
+    const int z_beg = part * per, z_end = min(J.chunks, z_beg + per);
+    float sum = 0.0f;
+    if (c < J.width) {
+      for (int z0 = z_beg; z0 < z_end; z0 += 8) {
+        float t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int z = z0 + u < z_end ? z0 + u : z_end - 1;
+          t[u] = J.partial[int64_t(z) * J.width + c];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (z0 + u < z_end) sum = (z0 + u == z_beg) ? t[u] : sum + t[u];
+      }
+    }
+    if (parts > 1) {
+      red[threadIdx.x] = sum;
+      __syncthreads();
+      if (part != 0) return;
+      for (int q = 1; q < parts && q * per < J.chunks; ++q) sum += red[q * cols + lc];
+    }
+    if (c >= J.width) return;
+    float* const out = c < J.split ? (J.out_lo ? J.out_lo + c : nullptr) : (J.out_hi ? J.out_hi + (c - J.split) : nullptr);
+    if (!out) return;
+    *out = sum;
+    const int64_t i = out - g;
+    adamw_one(p[i], sum, m[i], v[i], k, lr, b1, b2);
+    return;
+  }
+  // The rest of the arena: quad t of the runs, then the loose elements.
+  const int64_t t = int64_t(int(blockIdx.x) - fin_blocks) * 256 + threadIdx.x;
+  if (t < rest.quads) {
+    int lo = 0, hi = rest.segs - 1;  // the last run starting at or before t
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) / 2;
+      if (int64_t(rest.before[mid]) <= t) lo = mid; else hi = mid - 1;
+    }
+    const int64_t q = int64_t(rest.quad0[lo]) + (t - int64_t(rest.before[lo]));
+    v4f* p4 = reinterpret_cast<v4f*>(p);
+    const v4f* g4 = reinterpret_cast<const v4f*>(g);
+    v4f* m4 = reinterpret_cast<v4f*>(m);
+    v4f* v4 = reinterpret_cast<v4f*>(v);
+    v4f pq = p4[q], gq = g4[q], mq = m4[q], vq = v4[q];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float pc = pq[c], mc = mq[c], vc = vq[c];
+      adamw_one(pc, gq[c], mc, vc, k, lr, b1, b2);
+      pq[c] = pc;
+      mq[c] = mc;
+      vq[c] = vc;
+    }
+    p4[q] = pq;
+    m4[q] = mq;
+    v4[q] = vq;
+  } else if (t - rest.quads < rest.loose) {
+    const int64_t i = int64_t(rest.loose_at[t - rest.quads]);
+    adamw_one(p[i], g[i], m[i], v[i], k, lr, b1, b2);
+  }
+}
+void finalize_adamw(hipStream_t s, const ColumnJob* jobs, int count, float* p, float* g, float* m, float* v, int64_t n,
+                    AdamWConsts k, const float* lr_t, const float* c1, const float* c2) {
+  if (n <= 0) return;
+  if (count <= 0 || count > kColumnJobs) bad("finalize_adamw takes 1 to 48 jobs");
+  if (n >= (int64_t(1) << 32)) bad("finalize_adamw: an arena of 2^32 elements or more");
+  for (const void* a : {static_cast<const void*>(p), static_cast<const void*>(g), static_cast<const void*>(m),
+                        static_cast<const void*>(v)})
+    if (reinterpret_cast<uintptr_t>(a) % 16) bad("AdamW arenas must be 16-byte aligned");
+  ColumnJobs b{};
+  int blocks = 0;
+  b.count = count;
+  // The jobs' outputs as element ranges of the arena.
+  std::vector<std::pair<int64_t, int64_t>> taken;
+  for (int j = 0; j < count; ++j) {
+    b.job[j] = jobs[j];
+    const ColumnJob& J = b.job[j];
+    if (J.chunks <= 0 || J.width <= 0) bad("column finalize job without partials");
+    b.job[j].first = blocks;
+    b.job[j].parts = finalize_parts(J.chunks);
+    blocks += int((J.width + 256 / b.job[j].parts - 1) / (256 / b.job[j].parts));
+    const std::pair<const float*, int64_t> outs[2] = {{J.out_lo, int64_t(std::min(J.split, J.width))},
+                                                      {J.out_hi, int64_t(J.width) - std::min(J.split, J.width)}};
+    for (auto [o, len] : outs) {
+      if (!o || len <= 0) continue;
+      const int64_t at = o - g;
+      if (o < g || at + len > n) bad("finalize_adamw: a job's output lies outside the gradient arena");
+      taken.push_back({at, at + len});
+    }
+  }
+  std::sort(taken.begin(), taken.end());
+  FaRest rest{};
+  auto add_free = [&](int64_t a, int64_t e) {  // [a, e) is updated by the AdamW blocks
+    if (a >= e) return;
+    const int64_t qa = (a + 3) / 4, qe = e / 4;
+    if (qa >= qe) {
+      for (int64_t i = a; i < e; ++i) {
+        if (rest.loose >= kFaLoose) bad("finalize_adamw: too many unaligned elements");
+        rest.loose_at[rest.loose++] = uint32_t(i);
+      }
+      return;
+    }
+    for (int64_t i = a; i < 4 * qa; ++i) {
+      if (rest.loose >= kFaLoose) bad("finalize_adamw: too many unaligned elements");
+      rest.loose_at[rest.loose++] = uint32_t(i);
+    }
+    for (int64_t i = 4 * qe; i < e; ++i) {
+      if (rest.loose >= kFaLoose) bad("finalize_adamw: too many unaligned elements");
+      rest.loose_at[rest.loose++] = uint32_t(i);
+    }
+    if (rest.segs >= kFaSegs) bad("finalize_adamw: too many runs");
+    rest.quad0[rest.segs] = uint32_t(qa);
+    rest.before[rest.segs] = uint32_t(rest.quads);
+    rest.quads += qe - qa;
+    ++rest.segs;
+  };
+  int64_t at = 0;
+  for (auto [a, e] : taken) {
+    if (a < at) bad("finalize_adamw: overlapping job outputs");
+    add_free(at, a);
+    at = e;
+  }
+  add_free(at, n);
+  if (rest.segs == 0) {  // (one empty run keeps the search well defined)
+    rest.segs = 1;
+    rest.quad0[0] = 0;
+    rest.before[0] = 0;
+  }
+  const int64_t rest_blocks = (rest.quads + rest.loose + 255) / 256;
+  MSX_LAUNCH(k_finalize_adamw, dim3(unsigned(blocks + rest_blocks)), dim3(256), 0, s, b, blocks, rest, p, g, m, v, k,
+             lr_t, c1, c2);
+}
+
 __global__ void k_sgd(float* __restrict__ p, const float* __restrict__ g, int64_t n, const float* __restrict__ lr,
                       const LossScaleState* __restrict__ ls) {
   if (ls && ls->overflow) return;

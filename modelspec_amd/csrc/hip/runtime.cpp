@@ -1762,19 +1762,33 @@ void Executor::build() {
   }
   const size_t join_at = pending.size();
   // The reductions only the optimizer reads (LayerNorm gamma and beta sums, split-K weight
-  // gradients and their bias sums), in one launch.
-  if (!deferred.empty()) {
+  // gradients and their bias sums), in one launch; in the AdamW launch itself when every one is a
+  // gradient held in the arena and no loss scaling sits between them (finalize_adamw).
+  bool fuse_finalize = s_.opt_.fuse_optimizer && is_step_ && !deferred.empty() && deferred.size() <= size_t(hk::kColumnJobs) &&
+                       st.rule == Rule::AdamW && !st.updates.empty() && !s_.scaler_;
+  if (fuse_finalize) {
+    std::set<uint32_t> in_arena;
+    for (auto& [param, g] : st.gradients)
+      if (fixed_.count(g) && fixed_.at(g) == static_cast<void*>(s_.grad_ + s_.offset_[param])) in_arena.insert(g);
+    for (auto& d : deferred)
+      for (int64_t o : {d.lo, d.hi})
+        if (o >= 0 && !in_arena.count(uint32_t(o))) fuse_finalize = false;
+  }
+  double finalize_bytes = 0;
+  for (auto& d : deferred) finalize_bytes += 4.0 * double(int64_t(d.chunks) * d.width + d.width);
+  auto finalize_jobs = [deferred, F, A] {
+    std::vector<hk::ColumnJob> jobs;
+    for (auto& d : deferred)
+      jobs.push_back({static_cast<float*>(A(d.tok)) + d.offset, d.lo >= 0 ? F(uint32_t(d.lo)) : nullptr,
+                      d.hi >= 0 ? F(uint32_t(d.hi)) : nullptr, d.chunks, d.width, d.split, 0});
+    return jobs;
+  };
+  if (!deferred.empty() && !fuse_finalize) {
     std::string what = "ColumnFinalize x" + std::to_string(deferred.size());
-    double bytes = 0;
-    for (auto& d : deferred) bytes += 4.0 * double(int64_t(d.chunks) * d.width + d.width);
-    pending.push_back({[this, what, deferred, F, A] {
-                         return Launch{what, [this, deferred, F, A](hipStream_t s) {
-                                         std::vector<hk::ColumnJob> jobs;
-                                         for (auto& d : deferred)
-                                           jobs.push_back({static_cast<float*>(A(d.tok)) + d.offset,
-                                                           d.lo >= 0 ? F(uint32_t(d.lo)) : nullptr,
-                                                           d.hi >= 0 ? F(uint32_t(d.hi)) : nullptr, d.chunks,
-                                                           d.width, d.split, 0});
+    const double bytes = finalize_bytes;
+    pending.push_back({[what, finalize_jobs] {
+                         return Launch{what, [finalize_jobs](hipStream_t s) {
+                                         const std::vector<hk::ColumnJob> jobs = finalize_jobs();
                                          hk::column_finalize(s, jobs.data(), int(jobs.size()));
                                        }};
                        },
@@ -1799,10 +1813,22 @@ void Executor::build() {
         pending.push_back({[=] { return Launch{"GradCheck", [=](hipStream_t s) { hk::grad_check(s, s_.grad_, nt, ls); }}; }});
         pending.back().bytes = 4.0 * double(nt);
       }
-      pending.push_back({[=] {
-        return Launch{"AdamW", [=](hipStream_t s) { hk::adamw(s, s_.param_, s_.grad_, s_.m_, s_.v_, nt, c, F(lr), F(c1), F(c2), ls); }};
-      }});
-      pending.back().bytes = 7.0 * 4.0 * double(nt);
+      if (fuse_finalize) {
+        const std::string what = "ColumnFinalize x" + std::to_string(deferred.size()) + " + AdamW";
+        pending.push_back({[=] {
+          return Launch{what, [=](hipStream_t s) {
+                          const std::vector<hk::ColumnJob> jobs = finalize_jobs();
+                          hk::finalize_adamw(s, jobs.data(), int(jobs.size()), s_.param_, s_.grad_, s_.m_, s_.v_, nt, c,
+                                             F(lr), F(c1), F(c2));
+                        }};
+        }});
+        pending.back().bytes = finalize_bytes + 7.0 * 4.0 * double(nt);
+      } else {
+        pending.push_back({[=] {
+          return Launch{"AdamW", [=](hipStream_t s) { hk::adamw(s, s_.param_, s_.grad_, s_.m_, s_.v_, nt, c, F(lr), F(c1), F(c2), ls); }};
+        }});
+        pending.back().bytes = 7.0 * 4.0 * double(nt);
+      }
       if (ls) pending.push_back({[=] { return Launch{"LossScale", [=](hipStream_t s) { hk::loss_scale_update(s, ls); }}; }});
     } else if (st.rule == Rule::Sgd && !st.updates.empty()) {
       uint32_t rate = p.node(st.updates.begin()->second).operands[1];

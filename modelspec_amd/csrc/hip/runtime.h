@@ -73,6 +73,7 @@ struct SessionOptions {
   uint32_t scale_window = 2000;
   // Cross-entropy fused into its decoder head GEMMs (Executor::build).
   bool fuse_ce_head = false;
+  bool fuse_optimizer = true;  // the deferred column finalize inside the AdamW launch
   // Plan only: the step and forward programs are planned (launches, fusions, buffer offsets) and
   // nothing touches a device; such a session can print its plans and cannot run.
   bool plan_only = false;

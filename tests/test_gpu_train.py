@@ -81,3 +81,19 @@ def test_full_size_steps_track_the_oracle(ctx, oracle, config, steps, lr):
     got = ctx.train_config(config, steps=steps)
     want = oracle.train(config, steps=steps)
     compare_runs(config, got, want, step_ir, steps, lr)
+
+
+@pytest.mark.parametrize("config", ["bert_micro", "transformer_block"])
+def test_finalize_inside_adamw_is_bit_identical_to_separate_launches(ctx, config):
+    """MSX_FUSE_OPTIMIZER (the default) sums the deferred reductions inside the AdamW launch; the
+    separate finalize and AdamW launches give the same bits in every loss and parameter."""
+    steps = 6
+    try:
+        ctx.set_fusion(optimizer=False)
+        apart = ctx.train_config(config, steps=steps)
+        ctx.set_fusion(optimizer=True)
+        fused = ctx.train_config(config, steps=steps)
+    finally:
+        ctx.set_fusion()
+    assert np.array_equal(apart[0], fused[0])
+    assert np.array_equal(apart[1], fused[1])
