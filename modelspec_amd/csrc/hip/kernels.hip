@@ -458,9 +458,10 @@ void ln_backward(hipStream_t s, const float* x, const float* gamma, const float*
 // thread groups each add a contiguous share of a column's chunks in ascending order (8 loads in
 // flight); the shares' sums are then added in share order. The order is fixed, so the result does
 // not depend on timing. A job of many chunks (a LayerNorm's gamma and beta partials: few columns)
-// takes up to 8 parts so that no thread walks all of them; one of few chunks takes 1. The sum
-// goes to out_lo[c] (c < split) or out_hi[c - split] (a null output is skipped).
-int finalize_parts(int chunks) { return std::min(8, std::max(1, chunks / 16)); }
+// takes up to 32 parts (a share of at least 32 chunks each) so that no thread walks all of them;
+// one of few chunks takes 1. The sum goes to out_lo[c] (c < split) or out_hi[c - split] (a null
+// output is skipped).
+int finalize_parts(int chunks) { return std::min(32, std::max(1, chunks / 32)); }
 __global__ __launch_bounds__(256) void k_column_finalize(ColumnJobs jobs) {
   __shared__ float red[256];
   int j = 0;
