@@ -292,8 +292,14 @@ void sgd(hipStream_t s, float* p, const float* g, int64_t n, const float* lr, co
 // reductions are all gradients in the arena g[0, n): the blocks of the finalize jobs write each
 // finished gradient and update its parameter and moments at once; the other blocks run the
 // AdamW update over the rest of the arena. Results equal the two launches'.
+// With `loss`, one more block of the launch does what ce_loss does with those arguments (a loss
+// nothing in the step reads before the optimizer, logged at the step's end).
+struct CeLossJob {
+  const float* logits; const int32_t* labels; const float* w; const float* stats; float* loss; float* den;
+  int64_t rows, v, ld; const float* rowloss; LossLog log;
+};
 void finalize_adamw(hipStream_t s, const ColumnJob* jobs, int count, float* p, float* g, float* m, float* v, int64_t n,
-                    AdamWConsts k, const float* lr_t, const float* c1, const float* c2);
+                    AdamWConsts k, const float* lr_t, const float* c1, const float* c2, const CeLossJob* loss = nullptr);
 void grad_check(hipStream_t s, const float* g, int64_t n, LossScaleState* ls);
 void loss_scale_update(hipStream_t s, LossScaleState* ls);
 

@@ -810,10 +810,11 @@ void ce_stats(hipStream_t s, const float* logits, float* stats, int64_t rows, in
   MSX_LAUNCH(k_ce_stats, dim3(unsigned(rows)), dim3(256), 0, s, logits, stats, v, ld);
 }
 
-__global__ __launch_bounds__(256) void k_ce_loss(const float* __restrict__ x, const int32_t* __restrict__ labels,
-                                                 const float* __restrict__ w, const float* __restrict__ stats,
-                                                 float* __restrict__ loss, float* __restrict__ den_out, int64_t rows,
-                                                 int64_t v, int64_t ld, const float* __restrict__ rowloss, LossLog log) {
+// The loss of one block of 256 threads (k_ce_loss, and the tail block of k_finalize_adamw).
+__device__ __forceinline__ void ce_loss_block(const float* __restrict__ x, const int32_t* __restrict__ labels,
+                                              const float* __restrict__ w, const float* __restrict__ stats,
+                                              float* __restrict__ loss, float* __restrict__ den_out, int64_t rows,
+                                              int64_t v, int64_t ld, const float* __restrict__ rowloss, LossLog log) {
   __shared__ double num_s[256], den_s[256];
   double num = 0.0, den = 0.0;
   for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) {
@@ -849,6 +850,12 @@ __global__ __launch_bounds__(256) void k_ce_loss(const float* __restrict__ x, co
       log.counter[0] = c + 1;
     }
   }
+}
+__global__ __launch_bounds__(256) void k_ce_loss(const float* __restrict__ x, const int32_t* __restrict__ labels,
+                                                 const float* __restrict__ w, const float* __restrict__ stats,
+                                                 float* __restrict__ loss, float* __restrict__ den_out, int64_t rows,
+                                                 int64_t v, int64_t ld, const float* __restrict__ rowloss, LossLog log) {
+  ce_loss_block(x, labels, w, stats, loss, den_out, rows, v, ld, rowloss, log);
 }
 void ce_loss(hipStream_t s, const float* logits, const int32_t* labels, const float* w, const float* stats, float* loss,
              float* den, int64_t rows, int64_t v, int64_t ld, const float* rowloss, LossLog log) {
@@ -1412,17 +1419,24 @@ struct FaRest {  // (32-bit indices: the launch's arguments stay under 4 KiB)
 __global__ __launch_bounds__(256) void k_finalize_adamw(ColumnJobs jobs, int fin_blocks, FaRest rest, float* __restrict__ p,
                                                         float* __restrict__ g, float* __restrict__ m, float* __restrict__ v,
                                                         AdamWConsts k, const float* __restrict__ lr_t,
-                                                        const float* __restrict__ c1, const float* __restrict__ c2) {
+                                                        const float* __restrict__ c1, const float* __restrict__ c2,
+                                                        CeLossJob tail, int has_tail) {
+  if (has_tail && blockIdx.x == 0) {
+    ce_loss_block(tail.logits, tail.labels, tail.w, tail.stats, tail.loss, tail.den, tail.rows, tail.v, tail.ld,
+                  tail.rowloss, tail.log);
+    return;
+  }
+  const int bid = int(blockIdx.x) - has_tail;
   const float lr = lr_t[0], b1 = c1[0], b2 = c2[0];
-  if (int(blockIdx.x) < fin_blocks) {
+  if (bid < fin_blocks) {
     // A finalize block (k_column_finalize's arithmetic), then the update of each finished element.
     __shared__ float red[256];
     int j = 0;
-    while (j + 1 < jobs.count && int(blockIdx.x) >= jobs.job[j + 1].first) ++j;
+    while (j + 1 < jobs.count && bid >= jobs.job[j + 1].first) ++j;
     const ColumnJob& J = jobs.job[j];
     const int parts = J.parts, cols = 256 / parts;
     const int lc = threadIdx.x % cols, part = threadIdx.x / cols;
-    const int64_t c = int64_t(int(blockIdx.x) - J.first) * cols + lc;
+    const int64_t c = int64_t(bid - J.first) * cols + lc;
     const int per = (J.chunks + parts - 1) / parts;
     const int z_beg = part * per, z_end = min(J.chunks, z_beg + per);
     float sum = 0.0f;
@@ -1454,7 +1468,7 @@ __global__ __launch_bounds__(256) void k_finalize_adamw(ColumnJobs jobs, int fin
     return;
   }
   // The rest of the arena: quad t of the runs, then the loose elements.
-  const int64_t t = int64_t(int(blockIdx.x) - fin_blocks) * 256 + threadIdx.x;
+  const int64_t t = int64_t(bid - fin_blocks) * 256 + threadIdx.x;
   if (t < rest.quads) {
     int lo = 0, hi = rest.segs - 1;  // the last run starting at or before t
     while (lo < hi) {
@@ -1484,7 +1498,7 @@ __global__ __launch_bounds__(256) void k_finalize_adamw(ColumnJobs jobs, int fin
   }
 }
 void finalize_adamw(hipStream_t s, const ColumnJob* jobs, int count, float* p, float* g, float* m, float* v, int64_t n,
-                    AdamWConsts k, const float* lr_t, const float* c1, const float* c2) {
+                    AdamWConsts k, const float* lr_t, const float* c1, const float* c2, const CeLossJob* loss) {
   if (n <= 0) return;
   if (count <= 0 || count > kColumnJobs) bad("finalize_adamw takes 1 to 48 jobs");
   if (n >= (int64_t(1) << 32)) bad("finalize_adamw: an arena of 2^32 elements or more");
@@ -1551,8 +1565,9 @@ void finalize_adamw(hipStream_t s, const ColumnJob* jobs, int count, float* p, f
     rest.before[0] = 0;
   }
   const int64_t rest_blocks = (rest.quads + rest.loose + 255) / 256;
-  MSX_LAUNCH(k_finalize_adamw, dim3(unsigned(blocks + rest_blocks)), dim3(256), 0, s, b, blocks, rest, p, g, m, v, k,
-             lr_t, c1, c2);
+  const int tail = loss ? 1 : 0;
+  MSX_LAUNCH(k_finalize_adamw, dim3(unsigned(tail + blocks + rest_blocks)), dim3(256), 0, s, b, blocks, rest, p, g, m, v,
+             k, lr_t, c1, c2, loss ? *loss : CeLossJob{}, tail);
 }
 
 __global__ void k_sgd(float* __restrict__ p, const float* __restrict__ g, int64_t n, const float* __restrict__ lr,

@@ -763,6 +763,9 @@ void Executor::build() {
     bool side = false;
     std::vector<std::shared_ptr<GemmJob>> gemm;  // the GEMM(s) this launch runs, for grouping
     bool pure = false;
+    // A loss launch that may instead run as a block of the optimizer launch (finalize_adamw): its
+    // arguments at run time.
+    std::function<hk::CeLossJob()> loss_tail;
   };
   std::vector<Pending> pending;
   std::map<uint32_t, void*> ln_stats_tok;             // LN input value -> stats [rows, 2]
@@ -1560,6 +1563,14 @@ void Executor::build() {
                 hk::ce_loss(s, F(lg), I(lab), F(w), static_cast<float*>(A(st2)), F(lid), static_cast<float*>(A(den)), rows,
                             v, ld, static_cast<float*>(A(rl)), log);
               });
+              // Nothing but the optimizer reads the loss, and the row pass forms its own weight sum:
+              // the loss may be summed by a block of the optimizer launch instead.
+              if (is_step_ && only_optimizer_reads(int64_t(lid)))
+                pending.back().loss_tail = [=] {
+                  return hk::CeLossJob{F(lg), I(lab), F(w), static_cast<float*>(A(st2)), F(lid),
+                                       static_cast<float*>(A(den)), rows, v, ld, static_cast<float*>(A(rl)),
+                                       loss_log(rec)};
+                };
               bytes = 4.0 * double(2 * rows + 2);
             } else {
               bytes = pending[rows_launch].bytes;
@@ -1760,7 +1771,6 @@ void Executor::build() {
     }
     pending = std::move(merged);
   }
-  const size_t join_at = pending.size();
   // The reductions only the optimizer reads (LayerNorm gamma and beta sums, split-K weight
   // gradients and their bias sums), in one launch; in the AdamW launch itself when every one is a
   // gradient held in the arena and no loss scaling sits between them (finalize_adamw).
@@ -1774,6 +1784,22 @@ void Executor::build() {
       for (int64_t o : {d.lo, d.hi})
         if (o >= 0 && !in_arena.count(uint32_t(o))) fuse_finalize = false;
   }
+  // The loss launch joins the optimizer launch as one more block.
+  std::function<hk::CeLossJob()> loss_tail;
+  std::string loss_what;
+  if (fuse_finalize) {
+    size_t tails = 0;
+    for (auto& pd : pending) tails += pd.loss_tail ? 1 : 0;
+    if (tails == 1)
+      for (size_t q = 0; q < pending.size(); ++q)
+        if (pending[q].loss_tail) {
+          loss_tail = pending[q].loss_tail;
+          loss_what = pending[q].make().what;
+          pending.erase(pending.begin() + std::ptrdiff_t(q));
+          break;
+        }
+  }
+  const size_t join_at = pending.size();
   double finalize_bytes = 0;
   for (auto& d : deferred) finalize_bytes += 4.0 * double(int64_t(d.chunks) * d.width + d.width);
   auto finalize_jobs = [deferred, F, A] {
@@ -1814,12 +1840,15 @@ void Executor::build() {
         pending.back().bytes = 4.0 * double(nt);
       }
       if (fuse_finalize) {
-        const std::string what = "ColumnFinalize x" + std::to_string(deferred.size()) + " + AdamW";
+        const std::string what =
+            "ColumnFinalize x" + std::to_string(deferred.size()) + " + AdamW" + (loss_tail ? " + " + loss_what : "");
         pending.push_back({[=] {
           return Launch{what, [=](hipStream_t s) {
                           const std::vector<hk::ColumnJob> jobs = finalize_jobs();
+                          hk::CeLossJob tail{};
+                          if (loss_tail) tail = loss_tail();
                           hk::finalize_adamw(s, jobs.data(), int(jobs.size()), s_.param_, s_.grad_, s_.m_, s_.v_, nt, c,
-                                             F(lr), F(c1), F(c2));
+                                             F(lr), F(c1), F(c2), loss_tail ? &tail : nullptr);
                         }};
         }});
         pending.back().bytes = finalize_bytes + 7.0 * 4.0 * double(nt);

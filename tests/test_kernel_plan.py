@@ -109,8 +109,9 @@ def test_bert_tiny_step_plan_takes_the_fused_paths():
     """The BERT-tiny step (the benchmark and the 1,000-step parity run) plans the fusions the GPU
     op tests check one by one: the Embedding gathers inside the LayerNorm pass, the masked-row
     scatter with its DropoutGrad, the Q/K/V input-gradient chains as K-segment GEMMs (one ending in
-    a DropoutGrad epilogue), the loss logged by the cross-entropy loss launch, and no Dropout,
-    DropoutGrad, Embedding or RecordLoss launch of its own."""
+    a DropoutGrad epilogue), the loss summed and logged by a block of the optimizer launch (with the
+    deferred column finalize), and no Dropout, DropoutGrad, Embedding, RecordLoss, loss or finalize
+    launch of its own."""
     step_ir, forward_ir = api.compile_config("bert_tiny")
     launches = kernel_ir.parse_plan(api.plan(step_ir, forward_ir))["step"]["launches"]
     whats = [l["what"] for l in launches]
@@ -118,5 +119,7 @@ def test_bert_tiny_step_plan_takes_the_fused_paths():
     assert any(w.startswith("EmbeddingGrad") and "+DropoutGrad %" in w for w in whats), whats
     chains = [w for w in whats if w.startswith("MatMul") and w.count(" (+) ") == 2]
     assert len(chains) == 2 and sum("+DropoutGrad %" in w for w in chains) == 1, chains
-    assert any("+RecordLoss" in w for w in whats), whats
-    assert not any(w.split()[0] in ("Dropout", "DropoutGrad", "Embedding", "RecordLoss") for w in whats), whats
+    assert any(w.startswith("ColumnFinalize") and "+ AdamW + CrossEntropyRows" in w and "+RecordLoss" in w
+               for w in whats), whats
+    assert not any(w.split()[0] in ("Dropout", "DropoutGrad", "Embedding", "RecordLoss", "AdamW") for w in whats), whats
+    assert sum(w.startswith("CrossEntropyRows") for w in whats) == 1, whats
