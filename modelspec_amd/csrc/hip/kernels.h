@@ -184,6 +184,10 @@ struct EgApplySet { EgApplyJob job[kEgJobs]; int32_t count; };
 bool eg_sorted_fits(int64_t n, int64_t rows);
 size_t eg_plan_bytes(int64_t n, int64_t rows);
 void eg_plan(hipStream_t s, const EgPlanJob* jobs, int njobs);
+// The same plan made on the host (ids in host memory, plan into host memory of eg_plan_bytes), for
+// ids the host stages: it travels to the device with the step's inputs. Segments by ascending id,
+// positions ascending within a segment; ids outside [0, rows) are left out, as eg_plan does.
+void eg_plan_host(const int32_t* ids, int32_t n, int32_t rows, int32_t* plan);
 void eg_apply(hipStream_t s, const EgApplyJob* jobs, int njobs);
 
 void dropout(hipStream_t s, const float* x, float* o, int64_t n, const int32_t* token, uint64_t seed,

@@ -735,7 +735,26 @@ void Executor::build() {
         slot.offset = input_bytes_;
         input_bytes_ += slot_bytes(slot.count);
       }
-    if (device_pass == 0) host_bytes_ = input_bytes_;
+    if (device_pass == 0) {
+      // The plans of EmbeddingGrads whose ids the host stages: made on the host beside the inputs
+      // (the ids are in host memory before the step), so the step holds no plan launch.
+      plan_slots_.clear();
+      for (size_t k = 0; k < n && is_step_; ++k) {
+        const Node& x = p.nodes[k];
+        if (!need[k] || x.op != Op::EmbeddingGrad || optimizer.count(x.id)) continue;
+        const Node& ids = p.node(x.operands[0]);
+        const int64_t nn = ids.ty.shape[0], rows = x.rows;
+        if (ids.op != Op::Input || ids.ty.dtype != DType::I32 || !hk::eg_sorted_fits(nn, rows)) continue;
+        bool host = false;
+        for (auto& slot : inputs_) host = host || (slot.id == ids.id && !slot.device);
+        bool have = false;
+        for (auto& ps : plan_slots_) have = have || (ps.ids == ids.id && ps.rows == rows);
+        if (!host || have) continue;
+        plan_slots_.push_back({ids.name, ids.id, int32_t(nn), int32_t(rows), input_bytes_});
+        input_bytes_ += slot_bytes(int64_t(hk::eg_plan_bytes(nn, rows) / 4));
+      }
+      host_bytes_ = input_bytes_;
+    }
   }
   input_token_ = arena_.reserve(std::max<size_t>(input_bytes_, 256));
 
@@ -900,8 +919,13 @@ void Executor::build() {
       if (p.node(ids).op != Op::Input || !hk::eg_sorted_fits(nn, rows)) continue;
       auto key = std::make_pair(ids, rows);
       if (!by_ids.count(key)) {
-        by_ids[key] = R(hk::eg_plan_bytes(nn, rows));
-        jobs.push_back({ids, nn, rows, by_ids[key]});
+        for (auto& ps : plan_slots_)
+          if (ps.ids == ids && ps.rows == rows)  // made by the host in the input block (a token there)
+            by_ids[key] = static_cast<char*>(input_token_) + ps.offset;
+        if (!by_ids.count(key)) {
+          by_ids[key] = R(hk::eg_plan_bytes(nn, rows));
+          jobs.push_back({ids, nn, rows, by_ids[key]});
+        }
       }
       eg_plan_tok[x.id] = by_ids[key];
     }
@@ -1980,6 +2004,11 @@ void Executor::stage(const Batch& batch) {
     if (!src && in.count > 0) throw IrError("missing input `" + in.name + "`");
     if (int64_t(have) != in.count) throw IrError("input `" + in.name + "` has " + std::to_string(have) + " elements, not " + std::to_string(in.count));
     std::memcpy(host + in.offset, src, size_t(in.count) * 4);
+  }
+  for (auto& ps : plan_slots_) {
+    auto it = batch.i32.find(ps.ids_name);
+    if (it == batch.i32.end() || int64_t(it->second.size()) != ps.n) throw IrError("missing input `" + ps.ids_name + "`");
+    hk::eg_plan_host(it->second.data(), ps.n, ps.rows, reinterpret_cast<int32_t*>(host + ps.offset));
   }
   if (host_bytes_) {
     hip_check(hipMemcpyAsync(arena_.at(input_token_), host, host_bytes_, hipMemcpyHostToDevice, s_.stream_), "hipMemcpyAsync (inputs)");

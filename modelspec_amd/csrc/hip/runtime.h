@@ -215,6 +215,9 @@ class Executor {
   // device: written on the device by the corpus prologue, never staged by the host.
   struct InputSlot { std::string name; DType dtype; int64_t count; size_t offset; uint32_t id; bool device; };
   std::vector<InputSlot> inputs_;
+  // EmbeddingGrad plans of host-staged ids, made by the host in the input block (eg_plan_host).
+  struct PlanSlot { std::string ids_name; uint32_t ids; int32_t n, rows; size_t offset; };
+  std::vector<PlanSlot> plan_slots_;
   size_t input_bytes_ = 0, host_bytes_ = 0, draw_offset_ = 0;
   void* input_token_ = nullptr;
   static constexpr int kRing = 4;

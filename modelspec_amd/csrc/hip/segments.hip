@@ -24,6 +24,7 @@
 #include <rocprim/block/block_scan.hpp>
 
 #include <algorithm>
+#include <vector>
 
 namespace msx::hk {
 
@@ -263,6 +264,37 @@ __global__ __launch_bounds__(kPlanThreads) void k_eg_plan(EgPlanSet set) {
     out[L.counts + 2] = n_long;
     out[L.counts + 3] = n_valid;
   }
+}
+
+void eg_plan_host(const int32_t* ids, int32_t n, int32_t rows, int32_t* out) {
+  if (!eg_sorted_fits(n, rows)) bad("eg_plan_host: ids or table too large for the plan");
+  const PlanLayout L(n, rows);
+  // Counting sort by id: counts, then each named row's first slot; positions enter ascending.
+  std::vector<int32_t> base(size_t(rows) + 1, 0);
+  for (int32_t i = 0; i < n; ++i)
+    if (ids[i] >= 0 && ids[i] < rows) ++base[size_t(ids[i]) + 1];
+  int32_t seg = 0, lng = 0;
+  const int32_t words = (rows + 31) / 32;
+  for (int32_t w = 0; w < words; ++w) out[L.covered + w] = 0;
+  for (int32_t r = 0; r < rows; ++r) {
+    const int32_t c = base[size_t(r) + 1];
+    base[size_t(r) + 1] = base[size_t(r)] + c;
+    if (c) {
+      out[L.seg_start + seg] = base[size_t(r)];
+      out[L.seg_id + seg] = r;
+      out[L.covered + (r >> 5)] |= int32_t(1u << (r & 31));
+      if (c > kShortMax) out[L.longs + lng++] = seg;
+      ++seg;
+    }
+  }
+  const int32_t all_pos = base[size_t(rows)];
+  out[L.seg_start + seg] = all_pos;
+  for (int32_t i = 0; i < n; ++i)
+    if (ids[i] >= 0 && ids[i] < rows) out[L.order + base[size_t(ids[i])]++] = i;
+  out[L.counts + 0] = seg;
+  out[L.counts + 1] = seg;  // the short region walks every segment and skips the long ones
+  out[L.counts + 2] = lng;
+  out[L.counts + 3] = all_pos;
 }
 
 void eg_plan(hipStream_t s, const EgPlanJob* jobs, int njobs) {

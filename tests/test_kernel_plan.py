@@ -110,8 +110,8 @@ def test_bert_tiny_step_plan_takes_the_fused_paths():
     op tests check one by one: the Embedding gathers inside the LayerNorm pass, the masked-row
     scatter with its DropoutGrad, the Q/K/V input-gradient chains as K-segment GEMMs (one ending in
     a DropoutGrad epilogue), the loss summed and logged by a block of the optimizer launch (with the
-    deferred column finalize), and no Dropout, DropoutGrad, Embedding, RecordLoss, loss or finalize
-    launch of its own."""
+    deferred column finalize), the EmbeddingGrad plans made on the host, and no Dropout,
+    DropoutGrad, Embedding, RecordLoss, loss, finalize or EmbeddingPlan launch of its own."""
     step_ir, forward_ir = api.compile_config("bert_tiny")
     launches = kernel_ir.parse_plan(api.plan(step_ir, forward_ir))["step"]["launches"]
     whats = [l["what"] for l in launches]
@@ -123,3 +123,5 @@ def test_bert_tiny_step_plan_takes_the_fused_paths():
                for w in whats), whats
     assert not any(w.split()[0] in ("Dropout", "DropoutGrad", "Embedding", "RecordLoss", "AdamW") for w in whats), whats
     assert sum(w.startswith("CrossEntropyRows") for w in whats) == 1, whats
+    # The EmbeddingGrad plans of the host-staged ids are made by the host with the step's inputs.
+    assert not any(w.startswith("EmbeddingPlan") for w in whats), whats
