@@ -461,12 +461,52 @@ void ln_backward(hipStream_t s, const float* x, const float* gamma, const float*
 // takes up to 32 parts (a share of at least 32 chunks each) so that no thread walks all of them;
 // one of few chunks takes 1. The sum goes to out_lo[c] (c < split) or out_hi[c - split] (a null
 // output is skipped).
+// A job of few chunks whose columns, split point and pointers allow it (parts 0) takes four
+// columns a thread as 16-byte vectors, 1024 a block, each column still summed in ascending chunk
+// order: BERT-base's split-K weight gradients otherwise take hundreds of thousands of small
+// blocks a step.
 int finalize_parts(int chunks) { return std::min(32, std::max(1, chunks / 32)); }
+int finalize_parts(const ColumnJob& J) {
+  const int parts = finalize_parts(J.chunks);
+  auto a16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+  const bool vec = parts == 1 && J.width % 4 == 0 && J.split % 4 == 0 && a16(J.partial) && a16(J.out_lo) &&
+                   a16(J.out_hi);
+  return vec ? 0 : parts;
+}
+int finalize_blocks(const ColumnJob& J) {
+  const int cols = J.parts == 0 ? 1024 : 256 / J.parts;
+  return int((J.width + cols - 1) / cols);
+}
+// The vector form: thread t of block lb sums columns 4 (256 lb + t) .. + 3; returns false when
+// past the job's width. *out is where the four sums went (null for a skipped output).
+__device__ __forceinline__ bool finalize_vec(const ColumnJob& J, int lb, v4f& sum, float*& out) {
+  const int64_t c = (int64_t(lb) * 256 + threadIdx.x) * 4;
+  if (c >= J.width) return false;
+  const v4f* src = reinterpret_cast<const v4f*>(J.partial + c);
+  const int64_t stride = J.width / 4;
+  for (int z0 = 0; z0 < J.chunks; z0 += 8) {
+    v4f t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = src[int64_t(z0 + u < J.chunks ? z0 + u : J.chunks - 1) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (z0 + u < J.chunks) sum = (z0 + u == 0) ? t[u] : sum + t[u];
+  }
+  out = c < J.split ? (J.out_lo ? J.out_lo + c : nullptr) : (J.out_hi ? J.out_hi + (c - J.split) : nullptr);
+  if (out) *reinterpret_cast<v4f*>(out) = sum;
+  return true;
+}
 __global__ __launch_bounds__(256) void k_column_finalize(ColumnJobs jobs) {
   __shared__ float red[256];
   int j = 0;
   while (j + 1 < jobs.count && int(blockIdx.x) >= jobs.job[j + 1].first) ++j;
   const ColumnJob& J = jobs.job[j];
+  if (J.parts == 0) {
+    v4f sum{0.0f, 0.0f, 0.0f, 0.0f};
+    float* out = nullptr;
+    finalize_vec(J, int(blockIdx.x) - J.first, sum, out);
+    return;
+  }
   const int parts = J.parts, cols = 256 / parts;
   const int lc = threadIdx.x % cols, part = threadIdx.x / cols;
   const int64_t c = int64_t(int(blockIdx.x) - J.first) * cols + lc;
@@ -509,8 +549,8 @@ void column_finalize(hipStream_t s, const ColumnJob* jobs, int count) {
       b.job[j] = jobs[base + j];
       if (b.job[j].chunks <= 0 || b.job[j].width <= 0) bad("column finalize job without partials");
       b.job[j].first = blocks;
-      b.job[j].parts = finalize_parts(b.job[j].chunks);
-      blocks += int((b.job[j].width + 256 / b.job[j].parts - 1) / (256 / b.job[j].parts));
+      b.job[j].parts = finalize_parts(b.job[j]);
+      blocks += finalize_blocks(b.job[j]);
     }
     MSX_LAUNCH(k_column_finalize, dim3(unsigned(blocks)), dim3(256), 0, s, b);
   }
@@ -1434,6 +1474,15 @@ __global__ __launch_bounds__(256) void k_finalize_adamw(ColumnJobs jobs, int fin
     int j = 0;
     while (j + 1 < jobs.count && bid >= jobs.job[j + 1].first) ++j;
     const ColumnJob& J = jobs.job[j];
+    if (J.parts == 0) {
+      v4f sum{0.0f, 0.0f, 0.0f, 0.0f};
+      float* out = nullptr;
+      if (!finalize_vec(J, bid - J.first, sum, out) || !out) return;
+      const int64_t i = out - g;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) adamw_one(p[i + e], sum[e], m[i + e], v[i + e], k, lr, b1, b2);
+      return;
+    }
     const int parts = J.parts, cols = 256 / parts;
     const int lc = threadIdx.x % cols, part = threadIdx.x / cols;
     const int64_t c = int64_t(bid - J.first) * cols + lc;
@@ -1515,8 +1564,8 @@ void finalize_adamw(hipStream_t s, const ColumnJob* jobs, int count, float* p, f
     const ColumnJob& J = b.job[j];
     if (J.chunks <= 0 || J.width <= 0) bad("column finalize job without partials");
     b.job[j].first = blocks;
-    b.job[j].parts = finalize_parts(J.chunks);
-    blocks += int((J.width + 256 / b.job[j].parts - 1) / (256 / b.job[j].parts));
+    b.job[j].parts = finalize_parts(J);
+    blocks += finalize_blocks(b.job[j]);
     const std::pair<const float*, int64_t> outs[2] = {{J.out_lo, int64_t(std::min(J.split, J.width))},
                                                       {J.out_hi, int64_t(J.width) - std::min(J.split, J.width)}};
     for (auto [o, len] : outs) {
