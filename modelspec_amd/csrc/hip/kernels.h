@@ -167,7 +167,7 @@ void embedding_grad(hipStream_t s, const int32_t* ids, const float* g, float* ou
                     int64_t h, const float* addend = nullptr);
 
 // EmbeddingGrad as a sorted-segment scatter (segments.hip), bit-exact with embedding_grad: a plan
-// per table (ids of at most 8192 positions, eg_sorted_fits) made by eg_plan into a buffer of
+// per table (ids of at most 8192 positions made by eg_plan, 16384 by eg_plan_host) into a buffer of
 // eg_plan_bytes, then eg_apply writes out = e (or addend + e) for up to kEgJobs tables a launch.
 constexpr int kEgJobs = 3;
 struct EgPlanJob { const int32_t* ids; int32_t* plan; int32_t n, rows, pos_bits, key_bits; };
@@ -181,7 +181,8 @@ struct EgApplyJob {
   int32_t vec, blocks_short, blocks_long, blocks;  // set by eg_apply
 };
 struct EgApplySet { EgApplyJob job[kEgJobs]; int32_t count; };
-bool eg_sorted_fits(int64_t n, int64_t rows);
+bool eg_sorted_fits(int64_t n, int64_t rows);         // the apply (and a plan made by the host): n <= 16384
+bool eg_device_plan_fits(int64_t n, int64_t rows);  // eg_plan on the device: n <= 8192
 size_t eg_plan_bytes(int64_t n, int64_t rows);
 void eg_plan(hipStream_t s, const EgPlanJob* jobs, int njobs);
 // The same plan made on the host (ids in host memory, plan into host memory of eg_plan_bytes), for

@@ -923,6 +923,7 @@ void Executor::build() {
           if (ps.ids == ids && ps.rows == rows)  // made by the host in the input block (a token there)
             by_ids[key] = static_cast<char*>(input_token_) + ps.offset;
         if (!by_ids.count(key)) {
+          if (!hk::eg_device_plan_fits(nn, rows)) continue;  // the scatter kernel takes it instead
           by_ids[key] = R(hk::eg_plan_bytes(nn, rows));
           jobs.push_back({ids, nn, rows, by_ids[key]});
         }

@@ -40,7 +40,8 @@ constexpr int kTilePitch = 36;   // floats a staged row takes in LDS (32 + 4: fl
 constexpr int kAddBatch = MSX_EG_ADD_BATCH;  // staged values a column reads ahead of its adds
 constexpr int kApplyThreads = 256;
 constexpr int kCountRows = 36864;
-constexpr int kMaxPositions = 8192;  // ids a table's EmbeddingGrad takes on this path  // rows an LDS histogram of u32 counts holds (144 KiB)
+constexpr int kMaxPositions = 16384;  // ids a table's EmbeddingGrad takes on this path (apply)
+constexpr int kPlanPositions = 8192;  // ids the device plan takes (a plan made by the host: kMaxPositions)
 
 int bit_length(uint64_t v) {
   int b = 0;
@@ -68,6 +69,7 @@ bool eg_sorted_fits(int64_t n, int64_t rows) {
   const int pb = bit_length(uint64_t(n - 1)) > 0 ? bit_length(uint64_t(n - 1)) : 1;
   return pb + bit_length(uint64_t(rows)) <= 32;
 }
+bool eg_device_plan_fits(int64_t n, int64_t rows) { return n <= kPlanPositions && eg_sorted_fits(n, rows); }
 
 size_t eg_plan_bytes(int64_t n, int64_t rows) { return size_t(PlanLayout(n, rows).words) * 4; }
 
@@ -112,7 +114,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_eg_plan_count(EgPlanSet set) {
   for (int r = tid; r < rows; r += kPlanThreads) counts[r] = 0;
   for (int w = tid; w < words; w += kPlanThreads) named_rows[w] = 0;
   // Every id load in flight before the first atomic.
-  constexpr int kMaxPer = kMaxPositions / kPlanThreads;
+  constexpr int kMaxPer = kPlanPositions / kPlanThreads;
   int32_t id_of[kMaxPer], slot[kMaxPer];
 #pragma unroll
   for (int k = 0; k < kMaxPer; ++k) {
@@ -304,7 +306,7 @@ void eg_plan(hipStream_t s, const EgPlanJob* jobs, int njobs) {
   int64_t max_n = 0, dyn = 0;
   for (int q = 0; q < njobs; ++q) {
     EgPlanJob j = jobs[q];
-    if (!eg_sorted_fits(j.n, j.rows)) bad("eg_plan: ids or table too large for the block sort");
+    if (!eg_device_plan_fits(j.n, j.rows)) bad("eg_plan: ids or table too large for the block sort");
     j.pos_bits = std::max(1, bit_length(uint64_t(j.n - 1)));
     j.key_bits = j.pos_bits + bit_length(uint64_t(j.rows));
     set.job[q] = j;
