@@ -163,12 +163,15 @@ int msx_evaluate(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, cons
                  const char* labels, const char* weights, msx_heldout* out);
 
 /* msx_evaluate without device allocation. No counterpart in the reference: it is for callers that
- * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
- * that forbid hipMalloc). The row results and sums live in one static device array of the
- * library (512 KiB + 256 bytes a device, held until the process ends) instead of a buffer the
- * session allocates on its first evaluation; the call makes no hipMalloc or hipFree. A batch of
- * more than 65,536 rows (labels) is MSX_E_INVALID. Every call on one device shares the array and
- * clears its sums first, so calls that overlap on one device race. Results equal msx_evaluate's. */
+ * cannot allocate device memory (tight serving loops, harnesses that forbid hipMalloc). The row
+ * results and sums live in one static device array of the library (512 KiB + 256 bytes a device,
+ * held until the process ends) instead of a buffer the session allocates on its first
+ * evaluation; the call makes no hipMalloc or hipFree. A batch of more than 65,536 rows (labels)
+ * is MSX_E_INVALID. Calls on one device share the array: each holds a per-device lock from
+ * clearing the sums to reading them back, so concurrent calls from several threads run one after
+ * another. The call waits for the device and copies the sums to the host, so it cannot be
+ * recorded under HIP graph capture. It leaves the calling thread's current device as it found
+ * it. Results equal msx_evaluate's. */
 int msx_evaluate_static(msx_ctx* ctx, uint32_t n, const msx_tensor* const* inputs, const uint32_t* n_inputs,
                         const char* labels, const char* weights, msx_heldout* out);
 

@@ -455,7 +455,7 @@ int train_run(msx_ctx* ctx, const char* config, int64_t steps, uint64_t eval_eve
   if (train_seconds) *train_seconds = r.train_seconds;
   if (eval_seconds) *eval_seconds = r.eval_seconds;
   if (r.nonfinite_step >= 0)
-    return fail(MSX_E_NONFINITE, "E-TRAIN-001: a loss or an updated parameter is not finite at step " + std::to_string(r.nonfinite_step));
+    return fail(MSX_E_NONFINITE, "E-TRAIN-001: " + r.nonfinite_message);
   return MSX_OK;
 }
 }  // namespace
@@ -640,7 +640,7 @@ int msx_train_checkpointed(msx_ctx* ctx, const char* config, const char* packed_
     }
     if (start_step) *start_step = r.start_step;
     if (r.nonfinite_step >= 0)
-      return fail(MSX_E_NONFINITE, "E-TRAIN-001: a loss or an updated parameter is not finite at step " + std::to_string(r.nonfinite_step));
+      return fail(MSX_E_NONFINITE, "E-TRAIN-001: " + r.nonfinite_message);
     return MSX_OK;
   });
 }
@@ -666,7 +666,7 @@ int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t ma
     }
     if (train_seconds) *train_seconds = r.train_seconds;
     if (r.nonfinite_step >= 0)
-      return fail(MSX_E_NONFINITE, "E-TRAIN-001: a loss or an updated parameter is not finite at step " + std::to_string(r.nonfinite_step));
+      return fail(MSX_E_NONFINITE, "E-TRAIN-001: " + r.nonfinite_message);
     return MSX_OK;
   });
 }

@@ -8,6 +8,7 @@
 #include <cstring>
 #include <array>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <set>
 
@@ -23,20 +24,32 @@ static __device__ __align__(256) char scratch[kStaticScratchBytes];
 namespace msx {
 
 namespace {
+// One entry per device: the address of its copy of `scratch`, and the mutex that a call holds for
+// as long as it uses that copy, so calls on one device from several threads run one at a time.
+struct StaticScratch {
+  void* ptr = nullptr;
+  std::mutex use;
+};
 std::mutex g_scratch_mu;
-std::map<int, void*> g_scratch_at;
+std::map<int, std::unique_ptr<StaticScratch>> g_scratch_at;
 
-// The address of `scratch` on `device`, looked up with that device current on its first use.
-void* static_scratch(int device) {
+// The scratch entry of `device`. Its address is looked up on first use with that device current;
+// the caller's current device is restored afterwards.
+StaticScratch& static_scratch(int device) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   auto it = g_scratch_at.find(device);
-  if (it != g_scratch_at.end()) return it->second;
-  hip_check(hipSetDevice(device), "hipSetDevice (static scratch)");
+  if (it != g_scratch_at.end()) return *it->second;
+  int current = -1;
+  hip_check(hipGetDevice(&current), "hipGetDevice (static scratch)");
+  if (current != device) hip_check(hipSetDevice(device), "hipSetDevice (static scratch)");
   void* ptr = nullptr;
-  hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (static scratch)");
+  hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (current != device) hip_check(hipSetDevice(current), "hipSetDevice (restore)");
+  hip_check(e, "hipGetSymbolAddress (static scratch)");
   if (!ptr) throw HipError("hipGetSymbolAddress (static scratch): no address");
-  g_scratch_at[device] = ptr;
-  return ptr;
+  auto entry = std::make_unique<StaticScratch>();
+  entry->ptr = ptr;
+  return *(g_scratch_at[device] = std::move(entry));
 }
 }  // namespace
 
@@ -2377,11 +2390,15 @@ HeldOutSums Session::held_out_in(const HeldOut& h, bool no_alloc) {
   const size_t state_at = (size_t(rows) * 8 + 255) / 256 * 256;
   float* row_out = nullptr;
   hk::HeldOutState* state = nullptr;
+  std::unique_lock<std::mutex> scratch_lock;
   if (no_alloc) {
     if (rows > kStaticEvalRows)
       throw IrError("held-out evaluation without allocation: a batch of " + std::to_string(rows) + " rows exceeds " +
                     std::to_string(kStaticEvalRows));
-    char* base = static_cast<char*>(static_scratch(device_));
+    StaticScratch& sc = static_scratch(device_);
+    // Held until the sums are read back: no other call on this device uses the array meanwhile.
+    scratch_lock = std::unique_lock<std::mutex>(sc.use);
+    char* base = static_cast<char*>(sc.ptr);
     row_out = reinterpret_cast<float*>(base);
     state = reinterpret_cast<hk::HeldOutState*>(base + kStaticStateAt);
   } else if (rows > eval_rows_) {

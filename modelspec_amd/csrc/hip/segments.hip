@@ -12,9 +12,10 @@
 //   - a short segment: one wave sorts its positions across lanes, then with lanes over columns
 //     loads the segment's rows together and adds them in position order;
 //   - a long segment (a frequent id, or the padding slots that all name row 0): one block per
-//     32-column group orders the positions through an LDS bitmap of all n positions, then stages
-//     256 rows a round through LDS with every thread while one lane a column adds the staged rows
-//     in position order and the next round's loads are in flight;
+//     32-column group takes the positions in ascending order (as listed by a sorted plan, or
+//     ordered through an LDS bitmap of all n positions), then stages 256 rows a round through LDS
+//     with every thread, leaving out rows that are all zeros in the group, while one lane a column
+//     adds the staged rows in position order and the next round's loads are in flight;
 //   - the rows no id names: 32-row stripes of zeros (or of the addend).
 // The work per row is the reference's; only who adds which column differs.
 #include "kernels.h"
@@ -53,8 +54,9 @@ int bit_length(uint64_t v) {
 struct PlanLayout {
   int64_t counts, order, seg_start, seg_id, longs, covered, words;
   __host__ __device__ PlanLayout(int64_t n, int64_t rows) {
-    counts = 0;
-    order = 4;
+    counts = 0;  // [0] segments, [1] segments the short region walks, [2] long segments,
+                 // [3] positions, [4] 1 when each segment's positions are listed ascending
+    order = 8;
     seg_start = order + n;
     seg_id = seg_start + n + 1;
     longs = seg_id + n;
@@ -172,6 +174,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_eg_plan_count(EgPlanSet set) {
     out[L.counts + 1] = all_seg;  // the short region walks every segment and skips the long ones
     out[L.counts + 2] = all_long;
     out[L.counts + 3] = all_pos;
+    out[L.counts + 4] = 0;  // positions within a segment in arrival order
   }
 }
 
@@ -265,6 +268,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_eg_plan(EgPlanSet set) {
     out[L.counts + 1] = segments;
     out[L.counts + 2] = n_long;
     out[L.counts + 3] = n_valid;
+    out[L.counts + 4] = 1;  // the stable sort keeps positions ascending
   }
 }
 
@@ -297,6 +301,7 @@ void eg_plan_host(const int32_t* ids, int32_t n, int32_t rows, int32_t* out) {
   out[L.counts + 1] = seg;  // the short region walks every segment and skips the long ones
   out[L.counts + 2] = lng;
   out[L.counts + 3] = all_pos;
+  out[L.counts + 4] = 1;
 }
 
 void eg_plan(hipStream_t s, const EgPlanJob* jobs, int njobs) {
@@ -427,14 +432,17 @@ __device__ __forceinline__ int position_of_rank(int k, const int* pre, const uin
 }
 
 // The positions of ranks r0 .. r0 + 255 of a long segment, columns [c_lo, c_lo + cw): thread t's
-// row in registers (8 float4 when the group is whole and aligned).
+// row in registers (8 float4 when the group is whole and aligned). With `ordered` the segment's
+// positions are listed ascending at `ord`; otherwise ranks come from the bitmap.
 struct LongRow { float4 v[kLongCols / 4]; };
-__device__ __forceinline__ LongRow long_load(const EgApplyJob& j, const int* pre, const uint32_t* bm, int nw, int len,
-                                             int r0, int64_t c_lo, int cw, bool vec, int t) {
+__device__ __forceinline__ LongRow long_load(const EgApplyJob& j, bool ordered, const int32_t* ord, const int* pre,
+                                             const uint32_t* bm, int nw, int len, int r0, int64_t c_lo, int cw,
+                                             bool vec, int t) {
   LongRow r;
   const int k = r0 + t;
   if (k < len) {
-    const float* src = j.g + int64_t(position_of_rank(k, pre, bm, nw)) * j.h + c_lo;
+    const int p = ordered ? ord[k] : position_of_rank(k, pre, bm, nw);
+    const float* src = j.g + int64_t(p) * j.h + c_lo;
     if (vec) {
 #pragma unroll
       for (int u = 0; u < kLongCols / 4; ++u) r.v[u] = reinterpret_cast<const float4*>(src)[u];
@@ -481,34 +489,51 @@ __global__ __launch_bounds__(kApplyThreads) void k_eg_apply(EgApplySet set) {
     const int st = plan[L.seg_start + seg];
     const int len = plan[L.seg_start + seg + 1] - st;
     const int64_t id = plan[L.seg_id + seg];
-    // The segment's positions into a bitmap of all n, then each word's rank base.
     const int nw = (j.n + 31) / 32;
-    for (int w = tid; w < nw; w += kApplyThreads) bm[w] = 0;
-    __syncthreads();
-    for (int k = tid; k < len; k += kApplyThreads) {
-      const int p = plan[L.order + st + k];
-      atomicOr(&bm[p >> 5], 1u << (p & 31));
-    }
-    __syncthreads();
-    for (int w0 = 0; w0 < nw; w0 += kApplyThreads) {
-      const int w = w0 + tid;
-      int base = 0, all = 0;
-      WordScan().exclusive_scan(w < nw ? __popc(bm[w]) : 0, base, 0, all, word_scan);
-      if (w < nw) pre[w] = base + (w0 ? pre[w0 - 1] + __popc(bm[w0 - 1]) : 0);
+    const bool ordered = plan[L.counts + 4] != 0;
+    const int32_t* ord = plan + L.order + st;
+    if (!ordered) {
+      // The segment's positions into a bitmap of all n, then each word's rank base.
+      for (int w = tid; w < nw; w += kApplyThreads) bm[w] = 0;
       __syncthreads();
-    }
-    float acc = 0.0f;
-    LongRow r = long_load(j, pre, bm, nw, len, 0, c_lo, cw, vec, tid);
-    for (int r0 = 0; r0 < len; r0 += kLongRows) {
-      __syncthreads();  // the previous round's adds are done with the tile
-      if (r0 + tid < len) {
-#pragma unroll
-        for (int u = 0; u < kLongCols / 4; ++u) *reinterpret_cast<float4*>(&tile[tid * kTilePitch + 4 * u]) = r.v[u];
+      for (int k = tid; k < len; k += kApplyThreads) {
+        const int p = ord[k];
+        atomicOr(&bm[p >> 5], 1u << (p & 31));
       }
       __syncthreads();
-      if (r0 + kLongRows < len) r = long_load(j, pre, bm, nw, len, r0 + kLongRows, c_lo, cw, vec, tid);
+      for (int w0 = 0; w0 < nw; w0 += kApplyThreads) {
+        const int w = w0 + tid;
+        int base = 0, all = 0;
+        WordScan().exclusive_scan(w < nw ? __popc(bm[w]) : 0, base, 0, all, word_scan);
+        if (w < nw) pre[w] = base + (w0 ? pre[w0 - 1] + __popc(bm[w0 - 1]) : 0);
+        __syncthreads();
+      }
+    }
+    // Rows whose values in this column group are all +0 or -0 are left out of the add chain. From
+    // the +0 start the running sum is never -0 (an exact zero from nonzero operands rounds to +0,
+    // and +0 + -0 is +0), so adding a zero of either sign leaves it unchanged: the sum over the
+    // remaining rows, in position order, is the reference's bit for bit. The padding slots of a
+    // masked-row gather (weight 0, all naming row 0) make such a segment with no adds at all.
+    float acc = 0.0f;
+    LongRow r = long_load(j, ordered, ord, pre, bm, nw, len, 0, c_lo, cw, vec, tid);
+    for (int r0 = 0; r0 < len; r0 += kLongRows) {
+      bool nz = false;
+      if (r0 + tid < len) {
+#pragma unroll
+        for (int u = 0; u < kLongCols / 4; ++u)
+          nz |= r.v[u].x != 0.0f || r.v[u].y != 0.0f || r.v[u].z != 0.0f || r.v[u].w != 0.0f;
+      }
+      __syncthreads();  // the previous round's adds are done with the tile
+      int slot = 0, cnt = 0;
+      WordScan().exclusive_scan(nz ? 1 : 0, slot, 0, cnt, word_scan);
+      if (nz) {
+#pragma unroll
+        for (int u = 0; u < kLongCols / 4; ++u) *reinterpret_cast<float4*>(&tile[slot * kTilePitch + 4 * u]) = r.v[u];
+      }
+      __syncthreads();
+      if (r0 + kLongRows < len)
+        r = long_load(j, ordered, ord, pre, bm, nw, len, r0 + kLongRows, c_lo, cw, vec, tid);
       if (tid < cw) {
-        const int cnt = min(kLongRows, len - r0);
         int rr = 0;
         // kAddBatch staged values read ahead of their adds: the adds are one dependent chain, and
         // the reads' latency is paid once a batch.

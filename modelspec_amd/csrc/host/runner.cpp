@@ -333,33 +333,58 @@ RunResult run(const Compiled& c, Engine& engine, uint64_t steps, const RunOption
   // The state after k updates (train.rs:1075, 1285: `<stem>-<k>.msckpt` every n updates before
   // the end, the checkpoint path itself at the end).
   // Losses stay on the device between read-backs, as the reference's Vulkan runner keeps them
-  // (cli/src/train.rs:39-44): every loss so far and the parameters are checked where they are
-  // read back, at each checkpoint and after the last step. A non-finite loss names its own step;
-  // a non-finite parameter under finite losses names the step of the read-back that showed it.
-  // Returns false, with out.nonfinite_step and the losses through that step set, on the first.
-  auto finite_through = [&](uint64_t k, const std::vector<float>& losses,
-                            const std::vector<std::vector<float>>& params) {
+  // (cli/src/train.rs:39-44): every loss so far, the parameters and the AdamW moments are checked
+  // where they are read back, at each checkpoint and after the last step (runner.rs:156-227 checks
+  // each step on the host). A non-finite loss names its own step; a non-finite parameter or moment
+  // under finite losses names the step of the read-back that showed it. Returns false, with
+  // out.nonfinite_step, out.nonfinite_message and the losses through that step set, on the first.
+  auto finite_through = [&](uint64_t k, const std::vector<float>& losses, const std::vector<std::vector<float>>& params,
+                            bool with_moments) {
     for (size_t i = 0; i < losses.size(); ++i)
       if (!std::isfinite(losses[i])) {
         out.nonfinite_step = int64_t(start + i);
+        out.nonfinite_message = "the loss of step " + std::to_string(start + i) + " is not finite";
         out.losses.assign(losses.begin(), losses.begin() + i + 1);
         return false;
       }
-    for (const auto& p : params)
-      for (float x : p)
-        if (!std::isfinite(x)) {
-          out.nonfinite_step = int64_t(k);
-          out.losses = losses;
-          return false;
-        }
-    return true;
+    auto finite = [](const std::vector<float>& v) {
+      for (float x : v)
+        if (!std::isfinite(x)) return false;
+      return true;
+    };
+    const auto& decls = c.step.program.params;
+    std::vector<std::string> bad;
+    for (size_t q = 0; q < params.size() && q < decls.size(); ++q)
+      if (!finite(params[q])) bad.push_back("@" + decls[q].path);
+    std::string what = "parameter";
+    if (bad.empty() && with_moments && c.step.rule == Rule::AdamW) {
+      const auto m = engine.moments('m'), v = engine.moments('v');
+      std::vector<std::pair<std::string, char>> named;
+      for (size_t q = 0; q < decls.size(); ++q) {
+        if (q < m.size() && !finite(m[q])) named.emplace_back(decls[q].path, 'm');
+        if (q < v.size() && !finite(v[q])) named.emplace_back(decls[q].path, 'v');
+      }
+      std::sort(named.begin(), named.end());
+      for (auto& [path, mo] : named) bad.push_back(std::string(1, mo) + " @" + path);
+      what = "optimizer moment";
+    } else {
+      std::sort(bad.begin(), bad.end());
+    }
+    if (bad.empty()) return true;
+    std::string list;
+    for (auto& b : bad) list += (list.empty() ? "" : ", ") + b;
+    out.nonfinite_step = int64_t(k);
+    out.nonfinite_message = "the update of step " + std::to_string(k) + " leaves " +
+                            (what == "parameter" ? "a parameter" : "an optimizer moment") + " not finite: " + list;
+    out.losses = losses;
+    return false;
   };
   // Writes the state after k updates unless a loss or parameter read back is not finite; then
   // nothing is written and the run stops (returns false).
   auto checkpoint = [&](uint64_t k, const std::string& path) {
     auto w0 = std::chrono::steady_clock::now();
     std::vector<std::vector<float>> params = engine.params();
-    if (!finite_through(k, engine.losses(), params)) return false;
+    if (!finite_through(k, engine.losses(), params, true)) return false;
     Checkpoint ck = checkpoint_of(c.step, c.config.seed, k, params, engine.moments('m'), engine.moments('v'));
     write_checkpoint(path, ck);
     out.checkpoints.push_back(path);
@@ -390,9 +415,9 @@ RunResult run(const Compiled& c, Engine& engine, uint64_t steps, const RunOption
     masked_gather(last.i32.at(c.config.labels), last.f32.at(c.config.weights), uint64_t(rows->ty.count()), end, r, l, w);
   }
   out.params = engine.params();
-  if (!finite_through(end, out.losses, out.params)) return out;
+  if (!finite_through(end, out.losses, out.params, true)) return out;
   out.losses.push_back(engine.final_loss(last));
-  if (!finite_through(end, out.losses, {})) return out;
+  if (!finite_through(end, out.losses, {}, false)) return out;
   if (!o.checkpoint_path.empty()) checkpoint(end, o.checkpoint_path);
   return out;
 }

@@ -156,6 +156,10 @@ struct RunResult {
   std::vector<std::vector<float>> params;
   double train_seconds = 0;   // wall clock of the step loop (runner.rs loop; train.rs:17-31 --clock)
   int64_t nonfinite_step = -1;  // the step whose loss was not finite (absolute step number)
+  // With nonfinite_step: what was not finite, in the reference's words and order (runner.rs:156-
+  // 227): the loss, else the parameters by canonical path ("@path", in path order), else the AdamW
+  // moments ("m @path" / "v @path", in path order, m before v).
+  std::string nonfinite_message;
   uint64_t start_step = 0;       // the step the run started at (a resumed run's checkpoint step)
   std::vector<std::string> checkpoints;  // paths written, in order
   // Held-out metrics at every step k with k % eval_every == 0 and at the last step, on the

@@ -274,7 +274,7 @@ int orc_train(const char* config, int64_t steps, int64_t masked_rows, float* los
     msx::Compiled c = msx::compile_config(config, masked_rows, steps);
     OracleEngine e(c);
     msx::RunResult r = msx::run(c, e, c.config.steps);
-    if (r.nonfinite_step >= 0) { g_error = "E-TRAIN-001: non-finite loss at step " + std::to_string(r.nonfinite_step); return -1; }
+    if (r.nonfinite_step >= 0) { g_error = "E-TRAIN-001: " + r.nonfinite_message; return -1; }
     if (losses_len < r.losses.size()) { g_error = "losses buffer too small"; return -1; }
     std::memcpy(losses, r.losses.data(), r.losses.size() * sizeof(float));
     uint64_t off = 0;
@@ -418,7 +418,7 @@ int64_t orc_train_ckpt(const char* config, const char* packed_dir, int64_t steps
     if (checkpoint_path) o.checkpoint_path = checkpoint_path;
     msx::RunResult r = msx::run(c, e, n, o);
     if (r.nonfinite_step >= 0) {
-      g_error = "E-TRAIN-001: a loss or an updated parameter is not finite at step " + std::to_string(r.nonfinite_step);
+      g_error = "E-TRAIN-001: " + r.nonfinite_message;
       return -1;
     }
     if (losses) {

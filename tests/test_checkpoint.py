@@ -199,3 +199,13 @@ def test_a_diverged_run_stops_and_writes_no_later_checkpoint(oracle, tmp_path):
     assert not path.exists()
     with pytest.raises(RuntimeError, match="E-TRAIN-001"):
         oracle.train(str(src))
+
+
+def test_a_parameter_that_overflows_is_named_by_its_path(oracle, tmp_path):
+    """runner.rs:156-227: with the losses finite, the diagnostic names the parameters the update
+    left non-finite by canonical path. At lr 1e38 the first SGD update overflows w to inf while the
+    loss of step 0 is finite; a one-step run reads it back after its last update."""
+    src = tmp_path / "overflow.mspec"
+    src.write_text(DIVERGING.replace("lr = 1e30", "lr = 1e38").replace("steps = 6", "steps = 1"))
+    with pytest.raises(RuntimeError, match=r"E-TRAIN-001: the update of step 1 leaves a parameter not finite: @\S*w"):
+        oracle.train(str(src))

@@ -25,14 +25,27 @@ def test_full_run_tracks_the_oracle(ctx, config, steps, lr):
     step_ir, _ = api.compile_config(config, -1, steps)
     print(f"{config} {steps} steps", flush=True)
     got_l, got_p, _ = ctx.train_config(config, steps=steps)
-    # The MLP classifier's two biases end 7x and 3.8x past the whole-tensor bound: trained on
-    # uniform random labels, their gradients are batch sums of terms that nearly cancel, so the
-    # differences the two summation orders leave are large next to their small norms (0.037 and
-    # 0.018, against 19.9 and 5.5 for the weights, which hold the bound at 0.37 and 0.24). Every
-    # element still holds the per-element run tolerance (worst 0.41 of it). The transformer block
-    # and BERT-tiny hold the whole-tensor bound on every tensor, at 0.014 of it or less.
+    # Every loss and element within the run tolerance; the whole-tensor bound for every tensor
+    # except the MLP classifier's two biases, which test_mlp_classifier_biases_hold_the_whole_run_bound
+    # holds to it as a known failure. The transformer block and BERT-tiny hold the whole-tensor bound
+    # on every tensor, at 0.014 of it or less.
     run_fixtures.check_run(got_l, got_p, config, steps, lr, step_ir, key_biases(step_ir),
                            l2_bound=config != "mlp_classifier")
     # The run trains: the last losses are below the first.
     want_l = run_fixtures.load(config, steps)[0]
     assert want_l[-10:].mean() < want_l[:10].mean()
+
+
+@pytest.mark.xfail(strict=False, reason=(
+    "known gap: the MLP classifier's two biases end 7x and 3.8x past ||g - c|| <= 1e-4 ||c|| after "
+    "1,000 steps. Trained on uniform random labels, their gradients are batch sums of terms that "
+    "nearly cancel, so rounding differences (the GEMMs' MFMA accumulation order feeds every term) "
+    "are large next to their small norms (0.037 and 0.018; the weights hold the bound at 0.37 and "
+    "0.24 of it). Every element holds the per-element run tolerance (worst 0.41 of it)."))
+def test_mlp_classifier_biases_hold_the_whole_run_bound(ctx):
+    config, steps, lr = "mlp_classifier", 1000, 0.01
+    if not run_fixtures.available(config, steps):
+        pytest.skip(f"no committed oracle run of {config} for {steps} steps")
+    step_ir, _ = api.compile_config(config, -1, steps)
+    got_l, got_p, _ = ctx.train_config(config, steps=steps)
+    run_fixtures.check_run(got_l, got_p, config, steps, lr, step_ir, key_biases(step_ir), l2_bound=True)

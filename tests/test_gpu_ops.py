@@ -44,6 +44,57 @@ def test_matmul(ctx, oracle, m, k, n, ta, tb):
     assert ok, worst
 
 
+@pytest.mark.parametrize("m,k,n,ta,tb,bias", [
+    (1000, 64, 2200, False, True, True),    # both operands contiguous along K, ragged tiles
+    (520, 96, 4100, False, False, False),   # A along K, B along N; K tiles of 32
+    (2048, 80, 1028, True, False, True),    # neither along K (128 x 128 tiles)
+    (1500, 48, 1500, True, True, False),    # A along M, B along K
+    (100, 8192, 200, False, False, True),   # deep K: split-K slices and their sum
+    (36, 9216, 64, True, True, False),      # deep K, split, a 36-row operand along its rows
+    (36, 9000, 64, True, True, False),      # a K tail on an unpadded operand: the other kernel
+])
+def test_large_gemm_layouts(ctx, oracle, m, k, n, ta, tb, bias):
+    """The GEMMs of 2^21 outputs or more (or K of 8192 or more) run the direct-to-LDS kernel when
+    their layout allows: every pair of operand layouts, partial edge tiles, split-K with its slice
+    sum, and the bias epilogue, against the oracle."""
+    a = fast_values(91, m * k).reshape((k, m) if ta else (m, k))
+    b = fast_values(92, k * n).reshape((n, k) if tb else (k, n))
+    bv = fast_values(93, n)
+    p = Prog()
+    ai, bi_ = p.input("a", a.shape), p.input("b", b.shape)
+    lhs = p.op("Transpose", [ai], (m, k)) if ta else ai
+    rhs = p.op("Transpose", [bi_], (k, n)) if tb else bi_
+    y = p.op("MatMul", [lhs, rhs], (m, n))
+    inputs = {"a": a, "b": b}
+    if bias:
+        y = p.op("AddRows", [y, p.input("bias", (n,))], (m, n))
+        inputs["bias"] = bv
+    (g,), (w,) = both(ctx, oracle, p.out(y), inputs, (0,))
+    A = np.abs(a.T if ta else a).astype(np.float64)
+    B = np.abs(b.T if tb else b).astype(np.float64)
+    r = A @ B + (np.abs(bv) if bias else 0)
+    ok, worst = within(g, w, r.reshape(-1))
+    assert ok, worst
+
+
+@pytest.mark.parametrize("rows,m,n", [(2048, 1024, 2048), (1024, 4096, 512)])
+def test_large_weight_gradient_takes_the_bias_gradient(ctx, oracle, rows, m, n):
+    """dW = x^T dy with db = SumRows(dy) on the direct-to-LDS kernel (the column sums of its right
+    operand from the fragments the MFMAs read), and the transposed form (dW^T = dy^T x, the sums
+    as row sums of its left operand)."""
+    x, dy = fast_values(94, rows * m).reshape(rows, m), fast_values(95, rows * n).reshape(rows, n)
+    p = Prog()
+    xi, di = p.input("x", (rows, m)), p.input("dy", (rows, n))
+    dw = p.op("MatMul", [p.op("Transpose", [xi], (m, rows)), di], (m, n))
+    db = p.op("SumRows", [di], (n,))
+    dwt = p.op("MatMul", [p.op("Transpose", [di], (n, rows)), xi], (n, m))
+    (gw, gb, gt), (ww, wb, wt) = both(ctx, oracle, p.out(dw, db, dwt), {"x": x, "dy": dy}, (0, 1, 2))
+    r = np.abs(x.T).astype(np.float64) @ np.abs(dy)
+    assert within(gw, ww, r.reshape(-1))[0]
+    assert within(gb, wb, np.abs(dy).astype(np.float64).sum(0))[0]
+    assert within(gt, wt, r.T.reshape(-1))[0]
+
+
 def test_matmul_with_bias_epilogue_and_sum_rows(ctx, oracle):
     m, k, n = 4096, 128, 128
     x, w, bias = fast_values(3, m * k).reshape(m, k), fast_values(4, k * n, 0.1).reshape(k, n), fast_values(5, n)
@@ -361,6 +412,38 @@ def test_embedding_gather_and_sorted_segment_scatter_are_bit_exact(ctx, oracle, 
     got, want = both(ctx, oracle, p.out(e, dg), {"t": table, "ids": ids, "G": G}, (0, 1))
     for g, w in zip(got, want):
         assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
+
+
+@pytest.mark.parametrize("pad_kind", ["signed_zeros", "one_nonzero", "cancelling", "zero_column_groups"])
+def test_scatter_of_padding_slots_is_bit_exact(ctx, oracle, pad_kind):
+    """The masked-row scatter's shape: 832 gathered rows back into 4096 positions, the last 218
+    slots padding that all name row 0 (one long segment). Rows of +0/-0 in the padding are left
+    out of the device's add chain; the sum must still equal the oracle's sequential one bit for
+    bit: all signed zeros (+0), one nonzero padding row, x then -x then -0 rows (the exact zero of
+    a cancellation is +0), and rows that are zero in some 32-column groups only."""
+    rows, h, n, pad = 4096, 128, 832, 218
+    rng = np.random.default_rng(9)
+    ids = np.concatenate([np.sort(rng.choice(np.arange(1, rows), n - pad, replace=False)),
+                          np.zeros(pad, np.int64)]).astype(np.int32)
+    G = fast_values(18, n * h).reshape(n, h).copy()
+    zeros = np.where(rng.random((pad, h)) < 0.5, np.float32(-0.0), np.float32(0.0)).astype(np.float32)
+    G[n - pad:] = zeros
+    if pad_kind == "one_nonzero":
+        G[n - pad + 101, 37:70] = fast_values(5, 33)
+    elif pad_kind == "cancelling":
+        G[n - pad + 3] = fast_values(6, h)
+        G[n - pad + 150] = -G[n - pad + 3]
+    elif pad_kind == "zero_column_groups":
+        for r in range(0, pad, 3):
+            g = rng.integers(0, 4)
+            G[n - pad + r, 32 * g:32 * g + 32] = fast_values(100 + r, 32)
+    p = Prog()
+    ii, Gi = p.input("ids", (n,), "i32"), p.input("G", (n, h))
+    dg = p.op("EmbeddingGrad", [ii, Gi], (rows, h), f"[{rows}]")
+    got, want = both(ctx, oracle, p.out(dg), {"ids": ids, "G": G}, (0,))
+    assert np.array_equal(got[0].view(np.uint32), want[0].view(np.uint32))
+    if pad_kind == "signed_zeros":
+        assert np.all(got[0][0].view(np.uint32) == 0)  # +0, never -0
 
 
 def test_dropout_masks_are_bit_exact_at_full_size(ctx, oracle):

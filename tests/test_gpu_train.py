@@ -59,6 +59,35 @@ def test_linear_regression_is_bit_identical_to_the_golden_run(ctx, oracle):
     assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
 
 
+def test_linear_regression_on_the_baseline_distribution(ctx, oracle):
+    """BASELINE configs[0] as stated there: x ~ U(-1, 1) [8, 4], w_true ~ U(-1, 1) [4, 1] and
+    y = x w_true + N(0, 0.01) noise (standard deviation 0.01), a fresh batch each step, SGD lr 0.1
+    for 500 steps from the seed-42 xavier initialisation. The same step program and inputs go to
+    the oracle one step at a time (its printed step program: loss, gradient and updated weight);
+    the device run must equal it bit for bit, as the golden run does."""
+    steps = 500
+    step_ir, fwd = api.compile_config("linear_regression")
+    rng = np.random.default_rng(20250101)
+    w_true = rng.uniform(-1, 1, (4, 1))
+    batches = []
+    for _ in range(steps):
+        x = rng.uniform(-1, 1, (8, 4))
+        y = x @ w_true + rng.normal(0, 0.01, (8, 1))
+        batches.append({"x": x.astype(np.float32).reshape(-1), "y": y.astype(np.float32).reshape(-1)})
+    w0 = oracle.init_params("linear_regression", 4)
+    want_l, w = [], w0.copy()
+    for b in batches:
+        loss, w = oracle.run_program(step_ir, {"x": b["x"], "y": b["y"]}, params=[w], outputs=(0, 2))
+        want_l.append(loss[0])
+    ctx.load(step_ir, fwd, 42, 1)
+    ctx.set_params([w0])
+    got_l = ctx.run_steps(batches)
+    got_w = ctx.read_param(0, 4)
+    assert np.array_equal(np.asarray(got_l, np.float32), np.asarray(want_l, np.float32))
+    assert np.array_equal(got_w, w)
+    assert want_l[-1] < 1e-3 < want_l[0]  # it fits the teacher down to the noise
+
+
 @pytest.mark.parametrize("config,steps,lr", [
     ("mnist_mlp", 100, 0.1),
     ("mlp_micro", -1, 0.01),

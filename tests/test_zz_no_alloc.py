@@ -55,3 +55,38 @@ def test_the_static_evaluation_equals_the_allocating_one(ctx):
     ctx.load(step, logits_forward(65537, 2), 0, 1)
     with pytest.raises(api.MsxError, match="exceeds 65536"):
         ctx.evaluate_static(batches(rng, 1, 65537, 2), "labels", "weights")
+
+
+def test_static_evaluations_from_two_threads_do_not_mix(ctx):
+    """Two contexts on one device, each on its own thread, call the static evaluation in turn
+    with different batches (ctypes releases the GIL for the call, so the calls overlap): the
+    per-device lock keeps each call's sums its own, equal to that context's allocating result."""
+    import threading
+    step, _ = api.compile_config("mlp_micro")
+    rng = np.random.default_rng(5)
+    other = api.Context(0)
+    try:
+        jobs = []
+        for c, (rows, v) in ((ctx, (4096, 512)), (other, (3000, 129))):
+            c.load(step, logits_forward(rows, v), 0, 1)
+            bs = batches(rng, 2, rows, v)
+            jobs.append((c, bs, c.evaluate(bs, "labels", "weights")))
+        errors = []
+
+        def run(c, bs, want):
+            try:
+                for _ in range(20):
+                    same(c.evaluate_static(bs, "labels", "weights"), want)
+            except Exception as e:  # noqa: BLE001 - reported on the main thread
+                errors.append(e)
+
+        print("static evaluation on two threads", flush=True)
+        threads = [threading.Thread(target=run, args=j) for j in jobs]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join(timeout=100)
+        assert not any(t.is_alive() for t in threads)
+        assert not errors, errors
+    finally:
+        other.close()
