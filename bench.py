@@ -116,8 +116,8 @@ def _oracle_step_times(config, steps):
 class CpuBaseline:
     """The CPU oracle (a single-threaded C++ restatement of the reference interpreter) on
     `workers` x `steps` training steps of the config, as `workers` processes of one thread each,
-    started before the GPU is touched and collected after the GPU run; the value is the median
-    step. Spawned (not forked) processes, so no child inherits a GPU context."""
+    started after the GPU run; the value is the median step. Spawned (not forked) processes, so no
+    child inherits a GPU context."""
 
     def __init__(self, config, workers, steps):
         import multiprocessing as mp
@@ -164,6 +164,8 @@ def main():
                     help="untimed steps before the timed region: at least N steps run in all (the W warmup "
                          "steps count toward it)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--fuse-ce-head", choices=("on", "off"), default=None,
+                    help="force MSX_FUSE_CE_HEAD on or off (default: the library's default)")
     ap.add_argument("--step-times", action="store_true", help="print every timed step's ms to stderr")
     ap.add_argument("--launches", metavar="FILE", help="write every profiled launch (order, time, work, "
                     "kernels) to FILE as JSON lines")
@@ -177,11 +179,10 @@ def main():
         sys.exit(2)
 
     w = WORKLOADS[args.config]
-    cpu = None
-    if not args.no_cpu and args.config == "bert_tiny":
-        cpu = CpuBaseline(args.config, args.cpu_workers, args.cpu_steps)
     from modelspec_amd import api
     ctx = api.Context(0)
+    if args.fuse_ce_head is not None:
+        ctx.set_fusion(ce_head=args.fuse_ce_head == "on")
     # A fresh process's first ~25 steps hold stalls of 1.5-8 ms (measured on one MI355X, with and
     # without the hipGraph and the side stream); from 50 steps on there are none. The settle steps
     # run untimed after the W warmup steps' inputs, before the barrier that opens the timed region.
@@ -245,8 +246,11 @@ def main():
     }
     if w["mixed"]:
         out["loss_scale"] = ctx_scale
-    if cpu is not None:
-        out["cpu_baseline"] = cpu.result()
+    # The CPU baseline runs after the GPU run has finished (its processes start once the context is
+    # closed), so neither competes with the other for host cores or memory.
+    if not args.no_cpu and args.config == "bert_tiny":
+        out["cpu_baseline"] = CpuBaseline(args.config, args.cpu_workers, args.cpu_steps).result()
+        out["cpu_baseline"]["overlapped_gpu_run"] = False
     print(json.dumps(out), flush=True)
 
 

@@ -116,7 +116,8 @@ int msx_stats(msx_ctx* ctx, msx_run_stats* out);
  * No counterpart in the reference, which trains in f32 only. */
 int msx_set_precision(msx_ctx* ctx, int32_t mixed, float loss_scale, uint32_t scale_window);
 
-/* Optional fusions of the next msx_load or msx_prog_new. MSX_FUSE_CE_HEAD: a cross-entropy whose
+/* Optional fusions of the next msx_load, msx_prog_new or built-in config run (msx_train_config and
+ * the other config entry points). MSX_FUSE_CE_HEAD: a cross-entropy whose
  * logits come from a GEMM and whose gradient only GEMMs read is folded into those GEMMs (the
  * forward leaves per-tile row partials, the gradient is formed from the logits as it is loaded and
  * never stored); off by default, as it measured slower on BERT-tiny. No counterpart in the

@@ -27,6 +27,7 @@ SOURCES = [
     "hip/runtime.cpp",
     "hip/kernels.hip",
     "hip/gemm.hip",
+    "hip/gemm_lds.hip",
     "hip/attention.hip",
     "hip/data.hip",
     "hip/segments.hip",

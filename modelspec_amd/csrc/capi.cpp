@@ -96,9 +96,12 @@ struct msx_ctx {
 };
 
 namespace {
-msx::SessionOptions config_options(const msx::Compiled& c) {
+// A built-in config's session: its own precision, the context's fusion choices (msx_set_fusion).
+msx::SessionOptions config_options(const msx_ctx* ctx, const msx::Compiled& c) {
   msx::SessionOptions o;
   o.mixed = c.config.mixed;
+  o.fuse_ce_head = ctx->options.fuse_ce_head;
+  o.fuse_optimizer = ctx->options.fuse_optimizer;
   return o;
 }
 
@@ -413,7 +416,7 @@ int train_run(msx_ctx* ctx, const char* config, int64_t steps, uint64_t eval_eve
   ctx->prediction = c.prediction;
   ctx->seed = c.config.seed;
   ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction, corpus,
-                                                config_options(c));
+                                                config_options(ctx, c));
   // Each evaluation's metrics, finished with the host's weight sums as msx_evaluate does.
   struct Recording : msx::Engine {
     msx::Session& s;
@@ -620,7 +623,7 @@ int msx_train_checkpointed(msx_ctx* ctx, const char* config, const char* packed_
     ctx->seed = c.config.seed;
     ctx->session =
         std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction, corpus.get(),
-                                       config_options(c));
+                                       config_options(ctx, c));
     msx::RunOptions o;
     o.corpus = corpus.get();
     o.resume = from.get();
@@ -654,7 +657,7 @@ int msx_train_config(msx_ctx* ctx, const char* config, int64_t steps, int64_t ma
     ctx->forward = c.forward;
     ctx->prediction = c.prediction;
     ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction, nullptr,
-                                                  config_options(c));
+                                                  config_options(ctx, c));
     msx::RunResult r = msx::run(c, *ctx->session, c.config.steps);
     if (losses_len < r.losses.size()) return fail(MSX_E_INVALID, "losses buffer too small");
     std::memcpy(losses, r.losses.data(), r.losses.size() * 4);
@@ -681,7 +684,7 @@ int msx_bench_config(msx_ctx* ctx, const char* config, int64_t masked_rows, uint
     ctx->forward = c.forward;
     ctx->prediction = c.prediction;
     ctx->session = std::make_unique<msx::Session>(ctx->device, ctx->step, ctx->forward, c.config.seed, c.prediction, nullptr,
-                                                  config_options(c));
+                                                  config_options(ctx, c));
     msx::Session& s = *ctx->session;
     msx::Feed feed(c);
     if (feed.needs_teacher())

@@ -1,0 +1,406 @@
+// The large-shape f32 GEMM on gfx950: operand K tiles loaded straight into LDS.
+#include "gemm_common.h"
+
+#include <algorithm>
+
+namespace msx::hk {
+
+// ---------------------------------------------------------------------------------------------
+// The large-shape f32 GEMM (k_gemm_lds): operand K tiles move from global memory straight into an
+// NS-stage LDS ring (global_load_lds_dwordx4: no staging registers, no LDS store instructions), one
+// barrier a K tile, the loads of tile t + NS - 1 in flight while tile t is multiplied.
+//
+// Index mapping. The 16x16x4 f32 MFMA takes lane (c = l % 16, q = l / 16) to supply row c of its
+// 16-row operands at K index q of a K step. Step s (0..3) of a 16-K block maps q to the K index
+// 4 q + s, so a lane's four steps read four consecutive K of one row: one 16-byte LDS read. Which
+// output row or column an MFMA lane stands for is free as long as both operands and the output
+// agree, and is chosen so that every LDS read is 16 bytes:
+//   - an operand contiguous along K (KC) is staged as [row][K] (BK floats a row, the K group of
+//     row r at slot kq ^ f(r), so the 16 rows a quarter-wave reads at one K group hit distinct
+//     banks; the loading lane fetches the group its slot holds); MFMA block i of a wave takes rows
+//     16 i + c;
+//   - an operand contiguous along its rows (not KC) is staged as [K][row], as it lies in memory;
+//     lane c takes rows I c .. I c + I - 1 of the wave tile, one per MFMA block, one 16-byte read a
+//     K step.
+// The MFMA computes C^T tiles (B's fragment in the first operand), so a lane holds four
+// consecutive output columns: float4 stores of the output.
+// K must be a multiple of BK, or a KC operand's rows zero-padded up to the next multiple (its
+// leading dimension); a non-KC operand's K rows past K are clamped to the last one (their products
+// with the zero padding vanish). SUMS: 1, the row sums of op(A) over K; 2, the column sums of
+// op(B) (a bias gradient), taken from the fragments of the waves of the first wave column (row).
+namespace {
+#define MSX_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+// 16 bytes a lane from global memory into LDS at dst + 16 lane (the host pass sees an empty body).
+__device__ __forceinline__ void load_lds16(const float* src, float* dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, MSX_LDS_PTR(dst), 16, 0, 0);
+#endif
+}
+// Waits until at most n vector memory operations of this wave are outstanding (expcnt and lgkmcnt
+// unconstrained).
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (n) {
+#define MSX_W(N) case N: __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (((N) >> 4) << 14) | (7 << 4) | (0xF << 8)); break;
+    MSX_W(0) MSX_W(1) MSX_W(2) MSX_W(3) MSX_W(4) MSX_W(5) MSX_W(6) MSX_W(7) MSX_W(8) MSX_W(9) MSX_W(10)
+    MSX_W(11) MSX_W(12) MSX_W(13) MSX_W(14) MSX_W(15) MSX_W(16)
+#undef MSX_W
+    default: __builtin_amdgcn_s_waitcnt((7 << 4) | (0xF << 8)); break;
+  }
+}
+}  // namespace
+
+template <int BM, int BN, int WGM, int WGN, int BK, bool AKC, bool BKC, int NS, bool FP, int SUMS>
+__global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds(GemmPtrs ptrs, int64_t M, int64_t N, int64_t K,
+                                                             int64_t lda, int64_t ldb, int64_t ldc, int64_t kchunk,
+                                                             int64_t zero_to, bool vo, GemmOrder order) {
+  constexpr int W = WGM * WGN;
+  constexpr int WTM = BM / WGM, WTN = BN / WGN, I = WTM / 16, J = WTN / 16;
+  static_assert((I == 4 || I == 2) && (J == 4 || J == 2), "wave tiles of 2 or 4 MFMA blocks a side");
+  static_assert(BK == 16 || BK == 32, "K tiles of 16 or 32");
+  constexpr int SA = BM * BK, SB = BN * BK, SS = SA + SB;  // floats a stage
+  constexpr int LA = SA / 256, LB = SB / 256;              // 1 KB wave load instructions a tile
+  static_assert(LA % W == 0 && LB % W == 0, "whole load instructions a wave");
+  constexpr int PA = LA / W, PB = LB / W, LPT = PA + PB;   // a wave's load instructions a tile
+  constexpr int RPI = 256 / BK, LPR = BK / 4;              // KC: rows an instruction, lanes a row
+  constexpr int KB = BK / 16;                              // 16-K blocks a tile
+  __shared__ __align__(16) float smem[NS * SS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 15, q = lane >> 4;
+  // Consecutive blocks go to the 8 XCDs in turn; each XCD takes a contiguous run of the tile order.
+  const uint32_t per = gridDim.x / 8, tg = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (tg >= order.tiles) return;
+  const uint32_t tz = tg / (order.mt * order.nt), tr = tg % (order.mt * order.nt);
+  const uint32_t tm = order.m_fastest ? tr % order.mt : tr / order.nt;
+  const uint32_t tn = order.m_fastest ? tr / order.mt : tr % order.nt;
+  const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
+  // The slices cover K rounded up to BK.
+  const int64_t kpad = (K + BK - 1) / BK * BK;
+  const int64_t kbeg = int64_t(tz) * kchunk, kend = kpad < kbeg + kchunk ? kpad : kbeg + kchunk;
+  const int tiles = int((kend - kbeg) / BK);
+  const int wm = (wave / WGN) * WTM, wn = (wave % WGN) * WTN;
+  const float* __restrict__ A = ptrs.a[0];
+  const float* __restrict__ B = ptrs.b[0];
+  const GemmEpi epi = ptrs.epi[0];
+  const float* __restrict__ bias = epi.bias;
+  float* __restrict__ ws = ptrs.ws[0];
+  float* __restrict__ colsum = ptrs.colsum[0];
+  auto fsw = [](int r) { return BK == 16 ? (r >> 2) & 3 : (r >> 1) & 7; };
+  // Each load instruction's per-lane source at the slice's first K tile. KC: instruction t holds
+  // rows t RPI .. (lane L: row L / LPR, K group (L % LPR) ^ f(row)). Not KC: K rows t (256 / R) ..
+  // of R = BM (BN) floats (lane L: rows 4 (L % (R / 4)) .. + 3 at K row L / (R / 4)); the last
+  // K row a lane may read is kmax (clamped).
+  const float* srcA[PA];
+  const float* srcB[PB];
+  int kofA[PA], kofB[PB];
+  const int64_t kmax = K - 1;
+#pragma unroll
+  for (int h = 0; h < PA; ++h) {
+    const int t = wave * PA + h;
+    if (AKC) {
+      const int r = t * RPI + lane / LPR, kq = (lane % LPR) ^ fsw(t * RPI + lane / LPR);
+      const int64_t row = m0 + r < M ? m0 + r : M - 1;
+      srcA[h] = A + row * lda + kbeg + 4 * kq;
+      kofA[h] = 0;
+    } else {
+      constexpr int RQ = BM / 4, KR = 256 / BM;
+      const int kr = t * KR + lane / RQ;
+      int64_t col = m0 + 4 * (lane % RQ);
+      col = col + 3 < M ? col : ((M - 1) & ~int64_t(3));
+      srcA[h] = A + col;
+      kofA[h] = kr;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < PB; ++h) {
+    const int t = wave * PB + h;
+    if (BKC) {
+      const int r = t * RPI + lane / LPR, kq = (lane % LPR) ^ fsw(t * RPI + lane / LPR);
+      const int64_t row = n0 + r < N ? n0 + r : N - 1;
+      srcB[h] = B + row * ldb + kbeg + 4 * kq;
+      kofB[h] = 0;
+    } else {
+      constexpr int RQ = BN / 4, KR = 256 / BN;
+      const int kr = t * KR + lane / RQ;
+      int64_t col = n0 + 4 * (lane % RQ);
+      col = col + 3 < N ? col : ((N - 1) & ~int64_t(3));
+      srcB[h] = B + col;
+      kofB[h] = kr;
+    }
+  }
+  // Tile `tile` of the slice into its stage; past the last tile, the last tile again (into a stage
+  // nobody reads), so every iteration issues the same number of loads.
+  auto issue = [&](int tile) {
+    tile = tile < tiles ? tile : tiles - 1;
+    float* st = smem + (tile % NS) * SS;
+    const int64_t k0 = int64_t(tile) * BK;
+#pragma unroll
+    for (int h = 0; h < PA; ++h) {
+      const int t = wave * PA + h;
+      if (AKC) {
+        load_lds16(srcA[h] + k0, st + t * 256);
+      } else {
+        const int64_t kr = kbeg + k0 + kofA[h];
+        load_lds16(srcA[h] + (kr < kmax ? kr : kmax) * lda, st + t * 256);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < PB; ++h) {
+      const int t = wave * PB + h;
+      if (BKC) {
+        load_lds16(srcB[h] + k0, st + SA + t * 256);
+      } else {
+        const int64_t kr = kbeg + k0 + kofB[h];
+        load_lds16(srcB[h] + (kr < kmax ? kr : kmax) * ldb, st + SA + t * 256);
+      }
+    }
+  };
+  // This lane's output columns: group j is n0 + wn + 16 j + 4 q .. + 3 (KC B), or n0 + wn + 4 J q +
+  // 4 j .. + 3 (B not KC); the bias of each is loaded before the K loop.
+  v4f bias4[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    bias4[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if (bias && !ws) {
+      const int64_t col0 = n0 + wn + (BKC ? 16 * j + 4 * q : 4 * J * q + 4 * j);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) bias4[j][u] = col0 + u < N ? bias[col0 + u] : 0.0f;
+    }
+  }
+  v4f acc[I][J];
+#pragma unroll
+  for (int i = 0; i < I; ++i)
+#pragma unroll
+    for (int j = 0; j < J; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  // Sums over K of this lane's operand rows (SUMS): per MFMA block, the lane's K indices only.
+  constexpr int SN = SUMS == 1 ? I : SUMS == 2 ? J : 1;
+  float ksum[SN];
+#pragma unroll
+  for (int u = 0; u < SN; ++u) ksum[u] = 0.0f;
+  const bool sum_wave = SUMS == 1 ? wn == 0 : SUMS == 2 ? wm == 0 : false;
+  struct Frag { v4f a[KB][4], b[KB][4]; };
+  auto kc_at = [&](int r, int kq) { return (r / RPI) * 256 + (r % RPI) * BK + 4 * (kq ^ fsw(r)); };
+  auto read = [&](int tile, Frag& f) {
+    const float* As = smem + (tile % NS) * SS;
+    const float* Bs = As + SA;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      if (AKC) {
+#pragma unroll
+        for (int i = 0; i < I; ++i) f.a[kb][i] = *reinterpret_cast<const v4f*>(As + kc_at(wm + 16 * i + c, 4 * kb + q));
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const float* p = As + (16 * kb + 4 * q + s) * BM + wm + I * c;
+          if constexpr (I == 4) {
+            f.a[kb][s] = *reinterpret_cast<const v4f*>(p);
+          } else {
+            const float2 t2 = *reinterpret_cast<const float2*>(p);
+            f.a[kb][s] = v4f{t2.x, t2.y, 0.0f, 0.0f};
+          }
+        }
+      }
+      if (BKC) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) f.b[kb][j] = *reinterpret_cast<const v4f*>(Bs + kc_at(wn + 16 * j + c, 4 * kb + q));
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const float* p = Bs + (16 * kb + 4 * q + s) * BN + wn + J * c;
+          if constexpr (J == 4) {
+            f.b[kb][s] = *reinterpret_cast<const v4f*>(p);
+          } else {
+            const float2 t2 = *reinterpret_cast<const float2*>(p);
+            f.b[kb][s] = v4f{t2.x, t2.y, 0.0f, 0.0f};
+          }
+        }
+      }
+    }
+  };
+  auto mfma = [&](const Frag& f) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < I; ++i)
+#pragma unroll
+          for (int j = 0; j < J; ++j) {
+            const float a = AKC ? f.a[kb][i][s] : f.a[kb][s][i];
+            const float b = BKC ? f.b[kb][j][s] : f.b[kb][s][j];
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b, a, acc[i][j], 0, 0, 0);
+          }
+      if (SUMS != 0 && sum_wave) {
+#pragma unroll
+        for (int u = 0; u < SN; ++u)
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            ksum[u] += SUMS == 1 ? (AKC ? f.a[kb][u][s] : f.a[kb][s][u]) : (BKC ? f.b[kb][u][s] : f.b[kb][s][u]);
+      }
+    }
+  };
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p) issue(p);
+  if constexpr (!FP) {
+    // Tile t landed (the later tiles may still fly), then a bare barrier (a workgroup fence would
+    // wait for the prefetches too): every wave is past tile t - 1, whose stage takes tile t + NS - 1.
+    for (int t = 0; t < tiles; ++t) {
+      wait_vm((NS - 2) * LPT);
+      __builtin_amdgcn_s_barrier();
+      issue(t + NS - 1);
+      Frag f;
+      read(t, f);
+      mfma(f);
+    }
+  } else {
+    // Fragments one tile ahead: iteration t waits for tile t + 1 and reads its fragments, then
+    // multiplies tile t's, read in the iteration before.
+    static_assert(NS >= 3, "fragment prefetch needs three stages");
+    Frag f0, f1;
+    wait_vm((NS - 2) * LPT);
+    __builtin_amdgcn_s_barrier();
+    read(0, f0);
+    auto body = [&](int t, const Frag& cur, Frag& nxt) {
+      wait_vm((NS - 3) * LPT);
+      __builtin_amdgcn_s_barrier();
+      issue(t + NS - 1);
+      read(t + 1, nxt);
+      mfma(cur);
+    };
+    int t = 0;
+    for (; t + 2 <= tiles; t += 2) {
+      body(t, f0, f1);
+      body(t + 1, f1, f0);
+    }
+    if (t < tiles) mfma(f0);
+  }
+  wait_vm(0);  // no load may still write LDS when the block ends
+  float* out = ws ? ws + int64_t(tz) * M * N : ptrs.c[0];
+  const int64_t ldo = ws ? N : ldc, zto = ws ? N : zero_to;
+#pragma unroll
+  for (int i = 0; i < I; ++i) {
+    const int64_t row = m0 + wm + (AKC ? 16 * i + c : I * c + i);
+    if (row >= M) continue;
+    float* orow = out + row * ldo;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      int64_t col;
+      v4f v;
+      if (BKC) {
+        col = n0 + wn + 16 * j + 4 * q;
+        v = acc[i][j] + bias4[j];
+      } else {
+        // Columns wn + J (4 q + r) + jj: group j holds r = (4 j + u) / J, jj = (4 j + u) % J.
+        col = n0 + wn + 4 * J * q + 4 * j;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = acc[i][(4 * j + u) % J][(4 * j + u) / J];
+        v += bias4[j];
+      }
+      // The rest of the epilogue (activation or its gradient, addend, dropout gradient) after the
+      // bias, as the other kernel applies it.
+      const bool more = !ws && (epi.act != EPI_NONE || epi.addend || epi.drop_token);
+      if (vo && col + 3 < N) {
+        if (more) {
+          const float4 f = gemm_epilogue4(GemmEpi{nullptr, epi.addend, epi.pre_in, epi.pre_out, epi.act, epi.drop_token,
+                                                  epi.drop_threshold, epi.drop_scale, epi.drop_seed},
+                                          make_float4(v[0], v[1], v[2], v[3]), row, col, ldo);
+          v = v4f{f.x, f.y, f.z, f.w};
+        }
+        *reinterpret_cast<v4f*>(orow + col) = v;
+      } else {
+        const GemmEpi rest{nullptr, epi.addend, epi.pre_in, epi.pre_out, epi.act, epi.drop_token, epi.drop_threshold,
+                           epi.drop_scale, epi.drop_seed};
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (col + u < zto) orow[col + u] = col + u < N ? (more ? gemm_epilogue(rest, v[u], row, col + u, ldo) : v[u]) : 0.0f;
+      }
+    }
+  }
+  if constexpr (SUMS != 0) {
+    // The four lane groups q hold disjoint K indices: added across q (fixed order), then written by
+    // q = 0. Rows (SUMS 1): wm + 16 u + c (KC A) or wm + I c + u; columns (SUMS 2): wn + 16 u + c
+    // (KC B) or wn + J c + u.
+#pragma unroll
+    for (int u = 0; u < SN; ++u) {
+      ksum[u] += __shfl_xor(ksum[u], 16, 64);
+      ksum[u] += __shfl_xor(ksum[u], 32, 64);
+    }
+    if (sum_wave && q == 0 && colsum) {
+      const int64_t base = SUMS == 1 ? m0 + wm : n0 + wn, width = SUMS == 1 ? M : N;
+      constexpr bool kc = SUMS == 1 ? AKC : BKC;
+      constexpr int SPAN = SUMS == 1 ? I : J;
+      float* dst = colsum + (ws ? int64_t(tz) * width : 0);
+#pragma unroll
+      for (int u = 0; u < SN; ++u) {
+        const int64_t at = base + (kc ? 16 * u + c : SPAN * c + u);
+        if (at < width) dst[at] = ksum[u];
+      }
+    }
+  }
+}
+
+namespace {
+// Whether k_gemm_lds can read this problem with K tiles of bk: 16-byte aligned operands and rows;
+// a K tail only where every operand contiguous along K (KC) is zero-padded to the next multiple of
+// bk (an operand not contiguous along K has its K rows clamped, which only a zero partner
+// cancels), so both operands KC, or one KC and one clamped; the summed operand of a column sum
+// over a K tail KC (padding, not clamped rows); an operand contiguous along its rows whole groups
+// of 4 rows, or a pitch that holds the last group.
+bool lds_fits(const GemmArgs& g, int bk) {
+  const bool akc = !g.ta, bkc = g.tb;
+  auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (!a16(g.a) || !a16(g.b) || g.lda % 4 != 0 || g.ldb % 4 != 0) return false;
+  const int64_t kpad = (g.k + bk - 1) / bk * bk;
+  if (g.k % bk != 0) {
+    if (!akc && !bkc) return false;
+    if (akc && !(g.pad_a && g.lda >= kpad)) return false;
+    if (bkc && !(g.pad_b && g.ldb >= kpad)) return false;
+    if (g.colsum && !(g.sum_a ? akc : bkc)) return false;
+  }
+  auto rows_ok = [](bool kc, int64_t ld, int64_t extent) { return kc || extent % 4 == 0 || ld >= (extent + 3) / 4 * 4; };
+  return rows_ok(akc, g.lda, g.m) && rows_ok(bkc, g.ldb, g.n);
+}
+}  // namespace
+
+bool gemm_lds(hipStream_t s, const GemmArgs& g, const GemmPtrs& ptrs, int split, int64_t chunk) {
+  auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  float* ws = ptrs.ws[0];
+  const bool akc = !g.ta, bkc = g.tb;
+  const int lds_bk = akc && !bkc ? 32 : 16;
+  // Measured: faster for outputs of 2^21 or more (the decoder head, the FFN's 4096 x 512 products and
+  // their input gradients) and K of 8192 or more; slower for the K = 4096 weight gradients of
+  // 512 x 128 or smaller and the 4096 x 128 products. A cross-entropy head's fused variants (the
+  // gradient formed from the logits in the K loop) stay on k_gemm_w.
+  const bool lds = (g.m * g.n >= (int64_t(1) << 21) || g.k >= 8192) && chunk % lds_bk == 0 && lds_fits(g, lds_bk);
+  if (lds) {
+    // Tiles (measured on the decoder head shapes of BERT-tiny, 832 x 30522 x 128 and its two
+    // gradients): both operands KC 64 x 64, A KC 64 x 128 with eight waves and K tiles of 32,
+    // neither 128 x 128 (each wave 64 x 64: 16 accumulators).
+    const int bm = akc && bkc ? 64 : akc ? 64 : !bkc ? 128 : 64;
+    const int bn = akc && bkc ? 64 : akc ? 128 : !bkc ? 128 : 64;
+    const int64_t lmt = (g.m + bm - 1) / bm, lnt = (g.n + bn - 1) / bn;
+    const int64_t ltiles = lmt * lnt * split;
+    if (ltiles > (int64_t(1) << 30)) bad("gemm has too many tiles");
+    const GemmOrder lorder{uint32_t(lmt), uint32_t(lnt), uint32_t(ltiles), g.n * g.k >= g.m * g.k};
+    const dim3 lgrid(unsigned((ltiles + 7) / 8 * 8));
+    const bool lvo = ws ? (g.n % 4 == 0 && a16(ws))
+                        : (g.ldc % 4 == 0 && a16(g.c) && a16(g.addend) && a16(g.pre_in) && a16(g.pre_out));
+    const int64_t zero_to = g.pad_c ? g.ldc : g.n;
+    const int sums = g.colsum ? (g.sum_a ? 1 : 2) : 0;
+#define MSX_LDS(BM, BN, WGM, WGN, BK, AK, BKC_, NS, FP, S)                                                         \
+  MSX_LAUNCH((k_gemm_lds<BM, BN, WGM, WGN, BK, AK, BKC_, NS, FP, S>), lgrid, dim3(64 * WGM * WGN), 0, s, ptrs, g.m, \
+             g.n, g.k, g.lda, g.ldb, g.ldc, chunk, zero_to, lvo, lorder)
+#define MSX_LDS_S(BM, BN, WGM, WGN, BK, AK, BKC_, NS, FP)          \
+  if (sums == 1) MSX_LDS(BM, BN, WGM, WGN, BK, AK, BKC_, NS, FP, 1); \
+  else if (sums == 2) MSX_LDS(BM, BN, WGM, WGN, BK, AK, BKC_, NS, FP, 2); \
+  else MSX_LDS(BM, BN, WGM, WGN, BK, AK, BKC_, NS, FP, 0)
+    if (akc && bkc) { MSX_LDS_S(64, 64, 2, 2, 16, true, true, 3, true); }
+    else if (akc) { MSX_LDS_S(64, 128, 2, 4, 32, true, false, 3, true); }
+    else if (!bkc) { MSX_LDS_S(128, 128, 2, 2, 16, false, false, 3, false); }
+    else { MSX_LDS_S(64, 64, 2, 2, 16, false, true, 3, true); }
+#undef MSX_LDS_S
+#undef MSX_LDS
+    return true;
+  }
+  return false;
+}
+
+}  // namespace msx::hk
