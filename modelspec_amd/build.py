@@ -41,6 +41,11 @@ FLAGS = [
 ]
 
 
+# Per-source flags. The direct-to-LDS GEMMs keep their MFMA accumulators in VGPRs: with the
+# compiler's default choice (AGPRs) it rotated the accumulators through copies every K tile.
+FILE_FLAGS = {"hip/gemm_lds.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def build(verbose=False):
     objs = []
     build_dir = os.path.join(HERE, "_build")
@@ -50,7 +55,7 @@ def build(verbose=False):
         path = os.path.join(CSRC, src)
         obj = os.path.join(build_dir, src.replace("/", "_") + ".o")
         lang = ["-x", "hip"] if src.endswith((".hip", "runtime.cpp", "capi.cpp")) else []
-        cmd = [HIPCC] + [f for f in FLAGS if f != "-shared"] + ["-c"] + lang + [path, "-o", obj]
+        cmd = [HIPCC] + [f for f in FLAGS if f != "-shared"] + FILE_FLAGS.get(src, []) + ["-c"] + lang + [path, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
@@ -62,7 +67,7 @@ def build(verbose=False):
         if not src.endswith(".hip"):
             continue
         out = os.path.join(CODE_OBJECTS, os.path.basename(src).replace(".hip", ".hsaco"))
-        cmd = ([HIPCC] + [f for f in FLAGS if f not in ("-shared", "-fPIC")] +
+        cmd = ([HIPCC] + [f for f in FLAGS if f not in ("-shared", "-fPIC")] + FILE_FLAGS.get(src, []) +
                ["--genco", "--offload-device-only", "--no-gpu-bundle-output", os.path.join(CSRC, src), "-o", out])
         procs.append((src + " (code object)", subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
     failed = []

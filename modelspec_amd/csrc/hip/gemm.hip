@@ -19,7 +19,8 @@ constexpr int kSliceAlign = 32;  // split-K slices are multiples of this many K 
 template <int SPLIT>
 __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ ws, float* __restrict__ C, GemmEpi epi,
                                                     int64_t M, int64_t N, int64_t ldc, int splits,
-                                                    float* __restrict__ colsum, int64_t width) {
+                                                    float* __restrict__ colsum, int64_t width,
+                                                    _Float16* __restrict__ C16) {
   const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
   const int64_t mn = M * N;
   const bool cs = e >= mn;
@@ -40,7 +41,9 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ ws
     colsum[e - mn] = s;
   } else {
     const int64_t row = e / N, col = e - row * N;
-    C[row * ldc + col] = gemm_epilogue(epi, s, row, col, ldc);
+    const float v = gemm_epilogue(epi, s, row, col, ldc);
+    if (C) C[row * ldc + col] = v;
+    if (C16) C16[row * ldc + col] = _Float16(v);
   }
 }
 
@@ -540,6 +543,11 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
     ptrs.colsum[q] = o.colsum ? (ws ? ws + int64_t(split) * o.m * o.n : o.colsum) : nullptr;
     ptrs.ce_part[q] = o.ce_part;
     ptrs.ce_tab[q] = o.ce_tab;
+    ptrs.a16[q] = o.a16;
+    ptrs.b16[q] = o.b16;
+    ptrs.c16[q] = o.c16;
+    if ((o.a16 || o.b16 || o.c16) && !o.h16) bad("f16 operand copies outside mixed precision");
+    if (o.c16 && o.defer) bad("a deferred split-K output has no f16 copy");
   }
   ptrs.ce_cols = g.ce_cols;
   ptrs.ksegs = ksegs;
@@ -629,9 +637,13 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
   if (plan.wm == 2) MSX_KS_V(TA, TB, 2, 2, 16);             \
   else if (plan.wn == 2) MSX_KS_V(TA, TB, 1, 2, 16);        \
   else MSX_KS_V(TA, TB, 1, 1, 32);
-  // The large f32 shapes take k_gemm_lds when their layout allows it (gemm_lds.hip).
+  // The large f32 shapes take k_gemm_lds when their layout allows it, mixed-precision GEMMs whose
+  // operands both have f16 copies k_gemm_lds16 (gemm_lds.hip).
+  bool f16_out = false;  // the launched kernel writes the f16 output copies itself
   const bool lds = !g.h16 && ksegs == 1 && count == 1 && !ce && gemm_lds(s, g, ptrs, split, chunk);
-  if (lds) {
+  const bool lds16 = !lds && g.h16 && ksegs == 1 && !ce && gemm_lds16(s, list, count, ptrs, split, chunk);
+  if (lds16) f16_out = true;
+  if (lds || lds16) {
     // launched
   } else if (ksegs > 1) {
     if (!va || !vb || g.h16) bad("K segments need aligned f32 operands");
@@ -669,12 +681,16 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
     const int64_t total = g.m * g.n + (g.colsum ? width : 0);
     const unsigned blocks = unsigned((total + 255) / 256);
 #define MSX_SPLITK(S) MSX_LAUNCH(k_splitk_sum<S>, dim3(blocks), dim3(256), 0, s, ws, g.c, epi, g.m, g.n, g.ldc, \
-                                         split, g.colsum, width)
+                                         split, g.colsum, width, g.c16)
     if (split <= 8) MSX_SPLITK(8);
     else if (split <= 16) MSX_SPLITK(16);
     else MSX_SPLITK(32);
 #undef MSX_SPLITK
+    f16_out = true;
   }
+  // f16 output copies a kernel did not write: rounded from the f32 output.
+  for (int q = 0; q < count && !f16_out; ++q)
+    if (list[q].c16) to_f16_rows(s, list[q].c, list[q].ldc, list[q].c16, list[q].ldc, list[q].m, list[q].n);
 }
 
 }  // namespace msx::hk

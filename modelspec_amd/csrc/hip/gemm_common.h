@@ -78,5 +78,9 @@ struct GemmOrder {
 // with the caller's split-K slices (`split` slices of `chunk` K, partials in ptrs.ws[0]) when its
 // shape and layout suit it; returns false, launching nothing, otherwise.
 bool gemm_lds(hipStream_t s, const GemmArgs& g, const GemmPtrs& ptrs, int split, int64_t chunk);
+// The same for a mixed-precision group whose operands all have f16 copies (GemmArgs::a16, b16):
+// the f16 kernel reads them straight into LDS; it writes the f32 output (or split-K partials) and
+// the f16 output copies asked for.
+bool gemm_lds16(hipStream_t s, const GemmArgs* list, int count, const GemmPtrs& ptrs, int split, int64_t chunk);
 
 }  // namespace msx::hk

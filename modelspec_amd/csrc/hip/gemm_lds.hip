@@ -337,6 +337,235 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds(GemmPtrs ptrs, int6
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// The mixed-precision GEMM on f16 operands in HBM (k_gemm_lds16): K tiles of 32 halves move straight
+// into a 3-stage LDS ring as in k_gemm_lds, and v_mfma_f32_16x16x32_f16 takes 8 consecutive K of a
+// row a lane, f32 accumulation.
+//   - An operand contiguous along K (KC) is staged [row][32 K]: 64 bytes a row, its 16-byte chunk
+//     kq at slot kq ^ ((row >> 2) & 3), so the 16 rows a quarter-wave reads at one chunk hit
+//     distinct banks; lane (c, q) reads row c's chunk q with one 16-byte read.
+//   - An operand contiguous along its rows is staged [K][rows] as in memory, the 16-byte chunk ch of
+//     K row k at ch ^ 2 (k mod 4) within its group of 8 (128 bytes). A lane's 8 K of one row come
+//     from two ds_read_b64_tr_b16: in each 16-lane group, source lane l reads 4 rows x 1 K (8 bytes)
+//     at K row k0 + l / 4, rows base + 4 (l mod 4) .. + 3, and after the transpose lane c holds row
+//     base + c at K k0 .. k0 + 3.
+// Lane (c, q) thus supplies row c of its 16-row block at K 8q .. 8q + 7 in both layouts, and holds
+// output rows 16 i + c, columns 16 j + 4 q .. + 3 (the MFMA takes B's fragment first: C^T tiles).
+// K must be a multiple of 32, or the K-contiguous operands zero-padded to it; the K rows of an
+// operand along its rows are clamped to the last (their products with the padding vanish).
+namespace {
+typedef short v4s16 __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h16 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint32_t lds_at(const _Float16* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
+}
+// Eight transposed reads (four 16-row fragments of 8 halves) and the wait for them, as one block of
+// inline assembly: through the builtin the compiler waits for every global->LDS load in flight
+// (vmcnt(0), the prefetches too) before each transposed read, and separate asm reads would let it
+// use their registers before the data arrives.
+__device__ __forceinline__ void tr_read16x8(const uint32_t (&at)[8], v4s16 (&r)[8]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8\n"
+      "ds_read_b64_tr_b16 %1, %9\n"
+      "ds_read_b64_tr_b16 %2, %10\n"
+      "ds_read_b64_tr_b16 %3, %11\n"
+      "ds_read_b64_tr_b16 %4, %12\n"
+      "ds_read_b64_tr_b16 %5, %13\n"
+      "ds_read_b64_tr_b16 %6, %14\n"
+      "ds_read_b64_tr_b16 %7, %15\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+      : "v"(at[0]), "v"(at[1]), "v"(at[2]), "v"(at[3]), "v"(at[4]), "v"(at[5]), "v"(at[6]), "v"(at[7])
+      : "memory");
+#endif
+}
+}  // namespace
+
+template <int BM, int BN, int WGM, int WGN, bool AKC, bool BKC, int NS>
+__global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, int64_t M, int64_t N, int64_t K,
+                                                               int64_t lda, int64_t ldb, int64_t ldc, int64_t kchunk,
+                                                               int64_t zero_to, bool vo, GemmOrder order) {
+  constexpr int BK = 32, W = WGM * WGN;
+  constexpr int WTM = BM / WGM, WTN = BN / WGN, I = WTM / 16, J = WTN / 16;
+  static_assert(I >= 1 && J >= 1 && WTM % 16 == 0 && WTN % 16 == 0, "16-row MFMA blocks");
+  constexpr int SA = BM * BK, SB = BN * BK, SS = SA + SB;  // halves a stage
+  constexpr int LA = SA / 512, LB = SB / 512;               // 1 KB wave load instructions a tile
+  static_assert(LA % W == 0 && LB % W == 0, "whole load instructions a wave");
+  constexpr int PA = LA / W, PB = LB / W, LPT = PA + PB;
+  __shared__ __align__(16) _Float16 smem[NS * SS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 15, q = lane >> 4;
+  const uint32_t per = gridDim.x / 8, tg = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (tg >= order.tiles * uint32_t(ptrs.count)) return;
+  // The problem of the group, then its tile.
+  const int qp = int(tg / order.tiles);
+  const uint32_t t0 = tg - uint32_t(qp) * order.tiles;
+  const uint32_t tz = t0 / (order.mt * order.nt), tr = t0 % (order.mt * order.nt);
+  const uint32_t tm = order.m_fastest ? tr % order.mt : tr / order.nt;
+  const uint32_t tn = order.m_fastest ? tr / order.mt : tr % order.nt;
+  const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
+  const int64_t kpad = (K + BK - 1) / BK * BK;
+  const int64_t kbeg = int64_t(tz) * kchunk, kend = kpad < kbeg + kchunk ? kpad : kbeg + kchunk;
+  const int tiles = int((kend - kbeg) / BK);
+  const int wm = (wave / WGN) * WTM, wn = (wave % WGN) * WTN;
+  const _Float16* __restrict__ A = ptrs.a16[qp];
+  const _Float16* __restrict__ B = ptrs.b16[qp];
+  const GemmEpi epi = ptrs.epi[qp];
+  float* __restrict__ ws = ptrs.ws[qp];
+  const int64_t kmax = K - 1;
+  const _Float16* srcA[PA];
+  const _Float16* srcB[PB];
+  int kofA[PA], kofB[PB];
+#pragma unroll
+  for (int h = 0; h < PA; ++h) {
+    const int t = wave * PA + h;
+    if (AKC) {
+      const int r = t * 16 + lane / 4, ch = (lane % 4) ^ ((r >> 2) & 3);
+      const int64_t row = m0 + r < M ? m0 + r : M - 1;
+      srcA[h] = A + row * lda + kbeg + 8 * ch;
+      kofA[h] = 0;
+    } else {
+      constexpr int RQ = BM / 8, KR = 512 / BM;
+      const int kr = t * KR + lane / RQ, slot = lane % RQ;
+      const int ch = (slot & ~7) | ((slot & 7) ^ (2 * (kr & 3)));
+      int64_t col = m0 + 8 * ch;
+      col = col < M ? col : ((M - 1) & ~int64_t(7));
+      srcA[h] = A + col;
+      kofA[h] = kr;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < PB; ++h) {
+    const int t = wave * PB + h;
+    if (BKC) {
+      const int r = t * 16 + lane / 4, ch = (lane % 4) ^ ((r >> 2) & 3);
+      const int64_t row = n0 + r < N ? n0 + r : N - 1;
+      srcB[h] = B + row * ldb + kbeg + 8 * ch;
+      kofB[h] = 0;
+    } else {
+      constexpr int RQ = BN / 8, KR = 512 / BN;
+      const int kr = t * KR + lane / RQ, slot = lane % RQ;
+      const int ch = (slot & ~7) | ((slot & 7) ^ (2 * (kr & 3)));
+      int64_t col = n0 + 8 * ch;
+      col = col < N ? col : ((N - 1) & ~int64_t(7));
+      srcB[h] = B + col;
+      kofB[h] = kr;
+    }
+  }
+  auto issue = [&](int tile) {
+    tile = tile < tiles ? tile : tiles - 1;
+    _Float16* st = smem + (tile % NS) * SS;
+    const int64_t k0 = int64_t(tile) * BK;
+#pragma unroll
+    for (int h = 0; h < PA; ++h) {
+      const int t = wave * PA + h;
+      const int64_t kr = kbeg + k0 + kofA[h];
+      const _Float16* src = AKC ? srcA[h] + k0 : srcA[h] + (kr < kmax ? kr : kmax) * lda;
+      load_lds16(reinterpret_cast<const float*>(src), reinterpret_cast<float*>(st + t * 512));
+    }
+#pragma unroll
+    for (int h = 0; h < PB; ++h) {
+      const int t = wave * PB + h;
+      const int64_t kr = kbeg + k0 + kofB[h];
+      const _Float16* src = BKC ? srcB[h] + k0 : srcB[h] + (kr < kmax ? kr : kmax) * ldb;
+      load_lds16(reinterpret_cast<const float*>(src), reinterpret_cast<float*>(st + SA + t * 512));
+    }
+  };
+  v4f acc[I][J];
+#pragma unroll
+  for (int i = 0; i < I; ++i)
+#pragma unroll
+    for (int j = 0; j < J; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  auto kc_frag = [&](const _Float16* S, int r) {
+    return *reinterpret_cast<const v8h*>(S + r * 32 + 8 * (q ^ ((r >> 2) & 3)));
+  };
+  // The LDS address of the transposed read hh (K 8q + 4hh ..) of the 16 rows from base.
+  auto tr_at = [&](const _Float16* S, int R, int base, int hh) {
+    const int k = 8 * q + 4 * hh + c / 4;
+    const int row = base + 4 * (c % 4);
+    const int ch = row / 8, slot = (ch & ~7) | ((ch & 7) ^ (2 * (k & 3)));
+    return lds_at(S + k * R + slot * 8 + (row % 8));
+  };
+  // Four 16-row fragments of an operand along its rows (rows base0 + 16 u).
+  auto tr_frags = [&](const _Float16* S, int R, int base0, v8h (&out)[4]) {
+    uint32_t at[8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      at[2 * u] = tr_at(S, R, base0 + 16 * u, 0);
+      at[2 * u + 1] = tr_at(S, R, base0 + 16 * u, 1);
+    }
+    v4s16 r[8];
+    tr_read16x8(at, r);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const v4h16 lo = __builtin_bit_cast(v4h16, r[2 * u]), hi = __builtin_bit_cast(v4h16, r[2 * u + 1]);
+      out[u] = v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+  };
+  static_assert((AKC || I == 4) && (BKC || J == 4), "an operand along its rows takes four 16-row fragments a wave");
+  struct Frag { v8h a[I], b[J]; };
+  auto read = [&](int tile, Frag& f) {
+    const _Float16* As = smem + (tile % NS) * SS;
+    const _Float16* Bs = As + SA;
+    if constexpr (AKC) {
+#pragma unroll
+      for (int i = 0; i < I; ++i) f.a[i] = kc_frag(As, wm + 16 * i + c);
+    } else {
+      tr_frags(As, BM, wm, f.a);
+    }
+    if constexpr (BKC) {
+#pragma unroll
+      for (int j = 0; j < J; ++j) f.b[j] = kc_frag(Bs, wn + 16 * j + c);
+    } else {
+      tr_frags(Bs, BN, wn, f.b);
+    }
+  };
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p) issue(p);
+#pragma unroll 1
+  for (int t = 0; t < tiles; ++t) {
+    wait_vm((NS - 2) * LPT);
+    __builtin_amdgcn_s_barrier();
+    issue(t + NS - 1);
+    Frag f;
+    read(t, f);
+#pragma unroll
+    for (int i = 0; i < I; ++i)
+#pragma unroll
+      for (int j = 0; j < J; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
+  }
+  wait_vm(0);  // no load may still write LDS when the block ends
+  float* out = ws ? ws + int64_t(tz) * M * N : ptrs.c[qp];
+  _Float16* out16 = ws ? nullptr : ptrs.c16[qp];
+  const int64_t ldo = ws ? N : ldc, zto = ws ? N : zero_to;
+  const bool more = !ws && (epi.bias || epi.act != EPI_NONE || epi.addend || epi.drop_token);
+#pragma unroll
+  for (int i = 0; i < I; ++i) {
+    const int64_t row = m0 + wm + 16 * i + c;
+    if (row >= M) continue;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int64_t col = n0 + wn + 16 * j + 4 * q;
+      float4 v = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      if (vo && col + 3 < N) {
+        if (more) v = gemm_epilogue4(epi, v, row, col, ldo);
+        if (out) *reinterpret_cast<float4*>(out + row * ldo + col) = v;
+        if (out16)
+          *reinterpret_cast<v4h16*>(out16 + row * ldo + col) = v4h16{_Float16(v.x), _Float16(v.y), _Float16(v.z), _Float16(v.w)};
+      } else {
+        const float vs[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (col + u >= zto) continue;
+          const float x = col + u < N ? (more ? gemm_epilogue(epi, vs[u], row, col + u, ldo) : vs[u]) : 0.0f;
+          if (out) out[row * ldo + col + u] = x;
+          if (out16) out16[row * ldo + col + u] = _Float16(x);
+        }
+      }
+    }
+  }
+}
+
 namespace {
 // Whether k_gemm_lds can read this problem with K tiles of bk: 16-byte aligned operands and rows;
 // a K tail only where every operand contiguous along K (KC) is zero-padded to the next multiple of
@@ -401,6 +630,48 @@ bool gemm_lds(hipStream_t s, const GemmArgs& g, const GemmPtrs& ptrs, int split,
     return true;
   }
   return false;
+}
+
+bool gemm_lds16(hipStream_t s, const GemmArgs* list, int count, const GemmPtrs& ptrs, int split, int64_t chunk) {
+  constexpr int BK = 32;
+  const GemmArgs& g = list[0];
+  auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  const bool akc = !g.ta, bkc = g.tb;
+  const int64_t kpad = (g.k + BK - 1) / BK * BK;
+  if (g.colsum || chunk % BK != 0) return false;
+  for (int q = 0; q < count; ++q) {
+    const GemmArgs& o = list[q];
+    if (!o.a16 || !o.b16 || !a16(o.a16) || !a16(o.b16) || o.lda % 8 != 0 || o.ldb % 8 != 0) return false;
+    // A K tail only over zero padding of the K-contiguous operands (the other kind is clamped).
+    if (o.k % BK != 0 && ((!akc && !bkc) || (akc && !(o.pad_a && o.lda >= kpad)) || (bkc && !(o.pad_b && o.ldb >= kpad))))
+      return false;
+    // An operand along its rows: whole 8-row chunks, or a pitch that holds the last one.
+    if (!akc && o.m % 8 != 0 && o.lda < (o.m + 7) / 8 * 8) return false;
+    if (!bkc && o.n % 8 != 0 && o.ldb < (o.n + 7) / 8 * 8) return false;
+  }
+  constexpr int BM = 128, BN = 128;
+  const int64_t lmt = (g.m + BM - 1) / BM, lnt = (g.n + BN - 1) / BN;
+  const int64_t ltiles = lmt * lnt * split;
+  if (ltiles * count > (int64_t(1) << 30)) bad("gemm has too many tiles");
+  const GemmOrder lorder{uint32_t(lmt), uint32_t(lnt), uint32_t(ltiles), g.n * g.k >= g.m * g.k};
+  const dim3 lgrid(unsigned((ltiles * count + 7) / 8 * 8));
+  bool vo = true;
+  for (int q = 0; q < count; ++q) {
+    const GemmArgs& o = list[q];
+    vo = vo && (ptrs.ws[q] ? (o.n % 4 == 0 && a16(ptrs.ws[q]))
+                           : (o.ldc % 4 == 0 && a16(o.c) && a16(o.c16) && a16(o.bias) && a16(o.addend) && a16(o.pre_in) &&
+                              a16(o.pre_out)));
+  }
+  const int64_t zero_to = g.pad_c ? g.ldc : g.n;
+#define MSX_L16(AK, BKC_)                                                                                      \
+  MSX_LAUNCH((k_gemm_lds16<BM, BN, 2, 2, AK, BKC_, 3>), lgrid, dim3(256), 0, s, ptrs, g.m, g.n, g.k, g.lda, g.ldb, \
+             g.ldc, chunk, zero_to, vo, lorder)
+  if (akc && bkc) MSX_L16(true, true);
+  else if (akc) MSX_L16(true, false);
+  else if (bkc) MSX_L16(false, true);
+  else MSX_L16(false, false);
+#undef MSX_L16
+  return true;
 }
 
 }  // namespace msx::hk

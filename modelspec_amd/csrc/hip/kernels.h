@@ -27,6 +27,8 @@ void elementwise2(hipStream_t s, int op1, const float* a, const float* b, int op
                   float* o, int64_t n);
 void fill_from(hipStream_t s, const float* scalar, float* o, int64_t n);  // BroadcastScalar
 void fill_zero(hipStream_t s, void* o, int64_t bytes);                     // kernel, not a memset
+// y[r, c] = f16(x[r, c]) (round to nearest even) for r < rows, c < cols; rows ldx / ldy apart.
+void to_f16_rows(hipStream_t s, const float* x, int64_t ldx, _Float16* y, int64_t ldy, int64_t rows, int64_t cols);
 void copy(hipStream_t s, const float* a, float* o, int64_t n);
 
 // C[M,N] = op(A) op(B) (+ bias[N]); A is [M,K] row-major with leading dimension lda, or [K,M]
@@ -70,6 +72,13 @@ struct GemmArgs {
   const float4* ce_tab;
   int ce_operand;
   int64_t ce_cols;
+  // Mixed precision with f16 operands in HBM: with both a16 and b16 set (the operands' f16 copies,
+  // same layouts and leading dimensions as a and b), the GEMM reads them instead of a and b
+  // (k_gemm_lds16: no rounding at load). c16, when set, receives the output (after the epilogue)
+  // rounded to f16 as well, at ldc.
+  const _Float16* a16;
+  const _Float16* b16;
+  _Float16* c16;
   // K segments: with ksegs > 1 the product is the sum over s < ksegs of seg_a[s] seg_b[s], each
   // pair of the shape (m, k / ksegs, n) with a and b's transposes and leading dimensions, as one
   // contraction over k (a chain of like GEMMs added into one value); a and b are ignored then.
@@ -89,6 +98,9 @@ struct GemmPtrs {
   const float* a[kGemmGroupMax];
   const float* b[kGemmGroupMax];
   float* c[kGemmGroupMax];
+  const _Float16* a16[kGemmGroupMax];
+  const _Float16* b16[kGemmGroupMax];
+  _Float16* c16[kGemmGroupMax];
   GemmEpi epi[kGemmGroupMax];
   float* ws[kGemmGroupMax];
   float* colsum[kGemmGroupMax];
@@ -139,7 +151,8 @@ void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_
               float din_scale, const float* gamma, const float* beta, float* s_out, float* y_out, float* stats,
               const int32_t* dout_token, uint64_t dout_threshold, float dout_scale, float* yd_out, int64_t rows,
               int64_t h, uint64_t seed, const int32_t* gather = nullptr, int64_t src_rows = 0,
-              const int32_t* a_ids = nullptr, int64_t a_rows = 0, const int32_t* b_ids = nullptr, int64_t b_rows = 0);
+              const int32_t* a_ids = nullptr, int64_t a_rows = 0, const int32_t* b_ids = nullptr, int64_t b_rows = 0,
+              _Float16* y16 = nullptr, _Float16* yd16 = nullptr);  // f16 copies of y and yd
 
 // LayerNorm backward in one pass: dx when non-null, and when `partial` is non-null the per-block
 // partial sums [ln_backward_blocks, 2 h] of g * xhat (gamma gradient) then g (beta gradient), to be
@@ -151,7 +164,8 @@ enum LnbPost : int { LNB_DROPOUT, LNB_GELU_GRAD, LNB_RELU_GRAD };
 int64_t ln_backward_blocks(int64_t rows, int64_t h);
 void ln_backward(hipStream_t s, const float* x, const float* gamma, const float* g, const float* stats, float* dx,
                  float* partial, int64_t rows, int64_t h, float* dx2 = nullptr, int post = 0, const float* pre = nullptr,
-                 const int32_t* token = nullptr, uint64_t threshold = 0, float scale = 1.0f, uint64_t seed = 0);
+                 const int32_t* token = nullptr, uint64_t threshold = 0, float scale = 1.0f, uint64_t seed = 0,
+                 _Float16* dx16 = nullptr, _Float16* dx2_16 = nullptr);  // f16 copies of dx and dx2
 
 // Sums of block partials [chunks, width] over the blocks, columns below `split` to out_lo and the
 // rest to out_hi; up to kColumnJobs reductions a launch (`first` is set by column_finalize).

@@ -98,6 +98,37 @@ void fill_zero(hipStream_t s, void* o, int64_t bytes) {
                      static_cast<uint32_t*>(o), words);
 }
 
+__global__ __launch_bounds__(256) void k_to_f16_rows(const float* __restrict__ x, int64_t ldx, _Float16* __restrict__ y,
+                                                     int64_t ldy, int64_t rows, int64_t cols) {
+  const int64_t n = rows * cols;
+  for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < n; e += int64_t(gridDim.x) * 256) {
+    const int64_t r = e / cols, c = e - r * cols;
+    y[r * ldy + c] = _Float16(x[r * ldx + c]);
+  }
+}
+// Rows of whole 16-byte groups: block (x, y) converts groups 256 x + t of rows y, y + gridDim.y, ...
+__global__ __launch_bounds__(256) void k_to_f16_rows4(const float* __restrict__ x, int64_t ldx, _Float16* __restrict__ y,
+                                                      int64_t ldy, int64_t rows, int64_t groups) {
+  const int64_t gq = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (gq >= groups) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const v4f v = *reinterpret_cast<const v4f*>(x + r * ldx + 4 * gq);
+    *reinterpret_cast<v4h*>(y + r * ldy + 4 * gq) = v4h{_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
+  }
+}
+void to_f16_rows(hipStream_t s, const float* x, int64_t ldx, _Float16* y, int64_t ldy, int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return;
+  if (cols % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(y) % 8 == 0 && cols / 4 <= int64_t(256) * 2147483647) {
+    const int64_t groups = cols / 4;
+    MSX_LAUNCH(k_to_f16_rows4, dim3(blocks_for(groups, 256), unsigned(std::min<int64_t>(rows, 65535))), dim3(256), 0, s, x,
+               ldx, y, ldy, rows, groups);
+    return;
+  }
+  MSX_LAUNCH(k_to_f16_rows, dim3(std::min<unsigned>(blocks_for(rows * cols, 256), 16384)), dim3(256), 0, s, x, ldx, y, ldy,
+             rows, cols);
+}
+
 // ---------------------------------------------------------------------------------------------
 __global__ void k_transpose(const float* __restrict__ a, float* __restrict__ o, int64_t rows, int64_t cols) {
   __shared__ float t[32][33];
@@ -249,6 +280,9 @@ void layer_norm(hipStream_t s, const float* x, const float* gamma, const float* 
   MSX_LAUNCH(k_layer_norm, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, gamma, beta, y, stats, rows, h);
 }
 
+// f16 copies a kernel writes beside two of its f32 outputs (mixed precision: GEMM operands).
+struct Out16 { _Float16* a; _Float16* b; };
+
 // LayerNorm with its neighbours in one pass, a wave a row: s = [a +] [dropout](b), y = LN(s) (the
 // arithmetic of k_layer_norm), optionally yd = dropout(y); s, y, yd and the statistics each
 // written when asked. The dropout keep rule is k_dropout's (Philox word 0 of the element index).
@@ -256,6 +290,7 @@ void layer_norm(hipStream_t s, const float* x, const float* gamma, const float* 
 // (an Embedding of the sum: element indices are the source rows'; an id out of range gives 0).
 // With `ga` (`gb`), a (b) is itself an Embedding: row r of a is row ga.ids[r] of the table `a`, 0
 // for an id outside [0, ga.rows) (k_embedding's rule), and the gathered rows are not written.
+// o16 (mixed precision): f16 copies of y (a) and yd (b), written when non-null.
 struct DropoutSpec { const int32_t* token; uint64_t threshold; float scale; };
 struct RowGather { const int32_t* ids; int64_t rows; };
 template <int CPL>
@@ -265,7 +300,7 @@ __global__ __launch_bounds__(256) void k_ln_fused(const float* __restrict__ a, c
                                                   float* __restrict__ y_out, float* __restrict__ stats,
                                                   DropoutSpec dout, float* __restrict__ yd_out, int64_t rows, int64_t h,
                                                   uint32_t seed_lo, uint32_t seed_hi, const int32_t* __restrict__ gather,
-                                                  int64_t src_rows, RowGather ga, RowGather gb) {
+                                                  int64_t src_rows, RowGather ga, RowGather gb, Out16 o16) {
   const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
@@ -309,8 +344,13 @@ __global__ __launch_bounds__(256) void k_ln_fused(const float* __restrict__ a, c
     const float y = (sv[j] - mean) * rstd * gamma[c] + beta[c];
     if (s_out) s_out[i] = sv[j];
     if (y_out) y_out[i] = y;
-    if (yd_out)
-      yd_out[i] = uint64_t(philox_w0(uint32_t(i), 4u, ol, oh, seed_lo, seed_hi)) >= dout.threshold ? y * dout.scale : 0.0f;
+    if (o16.a) o16.a[i] = _Float16(y);
+    if (yd_out || o16.b) {
+      const float yd =
+          uint64_t(philox_w0(uint32_t(i), 4u, ol, oh, seed_lo, seed_hi)) >= dout.threshold ? y * dout.scale : 0.0f;
+      if (yd_out) yd_out[i] = yd;
+      if (o16.b) o16.b[i] = _Float16(yd);
+    }
   }
   if (stats && lane == 0) { stats[2 * row] = mean; stats[2 * row + 1] = rstd; }
 }
@@ -318,7 +358,7 @@ void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_
               float din_scale, const float* gamma, const float* beta, float* s_out, float* y_out, float* stats,
               const int32_t* dout_token, uint64_t dout_threshold, float dout_scale, float* yd_out, int64_t rows,
               int64_t h, uint64_t seed, const int32_t* gather, int64_t src_rows, const int32_t* a_ids, int64_t a_rows,
-              const int32_t* b_ids, int64_t b_rows) {
+              const int32_t* b_ids, int64_t b_rows, _Float16* y16, _Float16* yd16) {
   if (rows <= 0 || h <= 0) return;
   if (!gather) src_rows = rows;
   if ((a_ids || b_ids) && (gather || din_token)) bad("fused LayerNorm: gathered operands with a row gather or an input dropout");
@@ -328,7 +368,7 @@ void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_
   const int cpl = int((h + 63) / 64);
 #define MSX_LNF(C) MSX_LAUNCH(k_ln_fused<C>, dim3(blocks_for(rows, 4)), dim3(256), 0, s, a, b, din, gamma, beta, s_out, y_out, \
                               stats, dout, yd_out, rows, h, uint32_t(seed), uint32_t(seed >> 32), gather, src_rows, \
-                              RowGather{a_ids, a_rows}, RowGather{b_ids, b_rows})
+                              RowGather{a_ids, a_rows}, RowGather{b_ids, b_rows}, Out16{y16, yd16})
   if (cpl <= 1) MSX_LNF(1);
   else if (cpl <= 2) MSX_LNF(2);
   else if (cpl <= 4) MSX_LNF(4);
@@ -347,7 +387,7 @@ __global__ __launch_bounds__(256) void k_ln_backward(const float* __restrict__ x
                                                      float* __restrict__ dx, float* __restrict__ partial, int64_t rows,
                                                      int64_t h, int64_t rows_per, float* __restrict__ dx2, int post,
                                                      const float* __restrict__ pre, DropoutSpec dsp, uint32_t seed_lo,
-                                                     uint32_t seed_hi) {
+                                                     uint32_t seed_hi, Out16 o16) {
   extern __shared__ float red[];  // [4 waves][2 h]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t r0 = int64_t(blockIdx.x) * rows_per, r1 = std::min<int64_t>(rows, r0 + rows_per);
@@ -379,7 +419,7 @@ __global__ __launch_bounds__(256) void k_ln_backward(const float* __restrict__ x
       pg[j] += gv[j] * xhat;
       pb[j] += gv[j];
     }
-    if (dx || dx2) {
+    if (dx || dx2 || o16.a || o16.b) {
       const float mean_gx = wave_sum(s1) / width, mean_gx_xhat = wave_sum(s2) / width;
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
@@ -390,16 +430,20 @@ __global__ __launch_bounds__(256) void k_ln_backward(const float* __restrict__ x
           const int64_t i = row * h + c;
           const float v = rstd * ((gx - mean_gx) - xhat * mean_gx_xhat);
           if (dx) dx[i] = v;
-          if (dx2) {
+          if (o16.a) o16.a[i] = _Float16(v);
+          if (dx2 || o16.b) {
+            float w;
             if (post == LNB_DROPOUT)
-              dx2[i] = uint64_t(philox_w0(uint32_t(i), 4u, uint32_t(dsp.token[0]), uint32_t(dsp.token[1]), seed_lo, seed_hi)) >=
-                               dsp.threshold
-                           ? v * dsp.scale
-                           : 0.0f;
+              w = uint64_t(philox_w0(uint32_t(i), 4u, uint32_t(dsp.token[0]), uint32_t(dsp.token[1]), seed_lo, seed_hi)) >=
+                          dsp.threshold
+                      ? v * dsp.scale
+                      : 0.0f;
             else if (post == LNB_GELU_GRAD)
-              dx2[i] = d_gelu_grad(pre[i], v);
+              w = d_gelu_grad(pre[i], v);
             else
-              dx2[i] = pre[i] > 0.0f ? v : 0.0f;
+              w = pre[i] > 0.0f ? v : 0.0f;
+            if (dx2) dx2[i] = w;
+            if (o16.b) o16.b[i] = _Float16(w);
           }
         }
       }
@@ -430,9 +474,10 @@ int64_t ln_backward_blocks(int64_t rows, int64_t h) {
 }
 void ln_backward(hipStream_t s, const float* x, const float* gamma, const float* g, const float* stats, float* dx,
                  float* partial, int64_t rows, int64_t h, float* dx2, int post, const float* pre,
-                 const int32_t* token, uint64_t threshold, float scale, uint64_t seed) {
-  if (dx2 && post == LNB_DROPOUT && !token) bad("LayerNorm backward dropout without its token");
-  if (dx2 && post != LNB_DROPOUT && !pre) bad("LayerNorm backward activation gradient without its input");
+                 const int32_t* token, uint64_t threshold, float scale, uint64_t seed, _Float16* dx16,
+                 _Float16* dx2_16) {
+  if ((dx2 || dx2_16) && post == LNB_DROPOUT && !token) bad("LayerNorm backward dropout without its token");
+  if ((dx2 || dx2_16) && post != LNB_DROPOUT && !pre) bad("LayerNorm backward activation gradient without its input");
   const DropoutSpec dsp{token, threshold, scale};
   if (rows <= 0 || h <= 0) return;
   if (h > 1024) bad("LayerNorm backward rows wider than 1024");
@@ -441,7 +486,8 @@ void ln_backward(hipStream_t s, const float* x, const float* gamma, const float*
   const size_t lds = size_t(8 * h) * 4;
   const int cpl = int((h + 63) / 64);
 #define MSX_LNB(C) MSX_LAUNCH(k_ln_backward<C>, dim3(unsigned(blocks)), dim3(256), lds, s, x, gamma, g, stats, dx, \
-                              partial, rows, h, per, dx2, post, pre, dsp, uint32_t(seed), uint32_t(seed >> 32))
+                              partial, rows, h, per, dx2, post, pre, dsp, uint32_t(seed), uint32_t(seed >> 32), \
+                              Out16{dx16, dx2_16})
   // 12 columns a lane for H = 768 (BERT-base): 16 would hold a third of the registers idle and
   // cost a wave of occupancy on a bandwidth-bound pass.
   if (cpl <= 1) MSX_LNB(1);

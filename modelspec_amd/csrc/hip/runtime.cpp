@@ -122,6 +122,14 @@ void* Executor::ptr(uint32_t id) const {
 
 const void* Executor::value(uint32_t id) const { return ptr(id); }
 
+_Float16* Executor::ptr16(uint32_t id) const {
+  auto f = fixed16_.find(id);
+  if (f != fixed16_.end()) return f->second;
+  auto t = token16_.find(id);
+  if (t != token16_.end()) return static_cast<_Float16*>(arena_.at(t->second));
+  return nullptr;
+}
+
 void Executor::build() {
   const Program& p = p_;
   const size_t n = p.nodes.size();
@@ -665,6 +673,19 @@ void Executor::build() {
   // constant and is never folded.
   std::set<uint32_t> folded_scalar;
 
+  // Mixed precision: every value a GEMM reads as an operand gets an f16 copy in HBM, which the
+  // f16 GEMM (k_gemm_lds16) reads straight into LDS: a GEMM output's copy is written by the GEMM's
+  // epilogue, a LayerNorm's (forward or backward) by the LayerNorm pass, a parameter's by the
+  // optimizer launch (and every upload); other producers (attention, cross-entropy) are followed by
+  // a rounding pass. The f32 values stay for the kernels that read them in f32.
+  std::set<uint32_t> gemm_operands;
+  if (s_.opt_.mixed && !s_.opt_.fuse_ce_head)
+    for (size_t k = 0; k < n; ++k) {
+      const Node& x = p.nodes[k];
+      if (!need[k] || x.op != Op::MatMul || optimizer.count(x.id)) continue;
+      for (int side = 0; side < 2; ++side) gemm_operands.insert(resolve(p, x.operands[size_t(side)]).src);
+    }
+
   // --- storage ------------------------------------------------------------------------------
   std::map<uint32_t, float> constants;
   for (size_t k = 0; k < n; ++k) {
@@ -685,7 +706,10 @@ void Executor::build() {
           inputs_.push_back(InputSlot{x.name, x.ty.dtype, x.ty.count(), 0, x.id, s_.corpus_fed(p, x.name)});
         }
         break;
-      case Op::ParamRead: fixed_[x.id] = s_.param_ + s_.offset_[x.param]; break;
+      case Op::ParamRead:
+        fixed_[x.id] = s_.param_ + s_.offset_[x.param];
+        if (gemm_operands.count(x.id) && s_.param16_) fixed16_[x.id] = s_.param16_ + s_.offset_[x.param];
+        break;
       case Op::Scalar:
         // Under loss scaling the loss gradient's seed (the Scalar 1.0 of the loss subgraph) is
         // the device's current loss scale.
@@ -788,6 +812,7 @@ void Executor::build() {
     // Further K segments (A, B sources) of a chain of like GEMMs added into one value.
     std::vector<std::pair<uint32_t, uint32_t>> segs;
     std::string what;
+    bool c16 = false;  // mixed precision: the output's f16 copy is written too
   };
   struct Pending {
     std::function<Launch()> make;
@@ -815,6 +840,17 @@ void Executor::build() {
   auto I = [this](uint32_t id) { return static_cast<int32_t*>(ptr(id)); };
   auto shape = [&](uint32_t v) -> const std::vector<int64_t>& { return p.node(v).ty.shape; };
   const uint64_t seed = s_.seed_;
+  // Reserves the f16 copy of v when a GEMM reads v (see gemm_operands); true when it has one.
+  auto want16 = [&](int64_t v) -> bool {
+    if (v < 0 || !gemm_operands.count(uint32_t(v))) return false;
+    const uint32_t vid = uint32_t(v);
+    if (token16_.count(vid) || fixed16_.count(vid)) return true;
+    const Node& x = p.node(vid);
+    if (x.ty.rank() != 2 || x.ty.dtype != DType::F32) return false;
+    token16_[vid] = arena_.reserve(size_t(x.ty.shape[0] * ld_of(vid)) * 2);
+    return true;
+  };
+  auto H16 = [this](int64_t v) -> _Float16* { return v >= 0 ? ptr16(uint32_t(v)) : nullptr; };
   // The launch of one GEMM or a group of like GEMMs (one hk::gemm_group call).
   auto gemm_launch = [this, F, A, I](std::vector<std::shared_ptr<GemmJob>> jobs) {
     return [this, F, A, I, jobs]() {
@@ -852,6 +888,11 @@ void Executor::build() {
                           a.drop_scale = j.drop_scale;
                           a.drop_seed = s_.seed_;
                         }
+                        if (a.h16 && a.ce_operand == 0 && a.ksegs <= 1) {
+                          a.a16 = ptr16(j.asrc);
+                          a.b16 = ptr16(j.bsrc);
+                        }
+                        if (j.c16) a.c16 = ptr16(j.out_id);
                         list[q] = a;
                       }
                       hk::gemm_group(s, list, int(jobs.size()));
@@ -1178,6 +1219,7 @@ void Executor::build() {
         job->ce_part = ce_part;
         job->ce_tab = ce_tab;
         job->what = what;
+        job->c16 = g.h16 && !ce_part && g.ce_operand == 0 && !g.defer && want16(int64_t(out_id));
         pending.push_back({gemm_launch({job}), 0, 0, is_step_ && g.defer, {job}});
         pending.back().pure = true;
         if (g.defer && wsf > 0) {
@@ -1372,13 +1414,15 @@ void Executor::build() {
                                 {" embedding %", f.eb}})
             if (v >= 0) what += tag + std::to_string(v);
           what += " " + type_string(x.ty);
+          const bool y16 = want16(yv), yd16 = want16(f.dout);
           push([=](hipStream_t s) {
             auto fp = [&](int64_t v2) { return v2 >= 0 ? F(uint32_t(v2)) : nullptr; };
             hk::ln_fused(s, fp(av), F(uint32_t(bv)), tin >= 0 ? I(uint32_t(tin)) : nullptr, si.first, si.second, F(gm), F(bt),
                          fp(s_val), fp(yv), write_stats ? static_cast<float*>(A(stats)) : nullptr,
                          tout >= 0 ? I(uint32_t(tout)) : nullptr, so.first, so.second, fp(f.dout), rows, h, seed,
                          gids >= 0 ? I(uint32_t(gids)) : nullptr, src_rows, ea.ids >= 0 ? I(uint32_t(ea.ids)) : nullptr,
-                         ea.rows, eb.ids >= 0 ? I(uint32_t(eb.ids)) : nullptr, eb.rows);
+                         ea.rows, eb.ids >= 0 ? I(uint32_t(eb.ids)) : nullptr, eb.rows, y16 ? H16(yv) : nullptr,
+                         yd16 ? H16(f.dout) : nullptr);
           });
           bytes = 4.0 * double(count) * (2 + (av >= 0) + (f.add >= 0) + (yv >= 0) + (f.dout >= 0));
           break;
@@ -1421,12 +1465,14 @@ void Executor::build() {
           thr = dropout_threshold(pr);
           scl = 1.0f / (1.0f - pr);
         }
+        const bool dx16 = want16(dxv), post16 = want16(post);
         push([=](hipStream_t s) {
           hk::ln_backward(s, F(xv), gmv >= 0 ? F(uint32_t(gmv)) : nullptr, F(g), static_cast<float*>(A(stats)),
                           dxv >= 0 ? F(uint32_t(dxv)) : nullptr, part ? static_cast<float*>(A(part)) : nullptr, rows, h,
                           post >= 0 ? F(uint32_t(post)) : nullptr, kind,
                           post >= 0 && kind != hk::LNB_DROPOUT ? F(uint32_t(aux)) : nullptr,
-                          post >= 0 && kind == hk::LNB_DROPOUT ? I(uint32_t(aux)) : nullptr, thr, scl, seed);
+                          post >= 0 && kind == hk::LNB_DROPOUT ? I(uint32_t(aux)) : nullptr, thr, scl, seed,
+                          dx16 ? H16(dxv) : nullptr, post16 ? H16(post) : nullptr);
         });
         bytes = 4.0 * double(rows * h * (dxv >= 0 ? 3 : 2) + (gmv >= 0 ? h : 0) + (sums ? 2 * h : 0));
         if (sums) {
@@ -1667,6 +1713,22 @@ void Executor::build() {
       pending.back().flop = flop;
       pending.back().bytes = bytes;
     }
+    // A GEMM operand from a producer that writes no f16 copy (attention, its gradients, the
+    // cross-entropy gradient, the masked-row scatter): a rounding pass right after the launch that
+    // wrote it.
+    // (Ops whose value is written by a launch at or before their own place in the plan.)
+    const bool round_after = x.op == Op::Attention || x.op == Op::AttentionGradQ || x.op == Op::AttentionGradK ||
+                             x.op == Op::AttentionGradV || x.op == Op::CrossEntropyGrad || x.op == Op::LayerNorm ||
+                             x.op == Op::DropoutGrad || x.op == Op::EmbeddingGrad || x.op == Op::Add ||
+                             x.op == Op::Sub || x.op == Op::Mul || x.op == Op::Gelu || x.op == Op::GeluGrad ||
+                             x.op == Op::Dropout || x.op == Op::Embedding;
+    if (round_after && token_.count(id) && gemm_operands.count(id) && !token16_.count(id) && want16(int64_t(id))) {
+      const int64_t rows = x.ty.shape[0], cols = x.ty.shape[1], ld = ld_of(id);
+      pending.push_back({[=] {
+        return Launch{"RoundF16 %" + std::to_string(id), [=](hipStream_t s) { hk::to_f16_rows(s, F(id), ld, H16(id), ld, rows, cols); }};
+      }});
+      pending.back().bytes = 6.0 * double(rows * cols);
+    }
   }
   // GEMM chains: Add(..Add(Add(X, A1 B1), A2 B2).., An Bn), each product a GEMM of one shape and
   // configuration whose sum only the next Add reads, is one GEMM over the concatenated K (the
@@ -1897,6 +1959,12 @@ void Executor::build() {
         pending.back().bytes = 7.0 * 4.0 * double(nt);
       }
       if (ls) pending.push_back({[=] { return Launch{"LossScale", [=](hipStream_t s) { hk::loss_scale_update(s, ls); }}; }});
+      if (s_.param16_ || (s_.opt_.plan_only && s_.opt_.mixed)) {
+        pending.push_back({[=] {
+          return Launch{"ParamF16", [=](hipStream_t s) { hk::to_f16_rows(s, s_.param_, nt, s_.param16_, nt, 1, nt); }};
+        }});
+        pending.back().bytes = 6.0 * double(nt);
+      }
     } else if (st.rule == Rule::Sgd && !st.updates.empty()) {
       uint32_t rate = p.node(st.updates.begin()->second).operands[1];
       uint32_t lr_scalar = p.node(rate).operands[0];
@@ -2177,6 +2245,9 @@ Session::Session(int device, const TrainingStep& step, const Program& forward, u
   losses_dev_ = base + 4 * total_;
   counter_ = reinterpret_cast<uint32_t*>(base + 4 * total_ + loss_capacity_);
   if (opt_.mixed) {
+    hip_check(hipMalloc(&param16_, size_t(total_) * 2), "hipMalloc (f16 parameters)");
+    hip_check(hipMemset(param16_, 0, size_t(total_) * 2), "hipMemset (f16 parameters)");
+    stats_.device_bytes += size_t(total_) * 2;
     // The loss-scale state, in device memory for the whole run (read and written by the step).
     hip_check(hipMalloc(&scaler_, sizeof(hk::LossScaleState)), "hipMalloc (loss scale)");
     hk::LossScaleState init{opt_.loss_scale, 1.0f / opt_.loss_scale, 0, 0, 0, opt_.scale_window, 0, 0};
@@ -2196,6 +2267,7 @@ Session::~Session() {
   fwd_exec_.reset();
   corpus_.reset();
   if (scaler_) (void)hipFree(scaler_);
+  if (param16_) (void)hipFree(param16_);
   if (state_mem_) (void)hipFree(state_mem_);
   if (eval_mem_) (void)hipFree(eval_mem_);
   if (fork_) (void)hipEventDestroy(fork_);
@@ -2232,6 +2304,10 @@ void Session::upload_params(const std::vector<std::vector<float>>& values) {
   for (size_t q = 0; q < params.size(); ++q) {
     if (int64_t(values[q].size()) != params[q].ty.count()) throw IrError("set_params: `" + params[q].path + "` has the wrong size");
     hip_check(hipMemcpy(param_ + offset_[q], values[q].data(), values[q].size() * 4, hipMemcpyHostToDevice), "hipMemcpy (params)");
+  }
+  if (param16_) {
+    hk::to_f16_rows(stream_, param_, total_, param16_, total_, 1, total_);
+    sync();
   }
 }
 

@@ -158,6 +158,9 @@ class Session : public Engine {
   std::vector<int64_t> offset_;  // per ParamId, in floats
   int64_t total_ = 0, trained_ = 0;
   float *param_ = nullptr, *grad_ = nullptr, *m_ = nullptr, *v_ = nullptr;
+  // Mixed precision: the parameters rounded to f16 (the GEMMs' weight operands), refreshed after
+  // every upload and every optimizer step.
+  _Float16* param16_ = nullptr;
   float* losses_dev_ = nullptr;
   uint32_t* counter_ = nullptr;
   uint32_t loss_capacity_ = 1u << 20;
@@ -210,6 +213,10 @@ class Executor {
   DeviceArena arena_;
   std::map<uint32_t, void*> token_;   // arena reservation per value
   std::map<uint32_t, void*> fixed_;   // values living in the session's arenas
+  // Mixed precision: the f16 copy of a value GEMMs read as an operand, written by its producer.
+  std::map<uint32_t, void*> token16_;
+  std::map<uint32_t, _Float16*> fixed16_;  // parameters: their slice of the session's f16 copy
+  _Float16* ptr16(uint32_t id) const;      // nullptr when the value has no f16 copy
   std::vector<Launch> launches_;
   size_t join_at_ = SIZE_MAX;  // the first launch after the backward (it waits for the side stream)
   // device: written on the device by the corpus prologue, never staged by the host.
