@@ -446,7 +446,8 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k, bool defer, bool h16, bool
   const int64_t mn = m * n;
   SplitPlan p{};
   // A cross-entropy head (ce) always takes the largest tile, the one its kernels are built for.
-  if (h16 && (ce || mn >= (int64_t(1) << 21) || k >= 8192)) { p.wm = 4; p.wn = 4; p.wk = 32; }
+  // Mixed precision: the 128 x 128 tiles of k_gemm_lds16 (and k_gemm_w's largest f16 tile).
+  if (h16) { p.wm = 4; p.wn = 4; p.wk = 32; }
   else if (ce || mn >= (int64_t(1) << 21) || k >= 8192) { p.wm = 2; p.wn = 2; p.wk = 16; }
   else if (mn <= (int64_t(1) << 19)) { p.wm = 1; p.wn = 1; p.wk = 32; }
   else { p.wm = 1; p.wn = 2; p.wk = 16; }
@@ -491,6 +492,11 @@ int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs) {
   const int64_t width = g.sum_a ? g.m : g.n;
   jobs[1] = ColumnJob{g.workspace + int64_t(split) * g.m * g.n, g.colsum, nullptr, split, int32_t(width), int32_t(width), 0};
   return 2;
+}
+
+bool gemm_lds16_fits(const GemmArgs& g) {
+  if (!g.h16 || g.ksegs > 1 || g.ce_operand || g.ce_part || g.m <= 0 || g.n <= 0 || g.k <= 0) return false;
+  return lds16_layout(g, split_plan(g.m, g.n, g.k, g.defer, true, false).chunk);
 }
 
 void gemm(hipStream_t s, const GemmArgs& g) { gemm_group(s, &g, 1); }
@@ -643,6 +649,9 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
   const bool lds = !g.h16 && ksegs == 1 && count == 1 && !ce && gemm_lds(s, g, ptrs, split, chunk);
   const bool lds16 = !lds && g.h16 && ksegs == 1 && !ce && gemm_lds16(s, list, count, ptrs, split, chunk);
   if (lds16) f16_out = true;
+  for (int q = 0; q < count && !lds16; ++q)
+    if (!list[q].a || !list[q].b || !list[q].c)
+      bad("a GEMM on an f16-only operand or output needs k_gemm_lds16 (f16 copies, its layout)");
   if (lds || lds16) {
     // launched
   } else if (ksegs > 1) {
@@ -657,7 +666,7 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
     if (g.h16) { MSX_CE(4, 4, 32, true) }
     else { MSX_CE(2, 2, 16, false) }
   } else if (g.h16) {
-    if (g.colsum) bad("the mixed-precision GEMM takes no column sums");
+    if (g.colsum) bad("mixed-precision column sums need k_gemm_lds16's layout (f16 copies, K a multiple of 32)");
     if (!g.ta && !g.tb) { MSX_WIDE_HT(false, false) }
     else if (g.ta && !g.tb) { MSX_WIDE_HT(true, false) }
     else if (!g.ta && g.tb) { MSX_WIDE_HT(false, true) }

@@ -82,5 +82,8 @@ bool gemm_lds(hipStream_t s, const GemmArgs& g, const GemmPtrs& ptrs, int split,
 // the f16 kernel reads them straight into LDS; it writes the f32 output (or split-K partials) and
 // the f16 output copies asked for.
 bool gemm_lds16(hipStream_t s, const GemmArgs* list, int count, const GemmPtrs& ptrs, int split, int64_t chunk);
+// Whether k_gemm_lds16 takes a problem of this shape and layout with split-K slices of `chunk`
+// (its f16 operand copies present and 16-byte aligned aside).
+bool lds16_layout(const GemmArgs& g, int64_t chunk);
 
 }  // namespace msx::hk

@@ -382,7 +382,7 @@ __device__ __forceinline__ void tr_read16x8(const uint32_t (&at)[8], v4s16 (&r)[
 }
 }  // namespace
 
-template <int BM, int BN, int WGM, int WGN, bool AKC, bool BKC, int NS>
+template <int BM, int BN, int WGM, int WGN, bool AKC, bool BKC, int NS, int SUMS>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, int64_t M, int64_t N, int64_t K,
                                                                int64_t lda, int64_t ldb, int64_t ldc, int64_t kchunk,
                                                                int64_t zero_to, bool vo, GemmOrder order) {
@@ -412,6 +412,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
   const _Float16* __restrict__ B = ptrs.b16[qp];
   const GemmEpi epi = ptrs.epi[qp];
   float* __restrict__ ws = ptrs.ws[qp];
+  float* __restrict__ colsum = ptrs.colsum[qp];
   const int64_t kmax = K - 1;
   const _Float16* srcA[PA];
   const _Float16* srcB[PB];
@@ -520,6 +521,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
       tr_frags(Bs, BN, wn, f.b);
     }
   };
+  // Sums over K of this lane's operand rows (SUMS 1: op(A)'s rows, 2: op(B)'s columns, i.e. the
+  // fragments' rows), by the waves of the first wave column (row), which read every row of the
+  // operand: lane (c, q) adds its 8 K of rows 16 u + c of the wave tile, in K order.
+  constexpr int SN = SUMS == 1 ? I : SUMS == 2 ? J : 1;
+  float ksum[SN];
+#pragma unroll
+  for (int u = 0; u < SN; ++u) ksum[u] = 0.0f;
+  const bool sum_wave = SUMS == 1 ? wn == 0 : SUMS == 2 ? wm == 0 : false;
 #pragma unroll
   for (int p = 0; p < NS - 1; ++p) issue(p);
 #pragma unroll 1
@@ -533,6 +542,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
     for (int i = 0; i < I; ++i)
 #pragma unroll
       for (int j = 0; j < J; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
+    if (SUMS != 0 && sum_wave) {
+#pragma unroll
+      for (int u = 0; u < SN; ++u) {
+        // v_dot2_f32_f16 against (1, 1): two halves added into the f32 sum a VALU op.
+        const v8h h = SUMS == 1 ? f.a[u] : f.b[u];
+        typedef _Float16 v2h_ __attribute__((ext_vector_type(2)));
+        const v2h_ one{_Float16(1.0f), _Float16(1.0f)};
+        float x = ksum[u];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x = __builtin_amdgcn_fdot2(v2h_{h[2 * e], h[2 * e + 1]}, one, x, false);
+        ksum[u] = x;
+      }
+    }
   }
   wait_vm(0);  // no load may still write LDS when the block ends
   float* out = ws ? ws + int64_t(tz) * M * N : ptrs.c[qp];
@@ -561,6 +583,24 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
           if (out) out[row * ldo + col + u] = x;
           if (out16) out16[row * ldo + col + u] = _Float16(x);
         }
+      }
+    }
+  }
+  if constexpr (SUMS != 0) {
+    // The four lane groups q hold disjoint K: added across q (fixed order), written by q = 0 at
+    // row (column) base + 16 u + c; split-K slices into the workspace's sums, slice tz.
+#pragma unroll
+    for (int u = 0; u < SN; ++u) {
+      ksum[u] += __shfl_xor(ksum[u], 16, 64);
+      ksum[u] += __shfl_xor(ksum[u], 32, 64);
+    }
+    if (sum_wave && q == 0 && colsum) {
+      const int64_t base = SUMS == 1 ? m0 + wm : n0 + wn, width = SUMS == 1 ? M : N;
+      float* dst = colsum + (ws ? int64_t(tz) * width : 0);
+#pragma unroll
+      for (int u = 0; u < SN; ++u) {
+        const int64_t at = base + 16 * u + c;
+        if (at < width) dst[at] = ksum[u];
       }
     }
   }
@@ -632,22 +672,29 @@ bool gemm_lds(hipStream_t s, const GemmArgs& g, const GemmPtrs& ptrs, int split,
   return false;
 }
 
-bool gemm_lds16(hipStream_t s, const GemmArgs* list, int count, const GemmPtrs& ptrs, int split, int64_t chunk) {
+bool lds16_layout(const GemmArgs& o, int64_t chunk) {
   constexpr int BK = 32;
+  const bool akc = !o.ta, bkc = o.tb;
+  const int64_t kpad = (o.k + BK - 1) / BK * BK;
+  if (chunk % BK != 0 || o.lda % 8 != 0 || o.ldb % 8 != 0) return false;
+  // A K tail only over zero padding of the K-contiguous operands (the other kind is clamped, and
+  // a summed operand's clamped rows would enter its sums).
+  if (o.k % BK != 0 && ((!akc && !bkc) || (akc && !(o.pad_a && o.lda >= kpad)) || (bkc && !(o.pad_b && o.ldb >= kpad)) ||
+                        (o.colsum && !(o.sum_a ? akc : bkc))))
+    return false;
+  // An operand along its rows: whole 8-row chunks, or a pitch that holds the last one.
+  if (!akc && o.m % 8 != 0 && o.lda < (o.m + 7) / 8 * 8) return false;
+  if (!bkc && o.n % 8 != 0 && o.ldb < (o.n + 7) / 8 * 8) return false;
+  return true;
+}
+
+bool gemm_lds16(hipStream_t s, const GemmArgs* list, int count, const GemmPtrs& ptrs, int split, int64_t chunk) {
   const GemmArgs& g = list[0];
   auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   const bool akc = !g.ta, bkc = g.tb;
-  const int64_t kpad = (g.k + BK - 1) / BK * BK;
-  if (g.colsum || chunk % BK != 0) return false;
   for (int q = 0; q < count; ++q) {
     const GemmArgs& o = list[q];
-    if (!o.a16 || !o.b16 || !a16(o.a16) || !a16(o.b16) || o.lda % 8 != 0 || o.ldb % 8 != 0) return false;
-    // A K tail only over zero padding of the K-contiguous operands (the other kind is clamped).
-    if (o.k % BK != 0 && ((!akc && !bkc) || (akc && !(o.pad_a && o.lda >= kpad)) || (bkc && !(o.pad_b && o.ldb >= kpad))))
-      return false;
-    // An operand along its rows: whole 8-row chunks, or a pitch that holds the last one.
-    if (!akc && o.m % 8 != 0 && o.lda < (o.m + 7) / 8 * 8) return false;
-    if (!bkc && o.n % 8 != 0 && o.ldb < (o.n + 7) / 8 * 8) return false;
+    if (!o.a16 || !o.b16 || !a16(o.a16) || !a16(o.b16) || !lds16_layout(o, chunk)) return false;
   }
   constexpr int BM = 128, BN = 128;
   const int64_t lmt = (g.m + BM - 1) / BM, lnt = (g.n + BN - 1) / BN;
@@ -663,14 +710,20 @@ bool gemm_lds16(hipStream_t s, const GemmArgs* list, int count, const GemmPtrs& 
                               a16(o.pre_out)));
   }
   const int64_t zero_to = g.pad_c ? g.ldc : g.n;
-#define MSX_L16(AK, BKC_)                                                                                      \
-  MSX_LAUNCH((k_gemm_lds16<BM, BN, 2, 2, AK, BKC_, 3>), lgrid, dim3(256), 0, s, ptrs, g.m, g.n, g.k, g.lda, g.ldb, \
+  const int sums = g.colsum ? (g.sum_a ? 1 : 2) : 0;
+#define MSX_L16S(AK, BKC_, S)                                                                                      \
+  MSX_LAUNCH((k_gemm_lds16<BM, BN, 2, 2, AK, BKC_, 3, S>), lgrid, dim3(256), 0, s, ptrs, g.m, g.n, g.k, g.lda, g.ldb, \
              g.ldc, chunk, zero_to, vo, lorder)
-  if (akc && bkc) MSX_L16(true, true);
-  else if (akc) MSX_L16(true, false);
-  else if (bkc) MSX_L16(false, true);
-  else MSX_L16(false, false);
+#define MSX_L16(AK, BKC_)                  \
+  if (sums == 1) MSX_L16S(AK, BKC_, 1);      \
+  else if (sums == 2) MSX_L16S(AK, BKC_, 2); \
+  else MSX_L16S(AK, BKC_, 0)
+  if (akc && bkc) { MSX_L16(true, true); }
+  else if (akc) { MSX_L16(true, false); }
+  else if (bkc) { MSX_L16(false, true); }
+  else { MSX_L16(false, false); }
 #undef MSX_L16
+#undef MSX_L16S
   return true;
 }
 

@@ -75,7 +75,9 @@ struct GemmArgs {
   // Mixed precision with f16 operands in HBM: with both a16 and b16 set (the operands' f16 copies,
   // same layouts and leading dimensions as a and b), the GEMM reads them instead of a and b
   // (k_gemm_lds16: no rounding at load). c16, when set, receives the output (after the epilogue)
-  // rounded to f16 as well, at ldc.
+  // rounded to f16 as well, at ldc. An operand only its f16 copy holds (a or b null), or an output
+  // kept only as its f16 copy (c null, c16 set), needs k_gemm_lds16 (gemm_lds16_fits): another
+  // kernel refuses the problem.
   const _Float16* a16;
   const _Float16* b16;
   _Float16* c16;
@@ -124,6 +126,10 @@ int64_t gemm_workspace(int64_t m, int64_t n, int64_t k, bool colsum = false, boo
                        bool h16 = false, bool ce = false);
 // The column_finalize jobs that finish a deferred split-K gemm (0, 1 or 2 written to jobs).
 int gemm_deferred_jobs(const GemmArgs& g, ColumnJob* jobs);
+// Whether a mixed-precision problem of this shape and layout runs on k_gemm_lds16 once its f16
+// operand copies are given (16-byte aligned): no K segments or cross-entropy operand, whole
+// 16-byte groups of f16 in its rows, K a multiple of 32 or zero-padded to one.
+bool gemm_lds16_fits(const GemmArgs& g);
 void gemm(hipStream_t s, const GemmArgs& g);
 // `count` (1 .. kGemmGroupMax) independent GEMMs that differ only in their pointers, in one
 // launch; split-K slices of a group are summed by deferral only.

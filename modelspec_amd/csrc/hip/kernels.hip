@@ -106,23 +106,31 @@ __global__ __launch_bounds__(256) void k_to_f16_rows(const float* __restrict__ x
     y[r * ldy + c] = _Float16(x[r * ldx + c]);
   }
 }
-// Rows of whole 16-byte groups: block (x, y) converts groups 256 x + t of rows y, y + gridDim.y, ...
+// Rows in 16-byte groups: block (x, y) converts groups 256 x + t of rows y, y + gridDim.y, ...
+// When cols is not a multiple of 4 the last group of a row reaches into the row padding (both
+// strides hold it): its columns past cols are written as zero, so a GEMM that reads the padded
+// f16 row multiplies zeros there.
 __global__ __launch_bounds__(256) void k_to_f16_rows4(const float* __restrict__ x, int64_t ldx, _Float16* __restrict__ y,
-                                                      int64_t ldy, int64_t rows, int64_t groups) {
+                                                      int64_t ldy, int64_t rows, int64_t cols) {
   const int64_t gq = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (gq >= groups) return;
+  if (4 * gq >= cols) return;
+  const int live = int(cols - 4 * gq < 4 ? cols - 4 * gq : 4);
   for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
     const v4f v = *reinterpret_cast<const v4f*>(x + r * ldx + 4 * gq);
-    *reinterpret_cast<v4h*>(y + r * ldy + 4 * gq) = v4h{_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
+    v4h h;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) h[u] = u < live ? _Float16(v[u]) : _Float16(0.0f);
+    *reinterpret_cast<v4h*>(y + r * ldy + 4 * gq) = h;
   }
 }
 void to_f16_rows(hipStream_t s, const float* x, int64_t ldx, _Float16* y, int64_t ldy, int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return;
-  if (cols % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
-      reinterpret_cast<uintptr_t>(y) % 8 == 0 && cols / 4 <= int64_t(256) * 2147483647) {
-    const int64_t groups = cols / 4;
+  const int64_t groups = (cols + 3) / 4;
+  if (4 * groups <= std::min(ldx, ldy) && ldx % 4 == 0 && ldy % 4 == 0 &&
+      reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 8 == 0 &&
+      groups <= int64_t(256) * 2147483647) {
     MSX_LAUNCH(k_to_f16_rows4, dim3(blocks_for(groups, 256), unsigned(std::min<int64_t>(rows, 65535))), dim3(256), 0, s, x,
-               ldx, y, ldy, rows, groups);
+               ldx, y, ldy, rows, cols);
     return;
   }
   MSX_LAUNCH(k_to_f16_rows, dim3(std::min<unsigned>(blocks_for(rows * cols, 256), 16384)), dim3(256), 0, s, x, ldx, y, ldy,

@@ -252,14 +252,25 @@ void Executor::build() {
   for (auto [m, t] : mm_transposed) transposed_out.insert(t);
   // A SumRows of a MatMul's un-transposed B operand (the bias gradient beside its weight gradient)
   // is taken by that GEMM from its LDS tiles, when no reader of the sum comes before the GEMM.
+  // Under mixed precision only the f16 GEMM on the operands' f16 copies (k_gemm_lds16) takes the
+  // sums (of the f16 values): both operands' rows whole 16-byte groups of f16, K a multiple of 32.
   std::map<uint32_t, uint32_t> colsum_of;  // MatMul -> SumRows
   std::set<uint32_t> colsum_fused;
-  for (size_t k = 0; k < n && !s_.opt_.mixed; ++k) {
+  const bool mixed_twins = s_.opt_.mixed && !s_.opt_.fuse_ce_head;
+  auto sums_fit = [&](const Node& m) {
+    if (!s_.opt_.mixed) return true;
+    if (!mixed_twins || optimizer.count(m.id)) return false;
+    const Resolved ra = resolve(p, m.operands[0]), rb = resolve(p, m.operands[1]);
+    const auto &sa = p.node(ra.src).ty.shape, &sb = p.node(rb.src).ty.shape;
+    const int64_t k = p.node(m.operands[0]).ty.shape[1];
+    return sa.size() == 2 && sb.size() == 2 && sa[1] % 8 == 0 && sb[1] % 8 == 0 && k % 32 == 0;
+  };
+  for (size_t k = 0; k < n; ++k) {
     if (!need[k] || p.nodes[k].op != Op::SumRows) continue;
     const uint32_t a = p.nodes[k].operands[0];
     for (auto c : consumers[p.pos.at(a)]) {
       const Node& m = p.nodes[c];
-      if (m.op != Op::MatMul || mm_fused.count(m.id) || colsum_of.count(m.id)) continue;
+      if (m.op != Op::MatMul || mm_fused.count(m.id) || colsum_of.count(m.id) || !sums_fit(m)) continue;
       Resolved rb = resolve(p, m.operands[1]);
       if (rb.src != a || rb.flip) continue;
       bool late = true;
@@ -813,6 +824,8 @@ void Executor::build() {
     std::vector<std::pair<uint32_t, uint32_t>> segs;
     std::string what;
     bool c16 = false;  // mixed precision: the output's f16 copy is written too
+    // Mixed precision: false for an operand or output held only as its f16 copy.
+    bool a32 = true, b32 = true, c32 = true;
   };
   struct Pending {
     std::function<Launch()> make;
@@ -861,9 +874,9 @@ void Executor::build() {
                       for (size_t q = 0; q < jobs.size(); ++q) {
                         const GemmJob& j = *jobs[q];
                         hk::GemmArgs a = j.g;
-                        a.a = F(j.asrc);
-                        a.b = F(j.bsrc);
-                        a.c = F(j.out_id);
+                        a.a = j.a32 ? F(j.asrc) : nullptr;
+                        a.b = j.b32 ? F(j.bsrc) : nullptr;
+                        a.c = j.c32 ? F(j.out_id) : nullptr;
                         a.bias = j.bias_id >= 0 ? F(uint32_t(j.bias_id)) : nullptr;
                         a.workspace = j.ws ? static_cast<float*>(A(j.ws)) : nullptr;
                         a.ce_part = j.ce_part ? static_cast<float*>(A(j.ce_part)) : nullptr;
@@ -1714,15 +1727,16 @@ void Executor::build() {
       pending.back().bytes = bytes;
     }
     // A GEMM operand from a producer that writes no f16 copy (attention, its gradients, the
-    // cross-entropy gradient, the masked-row scatter): a rounding pass right after the launch that
-    // wrote it.
+    // cross-entropy gradient, the masked-row scatter, an input written before the plan runs): a
+    // rounding pass right after the launch that wrote it.
     // (Ops whose value is written by a launch at or before their own place in the plan.)
     const bool round_after = x.op == Op::Attention || x.op == Op::AttentionGradQ || x.op == Op::AttentionGradK ||
                              x.op == Op::AttentionGradV || x.op == Op::CrossEntropyGrad || x.op == Op::LayerNorm ||
                              x.op == Op::DropoutGrad || x.op == Op::EmbeddingGrad || x.op == Op::Add ||
                              x.op == Op::Sub || x.op == Op::Mul || x.op == Op::Gelu || x.op == Op::GeluGrad ||
-                             x.op == Op::Dropout || x.op == Op::Embedding;
-    if (round_after && token_.count(id) && gemm_operands.count(id) && !token16_.count(id) && want16(int64_t(id))) {
+                             x.op == Op::Dropout || x.op == Op::Embedding || (x.op == Op::Input && !is_moment_input(x.name));
+    if (round_after && (token_.count(id) || x.op == Op::Input) && gemm_operands.count(id) && !token16_.count(id) &&
+        want16(int64_t(id))) {
       const int64_t rows = x.ty.shape[0], cols = x.ty.shape[1], ld = ld_of(id);
       pending.push_back({[=] {
         return Launch{"RoundF16 %" + std::to_string(id), [=](hipStream_t s) { hk::to_f16_rows(s, F(id), ld, H16(id), ld, rows, cols); }};
@@ -1870,6 +1884,59 @@ void Executor::build() {
       merged.push_back(pd);
     }
     pending = std::move(merged);
+  }
+  // Mixed precision: a GEMM output that only k_gemm_lds16 launches read (as operands, or the
+  // column sums they take) is kept as its f16 copy alone: its producer (itself on k_gemm_lds16)
+  // writes no f32 value, and its readers get no f32 pointer for it, so that any other kernel
+  // refuses the problem loudly.
+  if (mixed_twins && !s_.opt_.plan_only) {
+    auto has16 = [&](uint32_t v) { return token16_.count(v) || fixed16_.count(v); };
+    std::map<uint32_t, GemmJob*> job_of;   // MatMul node -> its GEMM job
+    std::map<int64_t, GemmJob*> sums_of;  // fused SumRows node -> its GEMM job
+    std::map<uint32_t, GemmJob*> producer;
+    std::set<const GemmJob*> certain;     // jobs whose launch runs k_gemm_lds16
+    for (auto& pd : pending) {
+      bool all = !pd.gemm.empty();
+      for (auto& j : pd.gemm)
+        all = all && j->segs.empty() && has16(j->asrc) && has16(j->bsrc) && hk::gemm_lds16_fits(j->g);
+      for (auto& j : pd.gemm) {
+        const Node& jn = p.node(j->id);
+        job_of[jn.op == Op::AddRows ? jn.operands[0] : j->id] = j.get();
+        if (j->cs_id >= 0) sums_of[j->cs_id] = j.get();
+        producer[j->out_id] = j.get();
+        if (all) certain.insert(j.get());
+      }
+    }
+    auto gemm_only = [&](uint32_t v) {
+      if (outputs.count(v) || grad_values_pre.count(v) || !has16(v)) return false;
+      std::vector<size_t> readers = consumers[p.pos.at(v)];
+      for (size_t r = 0; r < readers.size(); ++r) {
+        const Node& c = p.nodes[readers[r]];
+        if (c.op == Op::Transpose && folded.count(c.id)) {
+          for (auto c2 : consumers[readers[r]]) readers.push_back(c2);
+          continue;
+        }
+        GemmJob* j = nullptr;
+        if (c.op == Op::MatMul && job_of.count(c.id)) j = job_of.at(c.id);
+        if (c.op == Op::SumRows && sums_of.count(c.id)) j = sums_of.at(c.id);
+        if (!j || !certain.count(j) || j->bias_id == int64_t(v) || (j->epi.node != j->id && j->epi.aux == int64_t(v)))
+          return false;
+        if (j->asrc != v && j->bsrc != v) return false;
+      }
+      return !readers.empty();
+    };
+    std::set<uint32_t> only16;
+    for (auto& [v, j] : producer)
+      if (j->c16 && certain.count(j) && !j->ws && gemm_only(v)) only16.insert(v);
+    for (auto& pd : pending)
+      for (auto& j : pd.gemm) {
+        if (only16.count(j->out_id)) {
+          j->c32 = false;
+          j->what += " (f16 only)";
+        }
+        if (only16.count(j->asrc)) j->a32 = false;
+        if (only16.count(j->bsrc)) j->b32 = false;
+      }
   }
   // The reductions only the optimizer reads (LayerNorm gamma and beta sums, split-K weight
   // gradients and their bias sums), in one launch; in the AdamW launch itself when every one is a

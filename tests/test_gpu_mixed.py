@@ -55,6 +55,37 @@ def test_a_mixed_gemm_is_the_product_of_f16_operands(mixed, m, k, n, ta, tb):
     assert np.all(np.abs(got - exact) <= 2.0 ** -10 * (np.abs(A) @ np.abs(Bm)) + 1e-6)
 
 
+@pytest.mark.parametrize("rows,m,n", [(4096, 768, 3072), (2880, 768, 768), (256, 64, 96), (16384, 128, 256),
+                                      (100, 40, 24), (1000, 36, 52)])
+def test_a_mixed_weight_gradient_takes_the_bias_gradient(mixed, rows, m, n):
+    """dW = x^T dy beside db = SumRows(dy), and the transposed form dW^T = dy^T x (the sums as row
+    sums of the left operand). Where the f16 GEMM reads both operands' f16 copies (rows whole
+    16-byte groups, K a multiple of 32) it takes db from its fragments: the f32 sum of dy rounded to
+    f16, |db - sum f16(dy)| <= 1e-5 sum |f16(dy)|. Elsewhere db is the separate f32 column sum of
+    dy itself (within 1e-5 of the float64 sum). Both within 2^-10 of the float64 sum of dy."""
+    x, dy = fast_values(41, rows * m, 0.5).reshape(rows, m), fast_values(42, rows * n, 0.5).reshape(rows, n)
+    p = Prog()
+    xi, di = p.input("x", (rows, m)), p.input("dy", (rows, n))
+    dw = p.op("MatMul", [p.op("Transpose", [xi], (m, rows)), di], (m, n))
+    db = p.op("SumRows", [di], (n,))
+    dwt = p.op("MatMul", [p.op("Transpose", [di], (n, rows)), xi], (n, m))
+    p.out(dw, db, dwt)
+    prog = mixed.program(p.text())
+    prog.run({"x": x, "dy": dy})
+    gw = prog.output(0, m * n).reshape(m, n).astype(np.float64)
+    gb = prog.output(1, n).astype(np.float64)
+    gt = prog.output(2, n * m).reshape(n, m).astype(np.float64)
+    X, D = f16(x), f16(dy)
+    r = np.abs(X.T) @ np.abs(D)
+    assert np.all(np.abs(gw - X.T @ D) <= 1e-5 * r + 1e-30)
+    assert np.all(np.abs(gt - D.T @ X) <= 1e-5 * r.T + 1e-30)
+    fused = m % 8 == 0 and n % 8 == 0 and rows % 32 == 0
+    want = D.sum(0) if fused else dy.astype(np.float64).sum(0)
+    mag = np.abs(D).sum(0)
+    assert np.all(np.abs(gb - want) <= 1e-5 * mag + 1e-30), float(np.max(np.abs(gb - want) / mag))
+    assert np.all(np.abs(gb - dy.astype(np.float64).sum(0)) <= 2.0 ** -10 * mag)
+
+
 @pytest.mark.parametrize("B,S,H,heads,masked", [(2, 128, 128, 2, True), (32, 176, 768, 12, True), (16, 272, 256, 16, False),
                                                 (2, 64, 256, 2, True)])
 def test_mixed_attention_and_gradients(mixed, oracle, B, S, H, heads, masked):
@@ -102,6 +133,17 @@ def test_a_mixed_run_tracks_the_f32_oracle(ctx, oracle):
     close = np.abs(got_p - want_p) <= 1e-2 * np.abs(want_p) + 3e-3
     assert close.mean() > 0.99, close.mean()
     assert ctx.loss_scale() == (65536.0, 0)
+
+
+def test_gemm_only_values_are_kept_as_f16_copies_alone(ctx):
+    """The BERT FFN's GELU output and the gradient of its pre-activation are read only by f16 GEMMs
+    (and the bias-gradient sums those take): their producers write the f16 copy alone. The run
+    itself is checked against the f32 oracle by the test above."""
+    _, _, loss, rows = api.bench_config(ctx, "bert_micro_mixed", 1, 2, profile_reps=1)
+    only = [r[0] for r in rows if "(f16 only)" in r[0]]
+    assert np.isfinite(loss)
+    assert any("+Gelu" in w for w in only) and any("+GeluGrad" in w for w in only), only
+    assert all("k_gemm_lds16" in r[4] for r in rows if "(f16 only)" in r[0])
 
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
