@@ -29,6 +29,7 @@ SOURCES = [
     "hip/gemm.hip",
     "hip/gemm_lds.hip",
     "hip/attention.hip",
+    "hip/flash16.hip",
     "hip/data.hip",
     "hip/segments.hip",
 ]
@@ -41,9 +42,10 @@ FLAGS = [
 ]
 
 
-# Per-source flags. The direct-to-LDS GEMMs keep their MFMA accumulators in VGPRs: with the
+# Per-source flags. The direct-to-LDS GEMMs and the f16 attention keep their MFMA accumulators in VGPRs: with the
 # compiler's default choice (AGPRs) it rotated the accumulators through copies every K tile.
-FILE_FLAGS = {"hip/gemm_lds.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+FILE_FLAGS = {"hip/gemm_lds.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+              "hip/flash16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def build(verbose=False):

@@ -1329,6 +1329,7 @@ void prepare_attention() {
     hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, int(kLdsMax));
     if (e != hipSuccess) throw std::runtime_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
   }
+  prepare_flash16();
 }
 
 }  // namespace msx::hk

@@ -1,5 +1,6 @@
 // The large-shape f32 GEMM on gfx950: operand K tiles loaded straight into LDS.
 #include "gemm_common.h"
+#include "lds_util.h"
 
 #include <algorithm>
 
@@ -28,26 +29,6 @@ namespace msx::hk {
 // leading dimension); a non-KC operand's K rows past K are clamped to the last one (their products
 // with the zero padding vanish). SUMS: 1, the row sums of op(A) over K; 2, the column sums of
 // op(B) (a bias gradient), taken from the fragments of the waves of the first wave column (row).
-namespace {
-#define MSX_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
-// 16 bytes a lane from global memory into LDS at dst + 16 lane (the host pass sees an empty body).
-__device__ __forceinline__ void load_lds16(const float* src, float* dst) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(src, MSX_LDS_PTR(dst), 16, 0, 0);
-#endif
-}
-// Waits until at most n vector memory operations of this wave are outstanding (expcnt and lgkmcnt
-// unconstrained).
-__device__ __forceinline__ void wait_vm(int n) {
-  switch (n) {
-#define MSX_W(N) case N: __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (((N) >> 4) << 14) | (7 << 4) | (0xF << 8)); break;
-    MSX_W(0) MSX_W(1) MSX_W(2) MSX_W(3) MSX_W(4) MSX_W(5) MSX_W(6) MSX_W(7) MSX_W(8) MSX_W(9) MSX_W(10)
-    MSX_W(11) MSX_W(12) MSX_W(13) MSX_W(14) MSX_W(15) MSX_W(16)
-#undef MSX_W
-    default: __builtin_amdgcn_s_waitcnt((7 << 4) | (0xF << 8)); break;
-  }
-}
-}  // namespace
 
 template <int BM, int BN, int WGM, int WGN, int BK, bool AKC, bool BKC, int NS, bool FP, int SUMS>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds(GemmPtrs ptrs, int64_t M, int64_t N, int64_t K,
@@ -353,34 +334,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds(GemmPtrs ptrs, int6
 // output rows 16 i + c, columns 16 j + 4 q .. + 3 (the MFMA takes B's fragment first: C^T tiles).
 // K must be a multiple of 32, or the K-contiguous operands zero-padded to it; the K rows of an
 // operand along its rows are clamped to the last (their products with the padding vanish).
-namespace {
-typedef short v4s16 __attribute__((ext_vector_type(4)));
-typedef _Float16 v4h16 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint32_t lds_at(const _Float16* p) {
-  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
-}
-// Eight transposed reads (four 16-row fragments of 8 halves) and the wait for them, as one block of
-// inline assembly: through the builtin the compiler waits for every global->LDS load in flight
-// (vmcnt(0), the prefetches too) before each transposed read, and separate asm reads would let it
-// use their registers before the data arrives.
-__device__ __forceinline__ void tr_read16x8(const uint32_t (&at)[8], v4s16 (&r)[8]) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  asm volatile(
-      "ds_read_b64_tr_b16 %0, %8\n"
-      "ds_read_b64_tr_b16 %1, %9\n"
-      "ds_read_b64_tr_b16 %2, %10\n"
-      "ds_read_b64_tr_b16 %3, %11\n"
-      "ds_read_b64_tr_b16 %4, %12\n"
-      "ds_read_b64_tr_b16 %5, %13\n"
-      "ds_read_b64_tr_b16 %6, %14\n"
-      "ds_read_b64_tr_b16 %7, %15\n"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
-      : "v"(at[0]), "v"(at[1]), "v"(at[2]), "v"(at[3]), "v"(at[4]), "v"(at[5]), "v"(at[6]), "v"(at[7])
-      : "memory");
-#endif
-}
-}  // namespace
 
 template <int BM, int BN, int WGM, int WGN, bool AKC, bool BKC, int NS, int SUMS>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, int64_t M, int64_t N, int64_t K,

@@ -689,12 +689,29 @@ void Executor::build() {
   // epilogue, a LayerNorm's (forward or backward) by the LayerNorm pass, a parameter's by the
   // optimizer launch (and every upload); other producers (attention, cross-entropy) are followed by
   // a rounding pass. The f32 values stay for the kernels that read them in f32.
+  // The f16 attention (flash16) reads its operands' copies the same way: q, k, v and the output
+  // gradient.
   std::set<uint32_t> gemm_operands;
+  auto flash = [&](const Node& x) {
+    if (!s_.opt_.mixed || s_.opt_.fuse_ce_head) return false;
+    if (x.op != Op::Attention && x.op != Op::AttentionGradQ && x.op != Op::AttentionGradK && x.op != Op::AttentionGradV)
+      return false;
+    const auto& ms = p.node(x.operands[3]).ty;
+    if (ms.dtype != DType::F32 || ms.rank() != 2 || x.heads <= 0) return false;
+    const int64_t B = ms.shape[0], S = ms.shape[1], L = p.node(x.operands[0]).ty.shape[0] / B;
+    const int64_t H = p.node(x.operands[0]).ty.shape[1];
+    return H % x.heads == 0 && hk::flash16_fits(L, S, H / x.heads);
+  };
   if (s_.opt_.mixed && !s_.opt_.fuse_ce_head)
     for (size_t k = 0; k < n; ++k) {
       const Node& x = p.nodes[k];
-      if (!need[k] || x.op != Op::MatMul || optimizer.count(x.id)) continue;
-      for (int side = 0; side < 2; ++side) gemm_operands.insert(resolve(p, x.operands[size_t(side)]).src);
+      if (!need[k] || optimizer.count(x.id)) continue;
+      if (x.op == Op::MatMul)
+        for (int side = 0; side < 2; ++side) gemm_operands.insert(resolve(p, x.operands[size_t(side)]).src);
+      if (flash(x)) {
+        for (int side = 0; side < 3; ++side) gemm_operands.insert(x.operands[size_t(side)]);
+        if (x.op != Op::Attention) gemm_operands.insert(x.operands[4]);
+      }
     }
 
   // --- storage ------------------------------------------------------------------------------
@@ -1525,6 +1542,61 @@ void Executor::build() {
         auto fkey = std::vector<uint32_t>{q, kv, v, mask, uint32_t(heads)};
         bool mfma = hk::attention_mfma(L, S, H / heads);
         const bool h16 = s_.opt_.mixed;  // mixed precision: the f16 MFMA
+        if (flash(x)) {
+          // The f16 attention on the operands' f16 copies, writing its outputs' copies itself.
+          if (!want16(q) || !want16(kv) || !want16(v) || (x.op != Op::Attention && !want16(o[4])))
+            throw IrError("f16 attention: an operand without its f16 copy");
+          if (x.op == Op::Attention) {
+            void* st2 = R(size_t(B * heads * L) * 8);
+            attn_fwd[fkey] = {id, st2};
+            const bool o16 = want16(id);
+            push([=](hipStream_t s) {
+              hk::flash16_fwd(s, H16(q), H16(kv), H16(v), F(mask), F(id), o16 ? H16(id) : nullptr,
+                              static_cast<float*>(A(st2)), B, L, S, H, heads);
+            });
+            pending.back().pure = true;
+            break;
+          }
+          auto key = o;
+          key.push_back(uint32_t(x.heads));
+          auto& grp = attn_groups.at(key);
+          int64_t first = -1;
+          for (auto g2 : grp)
+            if (g2 >= 0 && (first < 0 || p.pos.at(uint32_t(g2)) < p.pos.at(uint32_t(first)))) first = g2;
+          if (first != int64_t(id)) break;  // the group's first member launches for all three
+          const uint32_t g = o[4];
+          const std::array<int64_t, 3> members = grp;
+          what = "AttentionGrad16";
+          for (int e = 0; e < 3; ++e)
+            if (members[e] >= 0) what += std::string(" ") + "QKV"[e] + " %" + std::to_string(members[e]);
+          int64_t fwd_out = -1;
+          void *stats_tok = nullptr, *scratch_o = nullptr;
+          auto f = attn_fwd.find(fkey);
+          if (f != attn_fwd.end()) {
+            fwd_out = int64_t(f->second.first);
+            stats_tok = f->second.second;
+          } else {
+            scratch_o = R(size_t(shape(q)[0] * H) * 4);
+            stats_tok = R(size_t(B * heads * L) * 8);
+            push([=](hipStream_t s) {
+              hk::flash16_fwd(s, H16(q), H16(kv), H16(v), F(mask), static_cast<float*>(A(scratch_o)), nullptr,
+                              static_cast<float*>(A(stats_tok)), B, L, S, H, heads);
+            });
+          }
+          void* qterms = R(size_t(3 * B * heads * L) * 4);
+          bool m16[3];
+          for (int e = 0; e < 3; ++e) m16[e] = members[e] >= 0 && want16(members[e]);
+          push([=](hipStream_t s) {
+            auto out = [&](int64_t v2) { return v2 >= 0 ? F(uint32_t(v2)) : nullptr; };
+            auto out16 = [&](int e) { return m16[e] ? H16(members[e]) : nullptr; };
+            const float* fo = fwd_out >= 0 ? F(uint32_t(fwd_out)) : static_cast<float*>(A(scratch_o));
+            hk::flash16_bwd(s, H16(q), H16(kv), H16(v), F(mask), fo, F(g), H16(g), static_cast<float*>(A(stats_tok)),
+                            static_cast<float*>(A(qterms)), out(members[0]), out16(0), out(members[1]), out16(1),
+                            out(members[2]), out16(2), B, L, S, H, heads);
+          });
+          pending.back().pure = true;
+          break;
+        }
         if (x.op == Op::Attention) {
           void* st2 = mfma ? R(size_t(B * heads * L) * 8) : nullptr;
           attn_fwd[fkey] = {id, st2};

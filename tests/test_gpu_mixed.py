@@ -87,11 +87,13 @@ def test_a_mixed_weight_gradient_takes_the_bias_gradient(mixed, rows, m, n):
 
 
 @pytest.mark.parametrize("B,S,H,heads,masked", [(2, 128, 128, 2, True), (32, 176, 768, 12, True), (16, 272, 256, 16, False),
-                                                (2, 64, 256, 2, True)])
+                                                (2, 64, 256, 2, True), (4, 256, 256, 4, True), (2, 512, 128, 2, False),
+                                                (8, 128, 768, 12, True)])
 def test_mixed_attention_and_gradients(mixed, oracle, B, S, H, heads, masked):
     """Attention on the f16 MFMA (q, k, v, P, dO and dS rounded to f16, f32 accumulation and softmax
     statistics) against the oracle's f32 values: within 1e-3 + 4e-3 (|c| + r), r the f32 test's
-    magnitude bound, i.e. a few f16 roundings (2^-11 each) of the terms."""
+    magnitude bound, i.e. a few f16 roundings (2^-11 each) of the terms. 64-wide heads over rows
+    that are multiples of 128 take the f16-copy kernels (flash16), the others attention.hip's."""
     from test_gpu_ops import both
     n = B * S * H
     q, k, v, G = (fast_values(s, n, 0.5).reshape(B * S, H) for s in (12, 13, 14, 15))
