@@ -544,7 +544,8 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
     ptrs.a[q] = o.a;
     ptrs.b[q] = o.b;
     ptrs.c[q] = o.c;
-    ptrs.epi[q] = GemmEpi{o.bias, o.addend, o.pre_in, o.pre_out, o.act, o.drop_token, o.drop_threshold, o.drop_scale, o.drop_seed};
+    ptrs.epi[q] = GemmEpi{o.bias, o.addend, o.pre_in, o.pre_out, o.act, o.drop_token, o.drop_threshold, o.drop_scale, o.drop_seed,
+                          o.pre16};
     ptrs.ws[q] = ws;
     ptrs.colsum[q] = o.colsum ? (ws ? ws + int64_t(split) * o.m * o.n : o.colsum) : nullptr;
     ptrs.ce_part[q] = o.ce_part;
@@ -573,8 +574,15 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
   const GemmOrder order{uint32_t(mt), uint32_t(nt), uint32_t(tiles), g.n * g.k >= g.m * g.k};
   const dim3 wgrid(unsigned((tiles * problems + 7) / 8 * 8));
   const int64_t width = g.sum_a ? g.m : g.n;
-  if ((g.act == EPI_GELU_GRAD || g.act == EPI_RELU_GRAD) && !g.pre_in) bad("gemm activation gradient without its input");
-  const GemmEpi epi{g.bias, g.addend, g.pre_in, g.pre_out, g.act, g.drop_token, g.drop_threshold, g.drop_scale, g.drop_seed};
+  for (int q = 0; q < count; ++q) {
+    const GemmArgs& o = list[q];
+    if ((o.act == EPI_GELU_GRAD || o.act == EPI_RELU_GRAD) && !o.pre_in && !o.pre16)
+      bad("gemm activation gradient without its input");
+    if (o.pre16 && (!o.h16 || o.act == EPI_NONE || reinterpret_cast<uintptr_t>(o.pre16) % 8 || o.ldc % 4))
+      bad("an f16 pre-activation needs mixed precision, an activation and 8-byte aligned rows");
+  }
+  const GemmEpi epi{g.bias, g.addend, g.pre_in, g.pre_out, g.act, g.drop_token, g.drop_threshold, g.drop_scale, g.drop_seed,
+                    g.pre16};
   if (g.drop_token && (g.ldc != g.n || g.m * g.n > (int64_t(1) << 32)))
     bad("a GEMM's dropout epilogue needs a dense output of at most 2^32 elements");
   // float4 output groups: every row the epilogue touches 16-byte aligned (in every problem).
@@ -589,7 +597,7 @@ void gemm_group(hipStream_t s, const GemmArgs* list, int count) {
     const GemmArgs& o = list[q];
     vo = vo && (ptrs.ws[q] ? (o.n % 4 == 0 && a16(ptrs.ws[q]))
                            : ((o.n % 4 == 0 || (o.pad_c && !o.act && !o.addend)) && o.ldc % 4 == 0 && a16(o.c) &&
-                              a16(o.bias) && a16(o.addend) && a16(o.pre_in) && a16(o.pre_out)));
+                              a16(o.bias) && a16(o.addend) && a16(o.pre_in) && a16(o.pre_out) && a16(o.pre16)));
     va = va && aligned(o.a, o.lda, o.pad_a ? o.lda : (o.ta ? o.m : o.k / ksegs));
     vb = vb && aligned(o.b, o.ldb, o.pad_b ? o.ldb : (o.tb ? o.k / ksegs : o.n));
   }

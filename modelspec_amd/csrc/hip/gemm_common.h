@@ -11,6 +11,7 @@ namespace msx::hk {
 // with respect to the pre-activation pre_in[row, col], v the incoming gradient), then addend[row,
 // col] + v, then the dropout gradient (kept or zeroed by the dropout kernel's rule at the
 // element's index). Every step rounds as the separate kernel would (the same operation order).
+// With pre16 the pre-activation is kept as f16 instead (written rounded, read widened).
 __device__ __forceinline__ float epi_drop(const GemmEpi& e, float v, int64_t at) {
   const uint32_t w = philox_w0(uint32_t(at), 4u, uint32_t(e.drop_token[0]), uint32_t(e.drop_token[1]),
                                uint32_t(e.drop_seed), uint32_t(e.drop_seed >> 32));
@@ -20,10 +21,18 @@ __device__ __forceinline__ float gemm_epilogue(const GemmEpi& e, float v, int64_
   if (e.bias) v = v + e.bias[col];
   const int64_t at = row * ldc + col;
   switch (e.act) {
-    case EPI_GELU: if (e.pre_out) e.pre_out[at] = v; v = d_gelu(v); break;
-    case EPI_RELU: if (e.pre_out) e.pre_out[at] = v; v = v > 0.0f ? v : 0.0f; break;
-    case EPI_GELU_GRAD: v = d_gelu_grad(e.pre_in[at], v); break;
-    case EPI_RELU_GRAD: v = e.pre_in[at] > 0.0f ? v : 0.0f; break;
+    case EPI_GELU:
+      if (e.pre16) e.pre16[at] = _Float16(v);
+      else if (e.pre_out) e.pre_out[at] = v;
+      v = d_gelu(v);
+      break;
+    case EPI_RELU:
+      if (e.pre16) e.pre16[at] = _Float16(v);
+      else if (e.pre_out) e.pre_out[at] = v;
+      v = v > 0.0f ? v : 0.0f;
+      break;
+    case EPI_GELU_GRAD: v = d_gelu_grad(e.pre16 ? float(e.pre16[at]) : e.pre_in[at], v); break;
+    case EPI_RELU_GRAD: v = (e.pre16 ? float(e.pre16[at]) : e.pre_in[at]) > 0.0f ? v : 0.0f; break;
     default: break;
   }
   if (e.addend) v = e.addend[at] + v;
@@ -37,22 +46,32 @@ __device__ __forceinline__ float4 gemm_epilogue4(const GemmEpi& e, float4 v, int
     v = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
   }
   const int64_t at = row * ldc + col;
+  typedef _Float16 h4_ __attribute__((ext_vector_type(4)));
+  auto put_pre = [&]() {
+    if (e.pre16) *reinterpret_cast<h4_*>(e.pre16 + at) = h4_{_Float16(v.x), _Float16(v.y), _Float16(v.z), _Float16(v.w)};
+    else if (e.pre_out) *reinterpret_cast<float4*>(e.pre_out + at) = v;
+  };
+  auto get_pre = [&]() {
+    if (!e.pre16) return *reinterpret_cast<const float4*>(e.pre_in + at);
+    const h4_ h = *reinterpret_cast<const h4_*>(e.pre16 + at);
+    return make_float4(float(h[0]), float(h[1]), float(h[2]), float(h[3]));
+  };
   switch (e.act) {
     case EPI_GELU:
-      if (e.pre_out) *reinterpret_cast<float4*>(e.pre_out + at) = v;
+      put_pre();
       v = make_float4(d_gelu(v.x), d_gelu(v.y), d_gelu(v.z), d_gelu(v.w));
       break;
     case EPI_RELU:
-      if (e.pre_out) *reinterpret_cast<float4*>(e.pre_out + at) = v;
+      put_pre();
       v = make_float4(v.x > 0.0f ? v.x : 0.0f, v.y > 0.0f ? v.y : 0.0f, v.z > 0.0f ? v.z : 0.0f, v.w > 0.0f ? v.w : 0.0f);
       break;
     case EPI_GELU_GRAD: {
-      const float4 p = *reinterpret_cast<const float4*>(e.pre_in + at);
+      const float4 p = get_pre();
       v = make_float4(d_gelu_grad(p.x, v.x), d_gelu_grad(p.y, v.y), d_gelu_grad(p.z, v.z), d_gelu_grad(p.w, v.w));
       break;
     }
     case EPI_RELU_GRAD: {
-      const float4 p = *reinterpret_cast<const float4*>(e.pre_in + at);
+      const float4 p = get_pre();
       v = make_float4(p.x > 0.0f ? v.x : 0.0f, p.y > 0.0f ? v.y : 0.0f, p.z > 0.0f ? v.z : 0.0f, p.w > 0.0f ? v.w : 0.0f);
       break;
     }

@@ -281,14 +281,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds(GemmPtrs ptrs, int6
       if (vo && col + 3 < N) {
         if (more) {
           const float4 f = gemm_epilogue4(GemmEpi{nullptr, epi.addend, epi.pre_in, epi.pre_out, epi.act, epi.drop_token,
-                                                  epi.drop_threshold, epi.drop_scale, epi.drop_seed},
+                                                  epi.drop_threshold, epi.drop_scale, epi.drop_seed, epi.pre16},
                                           make_float4(v[0], v[1], v[2], v[3]), row, col, ldo);
           v = v4f{f.x, f.y, f.z, f.w};
         }
         *reinterpret_cast<v4f*>(orow + col) = v;
       } else {
         const GemmEpi rest{nullptr, epi.addend, epi.pre_in, epi.pre_out, epi.act, epi.drop_token, epi.drop_threshold,
-                           epi.drop_scale, epi.drop_seed};
+                           epi.drop_scale, epi.drop_seed, epi.pre16};
 #pragma unroll
         for (int u = 0; u < 4; ++u)
           if (col + u < zto) orow[col + u] = col + u < N ? (more ? gemm_epilogue(rest, v[u], row, col + u, ldo) : v[u]) : 0.0f;
@@ -335,13 +335,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds(GemmPtrs ptrs, int6
 // K must be a multiple of 32, or the K-contiguous operands zero-padded to it; the K rows of an
 // operand along its rows are clamped to the last (their products with the padding vanish).
 
-template <int BM, int BN, int WGM, int WGN, bool AKC, bool BKC, int NS, int SUMS>
+template <int BM, int BN, int WGM, int WGN, bool AKC, bool BKC, int NS, int SUMS, int MF = 16>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, int64_t M, int64_t N, int64_t K,
                                                                int64_t lda, int64_t ldb, int64_t ldc, int64_t kchunk,
                                                                int64_t zero_to, bool vo, GemmOrder order) {
   constexpr int BK = 32, W = WGM * WGN;
-  constexpr int WTM = BM / WGM, WTN = BN / WGN, I = WTM / 16, J = WTN / 16;
-  static_assert(I >= 1 && J >= 1 && WTM % 16 == 0 && WTN % 16 == 0, "16-row MFMA blocks");
+  constexpr int WTM = BM / WGM, WTN = BN / WGN, I = WTM / MF, J = WTN / MF;
+  static_assert(MF == 16 || MF == 32, "16x16x32 or 32x32x16 MFMA blocks");
+  static_assert(I >= 1 && J >= 1 && WTM % MF == 0 && WTN % MF == 0, "whole MFMA blocks a wave");
+  // MFMA blocks of MF rows: 16x16x32 (KS = 1 K step of 32 a tile) or 32x32x16 (KS = 2 of 16).
+  constexpr int KS = MF == 16 ? 1 : 2, NV = MF == 16 ? 4 : 16;
+  typedef float vacc __attribute__((ext_vector_type(NV)));
   constexpr int SA = BM * BK, SB = BN * BK, SS = SA + SB;  // halves a stage
   constexpr int LA = SA / 512, LB = SB / 512;               // 1 KB wave load instructions a tile
   static_assert(LA % W == 0 && LB % W == 0, "whole load instructions a wave");
@@ -425,58 +429,95 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
       load_lds16(reinterpret_cast<const float*>(src), reinterpret_cast<float*>(st + SA + t * 512));
     }
   };
-  v4f acc[I][J];
+  vacc acc[I][J];
 #pragma unroll
   for (int i = 0; i < I; ++i)
 #pragma unroll
-    for (int j = 0; j < J; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  auto kc_frag = [&](const _Float16* S, int r) {
-    return *reinterpret_cast<const v8h*>(S + r * 32 + 8 * (q ^ ((r >> 2) & 3)));
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < NV; ++e) acc[i][j][e] = 0.0f;
+  // Lane roles. MF 16: lane (c = l mod 16, q = l / 16) supplies row c of a 16-row block at K
+  // 8 q .. 8 q + 7. MF 32: lane (c = l mod 32, h = l / 32) supplies row c of a 32-row block at K
+  // 16 ks + 8 h .. + 7 of K step ks. Either way the lane's 8 K are one 16-byte chunk kq (kq = q,
+  // or 2 ks + h) of the row.
+  const int fc = MF == 16 ? c : lane & 31, fh = MF == 16 ? q : lane >> 5;
+  auto kc_frag = [&](const _Float16* S, int r, int kq) {
+    return *reinterpret_cast<const v8h*>(S + r * 32 + 8 * (kq ^ ((r >> 2) & 3)));
   };
-  // The LDS address of the transposed read hh (K 8q + 4hh ..) of the 16 rows from base.
-  auto tr_at = [&](const _Float16* S, int R, int base, int hh) {
-    const int k = 8 * q + 4 * hh + c / 4;
+  // The LDS address of the transposed read of K rows k0 .. k0 + 3 of the 16 rows from base: in each
+  // 16-lane group, source lane li reads K row k0 + li / 4, rows base + 4 (li mod 4) .. + 3.
+  auto tr_at = [&](const _Float16* S, int R, int base, int k0) {
+    const int k = k0 + c / 4;
     const int row = base + 4 * (c % 4);
     const int ch = row / 8, slot = (ch & ~7) | ((ch & 7) ^ (2 * (k & 3)));
     return lds_at(S + k * R + slot * 8 + (row % 8));
   };
-  // Four 16-row fragments of an operand along its rows (rows base0 + 16 u).
-  auto tr_frags = [&](const _Float16* S, int R, int base0, v8h (&out)[4]) {
-    uint32_t at[8];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      at[2 * u] = tr_at(S, R, base0 + 16 * u, 0);
-      at[2 * u + 1] = tr_at(S, R, base0 + 16 * u, 1);
-    }
-    v4s16 r[8];
-    tr_read16x8(at, r);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const v4h16 lo = __builtin_bit_cast(v4h16, r[2 * u]), hi = __builtin_bit_cast(v4h16, r[2 * u + 1]);
-      out[u] = v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  // The transposed reads (base row, first K row) of one 8-half fragment of this lane: MF 16, rows
+  // base .. + 15 at K 8 q + {0, 4}; MF 32, rows base + 16 (g mod 2) .. (g = l / 16) at K
+  // 16 ks + 8 (g / 2) + {0, 4}.
+  auto tr_pair = [&](int base, int ks, int hh, int& rb, int& k0) {
+    if constexpr (MF == 16) {
+      rb = base;
+      k0 = 8 * q + 4 * hh;
+    } else {
+      rb = base + 16 * (q & 1);
+      k0 = 16 * ks + 8 * (q >> 1) + 4 * hh;
     }
   };
-  static_assert((AKC || I == 4) && (BKC || J == 4), "an operand along its rows takes four 16-row fragments a wave");
-  struct Frag { v8h a[I], b[J]; };
+  static_assert((AKC || (I * KS) % 4 == 0) && (BKC || (J * KS) % 4 == 0),
+                "an operand along its rows takes its fragments in fours");
+  // Fragments (ks, u) of an operand along its rows, rows base0 + MF u, eight transposed reads a group
+  // of four.
+  auto tr_frags = [&](const _Float16* S, int R, int base0, auto& out) {
+    constexpr int U = sizeof(out[0]) / sizeof(out[0][0]);
+    constexpr int G = KS * U / 4;
+#pragma unroll
+    for (int g4 = 0; g4 < G; ++g4) {
+      uint32_t at[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int fi = 4 * g4 + e, ks = fi / U, u = fi % U;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          int rb, k0;
+          tr_pair(base0 + MF * u, ks, hh, rb, k0);
+          at[2 * e + hh] = tr_at(S, R, rb, k0);
+        }
+      }
+      v4s16 r[8];
+      tr_read16x8(at, r);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int fi = 4 * g4 + e, ks = fi / U, u = fi % U;
+        const v4h16 lo = __builtin_bit_cast(v4h16, r[2 * e]), hi = __builtin_bit_cast(v4h16, r[2 * e + 1]);
+        out[ks][u] = v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    }
+  };
+  struct Frag { v8h a[KS][I], b[KS][J]; };
   auto read = [&](int tile, Frag& f) {
     const _Float16* As = smem + (tile % NS) * SS;
     const _Float16* Bs = As + SA;
     if constexpr (AKC) {
 #pragma unroll
-      for (int i = 0; i < I; ++i) f.a[i] = kc_frag(As, wm + 16 * i + c);
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int i = 0; i < I; ++i) f.a[ks][i] = kc_frag(As, wm + MF * i + fc, MF == 16 ? q : 2 * ks + fh);
     } else {
       tr_frags(As, BM, wm, f.a);
     }
     if constexpr (BKC) {
 #pragma unroll
-      for (int j = 0; j < J; ++j) f.b[j] = kc_frag(Bs, wn + 16 * j + c);
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < J; ++j) f.b[ks][j] = kc_frag(Bs, wn + MF * j + fc, MF == 16 ? q : 2 * ks + fh);
     } else {
       tr_frags(Bs, BN, wn, f.b);
     }
   };
   // Sums over K of this lane's operand rows (SUMS 1: op(A)'s rows, 2: op(B)'s columns, i.e. the
   // fragments' rows), by the waves of the first wave column (row), which read every row of the
-  // operand: lane (c, q) adds its 8 K of rows 16 u + c of the wave tile, in K order.
+  // operand: the lane adds its 8 K of rows MF u + fc of the wave tile, in K order.
   constexpr int SN = SUMS == 1 ? I : SUMS == 2 ? J : 1;
   float ksum[SN];
 #pragma unroll
@@ -492,19 +533,29 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
     Frag f;
     read(t, f);
 #pragma unroll
-    for (int i = 0; i < I; ++i)
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int j = 0; j < J; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < I; ++i)
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          if constexpr (MF == 16)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.b[ks][j], f.a[ks][i], acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.b[ks][j], f.a[ks][i], acc[i][j], 0, 0, 0);
+        }
     if (SUMS != 0 && sum_wave) {
 #pragma unroll
       for (int u = 0; u < SN; ++u) {
         // v_dot2_f32_f16 against (1, 1): two halves added into the f32 sum a VALU op.
-        const v8h h = SUMS == 1 ? f.a[u] : f.b[u];
         typedef _Float16 v2h_ __attribute__((ext_vector_type(2)));
         const v2h_ one{_Float16(1.0f), _Float16(1.0f)};
         float x = ksum[u];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x = __builtin_amdgcn_fdot2(v2h_{h[2 * e], h[2 * e + 1]}, one, x, false);
+        for (int ks = 0; ks < KS; ++ks) {
+          const v8h h = SUMS == 1 ? f.a[ks][u] : f.b[ks][u];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x = __builtin_amdgcn_fdot2(v2h_{h[2 * e], h[2 * e + 1]}, one, x, false);
+        }
         ksum[u] = x;
       }
     }
@@ -514,45 +565,52 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
   _Float16* out16 = ws ? nullptr : ptrs.c16[qp];
   const int64_t ldo = ws ? N : ldc, zto = ws ? N : zero_to;
   const bool more = !ws && (epi.bias || epi.act != EPI_NONE || epi.addend || epi.drop_token);
+  // Output element (row, col) of block (i, j): the MFMA took B's fragment first, so the lane holds
+  // output row MF i + fc and, for each group g of 4 accumulators, the columns MF j + 8 g + 4 fh
+  // (MF 32) or 16 j + 4 q (MF 16) .. + 3.
 #pragma unroll
   for (int i = 0; i < I; ++i) {
-    const int64_t row = m0 + wm + 16 * i + c;
+    const int64_t row = m0 + wm + MF * i + fc;
     if (row >= M) continue;
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int64_t col = n0 + wn + 16 * j + 4 * q;
-      float4 v = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
-      if (vo && col + 3 < N) {
-        if (more) v = gemm_epilogue4(epi, v, row, col, ldo);
-        if (out) *reinterpret_cast<float4*>(out + row * ldo + col) = v;
-        if (out16)
-          *reinterpret_cast<v4h16*>(out16 + row * ldo + col) = v4h16{_Float16(v.x), _Float16(v.y), _Float16(v.z), _Float16(v.w)};
-      } else {
-        const float vs[4] = {v.x, v.y, v.z, v.w};
+    for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (col + u >= zto) continue;
-          const float x = col + u < N ? (more ? gemm_epilogue(epi, vs[u], row, col + u, ldo) : vs[u]) : 0.0f;
-          if (out) out[row * ldo + col + u] = x;
-          if (out16) out16[row * ldo + col + u] = _Float16(x);
+      for (int g = 0; g < NV / 4; ++g) {
+        const int64_t col = n0 + wn + MF * j + (MF == 16 ? 4 * q : 8 * g + 4 * fh);
+        float4 v = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+        if (vo && col + 3 < N) {
+          if (more) v = gemm_epilogue4(epi, v, row, col, ldo);
+          if (out) *reinterpret_cast<float4*>(out + row * ldo + col) = v;
+          if (out16)
+            *reinterpret_cast<v4h16*>(out16 + row * ldo + col) =
+                v4h16{_Float16(v.x), _Float16(v.y), _Float16(v.z), _Float16(v.w)};
+        } else {
+          const float vs[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (col + u >= zto) continue;
+            const float x = col + u < N ? (more ? gemm_epilogue(epi, vs[u], row, col + u, ldo) : vs[u]) : 0.0f;
+            if (out) out[row * ldo + col + u] = x;
+            if (out16) out16[row * ldo + col + u] = _Float16(x);
+          }
         }
       }
-    }
   }
   if constexpr (SUMS != 0) {
-    // The four lane groups q hold disjoint K: added across q (fixed order), written by q = 0 at
-    // row (column) base + 16 u + c; split-K slices into the workspace's sums, slice tz.
+    // The lane groups (q for MF 16, h for MF 32) hold disjoint K: added across them (fixed order),
+    // written by group 0 at row (column) base + MF u + fc; split-K slices into the workspace's
+    // sums, slice tz.
 #pragma unroll
     for (int u = 0; u < SN; ++u) {
-      ksum[u] += __shfl_xor(ksum[u], 16, 64);
+      if constexpr (MF == 16) ksum[u] += __shfl_xor(ksum[u], 16, 64);
       ksum[u] += __shfl_xor(ksum[u], 32, 64);
     }
-    if (sum_wave && q == 0 && colsum) {
+    if (sum_wave && fh == 0 && colsum) {
       const int64_t base = SUMS == 1 ? m0 + wm : n0 + wn, width = SUMS == 1 ? M : N;
       float* dst = colsum + (ws ? int64_t(tz) * width : 0);
 #pragma unroll
       for (int u = 0; u < SN; ++u) {
-        const int64_t at = base + 16 * u + c;
+        const int64_t at = base + MF * u + fc;
         if (at < width) dst[at] = ksum[u];
       }
     }
@@ -660,7 +718,7 @@ bool gemm_lds16(hipStream_t s, const GemmArgs* list, int count, const GemmPtrs& 
     const GemmArgs& o = list[q];
     vo = vo && (ptrs.ws[q] ? (o.n % 4 == 0 && a16(ptrs.ws[q]))
                            : (o.ldc % 4 == 0 && a16(o.c) && a16(o.c16) && a16(o.bias) && a16(o.addend) && a16(o.pre_in) &&
-                              a16(o.pre_out)));
+                              a16(o.pre_out) && a16(o.pre16)));
   }
   const int64_t zero_to = g.pad_c ? g.ldc : g.n;
   const int sums = g.colsum ? (g.sum_a ? 1 : 2) : 0;

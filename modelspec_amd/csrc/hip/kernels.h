@@ -52,10 +52,12 @@ struct GemmArgs {
   bool h16;
   // Epilogue after the bias: an activation (EPI_*: writing the pre-activation to pre_out when
   // non-null) or an activation gradient (pre_in the pre-activation), then addend + value.
-  // addend, pre_in and pre_out share the output's leading dimension.
+  // addend, pre_in and pre_out share the output's leading dimension. pre16 (mixed precision), when
+  // set, holds the pre-activation as f16 in place of pre_out (written) or pre_in (read).
   const float* addend;
   const float* pre_in;
   float* pre_out;
+  _Float16* pre16;
   int act;
   // Then, with drop_token, the dropout gradient of the result: element (r, c) (index r ldc + c;
   // ldc == n) kept when Philox word 0 of (index, drop_token, drop_seed) >= drop_threshold, then
@@ -92,6 +94,7 @@ enum GemmAct : int { EPI_NONE, EPI_GELU, EPI_RELU, EPI_GELU_GRAD, EPI_RELU_GRAD 
 struct GemmEpi {
   const float* bias; const float* addend; const float* pre_in; float* pre_out; int act;
   const int32_t* drop_token; uint64_t drop_threshold; float drop_scale; uint64_t drop_seed;
+  _Float16* pre16;
 };
 // The pointers of each problem of a GEMM group (problems of one shape and configuration, one
 // launch; block b works on problem b / tiles of the order).

@@ -53,6 +53,33 @@ __device__ __forceinline__ void tr_read16x8(const uint32_t (&at)[8], v4s16 (&r)[
       : "memory");
 #endif
 }
+// The same eight reads without the wait: r is not to be read before lds_wait8(r), which waits
+// for them and, taking r as its operands, keeps every use of r after it.
+__device__ __forceinline__ void tr_issue16x8(const uint32_t (&at)[8], v4s16 (&r)[8]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8\n"
+      "ds_read_b64_tr_b16 %1, %9\n"
+      "ds_read_b64_tr_b16 %2, %10\n"
+      "ds_read_b64_tr_b16 %3, %11\n"
+      "ds_read_b64_tr_b16 %4, %12\n"
+      "ds_read_b64_tr_b16 %5, %13\n"
+      "ds_read_b64_tr_b16 %6, %14\n"
+      "ds_read_b64_tr_b16 %7, %15"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+      : "v"(at[0]), "v"(at[1]), "v"(at[2]), "v"(at[3]), "v"(at[4]), "v"(at[5]), "v"(at[6]), "v"(at[7])
+      : "memory");
+#endif
+}
+__device__ __forceinline__ void lds_wait8(v4s16 (&r)[8]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
+               :
+               : "memory");
+#endif
+}
+
 // Four 16-byte LDS reads and the wait for them, in inline assembly for the reason above: LDS
 // the global->LDS loads do not write, read without waiting for those loads.
 __device__ __forceinline__ void lds_read4x16(const uint32_t (&at)[4], float4 (&r)[4]) {

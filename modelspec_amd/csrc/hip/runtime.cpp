@@ -843,6 +843,9 @@ void Executor::build() {
     bool c16 = false;  // mixed precision: the output's f16 copy is written too
     // Mixed precision: false for an operand or output held only as its f16 copy.
     bool a32 = true, b32 = true, c32 = true;
+    // Mixed precision: the epilogue's pre-activation (written by an activation, read by an
+    // activation gradient) held only as its f16 copy.
+    bool pre16 = false;
   };
   struct Pending {
     std::function<Launch()> make;
@@ -910,8 +913,14 @@ void Executor::build() {
                           }
                         }
                         if (j.epi.node != j.id && j.epi.act == hk::EPI_NONE) a.addend = F(uint32_t(j.epi.aux));
-                        if (j.epi.act == hk::EPI_GELU_GRAD || j.epi.act == hk::EPI_RELU_GRAD) a.pre_in = F(uint32_t(j.epi.aux));
-                        if (j.epi.act == hk::EPI_GELU || j.epi.act == hk::EPI_RELU) a.pre_out = F(j.id);
+                        if (j.epi.act == hk::EPI_GELU_GRAD || j.epi.act == hk::EPI_RELU_GRAD) {
+                          if (j.pre16) a.pre16 = ptr16(uint32_t(j.epi.aux));
+                          else a.pre_in = F(uint32_t(j.epi.aux));
+                        }
+                        if (j.epi.act == hk::EPI_GELU || j.epi.act == hk::EPI_RELU) {
+                          if (j.pre16) a.pre16 = ptr16(j.id);
+                          else a.pre_out = F(j.id);
+                        }
                         if (j.epi.drop >= 0) {
                           a.drop_token = I(j.drop_tok);
                           a.drop_threshold = j.drop_thr;
@@ -1997,6 +2006,36 @@ void Executor::build() {
       }
       return !readers.empty();
     };
+    // A pre-activation written by an activation epilogue and read only by activation-gradient
+    // epilogues (the GELU of the FFN and its gradient) is kept as f16 alone, as an f16 forward
+    // would have kept its input.
+    std::map<uint32_t, GemmJob*> epi_writer;  // epilogue consumer node -> its GEMM job
+    for (auto& pd : pending)
+      for (auto& j : pd.gemm)
+        if (j->epi.node != j->id) epi_writer[j->epi.node] = j.get();
+    for (auto& pd : pending)
+      for (auto& jp : pd.gemm) {
+        GemmJob* j = jp.get();
+        if ((j->epi.act != hk::EPI_GELU && j->epi.act != hk::EPI_RELU) || j->pre16 || j->g.ldc % 4) continue;
+        const uint32_t pv = j->id;
+        if (outputs.count(pv) || grad_values_pre.count(pv)) continue;
+        std::vector<GemmJob*> grads;
+        bool ok = true;
+        for (auto r : consumers[p.pos.at(pv)]) {
+          const Node& cn = p.nodes[r];
+          if (cn.id == j->epi.node) continue;
+          auto w = epi_writer.find(cn.id);
+          const bool fused_grad = (cn.op == Op::GeluGrad || cn.op == Op::ReluGrad) && w != epi_writer.end() &&
+                                  (w->second->epi.act == hk::EPI_GELU_GRAD || w->second->epi.act == hk::EPI_RELU_GRAD) &&
+                                  w->second->epi.aux == int64_t(pv) && w->second->g.ldc == j->g.ldc;
+          if (!fused_grad) { ok = false; break; }
+          grads.push_back(w->second);
+        }
+        if (!ok || grads.empty()) continue;
+        if (!token16_.count(pv)) token16_[pv] = arena_.reserve(size_t(j->g.m * j->g.ldc) * 2);
+        j->pre16 = true;
+        for (GemmJob* gj : grads) gj->pre16 = true;
+      }
     std::set<uint32_t> only16;
     for (auto& [v, j] : producer)
       if (j->c16 && certain.count(j) && !j->ws && gemm_only(v)) only16.insert(v);
