@@ -58,9 +58,10 @@ __device__ __forceinline__ uint32_t philox_w0(uint32_t c0, uint32_t c1, uint32_t
 #pragma unroll
   for (int round = 0; round < 10; ++round) {
     if (round > 0) { k0 += W0; k1 += W1; }
-    uint32_t hi0 = __umulhi(M0, c0), lo0 = M0 * c0, hi1 = __umulhi(M1, c2), lo1 = M1 * c2;
-    uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
-    c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+    // 32 x 32 -> 64-bit products: one v_mad_u64_u32 gives both halves (a mul_hi / mul_lo pair costs two).
+    const uint64_t p0 = uint64_t(M0) * c0, p1 = uint64_t(M1) * c2;
+    const uint32_t n0 = uint32_t(p1 >> 32) ^ c1 ^ k0, n2 = uint32_t(p0 >> 32) ^ c3 ^ k1;
+    c0 = n0; c1 = uint32_t(p1); c2 = n2; c3 = uint32_t(p0);
   }
   return c0;
 }
@@ -71,9 +72,10 @@ __device__ __forceinline__ uint4 philox_block4(uint32_t c0, uint32_t c1, uint32_
 #pragma unroll
   for (int round = 0; round < 10; ++round) {
     if (round > 0) { k0 += W0; k1 += W1; }
-    uint32_t hi0 = __umulhi(M0, c0), lo0 = M0 * c0, hi1 = __umulhi(M1, c2), lo1 = M1 * c2;
-    uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
-    c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+    // 32 x 32 -> 64-bit products: one v_mad_u64_u32 gives both halves (a mul_hi / mul_lo pair costs two).
+    const uint64_t p0 = uint64_t(M0) * c0, p1 = uint64_t(M1) * c2;
+    const uint32_t n0 = uint32_t(p1 >> 32) ^ c1 ^ k0, n2 = uint32_t(p0 >> 32) ^ c3 ^ k1;
+    c0 = n0; c1 = uint32_t(p1); c2 = n2; c3 = uint32_t(p0);
   }
   return make_uint4(c0, c1, c2, c3);
 }

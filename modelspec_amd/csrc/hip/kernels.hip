@@ -362,6 +362,75 @@ __global__ __launch_bounds__(256) void k_ln_fused(const float* __restrict__ a, c
   }
   if (stats && lane == 0) { stats[2 * row] = mean; stats[2 * row + 1] = rstd; }
 }
+// The same without row gathers or gathered operands, for rows of 256 VPL floats: lane l of a row's
+// wave takes the float4 groups l + 64 v (v < VPL), so every access is 16 bytes.
+template <int VPL>
+__global__ __launch_bounds__(256) void k_ln_fused4(const float* __restrict__ a, const float* __restrict__ b,
+                                                   DropoutSpec din, const float* __restrict__ gamma,
+                                                   const float* __restrict__ beta, float* __restrict__ s_out,
+                                                   float* __restrict__ y_out, float* __restrict__ stats,
+                                                   DropoutSpec dout, float* __restrict__ yd_out, int64_t rows,
+                                                   uint32_t seed_lo, uint32_t seed_hi, Out16 o16) {
+  constexpr int64_t h = 256 * VPL;
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const uint32_t il = din.token ? uint32_t(din.token[0]) : 0u, ih = din.token ? uint32_t(din.token[1]) : 0u;
+  float4 sv[VPL];
+  float sum = 0.0f;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int64_t i = row * h + 4 * (lane + 64 * v);
+    float4 x = *reinterpret_cast<const float4*>(b + i);
+    if (din.token) {
+      float* xs = reinterpret_cast<float*>(&x);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        xs[u] = uint64_t(philox_w0(uint32_t(i + u), 4u, il, ih, seed_lo, seed_hi)) >= din.threshold ? xs[u] * din.scale : 0.0f;
+    }
+    if (a) {
+      const float4 y = *reinterpret_cast<const float4*>(a + i);
+      x = make_float4(y.x + x.x, y.y + x.y, y.z + x.z, y.w + x.w);
+    }
+    sv[v] = x;
+    sum += ((x.x + x.y) + x.z) + x.w;
+  }
+  const float mean = wave_sum(sum) / float(h);
+  float q = 0.0f;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const float* xs = reinterpret_cast<const float*>(&sv[v]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) { const float d = xs[u] - mean; q = __builtin_fmaf(d, d, q); }
+  }
+  const float var = wave_sum(q) / float(h);
+  const float rstd = 1.0f / sqrtf(var + 1e-12f);
+  const uint32_t ol = dout.token ? uint32_t(dout.token[0]) : 0u, oh = dout.token ? uint32_t(dout.token[1]) : 0u;
+  typedef _Float16 h4_ __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int64_t c = 4 * (lane + 64 * v), i = row * h + c;
+    const float4 g = *reinterpret_cast<const float4*>(gamma + c), be = *reinterpret_cast<const float4*>(beta + c);
+    const float* xs = reinterpret_cast<const float*>(&sv[v]);
+    const float* gs = reinterpret_cast<const float*>(&g);
+    const float* bs = reinterpret_cast<const float*>(&be);
+    float y[4], yd[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      y[u] = (xs[u] - mean) * rstd * gs[u] + bs[u];
+      yd[u] = (yd_out || o16.b) && uint64_t(philox_w0(uint32_t(i + u), 4u, ol, oh, seed_lo, seed_hi)) >= dout.threshold
+                  ? y[u] * dout.scale
+                  : 0.0f;
+    }
+    if (s_out) *reinterpret_cast<float4*>(s_out + i) = sv[v];
+    if (y_out) *reinterpret_cast<float4*>(y_out + i) = make_float4(y[0], y[1], y[2], y[3]);
+    if (o16.a) *reinterpret_cast<h4_*>(o16.a + i) = h4_{_Float16(y[0]), _Float16(y[1]), _Float16(y[2]), _Float16(y[3])};
+    if (yd_out) *reinterpret_cast<float4*>(yd_out + i) = make_float4(yd[0], yd[1], yd[2], yd[3]);
+    if (o16.b) *reinterpret_cast<h4_*>(o16.b + i) = h4_{_Float16(yd[0]), _Float16(yd[1]), _Float16(yd[2]), _Float16(yd[3])};
+  }
+  if (stats && lane == 0) { stats[2 * row] = mean; stats[2 * row + 1] = rstd; }
+}
+
 void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_token, uint64_t din_threshold,
               float din_scale, const float* gamma, const float* beta, float* s_out, float* y_out, float* stats,
               const int32_t* dout_token, uint64_t dout_threshold, float dout_scale, float* yd_out, int64_t rows,
@@ -373,6 +442,19 @@ void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_
   if (h > 1024) bad("fused LayerNorm rows wider than 1024");
   if (rows * h > (int64_t(1) << 32)) bad("fused LayerNorm over more than 2^32 elements");
   const DropoutSpec din{din_token, din_threshold, din_scale}, dout{dout_token, dout_threshold, dout_scale};
+  auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (!gather && !a_ids && !b_ids && h % 256 == 0 && h <= 1024 && al16(a) && al16(b) && al16(gamma) && al16(beta) &&
+      al16(s_out) && al16(y_out) && al16(yd_out) && reinterpret_cast<uintptr_t>(y16) % 8 == 0 &&
+      reinterpret_cast<uintptr_t>(yd16) % 8 == 0) {
+#define MSX_LNF4(V) MSX_LAUNCH(k_ln_fused4<V>, dim3(blocks_for(rows, 4)), dim3(256), 0, s, a, b, din, gamma, beta, s_out, \
+                               y_out, stats, dout, yd_out, rows, uint32_t(seed), uint32_t(seed >> 32), Out16{y16, yd16})
+    if (h == 256) MSX_LNF4(1);
+    else if (h == 512) MSX_LNF4(2);
+    else if (h == 768) MSX_LNF4(3);
+    else MSX_LNF4(4);
+#undef MSX_LNF4
+    return;
+  }
   const int cpl = int((h + 63) / 64);
 #define MSX_LNF(C) MSX_LAUNCH(k_ln_fused<C>, dim3(blocks_for(rows, 4)), dim3(256), 0, s, a, b, din, gamma, beta, s_out, y_out, \
                               stats, dout, yd_out, rows, h, uint32_t(seed), uint32_t(seed >> 32), gather, src_rows, \

@@ -461,7 +461,7 @@ def test_dropout_masks_are_bit_exact_at_full_size(ctx, oracle):
     assert 0.88 < kept < 0.92
 
 
-@pytest.mark.parametrize("rows,h", [(4096, 128), (37, 200)])
+@pytest.mark.parametrize("rows,h", [(4096, 128), (37, 200), (1000, 768), (64, 256), (33, 1024)])
 def test_fused_layer_norm_neighbours(ctx, oracle, rows, h):
     """LayerNorm(e1 + e2) followed by a Dropout, and LayerNorm(a + Dropout(b)) with the residual sum
     kept for the backward, as the fused pass runs them: values within the per-kernel tolerance of
