@@ -325,9 +325,10 @@ struct LossScaleState {
   float scale, inv;
   uint32_t good, overflow, skipped, window, pad0, pad1;
 };
-// ls may be null (no loss scaling).
+// ls may be null (no loss scaling). p16 (mixed precision), when set, receives the updated
+// parameters rounded to f16 (left as they are when an overflowed step skips the update).
 void adamw(hipStream_t s, float* p, const float* g, float* m, float* v, int64_t n, AdamWConsts k, const float* lr_t,
-           const float* c1, const float* c2, const LossScaleState* ls = nullptr);
+           const float* c1, const float* c2, const LossScaleState* ls = nullptr, _Float16* p16 = nullptr);
 void sgd(hipStream_t s, float* p, const float* g, int64_t n, const float* lr, const LossScaleState* ls = nullptr);
 // column_finalize and adamw in one launch, for a step without loss scaling whose deferred
 // reductions are all gradients in the arena g[0, n): the blocks of the finalize jobs write each

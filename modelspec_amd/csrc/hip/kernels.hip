@@ -1545,9 +1545,11 @@ __device__ __forceinline__ void adamw_one(float& p, float g, float& m, float& v,
 __global__ __launch_bounds__(256) void k_adamw(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
                                                float* __restrict__ v, int64_t n, AdamWConsts k,
                                                const float* __restrict__ lr_t, const float* __restrict__ c1,
-                                               const float* __restrict__ c2, const LossScaleState* __restrict__ ls) {
+                                               const float* __restrict__ c2, const LossScaleState* __restrict__ ls,
+                                               _Float16* __restrict__ p16) {
   // A step whose scaled gradients overflowed makes no update (the loss scale halves instead).
   if (ls && ls->overflow) return;
+  typedef _Float16 h4_ __attribute__((ext_vector_type(4)));
   const float lr = lr_t[0], b1 = c1[0], b2 = c2[0], inv = ls ? ls->inv : 1.0f;
   const bool scaled = ls != nullptr;
   const int64_t quads = n / 4, stride = int64_t(gridDim.x) * blockDim.x;
@@ -1569,17 +1571,22 @@ __global__ __launch_bounds__(256) void k_adamw(float* __restrict__ p, const floa
     p4[q] = pq;
     m4[q] = mq;
     v4[q] = vq;
+    if (p16) reinterpret_cast<h4_*>(p16)[q] = h4_{_Float16(pq[0]), _Float16(pq[1]), _Float16(pq[2]), _Float16(pq[3])};
   }
-  for (int64_t i = quads * 4 + t; i < n; i += stride) adamw_one(p[i], scaled ? g[i] * inv : g[i], m[i], v[i], k, lr, b1, b2);
+  for (int64_t i = quads * 4 + t; i < n; i += stride) {
+    adamw_one(p[i], scaled ? g[i] * inv : g[i], m[i], v[i], k, lr, b1, b2);
+    if (p16) p16[i] = _Float16(p[i]);
+  }
 }
 void adamw(hipStream_t s, float* p, const float* g, float* m, float* v, int64_t n, AdamWConsts k, const float* lr_t,
-           const float* c1, const float* c2, const LossScaleState* ls) {
+           const float* c1, const float* c2, const LossScaleState* ls, _Float16* p16) {
   if (n <= 0) return;
   for (const void* a : {static_cast<const void*>(p), static_cast<const void*>(g), static_cast<const void*>(m),
                         static_cast<const void*>(v)})
     if (reinterpret_cast<uintptr_t>(a) % 16) bad("AdamW arenas must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(p16) % 8) bad("AdamW f16 parameter copy must be 8-byte aligned");
   MSX_LAUNCH(k_adamw, dim3(std::min<unsigned>(blocks_for((n + 3) / 4, 256), 16384)), dim3(256), 0, s, p, g, m, v, n,
-             k, lr_t, c1, c2, ls);
+             k, lr_t, c1, c2, ls, p16);
 }
 
 // The arena outside the finalize jobs' outputs: `segs` runs of whole 16-byte quads (first quad,

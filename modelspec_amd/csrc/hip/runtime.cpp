@@ -2131,13 +2131,16 @@ void Executor::build() {
         }});
         pending.back().bytes = finalize_bytes + 7.0 * 4.0 * double(nt);
       } else {
+        // Mixed precision: the launch writes the parameters' f16 copies as it updates them.
         pending.push_back({[=] {
-          return Launch{"AdamW", [=](hipStream_t s) { hk::adamw(s, s_.param_, s_.grad_, s_.m_, s_.v_, nt, c, F(lr), F(c1), F(c2), ls); }};
+          return Launch{"AdamW", [=](hipStream_t s) {
+                          hk::adamw(s, s_.param_, s_.grad_, s_.m_, s_.v_, nt, c, F(lr), F(c1), F(c2), ls, s_.param16_);
+                        }};
         }});
-        pending.back().bytes = 7.0 * 4.0 * double(nt);
+        pending.back().bytes = (7.0 * 4.0 + (s_.opt_.mixed ? 2.0 : 0.0)) * double(nt);
       }
       if (ls) pending.push_back({[=] { return Launch{"LossScale", [=](hipStream_t s) { hk::loss_scale_update(s, ls); }}; }});
-      if (s_.param16_ || (s_.opt_.plan_only && s_.opt_.mixed)) {
+      if (fuse_finalize && (s_.param16_ || (s_.opt_.plan_only && s_.opt_.mixed))) {
         pending.push_back({[=] {
           return Launch{"ParamF16", [=](hipStream_t s) { hk::to_f16_rows(s, s_.param_, nt, s_.param16_, nt, 1, nt); }};
         }});
