@@ -42,7 +42,7 @@ constexpr int kAddBatch = MSX_EG_ADD_BATCH;  // staged values a column reads ahe
 constexpr int kApplyThreads = 256;
 constexpr int kCountRows = 36864;
 constexpr int kMaxPositions = 16384;  // ids a table's EmbeddingGrad takes on this path (apply)
-constexpr int kPlanPositions = 8192;  // ids the device plan takes (a plan made by the host: kMaxPositions)
+constexpr int kPlanPositions = 8192;  // ids the device radix plan takes (the counting plan: kMaxPositions)
 
 int bit_length(uint64_t v) {
   int b = 0;
@@ -71,7 +71,9 @@ bool eg_sorted_fits(int64_t n, int64_t rows) {
   const int pb = bit_length(uint64_t(n - 1)) > 0 ? bit_length(uint64_t(n - 1)) : 1;
   return pb + bit_length(uint64_t(rows)) <= 32;
 }
-bool eg_device_plan_fits(int64_t n, int64_t rows) { return n <= kPlanPositions && eg_sorted_fits(n, rows); }
+bool eg_device_plan_fits(int64_t n, int64_t rows) {
+  return (rows <= kCountRows ? n <= kMaxPositions : n <= kPlanPositions) && eg_sorted_fits(n, rows);
+}
 
 size_t eg_plan_bytes(int64_t n, int64_t rows) { return size_t(PlanLayout(n, rows).words) * 4; }
 
@@ -116,7 +118,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_eg_plan_count(EgPlanSet set) {
   for (int r = tid; r < rows; r += kPlanThreads) counts[r] = 0;
   for (int w = tid; w < words; w += kPlanThreads) named_rows[w] = 0;
   // Every id load in flight before the first atomic.
-  constexpr int kMaxPer = kPlanPositions / kPlanThreads;
+  constexpr int kMaxPer = kMaxPositions / kPlanThreads;
   int32_t id_of[kMaxPer], slot[kMaxPer];
 #pragma unroll
   for (int k = 0; k < kMaxPer; ++k) {
@@ -133,7 +135,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_eg_plan_count(EgPlanSet set) {
   __syncthreads();
   // Thread t owns the rows [t*per, t*per + per): their counts in registers; positions, named
   // rows and long segments counted in 16-bit fields of one 64-bit value, scanned over the block
-  // once (each count is at most 8192).
+  // once (each count is at most 16384).
   constexpr int kMaxRowsPer = kCountRows / kPlanThreads;
   const int per = (rows + kPlanThreads - 1) / kPlanThreads;
   const int r0 = tid * per;

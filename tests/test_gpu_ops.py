@@ -398,7 +398,7 @@ def embedding_ids(kind, rows, n, rng):
     ("zipf", 30522, 128, 4096), ("positions", 128, 128, 4096), ("same", 50, 64, 3000), ("uniform", 7, 130, 1),
     ("uniform", 1000, 96, 1500), ("zipf", 40000, 128, 2048), ("uniform", 32768, 8, 16384),
     ("zipf", 30522, 768, 2048), ("same", 5, 128, 8192), ("uniform", 3, 33, 600), ("positions", 512, 256, 8000),
-    ("zipf", 4096, 128, 832),
+    ("zipf", 4096, 128, 832), ("zipf", 30522, 768, 16384), ("same", 5, 64, 16384), ("positions", 512, 64, 12288),
 ])
 def test_embedding_gather_and_sorted_segment_scatter_are_bit_exact(ctx, oracle, kind, rows, h, n):
     rng = np.random.default_rng(3)
