@@ -335,16 +335,20 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds(GemmPtrs ptrs, int6
 // K must be a multiple of 32, or the K-contiguous operands zero-padded to it; the K rows of an
 // operand along its rows are clamped to the last (their products with the padding vanish).
 
-template <int BM, int BN, int WGM, int WGN, bool AKC, bool BKC, int NS, int SUMS, int MF = 16>
+template <int BM, int BN, int WGM, int WGN, bool AKC, bool BKC, int NS, int SUMS, int MF = 16, int BK = 32>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, int64_t M, int64_t N, int64_t K,
                                                                int64_t lda, int64_t ldb, int64_t ldc, int64_t kchunk,
                                                                int64_t zero_to, bool vo, GemmOrder order) {
-  constexpr int BK = 32, W = WGM * WGN;
+  constexpr int W = WGM * WGN;
+  static_assert(BK == 32 || BK == 64, "K tiles of 32 or 64 halves");
   constexpr int WTM = BM / WGM, WTN = BN / WGN, I = WTM / MF, J = WTN / MF;
   static_assert(MF == 16 || MF == 32, "16x16x32 or 32x32x16 MFMA blocks");
   static_assert(I >= 1 && J >= 1 && WTM % MF == 0 && WTN % MF == 0, "whole MFMA blocks a wave");
   // MFMA blocks of MF rows: 16x16x32 (KS = 1 K step of 32 a tile) or 32x32x16 (KS = 2 of 16).
-  constexpr int KS = MF == 16 ? 1 : 2, NV = MF == 16 ? 4 : 16;
+  constexpr int KS = BK / (MF == 16 ? 32 : 16), NV = MF == 16 ? 4 : 16;
+  // A K-contiguous tile's rows: CPR 16-byte chunks (BK 32: 64 bytes, BK 64: a whole 128-byte line),
+  // RPI rows a 1 KB load instruction; chunk c of row r at slot c ^ swz(r).
+  constexpr int CPR = BK / 8, RPI = 64 / CPR;
   typedef float vacc __attribute__((ext_vector_type(NV)));
   constexpr int SA = BM * BK, SB = BN * BK, SS = SA + SB;  // halves a stage
   constexpr int LA = SA / 512, LB = SB / 512;               // 1 KB wave load instructions a tile
@@ -370,6 +374,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
   const GemmEpi epi = ptrs.epi[qp];
   float* __restrict__ ws = ptrs.ws[qp];
   float* __restrict__ colsum = ptrs.colsum[qp];
+  auto swz = [](int r) { return BK == 32 ? ((r >> 2) & 3) : (r & 7); };
   const int64_t kmax = K - 1;
   const _Float16* srcA[PA];
   const _Float16* srcB[PB];
@@ -378,7 +383,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
   for (int h = 0; h < PA; ++h) {
     const int t = wave * PA + h;
     if (AKC) {
-      const int r = t * 16 + lane / 4, ch = (lane % 4) ^ ((r >> 2) & 3);
+      const int r = t * RPI + lane / CPR, ch = (lane % CPR) ^ swz(r);
       const int64_t row = m0 + r < M ? m0 + r : M - 1;
       srcA[h] = A + row * lda + kbeg + 8 * ch;
       kofA[h] = 0;
@@ -396,7 +401,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
   for (int h = 0; h < PB; ++h) {
     const int t = wave * PB + h;
     if (BKC) {
-      const int r = t * 16 + lane / 4, ch = (lane % 4) ^ ((r >> 2) & 3);
+      const int r = t * RPI + lane / CPR, ch = (lane % CPR) ^ swz(r);
       const int64_t row = n0 + r < N ? n0 + r : N - 1;
       srcB[h] = B + row * ldb + kbeg + 8 * ch;
       kofB[h] = 0;
@@ -442,7 +447,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
   // or 2 ks + h) of the row.
   const int fc = MF == 16 ? c : lane & 31, fh = MF == 16 ? q : lane >> 5;
   auto kc_frag = [&](const _Float16* S, int r, int kq) {
-    return *reinterpret_cast<const v8h*>(S + r * 32 + 8 * (kq ^ ((r >> 2) & 3)));
+    return *reinterpret_cast<const v8h*>(S + r * BK + 8 * (kq ^ swz(r)));
   };
   // The LDS address of the transposed read of K rows k0 .. k0 + 3 of the 16 rows from base: in each
   // 16-lane group, source lane li reads K row k0 + li / 4, rows base + 4 (li mod 4) .. + 3.
@@ -458,7 +463,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
   auto tr_pair = [&](int base, int ks, int hh, int& rb, int& k0) {
     if constexpr (MF == 16) {
       rb = base;
-      k0 = 8 * q + 4 * hh;
+      k0 = 32 * ks + 8 * q + 4 * hh;
     } else {
       rb = base + 16 * (q & 1);
       k0 = 16 * ks + 8 * (q >> 1) + 4 * hh;
@@ -502,7 +507,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int i = 0; i < I; ++i) f.a[ks][i] = kc_frag(As, wm + MF * i + fc, MF == 16 ? q : 2 * ks + fh);
+        for (int i = 0; i < I; ++i) f.a[ks][i] = kc_frag(As, wm + MF * i + fc, MF == 16 ? 4 * ks + q : 2 * ks + fh);
     } else {
       tr_frags(As, BM, wm, f.a);
     }
@@ -510,7 +515,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_lds16(GemmPtrs ptrs, in
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int j = 0; j < J; ++j) f.b[ks][j] = kc_frag(Bs, wn + MF * j + fc, MF == 16 ? q : 2 * ks + fh);
+        for (int j = 0; j < J; ++j) f.b[ks][j] = kc_frag(Bs, wn + MF * j + fc, MF == 16 ? 4 * ks + q : 2 * ks + fh);
     } else {
       tr_frags(Bs, BN, wn, f.b);
     }
@@ -722,13 +727,17 @@ bool gemm_lds16(hipStream_t s, const GemmArgs* list, int count, const GemmPtrs& 
   }
   const int64_t zero_to = g.pad_c ? g.ldc : g.n;
   const int sums = g.colsum ? (g.sum_a ? 1 : 2) : 0;
-#define MSX_L16S(AK, BKC_, S)                                                                                      \
-  MSX_LAUNCH((k_gemm_lds16<BM, BN, 2, 2, AK, BKC_, 3, S>), lgrid, dim3(256), 0, s, ptrs, g.m, g.n, g.k, g.lda, g.ldb, \
-             g.ldc, chunk, zero_to, vo, lorder)
+  // 128x128 tiles, 2x2 waves, K tiles of 32 in a 2-stage ring, 16x16x32 blocks. Measured on the
+  // BERT-base step, A/B in one run on one box: a 3-stage ring 23.43 ms (2 stages 23.18); 32x32x16
+  // blocks 25.45; 4 stages 26.30; 256x128, 128x256 and 256x256 tiles 26.0, 25.8 and 26.6; K tiles
+  // of 64 (whole 128-byte rows of a K-contiguous operand a load) 24.6.
+#define MSX_L16S(AK, BKC_, S)                                                                                         \
+  MSX_LAUNCH((k_gemm_lds16<BM, BN, 2, 2, AK, BKC_, 2, S, 16, 32>), lgrid, dim3(256), 0, s, ptrs, g.m, g.n, g.k, g.lda, \
+             g.ldb, g.ldc, chunk, zero_to, vo, lorder);
 #define MSX_L16(AK, BKC_)                  \
-  if (sums == 1) MSX_L16S(AK, BKC_, 1);      \
-  else if (sums == 2) MSX_L16S(AK, BKC_, 2); \
-  else MSX_L16S(AK, BKC_, 0)
+  if (sums == 1) { MSX_L16S(AK, BKC_, 1) }      \
+  else if (sums == 2) { MSX_L16S(AK, BKC_, 2) } \
+  else { MSX_L16S(AK, BKC_, 0) }
   if (akc && bkc) { MSX_L16(true, true); }
   else if (akc) { MSX_L16(true, false); }
   else if (bkc) { MSX_L16(false, true); }
