@@ -461,7 +461,10 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k, bool defer, bool h16, bool
   // through K fastest): their partials all go through the finalize, m n floats a slice
   // (BERT-base's K = 16384 weight gradients: 4 slices 37.7 ms a step, 16 slices 38.0, 2 slices
   // 38.1).
-  const int64_t split = std::max<int64_t>(1, std::min(want, k / (defer ? (p.wm == 4 ? 4096 : 128) : 64)));
+  // (A deferred f16 product of K under 8192 takes slices of at least 512: BERT-base's head dense
+  // weight gradient, 768x768 at K = 2880, otherwise runs 36 blocks.)
+  const int64_t min_slice = defer ? (p.wm == 4 ? (k >= 8192 ? 4096 : 512) : 128) : 64;
+  const int64_t split = std::max<int64_t>(1, std::min(want, k / min_slice));
   p.chunk = ((k + split - 1) / split + kSliceAlign - 1) / kSliceAlign * kSliceAlign;
   p.split = int((k + p.chunk - 1) / p.chunk);
   return p;
