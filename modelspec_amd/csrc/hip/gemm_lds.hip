@@ -649,7 +649,7 @@ bool gemm_lds(hipStream_t s, const GemmArgs& g, const GemmPtrs& ptrs, int split,
   auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   float* ws = ptrs.ws[0];
   const bool akc = !g.ta, bkc = g.tb;
-  const int lds_bk = akc && !bkc ? 32 : 16;
+  const int lds_bk = !bkc ? 32 : 16;  // the K tile of the configuration chosen below
   // Measured: faster for outputs of 2^21 or more (the decoder head, the FFN's 4096 x 512 products and
   // their input gradients) and K of 8192 or more; slower for the K = 4096 weight gradients of
   // 512 x 128 or smaller and the 4096 x 128 products. A cross-entropy head's fused variants (the
@@ -658,7 +658,10 @@ bool gemm_lds(hipStream_t s, const GemmArgs& g, const GemmPtrs& ptrs, int split,
   if (lds) {
     // Tiles (measured on the decoder head shapes of BERT-tiny, 832 x 30522 x 128 and its two
     // gradients): both operands KC 64 x 64, A KC 64 x 128 with eight waves and K tiles of 32,
-    // neither 128 x 128 (each wave 64 x 64: 16 accumulators).
+    // neither 128 x 128 (each wave 64 x 64: 16 accumulators) with K tiles of 32. A/B in one run on
+    // one box (step ms): the weight gradient's K tiles of 32 against 16, 0.7604 against 0.7644; for
+    // the forward K tiles of 32, 128 x 64 or 64 x 128 tiles, and for A KC 64 x 128 with four waves
+    // (K tiles of 16 or 32) or 128 x 128, each 3-80 us a step slower.
     const int bm = akc && bkc ? 64 : akc ? 64 : !bkc ? 128 : 64;
     const int bn = akc && bkc ? 64 : akc ? 128 : !bkc ? 128 : 64;
     const int64_t lmt = (g.m + bm - 1) / bm, lnt = (g.n + bn - 1) / bn;
@@ -679,7 +682,7 @@ bool gemm_lds(hipStream_t s, const GemmArgs& g, const GemmPtrs& ptrs, int split,
   else MSX_LDS(BM, BN, WGM, WGN, BK, AK, BKC_, NS, FP, 0)
     if (akc && bkc) { MSX_LDS_S(64, 64, 2, 2, 16, true, true, 3, true); }
     else if (akc) { MSX_LDS_S(64, 128, 2, 4, 32, true, false, 3, true); }
-    else if (!bkc) { MSX_LDS_S(128, 128, 2, 2, 16, false, false, 3, false); }
+    else if (!bkc) { MSX_LDS_S(128, 128, 2, 2, 32, false, false, 3, false); }
     else { MSX_LDS_S(64, 64, 2, 2, 16, false, true, 3, true); }
 #undef MSX_LDS_S
 #undef MSX_LDS
