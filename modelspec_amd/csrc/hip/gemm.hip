@@ -456,6 +456,10 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k, bool defer, bool h16, bool
   if (defer || k >= 1024) {
     const int64_t blocks = p.wm == 2 ? 2048 : 1024;  // 128 x 128 tiles: 1024 (4 a CU)
     want = tiles < blocks / 4 ? (blocks + tiles - 1) / tiles : 1;
+    // An f32 product of K 8192 or more summed by its own launch (BERT-tiny's decoder input
+    // gradient, K 30522): half as many slices, 74 -> 37 (A/B in one run: 74 -> 68 us, half the
+    // partials written and read back; a quarter as many 74 us, 1.5 times as many 81 us).
+    if (!h16 && !defer && k >= 8192) want = std::max<int64_t>(1, want / 2);
   }
   // Deferred slices keep 128 K steps or more (4096 for 128 x 128 tiles, whose f16 blocks get
   // through K fastest): their partials all go through the finalize, m n floats a slice
