@@ -1585,7 +1585,8 @@ void adamw(hipStream_t s, float* p, const float* g, float* m, float* v, int64_t 
                         static_cast<const void*>(v)})
     if (reinterpret_cast<uintptr_t>(a) % 16) bad("AdamW arenas must be 16-byte aligned");
   if (reinterpret_cast<uintptr_t>(p16) % 8) bad("AdamW f16 parameter copy must be 8-byte aligned");
-  MSX_LAUNCH(k_adamw, dim3(std::min<unsigned>(blocks_for((n + 3) / 4, 256), 16384)), dim3(256), 0, s, p, g, m, v, n,
+  // Up to 65536 blocks (BERT-base's 110 M parameters: 643 -> 608 us against 16384, A/B in one run).
+  MSX_LAUNCH(k_adamw, dim3(std::min<unsigned>(blocks_for((n + 3) / 4, 256), 65536)), dim3(256), 0, s, p, g, m, v, n,
              k, lr_t, c1, c2, ls, p16);
 }
 

@@ -858,6 +858,7 @@ void Executor::build() {
     std::function<hk::CeLossJob()> loss_tail;
   };
   std::vector<Pending> pending;
+  std::vector<uint32_t> ln_posts;  // LayerNorm-backward second outputs with an f16 copy
   std::map<uint32_t, void*> ln_stats_tok;             // LN input value -> stats [rows, 2]
   std::map<uint32_t, void*> ce_stats_tok;             // logits value -> stats [rows, 2]
   std::map<std::pair<uint32_t, uint32_t>, void*> ce_den_tok;  // (logits, weights) -> den
@@ -1505,10 +1506,11 @@ void Executor::build() {
           scl = 1.0f / (1.0f - pr);
         }
         const bool dx16 = want16(dxv), post16 = want16(post);
+        if (post16) ln_posts.push_back(uint32_t(post));
         push([=](hipStream_t s) {
           hk::ln_backward(s, F(xv), gmv >= 0 ? F(uint32_t(gmv)) : nullptr, F(g), static_cast<float*>(A(stats)),
                           dxv >= 0 ? F(uint32_t(dxv)) : nullptr, part ? static_cast<float*>(A(part)) : nullptr, rows, h,
-                          post >= 0 ? F(uint32_t(post)) : nullptr, kind,
+                          post >= 0 && !only16_.count(uint32_t(post)) ? F(uint32_t(post)) : nullptr, kind,
                           post >= 0 && kind != hk::LNB_DROPOUT ? F(uint32_t(aux)) : nullptr,
                           post >= 0 && kind == hk::LNB_DROPOUT ? I(uint32_t(aux)) : nullptr, thr, scl, seed,
                           dx16 ? H16(dxv) : nullptr, post16 ? H16(post) : nullptr);
@@ -2039,6 +2041,13 @@ void Executor::build() {
     std::set<uint32_t> only16;
     for (auto& [v, j] : producer)
       if (j->c16 && certain.count(j) && !j->ws && gemm_only(v)) only16.insert(v);
+    // The same for a LayerNorm backward's second output (the dropout gradient of its dx) that
+    // only f16 GEMMs read: the pass writes its f16 copy alone.
+    for (uint32_t v : ln_posts)
+      if (gemm_only(v)) {
+        only16.insert(v);
+        only16_.insert(v);
+      }
     for (auto& pd : pending)
       for (auto& j : pd.gemm) {
         if (only16.count(j->out_id)) {

@@ -9,6 +9,7 @@
 
 #include <functional>
 #include <map>
+#include <set>
 #include <memory>
 #include <string>
 #include <vector>
@@ -216,6 +217,7 @@ class Executor {
   // Mixed precision: the f16 copy of a value GEMMs read as an operand, written by its producer.
   std::map<uint32_t, void*> token16_;
   std::map<uint32_t, _Float16*> fixed16_;  // parameters: their slice of the session's f16 copy
+  std::set<uint32_t> only16_;               // values kept as their f16 copy alone (no f32 value written)
   _Float16* ptr16(uint32_t id) const;      // nullptr when the value has no f16 copy
   std::vector<Launch> launches_;
   size_t join_at_ = SIZE_MAX;  // the first launch after the backward (it waits for the side stream)
