@@ -231,14 +231,13 @@ __global__ __launch_bounds__(64 * W) void k_flash_fwd16(const _Float16* __restri
   }
 }
 
-// Backward, query side: d_i (from the f32 output and its gradient) and dQ. Block (bh, y) as the
+// Backward, query side: d_i (from the f16 copies of the output and its gradient) and dQ. Block (bh, y) as the
 // forward's; keys and values streamed. Writes the per-query terms the key side reads, three planes
 // of B heads L floats: m_i log2(e), 1 / l_i, d_i.
 template <int W>
 __global__ __launch_bounds__(64 * W) void k_flash_bwd_q16(
     const _Float16* __restrict__ q, const _Float16* __restrict__ k, const _Float16* __restrict__ v,
-    const float* __restrict__ mask, const float* __restrict__ o, const float* __restrict__ go,
-    const _Float16* __restrict__ go16, const float* __restrict__ stats, float* __restrict__ qterms,
+    const float* __restrict__ mask, const _Float16* __restrict__ o16, const _Float16* __restrict__ go16, const float* __restrict__ stats, float* __restrict__ qterms,
     float* __restrict__ dq, _Float16* __restrict__ dq16, int L, int S, int H, int heads, float scale, int64_t plane) {
   __shared__ __align__(16) _Float16 ring[FNS][2][FTILE];
   extern __shared__ float mb[];
@@ -259,13 +258,14 @@ __global__ __launch_bounds__(64 * W) void k_flash_bwd_q16(
       qf[qb][h] = glob_frag(q + row, h, qq);
       gf[qb][h] = glob_frag(go16 + row, h, qq);
     }
+    // d_i from the f16 copies of the output and its gradient (the lane's 16 d, the fragments'),
+    // f32 products and sums.
     float s = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 16; e += 4) {
-      const v4f a = *reinterpret_cast<const v4f*>(o + row + 16 * qq + e);
-      const v4f g = *reinterpret_cast<const v4f*>(go + row + 16 * qq + e);
+    for (int h = 0; h < 2; ++h) {
+      const v8h a = glob_frag(o16 + row, h, qq);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s = __builtin_fmaf(g[r], a[r], s);
+      for (int e = 0; e < 8; ++e) s = __builtin_fmaf(float(gf[qb][h][e]), float(a[e]), s);
     }
     s += __shfl_xor(s, 16, 64);
     s += __shfl_xor(s, 32, 64);
@@ -516,19 +516,19 @@ void flash16_fwd(hipStream_t s, const _Float16* q, const _Float16* k, const _Flo
 }
 
 void flash16_bwd(hipStream_t s, const _Float16* q, const _Float16* k, const _Float16* v, const float* mask,
-                 const float* o, const float* go, const _Float16* go16, const float* stats, float* qterms, float* dq,
-                 _Float16* dq16, float* dk, _Float16* dk16, float* dv, _Float16* dv16, int64_t B, int64_t L, int64_t S,
-                 int64_t H, int64_t heads) {
+                 const _Float16* o16, const _Float16* go16, const float* stats, float* qterms, float* dq, _Float16* dq16,
+                 float* dk, _Float16* dk16, float* dv, _Float16* dv16, int64_t B, int64_t L, int64_t S, int64_t H,
+                 int64_t heads) {
   if (H / heads != FD || H % heads || !flash16_fits(L, S, FD)) bad("f16 attention: 64-wide heads, rows a multiple of 128");
-  if (!q || !k || !v || !o || !go || !go16 || !stats || !qterms || H % 8 || !aligned16(q) || !aligned16(k) ||
-      !aligned16(v) || !aligned16(o) || !aligned16(go) || !aligned16(go16) || !aligned16(qterms) || !aligned16(dq) ||
+  if (!q || !k || !v || !o16 || !go16 || !stats || !qterms || H % 8 || !aligned16(q) || !aligned16(k) ||
+      !aligned16(v) || !aligned16(o16) || !aligned16(go16) || !aligned16(qterms) || !aligned16(dq) ||
       !aligned16(dq16) || !aligned16(dk) || !aligned16(dk16) || !aligned16(dv) || !aligned16(dv16))
     bad("f16 attention backward: f16 operands, output, statistics, query terms and 16-byte aligned rows");
   const float scale = 1.0f / sqrtf(float(FD));
   const int64_t plane = B * heads * L;
   if (plane % 4) bad("f16 attention backward: query-term planes of whole 16-byte groups");
   MSX_LAUNCH(k_flash_bwd_q16<kFlashW>, dim3(unsigned(B * heads), unsigned(L / (32 * kFlashW))), dim3(64 * kFlashW),
-             size_t(S) * 4, s, q, k, v, mask, o, go, go16, stats, qterms, dq, dq16, int(L), int(S), int(H), int(heads),
+             size_t(S) * 4, s, q, k, v, mask, o16, go16, stats, qterms, dq, dq16, int(L), int(S), int(H), int(heads),
              scale, plane);
   if (!dk && !dk16 && !dv && !dv16) return;
   MSX_LAUNCH(k_flash_bwd_kv16<kFlashW>, dim3(unsigned(B * heads), unsigned(S / (32 * kFlashW))), dim3(64 * kFlashW), 0,

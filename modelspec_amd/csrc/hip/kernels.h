@@ -233,17 +233,17 @@ void attention_bwd(hipStream_t s, const float* q, const float* k, const float* v
 void prepare_attention();
 // Mixed-precision attention of 64-wide heads on the f16 operand copies (flash16.hip), for query and
 // key rows multiples of 128 (keys at most 4096): o and o16 (either may be null) the output in f32
-// and f16, stats as attention_fwd's. The backward takes the forward's f32 output o, the output
-// gradient go in f32 and f16, and qterms, 3 B heads L floats of scratch; any of the f32/f16
+// and f16, stats as attention_fwd's. The backward takes the f16 copies of the forward's output
+// and of the output gradient, and qterms, 3 B heads L floats of scratch; any of the f32/f16
 // gradient outputs may be null.
 bool flash16_fits(int64_t L, int64_t S, int64_t d);
 void prepare_flash16();
 void flash16_fwd(hipStream_t s, const _Float16* q, const _Float16* k, const _Float16* v, const float* mask, float* o,
                  _Float16* o16, float* stats, int64_t B, int64_t L, int64_t S, int64_t H, int64_t heads);
 void flash16_bwd(hipStream_t s, const _Float16* q, const _Float16* k, const _Float16* v, const float* mask,
-                 const float* o, const float* go, const _Float16* go16, const float* stats, float* qterms, float* dq,
-                 _Float16* dq16, float* dk, _Float16* dk16, float* dv, _Float16* dv16, int64_t B, int64_t L, int64_t S,
-                 int64_t H, int64_t heads);
+                 const _Float16* o16, const _Float16* go16, const float* stats, float* qterms, float* dq, _Float16* dq16,
+                 float* dk, _Float16* dk16, float* dv, _Float16* dv16, int64_t B, int64_t L, int64_t S, int64_t H,
+                 int64_t heads);
 
 // Cross-entropy over logits [rows, v] with row pitch ld (>= v): stats = [rows, 2] (max, total);
 // den = [1] f32 weight sum rounded from f64; the gradient o has row pitch ld too.

@@ -711,6 +711,7 @@ void Executor::build() {
       if (flash(x)) {
         for (int side = 0; side < 3; ++side) gemm_operands.insert(x.operands[size_t(side)]);
         if (x.op != Op::Attention) gemm_operands.insert(x.operands[4]);
+        else gemm_operands.insert(x.id);  // the output's f16 copy: the backward's d_i reads it
       }
     }
 
@@ -1590,7 +1591,7 @@ void Executor::build() {
             scratch_o = R(size_t(shape(q)[0] * H) * 4);
             stats_tok = R(size_t(B * heads * L) * 8);
             push([=](hipStream_t s) {
-              hk::flash16_fwd(s, H16(q), H16(kv), H16(v), F(mask), static_cast<float*>(A(scratch_o)), nullptr,
+              hk::flash16_fwd(s, H16(q), H16(kv), H16(v), F(mask), nullptr, static_cast<_Float16*>(A(scratch_o)),
                               static_cast<float*>(A(stats_tok)), B, L, S, H, heads);
             });
           }
@@ -1600,8 +1601,8 @@ void Executor::build() {
           push([=](hipStream_t s) {
             auto out = [&](int64_t v2) { return v2 >= 0 ? F(uint32_t(v2)) : nullptr; };
             auto out16 = [&](int e) { return m16[e] ? H16(members[e]) : nullptr; };
-            const float* fo = fwd_out >= 0 ? F(uint32_t(fwd_out)) : static_cast<float*>(A(scratch_o));
-            hk::flash16_bwd(s, H16(q), H16(kv), H16(v), F(mask), fo, F(g), H16(g), static_cast<float*>(A(stats_tok)),
+            const _Float16* fo = fwd_out >= 0 ? H16(fwd_out) : static_cast<_Float16*>(A(scratch_o));
+            hk::flash16_bwd(s, H16(q), H16(kv), H16(v), F(mask), fo, H16(g), static_cast<float*>(A(stats_tok)),
                             static_cast<float*>(A(qterms)), out(members[0]), out16(0), out(members[1]), out16(1),
                             out(members[2]), out16(2), B, L, S, H, heads);
           });
@@ -1999,6 +2000,10 @@ void Executor::build() {
           for (auto c2 : consumers[readers[r]]) readers.push_back(c2);
           continue;
         }
+        // The f16 attention reads q, k, v and the output gradient as their f16 copies only.
+        if (flash(c) && (c.operands[0] == v || c.operands[1] == v || c.operands[2] == v ||
+                         (c.op != Op::Attention && c.operands[4] == v)) && c.operands[3] != v)
+          continue;
         GemmJob* j = nullptr;
         if (c.op == Op::MatMul && job_of.count(c.id)) j = job_of.at(c.id);
         if (c.op == Op::SumRows && sums_of.count(c.id)) j = sums_of.at(c.id);
