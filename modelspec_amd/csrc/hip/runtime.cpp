@@ -859,7 +859,9 @@ void Executor::build() {
     std::function<hk::CeLossJob()> loss_tail;
   };
   std::vector<Pending> pending;
-  std::vector<uint32_t> ln_posts;  // LayerNorm-backward second outputs with an f16 copy
+  // Outputs of non-GEMM launches that write an f16 copy and may drop the f32 value (LayerNorm
+  // backward's second output, the f16 attention's outputs and gradients).
+  std::vector<uint32_t> ln_posts;
   std::map<uint32_t, void*> ln_stats_tok;             // LN input value -> stats [rows, 2]
   std::map<uint32_t, void*> ce_stats_tok;             // logits value -> stats [rows, 2]
   std::map<std::pair<uint32_t, uint32_t>, void*> ce_den_tok;  // (logits, weights) -> den
@@ -1562,8 +1564,9 @@ void Executor::build() {
             void* st2 = R(size_t(B * heads * L) * 8);
             attn_fwd[fkey] = {id, st2};
             const bool o16 = want16(id);
+            if (o16) ln_posts.push_back(id);  // kept as its f16 copy alone when only f16 kernels read it
             push([=](hipStream_t s) {
-              hk::flash16_fwd(s, H16(q), H16(kv), H16(v), F(mask), F(id), o16 ? H16(id) : nullptr,
+              hk::flash16_fwd(s, H16(q), H16(kv), H16(v), F(mask), only16_.count(id) ? nullptr : F(id), o16 ? H16(id) : nullptr,
                               static_cast<float*>(A(st2)), B, L, S, H, heads);
             });
             pending.back().pure = true;
@@ -1597,9 +1600,12 @@ void Executor::build() {
           }
           void* qterms = R(size_t(3 * B * heads * L) * 4);
           bool m16[3];
-          for (int e = 0; e < 3; ++e) m16[e] = members[e] >= 0 && want16(members[e]);
+          for (int e = 0; e < 3; ++e) {
+            m16[e] = members[e] >= 0 && want16(members[e]);
+            if (m16[e]) ln_posts.push_back(uint32_t(members[e]));
+          }
           push([=](hipStream_t s) {
-            auto out = [&](int64_t v2) { return v2 >= 0 ? F(uint32_t(v2)) : nullptr; };
+            auto out = [&](int64_t v2) { return v2 >= 0 && !only16_.count(uint32_t(v2)) ? F(uint32_t(v2)) : nullptr; };
             auto out16 = [&](int e) { return m16[e] ? H16(members[e]) : nullptr; };
             const _Float16* fo = fwd_out >= 0 ? H16(fwd_out) : static_cast<_Float16*>(A(scratch_o));
             hk::flash16_bwd(s, H16(q), H16(kv), H16(v), F(mask), fo, H16(g), static_cast<float*>(A(stats_tok)),
@@ -2046,8 +2052,9 @@ void Executor::build() {
     std::set<uint32_t> only16;
     for (auto& [v, j] : producer)
       if (j->c16 && certain.count(j) && !j->ws && gemm_only(v)) only16.insert(v);
-    // The same for a LayerNorm backward's second output (the dropout gradient of its dx) that
-    // only f16 GEMMs read: the pass writes its f16 copy alone.
+    // The same for a LayerNorm backward's second output (the dropout gradient of its dx) and the
+    // f16 attention's outputs and gradients that only f16 kernels read: their launches write the
+    // f16 copy alone.
     for (uint32_t v : ln_posts)
       if (gemm_only(v)) {
         only16.insert(v);
