@@ -161,7 +161,8 @@ void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_
               const int32_t* dout_token, uint64_t dout_threshold, float dout_scale, float* yd_out, int64_t rows,
               int64_t h, uint64_t seed, const int32_t* gather = nullptr, int64_t src_rows = 0,
               const int32_t* a_ids = nullptr, int64_t a_rows = 0, const int32_t* b_ids = nullptr, int64_t b_rows = 0,
-              _Float16* y16 = nullptr, _Float16* yd16 = nullptr);  // f16 copies of y and yd
+              _Float16* y16 = nullptr, _Float16* yd16 = nullptr,  // f16 copies of y and yd
+              const _Float16* b16 = nullptr);  // b read from its f16 copy instead (rows of 256..1024)
 
 // LayerNorm backward in one pass: dx when non-null, and when `partial` is non-null the per-block
 // partial sums [ln_backward_blocks, 2 h] of g * xhat (gamma gradient) then g (beta gradient), to be

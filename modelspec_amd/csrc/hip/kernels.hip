@@ -370,8 +370,10 @@ __global__ __launch_bounds__(256) void k_ln_fused4(const float* __restrict__ a, 
                                                    const float* __restrict__ beta, float* __restrict__ s_out,
                                                    float* __restrict__ y_out, float* __restrict__ stats,
                                                    DropoutSpec dout, float* __restrict__ yd_out, int64_t rows,
-                                                   uint32_t seed_lo, uint32_t seed_hi, Out16 o16) {
+                                                   uint32_t seed_lo, uint32_t seed_hi, Out16 o16,
+                                                   const _Float16* __restrict__ b16) {
   constexpr int64_t h = 256 * VPL;
+  typedef _Float16 h4_ __attribute__((ext_vector_type(4)));
   const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
@@ -381,7 +383,13 @@ __global__ __launch_bounds__(256) void k_ln_fused4(const float* __restrict__ a, 
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int64_t i = row * h + 4 * (lane + 64 * v);
-    float4 x = *reinterpret_cast<const float4*>(b + i);
+    float4 x;
+    if (b16) {
+      const h4_ hb = *reinterpret_cast<const h4_*>(b16 + i);
+      x = make_float4(float(hb[0]), float(hb[1]), float(hb[2]), float(hb[3]));
+    } else {
+      x = *reinterpret_cast<const float4*>(b + i);
+    }
     if (din.token) {
       float* xs = reinterpret_cast<float*>(&x);
 #pragma unroll
@@ -406,7 +414,6 @@ __global__ __launch_bounds__(256) void k_ln_fused4(const float* __restrict__ a, 
   const float var = wave_sum(q) / float(h);
   const float rstd = 1.0f / sqrtf(var + 1e-12f);
   const uint32_t ol = dout.token ? uint32_t(dout.token[0]) : 0u, oh = dout.token ? uint32_t(dout.token[1]) : 0u;
-  typedef _Float16 h4_ __attribute__((ext_vector_type(4)));
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int64_t c = 4 * (lane + 64 * v), i = row * h + c;
@@ -435,8 +442,9 @@ void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_
               float din_scale, const float* gamma, const float* beta, float* s_out, float* y_out, float* stats,
               const int32_t* dout_token, uint64_t dout_threshold, float dout_scale, float* yd_out, int64_t rows,
               int64_t h, uint64_t seed, const int32_t* gather, int64_t src_rows, const int32_t* a_ids, int64_t a_rows,
-              const int32_t* b_ids, int64_t b_rows, _Float16* y16, _Float16* yd16) {
+              const int32_t* b_ids, int64_t b_rows, _Float16* y16, _Float16* yd16, const _Float16* b16) {
   if (rows <= 0 || h <= 0) return;
+  if (!b && !b16) bad("fused LayerNorm without its second operand");
   if (!gather) src_rows = rows;
   if ((a_ids || b_ids) && (gather || din_token)) bad("fused LayerNorm: gathered operands with a row gather or an input dropout");
   if (h > 1024) bad("fused LayerNorm rows wider than 1024");
@@ -445,9 +453,9 @@ void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_
   auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   if (!gather && !a_ids && !b_ids && h % 256 == 0 && h <= 1024 && al16(a) && al16(b) && al16(gamma) && al16(beta) &&
       al16(s_out) && al16(y_out) && al16(yd_out) && reinterpret_cast<uintptr_t>(y16) % 8 == 0 &&
-      reinterpret_cast<uintptr_t>(yd16) % 8 == 0) {
+      reinterpret_cast<uintptr_t>(yd16) % 8 == 0 && reinterpret_cast<uintptr_t>(b16) % 8 == 0) {
 #define MSX_LNF4(V) MSX_LAUNCH(k_ln_fused4<V>, dim3(blocks_for(rows, 4)), dim3(256), 0, s, a, b, din, gamma, beta, s_out, \
-                               y_out, stats, dout, yd_out, rows, uint32_t(seed), uint32_t(seed >> 32), Out16{y16, yd16})
+                               y_out, stats, dout, yd_out, rows, uint32_t(seed), uint32_t(seed >> 32), Out16{y16, yd16}, b16)
     if (h == 256) MSX_LNF4(1);
     else if (h == 512) MSX_LNF4(2);
     else if (h == 768) MSX_LNF4(3);
@@ -455,6 +463,7 @@ void ln_fused(hipStream_t s, const float* a, const float* b, const int32_t* din_
 #undef MSX_LNF4
     return;
   }
+  if (b16) bad("fused LayerNorm: an f16 second operand needs rows of 256..1024 floats without gathers");
   const int cpl = int((h + 63) / 64);
 #define MSX_LNF(C) MSX_LAUNCH(k_ln_fused<C>, dim3(blocks_for(rows, 4)), dim3(256), 0, s, a, b, din, gamma, beta, s_out, y_out, \
                               stats, dout, yd_out, rows, h, uint32_t(seed), uint32_t(seed >> 32), gather, src_rows, \

@@ -714,6 +714,20 @@ void Executor::build() {
         else gemm_operands.insert(x.id);  // the output's f16 copy: the backward's d_i reads it
       }
     }
+  // A fused LayerNorm's second addend produced by a GEMM (the sublayer output, before its input
+  // dropout) is read from its f16 copy, as an f16 forward would hold it (rows of 256 .. 1024).
+  std::map<uint32_t, uint32_t> ln_b16;  // LayerNorm -> the addend it reads as f16
+  if (s_.opt_.mixed && !s_.opt_.fuse_ce_head)
+    for (auto& [lid, f] : ln_fused) {
+      if (f.add < 0 || f.b < 0 || f.gather >= 0 || f.ea >= 0 || f.eb >= 0) continue;
+      const Node& bn = p.node(uint32_t(f.b));
+      const int64_t h = p.node(lid).ty.shape[1];
+      if ((bn.op != Op::MatMul && bn.op != Op::AddRows) || bn.ty.rank() != 2 || bn.ty.dtype != DType::F32 ||
+          h % 256 != 0 || h > 1024)
+        continue;
+      gemm_operands.insert(uint32_t(f.b));
+      ln_b16[lid] = uint32_t(f.b);
+    }
 
   // --- storage ------------------------------------------------------------------------------
   std::map<uint32_t, float> constants;
@@ -1458,14 +1472,16 @@ void Executor::build() {
             if (v >= 0) what += tag + std::to_string(v);
           what += " " + type_string(x.ty);
           const bool y16 = want16(yv), yd16 = want16(f.dout);
+          const bool b16 = ln_b16.count(id) && ln_b16.at(id) == uint32_t(bv) && want16(bv);
           push([=](hipStream_t s) {
             auto fp = [&](int64_t v2) { return v2 >= 0 ? F(uint32_t(v2)) : nullptr; };
-            hk::ln_fused(s, fp(av), F(uint32_t(bv)), tin >= 0 ? I(uint32_t(tin)) : nullptr, si.first, si.second, F(gm), F(bt),
+            hk::ln_fused(s, fp(av), b16 && only16_.count(uint32_t(bv)) ? nullptr : F(uint32_t(bv)),
+                         tin >= 0 ? I(uint32_t(tin)) : nullptr, si.first, si.second, F(gm), F(bt),
                          fp(s_val), fp(yv), write_stats ? static_cast<float*>(A(stats)) : nullptr,
                          tout >= 0 ? I(uint32_t(tout)) : nullptr, so.first, so.second, fp(f.dout), rows, h, seed,
                          gids >= 0 ? I(uint32_t(gids)) : nullptr, src_rows, ea.ids >= 0 ? I(uint32_t(ea.ids)) : nullptr,
                          ea.rows, eb.ids >= 0 ? I(uint32_t(eb.ids)) : nullptr, eb.rows, y16 ? H16(yv) : nullptr,
-                         yd16 ? H16(f.dout) : nullptr);
+                         yd16 ? H16(f.dout) : nullptr, b16 ? H16(bv) : nullptr);
           });
           bytes = 4.0 * double(count) * (2 + (av >= 0) + (f.add >= 0) + (yv >= 0) + (f.dout >= 0));
           break;
@@ -2005,6 +2021,16 @@ void Executor::build() {
         if (c.op == Op::Transpose && folded.count(c.id)) {
           for (auto c2 : consumers[readers[r]]) readers.push_back(c2);
           continue;
+        }
+        // A fused LayerNorm reads its GEMM-produced addend as its f16 copy only (the Add, or the
+        // Dropout of it, that the pass applies).
+        {
+          bool ln_reads = false;
+          for (auto& [lid, bvv] : ln_b16) {
+            const LnFused& f = ln_fused.at(lid);
+            ln_reads = ln_reads || (bvv == v && (int64_t(c.id) == f.add || int64_t(c.id) == f.din));
+          }
+          if (ln_reads) continue;
         }
         // The f16 attention reads q, k, v and the output gradient as their f16 copies only.
         if (flash(c) && (c.operands[0] == v || c.operands[1] == v || c.operands[2] == v ||
