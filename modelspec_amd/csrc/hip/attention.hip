@@ -365,32 +365,48 @@ __global__ __launch_bounds__(64 * W) void k_attn_fwd_mfma(const float* __restric
   l += __shfl_xor(l, 16, 64);
   l += __shfl_xor(l, 32, 64);
   if constexpr (KS > 1) {
-    // The pair's second wave hands its maximum, sum and output rows over through LDS (the tiles
-    // are done with: the loop ended on a barrier); the first rescales both to the larger maximum.
-    static_assert(KS == 2, "two waves a query tile");
-    float* cb = sm + (wave / KS) * (32 + 16 * D);
-    if (half == 1 && active) {
+    // The group's other waves hand their maximum, sum and output rows over through LDS (the tiles
+    // are done with: the loop ended on a barrier); the first rescales them all to the largest
+    // maximum and adds them in wave order.
+    constexpr int CB = 32 + 16 * D;
+    float* cb = sm + (wave / KS) * (KS - 1) * CB;
+    if (half > 0 && active) {
+      float* mine = cb + (half - 1) * CB;
       if (g == 0) {
-        cb[c] = m;
-        cb[16 + c] = l;
+        mine[c] = m;
+        mine[16 + c] = l;
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int ct = 0; ct < D / 16; ++ct) cb[32 + (4 * g + r) * D + 16 * ct + c] = oacc[ct][r];
+        for (int ct = 0; ct < D / 16; ++ct) mine[32 + (4 * g + r) * D + 16 * ct + c] = oacc[ct][r];
     }
     __syncthreads();
-    if (half == 1 || !active) return;
-    const float m1 = cb[c], l1 = cb[16 + c], mn = fmaxf(m, m1);
-    const float a0 = m == -INFINITY ? 0.0f : expf(m - mn), a1 = m1 == -INFINITY ? 0.0f : expf(m1 - mn);
-    l = l * a0 + l1 * a1;
-    m = mn;
+    if (half > 0 || !active) return;
+    float mn = m;
+#pragma unroll
+    for (int h = 0; h < KS - 1; ++h) mn = fmaxf(mn, cb[h * CB + c]);
+    const float a0 = m == -INFINITY ? 0.0f : expf(m - mn);
+    l *= a0;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float b0 = __shfl(a0, 4 * g + r, 64), b1 = __shfl(a1, 4 * g + r, 64);
+      const float b0 = __shfl(a0, 4 * g + r, 64);
 #pragma unroll
-      for (int ct = 0; ct < D / 16; ++ct) oacc[ct][r] = oacc[ct][r] * b0 + cb[32 + (4 * g + r) * D + 16 * ct + c] * b1;
+      for (int ct = 0; ct < D / 16; ++ct) oacc[ct][r] *= b0;
     }
+#pragma unroll
+    for (int h = 0; h < KS - 1; ++h) {
+      const float* th = cb + h * CB;
+      const float m1 = th[c], a1 = m1 == -INFINITY ? 0.0f : expf(m1 - mn);
+      l += th[16 + c] * a1;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float b1 = __shfl(a1, 4 * g + r, 64);
+#pragma unroll
+        for (int ct = 0; ct < D / 16; ++ct) oacc[ct][r] += th[32 + (4 * g + r) * D + 16 * ct + c] * b1;
+      }
+    }
+    m = mn;
   }
   if (!active) return;
 #pragma unroll
@@ -431,7 +447,12 @@ __device__ __forceinline__ void attn_bwd_q_body(const float* __restrict__ q, con
   // d_i for query i0 + c: lane group g sums columns [g D/4, (g + 1) D/4).
   float dd = 0.0f;
 #pragma unroll
-  for (int t = 0; t < D / 4; ++t) dd = __builtin_fmaf(go[row + g * (D / 4) + t], o[row + g * (D / 4) + t], dd);
+  for (int t = 0; t < D / 16; ++t) {
+    const v4f a = *reinterpret_cast<const v4f*>(go + row + g * (D / 4) + 4 * t);
+    const v4f e = *reinterpret_cast<const v4f*>(o + row + g * (D / 4) + 4 * t);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) dd = __builtin_fmaf(a[u], e[u], dd);
+  }
   dd += __shfl_xor(dd, 16, 64);
   dd += __shfl_xor(dd, 32, 64);
   const int64_t srow = int64_t(blockIdx.x) * L + (active ? i0 : 0) + c;
@@ -498,21 +519,22 @@ __device__ __forceinline__ void attn_bwd_q_body(const float* __restrict__ q, con
     __syncthreads();
   }
   if constexpr (KS > 1) {
-    // The pair's partial dQ, the first wave's plus the second's.
-    static_assert(KS == 2, "two waves a query tile");
-    float* cb = sm + (wave / KS) * (16 * D);
-    if (half == 1 && active)
+    // The group's partial dQ, added in wave order.
+    float* cb = sm + (wave / KS) * (KS - 1) * (16 * D);
+    if (half > 0 && active)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int ct = 0; ct < D / 16; ++ct) cb[(4 * g + r) * D + 16 * ct + c] = acc[ct][r];
+        for (int ct = 0; ct < D / 16; ++ct) cb[(half - 1) * 16 * D + (4 * g + r) * D + 16 * ct + c] = acc[ct][r];
     __syncthreads();
-    if (half == 1) return;
+    if (half > 0) return;
     if (active)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int h = 0; h < KS - 1; ++h)
 #pragma unroll
-        for (int ct = 0; ct < D / 16; ++ct) acc[ct][r] += cb[(4 * g + r) * D + 16 * ct + c];
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int ct = 0; ct < D / 16; ++ct) acc[ct][r] += cb[h * 16 * D + (4 * g + r) * D + 16 * ct + c];
   }
   if (!active) return;
 #pragma unroll
@@ -565,40 +587,53 @@ __device__ __forceinline__ void attn_bwd_kv_body(const float* __restrict__ q, co
   static_assert(NT >= T, "a thread a row of the statistics");
   const int ntiles = (L + T - 1) / T;
   const int tid = int(threadIdx.x);
-  // The maximum, sum and d of query l0 + row (row clamped to the n rows of the tile).
-  auto fetch_stats = [&](float (&e)[3], int l0, int n) {
+  // The maximum and sum of query l0 + row (row clamped to the n rows of the tile), and its d: read
+  // from dsum, or formed as the dQ pass forms it (four sequential fma chains over a quarter of the
+  // columns each, then (p0 + p1) + (p2 + p3)), here by four neighbouring lanes a query, one chain
+  // each on 16-byte loads, combined by two lane swaps (the sums are symmetric, so every lane of
+  // the four holds the same value).
+  constexpr int PD = (4 * T + NT - 1) / NT;
+  auto fetch_stats = [&](float (&e)[2 + PD], int l0, int n) {
     if (tid < T) {
       const int64_t at = sbase + l0 + (tid < n ? tid : n - 1);
       e[0] = stats[2 * at];
       e[1] = stats[2 * at + 1];
+    }
+#pragma unroll
+    for (int pd = 0; pd < PD; ++pd) {
+      const int it = tid + NT * pd, rr = it >> 2, gg = it & 3;
+      float a = 0.0f;
       if (dsum) {
-        e[2] = dsum[at];
-      } else {
-        // d = rowsum(dO * O) as the dQ pass forms it: four sequential fma chains over a quarter
-        // of the columns each, then (p0 + p1) + (p2 + p3).
-        const int64_t qrow = qbase + int64_t(l0 + (tid < n ? tid : n - 1)) * H;
-        float pg[4];
+        if (gg == 0 && rr < T) a = dsum[sbase + l0 + (rr < n ? rr : n - 1)];
+      } else if (4 * T % NT == 0 || rr < T) {
+        const int64_t qrow = qbase + int64_t(l0 + (rr < n ? rr : n - 1)) * H + gg * (D / 4);
 #pragma unroll
-        for (int gg = 0; gg < 4; ++gg) {
-          float a = 0.0f;
+        for (int t = 0; t < D / 16; ++t) {
+          const v4f x = *reinterpret_cast<const v4f*>(go + qrow + 4 * t);
+          const v4f y = *reinterpret_cast<const v4f*>(o + qrow + 4 * t);
 #pragma unroll
-          for (int t = 0; t < D / 4; ++t) a = __builtin_fmaf(go[qrow + gg * (D / 4) + t], o[qrow + gg * (D / 4) + t], a);
-          pg[gg] = a;
+          for (int u = 0; u < 4; ++u) a = __builtin_fmaf(x[u], y[u], a);
         }
-        e[2] = (pg[0] + pg[1]) + (pg[2] + pg[3]);
+        a += __shfl_xor(a, 1, 64);
+        a += __shfl_xor(a, 2, 64);
       }
+      e[2 + pd] = a;
     }
   };
-  auto put_stats = [&](float* X, const float (&e)[3]) {
+  auto put_stats = [&](float* X, const float (&e)[2 + PD]) {
     if (tid < T) {
       X[3 * tid] = e[0];
       X[3 * tid + 1] = e[1];
-      X[3 * tid + 2] = e[2];
+    }
+#pragma unroll
+    for (int pd = 0; pd < PD; ++pd) {
+      const int it = tid + NT * pd;
+      if ((it & 3) == 0 && (it >> 2) < T) X[3 * (it >> 2) + 2] = e[2 + pd];
     }
   };
   {
     v4f qv[PT], gv[PT];
-    float e[3] = {0.0f, 0.0f, 0.0f};
+    float e[2 + PD] = {};
     fetch_pair<D, T, NT>(qv, gv, q + qbase, go + qbase, H, L < T ? L : T);
     fetch_stats(e, 0, L < T ? L : T);
     put_pair<D, T, NT>(Qb, Gb, qv, gv);
@@ -612,7 +647,7 @@ __device__ __forceinline__ void attn_bwd_kv_body(const float* __restrict__ q, co
     const int j = t & 1, l0 = t * T, n = L - l0 < T ? L - l0 : T;
     const bool more = t + 1 < ntiles;
     v4f qv[PT], gv[PT];
-    float e[3] = {0.0f, 0.0f, 0.0f};
+    float e[2 + PD] = {};
     if (more) {
       const int l1 = l0 + T, n1 = L - l1 < T ? L - l1 : T;
       fetch_pair<D, T, NT>(qv, gv, q + qbase + int64_t(l1) * H, go + qbase + int64_t(l1) * H, H, n1);
@@ -655,27 +690,28 @@ __device__ __forceinline__ void attn_bwd_kv_body(const float* __restrict__ q, co
     __syncthreads();
   }
   if constexpr (KS > 1) {
-    // The pair's partial dK and dV, the first wave's plus the second's.
-    static_assert(KS == 2, "two waves a key tile");
-    float* cb = sm + (wave / KS) * (32 * D);
-    if (half == 1 && active)
+    // The group's partial dK and dV, added in wave order.
+    float* cb = sm + (wave / KS) * (KS - 1) * (32 * D);
+    if (half > 0 && active)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int ct = 0; ct < D / 16; ++ct) {
-          cb[(4 * g + r) * D + 16 * ct + c] = dka[ct][r];
-          cb[16 * D + (4 * g + r) * D + 16 * ct + c] = dva[ct][r];
+          cb[(half - 1) * 32 * D + (4 * g + r) * D + 16 * ct + c] = dka[ct][r];
+          cb[(half - 1) * 32 * D + 16 * D + (4 * g + r) * D + 16 * ct + c] = dva[ct][r];
         }
     __syncthreads();
-    if (half == 1) return;
+    if (half > 0) return;
     if (active)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int h = 0; h < KS - 1; ++h)
 #pragma unroll
-        for (int ct = 0; ct < D / 16; ++ct) {
-          dka[ct][r] += cb[(4 * g + r) * D + 16 * ct + c];
-          dva[ct][r] += cb[16 * D + (4 * g + r) * D + 16 * ct + c];
-        }
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int ct = 0; ct < D / 16; ++ct) {
+            dka[ct][r] += cb[h * 32 * D + (4 * g + r) * D + 16 * ct + c];
+            dva[ct][r] += cb[h * 32 * D + 16 * D + (4 * g + r) * D + 16 * ct + c];
+          }
   }
   if (!active) return;
 #pragma unroll
@@ -918,7 +954,12 @@ __global__ __launch_bounds__(64 * W) void k_attn_bwd_q_h16(const float* __restri
   const int64_t row = (int64_t(b) * L + (active ? i0 : 0) + c) * H + head * D;
   float dd = 0.0f;
 #pragma unroll
-  for (int t = 0; t < D / 4; ++t) dd = __builtin_fmaf(go[row + g * (D / 4) + t], o[row + g * (D / 4) + t], dd);
+  for (int t = 0; t < D / 16; ++t) {
+    const v4f a = *reinterpret_cast<const v4f*>(go + row + g * (D / 4) + 4 * t);
+    const v4f e = *reinterpret_cast<const v4f*>(o + row + g * (D / 4) + 4 * t);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) dd = __builtin_fmaf(a[u], e[u], dd);
+  }
   dd += __shfl_xor(dd, 16, 64);
   dd += __shfl_xor(dd, 32, 64);
   const int64_t srow = int64_t(blockIdx.x) * L + (active ? i0 : 0) + c;
@@ -1119,7 +1160,8 @@ bool head_ok(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128; }
 // one tile, so one LDS buffer and no prefetch. Small problems whose streamed side is at most 128
 // rows (BERT-tiny: 512 wave tiles on 1024 SIMDs) take one 128-row tile shared by two waves a row
 // tile, twice the waves (f32 only; on BERT-tiny the backward pair went from 34 to 27 us a layer
-// and the step from 0.955 to 0.935 ms).
+// and the step from 0.955 to 0.935 ms; four waves a row tile in blocks of eight took the forward
+// from 10.0 to 11.3 us and the backward from 21.3 to 32.4 us).
 struct AttnPlan { int T, W, KS; bool one; };
 AttnPlan attn_plan(int64_t bh, int64_t rows, int64_t streamed, int64_t d, bool h16) {
   const int64_t tiles = bh * ((rows + 15) / 16);
