@@ -423,6 +423,138 @@ __global__ __launch_bounds__(64 * W) void k_attn_fwd_mfma(const float* __restric
   }
 }
 
+// The forward for rows of 128 keys and 64-wide heads (BERT-tiny's attention), with its operands in
+// registers: a block is KS waves on one 16-query tile, each taking 128 / KS of the keys. Every
+// operand goes from global memory straight into MFMA operand registers by 16-byte loads, all
+// issued at the start, so no LDS staging or barrier precedes the MFMA chains. The contraction
+// over d runs in the order d = 16 g + t (lane group g holds columns 16 g .. 16 g + 15 of its key
+// and query rows), and output column 4 c + ct is lane c's ct-th accumulator, so a lane's values
+// and its stores are four consecutive columns. The waves' maxima, sums and outputs combine
+// through LDS in wave order, rescaled to the largest maximum, as k_attn_fwd_mfma's do.
+template <int KS>
+__global__ __launch_bounds__(64 * KS) void k_attn_fwd_reg(const float* __restrict__ q, const float* __restrict__ k,
+                                                        const float* __restrict__ v, const float* __restrict__ mask,
+                                                        float* __restrict__ o, float* __restrict__ stats, int L, int H,
+                                                        int heads, float scale) {
+  constexpr int D = 64, S = 128, U = S / 16 / KS, CB = 32 + 16 * D;
+  __shared__ float cb[(KS - 1) * CB];
+  const int b = blockIdx.x / heads, head = blockIdx.x % heads;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const int i0 = blockIdx.y * 16, key0 = wave * (S / KS);
+  const int64_t kbase = int64_t(b) * S * H + head * D;
+  v4f qv[4], kv[U][4], vv[U][4], mv[U];
+  const float* qr = q + (int64_t(b) * L + i0 + c) * H + head * D + 16 * g;
+#pragma unroll
+  for (int t4 = 0; t4 < 4; ++t4) qv[t4] = *reinterpret_cast<const v4f*>(qr + 4 * t4);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const float* kr = k + kbase + int64_t(key0 + 16 * u + c) * H + 16 * g;
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4) kv[u][t4] = *reinterpret_cast<const v4f*>(kr + 4 * t4);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    mv[u] = *reinterpret_cast<const v4f*>(mask + int64_t(b) * S + key0 + 16 * u + 4 * g);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      vv[u][r] = *reinterpret_cast<const v4f*>(v + kbase + int64_t(key0 + 16 * u + 4 * g + r) * H + 4 * c);
+  }
+  // Every load is issued before any is waited for (otherwise the scheduler spreads them between
+  // the MFMAs, one round trip each): the empty asm takes each register as its operand.
+#pragma unroll
+  for (int t4 = 0; t4 < 4; ++t4) asm volatile("" : "+v"(qv[t4]));
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    asm volatile("" : "+v"(mv[u]));
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4) asm volatile("" : "+v"(kv[u][t4]), "+v"(vv[u][t4]));
+  }
+  // Scores: acc[u][r] = S[key key0 + 16 u + 4 g + r][query i0 + c].
+  v4f acc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) acc[u] = v4f{0, 0, 0, 0};
+#pragma unroll
+  for (int t = 0; t < 16; ++t)
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[u] = mfma4(kv[u][t >> 2][t & 3], qv[t >> 2][t & 3], acc[u]);
+  float m = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (mv[u][r] != 0.0f) m = fmaxf(m, acc[u][r] * scale);
+  m = fmaxf(m, __shfl_xor(m, 16, 64));
+  m = fmaxf(m, __shfl_xor(m, 32, 64));
+  float l = 0.0f;
+  v4f oacc[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) oacc[ct] = v4f{0, 0, 0, 0};
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = mv[u][r] != 0.0f ? expf(acc[u][r] * scale - m) : 0.0f;
+      l += p[r];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) oacc[ct] = mfma4(p[r], vv[u][r][ct], oacc[ct]);
+  }
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  if (wave > 0) {
+    float* mine = cb + (wave - 1) * CB;
+    if (g == 0) {
+      mine[c] = m;
+      mine[16 + c] = l;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) mine[32 + (4 * g + r) * D + 4 * c + ct] = oacc[ct][r];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+  float mn = m;
+#pragma unroll
+  for (int h = 0; h < KS - 1; ++h) mn = fmaxf(mn, cb[h * CB + c]);
+  const float a0 = m == -INFINITY ? 0.0f : expf(m - mn);
+  l *= a0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float b0 = __shfl(a0, 4 * g + r, 64);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) oacc[ct][r] *= b0;
+  }
+#pragma unroll
+  for (int h = 0; h < KS - 1; ++h) {
+    const float* th = cb + h * CB;
+    const float m1 = th[c], a1 = m1 == -INFINITY ? 0.0f : expf(m1 - mn);
+    l += th[16 + c] * a1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float b1 = __shfl(a1, 4 * g + r, 64);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) oacc[ct][r] += th[32 + (4 * g + r) * D + 4 * c + ct] * b1;
+    }
+  }
+  m = mn;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float row_total = __shfl(l, 4 * g + r, 64);
+    const int64_t orow = (int64_t(b) * L + i0 + 4 * g + r) * H + head * D + 4 * c;
+    *reinterpret_cast<v4f*>(o + orow) =
+        v4f{oacc[0][r] / row_total, oacc[1][r] / row_total, oacc[2][r] / row_total, oacc[3][r] / row_total};
+  }
+  if (stats && g == 0) {
+    const int64_t at = (int64_t(blockIdx.x) * L + i0 + c) * 2;
+    stats[at] = m;
+    stats[at + 1] = l;
+  }
+}
+
 // dQ and d_i = rowsum(dO * O), per 16 query rows, streaming key and value tiles; `by` is the
 // block's query-tile index (blockIdx.y of its own launch).
 template <int D, int T, int W, int KS>
@@ -1262,6 +1394,15 @@ void attention_fwd(hipStream_t s, const float* q, const float* k, const float* v
   if (!head_ok(d) || L > S) refuse("attention head width or query rows");
   float scale = 1.0f / sqrtf(float(d));
   if (attention_mfma(L, S, d)) {
+    // 128 keys of 64-wide heads in f32 (BERT-tiny): the register-operand forward, four waves a
+    // 16-query tile (8.5 us a layer against 10.0 for the LDS-staged kernel; two waves 9.9, eight
+    // 9.5; the step 0.755 -> 0.751 ms). Its 16-byte loads need 16-byte aligned rows.
+    const auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (!h16 && d == 64 && S == 128 && H % 4 == 0 && al16(q) && al16(k) && al16(v) && al16(mask) && al16(o)) {
+      dim3 grid(unsigned(B * heads), unsigned(L / 16));
+      MSX_LAUNCH(k_attn_fwd_reg<4>, grid, dim3(256), 0, s, q, k, v, mask, o, stats, int(L), int(H), int(heads), scale);
+      return;
+    }
     const AttnPlan plan = attn_plan(B * heads, L, S, d, h16);
     dim3 grid(unsigned(B * heads), row_blocks(L, plan));
 #define GO_H(T, W) launch_fwd_h<D, T, W>(s, grid, q, k, v, mask, o, stats, int(L), int(S), int(H), int(heads), scale)
